@@ -1,0 +1,271 @@
+#!/usr/bin/env python3
+"""Benchmark of the map+reduce hot path on one MI355X.
+
+Runs the BASELINE.json configurations through the HIP emitter's kernels
+(tca_program_launch, the C ABI) and prints ONE JSON line. The headline
+`value` is configs[1] (C2: fused row sum + row max over fp32 [8192, 8192]),
+in achieved HBM GB/s; every configuration is reported under "kernels" with
+its own roofline entry. A "step" is one launch of the compiled program over
+one batch of inputs already resident in HBM. Inputs rotate over enough
+buffer sets (>= 768 MB) that the 256 MB Infinity Cache cannot serve a
+repeat. Timing: hipEvents on the launch stream around the timed steps.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c1,c2,...]
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, AMD published
+MFMA_PEAK_TFLOPS = {"f32": 157.3, "bf16": 2500.0}  # dense, AMD published
+MALL_DEFEAT_BYTES = 768 << 20
+
+CONFIGS = {
+    # key: (program, description)
+    "c1": ("scale_relu", "C1 z=max(a*x+y,0) f32 [4096,4096]"),
+    "c2": ("row_sum_max_8192", "C2 row sum+max f32 [8192,8192]"),
+    "c3": ("softmax_4096", "C3 row softmax f32 [16384,4096]"),
+    "c4": ("layernorm_1024", "C4 layernorm f32 [32768,1024]"),
+    "c5f": ("gemm_f32", "C5 gemm f32 4096^3"),
+    "c5b": ("gemm_bf16", "C5 gemm bf16-in f32-acc 4096^3"),
+}
+
+
+def _events():
+    from tcacomp_amd import _lib
+    L = _lib.lib()
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    _lib.check(L.tca_rt_event_create(ctypes.byref(a)))
+    _lib.check(L.tca_rt_event_create(ctypes.byref(b)))
+    return a, b
+
+
+def _setup(key, dev):
+    """Returns (program, list of argument sets, scalars, work dict)."""
+    import numpy as np
+    import torch
+    from tcacomp_amd import inputs, programs, compiler
+
+    name = CONFIGS[key][0]
+    prog = compiler.compile_program(programs.CONFIG_PROGRAMS[name](), jit=os.environ.get("TCA_JIT", "0") != "0")
+
+    def dev_f32(a):
+        return torch.from_numpy(a).to(dev)
+
+    if key == "c1":
+        M = N = 4096
+        x, y = inputs.uniform((M, N, 1), -1, 1, 0), inputs.uniform((M, N, 1), -1, 1, 1)
+        algo = 3 * M * N * 4
+        per_set = algo
+        make = lambda i: [dev_f32(x), dev_f32(y), torch.empty((M, N), device=dev)]  # noqa: E731
+        scalars = [1.5]
+        work = {"bytes": algo, "bound": "hbm", "shape": [M, N]}
+        cpu = ("c1", (x, y))
+    elif key == "c2":
+        R = C = 8192
+        x = inputs.normal((R, C), 1.0, 0)
+        algo = R * C * 4 + 2 * R * 4
+        per_set = algo
+        make = lambda i: [dev_f32(x), torch.empty(R, device=dev), torch.empty(R, device=dev)]  # noqa: E731
+        scalars = []
+        work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = ("c2", (x,))
+    elif key == "c3":
+        R, C = 16384, 4096
+        x = inputs.normal((R, C), 2.0, 0)
+        algo = 2 * R * C * 4
+        per_set = algo
+        make = lambda i: [dev_f32(x), torch.empty((R, C), device=dev)]  # noqa: E731
+        scalars = []
+        work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = ("c3", (x,))
+    elif key == "c4":
+        R, C = 32768, 1024
+        x = inputs.normal((R, C), 1.0, 0)
+        g = inputs.uniform((C,), 0.5, 1.5, 1)
+        bt = inputs.uniform((C,), -0.1, 0.1, 2)
+        algo = 2 * R * C * 4 + 2 * C * 4
+        per_set = algo
+        make = lambda i: [dev_f32(x), dev_f32(g), dev_f32(bt), torch.empty((R, C), device=dev)]  # noqa: E731
+        scalars = [1.0 / C, 1e-5]
+        work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = ("c4", (x, g, bt))
+    else:
+        M = N = K = 4096
+        a = inputs.uniform((M, K), -1, 1, 0)
+        b = inputs.uniform((K, N), -1, 1, 1)
+        if key == "c5b":
+            ta = torch.from_numpy(a).to(dev).to(torch.bfloat16)
+            tb = torch.from_numpy(b).to(dev).to(torch.bfloat16)
+            elt = 2
+            dt = "bf16"
+        else:
+            ta, tb = dev_f32(a), dev_f32(b)
+            elt = 4
+            dt = "f32"
+        per_set = (M * K + K * N) * elt + M * N * 4
+        make = lambda i: [ta.clone(), tb.clone(), torch.empty((M, N), device=dev)]  # noqa: E731
+        scalars = []
+        work = {"flops": 2 * M * N * K, "bound": "mfma", "dtype": dt, "shape": [M, N, K],
+                "bytes": per_set}
+        cpu = (key, (a, b))
+    nsets = max(2, math.ceil(MALL_DEFEAT_BYTES / per_set))
+    sets = [make(i) for i in range(nsets)]
+    return prog, sets, scalars, work, cpu
+
+
+def _time(prog, sets, scalars, steps, warmup):
+    import torch
+    from tcacomp_amd import _lib
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    for i in range(warmup):
+        prog.launch(sets[i % len(sets)], scalars=scalars, stream=stream)
+    torch.cuda.synchronize()
+    e0, e1 = _events()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    _lib.check(L.tca_rt_event_record(e0, ctypes.c_void_p(stream)))
+    for i in range(steps):
+        prog.launch(sets[i % len(sets)], scalars=scalars, stream=stream)
+    _lib.check(L.tca_rt_event_record(e1, ctypes.c_void_p(stream)))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = ctypes.c_float()
+    _lib.check(L.tca_rt_event_elapsed_ms(e0, e1, ctypes.byref(ms)))
+    L.tca_rt_event_destroy(e0)
+    L.tca_rt_event_destroy(e1)
+    return ms.value / steps, wall * 1e3 / steps
+
+
+def _cpu_baseline(key, args, threads):
+    """The CPU oracle timed on this host on a bounded sample (best of 3).
+    Returns (value, unit, sample description)."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import numpy as np
+    import oracle
+
+    def best(f, reps=3):
+        t = []
+        for _ in range(reps):
+            s = time.perf_counter()
+            f()
+            t.append(time.perf_counter() - s)
+        return min(t)
+
+    if key == "c1":
+        x, y = args
+        xs, ys = x.reshape(-1), y.reshape(-1)
+        dt = best(lambda: oracle.scale_relu(xs, ys, 1.5, threads))
+        return 3 * xs.size * 4 / dt / 1e9, "GB/s", "full [4096,4096]"
+    if key == "c2":
+        (x,) = args
+        dt = best(lambda: oracle.row_sum_max(x, threads))
+        return (x.size * 4 + 2 * x.shape[0] * 4) / dt / 1e9, "GB/s", "full [8192,8192]"
+    if key == "c3":
+        (x,) = args
+        xs = np.ascontiguousarray(x[:2048])
+        dt = best(lambda: oracle.softmax(xs, threads))
+        return 2 * xs.size * 4 / dt / 1e9, "GB/s", "2048 of 16384 rows"
+    if key == "c4":
+        x, g, b = args
+        xs = np.ascontiguousarray(x[:8192])
+        dt = best(lambda: oracle.layernorm(xs, g, b, 1.0 / 1024, 1e-5, threads))
+        return (2 * xs.size * 4 + 2 * 1024 * 4) / dt / 1e9, "GB/s", "8192 of 32768 rows"
+    a, b = args
+    rows = 16 * max(1, threads)
+    asub = np.ascontiguousarray(a[:rows])
+    if key == "c5b":
+        asub, b = oracle.to_bf16_bits(asub), oracle.to_bf16_bits(b)
+    dt = best(lambda: oracle.gemm(asub, b, threads=threads), reps=1)
+    return 2 * rows * 4096 * 4096 / dt / 1e12, "TFLOP/s", "%d of 4096 rows" % rows
+
+
+def _traffic(symbol):
+    p = os.path.join(REPO, "profiles", "traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        t = json.load(f)
+    return t.get(symbol)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each config shards by rows "
+              "with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from tcacomp_amd import _lib
+    dev = torch.device("cuda:0")
+    _lib.check(_lib.lib().tca_rt_init(0))
+    keys = [k for k in args.configs.split(",") if k]
+    threads = int(os.environ.get("TCA_CPU_THREADS", "1"))
+    results = {}
+    for key in keys:
+        prog, sets, scalars, work, cpu = _setup(key, dev)
+        ms, wall_ms = _time(prog, sets, scalars, args.steps, args.warmup)
+        sym = prog.kernel_symbols()[0]
+        entry = {"config": CONFIGS[key][1], "kernel": sym, "family": prog.families()[0], "ms": ms,
+                 "host_wall_ms": wall_ms}
+        if work["bound"] == "hbm":
+            gbs = work["bytes"] / (ms * 1e-3) / 1e9
+            entry["roofline"] = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": gbs / HBM_PEAK_GBS, "traffic": _traffic(sym)}
+            entry["algorithmic_bytes"] = work["bytes"]
+        else:
+            tf = work["flops"] / (ms * 1e-3) / 1e12
+            peak = MFMA_PEAK_TFLOPS[work["dtype"]]
+            entry["roofline"] = {"bound": "mfma", "achieved": tf, "peak": peak, "unit": "TFLOP/s",
+                                 "frac": tf / peak, "traffic": _traffic(sym)}
+            entry["algorithmic_flops"] = work["flops"]
+        if not args.no_cpu:
+            v1, unit, sample = _cpu_baseline(key, cpu[1], 1)
+            entry["cpu_baseline"] = {"value": v1, "unit": unit, "cores": 1, "kind": "port", "sample": sample}
+            if threads > 1:
+                vn, _, _ = _cpu_baseline(key, cpu[1], threads)
+                entry["cpu_baseline_ncores"] = {"value": vn, "unit": unit, "cores": threads, "kind": "port",
+                                                "sample": sample}
+        results[key] = entry
+        print("[bench] %s %s %.4f ms %s" % (key, sym, ms, json.dumps(entry["roofline"])), file=sys.stderr,
+              flush=True)
+        del sets
+        torch.cuda.empty_cache()
+    head = results.get("c2") or next(iter(results.values()))
+    line = {
+        "metric": "achieved HBM GB/s (% of peak) per kernel; matmul TFLOP/s (% MFMA peak)",
+        "value": head["roofline"]["achieved"],
+        "unit": head["roofline"]["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded counter-based U/N generators, host-generated, resident in HBM)",
+        "config": {"workload": head["config"], "kernel": head["kernel"]},
+        "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+        "kernels": results,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

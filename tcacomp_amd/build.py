@@ -1,0 +1,99 @@
+"""In-tree build: the host library (libtcacomp.so) and every prebuilt code
+object the tests and the bench launch.
+
+The host library holds the runtime (plain HIP host API), the plan
+interpreter, the DSL builder and the HIP emitter; it is ordinary C++ built
+with g++ against the ROCm headers. Device code exists only as emitted
+kernels, compiled by hipcc for gfx950 into ``_kcache/``.
+"""
+import concurrent.futures
+import os
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(PKG_DIR)
+CSRC = os.path.join(PKG_DIR, "csrc")
+OBJ_DIR = os.path.join(PKG_DIR, "_build")
+LIB = os.path.join(PKG_DIR, "libtcacomp.so")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+SOURCES = [
+    "rt/runtime.cpp",
+    "rt/plan.cpp",
+    "cg/ir.cpp",
+    "cg/builder.cpp",
+    "cg/emit_hip.cpp",
+    "cg/gemm_emit.cpp",
+    "cg/capi.cpp",
+]
+
+CXXFLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+            "-I" + os.path.join(ROCM, "include"), "-I" + os.path.join(REPO, "include"),
+            "-I" + os.path.join(CSRC, "rt")]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("build step failed: %s\n%s%s" % (" ".join(cmd), r.stdout[-3000:], r.stderr[-3000:]))
+    return r
+
+
+def build_library(jobs=8):
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    objs = []
+    cmds = []
+    for s in SOURCES:
+        src = os.path.join(CSRC, s)
+        obj = os.path.join(OBJ_DIR, os.path.basename(s).replace(".cpp", ".o"))
+        objs.append(obj)
+        cmds.append(["g++"] + CXXFLAGS + ["-c", src, "-o", obj])
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(_run, cmds))
+    tmp = LIB + ".tmp"
+    _run(["g++", "-shared", "-o", tmp] + objs +
+         ["-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath," + os.path.join(ROCM, "lib")])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_kernels(jobs=8, force=False):
+    """Emits and compiles every registered program into _kcache/."""
+    from . import compiler, programs
+
+    jobs_list = []
+    for name, factory, flags in programs.all_builds():
+        prog = factory()
+        emitted = prog.emit(flags=flags)
+        key = compiler.cache_key(emitted.source, emitted.hipcc)
+        os.makedirs(compiler.KCACHE, exist_ok=True)
+        base = os.path.join(compiler.KCACHE, "%s-%s" % (prog.name, key))
+        with open(base + ".hip", "w") as f:
+            f.write(emitted.source)
+        with open(base + ".plan", "w") as f:
+            f.write(emitted.plan)
+        if force or not os.path.exists(base + ".hsaco"):
+            jobs_list.append((base + ".hip", base + ".hsaco", emitted.hipcc))
+
+    def one(j):
+        compiler.build_code_object(*j)
+        return j[1]
+
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
+        done = list(ex.map(one, jobs_list))
+    return done
+
+
+def build_all(force_kernels=False):
+    build_library()
+    # The freshly built library must be the one loaded.
+    from . import _lib
+    _lib._lib = None
+    return build_kernels(force=force_kernels)
+
+
+if __name__ == "__main__":
+    sys.path.insert(0, REPO)
+    out = build_all(force_kernels="--force" in sys.argv)
+    print("built %s and %d code object(s)" % (LIB, len(out)))

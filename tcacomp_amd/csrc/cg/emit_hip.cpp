@@ -1,0 +1,1185 @@
+// emit_hip.cpp — lowers a finished map+reduce graph to one HIP source file
+// (gfx950) plus its launch plan.
+//
+// Pass structure (the reference's HIR window, internal/pipeline/pipeline.go:
+// 41-52, restated for what the HIP path needs; the sm_86 LOWER window —
+// tiling search, tile-lower, schedule, final-lower — has no counterpart: each
+// family below fixes its own wave64 geometry):
+//   1. dead-chain elimination: a chain survives if it stores an output, or a
+//      local that a surviving later chain reads (internal/opt/dce/dce.go);
+//   2. nest fusion: consecutive chains with the identical iteration order
+//      fuse into one kernel when the fused family accepts them — the
+//      reference's GVN loop-nest fusion (design/optana/loop_fusion.md:7-22);
+//   3. local placement (memopt): a local whose producer and every reader sit
+//      in one fused kernel lives in registers; any other local lives in an
+//      HBM workspace the runtime provides (lifting the reference's
+//      "GMEM temporaries are refused" gate, internal/cg/cxx/emit.go:274-276);
+//   4. family classification + emission, one __global__ per nest.
+#include "emit.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <functional>
+#include <map>
+#include <set>
+#include <sstream>
+
+#include "gemm_emit.h"
+
+namespace tca {
+namespace cg {
+
+using ir::BinOp;
+using ir::Elem;
+using ir::Graph;
+using ir::Op;
+
+const char* FamilyName(Family f) {
+  switch (f) {
+    case Family::Elementwise: return "elementwise";
+    case Family::Row: return "row";
+    case Family::Gemm: return "gemm";
+    case Family::Generic: return "generic";
+  }
+  return "?";
+}
+
+std::vector<std::string> DeviceFlags(const std::string& target) {
+  return {"--genco",
+          "--offload-arch=" + target,
+          "-O3",
+          "-std=c++17",
+          "-ffp-contract=off",
+          "-fno-gpu-flush-denormals-to-zero",
+          "-fhip-fp32-correctly-rounded-divide-sqrt",
+          "-Xclang",
+          "-target-feature",
+          "-Xclang",
+          "-packed-fp32-ops",
+          "-Wno-unused-variable",
+          "-Wno-unused-but-set-variable"};
+}
+
+namespace detail {
+
+std::string CType(Elem e) {
+  switch (e) {
+    case Elem::F32: return "float";
+    case Elem::F16: return "_Float16";
+    case Elem::BF16: return "__bf16";
+    case Elem::I32: return "int32_t";
+    case Elem::U32: return "uint32_t";
+    case Elem::I8: return "int8_t";
+    case Elem::I16: return "int16_t";
+    case Elem::U8: return "uint8_t";
+    case Elem::U16: return "uint16_t";
+    case Elem::Bool: return "bool";
+  }
+  return "float";
+}
+
+// Scalar kernel-parameter type: 4-byte slots (rt/plan.cpp PackArgs).
+std::string ScalarArgType(Elem e) {
+  if (ir::IsFloat(e)) return "float";
+  if (e == Elem::U32 || e == Elem::U16 || e == Elem::U8) return "uint32_t";
+  return "int32_t";
+}
+
+std::string Literal(const ir::Expr& e) {
+  char buf[80];
+  switch (e.type) {
+    case Elem::F32:
+    case Elem::F16:
+    case Elem::BF16: {
+      std::string f;
+      if (std::isnan(e.value)) f = "__builtin_nanf(\"\")";
+      else if (std::isinf(e.value)) f = e.value > 0 ? "__builtin_inff()" : "(-__builtin_inff())";
+      else {
+        std::snprintf(buf, sizeof(buf), "%af", static_cast<float>(e.value));
+        f = buf;
+      }
+      if (e.type == Elem::F32) return f;
+      return "static_cast<" + CType(e.type) + ">(" + f + ")";
+    }
+    case Elem::Bool:
+      return e.value != 0.0 ? "true" : "false";
+    case Elem::U32:
+      std::snprintf(buf, sizeof(buf), "%.0fu", e.value);
+      return buf;
+    default:
+      std::snprintf(buf, sizeof(buf), "static_cast<%s>(%.0f)", CType(e.type).c_str(), e.value);
+      return buf;
+  }
+}
+
+std::string ExtentExpr(const Graph& g, int d) {
+  if (g.dims[d].extent > 0) return std::to_string(g.dims[d].extent) + "u";
+  return "d" + std::to_string(d);
+}
+
+// Emits pure scalar expression DAGs as SSA temporaries. One instance per
+// lexical scope: its memo is the common-subexpression table of that scope.
+class ExprGen {
+ public:
+  ExprGen(const Graph& g, std::ostringstream& out, std::string indent, int* counter)
+      : g_(g), out_(out), indent_(std::move(indent)), counter_(counter) {}
+
+  void Bind(int param, const std::string& value) { memo_[param] = value; }
+
+  std::string Gen(int id) {
+    auto it = memo_.find(id);
+    if (it != memo_.end()) return it->second;
+    const ir::Expr& e = g_.exprs[id];
+    std::string val;
+    switch (e.op) {
+      case Op::Const:
+        val = Literal(e);
+        memo_[id] = val;
+        return val;
+      case Op::Scalar: {
+        const Elem t = g_.scalars[e.index].elem;
+        val = "s" + std::to_string(e.index);
+        if (ScalarArgType(t) != CType(t)) val = "static_cast<" + CType(t) + ">(" + val + ")";
+        memo_[id] = val;
+        return val;
+      }
+      case Op::Param:
+        // Unbound lambda parameter: a classifier bug, never user error.
+        val = "/*unbound " + e.text + "*/0";
+        memo_[id] = val;
+        return val;
+      default:
+        break;
+    }
+    std::vector<std::string> a;
+    for (int x : e.args) a.push_back(Gen(x));
+    const std::string T = CType(e.type);
+    std::string rhs;
+    switch (e.op) {
+      case Op::Bin: {
+        const BinOp op = static_cast<BinOp>(e.code);
+        static const char* sym[] = {"+", "-", "*", "/", "%", "==", "!=", "<", "<=", ">", ">=", "&&", "||",
+                                    "&", "|", "^", "<<", ">>"};
+        std::string core = "(" + a[0] + " " + sym[static_cast<int>(op)] + " " + a[1] + ")";
+        const Elem in = g_.exprs[e.args[0]].type;
+        if (e.type == Elem::Bool || in == Elem::F32 || in == Elem::I32 || in == Elem::U32) rhs = core;
+        else rhs = "static_cast<" + T + ">" + core;
+        break;
+      }
+      case Op::Un: {
+        static const char* sym[] = {"-", "+", "!", "~"};
+        rhs = "static_cast<" + T + ">(" + std::string(sym[e.code]) + a[0] + ")";
+        break;
+      }
+      case Op::Select:
+        rhs = "(" + a[0] + " ? " + a[1] + " : " + a[2] + ")";
+        break;
+      case Op::Cast:
+        rhs = "static_cast<" + T + ">(" + a[0] + ")";
+        break;
+      case Op::Call: {
+        if (e.text == "fmaf") rhs = "__builtin_fmaf(" + a[0] + ", " + a[1] + ", " + a[2] + ")";
+        else if (e.text == "umin") rhs = "min(" + a[0] + ", " + a[1] + ")";
+        else if (e.text == "umax") rhs = "max(" + a[0] + ", " + a[1] + ")";
+        else {
+          rhs = e.text + "(";
+          for (size_t i = 0; i < a.size(); ++i) rhs += (i ? ", " : "") + a[i];
+          rhs += ")";
+        }
+        break;
+      }
+      default:
+        rhs = "0";
+        break;
+    }
+    val = "v" + std::to_string((*counter_)++);
+    out_ << indent_ << "const " << T << " " << val << " = " << rhs << ";\n";
+    memo_[id] = val;
+    return val;
+  }
+
+ private:
+  const Graph& g_;
+  std::ostringstream& out_;
+  std::string indent_;
+  int* counter_;
+  std::map<int, std::string> memo_;
+};
+
+void CollectScalars(const Graph& g, int id, std::set<int>* out) {
+  const ir::Expr& e = g.exprs[id];
+  if (e.op == Op::Scalar) out->insert(e.index);
+  for (int a : e.args) CollectScalars(g, a, out);
+}
+
+std::set<int> ChainScalars(const Graph& g, const ir::Chain& c) {
+  std::set<int> s;
+  CollectScalars(g, c.root.fn.body, &s);
+  for (const auto& r : c.reduces) {
+    CollectScalars(g, r.init, &s);
+    CollectScalars(g, r.fn.body, &s);
+  }
+  if (c.has_piped) CollectScalars(g, c.piped.fn.body, &s);
+  return s;
+}
+
+// Combiners a tree reduction may reassociate: acc OP now (either order)
+// with OP one of + * min max (float +,* reassociate within tolerance, as the
+// reference's WarpReducer does), integer bitwise ops, logical and/or.
+bool IsMonoidCombiner(const Graph& g, const ir::ReduceStage& r) {
+  const ir::Expr& b = g.exprs[r.fn.body];
+  const int acc = r.fn.params[0], now = r.fn.params[1];
+  if (b.args.size() != 2) return false;
+  const bool params = (b.args[0] == acc && b.args[1] == now) || (b.args[0] == now && b.args[1] == acc);
+  if (!params) return false;
+  if (b.op == Op::Bin) {
+    switch (static_cast<BinOp>(b.code)) {
+      case BinOp::Add:
+      case BinOp::Mul:
+      case BinOp::And:
+      case BinOp::Or:
+      case BinOp::Xor:
+      case BinOp::LAnd:
+      case BinOp::LOr:
+        return true;
+      default:
+        return false;
+    }
+  }
+  if (b.op == Op::Call)
+    return b.text == "fmaxf" || b.text == "fminf" || b.text == "umin" || b.text == "umax";
+  return false;
+}
+
+std::string Sym(const Graph& g, const std::string& prefix, int k) {
+  (void)g;
+  return prefix + "_k" + std::to_string(k);
+}
+
+}  // namespace detail
+
+using namespace detail;
+
+bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std::string& symbol,
+              const std::string& signature, int* counter, std::ostringstream* src, GemmEmitted* out,
+              std::string* err) {
+  (void)err;
+  std::ostringstream& o = *src;
+  const int ta = c.root.ops[m.a_op].tensor, tb = c.root.ops[m.b_op].tensor, tc = c.store_tensor;
+  const bool bf16 = m.in == Elem::BF16;
+  o << "// contraction over @" << g.dims[m.k].name << " on MFMA (" << (bf16 ? "bf16 32x32x16" : "f32 32x32x2")
+    << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << ", 128x128 tiles\n";
+  o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "(\n    " << signature << ") {\n";
+  o << "  const uint32_t M = " << ExtentExpr(g, m.m) << ", N = " << ExtentExpr(g, m.n) << ", K = "
+    << ExtentExpr(g, m.k) << ";\n";
+  o << "  const auto epi = [&](float acc, uint32_t cm, uint32_t cn) -> float {\n";
+  std::string val = "acc";
+  if (c.has_piped) {
+    ExprGen pg(g, o, "    ", counter);
+    pg.Bind(c.piped.fn.params[0], "acc");
+    for (size_t k = 0; k < c.piped.ops.size(); ++k) {
+      const auto& op = c.piped.ops[k];
+      const ir::Tensor& tt = g.tensors[op.tensor];
+      std::string off = "0u";
+      for (size_t i = 0; i < op.axes.size(); ++i) {
+        const std::string cc = op.axes[i] == m.m ? "cm" : "cn";
+        off = i == 0 ? cc : "(" + off + ") * " + ExtentExpr(g, tt.dims[i]) + " + " + cc;
+      }
+      pg.Bind(c.piped.fn.params[k + 1], "t" + std::to_string(op.tensor) + "[" + off + "]");
+    }
+    val = pg.Gen(c.piped.fn.body);
+  }
+  o << "    return " << val << ";\n  };\n";
+  o << "  tca::hip::gemm_" << (bf16 ? "bf16" : "f32") << "_128<" << (m.b_nk ? "true" : "false") << ">(t" << ta
+    << ", t" << tb << ", t" << tc << ", M, N, K, epi);\n}\n\n";
+  out->block = 256;
+  out->lds = 0;
+  out->grid = {g.dims[m.m].name + "/128", g.dims[m.n].name + "/128"};
+  out->detail = std::string(bf16 ? "bf16" : "f32") + " mfma 32x32 tile=128x128 bk=" + (bf16 ? "64" : "32") +
+                (m.b_nk ? " B=[n][k]" : " B=[k][n]");
+  return true;
+}
+
+namespace {
+
+struct Nest {
+  std::vector<int> chains;
+  Family family = Family::Generic;
+};
+
+struct Analysis {
+  std::vector<bool> live;
+  std::vector<Nest> nests;
+  std::vector<bool> hbm_local;  // per tensor
+  std::vector<int> reg_nest;    // per tensor: nest holding it in registers, or -1
+};
+
+// Tensors a chain reads (operands of both maps).
+std::set<int> ReadSet(const ir::Chain& c) {
+  std::set<int> s;
+  for (const auto& o : c.root.ops) s.insert(o.tensor);
+  if (c.has_piped)
+    for (const auto& o : c.piped.ops) s.insert(o.tensor);
+  return s;
+}
+
+// ---- row family geometry --------------------------------------------------
+
+struct RowGeom {
+  bool ok = false;
+  std::string why;
+  std::vector<int> as;  // common iteration order
+  std::vector<int> outer;
+  int col = -1;
+  uint32_t C = 0, V = 1, vecs = 0, tpr = 1, nv = 1, block = 256, rpb = 1;
+  bool tail = false;
+};
+
+enum class OpKind { RowTile, ColVec, RowScalar, Bad };
+
+OpKind Classify(const ir::Operand& o, const RowGeom& geo) {
+  if (o.axes == geo.as) return OpKind::RowTile;
+  if (o.axes.size() == 1 && o.axes[0] == geo.col) return OpKind::ColVec;
+  for (int a : o.axes)
+    if (a == geo.col) return OpKind::Bad;
+  std::set<int> outer(geo.outer.begin(), geo.outer.end());
+  for (int a : o.axes)
+    if (!outer.count(a)) return OpKind::Bad;
+  return OpKind::RowScalar;
+}
+
+RowGeom RowCheck(const Graph& g, const std::vector<int>& chains) {
+  RowGeom geo;
+  const ir::Chain& c0 = g.chains[chains[0]];
+  geo.as = c0.root.as;
+  geo.col = geo.as.back();
+  geo.outer.assign(geo.as.begin(), geo.as.end() - 1);
+  auto no = [&](const std::string& w) {
+    geo.ok = false;
+    geo.why = w;
+    return geo;
+  };
+  if (g.dims[geo.col].extent == 0) return no("row axis @" + g.dims[geo.col].name + " has a dynamic extent");
+  geo.C = static_cast<uint32_t>(g.dims[geo.col].extent);
+  std::set<int> produced_tile, produced_scalar;
+  for (int ci : chains) {
+    const ir::Chain& c = g.chains[ci];
+    if (c.root.as != geo.as) return no("iteration orders differ");
+    if (c.reduces.size() > 1) return no("more than one reduction in a chain");
+    if (c.reduces.size() == 1 && !IsMonoidCombiner(g, c.reduces[0]))
+      return no("combiner is not an associative-commutative op over (acc, now)");
+    for (const auto& o : c.root.ops) {
+      OpKind k = Classify(o, geo);
+      if (k == OpKind::Bad) return no("operand " + g.tensors[o.tensor].name + " is not row-shaped");
+      if (g.tensors[o.tensor].local) {
+        // Produced inside the nest: must match the producer's shape kind.
+        bool inside_tile = produced_tile.count(o.tensor) > 0, inside_scalar = produced_scalar.count(o.tensor) > 0;
+        if (inside_tile && k != OpKind::RowTile) return no("local read with a different shape");
+        if (inside_scalar && k != OpKind::RowScalar) return no("local read with a different shape");
+      }
+    }
+    if (c.has_piped)
+      for (const auto& o : c.piped.ops)
+        if (Classify(o, geo) != OpKind::RowScalar) return no("piped operand is not a row scalar");
+    const ir::Tensor& st = g.tensors[c.store_tensor];
+    if (c.reduces.empty()) {
+      if (c.store_axes != geo.as) return no("elementwise store is not in iteration order");
+      if (st.local) produced_tile.insert(c.store_tensor);
+    } else {
+      if (st.local) produced_scalar.insert(c.store_tensor);
+    }
+  }
+  geo.V = (geo.C % 4 == 0) ? 4 : (geo.C % 2 == 0 ? 2 : 1);
+  geo.vecs = geo.C / geo.V;
+  uint32_t tpr = 1;
+  while (tpr * 2 <= geo.vecs / 8 && tpr * 2 <= 1024) tpr *= 2;
+  geo.tpr = tpr;
+  geo.nv = (geo.vecs + tpr - 1) / tpr;
+  if (geo.nv > 16) return no("row of " + std::to_string(geo.C) + " elements exceeds the register-resident limit");
+  geo.tail = (geo.vecs % tpr) != 0;
+  geo.block = std::max<uint32_t>(256, tpr);
+  geo.rpb = geo.block / tpr;
+  geo.ok = true;
+  return geo;
+}
+
+// ---- elementwise family check --------------------------------------------
+
+bool DegenerateReduces(const Graph& g, const ir::Chain& c) {
+  for (const auto& r : c.reduces)
+    if (g.dims[r.axis].extent != 1) return false;
+  return true;
+}
+
+std::vector<int> DropUnit(const Graph& g, const std::vector<int>& axes) {
+  std::vector<int> out;
+  for (int a : axes)
+    if (g.dims[a].extent != 1) out.push_back(a);
+  return out;
+}
+
+class Emitter {
+ public:
+  Emitter(const Graph& g, const Options& o) : g_(g), opts_(o) {
+    prefix_ = opts_.kernel_name.empty() ? g.name : opts_.kernel_name;
+    std::string clean;
+    for (char ch : prefix_) clean += (isalnum(static_cast<unsigned char>(ch)) || ch == '_') ? ch : '_';
+    prefix_ = "tca_" + clean;
+  }
+
+  bool Run(Result* out, std::string* err) {
+    if (opts_.target != "gfx950") {
+      *err = "emit: unsupported target " + opts_.target + " (this backend emits CDNA4 code for gfx950 only)";
+      return false;
+    }
+    Analyze();
+    src_ << "// Generated by the tcacomp HIP emitter for " << opts_.target << ". Do not edit.\n";
+    src_ << "// program: " << g_.name << "\n";
+    src_ << "#include \"tca/hip/device.h\"\n";
+    if (uses_gemm_) src_ << "#include \"tca/hip/gemm.h\"\n";
+    src_ << "\n";
+    for (size_t ni = 0; ni < an_.nests.size(); ++ni) {
+      if (!EmitNest(static_cast<int>(ni), err)) return false;
+    }
+    if (an_.nests.empty()) {
+      *err = "emit: program " + g_.name + " stores no output";
+      return false;
+    }
+    out->source = src_.str();
+    out->plan = PlanText();
+    out->hipcc = DeviceFlags(opts_.target);
+    out->kernels = kernels_;
+    std::ostringstream rep;
+    for (const auto& k : kernels_) {
+      rep << k.symbol << " " << FamilyName(k.family) << " chains=";
+      for (size_t i = 0; i < k.chains.size(); ++i) rep << (i ? "," : "") << k.chains[i];
+      rep << " " << k.detail << "\n";
+    }
+    out->report = rep.str();
+    return true;
+  }
+
+ private:
+  struct PlanKernel {
+    std::string symbol;
+    uint32_t block = 256, lds = 0;
+    std::vector<std::string> grid;
+    std::vector<std::string> args;
+  };
+
+  // -------------------------------------------------------------- analysis
+  void Analyze() {
+    const int nc = static_cast<int>(g_.chains.size());
+    an_.live.assign(nc, false);
+    std::set<int> needed;
+    for (int i = nc - 1; i >= 0; --i) {
+      const ir::Chain& c = g_.chains[i];
+      const ir::Tensor& t = g_.tensors[c.store_tensor];
+      bool live = !t.local || needed.count(c.store_tensor);
+      if (!live) continue;
+      an_.live[i] = true;
+      if (t.local) needed.erase(c.store_tensor);
+      for (int r : ReadSet(c))
+        if (g_.tensors[r].local) needed.insert(r);
+    }
+    // Nest fusion.
+    std::vector<int> cur;
+    auto close = [&]() {
+      if (cur.empty()) return;
+      Nest n;
+      n.chains = cur;
+      n.family = ClassifyNest(cur);
+      an_.nests.push_back(n);
+      cur.clear();
+    };
+    for (int i = 0; i < nc; ++i) {
+      if (!an_.live[i]) continue;
+      if (!cur.empty() && opts_.allow_fused && g_.chains[i].root.as == g_.chains[cur[0]].root.as) {
+        std::vector<int> cand = cur;
+        cand.push_back(i);
+        if (RowCheck(g_, cand).ok && !IsGemm(cur) ) {
+          cur = cand;
+          continue;
+        }
+      }
+      close();
+      cur.push_back(i);
+    }
+    close();
+    // Local placement.
+    an_.hbm_local.assign(g_.tensors.size(), false);
+    an_.reg_nest.assign(g_.tensors.size(), -1);
+    for (size_t t = 0; t < g_.tensors.size(); ++t) {
+      if (!g_.tensors[t].local) continue;
+      int producer = -1;
+      std::set<int> readers;
+      for (size_t ni = 0; ni < an_.nests.size(); ++ni) {
+        for (int ci : an_.nests[ni].chains) {
+          if (g_.chains[ci].store_tensor == static_cast<int>(t)) producer = static_cast<int>(ni);
+          if (ReadSet(g_.chains[ci]).count(static_cast<int>(t))) readers.insert(static_cast<int>(ni));
+        }
+      }
+      if (producer < 0) continue;  // dead local
+      bool fused = an_.nests[producer].family == Family::Row && readers.size() == 1 && readers.count(producer);
+      if (fused) an_.reg_nest[t] = producer;
+      else an_.hbm_local[t] = true;
+    }
+    for (const auto& n : an_.nests) uses_gemm_ |= (n.family == Family::Gemm);
+  }
+
+  bool IsGemm(const std::vector<int>& chains) {
+    if (!opts_.allow_gemm || chains.size() != 1) return false;
+    GemmMatch m;
+    return MatchGemm(g_, g_.chains[chains[0]], &m);
+  }
+
+  Family ClassifyNest(const std::vector<int>& chains) {
+    if (chains.size() == 1) {
+      const ir::Chain& c = g_.chains[chains[0]];
+      if (IsGemm(chains)) return Family::Gemm;
+      if (opts_.allow_fused && DegenerateReduces(g_, c) && !ReadsRegLocalCandidate(c)) return Family::Elementwise;
+      if (opts_.allow_fused && RowCheck(g_, chains).ok) return Family::Row;
+      return Family::Generic;
+    }
+    return Family::Row;
+  }
+
+  bool ReadsRegLocalCandidate(const ir::Chain&) { return false; }
+
+  // ------------------------------------------------------------- plumbing
+  std::set<int> NestTensors(const Nest& n) {
+    std::set<int> ts;
+    for (int ci : n.chains) {
+      const ir::Chain& c = g_.chains[ci];
+      for (int t : ReadSet(c)) ts.insert(t);
+      ts.insert(c.store_tensor);
+    }
+    std::set<int> out;
+    for (int t : ts)
+      if (!g_.tensors[t].local || an_.hbm_local[t]) out.insert(t);
+    return out;
+  }
+
+  std::set<int> NestScalars(const Nest& n) {
+    std::set<int> s;
+    for (int ci : n.chains) {
+      auto cs = ChainScalars(g_, g_.chains[ci]);
+      s.insert(cs.begin(), cs.end());
+    }
+    return s;
+  }
+
+  bool IsStoredInNest(const Nest& n, int t) {
+    for (int ci : n.chains)
+      if (g_.chains[ci].store_tensor == t) return true;
+    return false;
+  }
+
+  // Kernel signature: tensors (declaration order), all dims, used scalars.
+  std::string Signature(const Nest& n, PlanKernel* pk) {
+    std::ostringstream s;
+    bool first = true;
+    auto sep = [&]() {
+      if (!first) s << ",\n    ";
+      first = false;
+    };
+    for (int t : NestTensors(n)) {
+      sep();
+      const bool written = IsStoredInNest(n, t);
+      s << (written ? "" : "const ") << CType(g_.tensors[t].elem) << "* __restrict__ t" << t << " /* "
+        << g_.tensors[t].name << " */";
+      pk->args.push_back("ptr " + g_.tensors[t].name);
+    }
+    for (size_t d = 0; d < g_.dims.size(); ++d) {
+      sep();
+      s << "uint32_t d" << d << " /* @" << g_.dims[d].name << " */";
+      pk->args.push_back("dim " + g_.dims[d].name);
+    }
+    for (int sc : NestScalars(n)) {
+      sep();
+      s << ScalarArgType(g_.scalars[sc].elem) << " s" << sc << " /* " << g_.scalars[sc].name << " */";
+      pk->args.push_back("scalar " + g_.scalars[sc].name);
+    }
+    return s.str();
+  }
+
+  std::string DimProduct(const std::vector<int>& axes) {
+    if (axes.empty()) return "1";
+    std::string s;
+    for (size_t i = 0; i < axes.size(); ++i) s += (i ? "*" : "") + g_.dims[axes[i]].name;
+    return s;
+  }
+
+  // Flat row-major offset of operand/store `axes` over tensor t, with the
+  // coordinate of axis a spelled coord(a).
+  std::string Offset(int t, const std::vector<int>& axes, const std::function<std::string(int)>& coord) {
+    const ir::Tensor& tt = g_.tensors[t];
+    if (axes.empty()) return "0u";
+    std::string off = coord(axes[0]);
+    for (size_t i = 1; i < axes.size(); ++i)
+      off = "(" + off + ") * " + ExtentExpr(g_, tt.dims[i]) + " + " + coord(axes[i]);
+    return off;
+  }
+
+  std::string Indent(int n) { return std::string(static_cast<size_t>(n) * 2, ' '); }
+
+  // ------------------------------------------------------------- families
+  bool EmitNest(int ni, std::string* err) {
+    const Nest& n = an_.nests[ni];
+    switch (n.family) {
+      case Family::Elementwise: return EmitElementwise(ni, err);
+      case Family::Row: return EmitRow(ni, err);
+      case Family::Gemm: return EmitGemmNest(ni, err);
+      case Family::Generic: return EmitGeneric(ni, err);
+    }
+    return false;
+  }
+
+  // E: flat streaming over the stored tensor; operands whose non-unit axes
+  // match the store's are read with 16-byte vector loads, others by index.
+  bool EmitElementwise(int ni, std::string* err) {
+    (void)err;
+    const Nest& n = an_.nests[ni];
+    const ir::Chain& c = g_.chains[n.chains[0]];
+    PlanKernel pk;
+    pk.symbol = Sym(g_, prefix_, ni);
+    const uint32_t kVec = 4, kUnroll = 4, kBlock = 256, kPerBlock = kVec * kUnroll * kBlock;
+    pk.block = kBlock;
+    pk.grid.push_back(DimProduct(c.store_axes) + "/" + std::to_string(kPerBlock));
+    const std::string sig = Signature(n, &pk);
+    const std::vector<int> outAxes = DropUnit(g_, c.store_axes);
+    std::ostringstream& o = src_;
+    o << "// statement #" << n.chains[0] << ": elementwise family, " << kVec << "-wide vectors x " << kUnroll
+      << " per thread\n";
+    o << "extern \"C\" __global__ void __launch_bounds__(" << kBlock << ") " << pk.symbol << "(\n    " << sig
+      << ") {\n";
+    o << "  const uint32_t n = " << ProductExpr(c.store_axes) << ";\n";
+    o << "  const uint64_t base = static_cast<uint64_t>(blockIdx.x) * " << kPerBlock << "u + threadIdx.x * " << kVec
+      << "u;\n";
+    // Operand classes.
+    struct Acc {
+      bool aligned;
+    };
+    std::vector<bool> rootAligned, pipedAligned;
+    for (const auto& op : c.root.ops) rootAligned.push_back(DropUnit(g_, op.axes) == outAxes);
+    if (c.has_piped)
+      for (const auto& op : c.piped.ops) pipedAligned.push_back(DropUnit(g_, op.axes) == outAxes);
+    const ir::Tensor& st = g_.tensors[c.store_tensor];
+    // Coordinates of element index `i` (only needed by unaligned operands).
+    auto coordDecl = [&](std::ostringstream& os, const std::string& ind, const std::string& idx) {
+      std::string rem = "rem_" + idx;
+      os << ind << "uint32_t " << rem << " = static_cast<uint32_t>(" << idx << ");\n";
+      for (int k = static_cast<int>(c.store_axes.size()) - 1; k >= 0; --k) {
+        int a = c.store_axes[k];
+        os << ind << "const uint32_t c" << a << "_" << idx << " = " << rem << " % " << ExtentExpr(g_, a) << "; "
+           << rem << " /= " << ExtentExpr(g_, a) << ";\n";
+      }
+    };
+    bool anyUnaligned = false;
+    for (bool b : rootAligned) anyUnaligned |= !b;
+    for (bool b : pipedAligned) anyUnaligned |= !b;
+    // Element body: value of element with flat index expression `idx`, where
+    // aligned operand k's value is `al(k)`.
+    auto body = [&](std::ostringstream& os, const std::string& ind, const std::string& idx,
+                    const std::function<std::string(bool piped, int k)>& alignedVal) -> std::string {
+      if (anyUnaligned) coordDecl(os, ind, idx);
+      auto coord = [&](int a) -> std::string {
+        if (g_.dims[a].extent == 1) return "0u";
+        return "c" + std::to_string(a) + "_" + idx;
+      };
+      ExprGen eg(g_, os, ind, &counter_);
+      for (size_t k = 0; k < c.root.ops.size(); ++k) {
+        const auto& op = c.root.ops[k];
+        std::string v = rootAligned[k] ? alignedVal(false, static_cast<int>(k))
+                                       : "t" + std::to_string(op.tensor) + "[" + Offset(op.tensor, op.axes, coord) + "]";
+        eg.Bind(c.root.fn.params[k], v);
+      }
+      std::string val = eg.Gen(c.root.fn.body);
+      for (const auto& r : c.reduces) {
+        ExprGen rg(g_, os, ind, &counter_);
+        rg.Bind(r.fn.params[0], rg.Gen(r.init));
+        rg.Bind(r.fn.params[1], val);
+        val = rg.Gen(r.fn.body);
+      }
+      if (c.has_piped) {
+        ExprGen pg(g_, os, ind, &counter_);
+        pg.Bind(c.piped.fn.params[0], val);
+        for (size_t k = 0; k < c.piped.ops.size(); ++k) {
+          const auto& op = c.piped.ops[k];
+          std::string v = pipedAligned[k] ? alignedVal(true, static_cast<int>(k))
+                                          : "t" + std::to_string(op.tensor) + "[" + Offset(op.tensor, op.axes, coord) + "]";
+          pg.Bind(c.piped.fn.params[k + 1], v);
+        }
+        val = pg.Gen(c.piped.fn.body);
+      }
+      return val;
+    };
+    // Fast path: the whole strip is in range.
+    o << "  if (base + " << (kUnroll - 1) * kVec * kBlock + kVec - 1 << "u < n) {\n";
+    for (size_t k = 0; k < c.root.ops.size(); ++k) {
+      if (!rootAligned[k]) continue;
+      const auto& op = c.root.ops[k];
+      o << "    tca::hip::vec<" << CType(g_.tensors[op.tensor].elem) << ", " << kVec << "> a" << k << "[" << kUnroll
+        << "];\n";
+    }
+    for (size_t k = 0; k < pipedAligned.size(); ++k) {
+      if (!pipedAligned[k]) continue;
+      const auto& op = c.piped.ops[k];
+      o << "    tca::hip::vec<" << CType(g_.tensors[op.tensor].elem) << ", " << kVec << "> p" << k << "[" << kUnroll
+        << "];\n";
+    }
+    o << "#pragma unroll\n    for (uint32_t u = 0; u < " << kUnroll << "u; ++u) {\n";
+    for (size_t k = 0; k < c.root.ops.size(); ++k) {
+      if (!rootAligned[k]) continue;
+      const auto& op = c.root.ops[k];
+      o << "      a" << k << "[u] = tca::hip::load_vec<" << CType(g_.tensors[op.tensor].elem) << ", " << kVec << ">(t"
+        << op.tensor << " + base + u * " << kVec * kBlock << "u);\n";
+    }
+    for (size_t k = 0; k < pipedAligned.size(); ++k) {
+      if (!pipedAligned[k]) continue;
+      const auto& op = c.piped.ops[k];
+      o << "      p" << k << "[u] = tca::hip::load_vec<" << CType(g_.tensors[op.tensor].elem) << ", " << kVec << ">(t"
+        << op.tensor << " + base + u * " << kVec * kBlock << "u);\n";
+    }
+    o << "    }\n";
+    o << "#pragma unroll\n    for (uint32_t u = 0; u < " << kUnroll << "u; ++u) {\n";
+    o << "      tca::hip::vec<" << CType(st.elem) << ", " << kVec << "> out;\n";
+    o << "#pragma unroll\n      for (uint32_t q = 0; q < " << kVec << "u; ++q) {\n";
+    o << "        const uint64_t e = base + u * " << kVec * kBlock << "u + q;\n";
+    {
+      std::ostringstream bodyS;
+      std::string val = body(bodyS, Indent(4), "e", [&](bool piped, int k) {
+        return std::string(piped ? "p" : "a") + std::to_string(k) + "[u][q]";
+      });
+      o << bodyS.str();
+      o << "        out[q] = " << val << ";\n";
+    }
+    o << "      }\n";
+    o << "      tca::hip::store_vec_nt<" << CType(st.elem) << ", " << kVec << ">(t" << c.store_tensor
+      << " + base + u * " << kVec * kBlock << "u, out);\n";
+    o << "    }\n";
+    o << "  } else {\n";
+    o << "    for (uint32_t u = 0; u < " << kUnroll << "u; ++u) {\n";
+    o << "      for (uint32_t q = 0; q < " << kVec << "u; ++q) {\n";
+    o << "        const uint64_t e = base + u * " << kVec * kBlock << "u + q;\n";
+    o << "        if (e >= n) continue;\n";
+    {
+      std::ostringstream bodyS;
+      std::string val = body(bodyS, Indent(4), "e", [&](bool piped, int k) {
+        const auto& op = piped ? c.piped.ops[k] : c.root.ops[k];
+        return "t" + std::to_string(op.tensor) + "[e]";
+      });
+      o << bodyS.str();
+      o << "        t" << c.store_tensor << "[e] = " << val << ";\n";
+    }
+    o << "      }\n    }\n  }\n}\n\n";
+    AddKernel(pk, Family::Elementwise, n.chains, "vec=4 unroll=4 block=256");
+    return true;
+  }
+
+  std::string ProductExpr(const std::vector<int>& axes) {
+    if (axes.empty()) return "1u";
+    std::string s;
+    for (size_t i = 0; i < axes.size(); ++i) s += (i ? " * " : "") + ExtentExpr(g_, axes[i]);
+    return s;
+  }
+
+  // X: one thread per output element; reductions fold sequentially in
+  // ascending index order from init — the reference's SeqReducer order
+  // (runtime/tca/reducer.h:36-57), hence bit-identical to the CPU oracle
+  // for every combiner.
+  bool EmitGeneric(int ni, std::string* err) {
+    (void)err;
+    const Nest& n = an_.nests[ni];
+    for (size_t k = 0; k < n.chains.size(); ++k) {
+      Nest single;
+      single.chains = {n.chains[k]};
+      single.family = Family::Generic;
+      const ir::Chain& c = g_.chains[n.chains[k]];
+      PlanKernel pk;
+      pk.symbol = Sym(g_, prefix_, ni) + (n.chains.size() > 1 ? "_" + std::to_string(k) : "");
+      pk.block = 256;
+      pk.grid.push_back(DimProduct(c.store_axes) + "/256");
+      const std::string sig = Signature(single, &pk);
+      std::ostringstream& o = src_;
+      o << "// statement #" << n.chains[k] << ": generic family, one thread per output element\n";
+      o << "extern \"C\" __global__ void __launch_bounds__(256) " << pk.symbol << "(\n    " << sig << ") {\n";
+      o << "  const uint32_t total = " << ProductExpr(c.store_axes) << ";\n";
+      o << "  const uint32_t o = blockIdx.x * 256u + threadIdx.x;\n";
+      o << "  if (o >= total) return;\n";
+      o << "  uint32_t rem = o;\n";
+      for (int k2 = static_cast<int>(c.store_axes.size()) - 1; k2 >= 0; --k2) {
+        int a = c.store_axes[k2];
+        o << "  const uint32_t c" << a << " = rem % " << ExtentExpr(g_, a) << "; rem /= " << ExtentExpr(g_, a)
+          << ";\n";
+      }
+      auto coord = [&](int a) { return "c" + std::to_string(a); };
+      const int R = static_cast<int>(c.reduces.size());
+      const std::string T = CType(g_.exprs[c.root.fn.body].type);
+      std::string val;
+      if (R == 0) {
+        ExprGen eg(g_, o, "  ", &counter_);
+        for (size_t q = 0; q < c.root.ops.size(); ++q) {
+          const auto& op = c.root.ops[q];
+          eg.Bind(c.root.fn.params[q], "t" + std::to_string(op.tensor) + "[" + Offset(op.tensor, op.axes, coord) + "]");
+        }
+        val = eg.Gen(c.root.fn.body);
+      } else {
+        // acc_r for reduce r; loops from the outermost reduce (R-1) inwards.
+        std::string ind = "  ";
+        {
+          ExprGen ig(g_, o, ind, &counter_);
+          const std::string iv = ig.Gen(c.reduces[R - 1].init);
+          o << ind << T << " acc" << R - 1 << " = " << iv << ";\n";
+        }
+        for (int r = R - 1; r >= 0; --r) {
+          const int a = c.reduces[r].axis;
+          o << ind << "for (uint32_t c" << a << " = 0; c" << a << " < " << ExtentExpr(g_, a) << "; ++c" << a
+            << ") {\n";
+          ind += "  ";
+          if (r > 0) {
+            ExprGen ig(g_, o, ind, &counter_);
+            const std::string iv = ig.Gen(c.reduces[r - 1].init);
+            o << ind << T << " acc" << r - 1 << " = " << iv << ";\n";
+          }
+        }
+        {
+          ExprGen eg(g_, o, ind, &counter_);
+          for (size_t q = 0; q < c.root.ops.size(); ++q) {
+            const auto& op = c.root.ops[q];
+            eg.Bind(c.root.fn.params[q],
+                    "t" + std::to_string(op.tensor) + "[" + Offset(op.tensor, op.axes, coord) + "]");
+          }
+          std::string v = eg.Gen(c.root.fn.body);
+          ExprGen rg(g_, o, ind, &counter_);
+          rg.Bind(c.reduces[0].fn.params[0], "acc0");
+          rg.Bind(c.reduces[0].fn.params[1], v);
+          const std::string nv = rg.Gen(c.reduces[0].fn.body);
+          o << ind << "acc0 = " << nv << ";\n";
+        }
+        for (int r = 0; r < R; ++r) {
+          ind.resize(ind.size() - 2);
+          o << ind << "}\n";
+          if (r + 1 < R) {
+            ExprGen rg(g_, o, ind, &counter_);
+            rg.Bind(c.reduces[r + 1].fn.params[0], "acc" + std::to_string(r + 1));
+            rg.Bind(c.reduces[r + 1].fn.params[1], "acc" + std::to_string(r));
+            const std::string nv = rg.Gen(c.reduces[r + 1].fn.body);
+            o << ind << "acc" << r + 1 << " = " << nv << ";\n";
+          }
+        }
+        val = "acc" + std::to_string(R - 1);
+      }
+      if (c.has_piped) {
+        ExprGen pg(g_, o, "  ", &counter_);
+        pg.Bind(c.piped.fn.params[0], val);
+        for (size_t q = 0; q < c.piped.ops.size(); ++q) {
+          const auto& op = c.piped.ops[q];
+          pg.Bind(c.piped.fn.params[q + 1],
+                  "t" + std::to_string(op.tensor) + "[" + Offset(op.tensor, op.axes, coord) + "]");
+        }
+        val = pg.Gen(c.piped.fn.body);
+      }
+      o << "  t" << c.store_tensor << "[o] = " << val << ";\n}\n\n";
+      AddKernel(pk, Family::Generic, {n.chains[k]}, "block=256 thread-per-output");
+    }
+    return true;
+  }
+
+  // R/F: one fused kernel per nest; each row is held in registers, every
+  // reduction folds per thread then meets across lanes once.
+  bool EmitRow(int ni, std::string* err) {
+    const Nest& n = an_.nests[ni];
+    RowGeom geo = RowCheck(g_, n.chains);
+    if (!geo.ok) {
+      *err = "emit: row family rejected a nest it classified: " + geo.why;
+      return false;
+    }
+    PlanKernel pk;
+    pk.symbol = Sym(g_, prefix_, ni);
+    pk.block = geo.block;
+    pk.grid.push_back(DimProduct(geo.outer) + "/" + std::to_string(geo.rpb));
+    const std::string sig = Signature(n, &pk);
+    std::ostringstream& o = src_;
+    const uint32_t seg = std::min<uint32_t>(geo.tpr, 64);
+    const uint32_t wpb = geo.block / 64;
+    o << "// statements";
+    for (int ci : n.chains) o << " #" << ci;
+    o << ": fused row family; row @" << g_.dims[geo.col].name << " = " << geo.C << " held in registers\n";
+    o << "// lanes/row " << geo.tpr << ", vectors/lane " << geo.nv << " x " << geo.V << ", rows/block " << geo.rpb
+      << "\n";
+    o << "extern \"C\" __global__ void __launch_bounds__(" << geo.block << ") " << pk.symbol << "(\n    " << sig
+      << ") {\n";
+    o << "  constexpr uint32_t TPR = " << geo.tpr << "u, NV = " << geo.nv << "u, V = " << geo.V
+      << "u, C = " << geo.C << "u, VECS = " << geo.vecs << "u, RPB = " << geo.rpb << "u;\n";
+    o << "  const uint32_t nrows = " << ProductExpr(geo.outer) << ";\n";
+    o << "  const uint32_t row = blockIdx.x * RPB + threadIdx.x / TPR;\n";
+    o << "  const uint32_t lane = threadIdx.x % TPR;\n";
+    o << "  const bool active = row < nrows;\n";
+    if (geo.tail) o << "  const bool tail_ok = (NV - 1u) * TPR + lane < VECS;\n";
+    else o << "  constexpr bool tail_ok = true;\n";
+    o << "  const uint64_t row_base = static_cast<uint64_t>(active ? row : 0u) * C;\n";
+    // Row coordinates.
+    o << "  uint32_t rrem = active ? row : 0u;\n";
+    for (int k = static_cast<int>(geo.outer.size()) - 1; k >= 0; --k) {
+      int a = geo.outer[k];
+      o << "  const uint32_t c" << a << " = rrem % " << ExtentExpr(g_, a) << "; rrem /= " << ExtentExpr(g_, a)
+        << ";\n";
+    }
+    auto coord = [&](int a) { return "c" + std::to_string(a); };
+    // Which tensors are register locals of this nest.
+    auto isReg = [&](int t) { return g_.tensors[t].local && an_.reg_nest[t] == ni; };
+    // Preload row tiles and column vectors read from memory.
+    std::set<int> tiles, cols, rscal;
+    for (int ci : n.chains) {
+      const ir::Chain& c = g_.chains[ci];
+      for (const auto& op : c.root.ops) {
+        OpKind k = Classify(op, geo);
+        if (isReg(op.tensor)) continue;
+        if (k == OpKind::RowTile) tiles.insert(op.tensor);
+        else if (k == OpKind::ColVec) cols.insert(op.tensor);
+      }
+    }
+    for (int t : tiles) {
+      const std::string T = CType(g_.tensors[t].elem);
+      o << "  tca::hip::vec<" << T << ", V> x" << t << "[NV];\n";
+      o << "#pragma unroll\n  for (uint32_t j = 0; j < NV; ++j) {\n";
+      o << "    if (active && (j + 1u < NV || tail_ok)) x" << t << "[j] = tca::hip::load_vec<" << T << ", V>(t" << t
+        << " + row_base + (j * TPR + lane) * V);\n";
+      o << "    else for (uint32_t q = 0; q < V; ++q) x" << t << "[j][q] = " << T << "(0);\n  }\n";
+    }
+    for (int t : cols) {
+      const std::string T = CType(g_.tensors[t].elem);
+      o << "  tca::hip::vec<" << T << ", V> x" << t << "[NV];\n";
+      o << "#pragma unroll\n  for (uint32_t j = 0; j < NV; ++j) {\n";
+      o << "    if (j + 1u < NV || tail_ok) x" << t << "[j] = tca::hip::load_vec<" << T << ", V>(t" << t
+        << " + (j * TPR + lane) * V);\n";
+      o << "    else for (uint32_t q = 0; q < V; ++q) x" << t << "[j][q] = " << T << "(0);\n  }\n";
+    }
+    // Row-scalar value of operand `op` (memory or register local).
+    std::map<int, std::string> regScalar;  // local tensor -> register variable
+    auto rowScalar = [&](const ir::Operand& op) -> std::string {
+      if (isReg(op.tensor)) return regScalar.count(op.tensor) ? regScalar[op.tensor] : "/*missing*/0";
+      return "(active ? t" + std::to_string(op.tensor) + "[" + Offset(op.tensor, op.axes, coord) + "] : " +
+             CType(g_.tensors[op.tensor].elem) + "(0))";
+    };
+    // Element value of the root map of chain c at (j, q).
+    auto elemValue = [&](std::ostringstream& os, const std::string& ind, const ir::Chain& c) -> std::string {
+      ExprGen eg(g_, os, ind, &counter_);
+      for (size_t k = 0; k < c.root.ops.size(); ++k) {
+        const auto& op = c.root.ops[k];
+        OpKind kind = Classify(op, geo);
+        std::string v;
+        if (kind == OpKind::RowTile || kind == OpKind::ColVec) v = "x" + std::to_string(op.tensor) + "[j][q]";
+        else v = rowScalar(op);
+        eg.Bind(c.root.fn.params[k], v);
+      }
+      return eg.Gen(c.root.fn.body);
+    };
+    std::vector<int> group;  // reduce chains with partials, not yet finalized
+    std::set<int> groupOut;
+    int groupNo = 0;
+    uint32_t lds = 0;
+    auto finalize = [&]() {
+      if (group.empty()) return;
+      // Lane reduction inside each segment/wave.
+      for (int ci : group) {
+        const ir::Chain& c = g_.chains[ci];
+        const std::string T = CType(g_.exprs[c.root.fn.body].type);
+        o << "  const auto comb" << ci << " = [](" << T << " acc, " << T << " now) -> " << T << " {\n";
+        ExprGen cg(g_, o, "    ", &counter_);
+        cg.Bind(c.reduces[0].fn.params[0], "acc");
+        cg.Bind(c.reduces[0].fn.params[1], "now");
+        std::string r = cg.Gen(c.reduces[0].fn.body);
+        o << "    return " << r << ";\n  };\n";
+        o << "  part" << ci << " = tca::hip::seg_allreduce<" << seg << ">(part" << ci << ", comb" << ci << ");\n";
+      }
+      if (geo.tpr > 64) {
+        const uint32_t wpr = geo.tpr / 64;
+        for (int ci : group) {
+          const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+          o << "  __shared__ " << T << " red" << ci << "[" << wpb << "];\n";
+          o << "  if (tca::hip::lane_id() == 0u) red" << ci << "[tca::hip::wave_id()] = part" << ci << ";\n";
+          lds += static_cast<uint32_t>(ir::ElemBytes(g_.exprs[g_.chains[ci].root.fn.body].type)) * wpb;
+        }
+        o << "  __syncthreads();\n";
+        o << "  {\n    const uint32_t w0 = (threadIdx.x / TPR) * " << wpr << "u;\n";
+        for (int ci : group) {
+          o << "    part" << ci << " = red" << ci << "[w0];\n";
+          o << "    for (uint32_t w = 1; w < " << wpr << "u; ++w) part" << ci << " = comb" << ci << "(part" << ci
+            << ", red" << ci << "[w0 + w]);\n";
+        }
+        o << "  }\n";
+      }
+      // init applied once per output, then the piped map, then the store.
+      for (int ci : group) {
+        const ir::Chain& c = g_.chains[ci];
+        const ir::ReduceStage& r = c.reduces[0];
+        ExprGen fg(g_, o, "  ", &counter_);
+        fg.Bind(r.fn.params[0], fg.Gen(r.init));
+        fg.Bind(r.fn.params[1], "part" + std::to_string(ci));
+        std::string val = fg.Gen(r.fn.body);
+        if (c.has_piped) {
+          ExprGen pg(g_, o, "  ", &counter_);
+          pg.Bind(c.piped.fn.params[0], val);
+          for (size_t k = 0; k < c.piped.ops.size(); ++k) pg.Bind(c.piped.fn.params[k + 1], rowScalar(c.piped.ops[k]));
+          val = pg.Gen(c.piped.fn.body);
+        }
+        const int st = c.store_tensor;
+        const std::string T = CType(g_.tensors[st].elem);
+        const std::string var = "r" + std::to_string(ci);
+        o << "  const " << T << " " << var << " = " << val << ";\n";
+        if (isReg(st)) regScalar[st] = var;
+        if (!isReg(st) || an_.hbm_local[st]) {
+          o << "  if (active && lane == 0u) t" << st << "[" << Offset(st, c.store_axes, coord) << "] = " << var
+            << ";\n";
+        }
+      }
+      group.clear();
+      groupOut.clear();
+      ++groupNo;
+    };
+    std::set<int> regTiles;  // register row-tile locals produced so far
+    for (int ci : n.chains) {
+      const ir::Chain& c = g_.chains[ci];
+      const std::set<int> reads = ReadSet(c);
+      bool dep = false;
+      for (int t : reads) dep |= groupOut.count(t) > 0;
+      if (c.reduces.empty() || dep) finalize();
+      if (!c.reduces.empty()) {
+        const std::string T = CType(g_.exprs[c.root.fn.body].type);
+        o << "  // statement #" << ci << ": reduce over @" << g_.dims[geo.col].name << " into "
+          << g_.tensors[c.store_tensor].name << "\n";
+        o << "  " << T << " part" << ci << " = " << T << "(0);\n";
+        o << "#pragma unroll\n  for (uint32_t j = 0; j < NV; ++j) {\n";
+        if (geo.tail) o << "    if (j + 1u == NV && !tail_ok) break;\n";
+        o << "#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) {\n";
+        std::ostringstream bs;
+        std::string v = elemValue(bs, "      ", c);
+        o << bs.str();
+        std::ostringstream cs;
+        ExprGen rg2(g_, cs, "        ", &counter_);
+        rg2.Bind(c.reduces[0].fn.params[0], "part" + std::to_string(ci));
+        rg2.Bind(c.reduces[0].fn.params[1], v);
+        std::string folded = rg2.Gen(c.reduces[0].fn.body);
+        o << "      if (j == 0u && q == 0u) part" << ci << " = " << v << ";\n";
+        o << "      else {\n" << cs.str() << "        part" << ci << " = " << folded << ";\n      }\n";
+        o << "    }\n  }\n";
+        group.push_back(ci);
+        groupOut.insert(c.store_tensor);
+      } else {
+        // Elementwise chain over the row: write a tile (memory or registers).
+        const int st = c.store_tensor;
+        const std::string T = CType(g_.tensors[st].elem);
+        o << "  // statement #" << ci << ": elementwise over the row into " << g_.tensors[st].name << "\n";
+        const bool reg = isReg(st);
+        if (reg) o << "  tca::hip::vec<" << T << ", V> x" << st << "[NV];\n";
+        o << "#pragma unroll\n  for (uint32_t j = 0; j < NV; ++j) {\n";
+        o << "    tca::hip::vec<" << T << ", V> outv;\n";
+        o << "#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) {\n";
+        std::ostringstream bs;
+        std::string v = elemValue(bs, "      ", c);
+        o << bs.str();
+        o << "      outv[q] = " << v << ";\n    }\n";
+        if (reg) o << "    x" << st << "[j] = outv;\n";
+        if (!reg || an_.hbm_local[st]) {
+          o << "    if (active && (j + 1u < NV || tail_ok)) tca::hip::store_vec_nt<" << T << ", V>(t" << st
+            << " + row_base + (j * TPR + lane) * V, outv);\n";
+        }
+        o << "  }\n";
+        if (reg) regTiles.insert(st);
+      }
+    }
+    finalize();
+    o << "}\n\n";
+    pk.lds = 0;  // static LDS only; the code object records it
+    (void)lds;
+    std::ostringstream det;
+    det << "row=" << geo.C << " lanes/row=" << geo.tpr << " vec/lane=" << geo.nv << "x" << geo.V
+        << " rows/block=" << geo.rpb << " block=" << geo.block;
+    AddKernel(pk, Family::Row, n.chains, det.str());
+    return true;
+  }
+
+  bool EmitGemmNest(int ni, std::string* err) {
+    const Nest& n = an_.nests[ni];
+    const ir::Chain& c = g_.chains[n.chains[0]];
+    GemmMatch m;
+    if (!MatchGemm(g_, c, &m)) {
+      *err = "emit: gemm family rejected a nest it classified";
+      return false;
+    }
+    PlanKernel pk;
+    pk.symbol = Sym(g_, prefix_, ni);
+    Nest single = n;
+    const std::string sig = Signature(single, &pk);
+    GemmEmitted ge;
+    if (!EmitGemm(g_, c, m, pk.symbol, sig, &counter_, &src_, &ge, err)) return false;
+    pk.block = ge.block;
+    pk.lds = ge.lds;
+    pk.grid = ge.grid;
+    AddKernel(pk, Family::Gemm, n.chains, ge.detail);
+    return true;
+  }
+
+  void AddKernel(const PlanKernel& pk, Family f, const std::vector<int>& chains, const std::string& detail) {
+    plan_kernels_.push_back(pk);
+    KernelInfo ki;
+    ki.symbol = pk.symbol;
+    ki.family = f;
+    ki.chains = chains;
+    ki.detail = detail;
+    kernels_.push_back(ki);
+  }
+
+  std::string PlanText() {
+    std::ostringstream p;
+    p << "tca-plan 1\nprogram " << g_.name << "\n";
+    for (const auto& d : g_.dims) p << "dim " << d.name << " " << d.extent << "\n";
+    for (size_t t = 0; t < g_.tensors.size(); ++t) {
+      const ir::Tensor& tt = g_.tensors[t];
+      std::string role;
+      if (!tt.local) role = g_.IsStored(static_cast<int>(t)) ? "out" : "in";
+      else if (an_.hbm_local[t]) role = "local";
+      else continue;  // register-resident or dead local: not part of the plan
+      p << "tensor " << tt.name << " " << ir::ElemName(tt.elem) << " " << role << " " << tt.dims.size();
+      for (int d : tt.dims) p << " " << g_.dims[d].name;
+      p << "\n";
+    }
+    for (const auto& s : g_.scalars) p << "scalar " << s.name << " " << ir::ElemName(s.elem) << "\n";
+    for (const auto& k : plan_kernels_) {
+      p << "kernel " << k.symbol << " " << k.block << " " << k.lds << " " << k.grid.size();
+      for (const auto& t : k.grid) p << " " << t;
+      p << "\n";
+      for (const auto& a : k.args) p << "arg " << a << "\n";
+    }
+    p << "end\n";
+    return p.str();
+  }
+
+  const Graph& g_;
+  Options opts_;
+  std::string prefix_;
+  Analysis an_;
+  std::ostringstream src_;
+  std::vector<PlanKernel> plan_kernels_;
+  std::vector<KernelInfo> kernels_;
+  int counter_ = 0;
+  bool uses_gemm_ = false;
+};
+
+}  // namespace
+
+bool Emit(const ir::Graph& g, const Options& opts, Result* out, std::string* err) {
+  std::string verr;
+  if (!ir::Verify(g, &verr)) {
+    *err = verr;
+    return false;
+  }
+  Emitter e(g, opts);
+  return e.Run(out, err);
+}
+
+}  // namespace cg
+}  // namespace tca

@@ -1,0 +1,90 @@
+// gemm_emit.cpp — see gemm_emit.h.
+#include "gemm_emit.h"
+
+#include <cmath>
+#include <map>
+
+namespace tca {
+namespace cg {
+
+using ir::BinOp;
+using ir::Elem;
+using ir::Op;
+
+namespace {
+
+// Body operand i is param p, or cast<f32>(param p) when the param is bf16.
+bool IsParamOrCast(const ir::Graph& g, int id, int param, Elem* in) {
+  const ir::Expr& e = g.exprs[id];
+  if (id == param) {
+    *in = e.type;
+    return e.type == Elem::F32;
+  }
+  if (e.op == Op::Cast && e.type == Elem::F32 && e.args[0] == param) {
+    *in = g.exprs[param].type;
+    return *in == Elem::BF16;
+  }
+  return false;
+}
+
+}  // namespace
+
+bool MatchGemm(const ir::Graph& g, const ir::Chain& c, GemmMatch* m) {
+  if (c.root.ops.size() != 2 || c.reduces.size() != 1) return false;
+  if (c.root.as.size() != 3) return false;
+  const ir::ReduceStage& r = c.reduces[0];
+  // init +0.0f
+  const ir::Expr& init = g.exprs[r.init];
+  if (init.op != Op::Const || init.type != Elem::F32 || init.value != 0.0 || std::signbit(init.value)) return false;
+  // acc + now
+  const ir::Expr& comb = g.exprs[r.fn.body];
+  if (comb.op != Op::Bin || static_cast<BinOp>(comb.code) != BinOp::Add) return false;
+  const int acc = r.fn.params[0], now = r.fn.params[1];
+  if (!((comb.args[0] == acc && comb.args[1] == now) || (comb.args[0] == now && comb.args[1] == acc))) return false;
+  // body: P0 * P1
+  const ir::Expr& body = g.exprs[c.root.fn.body];
+  if (body.op != Op::Bin || static_cast<BinOp>(body.code) != BinOp::Mul || body.type != Elem::F32) return false;
+  const int p0 = c.root.fn.params[0], p1 = c.root.fn.params[1];
+  Elem e0, e1;
+  bool direct = IsParamOrCast(g, body.args[0], p0, &e0) && IsParamOrCast(g, body.args[1], p1, &e1);
+  bool swapped = IsParamOrCast(g, body.args[0], p1, &e1) && IsParamOrCast(g, body.args[1], p0, &e0);
+  if (!direct && !swapped) return false;
+  if (e0 != e1) return false;
+  // Axes.
+  const int k = r.axis;
+  std::vector<int> live = c.LiveAxes();
+  if (live.size() != 2 || c.store_axes.size() != 2) return false;
+  if (g.tensors[c.store_tensor].elem != Elem::F32) return false;
+  const int mAx = c.store_axes[0], nAx = c.store_axes[1];
+  const auto& o0 = c.root.ops[0].axes;
+  const auto& o1 = c.root.ops[1].axes;
+  auto isA = [&](const std::vector<int>& ax) { return ax.size() == 2 && ax[0] == mAx && ax[1] == k; };
+  auto isBkn = [&](const std::vector<int>& ax) { return ax.size() == 2 && ax[0] == k && ax[1] == nAx; };
+  auto isBnk = [&](const std::vector<int>& ax) { return ax.size() == 2 && ax[0] == nAx && ax[1] == k; };
+  GemmMatch out;
+  if (isA(o0) && (isBkn(o1) || isBnk(o1))) {
+    out.a_op = 0;
+    out.b_op = 1;
+    out.b_nk = isBnk(o1);
+  } else if (isA(o1) && (isBkn(o0) || isBnk(o0))) {
+    out.a_op = 1;
+    out.b_op = 0;
+    out.b_nk = isBnk(o0);
+  } else {
+    return false;
+  }
+  // Piped epilogue operands must be indexed by m and/or n only.
+  if (c.has_piped)
+    for (const auto& op : c.piped.ops)
+      for (int a : op.axes)
+        if (a != mAx && a != nAx) return false;
+  out.m = mAx;
+  out.n = nAx;
+  out.k = k;
+  out.in = e0;
+  *m = out;
+  return true;
+}
+
+}  // namespace cg
+}  // namespace tca

@@ -1,0 +1,52 @@
+// gemm_emit.h — recognition and emission of the MFMA contraction family.
+//
+// A chain is a dense K-contraction exactly when (the reference's gemm
+// corpus: testing/kernels/llm/gemm.tca:7-22, mlp.tca, qk_score.tca):
+//   - the root map has two tensor operands and its body is l*r, or
+//     cast<f32>(l)*cast<f32>(r) for bf16 operands;
+//   - exactly one reduce, over the last `as` axis k, with init +0.0f and
+//     combiner acc+now (either order);
+//   - the store writes out[m][n] (f32) over the two remaining axes;
+//   - one operand is indexed [m][k], the other [k][n] or [n][k];
+//   - an optional piped map becomes the MFMA epilogue (scalars and tensor
+//     operands indexed by m and/or n).
+// Anything else falls back to another family; the match never guesses.
+#ifndef TCA_CG_GEMM_EMIT_H_
+#define TCA_CG_GEMM_EMIT_H_
+
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "ir.h"
+
+namespace tca {
+namespace cg {
+
+struct GemmMatch {
+  int a_op = -1, b_op = -1;  // root operand indices
+  int m = -1, n = -1, k = -1;
+  bool b_nk = false;  // B indexed [n][k]
+  ir::Elem in = ir::Elem::F32;
+};
+
+struct GemmEmitted {
+  uint32_t block = 256, lds = 0;
+  std::vector<std::string> grid;
+  std::string detail;
+};
+
+bool MatchGemm(const ir::Graph& g, const ir::Chain& c, GemmMatch* m);
+bool EmitGemm(const ir::Graph& g, const ir::Chain& c, const GemmMatch& m, const std::string& symbol,
+              const std::string& signature, int* counter, std::ostringstream* src, GemmEmitted* out,
+              std::string* err);
+
+namespace detail {
+std::string CType(ir::Elem e);
+std::string ExtentExpr(const ir::Graph& g, int d);
+}  // namespace detail
+
+}  // namespace cg
+}  // namespace tca
+
+#endif  // TCA_CG_GEMM_EMIT_H_

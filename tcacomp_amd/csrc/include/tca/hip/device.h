@@ -1,0 +1,123 @@
+// device.h — device primitives the HIP emitter's kernels are built from
+// (gfx950 / CDNA4, wave64). Included by every emitted .hip file.
+//
+// Reference counterparts and what changes:
+//   runtime/tca/reducer.h:60-167 (WarpReducer): a 32-lane __shfl_down_sync
+//     tree on EVERY Reduce(v) plus an SMEM slot fold per element. Here a
+//     thread folds its strip in registers and the lanes meet ONCE per
+//     output, through DPP (quad_perm, row_half_mirror, row_mirror) inside a
+//     16-lane row and ds_bpermute (__shfl_xor) across rows.
+//   runtime/tca/loader.h:60-232 (copy_row vec16, LoadTile*): per-element
+//     bounds predicates; here 16-byte vector loads with the tail handled
+//     once per strip.
+#ifndef TCA_HIP_DEVICE_H_
+#define TCA_HIP_DEVICE_H_
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tca {
+namespace hip {
+
+// A register vector of N elements of T (N * sizeof(T) <= 16 bytes per load).
+template <typename T, int N>
+struct alignas(sizeof(T) * N) vec {
+  T v[N];
+  __device__ __forceinline__ T& operator[](int i) { return v[i]; }
+  __device__ __forceinline__ const T& operator[](int i) const { return v[i]; }
+};
+
+template <typename T, int N>
+__device__ __forceinline__ vec<T, N> load_vec(const T* __restrict__ p) {
+  return *reinterpret_cast<const vec<T, N>*>(p);
+}
+
+// Streaming store: the output is not re-read by this kernel, so keep it out
+// of the caches' way.
+template <typename T, int N>
+__device__ __forceinline__ void store_vec_nt(T* __restrict__ p, const vec<T, N>& x) {
+  if constexpr (sizeof(T) * N == 16) {
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(*reinterpret_cast<const u4*>(&x), reinterpret_cast<u4*>(p));
+  } else if constexpr (sizeof(T) * N == 8) {
+    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+    __builtin_nontemporal_store(*reinterpret_cast<const u2*>(&x), reinterpret_cast<u2*>(p));
+  } else {
+    *reinterpret_cast<vec<T, N>*>(p) = x;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store_nt(T* __restrict__ p, T x) {
+  if constexpr (sizeof(T) == 4 || sizeof(T) == 8) {
+    __builtin_nontemporal_store(x, p);
+  } else {
+    *p = x;
+  }
+}
+
+// ---- 32-bit lane moves -------------------------------------------------
+
+template <typename T>
+__device__ __forceinline__ int to_bits(T v) {
+  if constexpr (sizeof(T) == 4) return __builtin_bit_cast(int, v);
+  else return static_cast<int>(v);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_bits(int b) {
+  if constexpr (sizeof(T) == 4) return __builtin_bit_cast(T, b);
+  else return static_cast<T>(b);
+}
+
+// DPP move within a 16-lane row. Controls used (CDNA3/4 ISA, DPP_CTRL):
+//   0xB1 quad_perm[1,0,3,2]  (lane ^ 1)
+//   0x4E quad_perm[2,3,0,1]  (lane ^ 2)
+//   0x141 row_half_mirror    (lane i <-> 7-i within each 8 lanes)
+//   0x140 row_mirror         (lane i <-> 15-i within each 16 lanes)
+template <int CTRL, typename T>
+__device__ __forceinline__ T dpp(T v) {
+  return from_bits<T>(__builtin_amdgcn_update_dpp(0, to_bits(v), CTRL, 0xF, 0xF, false));
+}
+
+template <typename T>
+__device__ __forceinline__ T xor_lanes(T v, int mask) {
+  return from_bits<T>(__shfl_xor(to_bits(v), mask, 64));
+}
+
+// One butterfly step of a segmented all-reduce. Before the step every group
+// of OFF consecutive lanes holds one value per group; after it every group
+// of 2*OFF lanes does. OFF 4 and 8 use mirrors: the partner sits in the other
+// half of the 2*OFF group, which is all a reduction needs.
+template <int OFF, typename T>
+__device__ __forceinline__ T partner(T v) {
+  if constexpr (OFF == 1) return dpp<0xB1>(v);
+  else if constexpr (OFF == 2) return dpp<0x4E>(v);
+  else if constexpr (OFF == 4) return dpp<0x141>(v);
+  else if constexpr (OFF == 8) return dpp<0x140>(v);
+  else return xor_lanes(v, OFF);
+}
+
+// All-reduce over aligned segments of SEG lanes (SEG a power of two <= 64);
+// every lane of a segment ends with the segment's total. `op` must be
+// associative and commutative (the classifier only admits such combiners).
+template <int SEG, typename T, typename Op>
+__device__ __forceinline__ T seg_allreduce(T v, Op op) {
+  if constexpr (SEG >= 2) v = op(v, partner<1>(v));
+  if constexpr (SEG >= 4) v = op(v, partner<2>(v));
+  if constexpr (SEG >= 8) v = op(v, partner<4>(v));
+  if constexpr (SEG >= 16) v = op(v, partner<8>(v));
+  if constexpr (SEG >= 32) v = op(v, partner<16>(v));
+  if constexpr (SEG >= 64) v = op(v, partner<32>(v));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
+__device__ __forceinline__ uint32_t wave_id() { return threadIdx.x >> 6; }
+
+__device__ __forceinline__ uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1u) / b; }
+
+}  // namespace hip
+}  // namespace tca
+
+#endif  // TCA_HIP_DEVICE_H_

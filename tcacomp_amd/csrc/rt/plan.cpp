@@ -1,0 +1,434 @@
+// plan.cpp — parse, bind and pack a launch plan (format in plan.h).
+#include "plan.h"
+
+#include <cstring>
+#include <sstream>
+
+namespace tca {
+namespace plan {
+
+namespace {
+
+const char* kDtypeNames[] = {"f32", "f16", "bf16", "i32", "u32", "i8", "i16", "u8", "u16", "bool"};
+const size_t kDtypeBytes[] = {4, 2, 2, 4, 4, 1, 2, 1, 2, 1};
+
+int FindDim(const Plan& p, const std::string& n) {
+  for (size_t i = 0; i < p.dims.size(); ++i)
+    if (p.dims[i].name == n) return static_cast<int>(i);
+  return -1;
+}
+int FindTensor(const Plan& p, const std::string& n) {
+  for (size_t i = 0; i < p.tensors.size(); ++i)
+    if (p.tensors[i].name == n) return static_cast<int>(i);
+  return -1;
+}
+int FindScalar(const Plan& p, const std::string& n) {
+  for (size_t i = 0; i < p.scalars.size(); ++i)
+    if (p.scalars[i].name == n) return static_cast<int>(i);
+  return -1;
+}
+
+bool ParseU64(const std::string& s, uint64_t* v) {
+  if (s.empty()) return false;
+  uint64_t x = 0;
+  for (char c : s) {
+    if (c < '0' || c > '9') return false;
+    uint64_t nx = x * 10 + static_cast<uint64_t>(c - '0');
+    if (nx / 10 != x) return false;
+    x = nx;
+  }
+  *v = x;
+  return true;
+}
+
+bool ParseTerm(const Plan& p, const std::string& s, Term* t, std::string* err) {
+  size_t slash = s.find('/');
+  if (slash == std::string::npos) {
+    *err = "grid term '" + s + "' lacks a '/divisor'";
+    return false;
+  }
+  if (!ParseU64(s.substr(slash + 1), &t->divisor) || t->divisor == 0) {
+    *err = "grid term '" + s + "' has a bad divisor";
+    return false;
+  }
+  std::string prod = s.substr(0, slash);
+  size_t start = 0;
+  while (start <= prod.size()) {
+    size_t star = prod.find('*', start);
+    std::string f = prod.substr(start, star == std::string::npos ? std::string::npos : star - start);
+    uint64_t c = 0;
+    if (ParseU64(f, &c)) {
+      t->const_factor *= c;
+    } else {
+      int d = FindDim(p, f);
+      if (d < 0) {
+        *err = "grid term '" + s + "' names unknown dim '" + f + "'";
+        return false;
+      }
+      t->dim_factors.push_back(d);
+    }
+    if (star == std::string::npos) break;
+    start = star + 1;
+  }
+  return true;
+}
+
+}  // namespace
+
+size_t DtypeBytes(int dtype) {
+  if (dtype < 0 || dtype > TCA_BOOL) return 0;
+  return kDtypeBytes[dtype];
+}
+
+const char* DtypeName(int dtype) {
+  if (dtype < 0 || dtype > TCA_BOOL) return "?";
+  return kDtypeNames[dtype];
+}
+
+int DtypeFromName(const std::string& s) {
+  for (int i = 0; i <= TCA_BOOL; ++i)
+    if (s == kDtypeNames[i]) return i;
+  return -1;
+}
+
+size_t Plan::ParamTensorCount() const {
+  size_t n = 0;
+  for (const auto& t : tensors)
+    if (t.role != Role::Local) ++n;
+  return n;
+}
+
+std::vector<int> Plan::FreeDims() const {
+  std::vector<bool> carried(dims.size(), false);
+  for (const auto& t : tensors) {
+    if (t.role == Role::Local) continue;
+    for (int d : t.dims) carried[d] = true;
+  }
+  std::vector<int> out;
+  for (size_t i = 0; i < dims.size(); ++i)
+    if (dims[i].extent == 0 && !carried[i]) out.push_back(static_cast<int>(i));
+  return out;
+}
+
+bool Parse(const std::string& text, Plan* out, std::string* err) {
+  Plan p;
+  std::istringstream in(text);
+  std::string line;
+  bool header = false, ended = false;
+  int lineno = 0;
+  auto bad = [&](const std::string& m) {
+    *err = "line " + std::to_string(lineno) + ": " + m;
+    return false;
+  };
+  while (std::getline(in, line)) {
+    ++lineno;
+    size_t hash = line.find('#');
+    if (hash != std::string::npos) line = line.substr(0, hash);
+    std::istringstream ls(line);
+    std::vector<std::string> tok;
+    std::string w;
+    while (ls >> w) tok.push_back(w);
+    if (tok.empty()) continue;
+    if (ended) return bad("text after 'end'");
+    const std::string& kw = tok[0];
+    if (!header) {
+      if (kw != "tca-plan" || tok.size() != 2 || tok[1] != "1") return bad("expected 'tca-plan 1'");
+      header = true;
+      continue;
+    }
+    if (kw == "program") {
+      if (tok.size() != 2) return bad("program <name>");
+      p.name = tok[1];
+    } else if (kw == "dim") {
+      uint64_t e = 0;
+      if (tok.size() != 3 || !ParseU64(tok[2], &e)) return bad("dim <name> <extent>");
+      if (e > 0xffffffffull) return bad("dim extent exceeds u32");
+      if (FindDim(p, tok[1]) >= 0) return bad("duplicate dim " + tok[1]);
+      p.dims.push_back({tok[1], e});
+    } else if (kw == "tensor") {
+      uint64_t rank = 0;
+      if (tok.size() < 5 || !ParseU64(tok[4], &rank) || tok.size() != 5 + rank)
+        return bad("tensor <name> <dtype> <role> <rank> <dims...>");
+      if (rank > TCA_MAX_RANK) return bad("tensor rank exceeds TCA_MAX_RANK");
+      Tensor t;
+      t.name = tok[1];
+      t.dtype = DtypeFromName(tok[2]);
+      if (t.dtype < 0) return bad("unknown dtype " + tok[2]);
+      if (tok[3] == "in") t.role = Role::In;
+      else if (tok[3] == "out") t.role = Role::Out;
+      else if (tok[3] == "local") t.role = Role::Local;
+      else return bad("unknown tensor role " + tok[3]);
+      for (uint64_t i = 0; i < rank; ++i) {
+        int d = FindDim(p, tok[5 + i]);
+        if (d < 0) return bad("tensor " + t.name + " names unknown dim " + tok[5 + i]);
+        t.dims.push_back(d);
+      }
+      if (FindTensor(p, t.name) >= 0) return bad("duplicate tensor " + t.name);
+      p.tensors.push_back(t);
+    } else if (kw == "scalar") {
+      if (tok.size() != 3) return bad("scalar <name> <dtype>");
+      Scalar s{tok[1], DtypeFromName(tok[2])};
+      if (s.dtype < 0) return bad("unknown dtype " + tok[2]);
+      p.scalars.push_back(s);
+    } else if (kw == "kernel") {
+      uint64_t block = 0, lds = 0, nterms = 0;
+      if (tok.size() < 5 || !ParseU64(tok[2], &block) || !ParseU64(tok[3], &lds) || !ParseU64(tok[4], &nterms) ||
+          tok.size() != 5 + nterms)
+        return bad("kernel <symbol> <block> <lds> <n-terms> <terms...>");
+      Kernel k;
+      k.symbol = tok[1];
+      k.block = static_cast<uint32_t>(block);
+      k.lds = static_cast<uint32_t>(lds);
+      for (uint64_t i = 0; i < nterms; ++i) {
+        Term t;
+        std::string e;
+        if (!ParseTerm(p, tok[5 + i], &t, &e)) return bad(e);
+        k.grid.push_back(t);
+      }
+      p.kernels.push_back(k);
+    } else if (kw == "arg") {
+      if (p.kernels.empty()) return bad("arg before any kernel");
+      if (tok.size() != 3) return bad("arg <ptr|dim|scalar> <name>");
+      Arg a;
+      if (tok[1] == "ptr") {
+        a.kind = ArgKind::Ptr;
+        a.index = FindTensor(p, tok[2]);
+      } else if (tok[1] == "dim") {
+        a.kind = ArgKind::Dim;
+        a.index = FindDim(p, tok[2]);
+      } else if (tok[1] == "scalar") {
+        a.kind = ArgKind::Scalar;
+        a.index = FindScalar(p, tok[2]);
+      } else {
+        return bad("unknown arg kind " + tok[1]);
+      }
+      if (a.index < 0) return bad("arg names unknown " + tok[1] + " " + tok[2]);
+      p.kernels.back().args.push_back(a);
+    } else if (kw == "end") {
+      ended = true;
+    } else {
+      return bad("unknown record '" + kw + "'");
+    }
+  }
+  if (!header) return bad("empty plan");
+  if (!ended) return bad("missing 'end'");
+  if (p.kernels.empty()) return bad("plan has no kernel");
+  *out = p;
+  return true;
+}
+
+std::string Serialize(const Plan& p) {
+  std::ostringstream o;
+  o << "tca-plan 1\nprogram " << p.name << "\n";
+  for (const auto& d : p.dims) o << "dim " << d.name << " " << d.extent << "\n";
+  for (const auto& t : p.tensors) {
+    o << "tensor " << t.name << " " << DtypeName(t.dtype) << " "
+      << (t.role == Role::In ? "in" : t.role == Role::Out ? "out" : "local") << " " << t.dims.size();
+    for (int d : t.dims) o << " " << p.dims[d].name;
+    o << "\n";
+  }
+  for (const auto& s : p.scalars) o << "scalar " << s.name << " " << DtypeName(s.dtype) << "\n";
+  for (const auto& k : p.kernels) {
+    o << "kernel " << k.symbol << " " << k.block << " " << k.lds << " " << k.grid.size();
+    for (const auto& t : k.grid) {
+      o << " ";
+      bool first = true;
+      if (t.const_factor != 1 || t.dim_factors.empty()) {
+        o << t.const_factor;
+        first = false;
+      }
+      for (int d : t.dim_factors) {
+        if (!first) o << "*";
+        o << p.dims[d].name;
+        first = false;
+      }
+      o << "/" << t.divisor;
+    }
+    o << "\n";
+    for (const auto& a : k.args) {
+      if (a.kind == ArgKind::Ptr) o << "arg ptr " << p.tensors[a.index].name << "\n";
+      else if (a.kind == ArgKind::Dim) o << "arg dim " << p.dims[a.index].name << "\n";
+      else o << "arg scalar " << p.scalars[a.index].name << "\n";
+    }
+  }
+  o << "end\n";
+  return o.str();
+}
+
+int Bind(const Plan& p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
+         uint32_t n_free_dims, std::vector<uint32_t>* dims, std::string* err) {
+  const size_t want = p.ParamTensorCount();
+  if (n_tensors != want) {
+    *err = "program " + p.name + " takes " + std::to_string(want) + " tensor(s), got " + std::to_string(n_tensors);
+    return TCA_ERR_INVALID;
+  }
+  if (want > 0 && tensors == nullptr) {
+    *err = "null tensor array";
+    return TCA_ERR_INVALID;
+  }
+  std::vector<int> free = p.FreeDims();
+  if (n_free_dims != free.size()) {
+    *err = "program " + p.name + " takes " + std::to_string(free.size()) + " free dim(s), got " +
+           std::to_string(n_free_dims);
+    return TCA_ERR_INVALID;
+  }
+  if (!free.empty() && free_dims == nullptr) {
+    *err = "null free-dim array";
+    return TCA_ERR_INVALID;
+  }
+  dims->assign(p.dims.size(), 0);
+  std::vector<bool> known(p.dims.size(), false);
+  std::vector<std::string> supplier(p.dims.size());
+  for (size_t i = 0; i < p.dims.size(); ++i) {
+    if (p.dims[i].extent > 0) {
+      (*dims)[i] = static_cast<uint32_t>(p.dims[i].extent);
+      known[i] = true;
+      supplier[i] = "its const extent";
+    }
+  }
+  for (size_t i = 0; i < free.size(); ++i) {
+    (*dims)[free[i]] = free_dims[i];
+    known[free[i]] = true;
+    supplier[free[i]] = "the free-dim argument";
+  }
+  uint32_t ti = 0;
+  for (const auto& t : p.tensors) {
+    if (t.role == Role::Local) continue;
+    const tca_tensor& a = tensors[ti++];
+    if (a.rank != t.dims.size()) {
+      *err = "tensor " + t.name + " has rank " + std::to_string(a.rank) + ", the program declares " +
+             std::to_string(t.dims.size());
+      return TCA_ERR_SHAPE;
+    }
+    if (a.dtype != t.dtype) {
+      *err = std::string("tensor ") + t.name + " has dtype " + DtypeName(a.dtype) + ", the program declares " +
+             DtypeName(t.dtype);
+      return TCA_ERR_SHAPE;
+    }
+    uint64_t elems = 1;
+    for (size_t ax = 0; ax < t.dims.size(); ++ax) {
+      const int d = t.dims[ax];
+      elems *= a.dims[ax];
+      if (!known[d]) {
+        (*dims)[d] = a.dims[ax];
+        known[d] = true;
+        supplier[d] = t.name + ".Dim(" + std::to_string(ax) + ")";
+      } else if ((*dims)[d] != a.dims[ax]) {
+        *err = t.name + ".Dim(" + std::to_string(ax) + ") = " + std::to_string(a.dims[ax]) + " must equal " +
+               p.dims[d].name + " = " + std::to_string((*dims)[d]) + " (from " + supplier[d] + ")";
+        return TCA_ERR_SHAPE;
+      }
+    }
+    if (elems > 0 && a.data == nullptr) {
+      *err = "tensor " + t.name + " has a null data pointer";
+      return TCA_ERR_INVALID;
+    }
+    if (elems > 0 && (reinterpret_cast<uintptr_t>(a.data) % 16u) != 0u) {
+      *err = "tensor " + t.name + " data is not 16-byte aligned (vector loads need it)";
+      return TCA_ERR_INVALID;
+    }
+    if (elems > 0xffffffffull) {
+      *err = "tensor " + t.name + " has more than 2^32-1 elements (u32 index domain)";
+      return TCA_ERR_SHAPE;
+    }
+  }
+  for (size_t i = 0; i < p.dims.size(); ++i) {
+    if (!known[i]) {
+      *err = "dim " + p.dims[i].name + " is not bound by any tensor or free-dim argument";
+      return TCA_ERR_SHAPE;
+    }
+  }
+  return TCA_OK;
+}
+
+size_t TensorBytes(const Plan& p, size_t tensor, const std::vector<uint32_t>& dims) {
+  const Tensor& t = p.tensors[tensor];
+  size_t n = DtypeBytes(t.dtype);
+  for (int d : t.dims) n *= dims[d];
+  return n;
+}
+
+bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims, uint64_t* grid, std::string* err) {
+  (void)p;
+  uint64_t g = 1;
+  for (const auto& t : k.grid) {
+    uint64_t prod = t.const_factor;
+    for (int d : t.dim_factors) {
+      prod *= dims[d];
+      if (prod > (1ull << 62)) {
+        *err = "kernel " + k.symbol + ": grid term overflows";
+        return false;
+      }
+    }
+    uint64_t q = (prod + t.divisor - 1) / t.divisor;
+    g *= q;
+    if (g > (1ull << 62)) {
+      *err = "kernel " + k.symbol + ": grid overflows";
+      return false;
+    }
+  }
+  *grid = g;
+  return true;
+}
+
+bool PackArgs(const Kernel& k, const Plan& p, const std::vector<void*>& ptrs, const std::vector<uint32_t>& dims,
+              const double* scalars, std::vector<unsigned char>* blob, std::string* err) {
+  blob->clear();
+  auto put = [&](const void* src, size_t n) {
+    size_t off = (blob->size() + n - 1) / n * n;  // natural alignment
+    blob->resize(off + n, 0);
+    std::memcpy(blob->data() + off, src, n);
+  };
+  for (const auto& a : k.args) {
+    switch (a.kind) {
+      case ArgKind::Ptr: {
+        void* ptr = ptrs[a.index];
+        put(&ptr, sizeof(ptr));
+        break;
+      }
+      case ArgKind::Dim: {
+        uint32_t v = dims[a.index];
+        put(&v, sizeof(v));
+        break;
+      }
+      case ArgKind::Scalar: {
+        const double v = scalars[a.index];
+        switch (p.scalars[a.index].dtype) {
+          case TCA_F32:
+          case TCA_F16:
+          case TCA_BF16: {
+            float f = static_cast<float>(v);
+            put(&f, 4);
+            break;
+          }
+          case TCA_U32:
+          case TCA_U16:
+          case TCA_U8: {
+            uint32_t u = static_cast<uint32_t>(v);
+            put(&u, 4);
+            break;
+          }
+          case TCA_BOOL: {
+            int32_t b = v != 0.0 ? 1 : 0;
+            put(&b, 4);
+            break;
+          }
+          default: {
+            int32_t i = static_cast<int32_t>(v);
+            put(&i, 4);
+            break;
+          }
+        }
+        break;
+      }
+    }
+  }
+  if (blob->empty()) {
+    *err = "kernel " + k.symbol + " has no arguments";
+    return false;
+  }
+  return true;
+}
+
+}  // namespace plan
+}  // namespace tca

@@ -1,0 +1,108 @@
+// plan.h — the launch plan: what the HIP emitter writes beside a code object
+// and what the runtime's one launcher interprets.
+//
+// Text format (one record per line, '#' starts a comment):
+//   tca-plan 1
+//   program <name>
+//   dim <name> <extent>                        extent 0 = dynamic (u32 at run time)
+//   tensor <name> <dtype> <in|out|local> <rank> <dim-name>...
+//   scalar <name> <dtype>
+//   kernel <symbol> <block> <lds-bytes> <n-terms> <term>...
+//       term = <factor>[*<factor>...]/<divisor>, factor = dim name or integer;
+//       grid = product over terms of ceil(product(factors) / divisor)
+//   arg ptr <tensor> | arg dim <name> | arg scalar <name>    (for the last kernel)
+//   end
+//
+// The shape contract Bind() enforces is the reference launcher's
+// (internal/cg/cxx/launch.go:98-130): each dynamic dim takes its value from
+// its first tensor occurrence in declaration order and every later
+// occurrence must agree; a dynamic dim no tensor carries is a "free dim"
+// passed explicitly; const extents are checked against the tensors too.
+#ifndef TCA_RT_PLAN_H_
+#define TCA_RT_PLAN_H_
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "tca_rt.h"
+
+namespace tca {
+namespace plan {
+
+enum class Role { In, Out, Local };
+enum class ArgKind { Ptr, Dim, Scalar };
+
+struct Dim {
+  std::string name;
+  uint64_t extent = 0;  // 0 = dynamic
+};
+
+struct Tensor {
+  std::string name;
+  int dtype = TCA_F32;
+  Role role = Role::In;
+  std::vector<int> dims;  // indices into Plan::dims
+};
+
+struct Scalar {
+  std::string name;
+  int dtype = TCA_F32;
+};
+
+struct Term {
+  std::vector<int> dim_factors;  // indices into Plan::dims
+  uint64_t const_factor = 1;
+  uint64_t divisor = 1;
+};
+
+struct Arg {
+  ArgKind kind = ArgKind::Ptr;
+  int index = 0;  // tensor, dim or scalar index
+};
+
+struct Kernel {
+  std::string symbol;
+  uint32_t block = 256;
+  uint32_t lds = 0;
+  std::vector<Term> grid;
+  std::vector<Arg> args;
+};
+
+struct Plan {
+  std::string name;
+  std::vector<Dim> dims;
+  std::vector<Tensor> tensors;
+  std::vector<Scalar> scalars;
+  std::vector<Kernel> kernels;
+
+  size_t ParamTensorCount() const;
+  // Dynamic dims carried by no in/out tensor, in declaration order.
+  std::vector<int> FreeDims() const;
+};
+
+size_t DtypeBytes(int dtype);
+const char* DtypeName(int dtype);
+int DtypeFromName(const std::string& s);
+
+bool Parse(const std::string& text, Plan* out, std::string* err);
+std::string Serialize(const Plan& p);
+
+// Resolves every dim value from the caller's tensors and free dims. Returns
+// a TCA_* status; *dims receives one value per Plan::dims entry.
+int Bind(const Plan& p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
+         uint32_t n_free_dims, std::vector<uint32_t>* dims, std::string* err);
+
+size_t TensorBytes(const Plan& p, size_t tensor, const std::vector<uint32_t>& dims);
+bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims, uint64_t* grid, std::string* err);
+// Packs the kernel arguments per the HIP kernarg ABI (natural alignment):
+// pointers 8 bytes, dims u32, scalars 4 bytes (f32 for float types, i32/u32
+// for integers, i32 for bool).
+bool PackArgs(const Kernel& k, const Plan& p, const std::vector<void*>& ptrs, const std::vector<uint32_t>& dims,
+              const double* scalars, std::vector<unsigned char>* blob, std::string* err);
+
+}  // namespace plan
+}  // namespace tca
+
+#endif  // TCA_RT_PLAN_H_

@@ -1,0 +1,440 @@
+// runtime.cpp — the tcacomp runtime over plain HIP, behind the C ABI of
+// include/tca_rt.h.
+//
+// Reference counterparts:
+//   runtime/tca/check.h:18-44      TCA_REQUIRE / TCA_CUDA_CHECK (exceptions)
+//   runtime/tca/launch.h:37-58     ValidateLaunch (32-lane grammar, SMEM opt-in)
+//   internal/cg/cxx/launch.go:23-156  the generated per-kernel launcher
+// The launcher is data-driven here: the emitter writes a launch plan next to
+// the code object and tca_program_launch interprets it, so the shape contract
+// (every dim occurrence must agree), geometry validation and argument packing
+// live in one audited place instead of being re-emitted per kernel.
+#include "tca_rt.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "plan.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(TCA_ERR_HIP, "%s failed: %s (%d)", what, hipGetErrorString(e), static_cast<int>(e));
+}
+
+#define TCA_HIP_TRY(expr)                       \
+  do {                                          \
+    hipError_t e_ = (expr);                     \
+    if (e_ != hipSuccess) return hip_fail(e_, #expr); \
+  } while (0)
+
+// Per-device launch limits, queried once per device.
+struct DeviceLimits {
+  bool valid = false;
+  int max_threads = 1024;
+  int max_lds = 65536;
+};
+
+std::mutex g_limits_mu;
+DeviceLimits g_limits[64];
+
+int query_limits(DeviceLimits* out) {
+  int dev = 0;
+  TCA_HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return fail(TCA_ERR_INVALID, "device id %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_limits_mu);
+  if (!g_limits[dev].valid) {
+    DeviceLimits l;
+    TCA_HIP_TRY(hipDeviceGetAttribute(&l.max_threads, hipDeviceAttributeMaxThreadsPerBlock, dev));
+    TCA_HIP_TRY(hipDeviceGetAttribute(&l.max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+    l.valid = true;
+    g_limits[dev] = l;
+  }
+  *out = g_limits[dev];
+  return TCA_OK;
+}
+
+// Launch grammar shared by the GPU path and the host-only validator: the
+// wave64 restatement of runtime/tca/launch.h:37-58.
+int check_geometry(uint32_t grid, uint32_t block, uint32_t lds, int max_threads, int max_lds) {
+  if (grid == 0) return fail(TCA_ERR_LAUNCH, "launch: grid must be >= 1 workgroup");
+  if (grid > 0x7fffffffu) return fail(TCA_ERR_LAUNCH, "launch: grid %u exceeds 2^31-1 workgroups", grid);
+  if (block == 0 || block % 64u != 0)
+    return fail(TCA_ERR_LAUNCH, "launch: block %u is not a positive multiple of the 64-lane wavefront", block);
+  if (block > static_cast<uint32_t>(max_threads))
+    return fail(TCA_ERR_LAUNCH, "launch: block %u exceeds the device limit of %d threads", block, max_threads);
+  if (lds > static_cast<uint32_t>(max_lds))
+    return fail(TCA_ERR_LAUNCH, "launch: %u bytes of LDS exceed the device limit of %d", lds, max_lds);
+  return TCA_OK;
+}
+
+}  // namespace
+
+struct tca_module_s {
+  hipModule_t mod = nullptr;
+};
+
+struct tca_event_s {
+  hipEvent_t ev = nullptr;
+};
+
+struct tca_program_s {
+  tca::plan::Plan plan;
+  hipModule_t mod = nullptr;
+  std::vector<hipFunction_t> funcs;
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
+  std::mutex mu;  // guards the workspace
+};
+
+extern "C" {
+
+const char* tca_rt_last_error(void) { return g_last_error.c_str(); }
+
+int tca_rt_init(int device) {
+  int n = 0;
+  TCA_HIP_TRY(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail(TCA_ERR_INVALID, "init: device %d not present (%d devices)", device, n);
+  TCA_HIP_TRY(hipSetDevice(device));
+  DeviceLimits l;
+  return query_limits(&l);
+}
+
+int tca_rt_device_info(int device, tca_device_info* out) {
+  if (out == nullptr) return fail(TCA_ERR_INVALID, "device_info: null output");
+  hipDeviceProp_t p;
+  TCA_HIP_TRY(hipGetDeviceProperties(&p, device));
+  std::memset(out, 0, sizeof(*out));
+  std::snprintf(out->name, sizeof(out->name), "%s", p.name);
+  std::snprintf(out->arch, sizeof(out->arch), "%.63s", p.gcnArchName);
+  out->compute_units = p.multiProcessorCount;
+  out->wavefront_size = p.warpSize;
+  out->max_threads_per_block = p.maxThreadsPerBlock;
+  out->max_lds_per_block = static_cast<int32_t>(p.sharedMemPerBlock);
+  out->clock_khz = p.clockRate;
+  out->total_global_mem = p.totalGlobalMem;
+  return TCA_OK;
+}
+
+int tca_rt_device_sync(void) {
+  TCA_HIP_TRY(hipDeviceSynchronize());
+  return TCA_OK;
+}
+
+int tca_rt_malloc(void** ptr, size_t bytes) {
+  if (ptr == nullptr) return fail(TCA_ERR_INVALID, "malloc: null output");
+  *ptr = nullptr;
+  if (bytes == 0) return TCA_OK;
+  TCA_HIP_TRY(hipMalloc(ptr, bytes));
+  return TCA_OK;
+}
+
+int tca_rt_free(void* ptr) {
+  if (ptr == nullptr) return TCA_OK;
+  TCA_HIP_TRY(hipFree(ptr));
+  return TCA_OK;
+}
+
+int tca_rt_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return TCA_OK;
+  TCA_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  return TCA_OK;
+}
+
+int tca_rt_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return TCA_OK;
+  TCA_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return TCA_OK;
+}
+
+int tca_rt_memset(void* dst, int value, size_t bytes) {
+  if (bytes == 0) return TCA_OK;
+  TCA_HIP_TRY(hipMemset(dst, value, bytes));
+  return TCA_OK;
+}
+
+int tca_rt_stream_create(tca_stream_t* out) {
+  if (out == nullptr) return fail(TCA_ERR_INVALID, "stream_create: null output");
+  hipStream_t s = nullptr;
+  // Default priority only: the stream carries no priority attribute.
+  TCA_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *out = s;
+  return TCA_OK;
+}
+
+int tca_rt_stream_destroy(tca_stream_t s) {
+  if (s == nullptr) return TCA_OK;
+  TCA_HIP_TRY(hipStreamDestroy(static_cast<hipStream_t>(s)));
+  return TCA_OK;
+}
+
+int tca_rt_stream_sync(tca_stream_t s) {
+  TCA_HIP_TRY(hipStreamSynchronize(static_cast<hipStream_t>(s)));
+  return TCA_OK;
+}
+
+int tca_rt_event_create(tca_event* out) {
+  if (out == nullptr) return fail(TCA_ERR_INVALID, "event_create: null output");
+  auto* e = new tca_event_s;
+  hipError_t err = hipEventCreate(&e->ev);
+  if (err != hipSuccess) {
+    delete e;
+    return hip_fail(err, "hipEventCreate");
+  }
+  *out = e;
+  return TCA_OK;
+}
+
+int tca_rt_event_destroy(tca_event ev) {
+  if (ev == nullptr) return TCA_OK;
+  hipError_t err = hipEventDestroy(ev->ev);
+  delete ev;
+  if (err != hipSuccess) return hip_fail(err, "hipEventDestroy");
+  return TCA_OK;
+}
+
+int tca_rt_event_record(tca_event ev, tca_stream_t s) {
+  if (ev == nullptr) return fail(TCA_ERR_INVALID, "event_record: null event");
+  TCA_HIP_TRY(hipEventRecord(ev->ev, static_cast<hipStream_t>(s)));
+  return TCA_OK;
+}
+
+int tca_rt_event_elapsed_ms(tca_event start, tca_event stop, float* ms) {
+  if (start == nullptr || stop == nullptr || ms == nullptr) return fail(TCA_ERR_INVALID, "event_elapsed: null argument");
+  TCA_HIP_TRY(hipEventSynchronize(stop->ev));
+  TCA_HIP_TRY(hipEventElapsedTime(ms, start->ev, stop->ev));
+  return TCA_OK;
+}
+
+int tca_rt_module_load(const char* hsaco_path, tca_module* out) {
+  if (hsaco_path == nullptr || out == nullptr) return fail(TCA_ERR_INVALID, "module_load: null argument");
+  std::ifstream f(hsaco_path, std::ios::binary);
+  if (!f) return fail(TCA_ERR_NOT_FOUND, "module_load: cannot open %s", hsaco_path);
+  auto* m = new tca_module_s;
+  hipError_t err = hipModuleLoad(&m->mod, hsaco_path);
+  if (err != hipSuccess) {
+    delete m;
+    return hip_fail(err, "hipModuleLoad");
+  }
+  *out = m;
+  return TCA_OK;
+}
+
+int tca_rt_module_unload(tca_module m) {
+  if (m == nullptr) return TCA_OK;
+  hipError_t err = hipModuleUnload(m->mod);
+  delete m;
+  if (err != hipSuccess) return hip_fail(err, "hipModuleUnload");
+  return TCA_OK;
+}
+
+int tca_rt_validate_launch(uint32_t grid, uint32_t block, uint32_t lds_bytes) {
+  int max_threads = 1024, max_lds = 160 * 1024;  // gfx950 limits when no device is queried
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) == hipSuccess && ndev > 0) {
+    DeviceLimits l;
+    if (query_limits(&l) == TCA_OK) {
+      max_threads = l.max_threads;
+      max_lds = l.max_lds;
+    }
+  }
+  return check_geometry(grid, block, lds_bytes, max_threads, max_lds);
+}
+
+int tca_rt_launch(tca_module m, const char* kernel, uint32_t grid, uint32_t block, uint32_t lds_bytes,
+                  void* args, size_t args_size, tca_stream_t s) {
+  if (m == nullptr || kernel == nullptr) return fail(TCA_ERR_INVALID, "launch: null module or kernel name");
+  DeviceLimits l;
+  int rc = query_limits(&l);
+  if (rc != TCA_OK) return rc;
+  rc = check_geometry(grid, block, lds_bytes, l.max_threads, l.max_lds);
+  if (rc != TCA_OK) return rc;
+  hipFunction_t fn = nullptr;
+  hipError_t err = hipModuleGetFunction(&fn, m->mod, kernel);
+  if (err != hipSuccess) return fail(TCA_ERR_NOT_FOUND, "launch: kernel %s not in module (%s)", kernel, hipGetErrorString(err));
+  size_t size = args_size;
+  void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
+  TCA_HIP_TRY(hipModuleLaunchKernel(fn, grid, 1, 1, block, 1, 1, lds_bytes, static_cast<hipStream_t>(s), nullptr, config));
+  return TCA_OK;
+}
+
+int tca_program_parse(const char* plan_text, tca_program* out) {
+  if (plan_text == nullptr || out == nullptr) return fail(TCA_ERR_INVALID, "program_parse: null argument");
+  auto* p = new tca_program_s;
+  std::string err;
+  if (!tca::plan::Parse(plan_text, &p->plan, &err)) {
+    delete p;
+    return fail(TCA_ERR_INVALID, "plan: %s", err.c_str());
+  }
+  *out = p;
+  return TCA_OK;
+}
+
+int tca_program_load(const char* hsaco_path, const char* plan_text, tca_program* out) {
+  if (hsaco_path == nullptr || out == nullptr) return fail(TCA_ERR_INVALID, "program_load: null argument");
+  tca_program p = nullptr;
+  int rc = tca_program_parse(plan_text, &p);
+  if (rc != TCA_OK) return rc;
+  std::ifstream f(hsaco_path, std::ios::binary);
+  if (!f) {
+    delete p;
+    return fail(TCA_ERR_NOT_FOUND, "program_load: cannot open %s", hsaco_path);
+  }
+  hipError_t err = hipModuleLoad(&p->mod, hsaco_path);
+  if (err != hipSuccess) {
+    delete p;
+    return hip_fail(err, "hipModuleLoad");
+  }
+  for (const auto& k : p->plan.kernels) {
+    hipFunction_t fn = nullptr;
+    err = hipModuleGetFunction(&fn, p->mod, k.symbol.c_str());
+    if (err != hipSuccess) {
+      (void)hipModuleUnload(p->mod);
+      delete p;
+      return fail(TCA_ERR_NOT_FOUND, "program_load: kernel %s missing from %s", k.symbol.c_str(), hsaco_path);
+    }
+    p->funcs.push_back(fn);
+  }
+  *out = p;
+  return TCA_OK;
+}
+
+int tca_program_unload(tca_program p) {
+  if (p == nullptr) return TCA_OK;
+  int rc = TCA_OK;
+  if (p->workspace != nullptr) {
+    hipError_t e = hipFree(p->workspace);
+    if (e != hipSuccess) rc = hip_fail(e, "hipFree(workspace)");
+  }
+  if (p->mod != nullptr) {
+    hipError_t e = hipModuleUnload(p->mod);
+    if (e != hipSuccess && rc == TCA_OK) rc = hip_fail(e, "hipModuleUnload");
+  }
+  delete p;
+  return rc;
+}
+
+int tca_program_signature(tca_program p, uint32_t* n_tensors, uint32_t* n_free_dims, uint32_t* n_scalars,
+                          uint32_t* n_kernels) {
+  if (p == nullptr) return fail(TCA_ERR_INVALID, "program_signature: null program");
+  const auto& pl = p->plan;
+  if (n_tensors) *n_tensors = static_cast<uint32_t>(pl.ParamTensorCount());
+  if (n_free_dims) *n_free_dims = static_cast<uint32_t>(pl.FreeDims().size());
+  if (n_scalars) *n_scalars = static_cast<uint32_t>(pl.scalars.size());
+  if (n_kernels) *n_kernels = static_cast<uint32_t>(pl.kernels.size());
+  return TCA_OK;
+}
+
+const char* tca_program_kernel_name(tca_program p, uint32_t i) {
+  if (p == nullptr || i >= p->plan.kernels.size()) return nullptr;
+  return p->plan.kernels[i].symbol.c_str();
+}
+
+int tca_program_check(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
+                      uint32_t n_free_dims) {
+  if (p == nullptr) return fail(TCA_ERR_INVALID, "program_check: null program");
+  std::vector<uint32_t> dims;
+  std::string err;
+  int code = tca::plan::Bind(p->plan, tensors, n_tensors, free_dims, n_free_dims, &dims, &err);
+  if (code != TCA_OK) return fail(code, "%s", err.c_str());
+  return TCA_OK;
+}
+
+int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
+                       uint32_t n_free_dims, const double* scalars, uint32_t n_scalars, tca_stream_t stream) {
+  if (p == nullptr) return fail(TCA_ERR_INVALID, "program_launch: null program");
+  if (p->mod == nullptr) return fail(TCA_ERR_INVALID, "program_launch: program was parsed, not loaded");
+  const auto& pl = p->plan;
+  std::vector<uint32_t> dims;
+  std::string err;
+  int code = tca::plan::Bind(pl, tensors, n_tensors, free_dims, n_free_dims, &dims, &err);
+  if (code != TCA_OK) return fail(code, "%s", err.c_str());
+  if (n_scalars != pl.scalars.size())
+    return fail(TCA_ERR_INVALID, "program %s takes %zu scalar(s), got %u", pl.name.c_str(), pl.scalars.size(), n_scalars);
+  if (n_scalars > 0 && scalars == nullptr) return fail(TCA_ERR_INVALID, "program_launch: null scalars");
+
+  // HBM locals: one workspace, each local at a 256-byte aligned offset.
+  std::vector<size_t> local_off(pl.tensors.size(), 0);
+  size_t ws_bytes = 0;
+  for (size_t t = 0; t < pl.tensors.size(); ++t) {
+    if (pl.tensors[t].role != tca::plan::Role::Local) continue;
+    local_off[t] = ws_bytes;
+    ws_bytes += (tca::plan::TensorBytes(pl, t, dims) + 255u) & ~static_cast<size_t>(255u);
+  }
+  void* ws = nullptr;
+  if (ws_bytes > 0) {
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (p->workspace_bytes < ws_bytes) {
+      if (p->workspace != nullptr) {
+        // The previous workspace may still be read by queued kernels.
+        TCA_HIP_TRY(hipDeviceSynchronize());
+        TCA_HIP_TRY(hipFree(p->workspace));
+        p->workspace = nullptr;
+        p->workspace_bytes = 0;
+      }
+      TCA_HIP_TRY(hipMalloc(&p->workspace, ws_bytes));
+      p->workspace_bytes = ws_bytes;
+    }
+    ws = p->workspace;
+  }
+
+  // Device pointer of each tensor slot (params from the caller, locals from
+  // the workspace).
+  std::vector<void*> ptrs(pl.tensors.size(), nullptr);
+  {
+    uint32_t ti = 0;
+    for (size_t t = 0; t < pl.tensors.size(); ++t) {
+      if (pl.tensors[t].role == tca::plan::Role::Local) {
+        ptrs[t] = static_cast<char*>(ws) + local_off[t];
+      } else {
+        ptrs[t] = tensors[ti++].data;
+      }
+    }
+  }
+
+  DeviceLimits l;
+  int rc = query_limits(&l);
+  if (rc != TCA_OK) return rc;
+  for (size_t ki = 0; ki < pl.kernels.size(); ++ki) {
+    const auto& k = pl.kernels[ki];
+    uint64_t grid = 0;
+    if (!tca::plan::GridSize(k, pl, dims, &grid, &err)) return fail(TCA_ERR_LAUNCH, "%s", err.c_str());
+    if (grid == 0) continue;  // nothing to compute (an empty output)
+    if (grid > 0x7fffffffull)
+      return fail(TCA_ERR_LAUNCH, "kernel %s: grid %llu exceeds 2^31-1", k.symbol.c_str(),
+                  static_cast<unsigned long long>(grid));
+    rc = check_geometry(static_cast<uint32_t>(grid), k.block, k.lds, l.max_threads, l.max_lds);
+    if (rc != TCA_OK) return rc;
+    std::vector<unsigned char> blob;
+    if (!tca::plan::PackArgs(k, pl, ptrs, dims, scalars, &blob, &err)) return fail(TCA_ERR_INVALID, "%s", err.c_str());
+    size_t size = blob.size();
+    void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, blob.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
+                      HIP_LAUNCH_PARAM_END};
+    hipError_t e = hipModuleLaunchKernel(p->funcs[ki], static_cast<uint32_t>(grid), 1, 1, k.block, 1, 1, k.lds,
+                                         static_cast<hipStream_t>(stream), nullptr, config);
+    if (e != hipSuccess) return hip_fail(e, "hipModuleLaunchKernel");
+  }
+  return TCA_OK;
+}
+
+}  // extern "C"

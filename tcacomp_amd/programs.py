@@ -1,0 +1,305 @@
+"""DSL programs: the benchmark configurations and the reference's suite.
+
+Each builder here is written against the pkg API exactly as a user of the
+reference would write it (pkg/chain.go rung order). Dims that the reference
+declares dynamic stay dynamic, so one code object serves every test size;
+the row length of the fused row configurations is a compile-time constant
+(as the reference's `8u`-style const dims are), which is what lets the row
+live in registers.
+
+Configurations:
+  scale_relu      C1  z = max(a*x + y, 0)            (degenerate-reduce encoding,
+                                                      testing/kernels/runtime/scale_copy.tca:3-10)
+  scale_relu_map  C1  same, elementwise Store rung   (wall W1 lifted)
+  row_sum_max     C2  row sum and row max             (two chains, one fused kernel)
+  softmax         C3  row softmax via two locals
+  layernorm       C4  mean/variance locals, then normalise with gamma/beta
+  gemm_f32        C5  C = A.B fp32                    (testing/kernels/llm/gemm.tca:7-22)
+  gemm_bf16       C5  C = cast(A).cast(B), bf16 inputs, fp32 accumulate
+
+Reference suite (testing/kernels/**.tca, shapes in testing/suite.toml): see
+SUITE below.
+"""
+from .pkg import (TBF16, TF32, At, Call, Cast, NewBuilder)
+
+NEG_INF = float("-inf")
+
+
+def _sum(b):
+    return lambda acc, v: b.Add(acc, v)
+
+
+def scale_relu(cols=0):
+    """C1 in the reference-legal encoding: x, y carry a trailing extent-1
+    axis that a degenerate reduce drops."""
+    b = NewBuilder("scale_relu")
+    M, N, U = b.Dim("M", 0), b.Dim("N", cols), b.Dim("e1", 1)
+    x = b.Tensor("x", TF32, M, N, U)
+    y = b.Tensor("y", TF32, M, N, U)
+    z = b.Tensor("z", TF32, M, N)
+    a = b.ScalarParam("a", TF32)
+    (b.Stmt().Iter(M, N, U)
+     .Map([At(x, M, N, U), At(y, M, N, U)], lambda l, r: Call("fmaxf", b.Add(b.Mul(a, l), r), b.Float32(0)))
+     .As(M, N, U)
+     .Reduce(b.Float32(0), _sum(b))
+     .Store(z, M, N))
+    return b.Build()
+
+
+def scale_relu_map():
+    """C1 written directly as an elementwise chain (Store after the root as)."""
+    b = NewBuilder("scale_relu_map")
+    M, N = b.Dim("M", 0), b.Dim("N", 0)
+    x = b.Tensor("x", TF32, M, N)
+    y = b.Tensor("y", TF32, M, N)
+    z = b.Tensor("z", TF32, M, N)
+    a = b.ScalarParam("a", TF32)
+    (b.Stmt().Iter(M, N)
+     .Map([At(x, M, N), At(y, M, N)], lambda l, r: Call("fmaxf", b.Add(b.Mul(a, l), r), b.Float32(0)))
+     .As(M, N)
+     .Store(z, M, N))
+    return b.Build()
+
+
+def row_sum_max(cols=8192):
+    """C2: two chains over the same nest; GVN-style fusion makes them one
+    kernel reading x once."""
+    b = NewBuilder("row_sum_max_%d" % cols)
+    R, C = b.Dim("R", 0), b.Dim("C", cols)
+    x = b.Tensor("x", TF32, R, C)
+    s = b.Tensor("sum", TF32, R)
+    m = b.Tensor("max", TF32, R)
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C)
+     .Reduce(b.Float32(0), _sum(b)).Store(s, R))
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C)
+     .Reduce(b.Float32(NEG_INF), lambda acc, v: Call("fmaxf", acc, v)).Store(m, R))
+    return b.Build()
+
+
+def softmax(cols=4096):
+    """C3: y = exp(x - rowmax) / rowsum(exp(x - rowmax))."""
+    b = NewBuilder("softmax_%d" % cols)
+    R, C = b.Dim("R", 0), b.Dim("C", cols)
+    x = b.Tensor("x", TF32, R, C)
+    y = b.Tensor("y", TF32, R, C)
+    mx = b.Local("mx", TF32, R)
+    den = b.Local("den", TF32, R)
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C)
+     .Reduce(b.Float32(NEG_INF), lambda acc, v: Call("fmaxf", acc, v)).Store(mx, R))
+    (b.Stmt().Iter(R, C).Map([At(x, R, C), At(mx, R)], lambda l, r: Call("expf", b.Sub(l, r))).As(R, C)
+     .Reduce(b.Float32(0), _sum(b)).Store(den, R))
+    (b.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(mx, R), At(den, R)], lambda l, r, s: b.Div(Call("expf", b.Sub(l, r)), s))
+     .As(R, C).Store(y, R, C))
+    return b.Build()
+
+
+def layernorm(cols=1024):
+    """C4: mean and (centred) variance over the row, then
+    (x - mean) * rsqrtf(var + eps) * gamma + beta."""
+    b = NewBuilder("layernorm_%d" % cols)
+    R, C = b.Dim("R", 0), b.Dim("C", cols)
+    x = b.Tensor("x", TF32, R, C)
+    gamma = b.Tensor("gamma", TF32, C)
+    beta = b.Tensor("beta", TF32, C)
+    y = b.Tensor("y", TF32, R, C)
+    mean = b.Local("mean", TF32, R)
+    var = b.Local("var", TF32, R)
+    inv_n = b.ScalarParam("inv_n", TF32)
+    eps = b.ScalarParam("eps", TF32)
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C)
+     .Reduce(b.Float32(0), _sum(b))
+     .Map([], lambda v: b.Mul(v, inv_n)).As(R).Store(mean, R))
+    (b.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(mean, R)], lambda l, r: b.Mul(b.Sub(l, r), b.Sub(l, r))).As(R, C)
+     .Reduce(b.Float32(0), _sum(b))
+     .Map([], lambda v: b.Mul(v, inv_n)).As(R).Store(var, R))
+    (b.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(mean, R), At(var, R), At(gamma, C), At(beta, C)],
+          lambda l, r, s, t, u: b.Add(b.Mul(b.Mul(b.Sub(l, r), Call("rsqrtf", b.Add(s, eps))), t), u))
+     .As(R, C).Store(y, R, C))
+    return b.Build()
+
+
+def _matmul(name, elem, b_nk=False, epilogue=None, scalars=()):
+    b = NewBuilder(name)
+    M, N, K = b.Dim("M", 0), b.Dim("N", 0), b.Dim("K", 0)
+    lhs = b.Tensor("lhs", elem, M, K)
+    rhs = b.Tensor("rhs", elem, N, K) if b_nk else b.Tensor("rhs", elem, K, N)
+    out = b.Tensor("out", TF32, M, N)
+    sc = [b.ScalarParam(s, TF32) for s in scalars]
+    if elem == TF32:
+        body = lambda l, r: b.Mul(l, r)  # noqa: E731
+    else:
+        body = lambda l, r: b.Mul(Cast(l, TF32), Cast(r, TF32))  # noqa: E731
+    rb = At(rhs, N, K) if b_nk else At(rhs, K, N)
+    ar = (b.Stmt().Iter(M, N, K).Map([At(lhs, M, K), rb], body).As(M, N, K)
+          .Reduce(b.Float32(0), _sum(b)))
+    if epilogue is not None:
+        ar.Map([], lambda v: epilogue(b, v, *sc)).As(M, N).Store(out, M, N)
+    else:
+        ar.Store(out, M, N)
+    return b.Build()
+
+
+def gemm_f32():
+    """C5 fp32."""
+    return _matmul("gemm_f32", TF32)
+
+
+def gemm_bf16():
+    """C5 bf16 inputs, fp32 accumulate."""
+    return _matmul("gemm_bf16", TBF16)
+
+
+# ---- the reference suite (testing/kernels/**.tca) ------------------------
+
+def _rank3_reduce(name, k_extent, body, scalars=(), piped=None, piped_scalars=(), middle=False):
+    """out[i][j] = sum_k f(x, z) over x, z [R, C, K] (or [R, K, C] when the
+    reduced axis is the middle one, as row_sum.tca and softmax.tca)."""
+    b = NewBuilder(name)
+    R, C, K = b.Dim("R", 0), b.Dim("C", 0), b.Dim("K" if k_extent == 0 else "e%d" % k_extent, k_extent)
+    shape = (R, K, C) if middle else (R, C, K)
+    x = b.Tensor("x", TF32, *shape)
+    z = b.Tensor("z", TF32, *shape)
+    out = b.Tensor("out", TF32, R, C)
+    sc = [b.ScalarParam(s, TF32) for s in scalars]
+    psc = [b.ScalarParam(s, TF32) for s in piped_scalars]
+    ar = (b.Stmt().Iter(*shape)
+          .Map([At(x, *shape), At(z, *shape)], lambda v, w: body(b, v, w, *sc))
+          .As(R, C, K)
+          .Reduce(b.Float32(0), _sum(b)))
+    if piped is not None:
+        ar.Map([], lambda v: piped(b, v, *psc)).As(R, C).Store(out, R, C)
+    else:
+        ar.Store(out, R, C)
+    return b.Build()
+
+
+def suite_dup_expr():
+    # testing/kernels/dedup/dup_expr.tca:23-37
+    return _rank3_reduce(
+        "dup_expr", 8,
+        lambda b, v, w, gain, bias: b.Mul(b.Add(b.Mul(b.Add(b.Mul(v, v), b.Mul(v, v)), gain),
+                                                b.Mul(b.Add(b.Mul(v, v), b.Mul(v, v)), bias)), w),
+        scalars=("gain", "bias"))
+
+
+def suite_dup_const():
+    # testing/kernels/dedup/dup_const.tca:16-30
+    def body(b, v, w):
+        f = b.Float32
+        t1 = b.Mul(b.Mul(f(0.5), b.Add(v, b.Mul(b.Mul(f(0.5), v), v))), b.Add(f(1.0), b.Mul(f(0.044715), v)))
+        arg = b.Add(b.Mul(f(0.79788456), b.Add(v, b.Mul(f(0.044715), v))), b.Mul(b.Mul(f(0.79788456), f(0.5)), v))
+        t2 = b.Mul(Call("tanhf", arg), b.Sub(f(1.0), f(0.5)))
+        return b.Mul(b.Add(t1, t2), w)
+    return _rank3_reduce("dup_const", 8, body)
+
+
+def suite_axpy3():
+    # testing/kernels/fusion/axpy3.tca:14-36
+    return _rank3_reduce(
+        "axpy3", 4, lambda b, v, w, alpha, beta: b.Add(b.Mul(alpha, v), b.Mul(beta, w)),
+        scalars=("alpha", "beta"),
+        piped=lambda b, v, gamma: b.Add(v, b.Mul(gamma, Call("tanhf", v))), piped_scalars=("gamma",))
+
+
+def suite_scale_copy():
+    # testing/kernels/runtime/scale_copy.tca:16-33
+    return _rank3_reduce("scale_copy", 4, lambda b, v, w, gain, bias: b.Mul(b.Add(b.Mul(gain, v), bias), w),
+                         scalars=("gain", "bias"))
+
+
+def suite_row_sum():
+    # testing/kernels/runtime/row_sum.tca:17-33 (reduce over the middle axis)
+    return _rank3_reduce("row_sum", 4, lambda b, v, w: b.Mul(v, w), middle=True)
+
+
+def suite_softmax():
+    # testing/kernels/fusion/softmax.tca:24-41 (reduce over the middle axis)
+    return _rank3_reduce("softmax_core", 8, lambda b, v, w: b.Mul(Call("expf", v), w), middle=True)
+
+
+def suite_transpose():
+    # testing/kernels/tiling/transpose.tca:24-40 (dynamic K, written as clause)
+    return _rank3_reduce("transpose", 0, lambda b, v, w: b.Mul(v, w))
+
+
+def suite_layernorm():
+    # testing/kernels/llm/layernorm.tca:17-40 (RMS-flavoured core, dynamic K)
+    return _rank3_reduce("layernorm_rms", 0, lambda b, v, w: b.Mul(b.Mul(v, v), w),
+                         piped=lambda b, v, inv_n, eps: b.Mul(v, Call("rsqrtf", b.Add(b.Mul(v, inv_n), eps))),
+                         piped_scalars=("inv_n", "eps"))
+
+
+def _gelu(b, v):
+    f = b.Float32
+    inner = b.Mul(f(0.79788456), b.Add(v, b.Mul(b.Mul(b.Mul(f(0.044715), v), v), v)))
+    return b.Mul(b.Mul(f(0.5), v), b.Add(f(1.0), Call("tanhf", inner)))
+
+
+def suite_gemm(name="gemm"):
+    # testing/kernels/llm/gemm.tca:7-22 (also mm_small / mm_mid / mm_splitk)
+    return _matmul(name, TF32)
+
+
+def suite_mlp():
+    # testing/kernels/fusion/mlp.tca:10-32
+    return _matmul("mlp", TF32, epilogue=lambda b, v: _gelu(b, v))
+
+
+def suite_qk_score():
+    # testing/kernels/llm/qk_score.tca:7-31 (kk indexed [n][k])
+    return _matmul("qk_score", TF32, b_nk=True, epilogue=lambda b, v, scale: b.Mul(v, scale), scalars=("scale",))
+
+
+# name -> (builder, suite dims [d0, d1, d2], scalars) ; dims/scalars from testing/suite.toml
+SUITE = {
+    "dup_expr": (suite_dup_expr, [256, 256, 8], {"gain": 1.5, "bias": 0.25}),
+    "dup_const": (suite_dup_const, [256, 256, 8], {}),
+    "axpy3": (suite_axpy3, [512, 512, 4], {"alpha": 2.0, "beta": 0.5, "gamma": 0.75}),
+    "mlp": (suite_mlp, [64, 128, 64], {}),
+    "softmax": (suite_softmax, [128, 8, 256], {}),
+    "mm_small": (lambda: suite_gemm("mm_small"), [32, 32, 32], {}),
+    "mm_mid": (lambda: suite_gemm("mm_mid"), [128, 256, 64], {}),
+    "mm_splitk": (lambda: suite_gemm("mm_splitk"), [64, 128, 64], {}),
+    "transpose": (suite_transpose, [192, 96, 8], {}),
+    "row_sum": (suite_row_sum, [512, 4, 1024], {}),
+    "scale_copy": (suite_scale_copy, [512, 512, 4], {"gain": 1.25, "bias": -0.125}),
+    "gemm": (suite_gemm, [128, 128, 96], {}),
+    "qk_score": (suite_qk_score, [128, 64, 192], {"scale": 0.125}),
+    "layernorm": (suite_layernorm, [128, 256, 64], {"inv_n": 0.015625, "eps": 0.00001}),
+}
+
+# Programs build() precompiles: (factory, emit flags). The generic-family
+# variants (fusion and MFMA disabled) exist so tests can check every family
+# against the same oracle.
+CONFIG_PROGRAMS = {
+    "scale_relu": scale_relu,
+    "scale_relu_map": scale_relu_map,
+    "row_sum_max_8192": lambda: row_sum_max(8192),
+    "softmax_4096": lambda: softmax(4096),
+    "layernorm_1024": lambda: layernorm(1024),
+    "gemm_f32": gemm_f32,
+    "gemm_bf16": gemm_bf16,
+    # small-row variants exercised by the parity tests (tails, few lanes per row)
+    "row_sum_max_1000": lambda: row_sum_max(1000),
+    "row_sum_max_64": lambda: row_sum_max(64),
+    "softmax_200": lambda: softmax(200),
+    "layernorm_96": lambda: layernorm(96),
+    "softmax_16384": lambda: softmax(16384),
+}
+
+
+def all_builds():
+    """(program factory, flags) pairs for every code object build() makes."""
+    from .pkg import EMIT_NO_FUSION, EMIT_NO_GEMM
+    out = []
+    for name, f in sorted(CONFIG_PROGRAMS.items()):
+        out.append((name, f, 0))
+    for name, (f, _, _) in sorted(SUITE.items()):
+        out.append(("suite_" + name, f, 0))
+    # generic-family lowering of the configs (cross-family parity)
+    for name in ("scale_relu", "row_sum_max_1000", "softmax_200", "layernorm_96", "gemm_f32"):
+        out.append((name + "_generic", CONFIG_PROGRAMS[name], EMIT_NO_FUSION | EMIT_NO_GEMM))
+    return out
