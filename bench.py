@@ -35,6 +35,8 @@ CONFIGS = {
     "c4": ("layernorm_1024", "C4 layernorm f32 [32768,1024]"),
     "c5f": ("gemm_f32", "C5 gemm f32 4096^3"),
     "c5b": ("gemm_bf16", "C5 gemm bf16-in f32-acc 4096^3"),
+    # not a configuration: the plain copy used to calibrate rocprof counters
+    "copy": ("copy_f32", "copy f32 [8192,8192] (counter calibration)"),
 }
 
 
@@ -59,7 +61,16 @@ def _setup(key, dev):
     def dev_f32(a):
         return torch.from_numpy(a).to(dev)
 
-    if key == "c1":
+    if key == "copy":
+        R = C = 8192
+        x = inputs.uniform((R, C), -1, 1, 0)
+        algo = 2 * R * C * 4
+        per_set = algo
+        make = lambda i: [dev_f32(x), torch.empty((R, C), device=dev)]  # noqa: E731
+        scalars = []
+        work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = None
+    elif key == "c1":
         M = N = 4096
         x, y = inputs.uniform((M, N, 1), -1, 1, 0), inputs.uniform((M, N, 1), -1, 1, 1)
         algo = 3 * M * N * 4
@@ -233,7 +244,7 @@ def main():
             entry["roofline"] = {"bound": "mfma", "achieved": tf, "peak": peak, "unit": "TFLOP/s",
                                  "frac": tf / peak, "traffic": _traffic(sym)}
             entry["algorithmic_flops"] = work["flops"]
-        if not args.no_cpu:
+        if not args.no_cpu and cpu is not None:
             v1, unit, sample = _cpu_baseline(key, cpu[1], 1)
             entry["cpu_baseline"] = {"value": v1, "unit": unit, "cores": 1, "kind": "port", "sample": sample}
             if threads > 1:

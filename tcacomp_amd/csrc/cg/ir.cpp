@@ -146,10 +146,13 @@ class Printer {
   std::string Lambda(const ir::Lambda& fn) {
     std::map<int, int> local;
     std::vector<int> order;
+    int next = 0;
     std::function<void(int)> visit = [&](int id) {
       if (local.count(id)) return;
       for (int a : g_.exprs[id].args) visit(a);
-      local[id] = static_cast<int>(order.size());
+      const Op op = g_.exprs[id].op;
+      const bool leaf = op == Op::Param || op == Op::Const || op == Op::Scalar;
+      local[id] = leaf ? 0 : next++;
       order.push_back(id);
     };
     std::ostringstream s;

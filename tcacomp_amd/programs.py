@@ -121,6 +121,17 @@ def layernorm(cols=1024):
     return b.Build()
 
 
+def copy_f32():
+    """y = x over [R, C]: the plain copy whose counter readings calibrate
+    FETCH_SIZE / WRITE_SIZE (known bytes in, known bytes out)."""
+    b = NewBuilder("copy_f32")
+    R, C = b.Dim("R", 0), b.Dim("C", 0)
+    x = b.Tensor("x", TF32, R, C)
+    y = b.Tensor("y", TF32, R, C)
+    b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C).Store(y, R, C)
+    return b.Build()
+
+
 def _matmul(name, elem, b_nk=False, epilogue=None, scalars=()):
     b = NewBuilder(name)
     M, N, K = b.Dim("M", 0), b.Dim("N", 0), b.Dim("K", 0)
@@ -288,6 +299,7 @@ CONFIG_PROGRAMS = {
     "softmax_200": lambda: softmax(200),
     "layernorm_96": lambda: layernorm(96),
     "softmax_16384": lambda: softmax(16384),
+    "copy_f32": copy_f32,
 }
 
 

@@ -1,0 +1,209 @@
+"""Host-only checks of the C ABI: every declared symbol is exported, the
+launch plan parses, the shape contract of the reference launcher
+(internal/cg/cxx/launch.go:98-130) and the wave64 launch grammar
+(replacing runtime/tca/launch.h:37-58) hold — no GPU needed."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from tcacomp_amd import _lib, build, compiler, programs
+from tcacomp_amd.compiler import TensorDesc
+from tcacomp_amd.pkg import EMIT_NO_FUSION, EMIT_NO_GEMM
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    for h in ("tca_rt.h", "tca_cg.h"):
+        text = open(os.path.join(REPO, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b(tca_[a-z0-9_]+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_functions()
+    assert len(names) >= 50
+    for n in sorted(names):
+        assert hasattr(L, n), "libtcacomp.so does not export %s" % n
+    bound = {s[0] for s in _lib.SIGNATURES}
+    assert names == bound, "ctypes bindings and headers disagree: %s" % (names ^ bound)
+
+
+def test_validate_launch_grammar():
+    L = _lib.lib()
+    assert L.tca_rt_validate_launch(1, 256, 0) == 0
+    assert L.tca_rt_validate_launch(1, 1024, 160 * 1024) == 0
+    assert L.tca_rt_validate_launch(0, 256, 0) == _lib.TCA_ERR_LAUNCH
+    assert L.tca_rt_validate_launch(1, 96, 0) == _lib.TCA_ERR_LAUNCH  # not a multiple of 64
+    assert "64-lane" in _lib.last_error()
+    assert L.tca_rt_validate_launch(1, 32, 0) == _lib.TCA_ERR_LAUNCH  # a 32-lane warp is not a wave
+    assert L.tca_rt_validate_launch(1, 2048, 0) == _lib.TCA_ERR_LAUNCH
+    assert L.tca_rt_validate_launch(1, 256, 160 * 1024 + 1) == _lib.TCA_ERR_LAUNCH
+
+
+PLAN = """tca-plan 1
+program p
+dim M 0
+dim N 0
+dim e4 4
+dim F 0
+tensor x f32 in 3 M N e4
+tensor w f32 in 1 N
+tensor y f32 out 2 M N
+tensor tmp f32 local 1 M
+scalar a f32
+kernel k0 256 0 2 M*N/1024 F/1
+arg ptr x
+arg ptr y
+arg dim M
+arg scalar a
+end
+"""
+
+
+def parse(text):
+    h = ctypes.c_void_p()
+    rc = _lib.lib().tca_program_parse(text.encode(), ctypes.byref(h))
+    return rc, h
+
+
+def test_plan_parse_and_signature():
+    rc, h = parse(PLAN)
+    assert rc == 0, _lib.last_error()
+    n = [ctypes.c_uint32() for _ in range(4)]
+    assert _lib.lib().tca_program_signature(h, *[ctypes.byref(x) for x in n]) == 0
+    assert [x.value for x in n] == [3, 1, 1, 1]  # x, w, y; free dim F; scalar a; one kernel
+    assert _lib.lib().tca_program_kernel_name(h, 0) == b"k0"
+    assert _lib.lib().tca_program_kernel_name(h, 1) is None
+    _lib.lib().tca_program_unload(h)
+
+
+@pytest.mark.parametrize("bad,msg", [
+    ("", "empty plan"),
+    ("tca-plan 2\nend\n", "tca-plan 1"),
+    (PLAN.replace("end\n", ""), "missing 'end'"),
+    (PLAN.replace("tensor w f32 in 1 N", "tensor w f99 in 1 N"), "unknown dtype"),
+    (PLAN.replace("M*N/1024", "M*Q/1024"), "unknown dim"),
+    (PLAN.replace("M*N/1024", "M*N/0"), "bad divisor"),
+    (PLAN.replace("arg dim M", "arg dim Z"), "unknown"),
+    (PLAN.replace("dim N 0", "dim M 0"), "duplicate dim"),
+])
+def test_plan_parse_errors(bad, msg):
+    rc, h = parse(bad)
+    assert rc == _lib.TCA_ERR_INVALID
+    assert msg in _lib.last_error()
+
+
+def _check(h, tensors, free=()):
+    arr = compiler._descriptors(tensors)
+    fd = (ctypes.c_uint32 * max(1, len(free)))(*free)
+    rc = _lib.lib().tca_program_check(h, arr, len(tensors), fd, len(free))
+    return rc, _lib.last_error()
+
+
+def test_shape_contract():
+    _, h = parse(PLAN)
+    P = 0x1000  # never dereferenced by the host-only check
+    ok = [TensorDesc(P, (5, 7, 4), 0), TensorDesc(P, (7,), 0), TensorDesc(P, (5, 7), 0)]
+    assert _check(h, ok, (3,)) == (0, _check(h, ok, (3,))[1])
+    rc, msg = _check(h, ok[:2], (3,))
+    assert rc == _lib.TCA_ERR_INVALID and "takes 3 tensor" in msg
+    rc, msg = _check(h, ok, ())
+    assert rc == _lib.TCA_ERR_INVALID and "free dim" in msg
+    rc, msg = _check(h, [TensorDesc(P, (5, 7, 4), 0), TensorDesc(P, (8,), 0), TensorDesc(P, (5, 7), 0)], (3,))
+    assert rc == _lib.TCA_ERR_SHAPE and "w.Dim(0)" in msg and "N = 7" in msg
+    rc, msg = _check(h, [TensorDesc(P, (5, 7, 3), 0), ok[1], ok[2]], (3,))
+    assert rc == _lib.TCA_ERR_SHAPE and "const extent" in msg
+    rc, msg = _check(h, [TensorDesc(P, (5, 7), 0), ok[1], ok[2]], (3,))
+    assert rc == _lib.TCA_ERR_SHAPE and "rank" in msg
+    rc, msg = _check(h, [ok[0], TensorDesc(P, (7,), 2), ok[2]], (3,))
+    assert rc == _lib.TCA_ERR_SHAPE and "dtype" in msg
+    rc, msg = _check(h, [TensorDesc(0, (5, 7, 4), 0), ok[1], ok[2]], (3,))
+    assert rc == _lib.TCA_ERR_INVALID and "null" in msg
+    rc, msg = _check(h, [TensorDesc(P + 4, (5, 7, 4), 0), ok[1], ok[2]], (3,))
+    assert rc == _lib.TCA_ERR_INVALID and "aligned" in msg
+    # empty tensors may carry a null pointer
+    assert _check(h, [TensorDesc(0, (0, 7, 4), 0), ok[1], TensorDesc(0, (0, 7), 0)], (3,))[0] == 0
+    # the u32 element-index domain (design/rt.md:392-399)
+    rc, msg = _check(h, [TensorDesc(P, (70000, 70000, 4), 0), TensorDesc(P, (70000,), 0),
+                         TensorDesc(P, (70000, 70000), 0)], (3,))
+    assert rc == _lib.TCA_ERR_SHAPE and "2^32" in msg
+    _lib.lib().tca_program_unload(h)
+
+
+def test_program_launch_without_module_is_refused():
+    _, h = parse(PLAN)
+    arr = compiler._descriptors([TensorDesc(0x1000, (5, 7, 4), 0), TensorDesc(0x1000, (7,), 0),
+                                 TensorDesc(0x1000, (5, 7), 0)])
+    fd = (ctypes.c_uint32 * 1)(3)
+    sc = (ctypes.c_double * 1)(1.0)
+    rc = _lib.lib().tca_program_launch(h, arr, 3, fd, 1, sc, 1, None)
+    assert rc == _lib.TCA_ERR_INVALID and "parsed, not loaded" in _lib.last_error()
+    _lib.lib().tca_program_unload(h)
+
+
+EXPECTED_FAMILIES = {
+    "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"],
+    "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"], "gemm_bf16": ["gemm"],
+    "copy_f32": ["elementwise"],
+}
+
+
+@pytest.mark.parametrize("name", sorted(EXPECTED_FAMILIES))
+def test_config_classification(name):
+    e = programs.CONFIG_PROGRAMS[name]().emit()
+    assert e.families() == EXPECTED_FAMILIES[name], e.report
+
+
+def test_fusion_disabled_lowers_every_chain_generically():
+    e = programs.CONFIG_PROGRAMS["softmax_4096"]().emit(flags=EMIT_NO_FUSION | EMIT_NO_GEMM)
+    assert e.families() == ["generic"] * 3
+    assert "tensor mx f32 local 1 R" in e.plan  # locals move to the HBM workspace
+
+
+def test_fused_locals_stay_in_registers():
+    e = programs.CONFIG_PROGRAMS["layernorm_1024"]().emit()
+    assert "local" not in e.plan  # mean/var never touch HBM
+    assert e.source.count("__syncthreads") == 0  # 32 lanes per row: no cross-wave exchange
+
+
+def test_nonfinite_literals_are_valid_hip():
+    # The reference formats -inf as the invalid token "-Inff" (internal/cg/cxx/naming.go:103-109).
+    src = programs.CONFIG_PROGRAMS["row_sum_max_8192"]().emit().source
+    assert "(-__builtin_inff())" in src and "Inff" not in src
+
+
+def test_device_flags():
+    e = programs.CONFIG_PROGRAMS["scale_relu"]().emit()
+    assert "-ffp-contract=off" in e.hipcc and "--offload-arch=gfx950" in e.hipcc
+    assert "-packed-fp32-ops" in e.hipcc and "-fno-gpu-flush-denormals-to-zero" in e.hipcc
+
+
+def test_target_other_than_gfx950_is_refused():
+    from tcacomp_amd.pkg import BuildError
+    with pytest.raises(BuildError, match="unsupported target"):
+        programs.CONFIG_PROGRAMS["scale_relu"]().emit(target="sm_86")
+
+
+def test_every_registered_program_is_prebuilt():
+    """build() must have produced every code object the GPU tests and the
+    bench launch (a GPU box never compiles)."""
+    missing = []
+    for name, factory, flags in programs.all_builds():
+        e = factory().emit(flags=flags)
+        key = compiler.cache_key(e.source, e.hipcc)
+        p = os.path.join(compiler.KCACHE, "%s-%s.hsaco" % (factory().name, key))
+        if not os.path.exists(p):
+            missing.append(name)
+    assert not missing, "not prebuilt (run __graft_entry__.build()): %s" % missing
+
+
+def test_build_sources_listed():
+    for s in build.SOURCES:
+        assert os.path.exists(os.path.join(build.CSRC, s))
