@@ -268,8 +268,9 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   std::ostringstream& o = *src;
   const int ta = c.root.ops[m.a_op].tensor, tb = c.root.ops[m.b_op].tensor, tc = c.store_tensor;
   const bool bf16 = m.in == Elem::BF16;
+  const int tile = bf16 ? 256 : 128;
   o << "// contraction over @" << g.dims[m.k].name << " on MFMA (" << (bf16 ? "bf16 32x32x16" : "f32 32x32x2")
-    << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << ", 128x128 tiles\n";
+    << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << ", " << tile << "x" << tile << " tiles\n";
   o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "(\n    " << signature << ") {\n";
   o << "  const uint32_t M = " << ExtentExpr(g, m.m) << ", N = " << ExtentExpr(g, m.n) << ", K = "
     << ExtentExpr(g, m.k) << ";\n";
@@ -291,12 +292,13 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
     val = pg.Gen(c.piped.fn.body);
   }
   o << "    return " << val << ";\n  };\n";
-  o << "  tca::hip::gemm_" << (bf16 ? "bf16" : "f32") << "_128<" << (m.b_nk ? "true" : "false") << ">(t" << ta
+  o << "  tca::hip::gemm_" << (bf16 ? "bf16" : "f32") << "_" << tile << "<" << (m.b_nk ? "true" : "false") << ">(t" << ta
     << ", t" << tb << ", t" << tc << ", M, N, K, epi);\n}\n\n";
   out->block = 256;
   out->lds = 0;
-  out->grid = {g.dims[m.m].name + "/128", g.dims[m.n].name + "/128"};
-  out->detail = std::string(bf16 ? "bf16" : "f32") + " mfma 32x32 tile=128x128 bk=" + (bf16 ? "64" : "32") +
+  out->grid = {g.dims[m.m].name + "/" + std::to_string(tile), g.dims[m.n].name + "/" + std::to_string(tile)};
+  out->detail = std::string(bf16 ? "bf16" : "f32") + " mfma 32x32 tile=" + std::to_string(tile) + "x" +
+                std::to_string(tile) + " bk=" + (bf16 ? "64" : "32") +
                 (m.b_nk ? " B=[n][k]" : " B=[k][n]");
   return true;
 }
@@ -733,13 +735,13 @@ class Emitter {
     for (size_t k = 0; k < c.root.ops.size(); ++k) {
       if (!rootAligned[k]) continue;
       const auto& op = c.root.ops[k];
-      o << "      a" << k << "[u] = tca::hip::load_vec<" << CType(g_.tensors[op.tensor].elem) << ", " << kVec << ">(t"
+      o << "      a" << k << "[u] = tca::hip::load_vec_nt<" << CType(g_.tensors[op.tensor].elem) << ", " << kVec << ">(t"
         << op.tensor << " + base + u * " << kVec * kBlock << "u);\n";
     }
     for (size_t k = 0; k < pipedAligned.size(); ++k) {
       if (!pipedAligned[k]) continue;
       const auto& op = c.piped.ops[k];
-      o << "      p" << k << "[u] = tca::hip::load_vec<" << CType(g_.tensors[op.tensor].elem) << ", " << kVec << ">(t"
+      o << "      p" << k << "[u] = tca::hip::load_vec_nt<" << CType(g_.tensors[op.tensor].elem) << ", " << kVec << ">(t"
         << op.tensor << " + base + u * " << kVec * kBlock << "u);\n";
     }
     o << "    }\n";
@@ -945,7 +947,7 @@ class Emitter {
       const std::string T = CType(g_.tensors[t].elem);
       o << "  tca::hip::vec<" << T << ", V> x" << t << "[NV];\n";
       o << "#pragma unroll\n  for (uint32_t j = 0; j < NV; ++j) {\n";
-      o << "    if (active && (j + 1u < NV || tail_ok)) x" << t << "[j] = tca::hip::load_vec<" << T << ", V>(t" << t
+      o << "    if (active && (j + 1u < NV || tail_ok)) x" << t << "[j] = tca::hip::load_vec_nt<" << T << ", V>(t" << t
         << " + row_base + (j * TPR + lane) * V);\n";
       o << "    else for (uint32_t q = 0; q < V; ++q) x" << t << "[j][q] = " << T << "(0);\n  }\n";
     }

@@ -32,6 +32,22 @@ __device__ __forceinline__ vec<T, N> load_vec(const T* __restrict__ p) {
   return *reinterpret_cast<const vec<T, N>*>(p);
 }
 
+// Streaming load: data read exactly once by this kernel.
+template <typename T, int N>
+__device__ __forceinline__ vec<T, N> load_vec_nt(const T* __restrict__ p) {
+  if constexpr (sizeof(T) * N == 16) {
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    u4 r = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
+    return __builtin_bit_cast(vec<T, N>, r);
+  } else if constexpr (sizeof(T) * N == 8) {
+    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+    u2 r = __builtin_nontemporal_load(reinterpret_cast<const u2*>(p));
+    return __builtin_bit_cast(vec<T, N>, r);
+  } else {
+    return *reinterpret_cast<const vec<T, N>*>(p);
+  }
+}
+
 // Streaming store: the output is not re-read by this kernel, so keep it out
 // of the caches' way.
 template <typename T, int N>

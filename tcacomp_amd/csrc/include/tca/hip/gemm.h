@@ -199,6 +199,454 @@ __device__ __forceinline__ void gemm_bf16_128(const __bf16* __restrict__ A, cons
       }
 }
 
+// ------------------------------------------------------- bf16 path, 256 tiles
+// Tile: BM = BN = 256, BK = 64; 4 waves as 2x2, each 128x128 = 4x4 MFMA
+// blocks (256 fp32 accumulators per lane). Per 16-deep K step a wave reads
+// 4 A + 4 B fragments (8 x 1 KiB of LDS) for 16 MFMAs.
+//
+// LDS layout: each [256][64] bf16 tile is unpadded (128-byte rows). A
+// 128-bit LDS access is served 16 lanes at a time across 64 four-byte banks
+// (256 bytes), i.e. two rows' worth; a 16-byte slot is (row parity, column
+// group). Logical row r is stored at physical row p = r ^ ((r / 8) % 2) and
+// its column group c at c ^ ((p / 2) % 8):
+//     element (r, k) -> p*64 + ((k/8) ^ ((p/2) % 8))*8 + k%8.
+// Then every 16-lane phase hits 16 distinct slots for all three access
+// patterns: fragment reads (16 consecutive rows, one column group), row
+// writes (8 lanes on one row's 8 groups, 8 lanes on the next row) and the
+// transposed B writes (8 lanes on one row, 8 on the row 8 further down,
+// whose parity the row permutation flips). Two such tile pairs (A, B)
+// double-buffer the K loop with one barrier per step: 128 KiB of LDS.
+// SWZ = 0 keeps the plain row-XOR swizzle (c ^ (r % 8)), optimal for a
+// 32-bank / 8-lane-phase LDS; SWZ = 1 is the layout above.
+template <int SWZ>
+__device__ __forceinline__ uint32_t swz64(uint32_t row, uint32_t cg) {
+  if constexpr (SWZ == 0) {
+    return row * 64u + ((cg ^ (row & 7u)) << 3);
+  } else {
+    const uint32_t p = row ^ ((row >> 3) & 1u);
+    return p * 64u + ((cg ^ ((p >> 1) & 7u)) << 3);
+  }
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// [K][N] B slice in LDS, 64 rows of 256 bf16 (512 bytes), 16-byte slots
+// XOR-swizzled by the row: element (k, n) -> k*256 + ((n/8) ^ 4*(k%4))*8 + n%8.
+// The XOR constant is even, so the two slots a transposing read covers stay
+// adjacent, and four consecutive rows land in four distinct 64-byte bank
+// groups (with the neighbouring 16 columns filling the other four).
+__device__ __forceinline__ uint32_t swz_kn(uint32_t k, uint32_t n) {
+  return k * 256u + ((((n >> 3) ^ ((k & 3u) << 2))) << 3) + (n & 7u);
+}
+
+// MFMA B operand (32 columns x 16 k) from a [K][N] LDS slice with the gfx950
+// transposing read ds_read_b64_tr_b16. Within each 16-lane group, lane j
+// points at four consecutive values R_j of one k row, and lane i receives
+// [R_{i/4}[i%4], R_{4+i/4}[i%4], R_{8+i/4}[i%4], R_{12+i/4}[i%4]]. With
+// lane j addressing row kb + j/4, columns nb + 4(j%4), lane i gets
+// B[kb + e][nb + i] for e = 0..3; a second read at kb + 4 completes the
+// lane's 8 k values. Group g of the wave covers columns 16(g%2) and k half
+// g/2, matching the MFMA B layout (column l%32, k 8(l/32)..+8).
+__device__ __forceinline__ bf16x8 frag_b_tr(const uint16_t* Bs, uint32_t n_col0, uint32_t k0, uint32_t lane) {
+  const uint32_t g = lane >> 4, j = lane & 15u;
+  const uint32_t nb = n_col0 + 16u * (g & 1u), kb = k0 + 8u * (g >> 1);
+  const uint32_t k = kb + (j >> 2), n = nb + 4u * (j & 3u);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(Bs + swz_kn(k, n)));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(Bs + swz_kn(k + 4u, n)));
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Interior 256x256 tile with K % 32 == 0 and 16-byte aligned rows: both
+// operand slices go HBM -> LDS with global_load_lds_dwordx4 (lane i of an
+// instruction fills bytes [16i, 16i+16) of a 1 KiB LDS chunk, from any
+// global address), so there is no register staging, no ds_write and no
+// register transpose. K advances in 32-deep slices through a 4-stage ring
+// (4 x 32 KiB): three slices are in flight while one is multiplied, with
+// one vmcnt wait and one barrier per slice.
+//
+// [rows][32] operand slices (A, and B given as [n][k]) use 64-byte rows,
+// 16-byte column groups swizzled by c ^ ((r / 4) % 4): a fragment read (16
+// consecutive rows, one group) then covers the 16 slots of a 256-byte bank
+// window. The [K][N] B slice uses swz_kn.
+__device__ __forceinline__ uint32_t swz32(uint32_t row, uint32_t cg) { return row * 32u + ((cg ^ ((row >> 2) & 3u)) << 3); }
+
+template <bool B_NK>
+__device__ __forceinline__ void gemm_bf16_256_dma(const uint16_t* __restrict__ A16, const uint16_t* __restrict__ B16,
+                                                  uint32_t N, uint32_t K, uint32_t m0, uint32_t n0, uint16_t* lds,
+                                                  f32x16 (&acc)[4][4]) {
+  constexpr uint32_t BK = 32, STAGES = 4, SLICE = 256u * BK;  // elements per operand slice
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t wm = (wave >> 1) * 128u, wn = (wave & 1u) * 128u;
+  // Per-lane element offsets of the 4 chunks (of 16) this wave fills per
+  // slice and operand: chunk ch = 4*wave + q covers LDS slots 64ch .. +63.
+  uint32_t offa[4], offb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t slot = (wave * 4u + q) * 64u + lane;
+    const uint32_t r = slot >> 2, c = (slot & 3u) ^ ((r >> 2) & 3u);  // inverse of swz32
+    offa[q] = r * K + c * 8u;
+    if constexpr (B_NK) {
+      offb[q] = r * K + c * 8u;
+    } else {
+      const uint32_t k = slot >> 5, sp = slot & 31u;  // [32][256]: 32 slots per row
+      offb[q] = k * N + ((sp ^ ((k & 3u) << 2)) << 3);
+    }
+  }
+  auto a_slice = [&](uint32_t s) { return lds + s * 2u * SLICE; };
+  auto b_slice = [&](uint32_t s) { return lds + s * 2u * SLICE + SLICE; };
+  auto issue = [&](uint32_t s, uint32_t k0) {
+    const uint16_t* a0 = A16 + static_cast<uint64_t>(m0) * K + k0;
+    const uint16_t* b0 = B_NK ? B16 + static_cast<uint64_t>(n0) * K + k0 : B16 + static_cast<uint64_t>(k0) * N + n0;
+    uint16_t* as = a_slice(s);
+    uint16_t* bs = b_slice(s);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t ch = wave * 4u + q;
+      __builtin_amdgcn_global_load_lds(a0 + offa[q], (lds_void*)(as + ch * 512u), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(b0 + offb[q], (lds_void*)(bs + ch * 512u), 16, 0, 0);
+    }
+  };
+  bf16x8 fa[4], fb[4];
+  auto load_frags = [&](uint32_t s, uint32_t ks) {
+    const uint16_t* As = a_slice(s);
+    const uint16_t* Bs = b_slice(s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[i] = *reinterpret_cast<const bf16x8*>(&As[swz32(wm + i * 32u + (lane & 31u), ks * 2u + (lane >> 5))]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (B_NK)
+        fb[j] = *reinterpret_cast<const bf16x8*>(&Bs[swz32(wn + j * 32u + (lane & 31u), ks * 2u + (lane >> 5))]);
+      else
+        fb[j] = frag_b_tr(Bs, wn + j * 32u, ks * 16u, lane);
+    }
+  };
+  auto mfma16 = [&](const bf16x8 (&ga)[4], const bf16x8 (&gb)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gb[j], ga[i], acc[i][j], 0, 0, 0);
+  };
+  // The barrier between slices waits only for the slice about to be read
+  // (vmcnt counts in issue order, 8 loads per slice and lane) and for this
+  // wave's LDS reads; a plain __syncthreads() would drain every slice in
+  // flight. s_waitcnt immediate: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
+  // vmcnt[5:4] at [15:14].
+  auto sync_slice = [&](uint32_t younger_slices) {
+    asm volatile("" ::: "memory");
+    if (younger_slices >= 2) __builtin_amdgcn_s_waitcnt(0x4070);       // vmcnt(16) lgkmcnt(0)
+    else if (younger_slices == 1) __builtin_amdgcn_s_waitcnt(0x0078);  // vmcnt(8)  lgkmcnt(0)
+    else __builtin_amdgcn_s_waitcnt(0x0070);                           // vmcnt(0)  lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // Pipeline over 32-deep slices in a 4-buffer ring. Iteration kt:
+  //   step A: MFMAs of (kt, k 0-15) while reading the (kt, k 16-31) fragments;
+  //   barrier: slice kt+1 has landed and every wave is done with slice kt-1,
+  //            so slice kt+3 is issued into kt-1's buffer;
+  //   step B: MFMAs of (kt, k 16-31) while reading the (kt+1, k 0-15)
+  //           fragments and issuing slice kt+3's loads.
+  // LDS reads and DMA issues are interleaved one by one between MFMAs.
+  const uint32_t nk = K / BK;
+  const uint32_t pre = nk < STAGES - 1 ? nk : STAGES - 1;
+  for (uint32_t s = 0; s < pre; ++s) issue(s, s * BK);
+  sync_slice(pre - 1);
+  load_frags(0, 0);
+  for (uint32_t kt = 0; kt < nk; ++kt) {
+    {
+      bf16x8 ga[4], gb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ga[i] = fa[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) gb[j] = fb[j];
+      load_frags(kt % STAGES, 1);
+      mfma16(ga, gb);
+#pragma unroll
+      for (int t = 0; t < 12; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
+    const bool more = kt + 1 < nk;
+    if (more) {
+      sync_slice(kt + 2 < nk ? 1u : 0u);
+      if (kt + 3 < nk) issue((kt + 3) % STAGES, (kt + 3) * BK);
+    }
+    {
+      bf16x8 ga[4], gb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ga[i] = fa[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) gb[j] = fb[j];
+      if (more) load_frags((kt + 1) % STAGES, 0);
+      mfma16(ga, gb);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);  // one global -> LDS load
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // one LDS read
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+    }
+  }
+}
+
+template <bool B_NK, typename Epi, int SWZ = 1, bool SPREAD = true, bool PREFETCH = true, bool DMA = true>
+__device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
+                                              float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
+  constexpr uint32_t BM = 256, BN = 256, BK = 64, TILE = BM * BK;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][TILE];  // [buffer][A, B]
+  const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  uint32_t tm, tn;
+  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
+  const bool dma_tile = DMA && m0 + BM <= M && n0 + BN <= N && K % 32u == 0u && N % 8u == 0u && K > 0u;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t wm = (wave >> 1) * 128u, wn = (wave & 1u) * 128u;
+  const bool vec_a = (K % 8u) == 0u;
+  const bool vec_b = B_NK ? (K % 8u) == 0u : (N % 8u) == 0u;
+  const uint16_t* __restrict__ A16 = reinterpret_cast<const uint16_t*>(A);
+  const uint16_t* __restrict__ B16 = reinterpret_cast<const uint16_t*>(B);
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  if (dma_tile) {
+    gemm_bf16_256_dma<B_NK>(A16, B16, N, K, m0, n0, &lds[0][0][0], acc);
+  } else {
+  u32x4 ra[8], rb[8];
+  // Interior tiles (the whole BMxBN block in range, rows 16-byte aligned)
+  // take unguarded vector loads addressed as a workgroup-uniform base plus a
+  // 32-bit per-lane byte offset; the test is uniform, so it is a scalar
+  // branch, not a per-lane mask.
+  const bool interior_mn = vec_a && vec_b && m0 + BM <= M && n0 + BN <= N;
+  const uint32_t off_rows = ((tid >> 3) * K + (tid & 7u) * 8u) * 2u;  // row-panel vector of this lane
+  const uint32_t off_kn = ((tid & 7u) * 8u * N + (tid >> 3) * 8u) * 2u;  // [K][N] block of this lane
+  auto at = [](const uint16_t* base, uint32_t byte_off) {
+    return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + byte_off);
+  };
+  // Rows of a K-contiguous panel (A, or B as [n][k]): 2048 16-byte vectors.
+  auto load_rows = [&](const uint16_t* __restrict__ P, uint32_t rows, uint32_t r0, uint32_t k0, bool vec, u32x4* r) {
+    if (interior_mn && k0 + BK <= K) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r[i] = at(P + static_cast<uint64_t>(r0 + i * 32u) * K + k0, off_rows);
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t v = i * 256u + tid, rr = v >> 3, gk = k0 + (v & 7u) * 8u, gr = r0 + rr;
+      if (vec && gr < rows && gk + 8u <= K) {
+        r[i] = *reinterpret_cast<const u32x4*>(P + static_cast<uint64_t>(gr) * K + gk);
+      } else {
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = (gr < rows && gk + e < K) ? P[static_cast<uint64_t>(gr) * K + gk + e] : 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[i][e] = h[2 * e] | (h[2 * e + 1] << 16);
+      }
+    }
+  };
+  // [K][N] panel: thread owns an 8(k) x 8(n) block; kb = tid % 8, nb = tid / 8.
+  auto load_b_kn = [&](uint32_t k0) {
+    const uint32_t kb = tid & 7u, nb = tid >> 3;
+    if (interior_mn && k0 + BK <= K) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) rb[i] = at(B16 + static_cast<uint64_t>(k0 + i) * N + n0, off_kn);
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t gk = k0 + kb * 8u + i, gn = n0 + nb * 8u;
+      if (vec_b && gk < K && gn + 8u <= N) {
+        rb[i] = *reinterpret_cast<const u32x4*>(B16 + static_cast<uint64_t>(gk) * N + gn);
+      } else {
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = (gk < K && gn + e < N) ? B16[static_cast<uint64_t>(gk) * N + gn + e] : 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rb[i][e] = h[2 * e] | (h[2 * e + 1] << 16);
+      }
+    }
+  };
+  // Stores of the staged slice into an LDS buffer, in halves so they can be
+  // spread between the MFMA steps of the current slice.
+  auto store_a = [&](uint32_t buf, int half) {
+    uint16_t* As = lds[buf][0];
+#pragma unroll
+    for (int i = half * 4; i < half * 4 + 4; ++i) {
+      const uint32_t v = i * 256u + tid;
+      *reinterpret_cast<u32x4*>(&As[swz64<SWZ>(v >> 3, v & 7u)]) = ra[i];
+    }
+  };
+  auto store_b = [&](uint32_t buf, int half) {
+    uint16_t* Bs = lds[buf][1];
+    if constexpr (B_NK) {
+#pragma unroll
+      for (int i = half * 4; i < half * 4 + 4; ++i) {
+        const uint32_t v = i * 256u + tid;
+        *reinterpret_cast<u32x4*>(&Bs[swz64<SWZ>(v >> 3, v & 7u)]) = rb[i];
+      }
+    } else {
+      // 8x8 transpose in registers: column n of the block gets its 8 k values.
+      const uint32_t kb = tid & 7u, nb = tid >> 3;
+#pragma unroll
+      for (int n = half * 4; n < half * 4 + 4; ++n) {
+        const int d = n >> 1;
+        u32x4 w;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = rb[2 * q][d], hi = rb[2 * q + 1][d];
+          w[q] = (n & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+        }
+        *reinterpret_cast<u32x4*>(&Bs[swz64<SWZ>(nb * 8u + n, kb)]) = w;
+      }
+    }
+  };
+  auto load_a = [&](uint32_t k0) { load_rows(A16, M, m0, k0, vec_a, ra); };
+  auto load_b = [&](uint32_t k0) {
+    if constexpr (B_NK) load_rows(B16, N, n0, k0, vec_b, rb);
+    else load_b_kn(k0);
+  };
+  auto frag = [&](const uint16_t* T, uint32_t row0, uint32_t cg) {
+    return *reinterpret_cast<const bf16x8*>(&T[swz64<SWZ>(row0 + (lane & 31u), cg)]);
+  };
+
+  // SPREAD: while slice kt is multiplied out of LDS buffer kt%2, slice kt+1
+  // (already in registers) is written into the other buffer a quarter per
+  // MFMA step, and the registers refill with slice kt+2 as soon as they are
+  // written out. Otherwise slice kt+1 is loaded at the top of the step and
+  // written after the MFMAs. One barrier per slice either way.
+  //
+  // The MFMA takes the B fragment as its first operand: it then computes the
+  // C^T block, so each lane ends up holding four consecutive columns of one
+  // row of C (a 16-byte store) instead of four rows of one column.
+  const uint32_t nk = (K + BK - 1) / BK;
+  if (nk > 0) {
+    load_a(0);
+    load_b(0);
+    store_a(0, 0);
+    store_a(0, 1);
+    store_b(0, 0);
+    store_b(0, 1);
+  }
+  if (SPREAD && nk > 1) {
+    load_a(BK);
+    load_b(BK);
+  }
+  __syncthreads();
+  for (uint32_t kt = 0; kt < nk; ++kt) {
+    const uint32_t buf = kt & 1u, nbuf = buf ^ 1u;
+    const bool has1 = kt + 1 < nk, has2 = kt + 2 < nk;
+    const uint16_t* As = lds[buf][0];
+    const uint16_t* Bs = lds[buf][1];
+    if (!SPREAD && has1) {
+      load_a((kt + 1) * BK);
+      load_b((kt + 1) * BK);
+    }
+    bf16x8 fa[4], fb[4];
+    if constexpr (PREFETCH) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fa[i] = frag(As, wm + i * 32u, lane >> 5);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fb[j] = frag(Bs, wn + j * 32u, lane >> 5);
+    }
+#pragma unroll
+    for (uint32_t ks = 0; ks < BK / 16; ++ks) {
+      const uint32_t cg = ks * 2u + (lane >> 5);
+      bf16x8 ga[4], gb[4];
+      if constexpr (PREFETCH) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ga[i] = fa[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gb[j] = fb[j];
+        if (ks + 1 < BK / 16) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) fa[i] = frag(As, wm + i * 32u, cg + 2u);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) fb[j] = frag(Bs, wn + j * 32u, cg + 2u);
+        }
+        // Keep the next step's LDS reads issued ahead of this step's MFMAs:
+        // without the fence the scheduler sinks them and re-waits on LDS
+        // latency between MFMA groups.
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ga[i] = frag(As, wm + i * 32u, cg);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gb[j] = frag(Bs, wn + j * 32u, cg);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gb[j], ga[i], acc[i][j], 0, 0, 0);
+      if (SPREAD && has1) {
+        if (ks == 0) store_a(nbuf, 0);
+        if (ks == 1) store_a(nbuf, 1);
+        if (ks == 2) store_b(nbuf, 0);
+        if (ks == 3) store_b(nbuf, 1);
+      }
+      if (SPREAD && has2) {
+        if (ks == 1) load_a((kt + 2) * BK);
+        if (ks == 3) load_b((kt + 2) * BK);
+      }
+    }
+    if (!SPREAD && has1) {
+      store_a(nbuf, 0);
+      store_a(nbuf, 1);
+      store_b(nbuf, 0);
+      store_b(nbuf, 1);
+    }
+    __syncthreads();
+  }
+  }  // general path
+  // acc[i][j][4g + q] = C[m][n + q] with m = m0 + wm + 32i + lane%32 and
+  // n = n0 + wn + 32j + 8g + 4*(lane/32).
+  const uint32_t mr = m0 + wm + (lane & 31u), nc = n0 + wn + 4u * (lane >> 5);
+  if (m0 + BM <= M && n0 + BN <= N && (N % 4u) == 0u) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t m = mr + 32u * i, n = nc + 32u * j + 8u * g;
+          float4 v;
+          v.x = epi(acc[i][j][4 * g + 0], m, n + 0);
+          v.y = epi(acc[i][j][4 * g + 1], m, n + 1);
+          v.z = epi(acc[i][j][4 * g + 2], m, n + 2);
+          v.w = epi(acc[i][j][4 * g + 3], m, n + 3);
+          *reinterpret_cast<float4*>(C + static_cast<uint64_t>(m) * N + n) = v;
+        }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t m = mr + 32u * i, n = nc + 32u * j + 8u * (e >> 2) + (e & 3);
+        if (m < M && n < N) C[static_cast<uint64_t>(m) * N + n] = epi(acc[i][j][e], m, n);
+      }
+}
+
 // ---------------------------------------------------------------- fp32 path
 // Tile: BM = BN = 128, BK = 32; 4 waves as 2x2, each 64x64 = 2x2 MFMA blocks.
 template <bool B_NK, typename Epi>

@@ -163,6 +163,11 @@ def gemm_bf16():
     return _matmul("gemm_bf16", TBF16)
 
 
+def gemm_bf16_nt():
+    """C5 with B given as [N][K] (the qk_score orientation), bf16 inputs."""
+    return _matmul("gemm_bf16_nt", TBF16, b_nk=True)
+
+
 # ---- the reference suite (testing/kernels/**.tca) ------------------------
 
 def _rank3_reduce(name, k_extent, body, scalars=(), piped=None, piped_scalars=(), middle=False):
@@ -293,6 +298,7 @@ CONFIG_PROGRAMS = {
     "layernorm_1024": lambda: layernorm(1024),
     "gemm_f32": gemm_f32,
     "gemm_bf16": gemm_bf16,
+    "gemm_bf16_nt": gemm_bf16_nt,
     # small-row variants exercised by the parity tests (tails, few lanes per row)
     "row_sum_max_1000": lambda: row_sum_max(1000),
     "row_sum_max_64": lambda: row_sum_max(64),

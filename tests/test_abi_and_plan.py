@@ -149,7 +149,7 @@ def test_program_launch_without_module_is_refused():
 
 
 EXPECTED_FAMILIES = {
-    "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"],
+    "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"],
     "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"], "gemm_bf16": ["gemm"],
     "copy_f32": ["elementwise"],
 }

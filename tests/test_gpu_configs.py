@@ -216,24 +216,48 @@ def test_c5_gemm_bf16(gpu, M, N, K):
                         "gemm bf16")
 
 
-def test_c5_gemm_exact_integers(gpu):
+@pytest.mark.parametrize("M,N,K", [(1, 1, 8), (33, 65, 17), (256, 256, 32), (512, 768, 512), (300, 520, 96)])
+def test_c5_gemm_bf16_nt(gpu, M, N, K):
+    """B given as [N][K]: shapes cover the direct-to-LDS interior path
+    (256-multiples, K % 32 == 0) and the general edge path in one launch."""
+    import torch
+    _say("C5 bf16 NT", M, N, K)
+    a = oracle.to_bf16_bits(inputs.uniform((M, K), -1, 1, 0))
+    b = oracle.to_bf16_bits(inputs.uniform((N, K), -1, 1, 1))
+    want = oracle.gemm(a, b, b_nk=True)
+    c = out_dev((M, N), gpu)
+    run(compiled("gemm_bf16_nt"), [to_dev(a.view(np.int16), gpu).view(torch.bfloat16),
+                                   to_dev(b.view(np.int16), gpu).view(torch.bfloat16), c])
+    got = host(c)
+    assert canaries(got) == 0
+    bound = _gemm_bound(oracle.bf16_bits_to_f32(a), np.ascontiguousarray(oracle.bf16_bits_to_f32(b).T), K)
+    assert_reduce_close(got, want, bound, K, "gemm bf16 nt")
+
+
+@pytest.mark.parametrize("M,N,K", [(96, 160, 64), (256, 512, 96)])
+def test_c5_gemm_exact_integers(gpu, M, N, K):
     """Small-integer operands: every product and partial sum is exact in
-    fp32, so any order gives the exact result (pins the MFMA lane layout:
-    a transposed or shifted fragment cannot pass)."""
-    M, N, K = 96, 160, 64
+    fp32, so any order gives the exact result (pins the MFMA lane layout,
+    the LDS swizzles and the transposing B reads: a transposed, shifted or
+    mis-swizzled fragment cannot pass). 256-multiples take the bf16
+    direct-to-LDS path, the other shape the general path."""
+    import torch
     rng = np.random.default_rng(5)
     a = rng.integers(-4, 5, (M, K)).astype(np.float32)
     b = rng.integers(-4, 5, (K, N)).astype(np.float32)
     want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
-    for name in ("gemm_f32",):
-        c = out_dev((M, N), gpu)
-        run(compiled(name), [to_dev(a, gpu), to_dev(b, gpu), c])
-        assert np.array_equal(host(c), want)
-    import torch
+    c = out_dev((M, N), gpu)
+    run(compiled("gemm_f32"), [to_dev(a, gpu), to_dev(b, gpu), c])
+    assert np.array_equal(host(c), want)
     ab, bb = oracle.to_bf16_bits(a), oracle.to_bf16_bits(b)
     c = out_dev((M, N), gpu)
     run(compiled("gemm_bf16"), [to_dev(ab.view(np.int16), gpu).view(torch.bfloat16),
                                 to_dev(bb.view(np.int16), gpu).view(torch.bfloat16), c])
+    assert np.array_equal(host(c), want)
+    bt = np.ascontiguousarray(bb.T)
+    c = out_dev((M, N), gpu)
+    run(compiled("gemm_bf16_nt"), [to_dev(ab.view(np.int16), gpu).view(torch.bfloat16),
+                                   to_dev(bt.view(np.int16), gpu).view(torch.bfloat16), c])
     assert np.array_equal(host(c), want)
 
 
