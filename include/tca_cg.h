@@ -53,8 +53,11 @@ enum {
 /* Unary operators (pkg/expr.go:233-240). */
 enum { TCA_NEG = 0, TCA_POS, TCA_LNOT, TCA_NOT };
 
-/* Emit flags. */
+/* Emit flags. Bits 8-11 / 12-15 carry the row family's vectors per lane and
+ * the elementwise family's vectors per thread (powers of two; 0 = default). */
 enum { TCA_EMIT_NO_FUSION = 1, TCA_EMIT_NO_GEMM = 2 };
+#define TCA_EMIT_ROW_VECTORS(n) ((n) << 8)
+#define TCA_EMIT_EW_UNROLL(n) ((n) << 12)
 
 tca_builder tca_builder_new(const char* name);
 void tca_builder_free(tca_builder b);

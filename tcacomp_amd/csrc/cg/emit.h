@@ -34,6 +34,11 @@ struct Options {
   bool comments = true;
   bool allow_fused = true;       // false: every chain lowers to the generic family
   bool allow_gemm = true;
+  // Geometry knobs (power-of-two values; 0 = default). Row family: target
+  // 16-byte vectors per lane and row operand (lanes per row follow from it).
+  // Elementwise family: 16-byte vectors per thread and operand.
+  int row_vectors_per_lane = 0;
+  int elementwise_unroll = 0;
 };
 
 struct KernelInfo {
