@@ -298,7 +298,7 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   out->lds = 0;
   out->grid = {g.dims[m.m].name + "/" + std::to_string(tile), g.dims[m.n].name + "/" + std::to_string(tile)};
   out->detail = std::string(bf16 ? "bf16" : "f32") + " mfma 32x32 tile=" + std::to_string(tile) + "x" +
-                std::to_string(tile) + " bk=" + (bf16 ? "64" : "32") +
+                std::to_string(tile) + (bf16 ? " bk=32 (direct-to-LDS ring; edge tiles 64)" : " bk=32") +
                 (m.b_nk ? " B=[n][k]" : " B=[k][n]");
   return true;
 }

@@ -51,154 +51,6 @@ __device__ __forceinline__ void gemm_tile_coords(uint32_t tiles_m, uint32_t tile
   *tn = in / rows;
 }
 
-// ---------------------------------------------------------------- bf16 path
-// Tile: BM = BN = 128, BK = 64; 4 waves as 2x2, each 64x64 = 2x2 MFMA blocks.
-template <bool B_NK, typename Epi>
-__device__ __forceinline__ void gemm_bf16_128(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
-                                              float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
-  constexpr int BM = 128, BN = 128, BK = 64, LDK = BK + 8;  // 8 bf16 = 16 B of padding per row
-  __shared__ __attribute__((aligned(16))) __bf16 As[BM * LDK];
-  __shared__ __attribute__((aligned(16))) __bf16 Bs[BN * LDK];
-  const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  uint32_t tm, tn;
-  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
-  const uint32_t m0 = tm * BM, n0 = tn * BN;
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t wm = (wave >> 1) * 64u, wn = (wave & 1u) * 64u;
-  const bool vec_a = (K % 8u) == 0u;
-  const bool vec_b = B_NK ? (K % 8u) == 0u : (N % 8u) == 0u;
-
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
-  // Register staging of one K slice: A 4 x 16 B per thread; B 4 x 16 B.
-  u32x4 ra[4], rb[4];
-  auto load_a = [&](uint32_t k0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t v = i * 256u + tid, r = v >> 3, kv = (v & 7u) * 8u;
-      const uint32_t gm = m0 + r, gk = k0 + kv;
-      if (vec_a && gm < M && gk + 8u <= K) {
-        ra[i] = *reinterpret_cast<const u32x4*>(A + static_cast<uint64_t>(gm) * K + gk);
-      } else {
-        uint16_t h[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          h[e] = (gm < M && gk + e < K) ? __builtin_bit_cast(uint16_t, A[static_cast<uint64_t>(gm) * K + gk + e]) : 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ra[i][e] = h[2 * e] | (static_cast<uint32_t>(h[2 * e + 1]) << 16);
-      }
-    }
-  };
-  auto load_b = [&](uint32_t k0) {
-    if constexpr (B_NK) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t v = i * 256u + tid, r = v >> 3, kv = (v & 7u) * 8u;
-        const uint32_t gn = n0 + r, gk = k0 + kv;
-        if (vec_b && gn < N && gk + 8u <= K) {
-          rb[i] = *reinterpret_cast<const u32x4*>(B + static_cast<uint64_t>(gn) * K + gk);
-        } else {
-          uint16_t h[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            h[e] = (gn < N && gk + e < K) ? __builtin_bit_cast(uint16_t, B[static_cast<uint64_t>(gn) * K + gk + e]) : 0;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) rb[i][e] = h[2 * e] | (static_cast<uint32_t>(h[2 * e + 1]) << 16);
-        }
-      }
-    } else {
-      // [K][N]: thread owns a 4(k) x 8(n) block: rows k0 + kb*4 + i, cols n0 + nb*8.
-      const uint32_t nb = tid & 15u, kb = tid >> 4;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t gk = k0 + kb * 4u + i, gn = n0 + nb * 8u;
-        if (vec_b && gk < K && gn + 8u <= N) {
-          rb[i] = *reinterpret_cast<const u32x4*>(B + static_cast<uint64_t>(gk) * N + gn);
-        } else {
-          uint16_t h[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            h[e] = (gk < K && gn + e < N) ? __builtin_bit_cast(uint16_t, B[static_cast<uint64_t>(gk) * N + gn + e]) : 0;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) rb[i][e] = h[2 * e] | (static_cast<uint32_t>(h[2 * e + 1]) << 16);
-        }
-      }
-    }
-  };
-  auto store_lds = [&]() {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t v = i * 256u + tid, r = v >> 3, kv = (v & 7u) * 8u;
-      *reinterpret_cast<u32x4*>(&As[r * LDK + kv]) = ra[i];
-    }
-    if constexpr (B_NK) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t v = i * 256u + tid, r = v >> 3, kv = (v & 7u) * 8u;
-        *reinterpret_cast<u32x4*>(&Bs[r * LDK + kv]) = rb[i];
-      }
-    } else {
-      // Transpose the 4x8 block: column n gets its 4 k values (8 bytes).
-      const uint32_t nb = tid & 15u, kb = tid >> 4;
-#pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        const int d = n >> 1, sh = (n & 1) * 16;
-        const uint32_t k0v = (rb[0][d] >> sh) & 0xffffu, k1v = (rb[1][d] >> sh) & 0xffffu;
-        const uint32_t k2v = (rb[2][d] >> sh) & 0xffffu, k3v = (rb[3][d] >> sh) & 0xffffu;
-        u32x2 w;
-        w[0] = k0v | (k1v << 16);
-        w[1] = k2v | (k3v << 16);
-        *reinterpret_cast<u32x2*>(&Bs[(nb * 8u + n) * LDK + kb * 4u]) = w;
-      }
-    }
-  };
-
-  const uint32_t nk = (K + BK - 1) / BK;
-  load_a(0);
-  load_b(0);
-  for (uint32_t kt = 0; kt < nk; ++kt) {
-    __syncthreads();
-    store_lds();
-    __syncthreads();
-    if (kt + 1 < nk) {
-      load_a((kt + 1) * BK);
-      load_b((kt + 1) * BK);
-    }
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const uint32_t kk = ks * 16u + (lane >> 5) * 8u;
-      bf16x8 fa[2], fb[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        fa[i] = *reinterpret_cast<const bf16x8*>(&As[(wm + i * 32u + (lane & 31u)) * LDK + kk]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        fb[j] = *reinterpret_cast<const bf16x8*>(&Bs[(wn + j * 32u + (lane & 31u)) * LDK + kk]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-    }
-  }
-  // Epilogue: lanes of one row write 32 consecutive floats.
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const uint32_t r = m0 + wm + i * 32u + 8u * (e >> 2) + 4u * (lane >> 5) + (e & 3);
-        const uint32_t c = n0 + wn + j * 32u + (lane & 31u);
-        if (r < M && c < N) C[static_cast<uint64_t>(r) * N + c] = epi(acc[i][j][e], r, c);
-      }
-}
-
 // ------------------------------------------------------- bf16 path, 256 tiles
 // Tile: BM = BN = 256, BK = 64; 4 waves as 2x2, each 128x128 = 4x4 MFMA
 // blocks (256 fp32 accumulators per lane). Per 16-deep K step a wave reads
@@ -273,6 +125,10 @@ __device__ __forceinline__ bf16x8 frag_b_tr(const uint16_t* Bs, uint32_t n_col0,
 // 16-byte column groups swizzled by c ^ ((r / 4) % 4): a fragment read (16
 // consecutive rows, one group) then covers the 16 slots of a 256-byte bank
 // window. The [K][N] B slice uses swz_kn.
+// s_waitcnt immediate for gfx9: vmcnt[3:0] | expcnt[6:4] (7 = no wait) |
+// lgkmcnt[11:8] | vmcnt[5:4] at [15:14].
+constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | (7 << 4) | ((lgkm & 15) << 8) | ((vm >> 4) << 14); }
+
 __device__ __forceinline__ uint32_t swz32(uint32_t row, uint32_t cg) { return row * 32u + ((cg ^ ((row >> 2) & 3u)) << 3); }
 
 template <bool B_NK>
@@ -326,81 +182,74 @@ __device__ __forceinline__ void gemm_bf16_256_dma(const uint16_t* __restrict__ A
         fb[j] = frag_b_tr(Bs, wn + j * 32u, ks * 16u, lane);
     }
   };
-  auto mfma16 = [&](const bf16x8 (&ga)[4], const bf16x8 (&gb)[4]) {
+  // One 16-deep step: the MFMAs of the fragments in hand, while the next
+  // step's fragments are read (and, when `dma`, a slice is issued). The
+  // instruction interleave is left to the compiler's scheduler, which moves
+  // MFMAs across the reads and the barrier better than a fixed pattern.
+  auto step = [&](uint32_t next_s, uint32_t next_ks, bool dma, uint32_t dma_s, uint32_t dma_k0) {
+    bf16x8 ga[4], gb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ga[i] = fa[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) gb[j] = fb[j];
+    if (dma) issue(dma_s, dma_k0);
+    load_frags(next_s, next_ks);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gb[j], ga[i], acc[i][j], 0, 0, 0);
   };
-  // The barrier between slices waits only for the slice about to be read
-  // (vmcnt counts in issue order, 8 loads per slice and lane) and for this
-  // wave's LDS reads; a plain __syncthreads() would drain every slice in
-  // flight. s_waitcnt immediate: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
-  // vmcnt[5:4] at [15:14].
-  auto sync_slice = [&](uint32_t younger_slices) {
-    asm volatile("" ::: "memory");
-    if (younger_slices >= 2) __builtin_amdgcn_s_waitcnt(0x4070);       // vmcnt(16) lgkmcnt(0)
-    else if (younger_slices == 1) __builtin_amdgcn_s_waitcnt(0x0078);  // vmcnt(8)  lgkmcnt(0)
-    else __builtin_amdgcn_s_waitcnt(0x0070);                           // vmcnt(0)  lgkmcnt(0)
+  // The barrier waits only for the slice about to be
+  // read (vmcnt counts in issue order, 8 loads per slice and lane); a plain
+  // __syncthreads() would drain every slice in flight. Its lgkmcnt leaves the
+  // step's own fragment reads (kReads per step) in flight but guarantees that
+  // the reads of the previous iteration, the last ones of the buffer the next
+  // DMA overwrites, have completed: LDS reads complete in order.
+  constexpr int kReads = B_NK ? 8 : 12;
+  constexpr int kWaitNext = waitcnt_imm(8, kReads), kWaitLast = waitcnt_imm(0, kReads);
+  auto barrier = [&]() {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
 
   // Pipeline over 32-deep slices in a 4-buffer ring. Iteration kt:
   //   step A: MFMAs of (kt, k 0-15) while reading the (kt, k 16-31) fragments;
-  //   barrier: slice kt+1 has landed and every wave is done with slice kt-1,
-  //            so slice kt+3 is issued into kt-1's buffer;
+  //   barrier: slice kt+1 has landed and every wave is done with slice kt-1;
   //   step B: MFMAs of (kt, k 16-31) while reading the (kt+1, k 0-15)
-  //           fragments and issuing slice kt+3's loads.
-  // LDS reads and DMA issues are interleaved one by one between MFMAs.
+  //           fragments and issuing slice kt+3 into kt-1's buffer.
+  // The main loop is branch-free (a branch around the reads or the DMA would
+  // pin the next slice's fragment reads ahead of step B's MFMAs and make them
+  // wait for those reads); the last three iterations, which issue nothing,
+  // are a separate tail.
   const uint32_t nk = K / BK;
   const uint32_t pre = nk < STAGES - 1 ? nk : STAGES - 1;
   for (uint32_t s = 0; s < pre; ++s) issue(s, s * BK);
-  sync_slice(pre - 1);
+  asm volatile("" ::: "memory");
+  if (pre >= 3u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 0));
+  else if (pre == 2u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
+  else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+  barrier();
   load_frags(0, 0);
-  for (uint32_t kt = 0; kt < nk; ++kt) {
-    {
-      bf16x8 ga[4], gb[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ga[i] = fa[i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) gb[j] = fb[j];
-      load_frags(kt % STAGES, 1);
-      mfma16(ga, gb);
-#pragma unroll
-      for (int t = 0; t < 12; ++t) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    }
-    const bool more = kt + 1 < nk;
-    if (more) {
-      sync_slice(kt + 2 < nk ? 1u : 0u);
-      if (kt + 3 < nk) issue((kt + 3) % STAGES, (kt + 3) * BK);
-    }
-    {
-      bf16x8 ga[4], gb[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ga[i] = fa[i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) gb[j] = fb[j];
-      if (more) load_frags((kt + 1) % STAGES, 0);
-      mfma16(ga, gb);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);  // one global -> LDS load
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // one LDS read
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
-    }
+  const uint32_t main_end = nk > STAGES - 1 ? nk - (STAGES - 1) : 0u;
+  for (uint32_t kt = 0; kt < main_end; ++kt) {
+    step(kt % STAGES, 1, false, 0, 0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kWaitNext);
+    barrier();
+    step((kt + 1) % STAGES, 0, true, (kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
   }
+  for (uint32_t kt = main_end; kt < nk; ++kt) {
+    step(kt % STAGES, 1, false, 0, 0);
+    if (kt + 1 < nk) {
+      asm volatile("" ::: "memory");
+      if (kt + 2 < nk) __builtin_amdgcn_s_waitcnt(kWaitNext);
+      else __builtin_amdgcn_s_waitcnt(kWaitLast);
+      barrier();
+    }
+    // On the last iteration this reads a stale buffer whose values are unused.
+    step((kt + 1) % STAGES, 0, false, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));  // nothing in flight past the loop
 }
 
 template <bool B_NK, typename Epi, int SWZ = 1, bool SPREAD = true, bool PREFETCH = true, bool DMA = true>

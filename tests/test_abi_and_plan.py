@@ -170,7 +170,7 @@ def test_fusion_disabled_lowers_every_chain_generically():
 def test_fused_locals_stay_in_registers():
     e = programs.CONFIG_PROGRAMS["layernorm_1024"]().emit()
     assert "local" not in e.plan  # mean/var never touch HBM
-    assert e.source.count("__syncthreads") == 0  # 32 lanes per row: no cross-wave exchange
+    assert e.source.count("__syncthreads") == 0  # one wave per row: no cross-wave exchange
 
 
 def test_nonfinite_literals_are_valid_hip():
