@@ -222,7 +222,7 @@ def _traffic(symbol):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b")
     ap.add_argument("--settle-ms", type=float, default=1000.0,

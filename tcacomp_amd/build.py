@@ -2,7 +2,7 @@
 object the tests and the bench launch.
 
 The host library holds the runtime (plain HIP host API), the plan
-interpreter, the DSL builder and the HIP emitter; it is ordinary C++ built
+interpreter, the DSL builder, the .tca text frontend and the HIP emitter; it is ordinary C++ built
 with g++ against the ROCm headers. Device code exists only as emitted
 kernels, compiled by hipcc for gfx950 into ``_kcache/``.
 """
@@ -26,6 +26,12 @@ SOURCES = [
     "cg/emit_hip.cpp",
     "cg/gemm_emit.cpp",
     "cg/capi.cpp",
+    "syntax/lexer.cpp",
+    "syntax/parser.cpp",
+    "syntax/check.cpp",
+    "syntax/lower.cpp",
+    "syntax/module.cpp",
+    "syntax/capi.cpp",
 ]
 
 CXXFLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
@@ -46,7 +52,7 @@ def build_library(jobs=8):
     cmds = []
     for s in SOURCES:
         src = os.path.join(CSRC, s)
-        obj = os.path.join(OBJ_DIR, os.path.basename(s).replace(".cpp", ".o"))
+        obj = os.path.join(OBJ_DIR, s.replace("/", "_").replace(".cpp", ".o"))
         objs.append(obj)
         cmds.append(["g++"] + CXXFLAGS + ["-c", src, "-o", obj])
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:

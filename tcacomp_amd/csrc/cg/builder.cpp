@@ -9,13 +9,6 @@
 namespace tca {
 namespace pkg {
 
-namespace {
-
-struct BuiltinSig {
-  int arity;
-  ir::Elem arg, result;
-};
-
 // The pure scalar-builtin registry (internal/ir/builtins.go:25-33).
 bool LookupBuiltin(const std::string& name, BuiltinSig* sig) {
   static const std::map<std::string, BuiltinSig> kBuiltins = {
@@ -32,6 +25,8 @@ bool LookupBuiltin(const std::string& name, BuiltinSig* sig) {
   *sig = it->second;
   return true;
 }
+
+namespace {
 
 // Lambda-parameter names (pkg/chain.go:83-87).
 const char* kRootNames[] = {"l", "r", "s", "t", "u", "w", "x", "y", "z"};

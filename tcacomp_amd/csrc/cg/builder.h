@@ -32,6 +32,14 @@
 namespace tca {
 namespace pkg {
 
+// One registered pure scalar builtin: arity, the (shared) argument type and
+// the result type.
+struct BuiltinSig {
+  int arity;
+  ir::Elem arg, result;
+};
+bool LookupBuiltin(const std::string& name, BuiltinSig* sig);
+
 class Builder {
  public:
   explicit Builder(std::string name);

@@ -4,22 +4,9 @@
 #include <string>
 
 #include "builder.h"
+#include "capi_types.h"
 #include "emit.h"
 #include "tca_cg.h"
-
-struct tca_builder_s {
-  explicit tca_builder_s(const char* name) : b(name ? name : "kernel") {}
-  tca::pkg::Builder b;
-  tca::ir::Graph built;
-  bool is_built = false;
-  std::string ir_text;
-  std::string expr_err;
-  std::string err;
-};
-
-struct tca_emit_result_s {
-  tca::cg::Result r;
-};
 
 namespace {
 

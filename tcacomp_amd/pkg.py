@@ -177,6 +177,14 @@ class Builder:
         if not self._h:
             raise MemoryError("tca_builder_new failed")
 
+    @classmethod
+    def _adopt(cls, name, handle):
+        """Wraps a builder handle made elsewhere (the .tca frontend)."""
+        b = cls.__new__(cls)
+        b.name = name
+        b._h = handle
+        return b
+
     def __del__(self):
         h = getattr(self, "_h", None)
         if h:

@@ -22,18 +22,27 @@ SUITE below.
 """
 from .pkg import (TBF16, TF32, At, Call, Cast, NewBuilder)
 
-NEG_INF = float("-inf")
-
 
 def _sum(b):
     return lambda acc, v: b.Add(acc, v)
+
+
+def _static(b, name, extent):
+    """A dim handle: dynamic under its name, or a compile-time extent under the
+    e<extent> name the .tca frontend gives unnamed static dims."""
+    return b.Dim(name, 0) if extent == 0 else b.Dim("e%d" % extent, extent)
+
+
+def _neg_inf(b):
+    """-inf as the .tca source spells it (-inf_f32: a negated literal)."""
+    return b.Neg(b.Float32(float("inf")))
 
 
 def scale_relu(cols=0):
     """C1 in the reference-legal encoding: x, y carry a trailing extent-1
     axis that a degenerate reduce drops."""
     b = NewBuilder("scale_relu")
-    M, N, U = b.Dim("M", 0), b.Dim("N", cols), b.Dim("e1", 1)
+    M, N, U = b.Dim("M", 0), _static(b, "N", cols), b.Dim("e1", 1)
     x = b.Tensor("x", TF32, M, N, U)
     y = b.Tensor("y", TF32, M, N, U)
     z = b.Tensor("z", TF32, M, N)
@@ -65,27 +74,27 @@ def row_sum_max(cols=8192):
     """C2: two chains over the same nest; GVN-style fusion makes them one
     kernel reading x once."""
     b = NewBuilder("row_sum_max_%d" % cols)
-    R, C = b.Dim("R", 0), b.Dim("C", cols)
+    R, C = b.Dim("R", 0), _static(b, "C", cols)
     x = b.Tensor("x", TF32, R, C)
     s = b.Tensor("sum", TF32, R)
     m = b.Tensor("max", TF32, R)
     (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C)
      .Reduce(b.Float32(0), _sum(b)).Store(s, R))
     (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C)
-     .Reduce(b.Float32(NEG_INF), lambda acc, v: Call("fmaxf", acc, v)).Store(m, R))
+     .Reduce(_neg_inf(b), lambda acc, v: Call("fmaxf", acc, v)).Store(m, R))
     return b.Build()
 
 
 def softmax(cols=4096):
     """C3: y = exp(x - rowmax) / rowsum(exp(x - rowmax))."""
     b = NewBuilder("softmax_%d" % cols)
-    R, C = b.Dim("R", 0), b.Dim("C", cols)
+    R, C = b.Dim("R", 0), _static(b, "C", cols)
     x = b.Tensor("x", TF32, R, C)
     y = b.Tensor("y", TF32, R, C)
     mx = b.Local("mx", TF32, R)
     den = b.Local("den", TF32, R)
     (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C)
-     .Reduce(b.Float32(NEG_INF), lambda acc, v: Call("fmaxf", acc, v)).Store(mx, R))
+     .Reduce(_neg_inf(b), lambda acc, v: Call("fmaxf", acc, v)).Store(mx, R))
     (b.Stmt().Iter(R, C).Map([At(x, R, C), At(mx, R)], lambda l, r: Call("expf", b.Sub(l, r))).As(R, C)
      .Reduce(b.Float32(0), _sum(b)).Store(den, R))
     (b.Stmt().Iter(R, C)
@@ -98,7 +107,7 @@ def layernorm(cols=1024):
     """C4: mean and (centred) variance over the row, then
     (x - mean) * rsqrtf(var + eps) * gamma + beta."""
     b = NewBuilder("layernorm_%d" % cols)
-    R, C = b.Dim("R", 0), b.Dim("C", cols)
+    R, C = b.Dim("R", 0), _static(b, "C", cols)
     x = b.Tensor("x", TF32, R, C)
     gamma = b.Tensor("gamma", TF32, C)
     beta = b.Tensor("beta", TF32, C)
@@ -132,11 +141,14 @@ def copy_f32():
     return b.Build()
 
 
-def _matmul(name, elem, b_nk=False, epilogue=None, scalars=()):
+def _matmul(name, elem, b_nk=False, epilogue=None, scalars=(), names=None):
+    """names = (M, K, N, lhs, rhs) spellings. Dims are declared in
+    first-appearance order (M, K, N), as the .tca frontend declares them."""
+    nm = names or ("M", "K", "N", "lhs", "rhs")
     b = NewBuilder(name)
-    M, N, K = b.Dim("M", 0), b.Dim("N", 0), b.Dim("K", 0)
-    lhs = b.Tensor("lhs", elem, M, K)
-    rhs = b.Tensor("rhs", elem, N, K) if b_nk else b.Tensor("rhs", elem, K, N)
+    M, K, N = b.Dim(nm[0], 0), b.Dim(nm[1], 0), b.Dim(nm[2], 0)
+    lhs = b.Tensor(nm[3], elem, M, K)
+    rhs = b.Tensor(nm[4], elem, N, K) if b_nk else b.Tensor(nm[4], elem, K, N)
     out = b.Tensor("out", TF32, M, N)
     sc = [b.ScalarParam(s, TF32) for s in scalars]
     if elem == TF32:
@@ -174,14 +186,19 @@ def _rank3_reduce(name, k_extent, body, scalars=(), piped=None, piped_scalars=()
     """out[i][j] = sum_k f(x, z) over x, z [R, C, K] (or [R, K, C] when the
     reduced axis is the middle one, as row_sum.tca and softmax.tca)."""
     b = NewBuilder(name)
-    R, C, K = b.Dim("R", 0), b.Dim("C", 0), b.Dim("K" if k_extent == 0 else "e%d" % k_extent, k_extent)
+    kname = "K" if k_extent == 0 else "e%d" % k_extent
+    if middle:  # dims in first-appearance order of x's shape, as the .tca frontend declares them
+        R, K, C = b.Dim("R", 0), b.Dim(kname, k_extent), b.Dim("C", 0)
+    else:
+        R, C, K = b.Dim("R", 0), b.Dim("C", 0), b.Dim(kname, k_extent)
     shape = (R, K, C) if middle else (R, C, K)
     x = b.Tensor("x", TF32, *shape)
     z = b.Tensor("z", TF32, *shape)
     out = b.Tensor("out", TF32, R, C)
     sc = [b.ScalarParam(s, TF32) for s in scalars]
     psc = [b.ScalarParam(s, TF32) for s in piped_scalars]
-    ar = (b.Stmt().Iter(*shape)
+    # the reduced axis iterates last (the frontend's relocation)
+    ar = (b.Stmt().Iter(R, C, K)
           .Map([At(x, *shape), At(z, *shape)], lambda v, w: body(b, v, w, *sc))
           .As(R, C, K)
           .Reduce(b.Float32(0), _sum(b)))
@@ -233,7 +250,7 @@ def suite_row_sum():
 
 def suite_softmax():
     # testing/kernels/fusion/softmax.tca:24-41 (reduce over the middle axis)
-    return _rank3_reduce("softmax_core", 8, lambda b, v, w: b.Mul(Call("expf", v), w), middle=True)
+    return _rank3_reduce("softmax", 8, lambda b, v, w: b.Mul(Call("expf", v), w), middle=True)
 
 
 def suite_transpose():
@@ -243,7 +260,7 @@ def suite_transpose():
 
 def suite_layernorm():
     # testing/kernels/llm/layernorm.tca:17-40 (RMS-flavoured core, dynamic K)
-    return _rank3_reduce("layernorm_rms", 0, lambda b, v, w: b.Mul(b.Mul(v, v), w),
+    return _rank3_reduce("layernorm", 0, lambda b, v, w: b.Mul(b.Mul(v, v), w),
                          piped=lambda b, v, inv_n, eps: b.Mul(v, Call("rsqrtf", b.Add(b.Mul(v, inv_n), eps))),
                          piped_scalars=("inv_n", "eps"))
 
@@ -266,7 +283,8 @@ def suite_mlp():
 
 def suite_qk_score():
     # testing/kernels/llm/qk_score.tca:7-31 (kk indexed [n][k])
-    return _matmul("qk_score", TF32, b_nk=True, epilogue=lambda b, v, scale: b.Mul(v, scale), scalars=("scale",))
+    return _matmul("qk_score", TF32, b_nk=True, epilogue=lambda b, v, scale: b.Mul(v, scale), scalars=("scale",),
+                   names=("H", "D", "N", "q", "kk"))
 
 
 # name -> (builder, suite dims [d0, d1, d2], scalars) ; dims/scalars from testing/suite.toml

@@ -17,7 +17,7 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def declared_functions():
     names = set()
-    for h in ("tca_rt.h", "tca_cg.h"):
+    for h in sorted(os.listdir(os.path.join(REPO, "include"))):
         text = open(os.path.join(REPO, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         for m in re.finditer(r"\b(tca_[a-z0-9_]+)\s*\(", text):
