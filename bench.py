@@ -35,9 +35,15 @@ CONFIGS = {
     "c4": ("layernorm_1024", "C4 layernorm f32 [32768,1024]"),
     "c5f": ("gemm_f32", "C5 gemm f32 4096^3"),
     "c5b": ("gemm_bf16", "C5 gemm bf16-in f32-acc 4096^3"),
+    # C2-C4 with the row length a run-time dim (streaming row family); same
+    # data and algorithmic bytes, not configurations of their own
+    "c2s": ("row_sum_max_dyn", "C2 with run-time row length (streaming family)"),
+    "c3s": ("softmax_dyn", "C3 with run-time row length (streaming family)"),
+    "c4s": ("layernorm_dyn", "C4 with run-time row length (streaming family)"),
     # not a configuration: the plain copy used to calibrate rocprof counters
     "copy": ("copy_f32", "copy f32 [8192,8192] (counter calibration)"),
 }
+STREAM_OF = {"c2s": "c2", "c3s": "c3", "c4s": "c4"}
 
 
 def _events():
@@ -57,6 +63,8 @@ def _setup(key, dev):
 
     name = CONFIGS[key][0]
     prog = compiler.compile_program(programs.CONFIG_PROGRAMS[name](), jit=os.environ.get("TCA_JIT", "0") != "0")
+    streamed = key in STREAM_OF
+    key = STREAM_OF.get(key, key)
 
     def dev_f32(a):
         return torch.from_numpy(a).to(dev)
@@ -129,6 +137,8 @@ def _setup(key, dev):
         cpu = (key, (a, b))
     nsets = max(2, math.ceil(MALL_DEFEAT_BYTES / per_set))
     sets = [make(i) for i in range(nsets)]
+    if streamed:
+        cpu = None  # the same CPU figure as the register-resident line
     return prog, sets, scalars, work, cpu
 
 
@@ -224,7 +234,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
                     help="untimed launches per config before the warmup steps, in wall-clock ms")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")

@@ -22,6 +22,7 @@ namespace cg {
 enum class Family {
   Elementwise,  // E: no real reduction; vectorised flat streaming
   Row,          // R/F: reductions (and maps) over the contiguous last axis of a fused nest
+  Stream,       // S: the same nests with a run-time (or register-exceeding) row length, streamed
   Gemm,         // G: dense K-contraction on MFMA
   Generic       // X: one thread per output element, sequential folds
 };

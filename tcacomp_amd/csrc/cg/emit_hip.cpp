@@ -39,6 +39,7 @@ const char* FamilyName(Family f) {
   switch (f) {
     case Family::Elementwise: return "elementwise";
     case Family::Row: return "row";
+    case Family::Stream: return "stream";
     case Family::Gemm: return "gemm";
     case Family::Generic: return "generic";
   }
@@ -351,6 +352,63 @@ OpKind Classify(const ir::Operand& o, const RowGeom& geo) {
   return OpKind::RowScalar;
 }
 
+// The structural conditions shared by the register-resident row family and
+// the streaming row family: every chain iterates (outer..., col) in one
+// order, at most one reduction per chain (over col) with an associative-
+// commutative combiner, operands are row tiles, column vectors or row
+// scalars. `stream` additionally refuses elementwise chains into locals (a
+// streamed row is never held, so a row-tile local could not be re-read).
+bool RowShape(const Graph& g, const std::vector<int>& chains, bool stream, RowGeom* out) {
+  RowGeom& geo = *out;
+  const ir::Chain& c0 = g.chains[chains[0]];
+  geo.as = c0.root.as;
+  geo.col = geo.as.back();
+  geo.outer.assign(geo.as.begin(), geo.as.end() - 1);
+  auto no = [&](const std::string& w) {
+    geo.ok = false;
+    geo.why = w;
+    return false;
+  };
+  std::set<int> produced_tile, produced_scalar;
+  for (int ci : chains) {
+    const ir::Chain& c = g.chains[ci];
+    if (c.root.as != geo.as) return no("iteration orders differ");
+    if (c.reduces.size() > 1) return no("more than one reduction in a chain");
+    if (c.reduces.size() == 1 && !IsMonoidCombiner(g, c.reduces[0]))
+      return no("combiner is not an associative-commutative op over (acc, now)");
+    for (const auto& o : c.root.ops) {
+      OpKind k = Classify(o, geo);
+      if (k == OpKind::Bad) return no("operand " + g.tensors[o.tensor].name + " is not row-shaped");
+      if (g.tensors[o.tensor].local) {
+        bool inside_tile = produced_tile.count(o.tensor) > 0, inside_scalar = produced_scalar.count(o.tensor) > 0;
+        if (inside_tile && k != OpKind::RowTile) return no("local read with a different shape");
+        if (inside_scalar && k != OpKind::RowScalar) return no("local read with a different shape");
+      }
+    }
+    if (c.has_piped)
+      for (const auto& o : c.piped.ops)
+        if (Classify(o, geo) != OpKind::RowScalar) return no("piped operand is not a row scalar");
+    const ir::Tensor& st = g.tensors[c.store_tensor];
+    if (c.reduces.empty()) {
+      if (c.store_axes != geo.as) return no("elementwise store is not in iteration order");
+      if (st.local && stream) return no("a streamed row cannot hold a row-tile local");
+      if (st.local) produced_tile.insert(c.store_tensor);
+    } else {
+      if (st.local) produced_scalar.insert(c.store_tensor);
+    }
+  }
+  geo.ok = true;
+  return true;
+}
+
+// Streaming row family: row length known only at run time (or too long for
+// registers); every chain of the nest streams the row.
+RowGeom StreamCheck(const Graph& g, const std::vector<int>& chains) {
+  RowGeom geo;
+  RowShape(g, chains, true, &geo);
+  return geo;
+}
+
 RowGeom RowCheck(const Graph& g, const std::vector<int>& chains, uint32_t nv_target) {
   RowGeom geo;
   const ir::Chain& c0 = g.chains[chains[0]];
@@ -364,35 +422,8 @@ RowGeom RowCheck(const Graph& g, const std::vector<int>& chains, uint32_t nv_tar
   };
   if (g.dims[geo.col].extent == 0) return no("row axis @" + g.dims[geo.col].name + " has a dynamic extent");
   geo.C = static_cast<uint32_t>(g.dims[geo.col].extent);
-  std::set<int> produced_tile, produced_scalar;
-  for (int ci : chains) {
-    const ir::Chain& c = g.chains[ci];
-    if (c.root.as != geo.as) return no("iteration orders differ");
-    if (c.reduces.size() > 1) return no("more than one reduction in a chain");
-    if (c.reduces.size() == 1 && !IsMonoidCombiner(g, c.reduces[0]))
-      return no("combiner is not an associative-commutative op over (acc, now)");
-    for (const auto& o : c.root.ops) {
-      OpKind k = Classify(o, geo);
-      if (k == OpKind::Bad) return no("operand " + g.tensors[o.tensor].name + " is not row-shaped");
-      if (g.tensors[o.tensor].local) {
-        // Produced inside the nest: must match the producer's shape kind.
-        bool inside_tile = produced_tile.count(o.tensor) > 0, inside_scalar = produced_scalar.count(o.tensor) > 0;
-        if (inside_tile && k != OpKind::RowTile) return no("local read with a different shape");
-        if (inside_scalar && k != OpKind::RowScalar) return no("local read with a different shape");
-      }
-    }
-    if (c.has_piped)
-      for (const auto& o : c.piped.ops)
-        if (Classify(o, geo) != OpKind::RowScalar) return no("piped operand is not a row scalar");
-    const ir::Tensor& st = g.tensors[c.store_tensor];
-    if (c.reduces.empty()) {
-      if (c.store_axes != geo.as) return no("elementwise store is not in iteration order");
-      if (st.local) produced_tile.insert(c.store_tensor);
-    } else {
-      if (st.local) produced_scalar.insert(c.store_tensor);
-    }
-  }
-  geo.V = (geo.C % 4 == 0) ? 4 : (geo.C % 2 == 0 ? 2 : 1);
+  if (!RowShape(g, chains, false, &geo)) return geo;
+  geo.V =(geo.C % 4 == 0) ? 4 : (geo.C % 2 == 0 ? 2 : 1);
   geo.vecs = geo.C / geo.V;
   uint32_t tpr = 1;
   while (tpr * 2 <= geo.vecs / nv_target && tpr * 2 <= 1024) tpr *= 2;
@@ -500,7 +531,7 @@ class Emitter {
       if (!cur.empty() && opts_.allow_fused && g_.chains[i].root.as == g_.chains[cur[0]].root.as) {
         std::vector<int> cand = cur;
         cand.push_back(i);
-        if (RowCheck(g_, cand, RowNV()).ok && !IsGemm(cur)) {
+        if ((RowCheck(g_, cand, RowNV()).ok || StreamCheck(g_, cand).ok) && !IsGemm(cur)) {
           cur = cand;
           continue;
         }
@@ -523,7 +554,8 @@ class Emitter {
         }
       }
       if (producer < 0) continue;  // dead local
-      bool fused = an_.nests[producer].family == Family::Row && readers.size() == 1 && readers.count(producer);
+      const Family pf = an_.nests[producer].family;
+      bool fused = (pf == Family::Row || pf == Family::Stream) && readers.size() == 1 && readers.count(producer);
       if (fused) an_.reg_nest[t] = producer;
       else an_.hbm_local[t] = true;
     }
@@ -542,9 +574,10 @@ class Emitter {
       if (IsGemm(chains)) return Family::Gemm;
       if (opts_.allow_fused && DegenerateReduces(g_, c) && !ReadsRegLocalCandidate(c)) return Family::Elementwise;
       if (opts_.allow_fused && RowCheck(g_, chains, RowNV()).ok) return Family::Row;
+      if (opts_.allow_fused && StreamCheck(g_, chains).ok) return Family::Stream;
       return Family::Generic;
     }
-    return Family::Row;
+    return RowCheck(g_, chains, RowNV()).ok ? Family::Row : Family::Stream;
   }
 
   bool ReadsRegLocalCandidate(const ir::Chain&) { return false; }
@@ -638,6 +671,7 @@ class Emitter {
     switch (n.family) {
       case Family::Elementwise: return EmitElementwise(ni, err);
       case Family::Row: return EmitRow(ni, err);
+      case Family::Stream: return EmitStream(ni, err);
       case Family::Gemm: return EmitGemmNest(ni, err);
       case Family::Generic: return EmitGeneric(ni, err);
     }
@@ -936,15 +970,20 @@ class Emitter {
         << ";\n";
     }
     auto coord = [&](int a) { return "c" + std::to_string(a); };
-    // Which tensors are register locals of this nest.
+    // Which tensors are register locals of this nest. Anything a chain of the
+    // nest stores is consumed by later chains of the nest from registers,
+    // never re-read from memory inside the same kernel (a store by one lane
+    // is not visible to the others without a barrier).
     auto isReg = [&](int t) { return g_.tensors[t].local && an_.reg_nest[t] == ni; };
+    std::set<int> produced;
+    for (int ci : n.chains) produced.insert(g_.chains[ci].store_tensor);
     // Preload row tiles and column vectors read from memory.
     std::set<int> tiles, cols, rscal;
     for (int ci : n.chains) {
       const ir::Chain& c = g_.chains[ci];
       for (const auto& op : c.root.ops) {
         OpKind k = Classify(op, geo);
-        if (isReg(op.tensor)) continue;
+        if (isReg(op.tensor) || produced.count(op.tensor)) continue;
         if (k == OpKind::RowTile) tiles.insert(op.tensor);
         else if (k == OpKind::ColVec) cols.insert(op.tensor);
       }
@@ -966,9 +1005,9 @@ class Emitter {
       o << "    else for (uint32_t q = 0; q < V; ++q) x" << t << "[j][q] = " << T << "(0);\n  }\n";
     }
     // Row-scalar value of operand `op` (memory or register local).
-    std::map<int, std::string> regScalar;  // local tensor -> register variable
+    std::map<int, std::string> regScalar;  // tensor produced in this nest -> register variable
     auto rowScalar = [&](const ir::Operand& op) -> std::string {
-      if (isReg(op.tensor)) return regScalar.count(op.tensor) ? regScalar[op.tensor] : "/*missing*/0";
+      if (regScalar.count(op.tensor)) return regScalar[op.tensor];
       return "(active ? t" + std::to_string(op.tensor) + "[" + Offset(op.tensor, op.axes, coord) + "] : " +
              CType(g_.tensors[op.tensor].elem) + "(0))";
     };
@@ -1038,7 +1077,7 @@ class Emitter {
         const std::string T = CType(g_.tensors[st].elem);
         const std::string var = "r" + std::to_string(ci);
         o << "  const " << T << " " << var << " = " << val << ";\n";
-        if (isReg(st)) regScalar[st] = var;
+        regScalar[st] = var;
         if (!isReg(st) || an_.hbm_local[st]) {
           o << "  if (active && lane == 0u) t" << st << "[" << Offset(st, c.store_axes, coord) << "] = " << var
             << ";\n";
@@ -1081,7 +1120,7 @@ class Emitter {
         const int st = c.store_tensor;
         const std::string T = CType(g_.tensors[st].elem);
         o << "  // statement #" << ci << ": elementwise over the row into " << g_.tensors[st].name << "\n";
-        const bool reg = isReg(st);
+        const bool reg = true;  // later chains of the nest read the register copy
         if (reg) o << "  tca::hip::vec<" << T << ", V> x" << st << "[NV];\n";
         o << "#pragma unroll\n  for (uint32_t j = 0; j < NV; ++j) {\n";
         o << "    tca::hip::vec<" << T << ", V> outv;\n";
@@ -1091,7 +1130,7 @@ class Emitter {
         o << bs.str();
         o << "      outv[q] = " << v << ";\n    }\n";
         if (reg) o << "    x" << st << "[j] = outv;\n";
-        if (!reg || an_.hbm_local[st]) {
+        if (!isReg(st) || an_.hbm_local[st]) {  // outputs and locals other nests read
           o << "    if (active && (j + 1u < NV || tail_ok)) tca::hip::store_vec_nt<" << T << ", V>(t" << st
             << " + row_base + (j * TPR + lane) * V, outv);\n";
         }
@@ -1107,6 +1146,211 @@ class Emitter {
     det << "row=" << geo.C << " lanes/row=" << geo.tpr << " vec/lane=" << geo.nv << "x" << geo.V
         << " rows/block=" << geo.rpb << " block=" << geo.block;
     AddKernel(pk, Family::Row, n.chains, det.str());
+    return true;
+  }
+
+  // The argument names of Signature(n), in its order.
+  std::string CallArgs(const Nest& n) {
+    std::string s;
+    auto add = [&](const std::string& a) { s += (s.empty() ? "" : ", ") + a; };
+    for (int t : NestTensors(n)) add("t" + std::to_string(t));
+    for (size_t d = 0; d < g_.dims.size(); ++d) add("d" + std::to_string(d));
+    for (int sc : NestScalars(n)) add("s" + std::to_string(sc));
+    return s;
+  }
+
+  // S: the row nests of family R with a row length known only at run time
+  // (or too long for registers). Every chain of the nest streams the row in
+  // 16-byte vectors (4 elements when the length allows it, else 1); S lanes
+  // share a row, S chosen at run time as the largest power of two <= 256
+  // that leaves every lane >= 8 vectors, so short rows pack many rows per
+  // wave and long ones spread over up to four waves. Each lane folds its
+  // strided share with a presence flag (lanes that saw nothing, and empty
+  // rows, contribute nothing; the output is then init), then the segment
+  // meets by shuffles and, past 64 lanes, through LDS. Row scalars produced
+  // in the nest stay in registers. Grid-stride over row groups, the grid
+  // capped at 2048 workgroups (8 per CU).
+  bool EmitStream(int ni, std::string* err) {
+    const Nest& n = an_.nests[ni];
+    RowGeom geo = StreamCheck(g_, n.chains);
+    if (!geo.ok) {
+      *err = "emit: stream family rejected a nest it classified: " + geo.why;
+      return false;
+    }
+    PlanKernel pk;
+    pk.symbol = Sym(g_, prefix_, ni);
+    pk.block = 256;
+    pk.grid.push_back(DimProduct(geo.outer) + "/1:2048");
+    const std::string sig = Signature(n, &pk);
+    std::ostringstream& o = src_;
+    const std::string body_fn = pk.symbol + "_rows";
+    auto coord = [&](int a) { return "c" + std::to_string(a); };
+    auto isReg = [&](int t) { return g_.tensors[t].local && an_.reg_nest[t] == ni; };
+    std::set<int> produced;
+    for (int ci : n.chains) produced.insert(g_.chains[ci].store_tensor);
+
+    o << "// statements";
+    for (int ci : n.chains) o << " #" << ci;
+    o << ": streaming row family; row @" << g_.dims[geo.col].name << " streamed, lanes/row chosen at run time\n";
+    o << "template <uint32_t V>\n__device__ __forceinline__ void " << body_fn << "(\n    " << sig << ") {\n";
+    o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
+    o << "  const uint32_t VECS = C / V;\n";
+    o << "  uint32_t S = 1u;\n  while (S < 256u && S * 16u <= VECS) S <<= 1;\n";
+    o << "  const uint32_t RPB = 256u / S, SEG = S < 64u ? S : 64u, WPR = S > 64u ? S / 64u : 1u;\n";
+    o << "  const uint32_t nrows = " << ProductExpr(geo.outer) << ";\n";
+    o << "  const uint32_t ngroups = (nrows + RPB - 1u) / RPB;\n";
+    // LDS for the cross-wave meeting of each reduction (rows of 128/256 lanes).
+    for (int ci : n.chains) {
+      const ir::Chain& c = g_.chains[ci];
+      if (c.reduces.empty()) continue;
+      const std::string T = CType(g_.exprs[c.root.fn.body].type);
+      o << "  __shared__ " << T << " red" << ci << "[4];\n  __shared__ int redh" << ci << "[4];\n";
+      o << "  const auto comb" << ci << " = [](" << T << " acc, " << T << " now) -> " << T << " {\n";
+      ExprGen cg(g_, o, "    ", &counter_);
+      cg.Bind(c.reduces[0].fn.params[0], "acc");
+      cg.Bind(c.reduces[0].fn.params[1], "now");
+      const std::string r = cg.Gen(c.reduces[0].fn.body);
+      o << "    return " << r << ";\n  };\n";
+    }
+    o << "  for (uint32_t grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {\n";
+    o << "    const uint32_t row = grp * RPB + threadIdx.x / S;\n";
+    o << "    const uint32_t lane = threadIdx.x % S;\n";
+    o << "    const bool active = row < nrows;\n";
+    o << "    const uint64_t row_base = static_cast<uint64_t>(active ? row : 0u) * C;\n";
+    o << "    uint32_t rrem = active ? row : 0u;\n";
+    for (int k = static_cast<int>(geo.outer.size()) - 1; k >= 0; --k) {
+      const int a = geo.outer[k];
+      o << "    const uint32_t c" << a << " = rrem % " << ExtentExpr(g_, a) << "; rrem /= " << ExtentExpr(g_, a) << ";\n";
+    }
+    // Row scalars read from memory: once per row.
+    std::map<int, std::string> regScalar;
+    std::set<int> loadedScalar;
+    for (int ci : n.chains) {
+      const ir::Chain& c = g_.chains[ci];
+      std::vector<const ir::Operand*> ops;
+      for (const auto& op : c.root.ops) ops.push_back(&op);
+      if (c.has_piped)
+        for (const auto& op : c.piped.ops) ops.push_back(&op);
+      for (const ir::Operand* op : ops) {
+        if (Classify(*op, geo) != OpKind::RowScalar || produced.count(op->tensor) || isReg(op->tensor)) continue;
+        if (!loadedScalar.insert(op->tensor).second) continue;
+        const std::string T = CType(g_.tensors[op->tensor].elem);
+        const std::string var = "rs" + std::to_string(op->tensor);
+        o << "    const " << T << " " << var << " = active ? t" << op->tensor << "[" << Offset(op->tensor, op->axes, coord)
+          << "] : " << T << "(0);\n";
+        regScalar[op->tensor] = var;
+      }
+    }
+    auto rowScalar = [&](const ir::Operand& op) -> std::string {
+      auto it = regScalar.find(op.tensor);
+      return it != regScalar.end() ? it->second : std::string("/*missing row scalar*/0");
+    };
+    // Loads of the row-tile / column-vector operands of chain c at vector v.
+    auto loads = [&](const ir::Chain& c, const std::string& ind) {
+      std::set<int> done;
+      for (const auto& op : c.root.ops) {
+        const OpKind k = Classify(op, geo);
+        if ((k != OpKind::RowTile && k != OpKind::ColVec) || !done.insert(op.tensor).second) continue;
+        const std::string T = CType(g_.tensors[op.tensor].elem);
+        if (k == OpKind::RowTile)
+          o << ind << "const auto x" << op.tensor << " = tca::hip::load_vec_nt<" << T << ", V>(t" << op.tensor
+            << " + row_base + static_cast<uint64_t>(v) * V);\n";
+        else
+          o << ind << "const auto x" << op.tensor << " = tca::hip::load_vec<" << T << ", V>(t" << op.tensor
+            << " + static_cast<uint64_t>(v) * V);\n";
+      }
+    };
+    auto elemValue = [&](std::ostringstream& os, const std::string& ind, const ir::Chain& c) -> std::string {
+      ExprGen eg(g_, os, ind, &counter_);
+      for (size_t k = 0; k < c.root.ops.size(); ++k) {
+        const auto& op = c.root.ops[k];
+        const OpKind kind = Classify(op, geo);
+        eg.Bind(c.root.fn.params[k], (kind == OpKind::RowTile || kind == OpKind::ColVec)
+                                         ? "x" + std::to_string(op.tensor) + "[q]"
+                                         : rowScalar(op));
+      }
+      return eg.Gen(c.root.fn.body);
+    };
+    for (int ci : n.chains) {
+      const ir::Chain& c = g_.chains[ci];
+      const int st = c.store_tensor;
+      if (!c.reduces.empty()) {
+        const std::string T = CType(g_.exprs[c.root.fn.body].type);
+        const std::string P = "part" + std::to_string(ci), H = "has" + std::to_string(ci);
+        o << "    // statement #" << ci << ": reduce over @" << g_.dims[geo.col].name << " into " << g_.tensors[st].name
+          << "\n";
+        o << "    " << T << " " << P << " = " << T << "(0);\n    bool " << H << " = false;\n";
+        o << "    if (active) {\n      for (uint32_t v = lane; v < VECS; v += S) {\n";
+        loads(c, "        ");
+        o << "#pragma unroll\n        for (uint32_t q = 0; q < V; ++q) {\n";
+        std::ostringstream bs;
+        const std::string ev = elemValue(bs, "          ", c);
+        o << bs.str();
+        o << "          " << P << " = " << H << " ? comb" << ci << "(" << P << ", " << ev << ") : " << ev << ";\n";
+        o << "          " << H << " = true;\n        }\n      }\n    }\n";
+        o << "    " << P << " = tca::hip::seg_allreduce_rt(" << P << ", " << H << ", SEG, comb" << ci << ");\n";
+        o << "    if (WPR > 1u) {\n";
+        o << "      if ((threadIdx.x & 63u) == 0u) { red" << ci << "[threadIdx.x >> 6] = " << P << "; redh" << ci
+          << "[threadIdx.x >> 6] = " << H << " ? 1 : 0; }\n";
+        o << "      __syncthreads();\n";
+        o << "      const uint32_t w0 = (threadIdx.x / S) * WPR;\n";
+        o << "      " << P << " = " << T << "(0);\n      " << H << " = false;\n";
+        o << "      for (uint32_t w = 0; w < WPR; ++w) {\n";
+        o << "        if (redh" << ci << "[w0 + w] == 0) continue;\n";
+        o << "        " << P << " = " << H << " ? comb" << ci << "(" << P << ", red" << ci << "[w0 + w]) : red" << ci
+          << "[w0 + w];\n";
+        o << "        " << H << " = true;\n      }\n";
+        o << "      __syncthreads();\n    }\n";
+        // init once per output (an empty row yields init), then the piped map.
+        const ir::ReduceStage& r = c.reduces[0];
+        std::string init;
+        {
+          ExprGen ig(g_, o, "    ", &counter_);
+          init = ig.Gen(r.init);
+        }
+        std::string val;
+        {
+          std::ostringstream fs;
+          ExprGen fg(g_, fs, "      ", &counter_);
+          fg.Bind(r.fn.params[0], init);
+          fg.Bind(r.fn.params[1], P);
+          val = fg.Gen(r.fn.body);
+          o << "    " << T << " fin" << ci << " = " << init << ";\n";
+          o << "    if (" << H << ") {\n" << fs.str() << "      fin" << ci << " = " << val << ";\n    }\n";
+          val = "fin" + std::to_string(ci);
+        }
+        if (c.has_piped) {
+          ExprGen pg(g_, o, "    ", &counter_);
+          pg.Bind(c.piped.fn.params[0], val);
+          for (size_t k = 0; k < c.piped.ops.size(); ++k) pg.Bind(c.piped.fn.params[k + 1], rowScalar(c.piped.ops[k]));
+          val = pg.Gen(c.piped.fn.body);
+        }
+        const std::string ST = CType(g_.tensors[st].elem);
+        const std::string var = "r" + std::to_string(ci);
+        o << "    const " << ST << " " << var << " = " << val << ";\n";
+        regScalar[st] = var;
+        if (!isReg(st) || an_.hbm_local[st])
+          o << "    if (active && lane == 0u) t" << st << "[" << Offset(st, c.store_axes, coord) << "] = " << var << ";\n";
+      } else {
+        const std::string T = CType(g_.tensors[st].elem);
+        o << "    // statement #" << ci << ": elementwise over the row into " << g_.tensors[st].name << "\n";
+        o << "    if (active) {\n      for (uint32_t v = lane; v < VECS; v += S) {\n";
+        loads(c, "        ");
+        o << "        tca::hip::vec<" << T << ", V> outv;\n";
+        o << "#pragma unroll\n        for (uint32_t q = 0; q < V; ++q) {\n";
+        std::ostringstream bs;
+        const std::string val = elemValue(bs, "          ", c);
+        o << bs.str();
+        o << "          outv[q] = " << val << ";\n        }\n";
+        o << "        tca::hip::store_vec_nt<" << T << ", V>(t" << st << " + row_base + static_cast<uint64_t>(v) * V, outv);\n";
+        o << "      }\n    }\n";
+      }
+    }
+    o << "  }\n}\n";
+    o << "extern \"C\" __global__ void __launch_bounds__(256) " << pk.symbol << "(\n    " << sig << ") {\n";
+    o << "  if ((" << ExtentExpr(g_, geo.col) << ") % 4u == 0u) " << body_fn << "<4u>(" << CallArgs(n) << ");\n";
+    o << "  else " << body_fn << "<1u>(" << CallArgs(n) << ");\n}\n\n";
+    AddKernel(pk, Family::Stream, n.chains, "row=runtime lanes/row=runtime(<=256) vec=4|1 grid-stride<=2048");
     return true;
   }
 

@@ -128,6 +128,24 @@ __device__ __forceinline__ T seg_allreduce(T v, Op op) {
   return v;
 }
 
+// All-reduce over aligned segments of `seg` lanes, a power of two <= 64 known
+// only at run time, of values that may be absent (`has` false: the lane saw
+// no element). Absent values are skipped; every lane of a segment ends with
+// the segment's total and the OR of the flags. Every lane of the wave must
+// call it (the shuffles are wave-wide). `op` must be associative and
+// commutative.
+template <typename T, typename Op>
+__device__ __forceinline__ T seg_allreduce_rt(T v, bool& has, uint32_t seg, Op op) {
+  for (uint32_t off = 1; off < seg; off <<= 1) {
+    const T o = xor_lanes(v, static_cast<int>(off));
+    const bool oh = __shfl_xor(static_cast<int>(has), static_cast<int>(off), 64) != 0;
+    if (has && oh) v = op(v, o);
+    else if (oh) v = o;
+    has = has || oh;
+  }
+  return v;
+}
+
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
 __device__ __forceinline__ uint32_t wave_id() { return threadIdx.x >> 6; }
 

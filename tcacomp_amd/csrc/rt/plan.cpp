@@ -47,7 +47,13 @@ bool ParseTerm(const Plan& p, const std::string& s, Term* t, std::string* err) {
     *err = "grid term '" + s + "' lacks a '/divisor'";
     return false;
   }
-  if (!ParseU64(s.substr(slash + 1), &t->divisor) || t->divisor == 0) {
+  const size_t colon = s.find(':', slash);
+  if (colon != std::string::npos && (!ParseU64(s.substr(colon + 1), &t->cap) || t->cap == 0)) {
+    *err = "grid term '" + s + "' has a bad cap";
+    return false;
+  }
+  if (!ParseU64(s.substr(slash + 1, colon == std::string::npos ? std::string::npos : colon - slash - 1), &t->divisor) ||
+      t->divisor == 0) {
     *err = "grid term '" + s + "' has a bad divisor";
     return false;
   }
@@ -243,6 +249,7 @@ std::string Serialize(const Plan& p) {
         first = false;
       }
       o << "/" << t.divisor;
+      if (t.cap != 0) o << ":" << t.cap;
     }
     o << "\n";
     for (const auto& a : k.args) {
@@ -361,6 +368,7 @@ bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims,
       }
     }
     uint64_t q = (prod + t.divisor - 1) / t.divisor;
+    if (t.cap != 0 && q > t.cap) q = t.cap;
     g *= q;
     if (g > (1ull << 62)) {
       *err = "kernel " + k.symbol + ": grid overflows";

@@ -8,8 +8,9 @@
 //   tensor <name> <dtype> <in|out|local> <rank> <dim-name>...
 //   scalar <name> <dtype>
 //   kernel <symbol> <block> <lds-bytes> <n-terms> <term>...
-//       term = <factor>[*<factor>...]/<divisor>, factor = dim name or integer;
-//       grid = product over terms of ceil(product(factors) / divisor)
+//       term = <factor>[*<factor>...]/<divisor>[:<cap>], factor = dim name or
+//       integer; grid = product over terms of ceil(product(factors) / divisor),
+//       each term limited to <cap> when one is given (grid-stride kernels)
 //   arg ptr <tensor> | arg dim <name> | arg scalar <name>    (for the last kernel)
 //   end
 //
@@ -55,6 +56,7 @@ struct Term {
   std::vector<int> dim_factors;  // indices into Plan::dims
   uint64_t const_factor = 1;
   uint64_t divisor = 1;
+  uint64_t cap = 0;  // 0 = none
 };
 
 struct Arg {

@@ -73,7 +73,7 @@ def scale_relu_map():
 def row_sum_max(cols=8192):
     """C2: two chains over the same nest; GVN-style fusion makes them one
     kernel reading x once."""
-    b = NewBuilder("row_sum_max_%d" % cols)
+    b = NewBuilder("row_sum_max_%s" % (cols or "dyn"))
     R, C = b.Dim("R", 0), _static(b, "C", cols)
     x = b.Tensor("x", TF32, R, C)
     s = b.Tensor("sum", TF32, R)
@@ -87,7 +87,7 @@ def row_sum_max(cols=8192):
 
 def softmax(cols=4096):
     """C3: y = exp(x - rowmax) / rowsum(exp(x - rowmax))."""
-    b = NewBuilder("softmax_%d" % cols)
+    b = NewBuilder("softmax_%s" % (cols or "dyn"))
     R, C = b.Dim("R", 0), _static(b, "C", cols)
     x = b.Tensor("x", TF32, R, C)
     y = b.Tensor("y", TF32, R, C)
@@ -106,7 +106,7 @@ def softmax(cols=4096):
 def layernorm(cols=1024):
     """C4: mean and (centred) variance over the row, then
     (x - mean) * rsqrtf(var + eps) * gamma + beta."""
-    b = NewBuilder("layernorm_%d" % cols)
+    b = NewBuilder("layernorm_%s" % (cols or "dyn"))
     R, C = b.Dim("R", 0), _static(b, "C", cols)
     x = b.Tensor("x", TF32, R, C)
     gamma = b.Tensor("gamma", TF32, C)
@@ -324,6 +324,10 @@ CONFIG_PROGRAMS = {
     "layernorm_96": lambda: layernorm(96),
     "softmax_16384": lambda: softmax(16384),
     "copy_f32": copy_f32,
+    # the same nests with the row length a run-time dim: the streaming family
+    "row_sum_max_dyn": lambda: row_sum_max(0),
+    "softmax_dyn": lambda: softmax(0),
+    "layernorm_dyn": lambda: layernorm(0),
 }
 
 

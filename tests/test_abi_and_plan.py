@@ -47,6 +47,13 @@ def test_validate_launch_grammar():
     assert L.tca_rt_validate_launch(1, 256, 160 * 1024 + 1) == _lib.TCA_ERR_LAUNCH
 
 
+def test_grid_term_cap():
+    rc, h = parse(PLAN.replace("M*N/1024", "M*N/1024:7"))
+    assert rc == 0, _lib.last_error()
+    rc, h2 = parse(PLAN.replace("M*N/1024", "M*N/1024:0"))
+    assert rc == _lib.TCA_ERR_INVALID and "bad cap" in _lib.last_error()
+
+
 PLAN = """tca-plan 1
 program p
 dim M 0
@@ -151,7 +158,8 @@ def test_program_launch_without_module_is_refused():
 EXPECTED_FAMILIES = {
     "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"],
     "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"], "gemm_bf16": ["gemm"],
-    "copy_f32": ["elementwise"],
+    "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"], "softmax_dyn": ["stream"],
+    "layernorm_dyn": ["stream"],
 }
 
 

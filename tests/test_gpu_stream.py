@@ -1,0 +1,86 @@
+"""The streaming row family (row length a run-time dim) against the CPU
+oracle. Same tolerances as test_gpu_configs.py: max bit-identical, sums
+within 1e-5*sqrt(K)*||terms||_2, softmax/layernorm relative 1e-5*sqrt(K).
+Row lengths cover: empty rows (the output is init), odd lengths (the
+one-element-per-load path), short rows packed many to a wave, and rows long
+enough for 128 and 256 lanes (the cross-wave LDS meeting)."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import assert_reduce_close, canaries, compiled, host, out_dev, reduce_tol, run, to_dev
+from tcacomp_amd import inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("C", [0, 1, 3, 7, 64, 1000, 4096, 4099, 8192, 50000])
+@pytest.mark.parametrize("R", [1, 7, 300])
+def test_stream_row_sum_max(gpu, R, C):
+    _say("stream C2", R, C)
+    x = inputs.normal((R, C), 1.0, 0)
+    ws, wm = oracle.row_sum_max(x)
+    s, m = out_dev((R,), gpu), out_dev((R,), gpu)
+    run(compiled("row_sum_max_dyn"), [to_dev(x, gpu), s, m])
+    gs, gm = host(s), host(m)
+    assert canaries(gs) == 0 and canaries(gm) == 0
+    assert np.array_equal(gm.view(np.uint32), wm.view(np.uint32)), "row max is not bit-identical"
+    if C == 0:
+        assert np.all(gs == 0.0) and np.all(np.isneginf(gm))  # empty rows: the inits
+    assert_reduce_close(gs, ws, np.sqrt((x.astype(np.float64) ** 2).sum(1)), C, "stream row sum")
+
+
+def test_stream_matches_register_family(gpu):
+    R, C = 64, 8192
+    x = inputs.normal((R, C), 1.0, 3)
+    outs = []
+    for name in ("row_sum_max_dyn", "row_sum_max_8192"):
+        s, m = out_dev((R,), gpu), out_dev((R,), gpu)
+        run(compiled(name), [to_dev(x, gpu), s, m])
+        outs.append((host(s), host(m)))
+    assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))
+    assert_reduce_close(outs[0][0], outs[1][0].astype(np.float32),
+                        2 * np.sqrt((x.astype(np.float64) ** 2).sum(1)), C, "stream vs row")
+
+
+@pytest.mark.parametrize("C", [1, 5, 200, 4096, 20000])
+@pytest.mark.parametrize("R", [1, 37])
+def test_stream_softmax(gpu, R, C):
+    _say("stream C3", R, C)
+    x = inputs.normal((R, C), 2.0, 0)
+    want = oracle.softmax(x)
+    y = out_dev((R, C), gpu)
+    run(compiled("softmax_dyn"), [to_dev(x, gpu), y])
+    got = host(y)
+    assert canaries(got) == 0
+    rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want.astype(np.float64)), 1e-30)
+    assert rel.max() <= reduce_tol(C), "softmax relative error %g" % rel.max()
+    assert np.abs(got.astype(np.float64).sum(1) - 1.0).max() <= reduce_tol(C)
+
+
+@pytest.mark.parametrize("C", [3, 96, 1024, 5000])
+@pytest.mark.parametrize("R", [1, 37])
+def test_stream_layernorm(gpu, R, C):
+    _say("stream C4", R, C)
+    x = inputs.normal((R, C), 1.0, 0)
+    g, b = inputs.uniform((C,), 0.5, 1.5, 1), inputs.uniform((C,), -0.1, 0.1, 2)
+    inv_n, eps = float(np.float32(1.0 / C)), 1e-5
+    want = oracle.layernorm(x, g, b, inv_n, eps)
+    y = out_dev((R, C), gpu)
+    run(compiled("layernorm_dyn"), [to_dev(x, gpu), to_dev(g, gpu), to_dev(b, gpu), y], scalars=[inv_n, eps])
+    got = host(y)
+    assert canaries(got) == 0
+    err = np.abs(got.astype(np.float64) - want)
+    assert err.max() <= reduce_tol(C) * (np.abs(want).max() + 1.0), "layernorm err %g" % err.max()
+
+
+def test_stream_empty_grid(gpu):
+    s, m = out_dev((0,), gpu), out_dev((0,), gpu)
+    run(compiled("row_sum_max_dyn"), [to_dev(np.zeros((0, 5), np.float32), gpu), s, m])  # no workgroups launched
