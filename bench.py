@@ -253,7 +253,7 @@ def main():
     for key in keys:
         prog, sets, scalars, work, cpu = _setup(key, dev)
         ms, wall_ms = _time(prog, sets, scalars, args.steps, args.warmup, args.settle_ms)
-        sym = prog.kernel_symbols()[0]
+        sym = prog.selected_symbols(sets[0])[0]
         entry = {"config": CONFIGS[key][1], "kernel": sym, "family": prog.families()[0], "ms": ms,
                  "host_wall_ms": wall_ms}
         if work["bound"] == "hbm":

@@ -94,6 +94,17 @@ class CompiledProgram:
         fd = (ctypes.c_uint32 * max(1, len(free_dims)))(*free_dims)
         return _lib.lib().tca_program_check(self.parsed(), arr, len(tensors), fd, len(free_dims))
 
+    def selected_symbols(self, tensors, free_dims=()):
+        """The kernels a launch with these tensors runs (launch guards
+        applied), in launch order."""
+        syms = self.kernel_symbols()
+        arr = _descriptors(tensors)
+        fd = (ctypes.c_uint32 * max(1, len(free_dims)))(*free_dims)
+        out = (ctypes.c_uint8 * max(1, len(syms)))()
+        _lib.check(_lib.lib().tca_program_selected(self.parsed(), arr, len(tensors), fd, len(free_dims), out,
+                                                   None, len(syms)))
+        return [s for s, f in zip(syms, out) if f]
+
     # -- GPU
     def load(self):
         if self._h is None:

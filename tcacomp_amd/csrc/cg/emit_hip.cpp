@@ -499,6 +499,7 @@ class Emitter {
     uint32_t block = 256, lds = 0;
     std::vector<std::string> grid;
     std::vector<std::string> args;
+    std::vector<std::string> when;  // launch guards: "<dim> <lo> <hi> <mod> <rem>"
   };
 
   // -------------------------------------------------------------- analysis
@@ -1160,17 +1161,33 @@ class Emitter {
   }
 
   // S: the row nests of family R with a row length known only at run time
-  // (or too long for registers). Every chain of the nest streams the row in
-  // 16-byte vectors (4 elements when the length allows it, else 1); S lanes
-  // share a row, S chosen at run time as the largest power of two <= 256
-  // that leaves every lane >= 8 vectors, so short rows pack many rows per
-  // wave and long ones spread over up to four waves. Each lane folds its
-  // strided share with a presence flag (lanes that saw nothing, and empty
-  // rows, contribute nothing; the output is then init), then the segment
-  // meets by shuffles and, past 64 lanes, through LDS. Row scalars produced
-  // in the nest stay in registers. Grid-stride over row groups, the grid
-  // capped at 2048 workgroups (8 per CU).
+  // (or too long for registers). The row is read in 16-byte vectors (4
+  // elements when the length allows it, 2 or 1 otherwise) by S lanes, S
+  // chosen at run time as the smallest power of two <= the block that
+  // leaves no lane more than 4 vectors, so short rows pack many rows per
+  // block and long ones spread over up to sixteen waves. Rows of <= 1024 x 4
+  // vectors are read from HBM once into a per-lane register cache of 4
+  // vectors (every later pass over the row reads registers; the small cache
+  // keeps occupancy at 8 waves per SIMD); longer rows are streamed, one pass
+  // per group of statements, 4 vectors in flight per lane, re-reads through
+  // the caches. Rows of <= 256 x 4 vectors run in 256-lane blocks (a
+  // cross-wave meeting stalls 4 waves, not 16), longer ones in 1024-lane
+  // blocks. Consecutive reductions that read none of each other's results
+  // share a pass. Lane l of a row holds vectors l, l + S, ...: NFULL of them,
+  // one more for l < REM. The loops run over the longest share (a count
+  // uniform over the block) with the vector index clamped into the row, so
+  // no load is under a lane mask; a lane folds or stores only its own
+  // vectors. Every lane of a non-empty row holds >= 1 vector (S <= vectors),
+  // so a lane's fold starts from its first element and the segment meets by
+  // shuffles and, past 64 lanes, through LDS; an empty row yields init. Row
+  // scalars produced in the nest stay in registers. Lanes past the last row
+  // read row 0 (in bounds) and store nothing. One block per row group: the
+  // plan's pack() grid term repeats the lane choice at launch (the loop
+  // over groups is grid-stride, so any grid is correct).
+  // One kernel per (vector width, small | large | streamed), chosen at
+  // launch by guards on the row length.
   bool EmitStream(int ni, std::string* err) {
+    constexpr uint32_t kBlock = 1024, kSmallBlock = 256, kCache = 4, kUnroll = 4;
     const Nest& n = an_.nests[ni];
     RowGeom geo = StreamCheck(g_, n.chains);
     if (!geo.ok) {
@@ -1179,8 +1196,6 @@ class Emitter {
     }
     PlanKernel pk;
     pk.symbol = Sym(g_, prefix_, ni);
-    pk.block = 256;
-    pk.grid.push_back(DimProduct(geo.outer) + "/1:2048");
     const std::string sig = Signature(n, &pk);
     std::ostringstream& o = src_;
     const std::string body_fn = pk.symbol + "_rows";
@@ -1188,23 +1203,62 @@ class Emitter {
     auto isReg = [&](int t) { return g_.tensors[t].local && an_.reg_nest[t] == ni; };
     std::set<int> produced;
     for (int ci : n.chains) produced.insert(g_.chains[ci].store_tensor);
+    // Passes over the row.
+    std::vector<std::vector<int>> passes;
+    {
+      std::set<int> outs;
+      for (int ci : n.chains) {
+        const ir::Chain& c = g_.chains[ci];
+        bool dep = false;
+        for (int t : ReadSet(c)) dep |= outs.count(t) > 0;
+        const bool red = !c.reduces.empty();
+        if (passes.empty() || !red || dep || g_.chains[passes.back()[0]].reduces.empty()) {
+          passes.push_back({ci});
+          outs.clear();
+        } else {
+          passes.back().push_back(ci);
+        }
+        outs.insert(c.store_tensor);
+      }
+    }
+    // Row tiles and column vectors per pass; the last pass reading each tile.
+    std::vector<std::vector<int>> passTiles(passes.size()), passCols(passes.size());
+    std::map<int, int> lastPass;
+    std::set<int> tiles;
+    for (size_t p = 0; p < passes.size(); ++p) {
+      std::set<int> seenT, seenC;
+      for (int ci : passes[p])
+        for (const auto& op : g_.chains[ci].root.ops) {
+          const OpKind k = Classify(op, geo);
+          if (k == OpKind::RowTile && seenT.insert(op.tensor).second) {
+            passTiles[p].push_back(op.tensor);
+            lastPass[op.tensor] = static_cast<int>(p);
+            tiles.insert(op.tensor);
+          } else if (k == OpKind::ColVec && seenC.insert(op.tensor).second) {
+            passCols[p].push_back(op.tensor);
+          }
+        }
+    }
 
     o << "// statements";
     for (int ci : n.chains) o << " #" << ci;
-    o << ": streaming row family; row @" << g_.dims[geo.col].name << " streamed, lanes/row chosen at run time\n";
-    o << "template <uint32_t V>\n__device__ __forceinline__ void " << body_fn << "(\n    " << sig << ") {\n";
+    o << ": streaming row family; row @" << g_.dims[geo.col].name
+      << " of run-time length, lanes/row chosen at run time; NV > 0: the row is cached in registers\n";
+    o << "template <uint32_t V, uint32_t NV, uint32_t BLOCK>\n__device__ __forceinline__ void " << body_fn << "(\n    "
+      << sig << ") {\n";
     o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
     o << "  const uint32_t VECS = C / V;\n";
-    o << "  uint32_t S = 1u;\n  while (S < 256u && S * 16u <= VECS) S <<= 1;\n";
-    o << "  const uint32_t RPB = 256u / S, SEG = S < 64u ? S : 64u, WPR = S > 64u ? S / 64u : 1u;\n";
+    o << "  uint32_t S = 1u;\n  while (S < BLOCK && S * " << kCache << "u < VECS) S <<= 1;\n";
+    o << "  const uint32_t RPB = BLOCK / S, SEG = S < 64u ? S : 64u, WPR = S > 64u ? S / 64u : 1u;\n";
+    o << "  const uint32_t NFULL = VECS / S, REM = VECS - NFULL * S;  // lane < REM holds NFULL + 1 vectors\n";
+    o << "  const uint32_t NLANE = NFULL + (REM > 0u ? 1u : 0u);\n";
     o << "  const uint32_t nrows = " << ProductExpr(geo.outer) << ";\n";
     o << "  const uint32_t ngroups = (nrows + RPB - 1u) / RPB;\n";
-    // LDS for the cross-wave meeting of each reduction (rows of 128/256 lanes).
     for (int ci : n.chains) {
       const ir::Chain& c = g_.chains[ci];
       if (c.reduces.empty()) continue;
       const std::string T = CType(g_.exprs[c.root.fn.body].type);
-      o << "  __shared__ " << T << " red" << ci << "[4];\n  __shared__ int redh" << ci << "[4];\n";
+      o << "  __shared__ " << T << " red" << ci << "[BLOCK / 64u];\n";
       o << "  const auto comb" << ci << " = [](" << T << " acc, " << T << " now) -> " << T << " {\n";
       ExprGen cg(g_, o, "    ", &counter_);
       cg.Bind(c.reduces[0].fn.params[0], "acc");
@@ -1236,8 +1290,8 @@ class Emitter {
         if (!loadedScalar.insert(op->tensor).second) continue;
         const std::string T = CType(g_.tensors[op->tensor].elem);
         const std::string var = "rs" + std::to_string(op->tensor);
-        o << "    const " << T << " " << var << " = active ? t" << op->tensor << "[" << Offset(op->tensor, op->axes, coord)
-          << "] : " << T << "(0);\n";
+        o << "    const " << T << " " << var << " = t" << op->tensor << "[" << Offset(op->tensor, op->axes, coord)
+          << "];\n";
         regScalar[op->tensor] = var;
       }
     }
@@ -1245,63 +1299,167 @@ class Emitter {
       auto it = regScalar.find(op.tensor);
       return it != regScalar.end() ? it->second : std::string("/*missing row scalar*/0");
     };
-    // Loads of the row-tile / column-vector operands of chain c at vector v.
-    auto loads = [&](const ir::Chain& c, const std::string& ind) {
-      std::set<int> done;
-      for (const auto& op : c.root.ops) {
-        const OpKind k = Classify(op, geo);
-        if ((k != OpKind::RowTile && k != OpKind::ColVec) || !done.insert(op.tensor).second) continue;
-        const std::string T = CType(g_.tensors[op.tensor].elem);
-        if (k == OpKind::RowTile)
-          o << ind << "const auto x" << op.tensor << " = tca::hip::load_vec_nt<" << T << ", V>(t" << op.tensor
-            << " + row_base + static_cast<uint64_t>(v) * V);\n";
-        else
-          o << ind << "const auto x" << op.tensor << " = tca::hip::load_vec<" << T << ", V>(t" << op.tensor
-            << " + static_cast<uint64_t>(v) * V);\n";
-      }
-    };
-    auto elemValue = [&](std::ostringstream& os, const std::string& ind, const ir::Chain& c) -> std::string {
+    // Register cache of the row tiles (NV > 0 only); tiles from memory are
+    // loaded up front, tiles produced in the nest as they are produced.
+    for (int t : tiles)
+      o << "    tca::hip::vec<" << CType(g_.tensors[t].elem) << ", V> xc" << t << "[NV > 0u ? NV : 1u];\n";
+    std::vector<int> fromMemory;
+    for (int t : tiles)
+      if (!produced.count(t)) fromMemory.push_back(t);
+    if (!fromMemory.empty()) {
+      o << "    if constexpr (NV > 0u) {\n#pragma unroll\n      for (uint32_t j = 0; j < NV; ++j) {\n";
+      o << "        if (j >= NLANE) break;\n";
+      o << "        const uint32_t v = min(lane + j * S, VECS - 1u);\n";
+      for (int t : fromMemory)
+        o << "        xc" << t << "[j] = tca::hip::load_vec_nt<" << CType(g_.tensors[t].elem) << ", V>(t" << t
+          << " + row_base + static_cast<uint64_t>(v) * V);\n";
+      o << "      }\n    }\n";
+    }
+    // Element value of chain c at element q of the vector whose operands are
+    // bound to x<t> (tiles and column vectors) at suffix `sfx`.
+    auto elemValue = [&](std::ostringstream& os, const std::string& ind, const ir::Chain& c,
+                         const std::string& sfx) -> std::string {
       ExprGen eg(g_, os, ind, &counter_);
       for (size_t k = 0; k < c.root.ops.size(); ++k) {
         const auto& op = c.root.ops[k];
         const OpKind kind = Classify(op, geo);
         eg.Bind(c.root.fn.params[k], (kind == OpKind::RowTile || kind == OpKind::ColVec)
-                                         ? "x" + std::to_string(op.tensor) + "[q]"
+                                         ? "x" + std::to_string(op.tensor) + sfx + "[q]"
                                          : rowScalar(op));
       }
       return eg.Gen(c.root.fn.body);
     };
-    for (int ci : n.chains) {
-      const ir::Chain& c = g_.chains[ci];
-      const int st = c.store_tensor;
-      if (!c.reduces.empty()) {
+    // Operand vectors of pass p at the (clamped) vector index variable `vc`,
+    // named x<t><sfx>: cached tiles alias the cache, others are loaded.
+    auto operands = [&](std::ostringstream& b, size_t p, const std::string& ind, bool cached, const std::string& vc,
+                        const std::string& sfx) {
+      for (int t : passTiles[p]) {
+        const std::string T = CType(g_.tensors[t].elem);
+        if (cached) {
+          b << ind << "const auto& x" << t << sfx << " = xc" << t << "[j];\n";
+        } else {
+          // Re-read by a later pass: let the caches keep it.
+          const bool again = lastPass[t] != static_cast<int>(p) || produced.count(t);
+          b << ind << "const auto x" << t << sfx << " = tca::hip::" << (again ? "load_vec" : "load_vec_nt") << "<"
+            << T << ", V>(t" << t << " + row_base + static_cast<uint64_t>(" << vc << ") * V);\n";
+        }
+      }
+      for (int t : passCols[p])
+        b << ind << "const auto x" << t << sfx << " = tca::hip::load_vec<" << CType(g_.tensors[t].elem) << ", V>(t"
+          << t << " + static_cast<uint64_t>(" << vc << ") * V);\n";
+    };
+    // Work of pass p on one vector (operands x<t><sfx>, index `vc`). `ok`: the
+    // vector is the lane's own (else the clamped index points elsewhere and
+    // nothing is folded or stored); "true" when known. `first`: the lane's
+    // first vector (the fold starts from its element 0).
+    auto work = [&](std::ostringstream& b, size_t p, const std::string& ind, bool cached, const std::string& vc,
+                    const std::string& ok, const std::string& sfx, bool first) {
+      const ir::Chain& c0 = g_.chains[passes[p][0]];
+      if (!c0.reduces.empty()) {
+        b << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) {\n";
+        for (int ci : passes[p]) {
+          const ir::Chain& c = g_.chains[ci];
+          const std::string P = "part" + std::to_string(ci);
+          std::ostringstream es;
+          const std::string ev = elemValue(es, ind + "  ", c, sfx);
+          b << es.str();
+          const std::string folded = "comb" + std::to_string(ci) + "(" + P + ", " + ev + ")";
+          if (first)
+            b << ind << "  " << P << " = q == 0u ? " << ev << " : " << folded << ";\n";
+          else if (ok == "true")
+            b << ind << "  " << P << " = " << folded << ";\n";
+          else
+            b << ind << "  " << P << " = " << ok << " ? " << folded << " : " << P << ";\n";
+        }
+        b << ind << "}\n";
+        return;
+      }
+      const int st = c0.store_tensor;
+      const std::string T = CType(g_.tensors[st].elem);
+      b << ind << "tca::hip::vec<" << T << ", V> outv" << sfx << ";\n";
+      b << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) {\n";
+      std::ostringstream es;
+      const std::string ev = elemValue(es, ind + "  ", c0, sfx);
+      b << es.str() << ind << "  outv" << sfx << "[q] = " << ev << ";\n" << ind << "}\n";
+      if (!isReg(st) || an_.hbm_local[st]) {
+        const bool again = tiles.count(st) > 0 && !cached;
+        b << ind << "if (active" << (ok == "true" ? std::string() : " && " + ok) << ") tca::hip::"
+          << (again ? "store_vec" : "store_vec_nt") << "<" << T << ", V>(t" << st
+          << " + row_base + static_cast<uint64_t>(" << vc << ") * V, outv" << sfx << ");\n";
+      }
+      if (cached && tiles.count(st)) b << ind << "xc" << st << "[j] = outv" << sfx << ";\n";
+    };
+    // Vector k of the lane: index, ownership, clamped index.
+    auto index = [&](std::ostringstream& b, const std::string& ind, const std::string& k, const std::string& sfx) {
+      b << ind << "const uint32_t v" << sfx << " = lane + (" << k << ") * S;\n";
+      b << ind << "const bool ok" << sfx << " = v" << sfx << " < VECS;\n";
+      b << ind << "const uint32_t vc" << sfx << " = ok" << sfx << " ? v" << sfx << " : VECS - 1u;\n";
+    };
+    for (size_t p = 0; p < passes.size(); ++p) {
+      const ir::Chain& c0 = g_.chains[passes[p][0]];
+      const bool red = !c0.reduces.empty();
+      o << "    // statement";
+      for (int ci : passes[p]) o << " #" << ci;
+      if (red) {
+        o << ": reduce over @" << g_.dims[geo.col].name << " into";
+        for (int ci : passes[p]) o << " " << g_.tensors[g_.chains[ci].store_tensor].name;
+      } else {
+        o << ": elementwise over the row into " << g_.tensors[c0.store_tensor].name;
+      }
+      o << "\n";
+      if (red)
+        for (int ci : passes[p]) {
+          const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+          o << "    " << T << " part" << ci << " = " << T << "(0);\n";
+        }
+      std::ostringstream b;
+      // Cached: vector j of the cache; j == 0 is always the lane's own.
+      b << "    if constexpr (NV > 0u) {\n#pragma unroll\n      for (uint32_t j = 0; j < NV; ++j) {\n";
+      b << "        if (j >= NLANE) break;\n";
+      index(b, "        ", "j", "");
+      operands(b, p, "        ", true, "vc", "");
+      b << "        if (j == 0u) {\n";
+      work(b, p, "          ", true, "vc", "true", "", red);
+      b << "        } else {\n";
+      work(b, p, "          ", true, "vc", "ok", "", false);
+      b << "        }\n      }\n";
+      // Streamed: the lane's first vector, then kUnroll in flight, then the rest.
+      b << "    } else if (NLANE > 0u) {\n      {\n";
+      b << "        const uint32_t vc = lane;\n";
+      operands(b, p, "        ", false, "vc", "");
+      work(b, p, "        ", false, "vc", "true", "", red);
+      b << "      }\n      uint32_t k = 1u;\n";
+      b << "      for (; k + " << kUnroll - 1 << "u < NLANE; k += " << kUnroll << "u) {\n";
+      for (uint32_t u = 0; u < kUnroll; ++u)
+        index(b, "        ", "k + " + std::to_string(u) + "u", "_" + std::to_string(u));
+      for (uint32_t u = 0; u < kUnroll; ++u)
+        operands(b, p, "        ", false, "vc_" + std::to_string(u), "_" + std::to_string(u));
+      for (uint32_t u = 0; u < kUnroll; ++u)
+        work(b, p, "        ", false, "vc_" + std::to_string(u), "ok_" + std::to_string(u), "_" + std::to_string(u),
+             false);
+      b << "      }\n      for (; k < NLANE; ++k) {\n";
+      index(b, "        ", "k", "");
+      operands(b, p, "        ", false, "vc", "");
+      work(b, p, "        ", false, "vc", "ok", "", false);
+      b << "      }\n    }\n";
+      o << b.str();
+      if (!red) continue;
+      for (int ci : passes[p])
+        o << "    part" << ci << " = tca::hip::seg_allreduce_rt(part" << ci << ", SEG, comb" << ci << ");\n";
+      o << "    if (WPR > 1u) {\n      if ((threadIdx.x & 63u) == 0u) {\n";
+      for (int ci : passes[p]) o << "        red" << ci << "[threadIdx.x >> 6] = part" << ci << ";\n";
+      o << "      }\n      __syncthreads();\n      const uint32_t w0 = (threadIdx.x / S) * WPR;\n";
+      for (int ci : passes[p]) {
+        o << "      part" << ci << " = red" << ci << "[w0];\n";
+        o << "      for (uint32_t w = 1; w < WPR; ++w) part" << ci << " = comb" << ci << "(part" << ci << ", red" << ci
+          << "[w0 + w]);\n";
+      }
+      o << "      __syncthreads();\n    }\n";
+      // init once per output (an empty row yields init), then the piped map.
+      for (int ci : passes[p]) {
+        const ir::Chain& c = g_.chains[ci];
+        const int st = c.store_tensor;
         const std::string T = CType(g_.exprs[c.root.fn.body].type);
-        const std::string P = "part" + std::to_string(ci), H = "has" + std::to_string(ci);
-        o << "    // statement #" << ci << ": reduce over @" << g_.dims[geo.col].name << " into " << g_.tensors[st].name
-          << "\n";
-        o << "    " << T << " " << P << " = " << T << "(0);\n    bool " << H << " = false;\n";
-        o << "    if (active) {\n      for (uint32_t v = lane; v < VECS; v += S) {\n";
-        loads(c, "        ");
-        o << "#pragma unroll\n        for (uint32_t q = 0; q < V; ++q) {\n";
-        std::ostringstream bs;
-        const std::string ev = elemValue(bs, "          ", c);
-        o << bs.str();
-        o << "          " << P << " = " << H << " ? comb" << ci << "(" << P << ", " << ev << ") : " << ev << ";\n";
-        o << "          " << H << " = true;\n        }\n      }\n    }\n";
-        o << "    " << P << " = tca::hip::seg_allreduce_rt(" << P << ", " << H << ", SEG, comb" << ci << ");\n";
-        o << "    if (WPR > 1u) {\n";
-        o << "      if ((threadIdx.x & 63u) == 0u) { red" << ci << "[threadIdx.x >> 6] = " << P << "; redh" << ci
-          << "[threadIdx.x >> 6] = " << H << " ? 1 : 0; }\n";
-        o << "      __syncthreads();\n";
-        o << "      const uint32_t w0 = (threadIdx.x / S) * WPR;\n";
-        o << "      " << P << " = " << T << "(0);\n      " << H << " = false;\n";
-        o << "      for (uint32_t w = 0; w < WPR; ++w) {\n";
-        o << "        if (redh" << ci << "[w0 + w] == 0) continue;\n";
-        o << "        " << P << " = " << H << " ? comb" << ci << "(" << P << ", red" << ci << "[w0 + w]) : red" << ci
-          << "[w0 + w];\n";
-        o << "        " << H << " = true;\n      }\n";
-        o << "      __syncthreads();\n    }\n";
-        // init once per output (an empty row yields init), then the piped map.
         const ir::ReduceStage& r = c.reduces[0];
         std::string init;
         {
@@ -1313,10 +1471,10 @@ class Emitter {
           std::ostringstream fs;
           ExprGen fg(g_, fs, "      ", &counter_);
           fg.Bind(r.fn.params[0], init);
-          fg.Bind(r.fn.params[1], P);
+          fg.Bind(r.fn.params[1], "part" + std::to_string(ci));
           val = fg.Gen(r.fn.body);
           o << "    " << T << " fin" << ci << " = " << init << ";\n";
-          o << "    if (" << H << ") {\n" << fs.str() << "      fin" << ci << " = " << val << ";\n    }\n";
+          o << "    if (VECS > 0u) {\n" << fs.str() << "      fin" << ci << " = " << val << ";\n    }\n";
           val = "fin" + std::to_string(ci);
         }
         if (c.has_piped) {
@@ -1330,27 +1488,42 @@ class Emitter {
         o << "    const " << ST << " " << var << " = " << val << ";\n";
         regScalar[st] = var;
         if (!isReg(st) || an_.hbm_local[st])
-          o << "    if (active && lane == 0u) t" << st << "[" << Offset(st, c.store_axes, coord) << "] = " << var << ";\n";
-      } else {
-        const std::string T = CType(g_.tensors[st].elem);
-        o << "    // statement #" << ci << ": elementwise over the row into " << g_.tensors[st].name << "\n";
-        o << "    if (active) {\n      for (uint32_t v = lane; v < VECS; v += S) {\n";
-        loads(c, "        ");
-        o << "        tca::hip::vec<" << T << ", V> outv;\n";
-        o << "#pragma unroll\n        for (uint32_t q = 0; q < V; ++q) {\n";
-        std::ostringstream bs;
-        const std::string val = elemValue(bs, "          ", c);
-        o << bs.str();
-        o << "          outv[q] = " << val << ";\n        }\n";
-        o << "        tca::hip::store_vec_nt<" << T << ", V>(t" << st << " + row_base + static_cast<uint64_t>(v) * V, outv);\n";
-        o << "      }\n    }\n";
+          o << "    if (active && lane == 0u) t" << st << "[" << Offset(st, c.store_axes, coord) << "] = " << var
+            << ";\n";
       }
     }
     o << "  }\n}\n";
-    o << "extern \"C\" __global__ void __launch_bounds__(256) " << pk.symbol << "(\n    " << sig << ") {\n";
-    o << "  if ((" << ExtentExpr(g_, geo.col) << ") % 4u == 0u) " << body_fn << "<4u>(" << CallArgs(n) << ");\n";
-    o << "  else " << body_fn << "<1u>(" << CallArgs(n) << ");\n}\n\n";
-    AddKernel(pk, Family::Stream, n.chains, "row=runtime lanes/row=runtime(<=256) vec=4|1 grid-stride<=2048");
+    // One kernel per (vector width, small | large | streamed); launch guards
+    // on the row length pick exactly one (C % 4 == 0: V 4; C % 4 == 2: V 2;
+    // odd: V 1; then the row length in vectors).
+    const std::string args = CallArgs(n);
+    const std::string cdim = g_.dims[geo.col].name;
+    const struct { uint32_t v, mod, rem; } widths[] = {{4, 4, 0}, {2, 4, 2}, {1, 2, 1}};
+    const struct { const char* tag; uint32_t block, nv; uint64_t lo_vecs, hi_vecs; } kinds[] = {
+        {"c", kSmallBlock, kCache, 0, uint64_t{kSmallBlock} * kCache},
+        {"l", kBlock, kCache, uint64_t{kSmallBlock} * kCache + 1, uint64_t{kBlock} * kCache},
+        {"s", kBlock, 0, uint64_t{kBlock} * kCache + 1, 0xffffffffull}};
+    const std::string symbol = pk.symbol;
+    for (const auto& w : widths) {
+      for (const auto& kd : kinds) {
+        const uint64_t lo = kd.lo_vecs * w.v, hi = std::min<uint64_t>(0xffffffffull, kd.hi_vecs * w.v);
+        PlanKernel vk = pk;
+        vk.symbol = symbol + "_" + kd.tag + std::to_string(w.v);
+        vk.block = kd.block;
+        vk.grid.push_back(DimProduct(geo.outer) + "/pack(" + cdim + "," + std::to_string(kCache * w.v) + "," +
+                          std::to_string(kd.block) + ")");
+        vk.when.push_back(cdim + " " + std::to_string(lo) + " " + std::to_string(hi) + " " + std::to_string(w.mod) +
+                          " " + std::to_string(w.rem));
+        o << "extern \"C\" __global__ void __launch_bounds__(" << kd.block << ") " << vk.symbol << "(\n    " << sig
+          << ") {\n  " << body_fn << "<" << w.v << "u, " << kd.nv << "u, " << kd.block << "u>(" << args << ");\n}\n";
+        std::ostringstream det;
+        det << "row=runtime (" << cdim << " % " << w.mod << " == " << w.rem << ", " << lo << ".." << hi << ": "
+            << (kd.nv ? "cached " + std::to_string(kd.nv) + " vectors/lane" : std::string("streamed")) << ") vec=" << w.v
+            << " lanes/row=runtime(<=" << kd.block << ") passes=" << passes.size() << " block=" << kd.block;
+        AddKernel(vk, Family::Stream, n.chains, det.str());
+      }
+    }
+    o << "\n";
     return true;
   }
 
@@ -1405,6 +1578,7 @@ class Emitter {
       for (const auto& t : k.grid) p << " " << t;
       p << "\n";
       for (const auto& a : k.args) p << "arg " << a << "\n";
+      for (const auto& w : k.when) p << "when " << w << "\n";
     }
     p << "end\n";
     return p.str();

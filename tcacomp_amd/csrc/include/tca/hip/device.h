@@ -48,6 +48,11 @@ __device__ __forceinline__ vec<T, N> load_vec_nt(const T* __restrict__ p) {
   }
 }
 
+template <typename T, int N>
+__device__ __forceinline__ void store_vec(T* __restrict__ p, const vec<T, N>& x) {
+  *reinterpret_cast<vec<T, N>*>(p) = x;
+}
+
 // Streaming store: the output is not re-read by this kernel, so keep it out
 // of the caches' way.
 template <typename T, int N>
@@ -74,16 +79,21 @@ __device__ __forceinline__ void store_nt(T* __restrict__ p, T x) {
 
 // ---- 32-bit lane moves -------------------------------------------------
 
+// The bits of a lane value of 1, 2 or 4 bytes, widened to one 32-bit lane
+// register (and back). Half-precision values move as their bit patterns.
 template <typename T>
 __device__ __forceinline__ int to_bits(T v) {
+  static_assert(sizeof(T) == 1 || sizeof(T) == 2 || sizeof(T) == 4, "lane values are at most 32 bits");
   if constexpr (sizeof(T) == 4) return __builtin_bit_cast(int, v);
-  else return static_cast<int>(v);
+  else if constexpr (sizeof(T) == 2) return static_cast<int>(__builtin_bit_cast(uint16_t, v));
+  else return static_cast<int>(__builtin_bit_cast(uint8_t, v));
 }
 
 template <typename T>
 __device__ __forceinline__ T from_bits(int b) {
   if constexpr (sizeof(T) == 4) return __builtin_bit_cast(T, b);
-  else return static_cast<T>(b);
+  else if constexpr (sizeof(T) == 2) return __builtin_bit_cast(T, static_cast<uint16_t>(b));
+  else return __builtin_bit_cast(T, static_cast<uint8_t>(b));
 }
 
 // DPP move within a 16-lane row. Controls used (CDNA3/4 ISA, DPP_CTRL):
@@ -128,22 +138,20 @@ __device__ __forceinline__ T seg_allreduce(T v, Op op) {
   return v;
 }
 
-// All-reduce over aligned segments of `seg` lanes, a power of two <= 64 known
-// only at run time, of values that may be absent (`has` false: the lane saw
-// no element). Absent values are skipped; every lane of a segment ends with
-// the segment's total and the OR of the flags. Every lane of the wave must
-// call it (the shuffles are wave-wide). `op` must be associative and
-// commutative.
+// All-reduce over aligned segments of `seg` lanes, `seg` a power of two
+// <= 64 known only at run time (uniform over the wave). Every lane of the
+// wave must call it; `op` must be associative and commutative.
 template <typename T, typename Op>
-__device__ __forceinline__ T seg_allreduce_rt(T v, bool& has, uint32_t seg, Op op) {
-  for (uint32_t off = 1; off < seg; off <<= 1) {
-    const T o = xor_lanes(v, static_cast<int>(off));
-    const bool oh = __shfl_xor(static_cast<int>(has), static_cast<int>(off), 64) != 0;
-    if (has && oh) v = op(v, o);
-    else if (oh) v = o;
-    has = has || oh;
+__device__ __forceinline__ T seg_allreduce_rt(T v, uint32_t seg, Op op) {
+  switch (seg) {
+    case 64: return seg_allreduce<64>(v, op);
+    case 32: return seg_allreduce<32>(v, op);
+    case 16: return seg_allreduce<16>(v, op);
+    case 8: return seg_allreduce<8>(v, op);
+    case 4: return seg_allreduce<4>(v, op);
+    case 2: return seg_allreduce<2>(v, op);
+    default: return v;
   }
-  return v;
 }
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }

@@ -52,8 +52,28 @@ bool ParseTerm(const Plan& p, const std::string& s, Term* t, std::string* err) {
     *err = "grid term '" + s + "' has a bad cap";
     return false;
   }
-  if (!ParseU64(s.substr(slash + 1, colon == std::string::npos ? std::string::npos : colon - slash - 1), &t->divisor) ||
-      t->divisor == 0) {
+  const std::string div = s.substr(slash + 1, colon == std::string::npos ? std::string::npos : colon - slash - 1);
+  if (div.compare(0, 5, "pack(") == 0 && div.back() == ')') {
+    // pack(<dim>,<elements per lane>,<block>): rows per block of the packed
+    // row families, a function of the row length.
+    const std::string in = div.substr(5, div.size() - 6);
+    const size_t c1 = in.find(','), c2 = c1 == std::string::npos ? c1 : in.find(',', c1 + 1);
+    if (c2 == std::string::npos || in.find(',', c2 + 1) != std::string::npos) {
+      *err = "grid term '" + s + "': pack(<dim>,<elements per lane>,<block>)";
+      return false;
+    }
+    t->pack_dim = FindDim(p, in.substr(0, c1));
+    if (t->pack_dim < 0) {
+      *err = "grid term '" + s + "' packs by an unknown dim";
+      return false;
+    }
+    if (!ParseU64(in.substr(c1 + 1, c2 - c1 - 1), &t->pack_epl) || t->pack_epl == 0 ||
+        !ParseU64(in.substr(c2 + 1), &t->pack_block) || t->pack_block == 0 ||
+        (t->pack_block & (t->pack_block - 1)) != 0) {
+      *err = "grid term '" + s + "' has a bad pack";
+      return false;
+    }
+  } else if (!ParseU64(div, &t->divisor) || t->divisor == 0) {
     *err = "grid term '" + s + "' has a bad divisor";
     return false;
   }
@@ -210,6 +230,16 @@ bool Parse(const std::string& text, Plan* out, std::string* err) {
       }
       if (a.index < 0) return bad("arg names unknown " + tok[1] + " " + tok[2]);
       p.kernels.back().args.push_back(a);
+    } else if (kw == "when") {
+      if (p.kernels.empty()) return bad("when before any kernel");
+      Guard g;
+      if (tok.size() != 6 || !ParseU64(tok[2], &g.lo) || !ParseU64(tok[3], &g.hi) || !ParseU64(tok[4], &g.mod) ||
+          !ParseU64(tok[5], &g.rem))
+        return bad("when <dim> <lo> <hi> <mod> <rem>");
+      g.dim = FindDim(p, tok[1]);
+      if (g.dim < 0) return bad("when names unknown dim " + tok[1]);
+      if (g.mod == 0 || g.rem >= g.mod || g.lo > g.hi) return bad("bad guard on " + tok[1]);
+      p.kernels.back().when.push_back(g);
     } else if (kw == "end") {
       ended = true;
     } else {
@@ -248,7 +278,8 @@ std::string Serialize(const Plan& p) {
         o << p.dims[d].name;
         first = false;
       }
-      o << "/" << t.divisor;
+      if (t.pack_dim >= 0) o << "/pack(" << p.dims[t.pack_dim].name << "," << t.pack_epl << "," << t.pack_block << ")";
+      else o << "/" << t.divisor;
       if (t.cap != 0) o << ":" << t.cap;
     }
     o << "\n";
@@ -257,6 +288,8 @@ std::string Serialize(const Plan& p) {
       else if (a.kind == ArgKind::Dim) o << "arg dim " << p.dims[a.index].name << "\n";
       else o << "arg scalar " << p.scalars[a.index].name << "\n";
     }
+    for (const auto& g : k.when)
+      o << "when " << p.dims[g.dim].name << " " << g.lo << " " << g.hi << " " << g.mod << " " << g.rem << "\n";
   }
   o << "end\n";
   return o.str();
@@ -367,7 +400,15 @@ bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims,
         return false;
       }
     }
-    uint64_t q = (prod + t.divisor - 1) / t.divisor;
+    uint64_t div = t.divisor;
+    if (t.pack_dim >= 0) {
+      // The kernel's own choice: S lanes per row, the smallest power of two
+      // <= block with S * epl >= the row length; block / S rows per block.
+      uint64_t lanes = 1;
+      while (lanes < t.pack_block && lanes * t.pack_epl < dims[t.pack_dim]) lanes <<= 1;
+      div = t.pack_block / lanes;
+    }
+    uint64_t q = (prod + div - 1) / div;
     if (t.cap != 0 && q > t.cap) q = t.cap;
     g *= q;
     if (g > (1ull << 62)) {
@@ -376,6 +417,14 @@ bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims,
     }
   }
   *grid = g;
+  return true;
+}
+
+bool Selected(const Kernel& k, const std::vector<uint32_t>& dims) {
+  for (const auto& g : k.when) {
+    const uint64_t v = dims[g.dim];
+    if (v < g.lo || v > g.hi || v % g.mod != g.rem) return false;
+  }
   return true;
 }
 

@@ -10,8 +10,16 @@
 //   kernel <symbol> <block> <lds-bytes> <n-terms> <term>...
 //       term = <factor>[*<factor>...]/<divisor>[:<cap>], factor = dim name or
 //       integer; grid = product over terms of ceil(product(factors) / divisor),
-//       each term limited to <cap> when one is given (grid-stride kernels)
+//       each term limited to <cap> when one is given (grid-stride kernels).
+//       divisor = integer | pack(<dim>,<epl>,<block>): rows per block of a
+//       packed row kernel, block / S with S the smallest power of two <= block
+//       such that S * epl >= dim (S lanes share a row of `dim` elements, each
+//       lane at most epl of them).
 //   arg ptr <tensor> | arg dim <name> | arg scalar <name>    (for the last kernel)
+//   when <dim> <lo> <hi> <mod> <rem>    (for the last kernel) the kernel runs only
+//       when lo <= dim <= hi and dim % mod == rem; every guard of a kernel must
+//       hold. Variants of one nest specialised on a run-time dim carry guards
+//       that partition its values, so exactly one of them launches.
 //   end
 //
 // The shape contract Bind() enforces is the reference launcher's
@@ -57,11 +65,18 @@ struct Term {
   uint64_t const_factor = 1;
   uint64_t divisor = 1;
   uint64_t cap = 0;  // 0 = none
+  int pack_dim = -1;  // >= 0: the divisor is pack(dim, pack_epl, pack_block)
+  uint64_t pack_epl = 0, pack_block = 0;
 };
 
 struct Arg {
   ArgKind kind = ArgKind::Ptr;
   int index = 0;  // tensor, dim or scalar index
+};
+
+struct Guard {
+  int dim = 0;  // index into Plan::dims
+  uint64_t lo = 0, hi = 0xffffffffull, mod = 1, rem = 0;
 };
 
 struct Kernel {
@@ -70,6 +85,7 @@ struct Kernel {
   uint32_t lds = 0;
   std::vector<Term> grid;
   std::vector<Arg> args;
+  std::vector<Guard> when;
 };
 
 struct Plan {
@@ -98,6 +114,8 @@ int Bind(const Plan& p, const tca_tensor* tensors, uint32_t n_tensors, const uin
 
 size_t TensorBytes(const Plan& p, size_t tensor, const std::vector<uint32_t>& dims);
 bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims, uint64_t* grid, std::string* err);
+// Whether every guard of k holds for the bound dims.
+bool Selected(const Kernel& k, const std::vector<uint32_t>& dims);
 // Packs the kernel arguments per the HIP kernarg ABI (natural alignment):
 // pointers 8 bytes, dims u32, scalars 4 bytes (f32 for float types, i32/u32
 // for integers, i32 for bool).

@@ -360,6 +360,27 @@ int tca_program_check(tca_program p, const tca_tensor* tensors, uint32_t n_tenso
   return TCA_OK;
 }
 
+int tca_program_selected(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
+                         uint32_t n_free_dims, uint8_t* selected, uint64_t* grids, uint32_t n_selected) {
+  if (p == nullptr) return fail(TCA_ERR_INVALID, "program_selected: null program");
+  if (n_selected != p->plan.kernels.size())
+    return fail(TCA_ERR_INVALID, "program_selected: program has %zu kernel(s), got room for %u", p->plan.kernels.size(),
+                n_selected);
+  if (n_selected > 0 && selected == nullptr) return fail(TCA_ERR_INVALID, "program_selected: null output");
+  std::vector<uint32_t> dims;
+  std::string err;
+  int code = tca::plan::Bind(p->plan, tensors, n_tensors, free_dims, n_free_dims, &dims, &err);
+  if (code != TCA_OK) return fail(code, "%s", err.c_str());
+  for (uint32_t i = 0; i < n_selected; ++i) {
+    const auto& k = p->plan.kernels[i];
+    selected[i] = tca::plan::Selected(k, dims) ? 1 : 0;
+    if (grids == nullptr) continue;
+    grids[i] = 0;
+    if (selected[i] && !tca::plan::GridSize(k, p->plan, dims, &grids[i], &err)) return fail(TCA_ERR_LAUNCH, "%s", err.c_str());
+  }
+  return TCA_OK;
+}
+
 int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
                        uint32_t n_free_dims, const double* scalars, uint32_t n_scalars, tca_stream_t stream) {
   if (p == nullptr) return fail(TCA_ERR_INVALID, "program_launch: null program");
@@ -417,6 +438,7 @@ int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tens
   if (rc != TCA_OK) return rc;
   for (size_t ki = 0; ki < pl.kernels.size(); ++ki) {
     const auto& k = pl.kernels[ki];
+    if (!tca::plan::Selected(k, dims)) continue;  // a variant for other dims
     uint64_t grid = 0;
     if (!tca::plan::GridSize(k, pl, dims, &grid, &err)) return fail(TCA_ERR_LAUNCH, "%s", err.c_str());
     if (grid == 0) continue;  // nothing to compute (an empty output)

@@ -167,6 +167,9 @@ class EmitResult:
     def families(self):
         return [line.split()[1] for line in self.report.splitlines() if line.strip()]
 
+    def kernel_symbols(self):
+        return [line.split()[0] for line in self.report.splitlines() if line.strip()]
+
 
 class Builder:
     """The public builder root (pkg/builder.go:35-45)."""

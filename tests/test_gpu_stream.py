@@ -1,9 +1,12 @@
 """The streaming row family (row length a run-time dim) against the CPU
 oracle. Same tolerances as test_gpu_configs.py: max bit-identical, sums
 within 1e-5*sqrt(K)*||terms||_2, softmax/layernorm relative 1e-5*sqrt(K).
-Row lengths cover: empty rows (the output is init), odd lengths (the
-one-element-per-load path), short rows packed many to a wave, and rows long
-enough for 128 and 256 lanes (the cross-wave LDS meeting)."""
+Row lengths cover every variant the launch guards choose between (vector
+width 4 / 2 / 1 by C mod 4; register-cached in 256-lane blocks up to 1024
+vectors per row, in 1024-lane blocks up to 4096, streamed beyond), both
+sides of each boundary, empty rows (the output is
+init), short rows packed many to a wave, and rows long enough for the
+cross-wave LDS meeting (up to 16 waves per row)."""
 import sys
 
 import numpy as np
@@ -21,7 +24,8 @@ def _say(*a):
     sys.stdout.flush()
 
 
-@pytest.mark.parametrize("C", [0, 1, 3, 7, 64, 1000, 4096, 4099, 8192, 50000])
+@pytest.mark.parametrize("C", [0, 1, 3, 6, 7, 64, 1000, 1023, 1025, 2046, 2050, 4096, 4099, 4100, 8190, 8192,
+                               10002, 16384, 16388, 50000])
 @pytest.mark.parametrize("R", [1, 7, 300])
 def test_stream_row_sum_max(gpu, R, C):
     _say("stream C2", R, C)
@@ -50,7 +54,7 @@ def test_stream_matches_register_family(gpu):
                         2 * np.sqrt((x.astype(np.float64) ** 2).sum(1)), C, "stream vs row")
 
 
-@pytest.mark.parametrize("C", [1, 5, 200, 4096, 20000])
+@pytest.mark.parametrize("C", [1, 5, 200, 4096, 4098, 12002, 16384, 20000])
 @pytest.mark.parametrize("R", [1, 37])
 def test_stream_softmax(gpu, R, C):
     _say("stream C3", R, C)
@@ -65,7 +69,7 @@ def test_stream_softmax(gpu, R, C):
     assert np.abs(got.astype(np.float64).sum(1) - 1.0).max() <= reduce_tol(C)
 
 
-@pytest.mark.parametrize("C", [3, 96, 1024, 5000])
+@pytest.mark.parametrize("C", [3, 96, 1024, 4097, 5000, 8194, 16384, 20000])
 @pytest.mark.parametrize("R", [1, 37])
 def test_stream_layernorm(gpu, R, C):
     _say("stream C4", R, C)
