@@ -135,13 +135,14 @@ int tca_program_check(tca_program p, const tca_tensor* tensors, uint32_t n_tenso
 /* Which kernels a launch with these tensors would run: selected[i] = 1 when
  * every launch guard of kernel i holds for the bound dims (a program may
  * carry variants of one kernel specialised on a run-time dim; their guards
- * pick one), and, when `grids` is not NULL, the grid each selected kernel
- * would launch with (0 for the others). Host-only. No counterpart in the
+ * pick one), and, when `grids` / `blocks` are not NULL, the grid and block
+ * each selected kernel would launch with (0 for the others; packed row
+ * kernels size their block at launch). Host-only. No counterpart in the
  * reference (its launcher has a single kernel per DSL kernel); for tests and
  * profilers. */
 int tca_program_selected(tca_program p, const tca_tensor* tensors, uint32_t n_tensors,
                          const uint32_t* free_dims, uint32_t n_free_dims, uint8_t* selected,
-                         uint64_t* grids, uint32_t n_selected);
+                         uint64_t* grids, uint32_t* blocks, uint32_t n_selected);
 /* Checks the contract, then launches, in order on `stream`, every kernel of
  * the program whose launch guards hold. Scalars are passed as doubles in declaration order and converted
  * to their declared types. Locals that live in HBM use a workspace the

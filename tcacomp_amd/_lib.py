@@ -90,7 +90,7 @@ SIGNATURES = [
      [_P, _c.POINTER(tca_tensor), _U32, _c.POINTER(_U32), _U32]),
     ("tca_program_selected", _c.c_int,
      [_P, _c.POINTER(tca_tensor), _U32, _c.POINTER(_U32), _U32, _c.POINTER(_c.c_uint8),
-      _c.POINTER(_c.c_uint64), _U32]),
+      _c.POINTER(_c.c_uint64), _c.POINTER(_U32), _U32]),
     ("tca_program_launch", _c.c_int,
      [_P, _c.POINTER(tca_tensor), _U32, _c.POINTER(_U32), _U32, _c.POINTER(_c.c_double), _U32, _P]),
     ("tca_program_kernel_name", _STR, [_P, _U32]),

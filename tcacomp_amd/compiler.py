@@ -102,7 +102,7 @@ class CompiledProgram:
         fd = (ctypes.c_uint32 * max(1, len(free_dims)))(*free_dims)
         out = (ctypes.c_uint8 * max(1, len(syms)))()
         _lib.check(_lib.lib().tca_program_selected(self.parsed(), arr, len(tensors), fd, len(free_dims), out,
-                                                   None, len(syms)))
+                                                   None, None, len(syms)))
         return [s for s, f in zip(syms, out) if f]
 
     # -- GPU

@@ -500,6 +500,7 @@ class Emitter {
     std::vector<std::string> grid;
     std::vector<std::string> args;
     std::vector<std::string> when;  // launch guards: "<dim> <lo> <hi> <mod> <rem>"
+    std::string pack;               // packed row kernel: "<dim> <epl> <min block>"
   };
 
   // -------------------------------------------------------------- analysis
@@ -967,8 +968,11 @@ class Emitter {
     o << "  uint32_t rrem = active ? row : 0u;\n";
     for (int k = static_cast<int>(geo.outer.size()) - 1; k >= 0; --k) {
       int a = geo.outer[k];
-      o << "  const uint32_t c" << a << " = rrem % " << ExtentExpr(g_, a) << "; rrem /= " << ExtentExpr(g_, a)
-        << ";\n";
+      if (k == 0)  // the outermost coordinate is what remains (row < nrows)
+        o << "  const uint32_t c" << a << " = rrem;\n";
+      else
+        o << "  const uint32_t c" << a << " = rrem % " << ExtentExpr(g_, a) << "; rrem /= " << ExtentExpr(g_, a)
+          << ";\n";
     }
     auto coord = [&](int a) { return "c" + std::to_string(a); };
     // Which tensors are register locals of this nest. Anything a chain of the
@@ -1170,9 +1174,9 @@ class Emitter {
   // vectors (every later pass over the row reads registers; the small cache
   // keeps occupancy at 8 waves per SIMD); longer rows are streamed, one pass
   // per group of statements, 4 vectors in flight per lane, re-reads through
-  // the caches. Rows of <= 256 x 4 vectors run in 256-lane blocks (a
-  // cross-wave meeting stalls 4 waves, not 16), longer ones in 1024-lane
-  // blocks. Consecutive reductions that read none of each other's results
+  // the caches. The block is sized at launch (the plan's pack record):
+  // max(256, S) lanes, so a row of many waves has a block of its own and a
+  // cross-wave meeting stalls only that row's waves. Consecutive reductions that read none of each other's results
   // share a pass. Lane l of a row holds vectors l, l + S, ...: NFULL of them,
   // one more for l < REM. The loops run over the longest share (a count
   // uniform over the block) with the vector index clamped into the row, so
@@ -1182,12 +1186,11 @@ class Emitter {
   // shuffles and, past 64 lanes, through LDS; an empty row yields init. Row
   // scalars produced in the nest stay in registers. Lanes past the last row
   // read row 0 (in bounds) and store nothing. One block per row group: the
-  // plan's pack() grid term repeats the lane choice at launch (the loop
-  // over groups is grid-stride, so any grid is correct).
-  // One kernel per (vector width, small | large | streamed), chosen at
-  // launch by guards on the row length.
+  // pack record repeats the lane choice at launch (the loop over groups is
+  // grid-stride, so any grid is correct). One kernel per (vector width,
+  // cached | streamed), chosen at launch by guards on the row length.
   bool EmitStream(int ni, std::string* err) {
-    constexpr uint32_t kBlock = 1024, kSmallBlock = 256, kCache = 4, kUnroll = 4;
+    constexpr uint32_t kBlock = 1024, kMinBlock = 256, kCache = 4, kUnroll = 4;
     const Nest& n = an_.nests[ni];
     RowGeom geo = StreamCheck(g_, n.chains);
     if (!geo.ok) {
@@ -1244,21 +1247,31 @@ class Emitter {
     for (int ci : n.chains) o << " #" << ci;
     o << ": streaming row family; row @" << g_.dims[geo.col].name
       << " of run-time length, lanes/row chosen at run time; NV > 0: the row is cached in registers\n";
-    o << "template <uint32_t V, uint32_t NV, uint32_t BLOCK>\n__device__ __forceinline__ void " << body_fn << "(\n    "
+    // EX: every lane holds exactly NV vectors (the row is NV * S vectors):
+    // no loop exit, ownership test or index clamp.
+    o << "template <uint32_t V, uint32_t NV, bool EX>\n__device__ __forceinline__ void " << body_fn << "(\n    "
       << sig << ") {\n";
+    // Block and lane counts are powers of two: shifts, not divisions.
+    // The launch block is max(kMinBlock, S) (the plan's pack record): derived
+    // here from the row length rather than read from the dispatch packet.
+    const uint32_t lgBlock = 31 - __builtin_clz(kBlock), lgMin = 31 - __builtin_clz(kMinBlock);
     o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
     o << "  const uint32_t VECS = C / V;\n";
-    o << "  uint32_t S = 1u;\n  while (S < BLOCK && S * " << kCache << "u < VECS) S <<= 1;\n";
-    o << "  const uint32_t RPB = BLOCK / S, SEG = S < 64u ? S : 64u, WPR = S > 64u ? S / 64u : 1u;\n";
-    o << "  const uint32_t NFULL = VECS / S, REM = VECS - NFULL * S;  // lane < REM holds NFULL + 1 vectors\n";
+    o << "  const uint32_t LS = tca::hip::pack_lanes_log2(VECS, " << kCache << "u, " << lgBlock
+      << "u);  // S = 2^LS lanes per row\n";
+    o << "  const uint32_t LB = LS > " << lgMin << "u ? LS : " << lgMin << "u;  // the block: 2^LB = max(" << kMinBlock
+      << ", S) lanes\n";
+    o << "  const uint32_t S = 1u << LS, LR = LB - LS;  // 2^LR rows per block\n";
+    o << "  const uint32_t SEG = S < 64u ? S : 64u, WPR = S > 64u ? S >> 6 : 1u;\n";
+    o << "  const uint32_t NFULL = VECS >> LS, REM = VECS & (S - 1u);  // lane < REM holds NFULL + 1 vectors\n";
     o << "  const uint32_t NLANE = NFULL + (REM > 0u ? 1u : 0u);\n";
     o << "  const uint32_t nrows = " << ProductExpr(geo.outer) << ";\n";
-    o << "  const uint32_t ngroups = (nrows + RPB - 1u) / RPB;\n";
+    o << "  const uint32_t ngroups = static_cast<uint32_t>((static_cast<uint64_t>(nrows) + (1u << LR) - 1u) >> LR);\n";
     for (int ci : n.chains) {
       const ir::Chain& c = g_.chains[ci];
       if (c.reduces.empty()) continue;
       const std::string T = CType(g_.exprs[c.root.fn.body].type);
-      o << "  __shared__ " << T << " red" << ci << "[BLOCK / 64u];\n";
+      o << "  __shared__ " << T << " red" << ci << "[" << kBlock / 64 << "];\n";
       o << "  const auto comb" << ci << " = [](" << T << " acc, " << T << " now) -> " << T << " {\n";
       ExprGen cg(g_, o, "    ", &counter_);
       cg.Bind(c.reduces[0].fn.params[0], "acc");
@@ -1267,14 +1280,18 @@ class Emitter {
       o << "    return " << r << ";\n  };\n";
     }
     o << "  for (uint32_t grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {\n";
-    o << "    const uint32_t row = grp * RPB + threadIdx.x / S;\n";
-    o << "    const uint32_t lane = threadIdx.x % S;\n";
+    o << "    const uint32_t row = (grp << LR) + (threadIdx.x >> LS);\n";
+    o << "    const uint32_t lane = threadIdx.x & (S - 1u);\n";
     o << "    const bool active = row < nrows;\n";
     o << "    const uint64_t row_base = static_cast<uint64_t>(active ? row : 0u) * C;\n";
     o << "    uint32_t rrem = active ? row : 0u;\n";
     for (int k = static_cast<int>(geo.outer.size()) - 1; k >= 0; --k) {
       const int a = geo.outer[k];
-      o << "    const uint32_t c" << a << " = rrem % " << ExtentExpr(g_, a) << "; rrem /= " << ExtentExpr(g_, a) << ";\n";
+      if (k == 0)  // the outermost coordinate is what remains (row < nrows)
+        o << "    const uint32_t c" << a << " = rrem;\n";
+      else
+        o << "    const uint32_t c" << a << " = rrem % " << ExtentExpr(g_, a) << "; rrem /= " << ExtentExpr(g_, a)
+          << ";\n";
     }
     // Row scalars read from memory: once per row.
     std::map<int, std::string> regScalar;
@@ -1308,8 +1325,8 @@ class Emitter {
       if (!produced.count(t)) fromMemory.push_back(t);
     if (!fromMemory.empty()) {
       o << "    if constexpr (NV > 0u) {\n#pragma unroll\n      for (uint32_t j = 0; j < NV; ++j) {\n";
-      o << "        if (j >= NLANE) break;\n";
-      o << "        const uint32_t v = min(lane + j * S, VECS - 1u);\n";
+      o << "        if (!EX && j >= NLANE) break;\n";
+      o << "        const uint32_t v = EX ? lane + j * S : min(lane + j * S, VECS - 1u);\n";
       for (int t : fromMemory)
         o << "        xc" << t << "[j] = tca::hip::load_vec_nt<" << CType(g_.tensors[t].elem) << ", V>(t" << t
           << " + row_base + static_cast<uint64_t>(v) * V);\n";
@@ -1392,7 +1409,7 @@ class Emitter {
     // Vector k of the lane: index, ownership, clamped index.
     auto index = [&](std::ostringstream& b, const std::string& ind, const std::string& k, const std::string& sfx) {
       b << ind << "const uint32_t v" << sfx << " = lane + (" << k << ") * S;\n";
-      b << ind << "const bool ok" << sfx << " = v" << sfx << " < VECS;\n";
+      b << ind << "const bool ok" << sfx << " = EX || v" << sfx << " < VECS;\n";
       b << ind << "const uint32_t vc" << sfx << " = ok" << sfx << " ? v" << sfx << " : VECS - 1u;\n";
     };
     for (size_t p = 0; p < passes.size(); ++p) {
@@ -1415,7 +1432,7 @@ class Emitter {
       std::ostringstream b;
       // Cached: vector j of the cache; j == 0 is always the lane's own.
       b << "    if constexpr (NV > 0u) {\n#pragma unroll\n      for (uint32_t j = 0; j < NV; ++j) {\n";
-      b << "        if (j >= NLANE) break;\n";
+      b << "        if (!EX && j >= NLANE) break;\n";
       index(b, "        ", "j", "");
       operands(b, p, "        ", true, "vc", "");
       b << "        if (j == 0u) {\n";
@@ -1448,13 +1465,13 @@ class Emitter {
         o << "    part" << ci << " = tca::hip::seg_allreduce_rt(part" << ci << ", SEG, comb" << ci << ");\n";
       o << "    if (WPR > 1u) {\n      if ((threadIdx.x & 63u) == 0u) {\n";
       for (int ci : passes[p]) o << "        red" << ci << "[threadIdx.x >> 6] = part" << ci << ";\n";
-      o << "      }\n      __syncthreads();\n      const uint32_t w0 = (threadIdx.x / S) * WPR;\n";
+      o << "      }\n      __syncthreads();\n      const uint32_t w0 = (threadIdx.x >> 6) & ~(WPR - 1u);  // the row's first wave\n";
       for (int ci : passes[p]) {
         o << "      part" << ci << " = red" << ci << "[w0];\n";
         o << "      for (uint32_t w = 1; w < WPR; ++w) part" << ci << " = comb" << ci << "(part" << ci << ", red" << ci
           << "[w0 + w]);\n";
       }
-      o << "      __syncthreads();\n    }\n";
+      o << "    }\n";
       // init once per output (an empty row yields init), then the piped map.
       for (int ci : passes[p]) {
         const ir::Chain& c = g_.chains[ci];
@@ -1492,34 +1509,46 @@ class Emitter {
             << ";\n";
       }
     }
+    // Each reduction has its own LDS slots, written once per group: only a
+    // next group (a grid-stride step, block-uniform) must wait until every
+    // wave has read them.
+    o << "    if (grp + gridDim.x < ngroups) __syncthreads();\n";
     o << "  }\n}\n";
-    // One kernel per (vector width, small | large | streamed); launch guards
-    // on the row length pick exactly one (C % 4 == 0: V 4; C % 4 == 2: V 2;
-    // odd: V 1; then the row length in vectors).
+    // One kernel per (vector width, cached | streamed); launch guards on the
+    // row length pick exactly one (C % 4 == 0: V 4; C % 4 == 2: V 2; odd:
+    // V 1; then the row length in vectors).
     const std::string args = CallArgs(n);
     const std::string cdim = g_.dims[geo.col].name;
     const struct { uint32_t v, mod, rem; } widths[] = {{4, 4, 0}, {2, 4, 2}, {1, 2, 1}};
-    const struct { const char* tag; uint32_t block, nv; uint64_t lo_vecs, hi_vecs; } kinds[] = {
-        {"c", kSmallBlock, kCache, 0, uint64_t{kSmallBlock} * kCache},
-        {"l", kBlock, kCache, uint64_t{kSmallBlock} * kCache + 1, uint64_t{kBlock} * kCache},
-        {"s", kBlock, 0, uint64_t{kBlock} * kCache + 1, 0xffffffffull}};
+    const uint64_t cachedVecs = uint64_t{kBlock} * kCache;
     const std::string symbol = pk.symbol;
     for (const auto& w : widths) {
-      for (const auto& kd : kinds) {
-        const uint64_t lo = kd.lo_vecs * w.v, hi = std::min<uint64_t>(0xffffffffull, kd.hi_vecs * w.v);
+      for (int cached = 1; cached >= 0; --cached) {
+        const uint64_t lo = cached ? 0 : (cachedVecs + 1) * w.v;
+        const uint64_t hi = cached ? cachedVecs * w.v : 0xffffffffull;
         PlanKernel vk = pk;
-        vk.symbol = symbol + "_" + kd.tag + std::to_string(w.v);
-        vk.block = kd.block;
-        vk.grid.push_back(DimProduct(geo.outer) + "/pack(" + cdim + "," + std::to_string(kCache * w.v) + "," +
-                          std::to_string(kd.block) + ")");
+        vk.symbol = symbol + (cached ? "_c" : "_s") + std::to_string(w.v);
+        vk.block = kBlock;
+        vk.pack = cdim + " " + std::to_string(kCache * w.v) + " " + std::to_string(kMinBlock);
+        vk.grid.push_back(DimProduct(geo.outer) + "/pack");
         vk.when.push_back(cdim + " " + std::to_string(lo) + " " + std::to_string(hi) + " " + std::to_string(w.mod) +
                           " " + std::to_string(w.rem));
-        o << "extern \"C\" __global__ void __launch_bounds__(" << kd.block << ") " << vk.symbol << "(\n    " << sig
-          << ") {\n  " << body_fn << "<" << w.v << "u, " << kd.nv << "u, " << kd.block << "u>(" << args << ");\n}\n";
+        o << "extern \"C\" __global__ void __launch_bounds__(" << kBlock << ") " << vk.symbol << "(\n    " << sig
+          << ") {\n";
+        if (cached) {
+          o << "  const uint32_t vecs = (" << ExtentExpr(g_, geo.col) << ") / " << w.v << "u;\n";
+          o << "  const uint32_t ls = tca::hip::pack_lanes_log2(vecs, " << kCache << "u, " << lgBlock << "u);\n";
+          o << "  if (vecs == (" << kCache << "u << ls)) " << body_fn << "<" << w.v << "u, " << kCache << "u, true>(" << args
+            << ");\n";
+          o << "  else " << body_fn << "<" << w.v << "u, " << kCache << "u, false>(" << args << ");\n}\n";
+        } else {
+          o << "  " << body_fn << "<" << w.v << "u, 0u, false>(" << args << ");\n}\n";
+        }
         std::ostringstream det;
         det << "row=runtime (" << cdim << " % " << w.mod << " == " << w.rem << ", " << lo << ".." << hi << ": "
-            << (kd.nv ? "cached " + std::to_string(kd.nv) + " vectors/lane" : std::string("streamed")) << ") vec=" << w.v
-            << " lanes/row=runtime(<=" << kd.block << ") passes=" << passes.size() << " block=" << kd.block;
+            << (cached ? "cached " + std::to_string(kCache) + " vectors/lane" : std::string("streamed")) << ") vec=" << w.v
+            << " lanes/row=runtime(<=" << kBlock << ") passes=" << passes.size() << " block=max(" << kMinBlock
+            << ",lanes/row)";
         AddKernel(vk, Family::Stream, n.chains, det.str());
       }
     }
@@ -1578,6 +1607,7 @@ class Emitter {
       for (const auto& t : k.grid) p << " " << t;
       p << "\n";
       for (const auto& a : k.args) p << "arg " << a << "\n";
+      if (!k.pack.empty()) p << "pack " << k.pack << "\n";
       for (const auto& w : k.when) p << "when " << w << "\n";
     }
     p << "end\n";

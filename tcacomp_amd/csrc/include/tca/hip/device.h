@@ -154,6 +154,15 @@ __device__ __forceinline__ T seg_allreduce_rt(T v, uint32_t seg, Op op) {
   }
 }
 
+// Lanes per row of the packed row kernels, as log2: the smallest power of
+// two 2^ls <= 2^log2_block with per_lane << ls >= vecs (no lane holds more
+// than per_lane vectors unless the row needs more than the whole block).
+__device__ __forceinline__ uint32_t pack_lanes_log2(uint32_t vecs, uint32_t per_lane, uint32_t log2_block) {
+  uint32_t ls = 0u;
+  while (ls < log2_block && (per_lane << ls) < vecs) ++ls;
+  return ls;
+}
+
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
 __device__ __forceinline__ uint32_t wave_id() { return threadIdx.x >> 6; }
 

@@ -1,6 +1,8 @@
 // plan.cpp — parse, bind and pack a launch plan (format in plan.h).
 #include "plan.h"
 
+#include <algorithm>
+
 #include <cstring>
 #include <sstream>
 
@@ -53,26 +55,8 @@ bool ParseTerm(const Plan& p, const std::string& s, Term* t, std::string* err) {
     return false;
   }
   const std::string div = s.substr(slash + 1, colon == std::string::npos ? std::string::npos : colon - slash - 1);
-  if (div.compare(0, 5, "pack(") == 0 && div.back() == ')') {
-    // pack(<dim>,<elements per lane>,<block>): rows per block of the packed
-    // row families, a function of the row length.
-    const std::string in = div.substr(5, div.size() - 6);
-    const size_t c1 = in.find(','), c2 = c1 == std::string::npos ? c1 : in.find(',', c1 + 1);
-    if (c2 == std::string::npos || in.find(',', c2 + 1) != std::string::npos) {
-      *err = "grid term '" + s + "': pack(<dim>,<elements per lane>,<block>)";
-      return false;
-    }
-    t->pack_dim = FindDim(p, in.substr(0, c1));
-    if (t->pack_dim < 0) {
-      *err = "grid term '" + s + "' packs by an unknown dim";
-      return false;
-    }
-    if (!ParseU64(in.substr(c1 + 1, c2 - c1 - 1), &t->pack_epl) || t->pack_epl == 0 ||
-        !ParseU64(in.substr(c2 + 1), &t->pack_block) || t->pack_block == 0 ||
-        (t->pack_block & (t->pack_block - 1)) != 0) {
-      *err = "grid term '" + s + "' has a bad pack";
-      return false;
-    }
+  if (div == "pack") {
+    t->packed = true;  // rows per block of the kernel's pack record
   } else if (!ParseU64(div, &t->divisor) || t->divisor == 0) {
     *err = "grid term '" + s + "' has a bad divisor";
     return false;
@@ -230,6 +214,16 @@ bool Parse(const std::string& text, Plan* out, std::string* err) {
       }
       if (a.index < 0) return bad("arg names unknown " + tok[1] + " " + tok[2]);
       p.kernels.back().args.push_back(a);
+    } else if (kw == "pack") {
+      if (p.kernels.empty()) return bad("pack before any kernel");
+      Kernel& k = p.kernels.back();
+      if (tok.size() != 4 || !ParseU64(tok[2], &k.pack_epl) || !ParseU64(tok[3], &k.pack_min_block))
+        return bad("pack <dim> <elements per lane> <min block>");
+      k.pack_dim = FindDim(p, tok[1]);
+      if (k.pack_dim < 0) return bad("pack names unknown dim " + tok[1]);
+      if (k.pack_epl == 0 || k.pack_min_block == 0 || k.pack_min_block > k.block || (k.block & (k.block - 1)) != 0 ||
+          k.pack_min_block % 64 != 0)
+        return bad("bad pack on " + tok[1] + " (power-of-two block, 64 <= min block <= block)");
     } else if (kw == "when") {
       if (p.kernels.empty()) return bad("when before any kernel");
       Guard g;
@@ -249,6 +243,12 @@ bool Parse(const std::string& text, Plan* out, std::string* err) {
   if (!header) return bad("empty plan");
   if (!ended) return bad("missing 'end'");
   if (p.kernels.empty()) return bad("plan has no kernel");
+  for (const auto& k : p.kernels)
+    for (const auto& t : k.grid)
+      if (t.packed && k.pack_dim < 0) {
+        *err = "kernel " + k.symbol + ": grid divisor 'pack' needs a pack record";
+        return false;
+      }
   *out = p;
   return true;
 }
@@ -278,7 +278,7 @@ std::string Serialize(const Plan& p) {
         o << p.dims[d].name;
         first = false;
       }
-      if (t.pack_dim >= 0) o << "/pack(" << p.dims[t.pack_dim].name << "," << t.pack_epl << "," << t.pack_block << ")";
+      if (t.packed) o << "/pack";
       else o << "/" << t.divisor;
       if (t.cap != 0) o << ":" << t.cap;
     }
@@ -288,6 +288,8 @@ std::string Serialize(const Plan& p) {
       else if (a.kind == ArgKind::Dim) o << "arg dim " << p.dims[a.index].name << "\n";
       else o << "arg scalar " << p.scalars[a.index].name << "\n";
     }
+    if (k.pack_dim >= 0)
+      o << "pack " << p.dims[k.pack_dim].name << " " << k.pack_epl << " " << k.pack_min_block << "\n";
     for (const auto& g : k.when)
       o << "when " << p.dims[g.dim].name << " " << g.lo << " " << g.hi << " " << g.mod << " " << g.rem << "\n";
   }
@@ -401,12 +403,9 @@ bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims,
       }
     }
     uint64_t div = t.divisor;
-    if (t.pack_dim >= 0) {
-      // The kernel's own choice: S lanes per row, the smallest power of two
-      // <= block with S * epl >= the row length; block / S rows per block.
-      uint64_t lanes = 1;
-      while (lanes < t.pack_block && lanes * t.pack_epl < dims[t.pack_dim]) lanes <<= 1;
-      div = t.pack_block / lanes;
+    if (t.packed) {
+      uint32_t block = 0;
+      div = PackRows(k, dims, &block);
     }
     uint64_t q = (prod + div - 1) / div;
     if (t.cap != 0 && q > t.cap) q = t.cap;
@@ -418,6 +417,19 @@ bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims,
   }
   *grid = g;
   return true;
+}
+
+uint32_t PackRows(const Kernel& k, const std::vector<uint32_t>& dims, uint32_t* block) {
+  if (k.pack_dim < 0) {
+    *block = k.block;
+    return 1;
+  }
+  // The kernel's own choice: S lanes per row, the smallest power of two <=
+  // the largest block with S * epl >= the row length.
+  uint64_t lanes = 1;
+  while (lanes < k.block && lanes * k.pack_epl < dims[k.pack_dim]) lanes <<= 1;
+  *block = static_cast<uint32_t>(std::max<uint64_t>(k.pack_min_block, lanes));
+  return static_cast<uint32_t>(*block / lanes);
 }
 
 bool Selected(const Kernel& k, const std::vector<uint32_t>& dims) {

@@ -11,11 +11,12 @@
 //       term = <factor>[*<factor>...]/<divisor>[:<cap>], factor = dim name or
 //       integer; grid = product over terms of ceil(product(factors) / divisor),
 //       each term limited to <cap> when one is given (grid-stride kernels).
-//       divisor = integer | pack(<dim>,<epl>,<block>): rows per block of a
-//       packed row kernel, block / S with S the smallest power of two <= block
-//       such that S * epl >= dim (S lanes share a row of `dim` elements, each
-//       lane at most epl of them).
+//       divisor = integer | pack: the rows per block of the kernel's pack record
 //   arg ptr <tensor> | arg dim <name> | arg scalar <name>    (for the last kernel)
+//   pack <dim> <epl> <min-block>    (for the last kernel) the kernel packs rows of
+//       `dim` elements: S lanes share a row, S the smallest power of two <= the
+//       kernel's block with S * epl >= dim; it launches with max(min-block, S)
+//       lanes per block, max(min-block, S) / S rows each
 //   when <dim> <lo> <hi> <mod> <rem>    (for the last kernel) the kernel runs only
 //       when lo <= dim <= hi and dim % mod == rem; every guard of a kernel must
 //       hold. Variants of one nest specialised on a run-time dim carry guards
@@ -65,8 +66,7 @@ struct Term {
   uint64_t const_factor = 1;
   uint64_t divisor = 1;
   uint64_t cap = 0;  // 0 = none
-  int pack_dim = -1;  // >= 0: the divisor is pack(dim, pack_epl, pack_block)
-  uint64_t pack_epl = 0, pack_block = 0;
+  bool packed = false;  // the divisor is the kernel's rows per block
 };
 
 struct Arg {
@@ -86,6 +86,8 @@ struct Kernel {
   std::vector<Term> grid;
   std::vector<Arg> args;
   std::vector<Guard> when;
+  int pack_dim = -1;  // >= 0: a packed row kernel (block chosen at launch)
+  uint64_t pack_epl = 0, pack_min_block = 0;
 };
 
 struct Plan {
@@ -114,6 +116,9 @@ int Bind(const Plan& p, const tca_tensor* tensors, uint32_t n_tensors, const uin
 
 size_t TensorBytes(const Plan& p, size_t tensor, const std::vector<uint32_t>& dims);
 bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims, uint64_t* grid, std::string* err);
+// Rows per block of a packed kernel (1 otherwise); *block receives the
+// launch block size.
+uint32_t PackRows(const Kernel& k, const std::vector<uint32_t>& dims, uint32_t* block);
 // Whether every guard of k holds for the bound dims.
 bool Selected(const Kernel& k, const std::vector<uint32_t>& dims);
 // Packs the kernel arguments per the HIP kernarg ABI (natural alignment):

@@ -361,7 +361,8 @@ int tca_program_check(tca_program p, const tca_tensor* tensors, uint32_t n_tenso
 }
 
 int tca_program_selected(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
-                         uint32_t n_free_dims, uint8_t* selected, uint64_t* grids, uint32_t n_selected) {
+                         uint32_t n_free_dims, uint8_t* selected, uint64_t* grids, uint32_t* blocks,
+                         uint32_t n_selected) {
   if (p == nullptr) return fail(TCA_ERR_INVALID, "program_selected: null program");
   if (n_selected != p->plan.kernels.size())
     return fail(TCA_ERR_INVALID, "program_selected: program has %zu kernel(s), got room for %u", p->plan.kernels.size(),
@@ -374,6 +375,10 @@ int tca_program_selected(tca_program p, const tca_tensor* tensors, uint32_t n_te
   for (uint32_t i = 0; i < n_selected; ++i) {
     const auto& k = p->plan.kernels[i];
     selected[i] = tca::plan::Selected(k, dims) ? 1 : 0;
+    if (blocks != nullptr) {
+      blocks[i] = 0;
+      if (selected[i]) (void)tca::plan::PackRows(k, dims, &blocks[i]);
+    }
     if (grids == nullptr) continue;
     grids[i] = 0;
     if (selected[i] && !tca::plan::GridSize(k, p->plan, dims, &grids[i], &err)) return fail(TCA_ERR_LAUNCH, "%s", err.c_str());
@@ -445,14 +450,16 @@ int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tens
     if (grid > 0x7fffffffull)
       return fail(TCA_ERR_LAUNCH, "kernel %s: grid %llu exceeds 2^31-1", k.symbol.c_str(),
                   static_cast<unsigned long long>(grid));
-    rc = check_geometry(static_cast<uint32_t>(grid), k.block, k.lds, l.max_threads, l.max_lds);
+    uint32_t block = k.block;
+    (void)tca::plan::PackRows(k, dims, &block);  // packed row kernels size the block at launch
+    rc = check_geometry(static_cast<uint32_t>(grid), block, k.lds, l.max_threads, l.max_lds);
     if (rc != TCA_OK) return rc;
     std::vector<unsigned char> blob;
     if (!tca::plan::PackArgs(k, pl, ptrs, dims, scalars, &blob, &err)) return fail(TCA_ERR_INVALID, "%s", err.c_str());
     size_t size = blob.size();
     void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, blob.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
                       HIP_LAUNCH_PARAM_END};
-    hipError_t e = hipModuleLaunchKernel(p->funcs[ki], static_cast<uint32_t>(grid), 1, 1, k.block, 1, 1, k.lds,
+    hipError_t e = hipModuleLaunchKernel(p->funcs[ki], static_cast<uint32_t>(grid), 1, 1, block, 1, 1, k.lds,
                                          static_cast<hipStream_t>(stream), nullptr, config);
     if (e != hipSuccess) return hip_fail(e, "hipModuleLaunchKernel");
   }

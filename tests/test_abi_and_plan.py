@@ -66,7 +66,7 @@ def test_launch_guards():
         arr = compiler._descriptors(ts)
         fd = (ctypes.c_uint32 * 1)(3)
         out = (ctypes.c_uint8 * 1)()
-        assert _lib.lib().tca_program_selected(h, arr, 3, fd, 1, out, None, 1) == 0, _lib.last_error()
+        assert _lib.lib().tca_program_selected(h, arr, 3, fd, 1, out, None, None, 1) == 0, _lib.last_error()
         return out[0]
     assert selected(5, 8) == 1
     assert selected(5, 6) == 0  # N % 4 != 0
@@ -82,13 +82,12 @@ def test_launch_guards():
     assert rc == _lib.TCA_ERR_INVALID and "before any kernel" in _lib.last_error()
 
 
-@pytest.mark.parametrize("C,variant", [(0, "c4"), (64, "c4"), (4096, "c4"), (4100, "l4"), (16384, "l4"),
-                                       (16388, "s4"), (6, "c2"), (2046, "c2"), (2050, "l2"), (8190, "l2"),
-                                       (8194, "s2"), (1, "c1"), (1023, "c1"), (1025, "l1"), (4095, "l1"),
-                                       (4097, "s1")])
+@pytest.mark.parametrize("C,variant", [(0, "c4"), (64, "c4"), (4096, "c4"), (4100, "c4"), (16384, "c4"),
+                                       (16388, "s4"), (6, "c2"), (2046, "c2"), (8190, "c2"), (8194, "s2"),
+                                       (1, "c1"), (1023, "c1"), (4095, "c1"), (4097, "s1")])
 def test_stream_variant_selection(C, variant):
     """The guards of the streaming row family partition the row length: one
-    kernel per (vector width, small | large | streamed) and exactly one runs."""
+    kernel per (vector width, cached | streamed) and exactly one runs."""
     e = programs.CONFIG_PROGRAMS["row_sum_max_dyn"]().emit()
     rc, h = parse(e.plan)
     assert rc == 0, _lib.last_error()
@@ -97,28 +96,28 @@ def test_stream_variant_selection(C, variant):
     syms = e.kernel_symbols()
     out = (ctypes.c_uint8 * len(syms))()
     grids = (ctypes.c_uint64 * len(syms))()
-    assert _lib.lib().tca_program_selected(h, arr, 3, None, 0, out, grids, len(syms)) == 0, _lib.last_error()
+    assert _lib.lib().tca_program_selected(h, arr, 3, None, 0, out, grids, None, len(syms)) == 0, _lib.last_error()
     chosen = [s for s, f in zip(syms, out) if f]
     assert chosen == ["tca_row_sum_max_dyn_k0_" + variant]
     assert [g for g, f in zip(grids, out) if not f] == [0] * (len(syms) - 1)
 
 
-@pytest.mark.parametrize("R,C,grid", [
-    (1000, 0, 4),         # 1 lane per row, 256 rows per 256-lane block
-    (1000, 16, 4),        # 4 vectors: still 1 lane
-    (1000, 68, 32),       # 17 vectors: 8 lanes, 32 rows per block
-    (1000, 1024, 250),    # 256 vectors: 64 lanes, 4 rows per block
-    (1000, 4096, 1000),   # 1024 vectors: 256 lanes, the whole small block
-    (1000, 4100, 500),    # 1025 vectors: 1024-lane block, 512 lanes, 2 rows
-    (1000, 16384, 1000),  # 4096 vectors: 1024 lanes
-    (1000, 80000, 1000),  # streamed: 1024 lanes
-    (5, 3, 1),            # odd length: 1-element vectors, 1 lane
-    (1000, 2047, 500),    # 2047 one-element vectors: 512 lanes of a 1024 block
-    (0, 64, 0)])          # no rows: no launch
-def test_pack_grid_term(R, C, grid):
-    """pack(C, epl, block): one block per group of rows sharing it, the lane
-    count per row chosen as the kernel chooses it (smallest power of two
-    with lanes * epl >= C, at most the block)."""
+@pytest.mark.parametrize("R,C,grid,block", [
+    (1000, 0, 4, 256),         # 1 lane per row, 256 rows per 256-lane block
+    (1000, 16, 4, 256),        # 4 vectors: still 1 lane
+    (1000, 68, 32, 256),       # 17 vectors: 8 lanes, 32 rows per block
+    (1000, 1024, 250, 256),    # 256 vectors: 64 lanes, 4 rows per block
+    (1000, 4096, 1000, 256),   # 1024 vectors: 256 lanes, one row per block
+    (1000, 4100, 1000, 512),   # 1025 vectors: 512 lanes, the block grows to the row
+    (1000, 16384, 1000, 1024),  # 4096 vectors: 1024 lanes
+    (1000, 80000, 1000, 1024),  # streamed: 1024 lanes
+    (5, 3, 1, 256),            # odd length: 1-element vectors, 1 lane
+    (1000, 2047, 1000, 512),   # 2047 one-element vectors: 512 lanes
+    (0, 64, 0, 256)])          # no rows: no launch
+def test_pack_record(R, C, grid, block):
+    """pack <C> <epl> <min block>: S lanes per row as the kernel chooses them
+    (smallest power of two with S * epl >= C, at most the kernel's block),
+    max(min block, S) lanes per block, one block per group of rows."""
     e = programs.CONFIG_PROGRAMS["row_sum_max_dyn"]().emit()
     _, h = parse(e.plan)
     P = 0x1000
@@ -127,15 +126,20 @@ def test_pack_grid_term(R, C, grid):
     syms = e.kernel_symbols()
     out = (ctypes.c_uint8 * len(syms))()
     grids = (ctypes.c_uint64 * len(syms))()
-    assert _lib.lib().tca_program_selected(h, arr, 3, None, 0, out, grids, len(syms)) == 0, _lib.last_error()
-    assert sum(grids) == grid, list(grids)
+    blocks = (ctypes.c_uint32 * len(syms))()
+    assert _lib.lib().tca_program_selected(h, arr, 3, None, 0, out, grids, blocks, len(syms)) == 0, _lib.last_error()
+    assert (sum(grids), sum(blocks)) == (grid, block), (list(grids), list(blocks))
 
 
-def test_pack_term_parse():
-    for term, ok in [("R/pack(N,16,256)", True), ("R/pack(N,16,256):9", True), ("R/pack(Q,16,256)", False),
-                     ("R/pack(N,0,256)", False), ("R/pack(N,16,96)", False), ("R/pack(N,16)", False)]:
-        rc, _ = parse(PLAN.replace("M*N/1024", term.replace("R", "M")))
-        assert (rc == 0) == ok, (term, _lib.last_error())
+def test_pack_record_parse():
+    for rec, term, ok in [("pack N 16 256", "M/pack", True), ("pack N 16 256", "M/pack:9", True),
+                          ("", "M/pack", False), ("pack Q 16 256", "M/pack", False),
+                          ("pack N 0 256", "M/pack", False), ("pack N 16 96", "M/pack", False),
+                          ("pack N 16 512", "M/pack", False), ("pack N 16", "M/pack", False)]:
+        text = PLAN.replace("M*N/1024", term).replace("arg scalar a\n", "arg scalar a\n%s\n" % rec if rec else
+                                                        "arg scalar a\n")
+        rc, _ = parse(text)
+        assert (rc == 0) == ok, (rec, term, _lib.last_error())
 
 
 PLAN = """tca-plan 1
@@ -242,8 +246,8 @@ def test_program_launch_without_module_is_refused():
 EXPECTED_FAMILIES = {
     "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"],
     "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"], "gemm_bf16": ["gemm"],
-    "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 9, "softmax_dyn": ["stream"] * 9,
-    "layernorm_dyn": ["stream"] * 9,
+    "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 6, "softmax_dyn": ["stream"] * 6,
+    "layernorm_dyn": ["stream"] * 6,
 }
 
 
