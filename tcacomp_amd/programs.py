@@ -20,7 +20,7 @@ Configurations (BASELINE.json):
 Reference suite (testing/kernels/**.tca, shapes in testing/suite.toml): see
 SUITE below.
 """
-from .pkg import (TBF16, TF32, At, Call, Cast, NewBuilder)
+from .pkg import (TBF16, TF32, TU8, TU32, At, Call, Cast, NewBuilder)
 
 
 def _sum(b):
@@ -127,6 +127,48 @@ def layernorm(cols=1024):
      .Map([At(x, R, C), At(mean, R), At(var, R), At(gamma, C), At(beta, C)],
           lambda l, r, s, t, u: b.Add(b.Mul(b.Mul(b.Sub(l, r), Call("rsqrtf", b.Add(s, eps))), t), u))
      .As(R, C).Store(y, R, C))
+    return b.Build()
+
+
+def row_stats_u32(cols=1000):
+    """Integer row reductions over u32 [R, C]: wrapping sum, xor and umax
+    (the monoid combiners of the row families on a 32-bit integer type)."""
+    b = NewBuilder("row_stats_u32_%s" % (cols or "dyn"))
+    R, C = b.Dim("R", 0), _static(b, "C", cols)
+    x = b.Tensor("x", TU32, R, C)
+    outs = [b.Tensor(n, TU32, R) for n in ("sum", "xor", "max")]
+    inits = [b.UInt32(0), b.UInt32(0), b.UInt32(0)]
+    fns = [lambda acc, v: b.Add(acc, v), lambda acc, v: b.BitXor(acc, v), lambda acc, v: Call("umax", acc, v)]
+    for o, i, f in zip(outs, inits, fns):
+        b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C).Reduce(i, f).Store(o, R)
+    return b.Build()
+
+
+def row_sum_bf16(cols=1000):
+    """Row sum and max of bf16 [R, C] accumulated in f32 (Cast per element)."""
+    b = NewBuilder("row_sum_bf16_%s" % (cols or "dyn"))
+    R, C = b.Dim("R", 0), _static(b, "C", cols)
+    x = b.Tensor("x", TBF16, R, C)
+    s = b.Tensor("sum", TF32, R)
+    m = b.Tensor("max", TF32, R)
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: Cast(v, TF32)).As(R, C)
+     .Reduce(b.Float32(0), _sum(b)).Store(s, R))
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: Cast(v, TF32)).As(R, C)
+     .Reduce(_neg_inf(b), lambda acc, v: Call("fmaxf", acc, v)).Store(m, R))
+    return b.Build()
+
+
+def row_sum_u8(cols=1000):
+    """Byte rows summed into u32 (Cast per element), then scaled to f32 by a
+    piped map: out = f32(sum) * scale."""
+    b = NewBuilder("row_sum_u8_%s" % (cols or "dyn"))
+    R, C = b.Dim("R", 0), _static(b, "C", cols)
+    x = b.Tensor("x", TU8, R, C)
+    out = b.Tensor("out", TF32, R)
+    scale = b.ScalarParam("scale", TF32)
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: Cast(v, TU32)).As(R, C)
+     .Reduce(b.UInt32(0), lambda acc, v: b.Add(acc, v))
+     .Map([], lambda v: b.Mul(Cast(v, TF32), scale)).As(R).Store(out, R))
     return b.Build()
 
 
@@ -328,6 +370,13 @@ CONFIG_PROGRAMS = {
     "row_sum_max_dyn": lambda: row_sum_max(0),
     "softmax_dyn": lambda: softmax(0),
     "layernorm_dyn": lambda: layernorm(0),
+    # other element types through the row and streaming families
+    "row_stats_u32_1000": lambda: row_stats_u32(1000),
+    "row_stats_u32_dyn": lambda: row_stats_u32(0),
+    "row_sum_bf16_1000": lambda: row_sum_bf16(1000),
+    "row_sum_bf16_dyn": lambda: row_sum_bf16(0),
+    "row_sum_u8_1000": lambda: row_sum_u8(1000),
+    "row_sum_u8_dyn": lambda: row_sum_u8(0),
 }
 
 
