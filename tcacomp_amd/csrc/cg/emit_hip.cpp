@@ -352,27 +352,47 @@ OpKind Classify(const ir::Operand& o, const RowGeom& geo) {
   return OpKind::RowScalar;
 }
 
+// True for a chain of a row nest that iterates only the outer axes (one level
+// shallower than the nest): a per-row scalar computation.
+bool IsRowScalarChain(const ir::Chain& c, const RowGeom& geo) { return c.root.as.size() + 1 == geo.as.size(); }
+
 // The structural conditions shared by the register-resident row family and
 // the streaming row family: every chain iterates (outer..., col) in one
-// order, at most one reduction per chain (over col) with an associative-
-// commutative combiner, operands are row tiles, column vectors or row
-// scalars. `stream` additionally refuses elementwise chains into locals (a
-// streamed row is never held, so a row-tile local could not be re-read).
+// order, or only (outer...) — the prefix fusion of a shallower nest
+// (internal/opt/gvn/gvn_test.go:458-518): a map over row scalars storing a
+// row scalar, evaluated once per row. At most one reduction per chain (over
+// col) with an associative-commutative combiner; operands are row tiles,
+// column vectors or row scalars. `stream` additionally refuses elementwise
+// chains into locals (a streamed row is never held, so a row-tile local
+// could not be re-read).
 bool RowShape(const Graph& g, const std::vector<int>& chains, bool stream, RowGeom* out) {
   RowGeom& geo = *out;
-  const ir::Chain& c0 = g.chains[chains[0]];
-  geo.as = c0.root.as;
-  geo.col = geo.as.back();
-  geo.outer.assign(geo.as.begin(), geo.as.end() - 1);
   auto no = [&](const std::string& w) {
     geo.ok = false;
     geo.why = w;
     return false;
   };
+  // The nest's iteration order is its deepest chain's.
+  geo.as = g.chains[chains[0]].root.as;
+  for (int ci : chains)
+    if (g.chains[ci].root.as.size() > geo.as.size()) geo.as = g.chains[ci].root.as;
+  if (geo.as.empty()) return no("no iteration axis");
+  geo.col = geo.as.back();
+  geo.outer.assign(geo.as.begin(), geo.as.end() - 1);
+  bool deep = false;
   std::set<int> produced_tile, produced_scalar;
   for (int ci : chains) {
     const ir::Chain& c = g.chains[ci];
+    if (IsRowScalarChain(c, geo) && c.root.as == geo.outer && !geo.outer.empty()) {
+      if (!c.reduces.empty()) return no("a per-row chain with a reduction");
+      for (const auto& o : c.root.ops)
+        if (Classify(o, geo) != OpKind::RowScalar) return no("per-row chain operand is not a row scalar");
+      if (c.store_axes != geo.outer) return no("per-row store is not in iteration order");
+      if (g.tensors[c.store_tensor].local) produced_scalar.insert(c.store_tensor);
+      continue;
+    }
     if (c.root.as != geo.as) return no("iteration orders differ");
+    deep = true;
     if (c.reduces.size() > 1) return no("more than one reduction in a chain");
     if (c.reduces.size() == 1 && !IsMonoidCombiner(g, c.reduces[0]))
       return no("combiner is not an associative-commutative op over (acc, now)");
@@ -397,6 +417,7 @@ bool RowShape(const Graph& g, const std::vector<int>& chains, bool stream, RowGe
       if (st.local) produced_scalar.insert(c.store_tensor);
     }
   }
+  if (!deep) return no("no chain iterates the row");
   geo.ok = true;
   return true;
 }
@@ -411,18 +432,14 @@ RowGeom StreamCheck(const Graph& g, const std::vector<int>& chains) {
 
 RowGeom RowCheck(const Graph& g, const std::vector<int>& chains, uint32_t nv_target) {
   RowGeom geo;
-  const ir::Chain& c0 = g.chains[chains[0]];
-  geo.as = c0.root.as;
-  geo.col = geo.as.back();
-  geo.outer.assign(geo.as.begin(), geo.as.end() - 1);
   auto no = [&](const std::string& w) {
     geo.ok = false;
     geo.why = w;
     return geo;
   };
+  if (!RowShape(g, chains, false, &geo)) return geo;
   if (g.dims[geo.col].extent == 0) return no("row axis @" + g.dims[geo.col].name + " has a dynamic extent");
   geo.C = static_cast<uint32_t>(g.dims[geo.col].extent);
-  if (!RowShape(g, chains, false, &geo)) return geo;
   geo.V =(geo.C % 4 == 0) ? 4 : (geo.C % 2 == 0 ? 2 : 1);
   geo.vecs = geo.C / geo.V;
   uint32_t tpr = 1;
@@ -530,7 +547,7 @@ class Emitter {
     };
     for (int i = 0; i < nc; ++i) {
       if (!an_.live[i]) continue;
-      if (!cur.empty() && opts_.allow_fused && g_.chains[i].root.as == g_.chains[cur[0]].root.as) {
+      if (!cur.empty() && opts_.allow_fused) {
         std::vector<int> cand = cur;
         cand.push_back(i);
         if ((RowCheck(g_, cand, RowNV()).ok || StreamCheck(g_, cand).ok) && !IsGemm(cur)) {
@@ -1099,6 +1116,21 @@ class Emitter {
       bool dep = false;
       for (int t : reads) dep |= groupOut.count(t) > 0;
       if (c.reduces.empty() || dep) finalize();
+      if (IsRowScalarChain(c, geo)) {
+        // Per-row map: evaluated once per row (by every lane of it).
+        const int st = c.store_tensor;
+        const std::string T = CType(g_.tensors[st].elem);
+        o << "  // statement #" << ci << ": per-row map into " << g_.tensors[st].name << "\n";
+        ExprGen eg(g_, o, "  ", &counter_);
+        for (size_t k = 0; k < c.root.ops.size(); ++k) eg.Bind(c.root.fn.params[k], rowScalar(c.root.ops[k]));
+        const std::string val = eg.Gen(c.root.fn.body);
+        const std::string var = "r" + std::to_string(ci);
+        o << "  const " << T << " " << var << " = " << val << ";\n";
+        regScalar[st] = var;
+        if (!isReg(st) || an_.hbm_local[st])
+          o << "  if (active && lane == 0u) t" << st << "[" << Offset(st, c.store_axes, coord) << "] = " << var << ";\n";
+        continue;
+      }
       if (!c.reduces.empty()) {
         const std::string T = CType(g_.exprs[c.root.fn.body].type);
         o << "  // statement #" << ci << ": reduce over @" << g_.dims[geo.col].name << " into "
@@ -1415,6 +1447,22 @@ class Emitter {
     for (size_t p = 0; p < passes.size(); ++p) {
       const ir::Chain& c0 = g_.chains[passes[p][0]];
       const bool red = !c0.reduces.empty();
+      if (IsRowScalarChain(c0, geo)) {
+        // Per-row map: evaluated once per row (by every lane of it).
+        const int st = c0.store_tensor;
+        const std::string T = CType(g_.tensors[st].elem);
+        o << "    // statement #" << passes[p][0] << ": per-row map into " << g_.tensors[st].name << "\n";
+        ExprGen eg(g_, o, "    ", &counter_);
+        for (size_t k = 0; k < c0.root.ops.size(); ++k) eg.Bind(c0.root.fn.params[k], rowScalar(c0.root.ops[k]));
+        const std::string val = eg.Gen(c0.root.fn.body);
+        const std::string var = "r" + std::to_string(passes[p][0]);
+        o << "    const " << T << " " << var << " = " << val << ";\n";
+        regScalar[st] = var;
+        if (!isReg(st) || an_.hbm_local[st])
+          o << "    if (active && lane == 0u) t" << st << "[" << Offset(st, c0.store_axes, coord) << "] = " << var
+            << ";\n";
+        continue;
+      }
       o << "    // statement";
       for (int ci : passes[p]) o << " #" << ci;
       if (red) {

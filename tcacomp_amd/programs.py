@@ -130,6 +130,37 @@ def layernorm(cols=1024):
     return b.Build()
 
 
+def layernorm_rstd(cols=1024):
+    """C4 with the reciprocal standard deviation as its own per-row chain
+    (iterating only the row axis, one level shallower than the others) and
+    also stored as an output: mean, var -> rstd = rsqrtf(var + eps) ->
+    y = (x - mean) * rstd * gamma + beta. Same arithmetic as layernorm()."""
+    b = NewBuilder("layernorm_rstd_%s" % (cols or "dyn"))
+    R, C = b.Dim("R", 0), _static(b, "C", cols)
+    x = b.Tensor("x", TF32, R, C)
+    gamma = b.Tensor("gamma", TF32, C)
+    beta = b.Tensor("beta", TF32, C)
+    y = b.Tensor("y", TF32, R, C)
+    rstd = b.Tensor("rstd", TF32, R)
+    mean = b.Local("mean", TF32, R)
+    var = b.Local("var", TF32, R)
+    inv_n = b.ScalarParam("inv_n", TF32)
+    eps = b.ScalarParam("eps", TF32)
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C)
+     .Reduce(b.Float32(0), _sum(b))
+     .Map([], lambda v: b.Mul(v, inv_n)).As(R).Store(mean, R))
+    (b.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(mean, R)], lambda l, r: b.Mul(b.Sub(l, r), b.Sub(l, r))).As(R, C)
+     .Reduce(b.Float32(0), _sum(b))
+     .Map([], lambda v: b.Mul(v, inv_n)).As(R).Store(var, R))
+    b.Stmt().Iter(R).Map([At(var, R)], lambda v: Call("rsqrtf", b.Add(v, eps))).As(R).Store(rstd, R)
+    (b.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(mean, R), At(rstd, R), At(gamma, C), At(beta, C)],
+          lambda l, r, s, t, u: b.Add(b.Mul(b.Mul(b.Sub(l, r), s), t), u))
+     .As(R, C).Store(y, R, C))
+    return b.Build()
+
+
 def row_stats_u32(cols=1000):
     """Integer row reductions over u32 [R, C]: wrapping sum, xor and umax
     (the monoid combiners of the row families on a 32-bit integer type)."""
@@ -370,6 +401,9 @@ CONFIG_PROGRAMS = {
     "row_sum_max_dyn": lambda: row_sum_max(0),
     "softmax_dyn": lambda: softmax(0),
     "layernorm_dyn": lambda: layernorm(0),
+    # a per-row chain fused between the reductions and the row map
+    "layernorm_rstd_1024": lambda: layernorm_rstd(1024),
+    "layernorm_rstd_dyn": lambda: layernorm_rstd(0),
     # other element types through the row and streaming families
     "row_stats_u32_1000": lambda: row_stats_u32(1000),
     "row_stats_u32_dyn": lambda: row_stats_u32(0),

@@ -247,8 +247,18 @@ EXPECTED_FAMILIES = {
     "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"],
     "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"], "gemm_bf16": ["gemm"],
     "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 6, "softmax_dyn": ["stream"] * 6,
-    "layernorm_dyn": ["stream"] * 6,
+    "layernorm_dyn": ["stream"] * 6, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 6,
 }
+
+
+def test_prefix_chain_fuses_into_the_row_kernel():
+    """A per-row chain (iterating only the row axis) fuses with the row nest
+    around it; its value stays in registers when it is a local and is stored
+    once per row when it is an output."""
+    e = programs.CONFIG_PROGRAMS["layernorm_rstd_1024"]().emit()
+    assert e.families() == ["row"]
+    assert "per-row map into rstd" in e.source
+    assert "tensor rstd f32 out 1 R" in e.plan and "local" not in e.plan
 
 
 @pytest.mark.parametrize("name", sorted(EXPECTED_FAMILIES))
