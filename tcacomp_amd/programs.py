@@ -20,7 +20,7 @@ Configurations (BASELINE.json):
 Reference suite (testing/kernels/**.tca, shapes in testing/suite.toml): see
 SUITE below.
 """
-from .pkg import (TBF16, TF32, TU8, TU32, At, Call, Cast, NewBuilder)
+from .pkg import (TBF16, TF16, TF32, TI32, TU8, TU32, At, Call, Cast, NewBuilder, Select)
 
 
 def _sum(b):
@@ -200,6 +200,67 @@ def row_sum_u8(cols=1000):
     (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: Cast(v, TU32)).As(R, C)
      .Reduce(b.UInt32(0), lambda acc, v: b.Add(acc, v))
      .Map([], lambda v: b.Mul(Cast(v, TF32), scale)).As(R).Store(out, R))
+    return b.Build()
+
+
+# Expression-layer parity programs: one output per expression over [N]
+# operands, so every operator, builtin and cast of the DSL (pkg/expr.go:
+# 140-341, internal/ir/builtins.go:25-33) runs on the device.
+EXPR_F32 = [
+    ("add", lambda b, l, r: b.Add(l, r)), ("sub", lambda b, l, r: b.Sub(l, r)),
+    ("mul", lambda b, l, r: b.Mul(l, r)), ("div", lambda b, l, r: b.Div(l, r)),
+    ("neg", lambda b, l, r: b.Neg(l)), ("sel", lambda b, l, r: Select(b.Lt(l, r), l, r)),
+    ("fmin", lambda b, l, r: Call("fminf", l, r)), ("fmax", lambda b, l, r: Call("fmaxf", l, r)),
+    ("fma", lambda b, l, r: Call("fmaf", l, r, l)), ("fabs", lambda b, l, r: Call("fabsf", l)),
+    ("sqrt", lambda b, l, r: Call("sqrtf", l)), ("exp", lambda b, l, r: Call("expf", l)),
+    ("log", lambda b, l, r: Call("logf", l)), ("rsqrt", lambda b, l, r: Call("rsqrtf", l)),
+    ("sin", lambda b, l, r: Call("sinf", l)), ("cos", lambda b, l, r: Call("cosf", l)),
+    ("tanh", lambda b, l, r: Call("tanhf", l)),
+]
+EXPR_I32 = [
+    ("add", lambda b, l, r: b.Add(l, r)), ("sub", lambda b, l, r: b.Sub(l, r)),
+    ("mul", lambda b, l, r: b.Mul(l, r)), ("div", lambda b, l, r: b.Div(l, r)),
+    ("mod", lambda b, l, r: b.Mod(l, r)), ("and", lambda b, l, r: b.BitAnd(l, r)),
+    ("or", lambda b, l, r: b.BitOr(l, r)), ("xor", lambda b, l, r: b.BitXor(l, r)),
+    ("shl", lambda b, l, r: b.Shl(b.BitAnd(l, b.Int32(0xFFFF)), b.BitAnd(r, b.Int32(15)))),
+    ("shr", lambda b, l, r: b.Shr(l, b.BitAnd(r, b.Int32(31)))),
+    ("neg", lambda b, l, r: b.Neg(l)), ("not", lambda b, l, r: b.BitsNot(l)),
+    ("cmp", lambda b, l, r: Select(b.And(b.Lt(l, r), b.Ne(l, b.Int32(0))), b.Int32(1),
+                                   Select(b.Or(b.Ge(l, r), b.Eq(r, b.Int32(7))), b.Int32(2), b.Int32(3)))),
+]
+EXPR_U32 = [
+    ("add", lambda b, l, r: b.Add(l, r)), ("sub", lambda b, l, r: b.Sub(l, r)),
+    ("mul", lambda b, l, r: b.Mul(l, r)), ("div", lambda b, l, r: b.Div(l, r)),
+    ("mod", lambda b, l, r: b.Mod(l, r)), ("shr", lambda b, l, r: b.Shr(l, b.BitAnd(r, b.UInt32(31)))),
+    ("umin", lambda b, l, r: Call("umin", l, r)), ("umax", lambda b, l, r: Call("umax", l, r)),
+    ("not", lambda b, l, r: b.BitsNot(l)), ("le", lambda b, l, r: Select(b.Le(l, r), l, r)),
+]
+
+
+def _expr_program(name, elem, table):
+    b = NewBuilder(name)
+    N = b.Dim("N", 0)
+    x, y = b.Tensor("x", elem, N), b.Tensor("y", elem, N)
+    def bound(f):
+        return lambda l, r: f(b, l, r)
+    for out_name, f in table:
+        out = b.Tensor(out_name, elem, N)
+        b.Stmt().Iter(N).Map([At(x, N), At(y, N)], bound(f)).As(N).Store(out, N)
+    return b.Build()
+
+
+def expr_casts():
+    """The casts between element types, from f32 x and i32 k over [N]."""
+    b = NewBuilder("expr_casts")
+    N = b.Dim("N", 0)
+    x, k = b.Tensor("x", TF32, N), b.Tensor("k", TI32, N)
+    outs = [("bf16", TBF16, lambda l, r: Cast(l, TBF16)), ("f16", TF16, lambda l, r: Cast(l, TF16)),
+            ("trunc", TI32, lambda l, r: Cast(l, TI32)), ("tof32", TF32, lambda l, r: Cast(r, TF32)),
+            ("tou8", TU8, lambda l, r: Cast(r, TU8)), ("tou32", TU32, lambda l, r: Cast(r, TU32)),
+            ("bf16f32", TF32, lambda l, r: Cast(Cast(l, TBF16), TF32))]
+    for out_name, elem, f in outs:
+        out = b.Tensor(out_name, elem, N)
+        b.Stmt().Iter(N).Map([At(x, N), At(k, N)], f).As(N).Store(out, N)
     return b.Build()
 
 
@@ -404,6 +465,11 @@ CONFIG_PROGRAMS = {
     # a per-row chain fused between the reductions and the row map
     "layernorm_rstd_1024": lambda: layernorm_rstd(1024),
     "layernorm_rstd_dyn": lambda: layernorm_rstd(0),
+    # the expression layer: every operator, builtin and cast on the device
+    "expr_f32": lambda: _expr_program("expr_f32", TF32, EXPR_F32),
+    "expr_i32": lambda: _expr_program("expr_i32", TI32, EXPR_I32),
+    "expr_u32": lambda: _expr_program("expr_u32", TU32, EXPR_U32),
+    "expr_casts": expr_casts,
     # other element types through the row and streaming families
     "row_stats_u32_1000": lambda: row_stats_u32(1000),
     "row_stats_u32_dyn": lambda: row_stats_u32(0),
