@@ -157,18 +157,21 @@ int tca_rt_free(void* ptr) {
 
 int tca_rt_memcpy_h2d(void* dst, const void* src, size_t bytes) {
   if (bytes == 0) return TCA_OK;
+  if (dst == nullptr || src == nullptr) return fail(TCA_ERR_INVALID, "memcpy_h2d: null pointer for %zu bytes", bytes);
   TCA_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
   return TCA_OK;
 }
 
 int tca_rt_memcpy_d2h(void* dst, const void* src, size_t bytes) {
   if (bytes == 0) return TCA_OK;
+  if (dst == nullptr || src == nullptr) return fail(TCA_ERR_INVALID, "memcpy_d2h: null pointer for %zu bytes", bytes);
   TCA_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
   return TCA_OK;
 }
 
 int tca_rt_memset(void* dst, int value, size_t bytes) {
   if (bytes == 0) return TCA_OK;
+  if (dst == nullptr) return fail(TCA_ERR_INVALID, "memset: null pointer for %zu bytes", bytes);
   TCA_HIP_TRY(hipMemset(dst, value, bytes));
   return TCA_OK;
 }
@@ -264,6 +267,7 @@ int tca_rt_validate_launch(uint32_t grid, uint32_t block, uint32_t lds_bytes) {
 int tca_rt_launch(tca_module m, const char* kernel, uint32_t grid, uint32_t block, uint32_t lds_bytes,
                   void* args, size_t args_size, tca_stream_t s) {
   if (m == nullptr || kernel == nullptr) return fail(TCA_ERR_INVALID, "launch: null module or kernel name");
+  if (args == nullptr && args_size > 0) return fail(TCA_ERR_INVALID, "launch: null argument blob of %zu bytes", args_size);
   DeviceLimits l;
   int rc = query_limits(&l);
   if (rc != TCA_OK) return rc;

@@ -313,3 +313,16 @@ def test_every_registered_program_is_prebuilt():
 def test_build_sources_listed():
     for s in build.SOURCES:
         assert os.path.exists(os.path.join(build.CSRC, s))
+
+
+def test_runtime_null_arguments_are_refused_before_hip():
+    """Host-side validation of the memory and launch entry points: a null
+    pointer with a non-zero size is TCA_ERR_INVALID with a message, no HIP
+    call is made (so this runs without a GPU)."""
+    L = _lib.lib()
+    assert L.tca_rt_memcpy_h2d(None, None, 16) == _lib.TCA_ERR_INVALID and "null" in _lib.last_error()
+    assert L.tca_rt_memcpy_d2h(None, None, 16) == _lib.TCA_ERR_INVALID
+    assert L.tca_rt_memset(None, 0, 16) == _lib.TCA_ERR_INVALID
+    assert L.tca_rt_memcpy_h2d(None, None, 0) == 0  # nothing to copy
+    assert L.tca_rt_free(None) == 0
+    assert L.tca_rt_launch(None, b"k", 1, 64, 0, None, 0, None) == _lib.TCA_ERR_INVALID
