@@ -40,6 +40,10 @@ CONFIGS = {
     "c2s": ("row_sum_max_dyn", "C2 with run-time row length (streaming family)"),
     "c3s": ("softmax_dyn", "C3 with run-time row length (streaming family)"),
     "c4s": ("layernorm_dyn", "C4 with run-time row length (streaming family)"),
+    # C2's reductions on few long rows (the streaming family's split rows):
+    # not configurations; shown because one workgroup per row would idle the GPU
+    "c2v": ("vec_sum_max", "sum+max of one f32 vector [67108864] (split rows, full reduction)"),
+    "c2r": ("row_sum_max_dyn", "row sum+max f32 [16,4194304] (split rows)"),
     # not a configuration: the plain copy used to calibrate rocprof counters
     "copy": ("copy_f32", "copy f32 [8192,8192] (counter calibration)"),
 }
@@ -69,7 +73,19 @@ def _setup(key, dev):
     def dev_f32(a):
         return torch.from_numpy(a).to(dev)
 
-    if key == "copy":
+    if key in ("c2v", "c2r"):
+        R, C = (1, 64 << 20) if key == "c2v" else (16, 4 << 20)
+        x = inputs.normal((R, C), 1.0, 0)
+        algo = R * C * 4 + 2 * R * 4
+        per_set = algo
+        if key == "c2v":
+            make = lambda i: [dev_f32(x.reshape(C)), torch.empty((), device=dev), torch.empty((), device=dev)]  # noqa: E731
+        else:
+            make = lambda i: [dev_f32(x), torch.empty(R, device=dev), torch.empty(R, device=dev)]  # noqa: E731
+        scalars = []
+        work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = None
+    elif key == "copy":
         R = C = 8192
         x = inputs.uniform((R, C), -1, 1, 0)
         algo = 2 * R * C * 4
@@ -234,7 +250,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
                     help="untimed launches per config before the warmup steps, in wall-clock ms")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")

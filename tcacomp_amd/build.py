@@ -69,12 +69,14 @@ def build_kernels(jobs=8, force=False):
     from . import compiler, programs
 
     jobs_list = []
+    current = set()
     for name, factory, flags in programs.all_builds():
         prog = factory()
         emitted = prog.emit(flags=flags)
         key = compiler.cache_key(emitted.source, emitted.hipcc)
         os.makedirs(compiler.KCACHE, exist_ok=True)
         base = os.path.join(compiler.KCACHE, "%s-%s" % (prog.name, key))
+        current.add(os.path.basename(base))
         with open(base + ".hip", "w") as f:
             f.write(emitted.source)
         with open(base + ".plan", "w") as f:
@@ -88,6 +90,11 @@ def build_kernels(jobs=8, force=False):
 
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
         done = list(ex.map(one, jobs_list))
+    # Drop code objects of earlier sources: the cache travels with the tree.
+    for f in os.listdir(compiler.KCACHE):
+        stem = f.rsplit(".", 1)[0]
+        if stem not in current:
+            os.remove(os.path.join(compiler.KCACHE, f))
     return done
 
 

@@ -1562,6 +1562,167 @@ class Emitter {
     // wave has read them.
     o << "    if (grp + gridDim.x < ngroups) __syncthreads();\n";
     o << "  }\n}\n";
+    // Few long rows: each row split over many blocks. Applies when the nest
+    // is one pass of reductions (no row maps, no per-row chains) and the
+    // rows are indexed by at most one axis. A partial kernel folds a chunk
+    // of >= 2048 vectors per block (P chunks per row, P = min(512,
+    // ceil(vectors / 4096)): 512 blocks of 1024 lanes are what the CUs hold
+    // at once, 1024 chunks measured 10% slower on a full reduction; with
+    // chunks of ceil(vectors / P) every chunk, the last included, holds >=
+    // 2048 vectors for rows > 4096 vectors, so every thread holds >= 1) and
+    // writes one partial per block and reduction into an HBM scratch
+    // [rows][512]; a
+    // merge kernel folds a row's P partials with one wave, applies init once
+    // and the piped map, and stores. Guards: the streamed row lengths with
+    // rows <= kSplitRows (one block per row would leave most CUs idle);
+    // with no row axis (a full reduction) the split replaces the streamed
+    // kernel outright.
+    constexpr uint32_t kSplitRows = 255, kChunkVecs = 4096, kMaxParts = 512, kPartBlock = 1024;
+    const bool split = passes.size() == 1 && !g_.chains[passes[0][0]].reduces.empty() && geo.outer.size() <= 1;
+    std::string part_fn, merge_fn;
+    std::vector<std::string> part_names;
+    if (split) {
+      part_fn = pk.symbol + "_part";
+      merge_fn = pk.symbol + "_merge";
+      const std::string splitDim = "__split";
+      extra_dims_.push_back(splitDim + " " + std::to_string(kMaxParts));
+      std::string partSig;
+      for (int ci : passes[0]) {
+        const ir::Chain& c = g_.chains[ci];
+        const ir::Elem pe = g_.exprs[c.root.fn.body].type;
+        const std::string nm = "__part" + std::to_string(ci);
+        part_names.push_back(nm);
+        std::string t = nm + " " + ir::ElemName(pe) + " local " + std::to_string(geo.outer.size() + 1);
+        for (int a : geo.outer) t += " " + g_.dims[a].name;
+        extra_tensors_.push_back(t + " " + splitDim);
+        partSig += ",\n    " + CType(pe) + "* __restrict__ p" + std::to_string(ci) + " /* " + nm + " */";
+      }
+      const std::string rowExpr = ProductExpr(geo.outer);
+      auto combs = [&](const std::string& ind) {
+        for (int ci : passes[0]) {
+          const ir::Chain& c = g_.chains[ci];
+          const std::string T = CType(g_.exprs[c.root.fn.body].type);
+          o << ind << "const auto comb" << ci << " = [](" << T << " acc, " << T << " now) -> " << T << " {\n";
+          ExprGen cg(g_, o, ind + "  ", &counter_);
+          cg.Bind(c.reduces[0].fn.params[0], "acc");
+          cg.Bind(c.reduces[0].fn.params[1], "now");
+          const std::string r = cg.Gen(c.reduces[0].fn.body);
+          o << ind << "  return " << r << ";\n" << ind << "};\n";
+        }
+      };
+      auto rowCoords = [&](const std::string& ind) {
+        for (int a : geo.outer) o << ind << "const uint32_t c" << a << " = r;\n";
+      };
+      // Row scalars the fold or the piped maps read from memory.
+      auto rowScalars = [&](const std::string& ind) {
+        std::set<int> done;
+        for (int ci : passes[0]) {
+          const ir::Chain& c = g_.chains[ci];
+          std::vector<const ir::Operand*> ops;
+          for (const auto& op : c.root.ops) ops.push_back(&op);
+          if (c.has_piped)
+            for (const auto& op : c.piped.ops) ops.push_back(&op);
+          for (const ir::Operand* op : ops) {
+            if (Classify(*op, geo) != OpKind::RowScalar || !done.insert(op->tensor).second) continue;
+            const std::string T = CType(g_.tensors[op->tensor].elem);
+            o << ind << "const " << T << " rs" << op->tensor << " = t" << op->tensor << "["
+              << Offset(op->tensor, op->axes, coord) << "];\n";
+          }
+        }
+      };
+      o << "// statements";
+      for (int ci : passes[0]) o << " #" << ci;
+      o << ": split rows, partial folds (" << kPartBlock << " lanes per chunk of a row)\n";
+      o << "template <uint32_t V>\n__device__ __forceinline__ void " << part_fn << "(\n    " << sig << partSig
+        << ") {\n";
+      o << "  constexpr uint32_t CV = " << kChunkVecs << "u, PMAX = " << kMaxParts << "u;\n";
+      o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
+      o << "  const uint32_t VECS = C / V;\n";
+      o << "  const uint32_t P = min(PMAX, (VECS + CV - 1u) / CV);\n";
+      o << "  const uint32_t r = blockIdx.x / P, p = blockIdx.x - r * P;\n";
+      o << "  if (r >= " << rowExpr << ") return;  // the grid is rows x P: never taken\n";
+      o << "  const uint32_t L = (VECS + P - 1u) / P;\n";
+      o << "  const uint32_t lo = p * L, hi = min(lo + L, VECS);  // hi - lo > " << kPartBlock << "\n";
+      o << "  const uint64_t row_base = static_cast<uint64_t>(r) * C;\n";
+      o << "  const bool active = true;\n";
+      rowCoords("  ");
+      rowScalars("  ");
+      combs("  ");
+      for (int ci : passes[0]) {
+        const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+        o << "  " << T << " part" << ci << " = " << T << "(0);\n";
+      }
+      std::ostringstream b;
+      b << "  {\n    const uint32_t vc = lo + threadIdx.x;\n";
+      operands(b, 0, "    ", false, "vc", "");
+      work(b, 0, "    ", false, "vc", "true", "", true);
+      b << "  }\n  uint32_t v0 = lo + threadIdx.x + " << kPartBlock << "u;\n";
+      b << "  for (; v0 + " << 3 * kPartBlock << "u < hi; v0 += " << 4 * kPartBlock << "u) {\n";
+      for (uint32_t u = 0; u < 4; ++u)
+        b << "    const uint32_t vc_" << u << " = v0 + " << u * kPartBlock << "u;\n";
+      for (uint32_t u = 0; u < 4; ++u) operands(b, 0, "    ", false, "vc_" + std::to_string(u), "_" + std::to_string(u));
+      for (uint32_t u = 0; u < 4; ++u)
+        work(b, 0, "    ", false, "vc_" + std::to_string(u), "true", "_" + std::to_string(u), false);
+      b << "  }\n  for (; v0 < hi; v0 += " << kPartBlock << "u) {\n    const uint32_t vc = v0;\n";
+      operands(b, 0, "    ", false, "vc", "");
+      work(b, 0, "    ", false, "vc", "true", "", false);
+      b << "  }\n";
+      o << b.str();
+      for (int ci : passes[0]) {
+        const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+        o << "  part" << ci << " = tca::hip::seg_allreduce<64>(part" << ci << ", comb" << ci << ");\n";
+        o << "  __shared__ " << T << " red" << ci << "[" << kPartBlock / 64 << "];\n";
+        o << "  if ((threadIdx.x & 63u) == 0u) red" << ci << "[threadIdx.x >> 6] = part" << ci << ";\n";
+      }
+      o << "  __syncthreads();\n  if (threadIdx.x == 0u) {\n";
+      for (int ci : passes[0]) {
+        const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+        o << "    " << T << " acc" << ci << " = red" << ci << "[0];\n";
+        o << "    for (uint32_t w = 1; w < " << kPartBlock / 64 << "u; ++w) acc" << ci << " = comb" << ci << "(acc" << ci
+          << ", red" << ci << "[w]);\n";
+        o << "    p" << ci << "[static_cast<uint64_t>(r) * PMAX + p] = acc" << ci << ";\n";
+      }
+      o << "  }\n}\n";
+      // Merge: one wave per row.
+      o << "template <uint32_t V>\n__device__ __forceinline__ void " << merge_fn << "(\n    " << sig << partSig
+        << ") {\n";
+      o << "  constexpr uint32_t CV = " << kChunkVecs << "u, PMAX = " << kMaxParts << "u;\n";
+      o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
+      o << "  const uint32_t P = min(PMAX, (C / V + CV - 1u) / CV);\n";
+      o << "  const uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63u;\n";
+      o << "  if (r >= " << rowExpr << ") return;  // whole waves\n";
+      rowCoords("  ");
+      rowScalars("  ");
+      combs("  ");
+      for (int ci : passes[0]) {
+        const ir::Chain& c = g_.chains[ci];
+        const int st = c.store_tensor;
+        const std::string T = CType(g_.exprs[c.root.fn.body].type);
+        const std::string A = "m" + std::to_string(ci), H = "h" + std::to_string(ci);
+        o << "  " << T << " " << A << " = " << T << "(0);\n  bool " << H << " = false;\n";
+        o << "  for (uint32_t i = lane; i < P; i += 64u) {\n";
+        o << "    const " << T << " pv = p" << ci << "[static_cast<uint64_t>(r) * PMAX + i];\n";
+        o << "    " << A << " = " << H << " ? comb" << ci << "(" << A << ", pv) : pv;\n    " << H << " = true;\n  }\n";
+        o << "  " << A << " = tca::hip::wave_allreduce_present(" << A << ", " << H << ", comb" << ci << ");\n";
+        o << "  if (lane == 0u) {\n";
+        const ir::ReduceStage& rs = c.reduces[0];
+        ExprGen fg(g_, o, "    ", &counter_);
+        fg.Bind(rs.fn.params[0], fg.Gen(rs.init));
+        fg.Bind(rs.fn.params[1], A);
+        std::string val = fg.Gen(rs.fn.body);  // P >= 1: init applied once to the row's total
+        if (c.has_piped) {
+          ExprGen pg(g_, o, "    ", &counter_);
+          pg.Bind(c.piped.fn.params[0], val);
+          for (size_t k = 0; k < c.piped.ops.size(); ++k)
+            pg.Bind(c.piped.fn.params[k + 1], "rs" + std::to_string(c.piped.ops[k].tensor));
+          val = pg.Gen(c.piped.fn.body);
+        }
+        if (!isReg(st) || an_.hbm_local[st])
+          o << "    t" << st << "[" << Offset(st, c.store_axes, coord) << "] = " << val << ";\n";
+        o << "  }\n";
+      }
+      o << "}\n";
+    }
     // One kernel per (vector width, cached | streamed); launch guards on the
     // row length pick exactly one (C % 4 == 0: V 4; C % 4 == 2: V 2; odd:
     // V 1; then the row length in vectors).
@@ -1570,10 +1731,13 @@ class Emitter {
     const struct { uint32_t v, mod, rem; } widths[] = {{4, 4, 0}, {2, 4, 2}, {1, 2, 1}};
     const uint64_t cachedVecs = uint64_t{kBlock} * kCache;
     const std::string symbol = pk.symbol;
+    const std::string rowGuard =
+        geo.outer.size() == 1 ? g_.dims[geo.outer[0]].name : std::string();  // the split's row-count dim
     for (const auto& w : widths) {
       for (int cached = 1; cached >= 0; --cached) {
         const uint64_t lo = cached ? 0 : (cachedVecs + 1) * w.v;
         const uint64_t hi = cached ? cachedVecs * w.v : 0xffffffffull;
+        if (!cached && split && rowGuard.empty()) continue;  // a full reduction always splits
         PlanKernel vk = pk;
         vk.symbol = symbol + (cached ? "_c" : "_s") + std::to_string(w.v);
         vk.block = kBlock;
@@ -1581,6 +1745,7 @@ class Emitter {
         vk.grid.push_back(DimProduct(geo.outer) + "/pack");
         vk.when.push_back(cdim + " " + std::to_string(lo) + " " + std::to_string(hi) + " " + std::to_string(w.mod) +
                           " " + std::to_string(w.rem));
+        if (!cached && split) vk.when.push_back(rowGuard + " " + std::to_string(kSplitRows + 1) + " 4294967295 1 0");
         o << "extern \"C\" __global__ void __launch_bounds__(" << kBlock << ") " << vk.symbol << "(\n    " << sig
           << ") {\n";
         if (cached) {
@@ -1598,6 +1763,40 @@ class Emitter {
             << " lanes/row=runtime(<=" << kBlock << ") passes=" << passes.size() << " block=max(" << kMinBlock
             << ",lanes/row)";
         AddKernel(vk, Family::Stream, n.chains, det.str());
+      }
+      if (!split) continue;
+      // The split pair for this width: partial folds, then the merge.
+      const uint64_t lo = (cachedVecs + 1) * w.v;
+      std::string partArgs = args;
+      for (int ci : passes[0]) partArgs += ", p" + std::to_string(ci);
+      std::string partSig2;
+      for (int ci : passes[0]) {
+        const ir::Elem pe = g_.exprs[g_.chains[ci].root.fn.body].type;
+        partSig2 += ",\n    " + CType(pe) + "* __restrict__ p" + std::to_string(ci);
+      }
+      for (int merge = 0; merge <= 1; ++merge) {
+        PlanKernel sk = pk;
+        sk.symbol = symbol + (merge ? "_m" : "_p") + std::to_string(w.v);
+        sk.block = merge ? 256 : kPartBlock;
+        for (const auto& nm : part_names) sk.args.push_back("ptr " + nm);
+        if (merge) {
+          sk.grid.push_back(rowGuard.empty() ? std::string("1/1") : DimProduct(geo.outer) + "/4");
+        } else {
+          if (!rowGuard.empty()) sk.grid.push_back(DimProduct(geo.outer) + "/1");
+          sk.grid.push_back(cdim + "/" + std::to_string(uint64_t{kChunkVecs} * w.v) + ":" + std::to_string(kMaxParts));
+        }
+        sk.when.push_back(cdim + " " + std::to_string(lo) + " 4294967295 " + std::to_string(w.mod) + " " +
+                          std::to_string(w.rem));
+        if (!rowGuard.empty()) sk.when.push_back(rowGuard + " 0 " + std::to_string(kSplitRows) + " 1 0");
+        o << "extern \"C\" __global__ void __launch_bounds__(" << sk.block << ") " << sk.symbol << "(\n    " << sig
+          << partSig2 << ") {\n  " << (merge ? merge_fn : part_fn) << "<" << w.v << "u>(" << partArgs << ");\n}\n";
+        std::ostringstream det;
+        det << "row=runtime (" << cdim << " % " << w.mod << " == " << w.rem << ", >= " << lo
+            << (rowGuard.empty() ? std::string() : ", rows <= " + std::to_string(kSplitRows)) << ": split) vec=" << w.v
+            << (merge ? " merge: one wave per row over <= " + std::to_string(kMaxParts) + " partials"
+                      : " partial: " + std::to_string(kPartBlock) + " lanes per chunk of >= " +
+                            std::to_string(kChunkVecs / 2) + " vectors");
+        AddKernel(sk, Family::Stream, n.chains, det.str());
       }
     }
     o << "\n";
@@ -1639,6 +1838,7 @@ class Emitter {
     std::ostringstream p;
     p << "tca-plan 1\nprogram " << g_.name << "\n";
     for (const auto& d : g_.dims) p << "dim " << d.name << " " << d.extent << "\n";
+    for (const auto& d : extra_dims_) p << "dim " << d << "\n";
     for (size_t t = 0; t < g_.tensors.size(); ++t) {
       const ir::Tensor& tt = g_.tensors[t];
       std::string role;
@@ -1649,6 +1849,7 @@ class Emitter {
       for (int d : tt.dims) p << " " << g_.dims[d].name;
       p << "\n";
     }
+    for (const auto& t : extra_tensors_) p << "tensor " << t << "\n";
     for (const auto& s : g_.scalars) p << "scalar " << s.name << " " << ir::ElemName(s.elem) << "\n";
     for (const auto& k : plan_kernels_) {
       p << "kernel " << k.symbol << " " << k.block << " " << k.lds << " " << k.grid.size();
@@ -1666,6 +1867,8 @@ class Emitter {
   Options opts_;
   std::string prefix_;
   Analysis an_;
+  std::vector<std::string> extra_dims_;     // plan-only dims: "<name> <extent>"
+  std::vector<std::string> extra_tensors_;  // plan-only HBM locals: "<name> <dtype> local <rank> <dims...>"
   std::ostringstream src_;
   std::vector<PlanKernel> plan_kernels_;
   std::vector<KernelInfo> kernels_;

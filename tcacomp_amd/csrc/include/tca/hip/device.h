@@ -154,6 +154,22 @@ __device__ __forceinline__ T seg_allreduce_rt(T v, uint32_t seg, Op op) {
   }
 }
 
+// All-reduce over the wave of values that may be absent (`has` false: the
+// lane holds nothing). Every lane ends with the total of the present values
+// and the OR of the flags. Every lane of the wave must call it; `op` must be
+// associative and commutative.
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_allreduce_present(T v, bool& has, Op op) {
+  for (int off = 1; off < 64; off <<= 1) {
+    const T o = xor_lanes(v, off);
+    const bool oh = __shfl_xor(static_cast<int>(has), off, 64) != 0;
+    if (has && oh) v = op(v, o);
+    else if (oh) v = o;
+    has = has || oh;
+  }
+  return v;
+}
+
 // Lanes per row of the packed row kernels, as log2: the smallest power of
 // two 2^ls <= 2^log2_block with per_lane << ls >= vecs (no lane holds more
 // than per_lane vectors unless the row needs more than the whole block).

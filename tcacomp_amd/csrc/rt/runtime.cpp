@@ -403,11 +403,19 @@ int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tens
     return fail(TCA_ERR_INVALID, "program %s takes %zu scalar(s), got %u", pl.name.c_str(), pl.scalars.size(), n_scalars);
   if (n_scalars > 0 && scalars == nullptr) return fail(TCA_ERR_INVALID, "program_launch: null scalars");
 
-  // HBM locals: one workspace, each local at a 256-byte aligned offset.
+  // HBM locals: one workspace, each local at a 256-byte aligned offset; only
+  // the locals some kernel selected for these dims takes (a variant's
+  // scratch is sized for the dims it runs on).
+  std::vector<bool> used(pl.tensors.size(), false);
+  for (const auto& k : pl.kernels) {
+    if (!tca::plan::Selected(k, dims)) continue;
+    for (const auto& a : k.args)
+      if (a.kind == tca::plan::ArgKind::Ptr) used[a.index] = true;
+  }
   std::vector<size_t> local_off(pl.tensors.size(), 0);
   size_t ws_bytes = 0;
   for (size_t t = 0; t < pl.tensors.size(); ++t) {
-    if (pl.tensors[t].role != tca::plan::Role::Local) continue;
+    if (pl.tensors[t].role != tca::plan::Role::Local || !used[t]) continue;
     local_off[t] = ws_bytes;
     ws_bytes += (tca::plan::TensorBytes(pl, t, dims) + 255u) & ~static_cast<size_t>(255u);
   }

@@ -161,6 +161,20 @@ def layernorm_rstd(cols=1024):
     return b.Build()
 
 
+def vec_sum_max():
+    """Full reductions: sum and max of a vector x [N] into two rank-0
+    outputs (no row axis: the streaming family's split rows over the whole
+    GPU)."""
+    b = NewBuilder("vec_sum_max")
+    N = b.Dim("N", 0)
+    x = b.Tensor("x", TF32, N)
+    s = b.Tensor("sum", TF32)
+    m = b.Tensor("max", TF32)
+    b.Stmt().Iter(N).Map([At(x, N)], lambda v: v).As(N).Reduce(b.Float32(0), _sum(b)).Store(s)
+    b.Stmt().Iter(N).Map([At(x, N)], lambda v: v).As(N).Reduce(_neg_inf(b), lambda acc, v: Call("fmaxf", acc, v)).Store(m)
+    return b.Build()
+
+
 def row_stats_u32(cols=1000):
     """Integer row reductions over u32 [R, C]: wrapping sum, xor and umax
     (the monoid combiners of the row families on a 32-bit integer type)."""
@@ -462,6 +476,7 @@ CONFIG_PROGRAMS = {
     "row_sum_max_dyn": lambda: row_sum_max(0),
     "softmax_dyn": lambda: softmax(0),
     "layernorm_dyn": lambda: layernorm(0),
+    "vec_sum_max": vec_sum_max,
     # a per-row chain fused between the reductions and the row map
     "layernorm_rstd_1024": lambda: layernorm_rstd(1024),
     "layernorm_rstd_dyn": lambda: layernorm_rstd(0),

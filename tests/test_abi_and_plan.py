@@ -82,24 +82,46 @@ def test_launch_guards():
     assert rc == _lib.TCA_ERR_INVALID and "before any kernel" in _lib.last_error()
 
 
-@pytest.mark.parametrize("C,variant", [(0, "c4"), (64, "c4"), (4096, "c4"), (4100, "c4"), (16384, "c4"),
-                                       (16388, "s4"), (6, "c2"), (2046, "c2"), (8190, "c2"), (8194, "s2"),
-                                       (1, "c1"), (1023, "c1"), (4095, "c1"), (4097, "s1")])
-def test_stream_variant_selection(C, variant):
-    """The guards of the streaming row family partition the row length: one
-    kernel per (vector width, cached | streamed) and exactly one runs."""
+@pytest.mark.parametrize("R,C,variants", [
+    (3, 0, ["c4"]), (3, 64, ["c4"]), (3, 4096, ["c4"]), (3, 4100, ["c4"]), (3, 16384, ["c4"]),
+    (300, 16388, ["s4"]), (3, 6, ["c2"]), (3, 2046, ["c2"]), (3, 8190, ["c2"]), (300, 8194, ["s2"]),
+    (3, 1, ["c1"]), (3, 1023, ["c1"]), (3, 4095, ["c1"]), (300, 4097, ["s1"]),
+    # few long rows: the split pair (partial folds, then the merge), in launch order
+    (3, 16388, ["p4", "m4"]), (255, 8194, ["p2", "m2"]), (1, 4097, ["p1", "m1"]), (256, 16388, ["s4"])])
+def test_stream_variant_selection(R, C, variants):
+    """The guards of the streaming row family partition (rows, row length):
+    one kernel per (vector width, cached | streamed), or for <= 255 long rows
+    a split pair, and exactly that runs."""
     e = programs.CONFIG_PROGRAMS["row_sum_max_dyn"]().emit()
     rc, h = parse(e.plan)
     assert rc == 0, _lib.last_error()
     P = 0x1000
-    arr = compiler._descriptors([TensorDesc(P, (3, C), 0), TensorDesc(P, (3,), 0), TensorDesc(P, (3,), 0)])
+    arr = compiler._descriptors([TensorDesc(P, (R, C), 0), TensorDesc(P, (R,), 0), TensorDesc(P, (R,), 0)])
     syms = e.kernel_symbols()
     out = (ctypes.c_uint8 * len(syms))()
     grids = (ctypes.c_uint64 * len(syms))()
     assert _lib.lib().tca_program_selected(h, arr, 3, None, 0, out, grids, None, len(syms)) == 0, _lib.last_error()
     chosen = [s for s, f in zip(syms, out) if f]
-    assert chosen == ["tca_row_sum_max_dyn_k0_" + variant]
-    assert [g for g, f in zip(grids, out) if not f] == [0] * (len(syms) - 1)
+    assert chosen == ["tca_row_sum_max_dyn_k0_" + v for v in variants]
+    assert [g for g, f in zip(grids, out) if not f] == [0] * (len(syms) - len(variants))
+
+
+@pytest.mark.parametrize("R,C,part_grid,merge_grid", [(1, 16388, 2, 1), (3, 10**6, 3 * 62, 1),
+                                                      (255, 8 * 10**6, 255 * 489, 64), (1, 4 * 10**8, 512, 1)])
+def test_split_geometry(R, C, part_grid, merge_grid):
+    """Split rows: P = min(512, ceil(C / (4096 V))) chunks per row, one
+    1024-lane block per chunk; the merge takes one wave per row, 4 per block."""
+    e = programs.CONFIG_PROGRAMS["row_sum_max_dyn"]().emit()
+    _, h = parse(e.plan)
+    P = 0x1000
+    arr = compiler._descriptors([TensorDesc(P, (R, C), 0), TensorDesc(P, (R,), 0), TensorDesc(P, (R,), 0)])
+    syms = e.kernel_symbols()
+    out = (ctypes.c_uint8 * len(syms))()
+    grids = (ctypes.c_uint64 * len(syms))()
+    blocks = (ctypes.c_uint32 * len(syms))()
+    assert _lib.lib().tca_program_selected(h, arr, 3, None, 0, out, grids, blocks, len(syms)) == 0, _lib.last_error()
+    sel = [(s, g, b) for s, f, g, b in zip(syms, out, grids, blocks) if f]
+    assert [g for _, g, _ in sel] == [part_grid, merge_grid] and [b for _, _, b in sel] == [1024, 256], sel
 
 
 @pytest.mark.parametrize("R,C,grid,block", [
@@ -246,7 +268,7 @@ def test_program_launch_without_module_is_refused():
 EXPECTED_FAMILIES = {
     "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"],
     "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"], "gemm_bf16": ["gemm"],
-    "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 6, "softmax_dyn": ["stream"] * 6,
+    "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 12, "softmax_dyn": ["stream"] * 6,
     "layernorm_dyn": ["stream"] * 6, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 6,
 }
 

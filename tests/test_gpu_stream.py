@@ -85,6 +85,50 @@ def test_stream_layernorm(gpu, R, C):
     assert err.max() <= reduce_tol(C) * (np.abs(want).max() + 1.0), "layernorm err %g" % err.max()
 
 
+@pytest.mark.parametrize("R,C", [(1, 16388), (3, 1_000_000), (7, 4097), (255, 8194), (2, 4_000_002),
+                                 (1, 50_000_000)])
+def test_split_rows(gpu, R, C):
+    """Few long rows: each row split over many blocks (partial folds into an
+    HBM scratch, then a merge); every vector width."""
+    _say("split C2", R, C)
+    x = inputs.normal((R, C), 1.0, 7)
+    ws, wm = oracle.row_sum_max(x)
+    s, m = out_dev((R,), gpu), out_dev((R,), gpu)
+    run(compiled("row_sum_max_dyn"), [to_dev(x, gpu), s, m])
+    gs, gm = host(s), host(m)
+    assert np.array_equal(gm.view(np.uint32), wm.view(np.uint32)), "row max is not bit-identical"
+    assert_reduce_close(gs, ws, np.sqrt((x.astype(np.float64) ** 2).sum(1)), C, "split row sum")
+
+
+@pytest.mark.parametrize("N", [16388, 1_000_004, 64 * 1024 * 1024 + 2])
+def test_full_reduction(gpu, N):
+    """sum and max of a whole vector into rank-0 outputs."""
+    _say("full reduction", N)
+    x = inputs.normal((1, N), 1.0, 9)
+    ws, wm = oracle.row_sum_max(x)
+    s, m = out_dev((), gpu), out_dev((), gpu)
+    run(compiled("vec_sum_max"), [to_dev(x.reshape(N), gpu), s, m])
+    assert np.float32(host(m)).view(np.uint32) == wm.view(np.uint32)[0]
+    assert_reduce_close(np.array([host(s)]), ws, np.array([np.sqrt((x.astype(np.float64) ** 2).sum())]), N,
+                        "full sum")
+
+
+def test_split_integer_rows(gpu):
+    """The split path on u32 monoids: exact."""
+    from tcacomp_amd.compiler import TensorDesc
+    import torch
+    R, C = 2, 1_000_000
+    x = np.random.default_rng(11).integers(0, 2**32, size=(R, C), dtype=np.uint64).astype(np.uint32)
+    xt = torch.from_numpy(x.view(np.int32)).to(gpu)
+    outs = [torch.zeros(R, dtype=torch.int32, device=gpu) for _ in range(3)]
+    run(compiled("row_stats_u32_dyn"), [TensorDesc(xt.data_ptr(), (R, C), 4)] +
+        [TensorDesc(o.data_ptr(), (R,), 4) for o in outs])
+    got = [o.cpu().numpy().view(np.uint32) for o in outs]
+    assert np.array_equal(got[0], (x.astype(np.uint64).sum(1) % (1 << 32)).astype(np.uint32))
+    assert np.array_equal(got[1], np.bitwise_xor.reduce(x, axis=1))
+    assert np.array_equal(got[2], x.max(1))
+
+
 def test_stream_empty_grid(gpu):
     s, m = out_dev((0,), gpu), out_dev((0,), gpu)
     run(compiled("row_sum_max_dyn"), [to_dev(np.zeros((0, 5), np.float32), gpu), s, m])  # no workgroups launched
