@@ -38,7 +38,12 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+// The HIP error becomes this library's status and message; HIP's per-thread
+// last-error slot is cleared, so another user of HIP in the process (a
+// framework checking hipGetLastError after its own launches) does not
+// inherit a failure that was already reported here.
 int hip_fail(hipError_t e, const char* what) {
+  (void)hipGetLastError();
   return fail(TCA_ERR_HIP, "%s failed: %s (%d)", what, hipGetErrorString(e), static_cast<int>(e));
 }
 

@@ -152,6 +152,11 @@ def test_error_paths(rt):
     p = ctypes.c_void_p()
     rc = rt.tca_rt_malloc(ctypes.byref(p), 1 << 62)  # more than the device holds
     assert rc != 0 and _lib.last_error()
+    # the failure is reported here and not left in HIP's last-error slot for
+    # the next HIP user in the process (torch checks it after its launches)
+    import torch
+    torch.full((16,), 1.0, device="cuda:0")
+    torch.cuda.synchronize()
     # a program launch whose tensors disagree with the plan
     prog = compiled("scale_relu_map")
     h = prog.load()
