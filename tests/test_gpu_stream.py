@@ -113,6 +113,21 @@ def test_full_reduction(gpu, N):
                         "full sum")
 
 
+def test_split_rows_repeated_shapes(gpu):
+    """Split rows keep their partials in the program's workspace, laid out per
+    launch from the row count: launches in a row with different row counts
+    (and so different layouts, the workspace reused or regrown) all stay
+    exact on the max and within tolerance on the sum."""
+    prog = compiled("row_sum_max_dyn")
+    for R, C in [(3, 100_000), (3, 100_000), (2, 300_000), (5, 50_000), (1, 200_004), (3, 100_000)]:
+        x = inputs.normal((R, C), 1.0, R + C)
+        ws, wm = oracle.row_sum_max(x)
+        s, m = out_dev((R,), gpu), out_dev((R,), gpu)
+        run(prog, [to_dev(x, gpu), s, m])
+        assert np.array_equal(host(m).view(np.uint32), wm.view(np.uint32)), (R, C)
+        assert_reduce_close(host(s), ws, np.sqrt((x.astype(np.float64) ** 2).sum(1)), C, "repeated split")
+
+
 def test_split_integer_rows(gpu):
     """The split path on u32 monoids: exact."""
     from tcacomp_amd.compiler import TensorDesc
