@@ -44,6 +44,10 @@ CONFIGS = {
     # not configurations; shown because one workgroup per row would idle the GPU
     "c2v": ("vec_sum_max", "sum+max of one f32 vector [67108864] (split rows, full reduction)"),
     "c2r": ("row_sum_max_dyn", "row sum+max f32 [16,4194304] (split rows)"),
+    # C2's reductions over narrow element types (16-byte vectors of 8 bf16 /
+    # 16 u8 elements): not configurations, the same family on other dtypes
+    "c2h": ("row_sum_bf16_dyn", "row sum+max bf16 -> f32 [8192,16384] (streaming family)"),
+    "c2u": ("row_sum_u8_dyn", "row sum u8 -> u32 -> f32 scaled [8192,32768] (streaming family)"),
     # not a configuration: the plain copy used to calibrate rocprof counters
     "copy": ("copy_f32", "copy f32 [8192,8192] (counter calibration)"),
 }
@@ -83,6 +87,21 @@ def _setup(key, dev):
         else:
             make = lambda i: [dev_f32(x), torch.empty(R, device=dev), torch.empty(R, device=dev)]  # noqa: E731
         scalars = []
+        work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = None
+    elif key in ("c2h", "c2u"):
+        R, C = (8192, 16384) if key == "c2h" else (8192, 32768)
+        if key == "c2h":
+            xd = torch.from_numpy(inputs.normal((R, C), 1.0, 0)).to(dev).to(torch.bfloat16)
+            algo = R * C * 2 + 2 * R * 4
+            make = lambda i: [xd.clone(), torch.empty(R, device=dev), torch.empty(R, device=dev)]  # noqa: E731
+            scalars = []
+        else:
+            xd = torch.from_numpy(np.random.default_rng(0).integers(0, 256, size=(R, C), dtype=np.uint8)).to(dev)
+            algo = R * C + R * 4
+            make = lambda i: [xd.clone(), torch.empty(R, device=dev)]  # noqa: E731
+            scalars = [0.37]
+        per_set = algo
         work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
         cpu = None
     elif key == "copy":
@@ -250,7 +269,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c2h,c2u")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
                     help="untimed launches per config before the warmup steps, in wall-clock ms")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")

@@ -430,6 +430,30 @@ RowGeom StreamCheck(const Graph& g, const std::vector<int>& chains) {
   return geo;
 }
 
+// Integer partials of 32 bits get a fold fence after each vector (the
+// compiler would otherwise reassociate the adds of all vectors in flight).
+bool FoldFenced(ir::Elem e) { return ir::IsInt(e) && ir::ElemBytes(e) == 4; }
+
+// Elements per vector of a row nest: 16 bytes of its widest row-shaped
+// tensor (row tiles and column vectors it reads, row tiles it writes,
+// register locals included), so the widest moves in 16-byte vectors and the
+// narrower ones in shorter vectors of the same element count (a bf16 row
+// summed into f32: 8 elements, 16 bytes per load; a bf16 row mapped into an
+// f32 tile: 4 elements, 8 + 16 bytes).
+uint32_t RowVecMax(const Graph& g, const std::vector<int>& chains, const RowGeom& geo) {
+  size_t widest = 1;
+  for (int ci : chains) {
+    const ir::Chain& c = g.chains[ci];
+    if (IsRowScalarChain(c, geo)) continue;
+    for (const auto& o : c.root.ops) {
+      const OpKind k = Classify(o, geo);
+      if (k == OpKind::RowTile || k == OpKind::ColVec) widest = std::max(widest, ir::ElemBytes(g.tensors[o.tensor].elem));
+    }
+    if (c.reduces.empty()) widest = std::max(widest, ir::ElemBytes(g.tensors[c.store_tensor].elem));
+  }
+  return static_cast<uint32_t>(std::max<size_t>(1, 16 / widest));
+}
+
 RowGeom RowCheck(const Graph& g, const std::vector<int>& chains, uint32_t nv_target) {
   RowGeom geo;
   auto no = [&](const std::string& w) {
@@ -440,7 +464,8 @@ RowGeom RowCheck(const Graph& g, const std::vector<int>& chains, uint32_t nv_tar
   if (!RowShape(g, chains, false, &geo)) return geo;
   if (g.dims[geo.col].extent == 0) return no("row axis @" + g.dims[geo.col].name + " has a dynamic extent");
   geo.C = static_cast<uint32_t>(g.dims[geo.col].extent);
-  geo.V =(geo.C % 4 == 0) ? 4 : (geo.C % 2 == 0 ? 2 : 1);
+  geo.V = RowVecMax(g, chains, geo);  // then the widest power of two dividing the row
+  while (geo.C % geo.V != 0) geo.V /= 2;
   geo.vecs = geo.C / geo.V;
   uint32_t tpr = 1;
   while (tpr * 2 <= geo.vecs / nv_target && tpr * 2 <= 1024) tpr *= 2;
@@ -705,7 +730,19 @@ class Emitter {
     const ir::Chain& c = g_.chains[n.chains[0]];
     PlanKernel pk;
     pk.symbol = Sym(g_, prefix_, ni);
-    const uint32_t kVec = 4, kUnroll = EwUnroll(), kBlock = 256, kPerBlock = kVec * kUnroll * kBlock;
+    // Elements per vector: 16 bytes of the widest tensor moved in vectors
+    // (the store and the operands aligned with it).
+    size_t widest = ir::ElemBytes(g_.tensors[c.store_tensor].elem);
+    {
+      const std::vector<int> storeAxes = DropUnit(g_, c.store_axes);
+      for (const auto& op : c.root.ops)
+        if (DropUnit(g_, op.axes) == storeAxes) widest = std::max(widest, ir::ElemBytes(g_.tensors[op.tensor].elem));
+      if (c.has_piped)
+        for (const auto& op : c.piped.ops)
+          if (DropUnit(g_, op.axes) == storeAxes) widest = std::max(widest, ir::ElemBytes(g_.tensors[op.tensor].elem));
+    }
+    const uint32_t kVec = static_cast<uint32_t>(std::max<size_t>(1, 16 / widest)), kUnroll = EwUnroll(), kBlock = 256,
+                   kPerBlock = kVec * kUnroll * kBlock;
     pk.block = kBlock;
     pk.grid.push_back(DimProduct(c.store_axes) + "/" + std::to_string(kPerBlock));
     const std::string sig = Signature(n, &pk);
@@ -805,7 +842,7 @@ class Emitter {
     }
     o << "    }\n";
     o << "#pragma unroll\n    for (uint32_t u = 0; u < " << kUnroll << "u; ++u) {\n";
-    o << "      tca::hip::vec<" << CType(st.elem) << ", " << kVec << "> out;\n";
+    o << "      tca::hip::vec<" << CType(st.elem) << ", " << kVec << "> out{};\n";
     o << "#pragma unroll\n      for (uint32_t q = 0; q < " << kVec << "u; ++q) {\n";
     o << "        const uint64_t e = base + u * " << kVec * kBlock << "u + q;\n";
     {
@@ -814,7 +851,7 @@ class Emitter {
         return std::string(piped ? "p" : "a") + std::to_string(k) + "[u][q]";
       });
       o << bodyS.str();
-      o << "        out[q] = " << val << ";\n";
+      o << "        out.set(q, " << val << ");\n";
     }
     o << "      }\n";
     o << "      tca::hip::store_vec_nt<" << CType(st.elem) << ", " << kVec << ">(t" << c.store_tensor
@@ -835,7 +872,8 @@ class Emitter {
       o << "        t" << c.store_tensor << "[e] = " << val << ";\n";
     }
     o << "      }\n    }\n  }\n}\n\n";
-    AddKernel(pk, Family::Elementwise, n.chains, "vec=4 unroll=" + std::to_string(kUnroll) + " block=256");
+    AddKernel(pk, Family::Elementwise, n.chains,
+              "vec=" + std::to_string(kVec) + " unroll=" + std::to_string(kUnroll) + " block=256");
     return true;
   }
 
@@ -1016,7 +1054,7 @@ class Emitter {
       o << "#pragma unroll\n  for (uint32_t j = 0; j < NV; ++j) {\n";
       o << "    if (active && (j + 1u < NV || tail_ok)) x" << t << "[j] = tca::hip::load_vec_nt<" << T << ", V>(t" << t
         << " + row_base + (j * TPR + lane) * V);\n";
-      o << "    else for (uint32_t q = 0; q < V; ++q) x" << t << "[j][q] = " << T << "(0);\n  }\n";
+      o << "    else x" << t << "[j] = tca::hip::vec<" << T << ", V>{};\n  }\n";
     }
     for (int t : cols) {
       const std::string T = CType(g_.tensors[t].elem);
@@ -1024,7 +1062,7 @@ class Emitter {
       o << "#pragma unroll\n  for (uint32_t j = 0; j < NV; ++j) {\n";
       o << "    if (j + 1u < NV || tail_ok) x" << t << "[j] = tca::hip::load_vec<" << T << ", V>(t" << t
         << " + (j * TPR + lane) * V);\n";
-      o << "    else for (uint32_t q = 0; q < V; ++q) x" << t << "[j][q] = " << T << "(0);\n  }\n";
+      o << "    else x" << t << "[j] = tca::hip::vec<" << T << ", V>{};\n  }\n";
     }
     // Row-scalar value of operand `op` (memory or register local).
     std::map<int, std::string> regScalar;  // tensor produced in this nest -> register variable
@@ -1149,7 +1187,9 @@ class Emitter {
         std::string folded = rg2.Gen(c.reduces[0].fn.body);
         o << "      if (j == 0u && q == 0u) part" << ci << " = " << v << ";\n";
         o << "      else {\n" << cs.str() << "        part" << ci << " = " << folded << ";\n      }\n";
-        o << "    }\n  }\n";
+        o << "    }\n";
+        if (FoldFenced(g_.exprs[c.root.fn.body].type)) o << "    tca::hip::fold_fence(part" << ci << ");\n";
+        o << "  }\n";
         group.push_back(ci);
         groupOut.insert(c.store_tensor);
       } else {
@@ -1160,12 +1200,12 @@ class Emitter {
         const bool reg = true;  // later chains of the nest read the register copy
         if (reg) o << "  tca::hip::vec<" << T << ", V> x" << st << "[NV];\n";
         o << "#pragma unroll\n  for (uint32_t j = 0; j < NV; ++j) {\n";
-        o << "    tca::hip::vec<" << T << ", V> outv;\n";
+        o << "    tca::hip::vec<" << T << ", V> outv{};\n";
         o << "#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) {\n";
         std::ostringstream bs;
         std::string v = elemValue(bs, "      ", c);
         o << bs.str();
-        o << "      outv[q] = " << v << ";\n    }\n";
+        o << "      outv.set(q, " << v << ");\n    }\n";
         if (reg) o << "    x" << st << "[j] = outv;\n";
         if (!isReg(st) || an_.hbm_local[st]) {  // outputs and locals other nests read
           o << "    if (active && (j + 1u < NV || tail_ok)) tca::hip::store_vec_nt<" << T << ", V>(t" << st
@@ -1197,8 +1237,9 @@ class Emitter {
   }
 
   // S: the row nests of family R with a row length known only at run time
-  // (or too long for registers). The row is read in 16-byte vectors (4
-  // elements when the length allows it, 2 or 1 otherwise) by S lanes, S
+  // (or too long for registers). The row is read in 16-byte vectors (of
+  // its widest row-shaped tensor: 4 f32, 8 bf16, 16 u8 elements, when the
+  // length allows it; halved down to 1 otherwise) by S lanes, S
   // chosen at run time as the smallest power of two <= the block that
   // leaves no lane more than 4 vectors, so short rows pack many rows per
   // block and long ones spread over up to sixteen waves. Rows of <= 1024 x 4
@@ -1421,15 +1462,18 @@ class Emitter {
             b << ind << "  " << P << " = " << ok << " ? " << folded << " : " << P << ";\n";
         }
         b << ind << "}\n";
+        for (int ci : passes[p])
+          if (FoldFenced(g_.exprs[g_.chains[ci].root.fn.body].type))
+            b << ind << "tca::hip::fold_fence(part" << ci << ");\n";
         return;
       }
       const int st = c0.store_tensor;
       const std::string T = CType(g_.tensors[st].elem);
-      b << ind << "tca::hip::vec<" << T << ", V> outv" << sfx << ";\n";
+      b << ind << "tca::hip::vec<" << T << ", V> outv" << sfx << "{};\n";
       b << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) {\n";
       std::ostringstream es;
       const std::string ev = elemValue(es, ind + "  ", c0, sfx);
-      b << es.str() << ind << "  outv" << sfx << "[q] = " << ev << ";\n" << ind << "}\n";
+      b << es.str() << ind << "  outv" << sfx << ".set(q, " << ev << ");\n" << ind << "}\n";
       if (!isReg(st) || an_.hbm_local[st]) {
         const bool again = tiles.count(st) > 0 && !cached;
         b << ind << "if (active" << (ok == "true" ? std::string() : " && " + ok) << ") tca::hip::"
@@ -1724,11 +1768,21 @@ class Emitter {
       o << "}\n";
     }
     // One kernel per (vector width, cached | streamed); launch guards on the
-    // row length pick exactly one (C % 4 == 0: V 4; C % 4 == 2: V 2; odd:
-    // V 1; then the row length in vectors).
+    // row length pick exactly one: the widest width W (16 bytes of the
+    // widest row-shaped tensor) for C % W == 0, then each smaller power of
+    // two v for C % 2v == v (f32: C % 4 == 0: V 4; C % 4 == 2: V 2; odd:
+    // V 1), then the row length in vectors.
     const std::string args = CallArgs(n);
     const std::string cdim = g_.dims[geo.col].name;
-    const struct { uint32_t v, mod, rem; } widths[] = {{4, 4, 0}, {2, 4, 2}, {1, 2, 1}};
+    struct Width {
+      uint32_t v, mod, rem;
+    };
+    std::vector<Width> widths;
+    {
+      const uint32_t vmax = RowVecMax(g_, n.chains, geo);
+      widths.push_back({vmax, vmax, 0});
+      for (uint32_t v = vmax / 2; v >= 1; v /= 2) widths.push_back({v, 2 * v, v});
+    }
     const uint64_t cachedVecs = uint64_t{kBlock} * kCache;
     const std::string symbol = pk.symbol;
     const std::string rowGuard =

@@ -106,6 +106,35 @@ def test_stream_variant_selection(R, C, variants):
     assert [g for g, f in zip(grids, out) if not f] == [0] * (len(syms) - len(variants))
 
 
+@pytest.mark.parametrize("prog,dtype,R,C,variants", [
+    # bf16 rows summed into f32: 8-element (16-byte) vectors, halved by the row length's residue
+    ("row_sum_bf16_dyn", 2, 3, 1000, ["c8"]), ("row_sum_bf16_dyn", 2, 3, 32768, ["c8"]),
+    ("row_sum_bf16_dyn", 2, 300, 32776, ["s8"]), ("row_sum_bf16_dyn", 2, 3, 32776, ["p8", "m8"]),
+    ("row_sum_bf16_dyn", 2, 3, 12, ["c4"]), ("row_sum_bf16_dyn", 2, 300, 16388, ["s4"]),
+    ("row_sum_bf16_dyn", 2, 3, 6, ["c2"]), ("row_sum_bf16_dyn", 2, 3, 5, ["c1"]),
+    # u8 rows: 16-element vectors
+    ("row_sum_u8_dyn", 7, 3, 4096, ["c16"]), ("row_sum_u8_dyn", 7, 300, 65552, ["s16"]),
+    ("row_sum_u8_dyn", 7, 1, 65552, ["p16", "m16"]), ("row_sum_u8_dyn", 7, 3, 1000, ["c8"]),
+    ("row_sum_u8_dyn", 7, 3, 20, ["c4"]), ("row_sum_u8_dyn", 7, 3, 6, ["c2"]), ("row_sum_u8_dyn", 7, 3, 0, ["c16"]),
+    ("row_sum_u8_dyn", 7, 300, 4097, ["s1"])])
+def test_narrow_stream_variant_selection(prog, dtype, R, C, variants):
+    """Narrow element types: the widest width moves 16 bytes of the row's
+    element type per load (8 bf16, 16 u8); the guards still partition the
+    row lengths, one kernel (or one split pair) per launch."""
+    e = programs.CONFIG_PROGRAMS[prog]().emit()
+    rc, h = parse(e.plan)
+    assert rc == 0, _lib.last_error()
+    P = 0x1000
+    nout = 2 if prog.startswith("row_sum_bf16") else 1
+    arr = compiler._descriptors([TensorDesc(P if R * C else 0, (R, C), dtype)] +
+                                [TensorDesc(P, (R,), 0)] * nout)
+    syms = e.kernel_symbols()
+    out = (ctypes.c_uint8 * len(syms))()
+    assert _lib.lib().tca_program_selected(h, arr, 1 + nout, None, 0, out, None, None, len(syms)) == 0, \
+        _lib.last_error()
+    assert [s for s, f in zip(syms, out) if f] == ["tca_%s_k0_%s" % (prog, v) for v in variants]
+
+
 @pytest.mark.parametrize("R,C,part_grid,merge_grid", [(1, 16388, 2, 1), (3, 10**6, 3 * 62, 1),
                                                       (255, 8 * 10**6, 255 * 489, 64), (1, 4 * 10**8, 512, 1)])
 def test_split_geometry(R, C, part_grid, merge_grid):
@@ -270,6 +299,8 @@ EXPECTED_FAMILIES = {
     "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"], "gemm_bf16": ["gemm"],
     "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 12, "softmax_dyn": ["stream"] * 6,
     "layernorm_dyn": ["stream"] * 6, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 6,
+    # narrow rows: one more width per halving of the element size (8 bf16, 16 u8 elements per vector)
+    "row_sum_bf16_dyn": ["stream"] * 16, "row_sum_u8_dyn": ["stream"] * 20, "row_stats_u32_dyn": ["stream"] * 12,
 }
 
 

@@ -39,12 +39,17 @@ def _u32_out(shape, dev):
 
 
 STATIC_C = 1000
-DYN_C = [0, 1, 3, 6, 1000, 4096, 5003, 20000]
+# Row lengths covering every vector width of each element type (u8: 16, 8,
+# 4, 2, 1 elements; bf16: 8, 4, 2, 1; u32: 4, 2, 1), register-cached and
+# streamed rows, and (<= 255 rows) split rows.
+DYN_C = [0, 1, 3, 6, 12, 20, 1000, 4096, 5003, 20000, 40004, 65544, 70000, 140000]
+LONG_C = [40004, 70000]  # also with > 255 rows: streamed without a split
 
 
 def _cases():
     out = [("_1000", STATIC_C, 37)]
     out += [("_dyn", c, r) for c in DYN_C for r in (1, 37)]
+    out += [("_dyn", c, 300) for c in LONG_C]
     return out
 
 
