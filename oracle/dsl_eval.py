@@ -1,0 +1,207 @@
+"""TEST INFRASTRUCTURE ONLY: CPU evaluation of the random row programs of
+tcacomp_amd/randprog.py (the checker of tests/test_gpu_random.py, never the
+thing measured or shipped; only tests/ may import it).
+
+The DSL semantics restated here, per statement:
+- a chain's root map is evaluated per element of its iteration space
+  (pkg/chain.go:360-420), operands bound by subscript (pkg/chain.go:153-176);
+- Reduce drops the last live axis (pkg/chain.go:262) and folds
+  acc = fn(acc, v) starting from init, once per output; an empty reduce
+  yields init (runtime/tca/reducer.h:36-57; design/tca.md:299, :711);
+- the piped map after a reduce sees the reduced value first, then its own
+  operands, over the remaining axes (pkg/chain.go:301-316);
+- stores write the chain's result at its store subscripts
+  (pkg/chain.go:326-350); locals are read back by later chains.
+Scalar arithmetic is IEEE float32 (numpy's float32 ufuncs are correctly
+rounded, as the device's basic operations are under -ffp-contract=off) or
+wrapping uint32.
+
+The fold order of a float sum is not reproduced: evaluate() reports
+whether every sum is exact (integer-valued terms, sum of magnitudes below
+2^24 per output), in which case every order gives the same float32 and the
+device must match it exactly. evaluate_scalar() is a brute-force element
+loop in the reference's sequential fold order, used to pin evaluate() on
+tiny inputs.
+"""
+import numpy as np
+
+EXACT_LIMIT = float(1 << 24)
+
+
+def _f32(v):
+    return np.float32(v)
+
+
+def _binop(op, elem, a, b):
+    if op == "add":
+        return a + b
+    if op == "sub":
+        return a - b
+    if op == "mul":
+        return a * b
+    if op == "max":
+        return np.fmax(a, b) if elem == "f32" else np.maximum(a, b)
+    if op == "min":
+        return np.fmin(a, b) if elem == "f32" else np.minimum(a, b)
+    if op == "div1":
+        return a / (np.abs(b) + _f32(1.0))
+    if op == "xor":
+        return a ^ b
+    if op == "and":
+        return a & b
+    if op == "or":
+        return a | b
+    raise ValueError(op)
+
+
+def _eval(e, env, elem):
+    k = e[0]
+    if k == "leaf":
+        return env[e[1]]
+    if k == "const":
+        return _f32(e[1]) if elem == "f32" else np.uint32(e[1])
+    a = [_eval(x, env, elem) for x in e[1:]]
+    if k == "sel":
+        return np.where(a[0] < a[1], a[2], a[3])
+    if k == "neg":
+        return -a[0]
+    if k == "abs":
+        return np.abs(a[0])
+    return _binop(k, elem, a[0], a[1])
+
+
+def _init(elem, comb):
+    if elem == "f32":
+        return {"sum": _f32(0.0), "max": _f32(-np.inf), "min": _f32(np.inf)}[comb]
+    return np.uint32({"sum": 0, "xor": 0, "max": 0, "min": 0xFFFFFFFF}[comb])
+
+
+def _reduce(elem, comb, terms):
+    """Reduced values of `terms` over the last axis, and whether a float sum
+    is exact (order-independent)."""
+    init = _init(elem, comb)
+    if elem == "f32":
+        if comb == "sum":
+            t = terms.astype(np.float64)
+            exact = bool(np.all(np.isfinite(t)) and np.all(np.floor(t) == t) and
+                         np.all(np.abs(t).sum(axis=-1) < EXACT_LIMIT))
+            return (init + t.sum(axis=-1)).astype(np.float32), exact
+        f = np.fmax if comb == "max" else np.fmin
+        if terms.shape[-1] == 0:
+            return np.full(terms.shape[:-1], init, np.float32), True
+        return f(init, f.reduce(terms, axis=-1)).astype(np.float32), True
+    if comb == "sum":
+        return (terms.astype(np.uint64).sum(axis=-1) % (1 << 32)).astype(np.uint32), True
+    if comb == "xor":
+        return np.bitwise_xor.reduce(terms, axis=-1).astype(np.uint32), True
+    if terms.shape[-1] == 0:
+        return np.full(terms.shape[:-1], init, np.uint32), True
+    f = np.maximum if comb == "max" else np.minimum
+    return f(init, f.reduce(terms, axis=-1)).astype(np.uint32), True
+
+
+def evaluate(spec, tiles, col, row, scalars):
+    """Expected outputs of `spec`. tiles: {name: array [rows..., C]} already
+    in the work type (f32 or u32: bf16 and u8 storage widens exactly); col:
+    g [C] or None; row: r [rows...] or None; scalars: {name: value}.
+    Returns ({output name: array}, every float sum exact)."""
+    elem = spec.elem
+    dt = np.float32 if elem == "f32" else np.uint32
+    first = next(iter(tiles.values()))
+    full = first.shape
+    rows = full[:-1]
+    rowvals = {}
+    if row is not None:
+        rowvals["r"] = row.astype(dt)
+    scal = {n: (_f32(v) if elem == "f32" else np.uint32(v)) for n, v in scalars.items()}
+    outs, exact = {}, True
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        for st in spec.stmts:
+            if st["kind"] in ("reduce", "map"):
+                env = {n: a.astype(dt) for n, a in tiles.items()}
+                if col is not None:
+                    env["g"] = col.astype(dt)
+                env.update({n: v[..., None] for n, v in rowvals.items()})
+                env.update(scal)
+                val = np.broadcast_to(np.asarray(_eval(st["expr"], env, elem), dt), full)
+                if st["kind"] == "map":
+                    outs[st["out"]] = np.array(val, dt)
+                    continue
+                red, ok = _reduce(elem, st["comb"], val)
+                exact = exact and ok
+                if st["piped"] is not None:
+                    penv = dict(rowvals)
+                    penv.update(scal)
+                    penv["v"] = red
+                    red = np.broadcast_to(np.asarray(_eval(st["piped"], penv, elem), dt), rows)
+                res = np.array(red, dt)
+            else:
+                env = dict(rowvals)
+                env.update(scal)
+                res = np.array(np.broadcast_to(np.asarray(_eval(st["expr"], env, elem), dt), rows), dt)
+            rowvals[st["out"]] = res
+            if not st["local"]:
+                outs[st["out"]] = res
+    return outs, exact
+
+
+def evaluate_scalar(spec, tiles, col, row, scalars):
+    """Brute force: every output element computed alone, every reduce folded
+    sequentially from init in ascending index order (runtime/tca/reducer.h:
+    36-57), with float32 / uint32 scalars. For tiny shapes only."""
+    elem = spec.elem
+    cast = _f32 if elem == "f32" else np.uint32
+    first = next(iter(tiles.values()))
+    full = first.shape
+    rows = full[:-1]
+    C = full[-1]
+    rowvals = {}
+    if row is not None:
+        rowvals["r"] = {idx: cast(row[idx]) for idx in np.ndindex(*rows)}
+    scal = {n: cast(v) for n, v in scalars.items()}
+    outs = {}
+    combs = {"sum": lambda a, b: a + b, "xor": lambda a, b: a ^ b,
+             "max": (lambda a, b: np.fmax(a, b)) if elem == "f32" else (lambda a, b: max(a, b)),
+             "min": (lambda a, b: np.fmin(a, b)) if elem == "f32" else (lambda a, b: min(a, b))}
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        for st in spec.stmts:
+            if st["kind"] == "map":
+                out = np.zeros(full, np.float32 if elem == "f32" else np.uint32)
+                for idx in np.ndindex(*full):
+                    env = {n: cast(a[idx]) for n, a in tiles.items()}
+                    if col is not None:
+                        env["g"] = cast(col[idx[-1]])
+                    env.update({n: v[idx[:-1]] for n, v in rowvals.items()})
+                    env.update(scal)
+                    out[idx] = _eval(st["expr"], env, elem)
+                outs[st["out"]] = out
+                continue
+            res = {}
+            for ridx in np.ndindex(*rows):
+                if st["kind"] == "reduce":
+                    acc = _init(elem, st["comb"])
+                    for c in range(C):
+                        idx = ridx + (c,)
+                        env = {n: cast(a[idx]) for n, a in tiles.items()}
+                        if col is not None:
+                            env["g"] = cast(col[c])
+                        env.update({n: v[ridx] for n, v in rowvals.items()})
+                        env.update(scal)
+                        acc = cast(combs[st["comb"]](acc, cast(_eval(st["expr"], env, elem))))
+                    if st["piped"] is not None:
+                        env = {n: v[ridx] for n, v in rowvals.items()}
+                        env.update(scal)
+                        env["v"] = acc
+                        acc = cast(_eval(st["piped"], env, elem))
+                    res[ridx] = acc
+                else:
+                    env = {n: v[ridx] for n, v in rowvals.items()}
+                    env.update(scal)
+                    res[ridx] = cast(_eval(st["expr"], env, elem))
+            rowvals[st["out"]] = res
+            if not st["local"]:
+                arr = np.zeros(rows, np.float32 if elem == "f32" else np.uint32)
+                for ridx, v in res.items():
+                    arr[ridx] = v
+                outs[st["out"]] = arr
+    return outs

@@ -169,8 +169,10 @@ class ExprGen {
         break;
       }
       case Op::Un: {
+        // The operand is parenthesized: a negative literal operand would
+        // otherwise spell the decrement operator (--0x1p+1f).
         static const char* sym[] = {"-", "+", "!", "~"};
-        rhs = "static_cast<" + T + ">(" + std::string(sym[e.code]) + a[0] + ")";
+        rhs = "static_cast<" + T + ">(" + std::string(sym[e.code]) + "(" + a[0] + "))";
         break;
       }
       case Op::Select:

@@ -1,0 +1,139 @@
+"""Seeded random row programs (tcacomp_amd/randprog.py) on the device
+against the CPU evaluation of the same spec (oracle/dsl_eval.py).
+
+Each program runs over row counts and row lengths that reach every variant
+its family has: static lengths of every vector width, run-time lengths from
+empty rows to rows streamed past the register cache, split rows, one and
+two row axes. f32 inputs are small integers, so every float sum is exact
+(the evaluator checks it) and every output must match bit for bit up to the
+sign of zero: elementwise arithmetic is correctly rounded on both sides
+under -ffp-contract=off, and an exact sum does not depend on the fold
+order. u32 programs are exact by construction (wrapping arithmetic).
+"""
+import sys
+import zlib
+
+import numpy as np
+import pytest
+
+from dsl_eval import evaluate
+from helpers import CANARY
+from tcacomp_amd import compiler, randprog
+from tcacomp_amd.compiler import TensorDesc
+from tcacomp_amd.pkg import EMIT_NO_FUSION, EMIT_NO_GEMM
+
+pytestmark = pytest.mark.gpu
+
+U32 = 4  # tca dtype code (include/tca_rt.h)
+DYN_C = [0, 1, 3, 6, 64, 1000, 4100, 20000, 70001, 140000]
+ROWS = {1: [(1,), (37,), (300,)], 2: [(1, 1), (3, 37), (20, 15)]}
+
+
+def _shapes(spec, generic):
+    rows = ROWS[spec.outer]
+    if spec.c:
+        return [r + (spec.c,) for r in rows]
+    out = [rows[j % 3] + (c,) for j, c in enumerate(DYN_C)]
+    out.append(rows[2] + (70000,))  # > 255 rows of a streamed length: no split
+    if generic:  # one thread folds a whole row: keep the rows short
+        return [s for s in out if s[-1] <= 70001]
+    out.append(rows[0] + (2 << 20,))  # one long row: split over the GPU
+    return out
+
+
+_progs = {}
+
+
+def _program(spec, generic):
+    key = (spec.name, generic)
+    if key not in _progs:
+        flags = EMIT_NO_FUSION | EMIT_NO_GEMM if generic else 0
+        _progs[key] = compiler.compile_program(randprog.build(spec), flags=flags)
+    return _progs[key]
+
+
+def _inputs(spec, shape, bound):
+    rng = np.random.default_rng(zlib.crc32(("%s %s %d" % (spec.name, shape, bound)).encode()))
+    rows, C = shape[:-1], shape[-1]
+    if spec.elem == "f32":
+        tiles = {t: rng.integers(-bound, bound + 1, size=shape).astype(np.float32) for t, _ in spec.tiles}
+        col = rng.integers(-2, 3, size=(C,)).astype(np.float32) if spec.col else None
+        row = rng.integers(-bound, bound + 1, size=rows).astype(np.float32) if spec.row else None
+    else:
+        tiles = {}
+        for t, st in spec.tiles:
+            hi = 256 if st == "u8" else 1 << 32
+            tiles[t] = rng.integers(0, hi, size=shape, dtype=np.uint64).astype(np.uint32)
+        col = rng.integers(0, 1 << 32, size=(C,), dtype=np.uint64).astype(np.uint32) if spec.col else None
+        row = rng.integers(0, 1 << 32, size=rows, dtype=np.uint64).astype(np.uint32) if spec.row else None
+    return tiles, col, row
+
+
+def _dev(a, storage, dev):
+    """A device tensor (or descriptor) holding `a` in the storage type."""
+    import torch
+    if storage == "f32":
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev), None
+    if storage == "bf16":
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(torch.bfloat16), None
+    if storage == "u8":
+        return torch.from_numpy(np.ascontiguousarray(a.astype(np.uint8))).to(dev), None
+    t = torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(dev)
+    return t, TensorDesc(t.data_ptr() if t.numel() else 0, a.shape, U32)
+
+
+def _check(spec, generic, gpu):
+    import torch
+    prog = _program(spec, generic)
+    for shape in _shapes(spec, generic):
+        rows = shape[:-1]
+        print("random", spec.name, "generic" if generic else "fused", shape, flush=True)
+        sys.stdout.flush()
+        for bound in (8, 3, 1):
+            tiles, col, row = _inputs(spec, shape, bound)
+            want, exact = evaluate(spec, tiles, col, row, dict(spec.scalars))
+            if exact:
+                break
+        assert exact, "no input range keeps the f32 sums of %s exact at %s" % (spec.name, shape)
+        keep, args = [], []
+        for t, st in spec.tiles:
+            d, desc = _dev(tiles[t], st, gpu)
+            keep.append(d)
+            args.append(desc or d)
+        for a in ([col] if spec.col else []) + ([row] if spec.row else []):
+            d, desc = _dev(a, spec.elem, gpu)
+            keep.append(d)
+            args.append(desc or d)
+        outs = {}
+        for st in spec.stmts:
+            if st["local"]:
+                continue
+            oshape = shape if st["kind"] == "map" else rows
+            if spec.elem == "f32":
+                o = torch.full(oshape, CANARY, device=gpu)
+                args.append(o)
+            else:
+                o = torch.full(oshape, 0x5A5A5A5A, dtype=torch.int32, device=gpu)
+                args.append(TensorDesc(o.data_ptr() if o.numel() else 0, oshape, U32))
+            outs[st["out"]] = o
+        prog.launch(args, scalars=[v for _, v in spec.scalars])
+        torch.cuda.synchronize()
+        for name, o in outs.items():
+            got = o.cpu().numpy()
+            if spec.elem == "u32":
+                got = got.view(np.uint32)
+            np.testing.assert_array_equal(got, want[name], err_msg="%s %s output %s" % (spec.name, shape, name))
+        del keep, args, outs
+
+
+@pytest.mark.parametrize("spec", randprog.specs(), ids=lambda s: s.name)
+def test_random_program(gpu, spec):
+    _check(spec, False, gpu)
+
+
+@pytest.mark.parametrize("spec", [s for s in randprog.specs() if s.name in randprog.GENERIC_TOO],
+                         ids=lambda s: s.name)
+def test_random_program_generic(gpu, spec):
+    """The same program lowered with fusion off: one thread per output,
+    sequential folds (the generic family)."""
+    _check(spec, True, gpu)

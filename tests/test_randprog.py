@@ -1,0 +1,122 @@
+"""Host-only checks of the random row programs and of their CPU evaluator
+(oracle/dsl_eval.py): every program builds and emits; the vectorized
+evaluator agrees with a brute-force element loop in the reference's
+sequential fold order (runtime/tca/reducer.h:36-57) on tiny shapes, with
+hand-computed answers, and with the C oracle's row sum and max."""
+import numpy as np
+import pytest
+
+import oracle
+from dsl_eval import evaluate, evaluate_scalar
+from tcacomp_amd import randprog
+from tcacomp_amd.randprog import Spec
+
+SPECS = randprog.specs()
+
+
+def test_programs_are_deterministic_and_distinct():
+    again = randprog.specs()
+    assert [s.name for s in SPECS] == [s.name for s in again]
+    assert [repr(s.stmts) for s in SPECS] == [repr(s.stmts) for s in again]
+    assert len({repr(s.stmts) for s in SPECS}) == len(SPECS)
+
+
+@pytest.mark.parametrize("spec", SPECS, ids=lambda s: s.name)
+def test_program_emits_one_fused_nest(spec):
+    e = randprog.build(spec).emit()
+    fams = set(e.families())
+    assert fams == ({"stream"} if spec.c == 0 or spec.c == 70000 else {"row"}), e.report
+
+
+def _tiny_inputs(spec, shape, seed):
+    rng = np.random.default_rng(seed)
+    rows, C = shape[:-1], shape[-1]
+    if spec.elem == "f32":
+        tiles = {t: rng.integers(-4, 5, size=shape).astype(np.float32) for t, _ in spec.tiles}
+        col = rng.integers(-2, 3, size=(C,)).astype(np.float32) if spec.col else None
+        row = rng.integers(-4, 5, size=rows).astype(np.float32) if spec.row else None
+    else:
+        tiles = {t: rng.integers(0, 1 << 32, size=shape, dtype=np.uint64).astype(np.uint32) for t, _ in spec.tiles}
+        col = rng.integers(0, 1 << 32, size=(C,), dtype=np.uint64).astype(np.uint32) if spec.col else None
+        row = rng.integers(0, 1 << 32, size=rows, dtype=np.uint64).astype(np.uint32) if spec.row else None
+    return tiles, col, row
+
+
+@pytest.mark.parametrize("spec", SPECS, ids=lambda s: s.name)
+def test_evaluator_matches_brute_force(spec):
+    rows = (3,) if spec.outer == 1 else (2, 2)
+    for C in (0, 1, 5):
+        tiles, col, row = _tiny_inputs(spec, rows + (C,), C)
+        fast, exact = evaluate(spec, tiles, col, row, dict(spec.scalars))
+        assert exact
+        slow = evaluate_scalar(spec, tiles, col, row, dict(spec.scalars))
+        assert sorted(fast) == sorted(slow) == sorted(spec.outputs())
+        for k in fast:
+            np.testing.assert_array_equal(fast[k], slow[k], err_msg="%s C=%d %s" % (spec.name, C, k))
+
+
+def _spec(stmts, elem="f32", tiles=(("x0", "f32"),), col=False, row=False, scalars=()):
+    return Spec("hand", elem, 0, 1, list(tiles), col, row, list(scalars), stmts)
+
+
+X0 = ("leaf", "x0")
+
+
+def test_known_answers_f32():
+    spec = _spec([
+        {"kind": "reduce", "expr": X0, "comb": "sum", "piped": None, "out": "o0", "local": False},
+        {"kind": "reduce", "expr": X0, "comb": "max", "piped": None, "out": "l1", "local": True},
+        # piped: v * s0 + r
+        {"kind": "reduce", "expr": ("mul", X0, ("leaf", "g")), "comb": "min",
+         "piped": ("add", ("mul", ("leaf", "v"), ("leaf", "s0")), ("leaf", "r")), "out": "o2", "local": False},
+        {"kind": "rowmap", "expr": ("sub", ("leaf", "l1"), ("const", 1.0)), "out": "o3", "local": False},
+        {"kind": "map", "expr": ("sub", X0, ("leaf", "l1")), "out": "y4", "local": False},
+    ], col=True, row=True, scalars=[("s0", 2.0)])
+    x = np.array([[1, 2, 3], [4, -5, 6]], np.float32)
+    g = np.array([1, -1, 2], np.float32)
+    r = np.array([10, 20], np.float32)
+    out, exact = evaluate(spec, {"x0": x}, g, r, {"s0": 2.0})
+    assert exact
+    np.testing.assert_array_equal(out["o0"], [6, 5])
+    np.testing.assert_array_equal(out["o2"], [2 * -2 + 10, 2 * 4 + 20])  # min(x*g): rows [1,-2,6], [4,5,12]
+    np.testing.assert_array_equal(out["o3"], [2, 5])
+    np.testing.assert_array_equal(out["y4"], [[-2, -1, 0], [-2, -11, 0]])
+
+
+def test_known_answers_empty_rows_and_u32():
+    spec = _spec([
+        {"kind": "reduce", "expr": X0, "comb": c, "piped": None, "out": "o%d" % i, "local": False}
+        for i, c in enumerate(["sum", "max", "min"])])
+    out, _ = evaluate(spec, {"x0": np.zeros((2, 0), np.float32)}, None, None, {})
+    np.testing.assert_array_equal(out["o0"], [0, 0])
+    np.testing.assert_array_equal(out["o1"], [-np.inf, -np.inf])
+    np.testing.assert_array_equal(out["o2"], [np.inf, np.inf])
+    spec = _spec([
+        {"kind": "reduce", "expr": X0, "comb": c, "piped": None, "out": "o%d" % i, "local": False}
+        for i, c in enumerate(["sum", "xor", "max", "min"])], elem="u32", tiles=(("x0", "u32"),))
+    x = np.array([[0xFFFFFFFF, 2, 5]], np.uint32)
+    out, _ = evaluate(spec, {"x0": x}, None, None, {})
+    assert [int(out[k][0]) for k in ("o0", "o1", "o2", "o3")] == [6, 0xFFFFFFFF ^ 2 ^ 5, 0xFFFFFFFF, 2]
+    out, _ = evaluate(spec, {"x0": np.zeros((1, 0), np.uint32)}, None, None, {})
+    assert [int(out[k][0]) for k in ("o0", "o1", "o2", "o3")] == [0, 0, 0, 0xFFFFFFFF]
+
+
+def test_evaluator_matches_c_oracle_row_sum_max():
+    """The reference's row_sum runner restated in C (oracle.c), on exact data."""
+    spec = _spec([
+        {"kind": "reduce", "expr": X0, "comb": "sum", "piped": None, "out": "o0", "local": False},
+        {"kind": "reduce", "expr": X0, "comb": "max", "piped": None, "out": "o1", "local": False}])
+    x = np.random.default_rng(5).integers(-100, 101, size=(64, 777)).astype(np.float32)
+    out, exact = evaluate(spec, {"x0": x}, None, None, {})
+    s, m = oracle.row_sum_max(x)
+    assert exact
+    np.testing.assert_array_equal(out["o0"], s)
+    np.testing.assert_array_equal(out["o1"], m)
+
+
+def test_inexact_sums_are_reported():
+    spec = _spec([{"kind": "reduce", "expr": X0, "comb": "sum", "piped": None, "out": "o0", "local": False}])
+    _, exact = evaluate(spec, {"x0": np.full((1, 4), 0.5, np.float32)}, None, None, {})
+    assert not exact  # non-integer terms
+    _, exact = evaluate(spec, {"x0": np.full((1, 3), 2.0 ** 23, np.float32)}, None, None, {})
+    assert not exact  # partial sums past 2^24
