@@ -335,7 +335,7 @@ def test_fused_locals_stay_in_registers():
 def test_nonfinite_literals_are_valid_hip():
     # The reference formats -inf as the invalid token "-Inff" (internal/cg/cxx/naming.go:103-109).
     src = programs.CONFIG_PROGRAMS["row_sum_max_8192"]().emit().source
-    assert "(-__builtin_inff())" in src and "Inff" not in src
+    assert "(-(__builtin_inff()))" in src and "Inff" not in src
 
 
 def test_device_flags():
