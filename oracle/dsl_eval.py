@@ -1,6 +1,6 @@
-"""TEST INFRASTRUCTURE ONLY: CPU evaluation of the random row programs of
-tcacomp_amd/randprog.py (the checker of tests/test_gpu_random.py, never the
-thing measured or shipped; only tests/ may import it).
+"""TEST INFRASTRUCTURE ONLY: CPU evaluation of the random row and grid
+programs of tcacomp_amd/randprog.py (the checker of tests/test_gpu_random.py,
+never the thing measured or shipped; only tests/ may import it).
 
 The DSL semantics restated here, per statement:
 - a chain's root map is evaluated per element of its iteration space
@@ -204,4 +204,96 @@ def evaluate_scalar(spec, tiles, col, row, scalars):
                 for ridx, v in res.items():
                     arr[ridx] = v
                 outs[st["out"]] = arr
+    return outs
+
+
+def evaluate_grid(spec, x0, xt, col, row, scalars):
+    """Expected outputs of a grid spec (randprog.GridSpec): x0 [R, C] in the
+    work type, xt [C, R] (read at (c, r)), g [C], r [R] or None. `map`
+    stores y [R, C], `tmap` its transpose [C, R], `colreduce` folds over R
+    (the reduce drops the last live axis of As(C, R)) into [C]. Returns
+    ({output: array}, every float sum exact)."""
+    elem = spec.elem
+    dt = np.float32 if elem == "f32" else np.uint32
+    R, C = x0.shape
+    env = {"x0": x0.astype(dt)}
+    if xt is not None:
+        env["xt"] = xt.astype(dt).T
+    if col is not None:
+        env["g"] = col.astype(dt)[None, :]
+    if row is not None:
+        env["r"] = row.astype(dt)[:, None]
+    scal = {n: (_f32(v) if elem == "f32" else np.uint32(v)) for n, v in scalars.items()}
+    env.update(scal)
+    outs, exact = {}, True
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        for st in spec.stmts:
+            val = np.array(np.broadcast_to(np.asarray(_eval(st["expr"], env, elem), dt), (R, C)), dt)
+            if st["kind"] == "map":
+                outs[st["out"]] = val
+            elif st["kind"] == "tmap":
+                outs[st["out"]] = np.ascontiguousarray(val.T)
+            else:
+                red, ok = _reduce(elem, st["comb"], np.ascontiguousarray(val.T))
+                exact = exact and ok
+                if st["piped"] is not None:
+                    penv = dict(scal)
+                    penv["v"] = red
+                    if col is not None:
+                        penv["g"] = col.astype(dt)
+                    red = np.broadcast_to(np.asarray(_eval(st["piped"], penv, elem), dt), (C,))
+                outs[st["out"]] = np.array(red, dt)
+    return outs, exact
+
+
+def evaluate_grid_scalar(spec, x0, xt, col, row, scalars):
+    """Brute force of evaluate_grid: one element at a time, folds in
+    ascending r from init (runtime/tca/reducer.h:36-57). Tiny shapes only."""
+    elem = spec.elem
+    cast = _f32 if elem == "f32" else np.uint32
+    dt = np.float32 if elem == "f32" else np.uint32
+    R, C = x0.shape
+    scal = {n: cast(v) for n, v in scalars.items()}
+    combs = {"sum": lambda a, b: a + b, "xor": lambda a, b: a ^ b,
+             "max": (lambda a, b: np.fmax(a, b)) if elem == "f32" else (lambda a, b: max(a, b)),
+             "min": (lambda a, b: np.fmin(a, b)) if elem == "f32" else (lambda a, b: min(a, b))}
+
+    def env_at(r, c):
+        env = {"x0": cast(x0[r, c])}
+        if xt is not None:
+            env["xt"] = cast(xt[c, r])
+        if col is not None:
+            env["g"] = cast(col[c])
+        if row is not None:
+            env["r"] = cast(row[r])
+        env.update(scal)
+        return env
+
+    outs = {}
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        for st in spec.stmts:
+            if st["kind"] in ("map", "tmap"):
+                out = np.zeros((R, C) if st["kind"] == "map" else (C, R), dt)
+                for r in range(R):
+                    for c in range(C):
+                        v = cast(_eval(st["expr"], env_at(r, c), elem))
+                        if st["kind"] == "map":
+                            out[r, c] = v
+                        else:
+                            out[c, r] = v
+                outs[st["out"]] = out
+                continue
+            out = np.zeros((C,), dt)
+            for c in range(C):
+                acc = _init(elem, st["comb"])
+                for r in range(R):
+                    acc = cast(combs[st["comb"]](acc, cast(_eval(st["expr"], env_at(r, c), elem))))
+                if st["piped"] is not None:
+                    penv = dict(scal)
+                    penv["v"] = acc
+                    if col is not None:
+                        penv["g"] = cast(col[c])
+                    acc = cast(_eval(st["piped"], penv, elem))
+                out[c] = acc
+            outs[st["out"]] = out
     return outs

@@ -203,8 +203,45 @@ def _rename(e, old, new):
 _ELEM = {"f32": TF32, "bf16": TBF16, "u32": TU32, "u8": TU8}
 
 
+def _lower(b, elem, e, env):
+    """Builder expression of tree `e`; `env` maps operand names to Exprs."""
+    k = e[0]
+    if k == "leaf":
+        return env[e[1]]
+    if k == "const":
+        return b.Float32(e[1]) if elem == "f32" else b.UInt32(e[1])
+    a = [_lower(b, elem, x, env) for x in e[1:]]
+    if k == "add":
+        return b.Add(a[0], a[1])
+    if k == "sub":
+        return b.Sub(a[0], a[1])
+    if k == "mul":
+        return b.Mul(a[0], a[1])
+    if k == "max":
+        return Call("fmaxf" if elem == "f32" else "umax", a[0], a[1])
+    if k == "min":
+        return Call("fminf" if elem == "f32" else "umin", a[0], a[1])
+    if k == "sel":
+        return Select(b.Lt(a[0], a[1]), a[2], a[3])
+    if k == "neg":
+        return b.Neg(a[0])
+    if k == "abs":
+        return Call("fabsf", a[0])
+    if k == "div1":
+        return b.Div(a[0], b.Add(Call("fabsf", a[1]), b.Float32(1.0)))
+    if k == "xor":
+        return b.BitXor(a[0], a[1])
+    if k == "and":
+        return b.BitAnd(a[0], a[1])
+    if k == "or":
+        return b.BitOr(a[0], a[1])
+    raise ValueError(k)
+
+
 def build(spec):
     """The pkg.Program of a spec."""
+    if getattr(spec, "kind", "row") == "grid":
+        return _build_grid(spec)
     b = NewBuilder(spec.name)
     rows = [b.Dim("B", 0), b.Dim("R", 0)] if spec.outer == 2 else [b.Dim("R", 0)]
     C = b.Dim("C", 0) if spec.c == 0 else b.Dim("e%d" % spec.c, spec.c)
@@ -226,39 +263,6 @@ def build(spec):
         else:
             ops[st["out"]] = (b.Tensor(st["out"], work, *rows), rows, False)
 
-    def lower(e, env):
-        k = e[0]
-        if k == "leaf":
-            return env[e[1]]
-        if k == "const":
-            return b.Float32(e[1]) if spec.elem == "f32" else b.UInt32(e[1])
-        a = [lower(x, env) for x in e[1:]]
-        if k == "add":
-            return b.Add(a[0], a[1])
-        if k == "sub":
-            return b.Sub(a[0], a[1])
-        if k == "mul":
-            return b.Mul(a[0], a[1])
-        if k == "max":
-            return Call("fmaxf" if spec.elem == "f32" else "umax", a[0], a[1])
-        if k == "min":
-            return Call("fminf" if spec.elem == "f32" else "umin", a[0], a[1])
-        if k == "sel":
-            return Select(b.Lt(a[0], a[1]), a[2], a[3])
-        if k == "neg":
-            return b.Neg(a[0])
-        if k == "abs":
-            return Call("fabsf", a[0])
-        if k == "div1":
-            return b.Div(a[0], b.Add(Call("fabsf", a[1]), b.Float32(1.0)))
-        if k == "xor":
-            return b.BitXor(a[0], a[1])
-        if k == "and":
-            return b.BitAnd(a[0], a[1])
-        if k == "or":
-            return b.BitOr(a[0], a[1])
-        raise ValueError(k)
-
     def operands(e, extra=()):
         names = [n for n in leaves(e) if n not in scal and n not in extra]
         return names, [At(ops[n][0], *ops[n][1]) for n in names]
@@ -270,7 +274,7 @@ def build(spec):
                 if ops[n][2]:
                     env[n] = Cast(env[n], work)
             env.update(scal)
-            return lower(e, env)
+            return _lower(b, spec.elem, e, env)
         return f
 
     for st in spec.stmts:
@@ -309,6 +313,108 @@ def _init_comb(b, elem, comb):
     return b.UInt32(0xFFFFFFFF), lambda acc, v: Call("umin", acc, v)
 
 
+class GridSpec:
+    """One random grid program over [R, C]: elementwise maps (`map` stores
+    y [R, C], `tmap` stores the transposed z [C, R]) and reductions over the
+    leading axis (`colreduce`: out [C] = fold over R, the iteration order
+    written As(C, R) so the reduce drops R). Operands: row tiles x<k> [R, C],
+    a transposed tile xt [C, R] read at (c, r), g [C], r [R], scalars."""
+
+    kind = "grid"
+
+    def __init__(self, name, elem, c, tiles, trans, col, row, scalars, stmts):
+        self.name, self.elem, self.c, self.tiles, self.trans = name, elem, c, tiles, trans
+        self.col, self.row, self.scalars, self.stmts = col, row, scalars, stmts
+
+    def outputs(self):
+        return [s["out"] for s in self.stmts]
+
+
+def generate_grid(seed, elem, dynamic):
+    """The spec of random grid program `seed` (deterministic)."""
+    rng = random.Random(0x6A09E667 ^ (seed * 0x9E3779B1))
+    c = 0 if dynamic else rng.choice(STATIC_C[:8])
+    if elem == "f32":
+        tiles = [("x0", rng.choice(["f32", "f32", "bf16"]))]
+        scalars = [("s%d" % k, rng.choice([-1.0, 2.0, 3.0])) for k in range(rng.choice([0, 1]))]
+    else:
+        tiles = [("x0", rng.choice(["u32", "u8"]))]
+        scalars = [("s%d" % k, rng.choice([3, 0xFFFFFFFF])) for k in range(rng.choice([0, 1]))]
+    trans = rng.random() < 0.6
+    col = rng.random() < 0.5
+    row = rng.random() < 0.5
+    pool = ["x0"] + (["xt"] if trans else []) + (["g"] if col else []) + (["r"] if row else [])
+    sc_pool = [n for n, _ in scalars]
+    stmts = []
+    for i in range(rng.choice([1, 2, 3])):
+        kind = rng.choice(["map", "map", "tmap", "colreduce"])
+        if kind == "colreduce":
+            e = _expr(rng, elem, pool + sc_pool, 2, False, 1)
+            comb = rng.choice(F32_COMBS if elem == "f32" else U32_COMBS)
+            piped = None
+            if rng.random() < 0.4:
+                piped = _expr(rng, elem, ["v"] + (["g"] if col else []) + sc_pool, 2, elem == "f32", 2)
+                if "v" not in leaves(piped):
+                    piped = ("add", ("leaf", "v"), piped)
+        else:
+            e = _expr(rng, elem, pool + sc_pool, 3, elem == "f32", 2)
+            comb = piped = None
+        if not any(l in ("x0", "xt") for l in leaves(e)):
+            e = ("add", ("leaf", rng.choice(["x0", "xt"] if trans else ["x0"])), e)
+        stmts.append({"kind": kind, "expr": e, "comb": comb, "piped": piped, "out": "%s%d" % (kind[0], i)})
+    name = "grid_%s_%s_%d" % (elem, "dyn" if dynamic else "c%d" % c, seed)
+    return GridSpec(name, elem, c, tiles, trans, col, row, scalars, stmts)
+
+
+def _build_grid(spec):
+    b = NewBuilder(spec.name)
+    R = b.Dim("R", 0)
+    C = b.Dim("C", 0) if spec.c == 0 else b.Dim("e%d" % spec.c, spec.c)
+    work = TF32 if spec.elem == "f32" else TU32
+    ops = {}  # operand name -> (tensor, subscript axes, cast to the work type)
+    x0_storage = spec.tiles[0][1]
+    ops["x0"] = (b.Tensor("x0", _ELEM[x0_storage], R, C), [R, C], x0_storage != spec.elem)
+    if spec.trans:
+        ops["xt"] = (b.Tensor("xt", work, C, R), [C, R], False)
+    if spec.col:
+        ops["g"] = (b.Tensor("g", work, C), [C], False)
+    if spec.row:
+        ops["r"] = (b.Tensor("r", work, R), [R], False)
+    scal = {n: b.ScalarParam(n, work) for n, _ in spec.scalars}
+    outs = {}
+    for st in spec.stmts:
+        dims = {"map": (R, C), "tmap": (C, R), "colreduce": (C,)}[st["kind"]]
+        outs[st["out"]] = b.Tensor(st["out"], work, *dims)
+
+    def fn_for(e, names, pre=()):
+        def f(*params):
+            env = dict(zip(list(pre) + names, params))
+            for n in names:
+                if ops[n][2]:
+                    env[n] = Cast(env[n], work)
+            env.update(scal)
+            return _lower(b, spec.elem, e, env)
+        return f
+
+    for st in spec.stmts:
+        names = [n for n in leaves(st["expr"]) if n not in scal]
+        operand_list = [At(ops[n][0], *ops[n][1]) for n in names]
+        chain = b.Stmt().Iter(R, C).Map(operand_list, fn_for(st["expr"], names))
+        if st["kind"] == "map":
+            chain.As(R, C).Store(outs[st["out"]], R, C)
+        elif st["kind"] == "tmap":
+            chain.As(R, C).Store(outs[st["out"]], C, R)
+        else:
+            init, comb = _init_comb(b, spec.elem, st["comb"])
+            chain = chain.As(C, R).Reduce(init, comb)
+            if st["piped"] is not None:
+                pnames = [n for n in leaves(st["piped"]) if n not in scal and n != "v"]
+                chain = chain.Map([At(ops[n][0], *ops[n][1]) for n in pnames],
+                                  fn_for(st["piped"], pnames, pre=("v",))).As(C)
+            chain.Store(outs[st["out"]], C)
+    return b.Build()
+
+
 # The registered random programs: (elem, dynamic row length, seed).
 PROGRAMS = ([("f32", True, s) for s in range(10)] + [("f32", False, s) for s in range(10, 20)] +
             [("u32", True, s) for s in range(20, 25)] + [("u32", False, s) for s in range(25, 30)])
@@ -320,5 +426,11 @@ GENERIC_TOO = {"rand_f32_dyn_0", "rand_f32_dyn_1", "rand_f32_c3_12", "rand_f32_c
                "rand_u32_c1000_26"}
 
 
+# Random grid programs: (elem, dynamic row length, seed).
+GRID_PROGRAMS = ([("f32", True, s) for s in range(40, 46)] + [("f32", False, s) for s in range(46, 50)] +
+                 [("u32", True, s) for s in range(50, 53)] + [("u32", False, s) for s in range(53, 55)])
+
+
 def specs():
-    return [generate(seed, elem, dyn) for elem, dyn, seed in PROGRAMS]
+    return ([generate(seed, elem, dyn) for elem, dyn, seed in PROGRAMS] +
+            [generate_grid(seed, elem, dyn) for elem, dyn, seed in GRID_PROGRAMS])

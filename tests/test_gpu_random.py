@@ -16,7 +16,7 @@ import zlib
 import numpy as np
 import pytest
 
-from dsl_eval import evaluate
+from dsl_eval import evaluate, evaluate_grid
 from helpers import CANARY
 from tcacomp_amd import compiler, randprog
 from tcacomp_amd.compiler import TensorDesc
@@ -126,13 +126,72 @@ def _check(spec, generic, gpu):
         del keep, args, outs
 
 
-@pytest.mark.parametrize("spec", randprog.specs(), ids=lambda s: s.name)
+ROW_SPECS = [s for s in randprog.specs() if getattr(s, "kind", "row") == "row"]
+GRID_SPECS = [s for s in randprog.specs() if getattr(s, "kind", "row") == "grid"]
+GRID_SHAPES = [(1, 0), (0, 5), (1, 1), (37, 3), (300, 64), (37, 1000), (300, 4100), (5, 70001), (1000, 1000)]
+
+
+@pytest.mark.parametrize("spec", ROW_SPECS, ids=lambda s: s.name)
 def test_random_program(gpu, spec):
     _check(spec, False, gpu)
 
 
-@pytest.mark.parametrize("spec", [s for s in randprog.specs() if s.name in randprog.GENERIC_TOO],
-                         ids=lambda s: s.name)
+@pytest.mark.parametrize("spec", GRID_SPECS, ids=lambda s: s.name)
+def test_random_grid_program(gpu, spec):
+    """Elementwise maps with broadcast and transposed operands, transposed
+    stores, reductions over the leading axis (elementwise, streaming and
+    generic families)."""
+    import torch
+    prog = _program(spec, False)
+    shapes = [(r, spec.c) for r in (1, 37, 300)] if spec.c else GRID_SHAPES
+    for R, C in shapes:
+        print("random", spec.name, (R, C), flush=True)
+        sys.stdout.flush()
+        for bound in (8, 3, 1):
+            rng = np.random.default_rng(zlib.crc32(("%s %d %d %d" % (spec.name, R, C, bound)).encode()))
+            if spec.elem == "f32":
+                gen = lambda *shape: rng.integers(-bound, bound + 1, size=shape).astype(np.float32)  # noqa: E731
+            else:
+                gen = lambda *shape: rng.integers(0, 1 << 32, size=shape, dtype=np.uint64).astype(np.uint32)  # noqa: E731
+            x0 = gen(R, C)
+            if spec.tiles[0][1] == "u8":
+                x0 = x0 & np.uint32(0xFF)
+            xt = gen(C, R) if spec.trans else None
+            g = gen(C) if spec.col else None
+            r = gen(R) if spec.row else None
+            want, exact = evaluate_grid(spec, x0, xt, g, r, dict(spec.scalars))
+            if exact:
+                break
+        assert exact, "no input range keeps the f32 sums of %s exact at %s" % (spec.name, (R, C))
+        keep, args = [], []
+        d, desc = _dev(x0, spec.tiles[0][1], gpu)
+        keep.append(d)
+        args.append(desc or d)
+        for a in [a for a in (xt, g, r) if a is not None]:
+            d, desc = _dev(a, spec.elem, gpu)
+            keep.append(d)
+            args.append(desc or d)
+        outs = {}
+        for st in spec.stmts:
+            oshape = {"map": (R, C), "tmap": (C, R), "colreduce": (C,)}[st["kind"]]
+            if spec.elem == "f32":
+                o = torch.full(oshape, CANARY, device=gpu)
+                args.append(o)
+            else:
+                o = torch.full(oshape, 0x5A5A5A5A, dtype=torch.int32, device=gpu)
+                args.append(TensorDesc(o.data_ptr() if o.numel() else 0, oshape, U32))
+            outs[st["out"]] = o
+        prog.launch(args, scalars=[v for _, v in spec.scalars])
+        torch.cuda.synchronize()
+        for name, o in outs.items():
+            got = o.cpu().numpy()
+            if spec.elem == "u32":
+                got = got.view(np.uint32)
+            np.testing.assert_array_equal(got, want[name], err_msg="%s %s output %s" % (spec.name, (R, C), name))
+        del keep, args, outs
+
+
+@pytest.mark.parametrize("spec", [s for s in ROW_SPECS if s.name in randprog.GENERIC_TOO], ids=lambda s: s.name)
 def test_random_program_generic(gpu, spec):
     """The same program lowered with fusion off: one thread per output,
     sequential folds (the generic family)."""

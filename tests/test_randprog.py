@@ -7,18 +7,19 @@ import numpy as np
 import pytest
 
 import oracle
-from dsl_eval import evaluate, evaluate_scalar
+from dsl_eval import evaluate, evaluate_grid, evaluate_grid_scalar, evaluate_scalar
 from tcacomp_amd import randprog
 from tcacomp_amd.randprog import Spec
 
-SPECS = randprog.specs()
+SPECS = [s for s in randprog.specs() if getattr(s, "kind", "row") == "row"]
+GRIDS = [s for s in randprog.specs() if getattr(s, "kind", "row") == "grid"]
 
 
 def test_programs_are_deterministic_and_distinct():
     again = randprog.specs()
-    assert [s.name for s in SPECS] == [s.name for s in again]
-    assert [repr(s.stmts) for s in SPECS] == [repr(s.stmts) for s in again]
-    assert len({repr(s.stmts) for s in SPECS}) == len(SPECS)
+    assert [s.name for s in SPECS + GRIDS] == [s.name for s in again]
+    assert [repr(s.stmts) for s in SPECS + GRIDS] == [repr(s.stmts) for s in again]
+    assert len({repr(s.stmts) for s in SPECS + GRIDS}) == len(again)
 
 
 @pytest.mark.parametrize("spec", SPECS, ids=lambda s: s.name)
@@ -120,3 +121,40 @@ def test_inexact_sums_are_reported():
     assert not exact  # non-integer terms
     _, exact = evaluate(spec, {"x0": np.full((1, 3), 2.0 ** 23, np.float32)}, None, None, {})
     assert not exact  # partial sums past 2^24
+
+
+def _grid_inputs(spec, R, C, seed):
+    rng = np.random.default_rng(seed)
+    if spec.elem == "f32":
+        gen = lambda *shape: rng.integers(-4, 5, size=shape).astype(np.float32)  # noqa: E731
+    else:
+        gen = lambda *shape: rng.integers(0, 1 << 32, size=shape, dtype=np.uint64).astype(np.uint32)  # noqa: E731
+    return (gen(R, C), gen(C, R) if spec.trans else None, gen(C) if spec.col else None,
+            gen(R) if spec.row else None)
+
+
+@pytest.mark.parametrize("spec", GRIDS, ids=lambda s: s.name)
+def test_grid_evaluator_matches_brute_force(spec):
+    for R, C in ((3, 4), (1, 1), (0, 3), (4, 0)):
+        x0, xt, g, r = _grid_inputs(spec, R, C, R * 10 + C)
+        fast, exact = evaluate_grid(spec, x0, xt, g, r, dict(spec.scalars))
+        assert exact
+        slow = evaluate_grid_scalar(spec, x0, xt, g, r, dict(spec.scalars))
+        assert sorted(fast) == sorted(slow) == sorted(spec.outputs())
+        for k in fast:
+            np.testing.assert_array_equal(fast[k], slow[k], err_msg="%s %dx%d %s" % (spec.name, R, C, k))
+
+
+def test_grid_known_answers():
+    from tcacomp_amd.randprog import GridSpec
+    spec = GridSpec("hand", "f32", 0, [("x0", "f32")], True, True, False, [], [
+        {"kind": "map", "expr": ("sub", X0, ("leaf", "xt")), "comb": None, "piped": None, "out": "m0"},
+        {"kind": "tmap", "expr": X0, "comb": None, "piped": None, "out": "t1"},
+        {"kind": "colreduce", "expr": X0, "comb": "sum", "piped": ("mul", ("leaf", "v"), ("leaf", "g")),
+         "out": "c2"}])
+    x = np.array([[1, 2], [3, 4]], np.float32)
+    xt = np.array([[10, 20], [30, 40]], np.float32)  # xt[c, r]
+    out, _ = evaluate_grid(spec, x, xt, np.array([1, -1], np.float32), None, {})
+    np.testing.assert_array_equal(out["m0"], [[1 - 10, 2 - 30], [3 - 20, 4 - 40]])
+    np.testing.assert_array_equal(out["t1"], [[1, 3], [2, 4]])
+    np.testing.assert_array_equal(out["c2"], [4, -6])
