@@ -48,6 +48,9 @@ CONFIGS = {
     # 16 u8 elements): not configurations, the same family on other dtypes
     "c2h": ("row_sum_bf16_dyn", "row sum+max bf16 -> f32 [8192,16384] (streaming family)"),
     "c2u": ("row_sum_u8_dyn", "row sum u8 -> u32 -> f32 scaled [8192,32768] (streaming family)"),
+    # C2's reductions over the non-contiguous axis (the column family): the
+    # reference's middle-axis reduction form; not a configuration
+    "c2c": ("col_sum_max_dyn", "column sum+max f32 [8192,8192] (column family)"),
     # not a configuration: the plain copy used to calibrate rocprof counters
     "copy": ("copy_f32", "copy f32 [8192,8192] (counter calibration)"),
 }
@@ -77,7 +80,16 @@ def _setup(key, dev):
     def dev_f32(a):
         return torch.from_numpy(a).to(dev)
 
-    if key in ("c2v", "c2r"):
+    if key == "c2c":
+        R = C = 8192
+        x = inputs.normal((R, C), 1.0, 0)
+        algo = R * C * 4 + 2 * C * 4
+        per_set = algo
+        make = lambda i: [dev_f32(x), torch.empty(C, device=dev), torch.empty(C, device=dev)]  # noqa: E731
+        scalars = []
+        work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = None
+    elif key in ("c2v", "c2r"):
         R, C = (1, 64 << 20) if key == "c2v" else (16, 4 << 20)
         x = inputs.normal((R, C), 1.0, 0)
         algo = R * C * 4 + 2 * R * 4
@@ -269,7 +281,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c2h,c2u")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c2h,c2u,c2c")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
                     help="untimed launches per config before the warmup steps, in wall-clock ms")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")

@@ -23,6 +23,7 @@ enum class Family {
   Elementwise,  // E: no real reduction; vectorised flat streaming
   Row,          // R/F: reductions (and maps) over the contiguous last axis of a fused nest
   Stream,       // S: the same nests with a run-time (or register-exceeding) row length, streamed
+  Col,          // C: reductions over a non-contiguous axis (the reduced axis outside the contiguous one)
   Gemm,         // G: dense K-contraction on MFMA
   Generic       // X: one thread per output element, sequential folds
 };

@@ -40,6 +40,7 @@ const char* FamilyName(Family f) {
     case Family::Elementwise: return "elementwise";
     case Family::Row: return "row";
     case Family::Stream: return "stream";
+    case Family::Col: return "col";
     case Family::Gemm: return "gemm";
     case Family::Generic: return "generic";
   }
@@ -481,6 +482,78 @@ RowGeom RowCheck(const Graph& g, const std::vector<int>& chains, uint32_t nv_tar
   return geo;
 }
 
+// ---- column family geometry -----------------------------------------------
+
+// Column family: a reduction over an axis that is not the contiguous one —
+// the reference's middle-axis reductions (testing/kernels/runtime/
+// row_sum.tca, softmax.tca): every chain iterates (outer..., c, r), the
+// reduced axis r last, over tiles laid out (outer..., r, c) with c
+// contiguous. One reduce per chain with an associative-commutative
+// combiner, stored at (outer..., c); operands are tiles, column vectors
+// ((outer...,) c: one value per output), row vectors ((outer...,) r) and
+// outer scalars; piped maps read column vectors and outer scalars. The
+// chains of a nest read none of each other's results (one pass).
+struct ColGeom {
+  bool ok = false;
+  std::string why;
+  std::vector<int> as, outer;
+  int c = -1, r = -1;
+};
+
+enum class ColKind { Tile, ColVec, RowVec, Outer, Bad };
+
+ColKind ClassifyCol(const ir::Operand& o, const ColGeom& geo) {
+  std::vector<int> tile(geo.outer), cv(geo.outer), rv(geo.outer);
+  tile.push_back(geo.r);
+  tile.push_back(geo.c);
+  cv.push_back(geo.c);
+  rv.push_back(geo.r);
+  if (o.axes == tile) return ColKind::Tile;
+  if (o.axes == cv || (o.axes.size() == 1 && o.axes[0] == geo.c)) return ColKind::ColVec;
+  if (o.axes == rv || (o.axes.size() == 1 && o.axes[0] == geo.r)) return ColKind::RowVec;
+  const std::set<int> outer(geo.outer.begin(), geo.outer.end());
+  for (int a : o.axes)
+    if (!outer.count(a)) return ColKind::Bad;
+  return ColKind::Outer;
+}
+
+ColGeom ColCheck(const Graph& g, const std::vector<int>& chains) {
+  ColGeom geo;
+  auto no = [&](const std::string& w) {
+    geo.ok = false;
+    geo.why = w;
+    return geo;
+  };
+  geo.as = g.chains[chains[0]].root.as;
+  if (geo.as.size() < 2) return no("fewer than two iteration axes");
+  geo.r = geo.as.back();
+  geo.c = geo.as[geo.as.size() - 2];
+  geo.outer.assign(geo.as.begin(), geo.as.end() - 2);
+  std::set<int> stored;
+  for (int ci : chains) stored.insert(g.chains[ci].store_tensor);
+  std::vector<int> out_axes(geo.outer);
+  out_axes.push_back(geo.c);
+  for (int ci : chains) {
+    const ir::Chain& c = g.chains[ci];
+    if (c.root.as != geo.as) return no("iteration orders differ");
+    if (c.reduces.size() != 1) return no("not exactly one reduction");
+    if (!IsMonoidCombiner(g, c.reduces[0])) return no("combiner is not an associative-commutative op over (acc, now)");
+    if (c.store_axes != out_axes) return no("store is not at (outer..., column)");
+    for (const auto& o : c.root.ops) {
+      if (ClassifyCol(o, geo) == ColKind::Bad) return no("operand " + g.tensors[o.tensor].name + " is not column-shaped");
+      if (stored.count(o.tensor)) return no("a chain reads a result of the same nest");
+    }
+    if (c.has_piped)
+      for (const auto& o : c.piped.ops) {
+        const ColKind k = ClassifyCol(o, geo);
+        if (k != ColKind::ColVec && k != ColKind::Outer) return no("piped operand is not per output");
+        if (stored.count(o.tensor)) return no("a chain reads a result of the same nest");
+      }
+  }
+  geo.ok = true;
+  return geo;
+}
+
 // ---- elementwise family check --------------------------------------------
 
 bool DegenerateReduces(const Graph& g, const ir::Chain& c) {
@@ -545,6 +618,7 @@ class Emitter {
     std::vector<std::string> args;
     std::vector<std::string> when;  // launch guards: "<dim> <lo> <hi> <mod> <rem>"
     std::string pack;               // packed row kernel: "<dim> <epl> <min block>"
+    std::string split;              // row-split reduction: "<dim> <rows-min> <blocks> <merge> <n> <terms>"
   };
 
   // -------------------------------------------------------------- analysis
@@ -577,7 +651,7 @@ class Emitter {
       if (!cur.empty() && opts_.allow_fused) {
         std::vector<int> cand = cur;
         cand.push_back(i);
-        if ((RowCheck(g_, cand, RowNV()).ok || StreamCheck(g_, cand).ok) && !IsGemm(cur)) {
+        if ((RowCheck(g_, cand, RowNV()).ok || StreamCheck(g_, cand).ok || ColCheck(g_, cand).ok) && !IsGemm(cur)) {
           cur = cand;
           continue;
         }
@@ -621,9 +695,11 @@ class Emitter {
       if (opts_.allow_fused && DegenerateReduces(g_, c) && !ReadsRegLocalCandidate(c)) return Family::Elementwise;
       if (opts_.allow_fused && RowCheck(g_, chains, RowNV()).ok) return Family::Row;
       if (opts_.allow_fused && StreamCheck(g_, chains).ok) return Family::Stream;
+      if (opts_.allow_fused && ColCheck(g_, chains).ok) return Family::Col;
       return Family::Generic;
     }
-    return RowCheck(g_, chains, RowNV()).ok ? Family::Row : Family::Stream;
+    if (RowCheck(g_, chains, RowNV()).ok) return Family::Row;
+    return StreamCheck(g_, chains).ok ? Family::Stream : Family::Col;
   }
 
   bool ReadsRegLocalCandidate(const ir::Chain&) { return false; }
@@ -718,6 +794,7 @@ class Emitter {
       case Family::Elementwise: return EmitElementwise(ni, err);
       case Family::Row: return EmitRow(ni, err);
       case Family::Stream: return EmitStream(ni, err);
+      case Family::Col: return EmitCol(ni, err);
       case Family::Gemm: return EmitGemmNest(ni, err);
       case Family::Generic: return EmitGeneric(ni, err);
     }
@@ -1859,6 +1936,401 @@ class Emitter {
     return true;
   }
 
+  // C: reductions over a non-contiguous axis. Threads span the contiguous
+  // axis in vectors of V elements (16 bytes of the widest tile or column
+  // vector): SL = min(64, smallest power of two >= C / V) threads per row
+  // and 256 / SL rows per block step, 256 threads per block. A block owns 64
+  // column vectors of one outer index and a chunk of the reduced axis: P
+  // chunks, P = col_split(R, column blocks, 64, 1024) — enough blocks to
+  // fill the GPU, >= 64 rows each, and a partial scratch of at most
+  // 1024 x 64 vectors. Chunk p covers rows [p R / P, (p + 1) R / P), never empty when
+  // P > 1 (P <= R). Each thread folds its columns over its rows in registers
+  // with 4 rows in flight; the row slots of a block meet in LDS. With P = 1
+  // the block applies init and the piped map and stores; otherwise it writes
+  // its partials and a merge kernel (launched only when P > 1; 64 outputs
+  // per block, its 16 waves folding every 16th chunk) combines them. Loads
+  // are unmasked: lanes past the last column read the row's last vector and
+  // store nothing.
+  bool EmitCol(int ni, std::string* err) {
+    // Swept on MI355X (column sum+max, [8192, 8192] .. [16, 4 Mi]): spans of
+    // 64 vectors beat 256 (4.7-5.7 against 4.3-4.8 TB/s) and a 1024-block
+    // split target beats 512 and 2048.
+    constexpr uint32_t kWaves = 4, kRowsMin = 64, kBlocks = 1024, kUnroll = 4, kMergeWaves = 16, kSpan = 64,
+                       kLogSpan = 6;
+    const Nest& n = an_.nests[ni];
+    const ColGeom geo = ColCheck(g_, n.chains);
+    if (!geo.ok) {
+      *err = "emit: column family rejected a nest it classified: " + geo.why;
+      return false;
+    }
+    PlanKernel pk;
+    pk.symbol = Sym(g_, prefix_, ni);
+    const std::string sig = Signature(n, &pk);
+    const std::string sym = pk.symbol;
+    std::ostringstream& o = src_;
+    size_t widest = 1;
+    for (int ci : n.chains)
+      for (const auto& op : g_.chains[ci].root.ops) {
+        const ColKind k = ClassifyCol(op, geo);
+        if (k == ColKind::Tile || k == ColKind::ColVec)
+          widest = std::max(widest, ir::ElemBytes(g_.tensors[op.tensor].elem));
+      }
+    const uint32_t vmax = static_cast<uint32_t>(std::max<size_t>(1, 16 / widest));
+    // Partial scratch: one plan-only local per reduction.
+    const std::string partDim = "__coldim" + std::to_string(ni);
+    extra_dims_.push_back(partDim + " " + std::to_string(uint64_t{kBlocks} * kSpan * vmax));
+    std::string partSig, partArgs;
+    std::vector<std::string> partNames;
+    for (int ci : n.chains) {
+      const ir::Elem pe = g_.exprs[g_.chains[ci].root.fn.body].type;
+      const std::string nm = "__colpart" + std::to_string(ci);
+      partNames.push_back(nm);
+      extra_tensors_.push_back(nm + " " + ir::ElemName(pe) + " local 1 " + partDim);
+      partSig += ",\n    " + CType(pe) + "* __restrict__ p" + std::to_string(ci) + " /* " + nm + " */";
+      partArgs += ", p" + std::to_string(ci);
+    }
+    // Operands by kind (root and piped maps), each loaded once per kind.
+    std::vector<int> tiles, colvecs, rowvecs, outers;
+    auto note = [](std::vector<int>& v, int t) {
+      if (std::find(v.begin(), v.end(), t) == v.end()) v.push_back(t);
+    };
+    std::map<int, const ir::Operand*> opOf;
+    for (int ci : n.chains) {
+      const ir::Chain& c = g_.chains[ci];
+      std::vector<const ir::Operand*> ops;
+      for (const auto& op : c.root.ops) ops.push_back(&op);
+      if (c.has_piped)
+        for (const auto& op : c.piped.ops) ops.push_back(&op);
+      for (const ir::Operand* op : ops) {
+        opOf[op->tensor] = op;
+        switch (ClassifyCol(*op, geo)) {
+          case ColKind::Tile: note(tiles, op->tensor); break;
+          case ColKind::ColVec: note(colvecs, op->tensor); break;
+          case ColKind::RowVec: note(rowvecs, op->tensor); break;
+          default: note(outers, op->tensor); break;
+        }
+      }
+    }
+    auto kindOf = [&](int t) { return ClassifyCol(*opOf[t], geo); };
+    // Coordinates: outer axes c<a>, the column `colv`, the row `rowv`.
+    auto coordFn = [&](const std::string& colv, const std::string& rowv) {
+      return [&, colv, rowv](int a) -> std::string {
+        if (a == geo.c) return colv;
+        if (a == geo.r) return rowv;
+        return "c" + std::to_string(a);
+      };
+    };
+    auto outerCoords = [&](const std::string& ind, const std::string& flat) {
+      o << ind << "uint32_t orem = " << flat << ";\n";
+      for (int k = static_cast<int>(geo.outer.size()) - 1; k >= 0; --k) {
+        const int a = geo.outer[k];
+        if (k == 0)
+          o << ind << "const uint32_t c" << a << " = orem;\n";
+        else
+          o << ind << "const uint32_t c" << a << " = orem % " << ExtentExpr(g_, a) << "; orem /= " << ExtentExpr(g_, a)
+            << ";\n";
+      }
+      o << ind << "(void)orem;\n";
+    };
+    auto combs = [&](const std::string& ind) {
+      for (int ci : n.chains) {
+        const ir::Chain& c = g_.chains[ci];
+        const std::string T = CType(g_.exprs[c.root.fn.body].type);
+        o << ind << "const auto comb" << ci << " = [](" << T << " acc, " << T << " now) -> " << T << " {\n";
+        ExprGen cg(g_, o, ind + "  ", &counter_);
+        cg.Bind(c.reduces[0].fn.params[0], "acc");
+        cg.Bind(c.reduces[0].fn.params[1], "now");
+        const std::string r = cg.Gen(c.reduces[0].fn.body);
+        o << ind << "  return " << r << ";\n" << ind << "};\n";
+      }
+    };
+    // init, the piped map and the store of chain ci's reduced value `acc`
+    // (`present`: the value folded anything) at column `col`, with column
+    // vectors read by `colval`.
+    auto finish = [&](std::ostringstream& b, const std::string& ind, int ci, const std::string& acc,
+                      const std::string& present, const std::string& col,
+                      const std::function<std::string(int)>& colval) {
+      const ir::Chain& c = g_.chains[ci];
+      const ir::ReduceStage& r = c.reduces[0];
+      const std::string T = CType(g_.exprs[c.root.fn.body].type);
+      ExprGen ig(g_, b, ind, &counter_);
+      const std::string init = ig.Gen(r.init);
+      const std::string fin = "fin" + std::to_string(ci);
+      b << ind << T << " " << fin << " = " << init << ";\n";
+      b << ind << "if (" << present << ") {\n";
+      {
+        ExprGen fg(g_, b, ind + "  ", &counter_);
+        fg.Bind(r.fn.params[0], init);
+        fg.Bind(r.fn.params[1], acc);
+        const std::string v = fg.Gen(r.fn.body);
+        b << ind << "  " << fin << " = " << v << ";\n";
+      }
+      b << ind << "}\n";
+      std::string val = fin;
+      if (c.has_piped) {
+        ExprGen pg(g_, b, ind, &counter_);
+        pg.Bind(c.piped.fn.params[0], val);
+        for (size_t k = 0; k < c.piped.ops.size(); ++k) {
+          const int t = c.piped.ops[k].tensor;
+          pg.Bind(c.piped.fn.params[k + 1], kindOf(t) == ColKind::ColVec ? colval(t) : "os" + std::to_string(t));
+        }
+        val = pg.Gen(c.piped.fn.body);
+      }
+      const int st = c.store_tensor;
+      b << ind << "t" << st << "[" << Offset(st, c.store_axes, coordFn(col, "0u")) << "] = " << val << ";\n";
+    };
+
+    o << "// statements";
+    for (int ci : n.chains) o << " #" << ci;
+    o << ": column family; reduce over @" << g_.dims[geo.r].name << " (not contiguous) per column of @"
+      << g_.dims[geo.c].name << "\n";
+    // ---- partial folds
+    o << "template <uint32_t V>\n__device__ __forceinline__ void " << sym << "_part(\n    " << sig << partSig
+      << ") {\n";
+    o << "  constexpr uint32_t W = " << kWaves << "u, RMIN = " << kRowsMin << "u, BLOCKS = " << kBlocks
+      << "u, SPAN = " << kSpan << "u, LSPAN = " << kLogSpan << "u;  // SPAN column vectors per block\n";
+    o << "  const uint32_t C = " << ExtentExpr(g_, geo.c) << ", R = " << ExtentExpr(g_, geo.r) << ";\n";
+    o << "  const uint32_t NOUT = " << ProductExpr(geo.outer) << ";\n";
+    o << "  const uint32_t VEC = C / V, CB = (VEC + SPAN - 1u) / SPAN, NCB = NOUT * CB;\n";
+    o << "  const uint32_t P = tca::hip::col_split(R, NCB, RMIN, BLOCKS);\n";
+    o << "  const uint32_t p = blockIdx.x / NCB, cbk = blockIdx.x - p * NCB;\n";
+    o << "  const uint32_t ob = cbk / CB, cb = cbk - ob * CB;\n";
+    o << "  uint32_t LSL = 0u;  // SL = 2^LSL lanes per row, the smallest power of two >= VEC, at most SPAN\n";
+    o << "  while (LSL < LSPAN && (1u << LSL) < VEC) ++LSL;\n";
+    o << "  const uint32_t SL = 1u << LSL, STEP = (W * 64u) >> LSL;  // STEP rows per block step\n";
+    o << "  const uint32_t cg = threadIdx.x & (SL - 1u), slot = threadIdx.x >> LSL;\n";
+    o << "  const uint32_t cvec = cb * SPAN + cg;\n";
+    o << "  const uint32_t col0 = (cvec < VEC ? cvec : VEC - 1u) * V;  // clamped: loads stay in the row\n";
+    o << "  const uint32_t r_lo = static_cast<uint32_t>(static_cast<uint64_t>(p) * R / P);\n";
+    o << "  const uint32_t r_hi = static_cast<uint32_t>(static_cast<uint64_t>(p + 1u) * R / P);\n";
+    outerCoords("  ", "ob");
+    combs("  ");
+    const auto at0 = coordFn("col0", "0u");
+    for (int t : colvecs)
+      o << "  const auto cv" << t << " = tca::hip::load_vec<" << CType(g_.tensors[t].elem) << ", V>(t" << t << " + "
+        << Offset(t, opOf[t]->axes, at0) << ");\n";
+    for (int t : outers)
+      o << "  const " << CType(g_.tensors[t].elem) << " os" << t << " = t" << t << "[" << Offset(t, opOf[t]->axes, at0)
+        << "];\n";
+    for (int ci : n.chains) {
+      const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+      o << "  " << T << " part" << ci << "[V];\n";
+      o << "#pragma unroll\n  for (uint32_t q = 0; q < V; ++q) part" << ci << "[q] = " << T << "(0);\n";
+    }
+    // Loads of row `rv` into x<t><sfx> / rv<t><sfx>, then the fold.
+    auto loads = [&](std::ostringstream& b, const std::string& ind, const std::string& rv, const std::string& sfx) {
+      const auto at = coordFn("col0", rv);
+      for (int t : tiles)
+        b << ind << "const auto x" << t << sfx << " = tca::hip::load_vec_nt<" << CType(g_.tensors[t].elem) << ", V>(t"
+          << t << " + " << Offset(t, opOf[t]->axes, at) << ");\n";
+      for (int t : rowvecs)
+        b << ind << "const " << CType(g_.tensors[t].elem) << " rv" << t << sfx << " = t" << t << "["
+          << Offset(t, opOf[t]->axes, at) << "];\n";
+    };
+    auto fold = [&](std::ostringstream& b, const std::string& ind, const std::string& sfx, bool first,
+                    const std::string& ok) {
+      b << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) {\n";
+      for (int ci : n.chains) {
+        const ir::Chain& c = g_.chains[ci];
+        ExprGen eg(g_, b, ind + "  ", &counter_);
+        for (size_t k = 0; k < c.root.ops.size(); ++k) {
+          const int t = c.root.ops[k].tensor;
+          std::string v;
+          switch (kindOf(t)) {
+            case ColKind::Tile: v = "x" + std::to_string(t) + sfx + "[q]"; break;
+            case ColKind::ColVec: v = "cv" + std::to_string(t) + "[q]"; break;
+            case ColKind::RowVec: v = "rv" + std::to_string(t) + sfx; break;
+            default: v = "os" + std::to_string(t); break;
+          }
+          eg.Bind(c.root.fn.params[k], v);
+        }
+        const std::string ev = eg.Gen(c.root.fn.body);
+        const std::string P = "part" + std::to_string(ci) + "[q]";
+        if (first) b << ind << "  " << P << " = " << ev << ";\n";
+        else if (ok.empty()) b << ind << "  " << P << " = comb" << ci << "(" << P << ", " << ev << ");\n";
+        else b << ind << "  " << P << " = " << ok << " ? comb" << ci << "(" << P << ", " << ev << ") : " << P << ";\n";
+      }
+      b << ind << "}\n";
+      for (int ci : n.chains)
+        if (FoldFenced(g_.exprs[g_.chains[ci].root.fn.body].type))
+          b << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) tca::hip::fold_fence(part" << ci
+            << "[q]);\n";
+    };
+    {
+      // Rows in groups of kUnroll (loads in flight together). The first and
+      // the last group clamp rows past the chunk to its last row and fold
+      // only the rows they own, so a short chunk still issues its loads at
+      // once.
+      std::ostringstream b;
+      auto group = [&](const std::string& ind, bool clamped, bool first) {
+        for (uint32_t u = 0; u < kUnroll; ++u) {
+          const std::string us = std::to_string(u);
+          if (clamped) {
+            b << ind << "const bool ok_" << us << " = r + " << us << "u * STEP < r_hi;\n";
+            b << ind << "const uint32_t rr_" << us << " = ok_" << us << " ? r + " << us << "u * STEP : r_hi - 1u;\n";
+            loads(b, ind, "rr_" + us, "_" + us);
+          } else {
+            loads(b, ind, "r + " + us + "u * STEP", "_" + us);
+          }
+        }
+        for (uint32_t u = 0; u < kUnroll; ++u)
+          fold(b, ind, "_" + std::to_string(u), first && u == 0, clamped && !(first && u == 0) ? "ok_" + std::to_string(u) : "");
+      };
+      b << "  uint32_t r = r_lo + slot;\n  const bool has = r < r_hi;\n  if (has) {\n    {\n";
+      group("      ", true, true);
+      b << "    }\n    r += " << kUnroll << "u * STEP;\n";
+      b << "    for (; r + " << kUnroll - 1 << "u * STEP < r_hi; r += " << kUnroll << "u * STEP) {\n";
+      group("      ", false, false);
+      b << "    }\n    if (r < r_hi) {\n";
+      group("      ", true, false);
+      b << "    }\n  }\n";
+      o << b.str();
+    }
+    // Row slots meet in LDS: slot s holds rows r_lo + s + k STEP.
+    for (int ci : n.chains) {
+      const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+      o << "  __shared__ " << T << " red" << ci << "[W * 64u * V];\n";
+      o << "  if (has) {\n#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) red" << ci
+        << "[slot * (SL * V) + cg * V + q] = part" << ci << "[q];\n  }\n";
+    }
+    o << "  __syncthreads();\n";
+    o << "  const uint32_t nrow = r_hi - r_lo, nslot = nrow < STEP ? nrow : STEP;  // slots holding rows\n";
+    o << "  if (slot == 0u && cvec < VEC) {  // the threads of slot 0 (threadIdx.x < SL) finish\n";
+    o << "#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) {\n";
+    o << "      const uint32_t cq = cvec * V + q;  // this thread's output column (col0 + q)\n";
+    o << "      (void)cq;\n";
+    for (int ci : n.chains) {
+      const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+      o << "      " << T << " acc" << ci << " = red" << ci << "[cg * V + q];\n";
+      o << "      for (uint32_t s2 = 1u; s2 < nslot; ++s2) acc" << ci << " = comb" << ci << "(acc" << ci << ", red" << ci
+        << "[s2 * (SL * V) + cg * V + q]);\n";
+    }
+    o << "      if (P == 1u) {\n";
+    {
+      std::ostringstream b;
+      for (int ci : n.chains)
+        finish(b, "        ", ci, "acc" + std::to_string(ci), "nslot > 0u", "cq",
+               [&](int t) { return "cv" + std::to_string(t) + "[q]"; });
+      o << b.str();
+    }
+    o << "      } else {\n";
+    for (int ci : n.chains)
+      o << "        p" << ci << "[(static_cast<uint64_t>(p) * NCB + cbk) * (SPAN * V) + cg * V + q] = acc" << ci << ";\n";
+    o << "      }\n    }\n  }\n}\n";
+    // ---- merge of the P chunks: a block takes 64 consecutive outputs, its
+    // 16 waves fold chunks w, w + 16, ... (4 loads in flight, 64 outputs
+    // per load: one 256-byte segment), and the waves meet in LDS.
+    o << "template <uint32_t V>\n__device__ __forceinline__ void " << sym << "_merge(\n    " << sig << partSig
+      << ") {\n";
+    o << "  constexpr uint32_t RMIN = " << kRowsMin << "u, BLOCKS = " << kBlocks << "u, MW = " << kMergeWaves
+      << "u, SPAN = " << kSpan << "u;\n";
+    o << "  const uint32_t C = " << ExtentExpr(g_, geo.c) << ", R = " << ExtentExpr(g_, geo.r) << ";\n";
+    o << "  const uint32_t NOUT = " << ProductExpr(geo.outer) << ";\n";
+    o << "  const uint32_t VEC = C / V, CB = (VEC + SPAN - 1u) / SPAN, NCB = NOUT * CB;\n";
+    o << "  const uint32_t P = tca::hip::col_split(R, NCB, RMIN, BLOCKS);  // > 1: launched only then\n";
+    o << "  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;\n";
+    o << "  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 64u + lane;\n";
+    o << "  const bool active = i < static_cast<uint64_t>(NOUT) * C;\n";
+    o << "  const uint64_t ic = active ? i : 0u;  // lanes past the end read output 0 and store nothing\n";
+    o << "  const uint32_t ob = static_cast<uint32_t>(ic / C), cq = static_cast<uint32_t>(ic - static_cast<uint64_t>(ob) * C);\n";
+    o << "  const uint32_t cb = cq / (SPAN * V), within = cq - cb * (SPAN * V), cbk = ob * CB + cb;\n";
+    o << "  const uint64_t stride = static_cast<uint64_t>(NCB) * (SPAN * V);\n";
+    o << "  const uint64_t base = static_cast<uint64_t>(cbk) * (SPAN * V) + within;\n";
+    outerCoords("  ", "ob");
+    combs("  ");
+    const auto atq = coordFn("cq", "0u");
+    for (int t : outers)
+      o << "  const " << CType(g_.tensors[t].elem) << " os" << t << " = t" << t << "[" << Offset(t, opOf[t]->axes, atq)
+        << "];\n";
+    for (int ci : n.chains) {
+      const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+      const std::string A = "acc" + std::to_string(ci), pp = "p" + std::to_string(ci);
+      o << "  " << T << " " << A << " = " << T << "(0);\n";
+      o << "  if (w < P) {\n";
+      o << "    " << A << " = " << pp << "[static_cast<uint64_t>(w) * stride + base];\n";
+      o << "    uint32_t k = w + MW;\n";
+      o << "    for (; k + 3u * MW < P; k += 4u * MW) {\n";
+      for (int u = 0; u < 4; ++u)
+        o << "      const " << T << " m" << u << " = " << pp << "[static_cast<uint64_t>(k + " << u << "u * MW) * stride + base];\n";
+      for (int u = 0; u < 4; ++u) o << "      " << A << " = comb" << ci << "(" << A << ", m" << u << ");\n";
+      o << "    }\n";
+      o << "    for (; k < P; k += MW) " << A << " = comb" << ci << "(" << A << ", " << pp
+        << "[static_cast<uint64_t>(k) * stride + base]);\n";
+      o << "  }\n";
+      o << "  __shared__ " << T << " mred" << ci << "[MW * 64u];\n";
+      o << "  if (w < P) mred" << ci << "[w * 64u + lane] = " << A << ";\n";
+    }
+    o << "  __syncthreads();\n";
+    o << "  if (w != 0u || !active) return;\n";
+    o << "  const uint32_t nw = P < MW ? P : MW;  // waves holding chunks (every one of them holds >= 1)\n";
+    {
+      std::ostringstream b;
+      for (int ci : n.chains) {
+        const std::string A = "acc" + std::to_string(ci);
+        b << "  for (uint32_t s2 = 1u; s2 < nw; ++s2) " << A << " = comb" << ci << "(" << A << ", mred" << ci
+          << "[s2 * 64u + lane]);\n";
+        finish(b, "  ", ci, A, "true", "cq", [&](int t) {
+          return "t" + std::to_string(t) + "[" + Offset(t, opOf[t]->axes, atq) + "]";
+        });
+      }
+      o << b.str();
+    }
+    o << "}\n";
+    // ---- one (partial, merge) pair per vector width
+    const std::string args = CallArgs(n);
+    const std::string cdim = g_.dims[geo.c].name, rdim = g_.dims[geo.r].name;
+    struct Width {
+      uint32_t v, mod, rem;
+    };
+    std::vector<Width> widths;
+    {
+      widths.push_back({vmax, vmax, 0});
+      for (uint32_t v = vmax / 2; v >= 1; v /= 2) widths.push_back({v, 2 * v, v});
+      const uint64_t ext = g_.dims[geo.c].extent;
+      if (ext > 0) {  // a compile-time row length: only its width
+        std::vector<Width> one;
+        for (const auto& w : widths)
+          if (ext % w.mod == w.rem) one.push_back(w);
+        widths = one;
+      }
+    }
+    const std::string outerTerm = DimProduct(geo.outer) + "/1";
+    for (const auto& wd : widths) {
+      const std::string cbTerm = cdim + "/" + std::to_string(kSpan * wd.v);
+      const std::string splitRec = rdim + " " + std::to_string(kRowsMin) + " " + std::to_string(kBlocks);
+      for (int merge = 0; merge <= 1; ++merge) {
+        PlanKernel k = pk;
+        k.symbol = sym + (merge ? "_m" : "_p") + std::to_string(wd.v);
+        k.block = merge ? 64 * kMergeWaves : 256;
+        for (const auto& nm : partNames) k.args.push_back("ptr " + nm);
+        if (merge) k.grid.push_back(DimProduct([&] {
+          std::vector<int> a(geo.outer);
+          a.push_back(geo.c);
+          return a;
+        }()) + "/64");
+        else {
+          k.grid.push_back(outerTerm);
+          k.grid.push_back(cbTerm);
+        }
+        k.split = splitRec + " " + std::to_string(merge) + " 2 " + outerTerm + " " + cbTerm;
+        if (g_.dims[geo.c].extent == 0)
+          k.when.push_back(cdim + " 0 4294967295 " + std::to_string(wd.mod) + " " + std::to_string(wd.rem));
+        o << "extern \"C\" __global__ void __launch_bounds__(" << k.block << ") " << k.symbol << "(\n    " << sig << partSig
+          << ") {\n  " << sym << (merge ? "_merge" : "_part") << "<" << wd.v << "u>(" << args << partArgs << ");\n}\n";
+        std::ostringstream det;
+        det << "reduce @" << rdim << " per column of @" << cdim << " vec=" << wd.v
+            << (g_.dims[geo.c].extent == 0 ? " (" + cdim + " % " + std::to_string(wd.mod) + " == " +
+                                                  std::to_string(wd.rem) + ")"
+                                            : std::string())
+            << (merge ? " merge: 64 outputs per block, 16 waves over the P chunks (P > 1 only)"
+                      : " partial: 64 column vectors x a chunk of rows per block, P = col_split");
+        AddKernel(k, Family::Col, n.chains, det.str());
+      }
+    }
+    o << "\n";
+    return true;
+  }
+
   bool EmitGemmNest(int ni, std::string* err) {
     const Nest& n = an_.nests[ni];
     const ir::Chain& c = g_.chains[n.chains[0]];
@@ -1913,6 +2385,7 @@ class Emitter {
       p << "\n";
       for (const auto& a : k.args) p << "arg " << a << "\n";
       if (!k.pack.empty()) p << "pack " << k.pack << "\n";
+      if (!k.split.empty()) p << "split " << k.split << "\n";
       for (const auto& w : k.when) p << "when " << w << "\n";
     }
     p << "end\n";

@@ -212,6 +212,19 @@ __device__ __forceinline__ uint32_t pack_lanes_log2(uint32_t vecs, uint32_t per_
   return ls;
 }
 
+// Row chunks P of a split column reduction (the plan's split record
+// computes the same number at launch): at least rows_min rows per chunk,
+// and no more chunks than keep col_blocks * P <= blocks; 1 when there are
+// no rows or the column blocks alone reach `blocks`.
+__device__ __forceinline__ uint32_t col_split(uint32_t rows, uint32_t col_blocks, uint32_t rows_min,
+                                              uint32_t blocks) {
+  if (rows == 0u || col_blocks == 0u) return 1u;
+  uint32_t p = (rows + rows_min - 1u) / rows_min;
+  const uint32_t cap = blocks / col_blocks;
+  if (p > cap) p = cap;
+  return p ? p : 1u;
+}
+
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
 __device__ __forceinline__ uint32_t wave_id() { return threadIdx.x >> 6; }
 

@@ -224,6 +224,24 @@ bool Parse(const std::string& text, Plan* out, std::string* err) {
       if (k.pack_epl == 0 || k.pack_min_block == 0 || k.pack_min_block > k.block || (k.block & (k.block - 1)) != 0 ||
           k.pack_min_block % 64 != 0)
         return bad("bad pack on " + tok[1] + " (power-of-two block, 64 <= min block <= block)");
+    } else if (kw == "split") {
+      if (p.kernels.empty()) return bad("split before any kernel");
+      Kernel& k = p.kernels.back();
+      uint64_t merge = 0, nt = 0;
+      if (tok.size() < 6 || !ParseU64(tok[2], &k.split_rows_min) || !ParseU64(tok[3], &k.split_blocks) ||
+          !ParseU64(tok[4], &merge) || !ParseU64(tok[5], &nt) || tok.size() != 6 + nt)
+        return bad("split <dim> <rows-min> <blocks> <merge> <n-terms> <term>...");
+      k.split_dim = FindDim(p, tok[1]);
+      if (k.split_dim < 0) return bad("split names unknown dim " + tok[1]);
+      if (k.split_rows_min == 0 || k.split_blocks == 0 || merge > 1) return bad("bad split on " + tok[1]);
+      k.split_merge = merge == 1;
+      for (uint64_t i = 0; i < nt; ++i) {
+        Term t;
+        std::string e;
+        if (!ParseTerm(p, tok[6 + i], &t, &e)) return bad(e);
+        if (t.packed) return bad("a split term cannot divide by 'pack'");
+        k.split_terms.push_back(t);
+      }
     } else if (kw == "when") {
       if (p.kernels.empty()) return bad("when before any kernel");
       Guard g;
@@ -253,6 +271,49 @@ bool Parse(const std::string& text, Plan* out, std::string* err) {
   return true;
 }
 
+namespace {
+
+std::string TermText(const Plan& p, const Term& t) {
+  std::ostringstream o;
+  bool first = true;
+  if (t.const_factor != 1 || t.dim_factors.empty()) {
+    o << t.const_factor;
+    first = false;
+  }
+  for (int d : t.dim_factors) {
+    if (!first) o << "*";
+    o << p.dims[d].name;
+    first = false;
+  }
+  if (t.packed) o << "/pack";
+  else o << "/" << t.divisor;
+  if (t.cap != 0) o << ":" << t.cap;
+  return o.str();
+}
+
+// ceil(product of the term's factors / divisor), limited to the cap; the
+// divisor of a packed term is the kernel's rows per block.
+uint64_t TermValue(const Kernel& k, const Term& t, const std::vector<uint32_t>& dims, bool* overflow) {
+  uint64_t prod = t.const_factor;
+  for (int d : t.dim_factors) {
+    prod *= dims[d];
+    if (prod > (1ull << 62)) {
+      *overflow = true;
+      return 0;
+    }
+  }
+  uint64_t div = t.divisor;
+  if (t.packed) {
+    uint32_t block = 0;
+    div = PackRows(k, dims, &block);
+  }
+  uint64_t q = (prod + div - 1) / div;
+  if (t.cap != 0 && q > t.cap) q = t.cap;
+  return q;
+}
+
+}  // namespace
+
 std::string Serialize(const Plan& p) {
   std::ostringstream o;
   o << "tca-plan 1\nprogram " << p.name << "\n";
@@ -266,22 +327,7 @@ std::string Serialize(const Plan& p) {
   for (const auto& s : p.scalars) o << "scalar " << s.name << " " << DtypeName(s.dtype) << "\n";
   for (const auto& k : p.kernels) {
     o << "kernel " << k.symbol << " " << k.block << " " << k.lds << " " << k.grid.size();
-    for (const auto& t : k.grid) {
-      o << " ";
-      bool first = true;
-      if (t.const_factor != 1 || t.dim_factors.empty()) {
-        o << t.const_factor;
-        first = false;
-      }
-      for (int d : t.dim_factors) {
-        if (!first) o << "*";
-        o << p.dims[d].name;
-        first = false;
-      }
-      if (t.packed) o << "/pack";
-      else o << "/" << t.divisor;
-      if (t.cap != 0) o << ":" << t.cap;
-    }
+    for (const auto& t : k.grid) o << " " << TermText(p, t);
     o << "\n";
     for (const auto& a : k.args) {
       if (a.kind == ArgKind::Ptr) o << "arg ptr " << p.tensors[a.index].name << "\n";
@@ -290,6 +336,12 @@ std::string Serialize(const Plan& p) {
     }
     if (k.pack_dim >= 0)
       o << "pack " << p.dims[k.pack_dim].name << " " << k.pack_epl << " " << k.pack_min_block << "\n";
+    if (k.split_dim >= 0) {
+      o << "split " << p.dims[k.split_dim].name << " " << k.split_rows_min << " " << k.split_blocks << " "
+        << (k.split_merge ? 1 : 0) << " " << k.split_terms.size();
+      for (const auto& t : k.split_terms) o << " " << TermText(p, t);
+      o << "\n";
+    }
     for (const auto& g : k.when)
       o << "when " << p.dims[g.dim].name << " " << g.lo << " " << g.hi << " " << g.mod << " " << g.rem << "\n";
   }
@@ -393,23 +445,23 @@ size_t TensorBytes(const Plan& p, size_t tensor, const std::vector<uint32_t>& di
 bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims, uint64_t* grid, std::string* err) {
   (void)p;
   uint64_t g = 1;
+  bool overflow = false;
   for (const auto& t : k.grid) {
-    uint64_t prod = t.const_factor;
-    for (int d : t.dim_factors) {
-      prod *= dims[d];
-      if (prod > (1ull << 62)) {
-        *err = "kernel " + k.symbol + ": grid term overflows";
-        return false;
-      }
+    const uint64_t q = TermValue(k, t, dims, &overflow);
+    if (overflow) {
+      *err = "kernel " + k.symbol + ": grid term overflows";
+      return false;
     }
-    uint64_t div = t.divisor;
-    if (t.packed) {
-      uint32_t block = 0;
-      div = PackRows(k, dims, &block);
-    }
-    uint64_t q = (prod + div - 1) / div;
-    if (t.cap != 0 && q > t.cap) q = t.cap;
     g *= q;
+    if (g > (1ull << 62)) {
+      *err = "kernel " + k.symbol + ": grid overflows";
+      return false;
+    }
+  }
+  if (k.split_dim >= 0) {
+    const uint64_t chunks = SplitChunks(k, dims);
+    if (k.split_merge) g = chunks > 1 ? g : 0;
+    else g *= chunks;
     if (g > (1ull << 62)) {
       *err = "kernel " + k.symbol + ": grid overflows";
       return false;
@@ -417,6 +469,22 @@ bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims,
   }
   *grid = g;
   return true;
+}
+
+uint64_t SplitChunks(const Kernel& k, const std::vector<uint32_t>& dims) {
+  if (k.split_dim < 0) return 1;
+  uint64_t blocks = 1;
+  bool overflow = false;
+  for (const auto& t : k.split_terms) {
+    blocks *= TermValue(k, t, dims, &overflow);
+    if (overflow || blocks > (1ull << 62)) return 1;  // far more column blocks than the target: no split
+  }
+  const uint64_t rows = dims[k.split_dim];
+  if (rows == 0 || blocks == 0) return 1;
+  uint64_t chunks = (rows + k.split_rows_min - 1) / k.split_rows_min;
+  const uint64_t cap = k.split_blocks / blocks;
+  if (chunks > cap) chunks = cap;
+  return chunks ? chunks : 1;
 }
 
 uint32_t PackRows(const Kernel& k, const std::vector<uint32_t>& dims, uint32_t* block) {

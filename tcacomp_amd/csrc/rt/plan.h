@@ -17,6 +17,12 @@
 //       `dim` elements: S lanes share a row, S the smallest power of two <= the
 //       kernel's block with S * epl >= dim; it launches with max(min-block, S)
 //       lanes per block, max(min-block, S) / S rows each
+//   split <rdim> <rows-min> <blocks> <merge> <n-terms> <term>...    (for the last
+//       kernel) a reduction over `rdim` split into P row chunks: with B the
+//       product of the terms (the column blocks), P = 1 when rdim or B is 0,
+//       else min(ceil(rdim / rows-min), max(1, blocks / B)). merge 0: the
+//       grid is multiplied by P; merge 1: the kernel (the merge of the P
+//       partials) launches only when P > 1.
 //   when <dim> <lo> <hi> <mod> <rem>    (for the last kernel) the kernel runs only
 //       when lo <= dim <= hi and dim % mod == rem; every guard of a kernel must
 //       hold. Variants of one nest specialised on a run-time dim carry guards
@@ -88,6 +94,10 @@ struct Kernel {
   std::vector<Guard> when;
   int pack_dim = -1;  // >= 0: a packed row kernel (block chosen at launch)
   uint64_t pack_epl = 0, pack_min_block = 0;
+  int split_dim = -1;  // >= 0: a row-split reduction (see the split record)
+  uint64_t split_rows_min = 0, split_blocks = 0;
+  bool split_merge = false;
+  std::vector<Term> split_terms;
 };
 
 struct Plan {
@@ -119,6 +129,8 @@ bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims,
 // Rows per block of a packed kernel (1 otherwise); *block receives the
 // launch block size.
 uint32_t PackRows(const Kernel& k, const std::vector<uint32_t>& dims, uint32_t* block);
+// Row chunks P of a split kernel (1 for a kernel without a split record).
+uint64_t SplitChunks(const Kernel& k, const std::vector<uint32_t>& dims);
 // Whether every guard of k holds for the bound dims.
 bool Selected(const Kernel& k, const std::vector<uint32_t>& dims);
 // Packs the kernel arguments per the HIP kernarg ABI (natural alignment):

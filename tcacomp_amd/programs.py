@@ -217,6 +217,47 @@ def row_sum_u8(cols=1000):
     return b.Build()
 
 
+def col_sum_max():
+    """Column sum and max of f32 x [R, C] (both dims run-time): reductions
+    over the non-contiguous axis, written As(C, R) so the reduce drops R (the
+    reference's middle-axis form, testing/kernels/runtime/row_sum.tca)."""
+    b = NewBuilder("col_sum_max_dyn")
+    R, C = b.Dim("R", 0), b.Dim("C", 0)
+    x = b.Tensor("x", TF32, R, C)
+    s = b.Tensor("sum", TF32, C)
+    m = b.Tensor("max", TF32, C)
+    b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(C, R).Reduce(b.Float32(0), _sum(b)).Store(s, C)
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(C, R)
+     .Reduce(_neg_inf(b), lambda acc, v: Call("fmaxf", acc, v)).Store(m, C))
+    return b.Build()
+
+
+def col_mean_bf16():
+    """Per (batch, column) scaled sum of bf16 x [B, R, C] over R, plus a
+    column offset: out[b, c] = sum_r f32(x[b, r, c]) * scale + g[c]."""
+    b = NewBuilder("col_mean_bf16")
+    B, R, C = b.Dim("B", 0), b.Dim("R", 0), b.Dim("C", 0)
+    x = b.Tensor("x", TBF16, B, R, C)
+    g = b.Tensor("g", TF32, C)
+    out = b.Tensor("out", TF32, B, C)
+    scale = b.ScalarParam("scale", TF32)
+    (b.Stmt().Iter(B, R, C).Map([At(x, B, R, C)], lambda v: Cast(v, TF32)).As(B, C, R)
+     .Reduce(b.Float32(0), _sum(b))
+     .Map([At(g, C)], lambda v, gg: b.Add(b.Mul(v, scale), gg)).As(B, C).Store(out, B, C))
+    return b.Build()
+
+
+def col_sum_u8():
+    """Column sums of bytes u8 x [R, C] into u32 (16-element vectors)."""
+    b = NewBuilder("col_sum_u8")
+    R, C = b.Dim("R", 0), b.Dim("C", 0)
+    x = b.Tensor("x", TU8, R, C)
+    s = b.Tensor("sum", TU32, C)
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: Cast(v, TU32)).As(C, R)
+     .Reduce(b.UInt32(0), lambda acc, v: b.Add(acc, v)).Store(s, C))
+    return b.Build()
+
+
 # Expression-layer parity programs: one output per expression over [N]
 # operands, so every operator, builtin and cast of the DSL (pkg/expr.go:
 # 140-341, internal/ir/builtins.go:25-33) runs on the device.
@@ -457,6 +498,9 @@ SUITE = {
 # variants (fusion and MFMA disabled) exist so tests can check every family
 # against the same oracle.
 CONFIG_PROGRAMS = {
+    "col_sum_max_dyn": col_sum_max,
+    "col_mean_bf16": col_mean_bf16,
+    "col_sum_u8": col_sum_u8,
     "scale_relu": scale_relu,
     "scale_relu_map": scale_relu_map,
     "row_sum_max_8192": lambda: row_sum_max(8192),

@@ -135,6 +135,44 @@ def test_narrow_stream_variant_selection(prog, dtype, R, C, variants):
     assert [s for s, f in zip(syms, out) if f] == ["tca_%s_k0_%s" % (prog, v) for v in variants]
 
 
+@pytest.mark.parametrize("R,C,variant,part_grid,merge_grid", [
+    (8192, 8192, 4, 32 * 32, 128),     # 32 column blocks (64 vectors each) x P = min(128, 1024 / 32) row chunks
+    (65536, 1024, 4, 4 * 256, 16),     # P = min(1024, 256); the merge takes 64 outputs per block
+    (1024, 65536, 4, 256 * 4, 1024),   # P = min(16, 4)
+    (16, 4 << 20, 4, 16384, 0),        # the column blocks alone exceed 1024: P = 1, no merge
+    (100, 3, 1, 2, 1),                 # odd columns: 1-element vectors; P = min(2, 1024)
+    (64, 1022, 2, 8, 0),               # C % 4 == 2: 511 vectors, 8 column blocks; P = min(1, 128) = 1
+    (0, 100, 4, 1, 0),                 # no rows: one chunk, init stored
+    (100, 0, 4, 0, 0)])                # no columns: nothing runs
+def test_col_split_geometry(R, C, variant, part_grid, merge_grid):
+    """Column family: P row chunks per column block (>= 64 rows each, at most
+    1024 blocks in all), the merge launched only when P > 1."""
+    e = programs.CONFIG_PROGRAMS["col_sum_max_dyn"]().emit()
+    assert set(e.families()) == {"col"}
+    rc, h = parse(e.plan)
+    assert rc == 0, _lib.last_error()
+    P = 0x1000
+    arr = compiler._descriptors([TensorDesc(P if R * C else 0, (R, C), 0), TensorDesc(P if C else 0, (C,), 0),
+                                 TensorDesc(P if C else 0, (C,), 0)])
+    syms = e.kernel_symbols()
+    out = (ctypes.c_uint8 * len(syms))()
+    grids = (ctypes.c_uint64 * len(syms))()
+    assert _lib.lib().tca_program_selected(h, arr, 3, None, 0, out, grids, None, len(syms)) == 0, _lib.last_error()
+    sel = {s: g for s, f, g in zip(syms, out, grids) if f}
+    base = "tca_col_sum_max_dyn_k0_"
+    assert sel == {base + "p%d" % variant: part_grid, base + "m%d" % variant: merge_grid}, sel
+
+
+def test_split_record_parse():
+    for rec, ok in [("split M 64 2048 0 1 N/256", True), ("split M 64 2048 1 2 1/1 N/4", True),
+                    ("split Q 64 2048 0 1 N/256", False), ("split M 0 2048 0 1 N/256", False),
+                    ("split M 64 0 0 1 N/256", False), ("split M 64 2048 2 1 N/256", False),
+                    ("split M 64 2048 0 2 N/256", False), ("split M 64 2048 0 1 N/pack", False),
+                    ("split M 64 2048 0 1 Q/4", False)]:
+        rc, _ = parse(PLAN.replace("arg scalar a\n", "arg scalar a\n%s\n" % rec))
+        assert (rc == 0) == ok, (rec, _lib.last_error())
+
+
 @pytest.mark.parametrize("R,C,part_grid,merge_grid", [(1, 16388, 2, 1), (3, 10**6, 3 * 62, 1),
                                                       (255, 8 * 10**6, 255 * 489, 64), (1, 4 * 10**8, 512, 1)])
 def test_split_geometry(R, C, part_grid, merge_grid):
@@ -301,6 +339,8 @@ EXPECTED_FAMILIES = {
     "layernorm_dyn": ["stream"] * 6, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 6,
     # narrow rows: one more width per halving of the element size (8 bf16, 16 u8 elements per vector)
     "row_sum_bf16_dyn": ["stream"] * 16, "row_sum_u8_dyn": ["stream"] * 20, "row_stats_u32_dyn": ["stream"] * 12,
+    # column reductions: a (partial, merge) pair per vector width
+    "col_sum_max_dyn": ["col"] * 6, "col_mean_bf16": ["col"] * 8, "col_sum_u8": ["col"] * 10,
 }
 
 

@@ -1,0 +1,75 @@
+"""The column family on the device: reductions over a non-contiguous axis
+(As(C, R) drops R; the reference's middle-axis reductions,
+testing/kernels/runtime/row_sum.tca), at shapes that reach every path:
+no rows or no columns, narrow rows (several rows per wave step), every
+vector width, one row chunk (the partial kernel stores) and many (partials,
+then the merge), several batch indices.
+
+Expected values: integer-valued f32 inputs keep every sum exact (partial
+sums below 2^24), so the device matches the float64 sum rounded once, bit
+for bit, in any fold order; max is exact; u8 -> u32 sums are exact;
+col_mean_bf16's piped map is one rounded multiply and one rounded add on
+both sides."""
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import CANARY, compiled, run, to_dev
+from tcacomp_amd.compiler import TensorDesc
+
+pytestmark = pytest.mark.gpu
+
+U32 = 4
+
+SHAPES = [(0, 5), (5, 0), (1, 1), (3, 7), (100, 3), (1000, 16), (64, 8192), (8192, 8192), (65536, 1024),
+          (2, 1 << 20), (300, 1022), (4097, 513), (70000, 12)]
+
+
+def _ints(shape, bound, seed):
+    return np.random.default_rng(seed).integers(-bound, bound + 1, size=shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("R,C", SHAPES)
+def test_col_sum_max(gpu, R, C):
+    print("col_sum_max", R, C, flush=True)
+    sys.stdout.flush()
+    x = _ints((R, C), 8, R * 7 + C)
+    s = to_dev(np.full(C, CANARY, np.float32), gpu)
+    m = to_dev(np.full(C, CANARY, np.float32), gpu)
+    run(compiled("col_sum_max_dyn"), [to_dev(x, gpu), s, m])
+    assert np.abs(x).sum(axis=0).max(initial=0) < 2 ** 24  # exact sums
+    want_s = x.astype(np.float64).sum(axis=0).astype(np.float32)
+    want_m = np.max(x, axis=0, initial=-np.inf).astype(np.float32)
+    np.testing.assert_array_equal(s.cpu().numpy(), want_s)
+    np.testing.assert_array_equal(m.cpu().numpy(), want_m)
+
+
+@pytest.mark.parametrize("B,R,C", [(1, 1, 8), (2, 1000, 520), (3, 5, 8), (4, 300, 4100), (2, 0, 16),
+                                   (5, 2000, 6), (1, 20000, 2048)])
+def test_col_mean_bf16(gpu, B, R, C):
+    import torch
+    print("col_mean_bf16", B, R, C, flush=True)
+    sys.stdout.flush()
+    x = _ints((B, R, C), 8, B * 31 + R * 7 + C)  # small integers: exact in bf16
+    g = _ints((C,), 3, 1) * np.float32(0.5)
+    scale = 0.125
+    out = to_dev(np.full((B, C), CANARY, np.float32), gpu)
+    xd = torch.from_numpy(x).to(gpu).to(torch.bfloat16)
+    run(compiled("col_mean_bf16"), [xd, to_dev(g, gpu), out], scalars=[scale])
+    ssum = x.astype(np.float64).sum(axis=1).astype(np.float32)
+    want = ssum * np.float32(scale) + g[None, :]
+    np.testing.assert_array_equal(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("R,C", [(1, 16), (7, 33), (5000, 4096), (300, 1000), (100000, 48), (3, 1 << 20),
+                                 (0, 64)])
+def test_col_sum_u8(gpu, R, C):
+    import torch
+    print("col_sum_u8", R, C, flush=True)
+    sys.stdout.flush()
+    x = np.random.default_rng(R + C).integers(0, 256, size=(R, C), dtype=np.uint8)
+    o = torch.full((C,), 0x5A5A5A5A, dtype=torch.int32, device=gpu)
+    run(compiled("col_sum_u8"), [to_dev(x, gpu), TensorDesc(o.data_ptr(), (C,), U32)])
+    want = (x.astype(np.uint64).sum(axis=0) % (1 << 32)).astype(np.uint32)
+    np.testing.assert_array_equal(o.cpu().numpy().view(np.uint32), want)
