@@ -1822,10 +1822,16 @@ class Emitter {
         const int st = c.store_tensor;
         const std::string T = CType(g_.exprs[c.root.fn.body].type);
         const std::string A = "m" + std::to_string(ci), H = "h" + std::to_string(ci);
+        // P <= PMAX = 8 x 64: each lane's (at most 8) partials are loaded at
+        // once, indices clamped into the row's partials, then folded in order.
         o << "  " << T << " " << A << " = " << T << "(0);\n  bool " << H << " = false;\n";
-        o << "  for (uint32_t i = lane; i < P; i += 64u) {\n";
-        o << "    const " << T << " pv = p" << ci << "[static_cast<uint64_t>(r) * PMAX + i];\n";
-        o << "    " << A << " = " << H << " ? comb" << ci << "(" << A << ", pv) : pv;\n    " << H << " = true;\n  }\n";
+        o << "  {\n    " << T << " pv[PMAX / 64u];\n";
+        o << "#pragma unroll\n    for (uint32_t k = 0; k < PMAX / 64u; ++k)\n";
+        o << "      pv[k] = p" << ci << "[static_cast<uint64_t>(r) * PMAX + min(lane + 64u * k, P - 1u)];\n";
+        o << "#pragma unroll\n    for (uint32_t k = 0; k < PMAX / 64u; ++k) {\n";
+        o << "      if (lane + 64u * k < P) {\n";
+        o << "        " << A << " = " << H << " ? comb" << ci << "(" << A << ", pv[k]) : pv[k];\n        " << H
+          << " = true;\n      }\n    }\n  }\n";
         o << "  " << A << " = tca::hip::wave_allreduce_present(" << A << ", " << H << ", comb" << ci << ");\n";
         o << "  if (lane == 0u) {\n";
         const ir::ReduceStage& rs = c.reduces[0];
