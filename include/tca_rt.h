@@ -145,8 +145,10 @@ int tca_program_selected(tca_program p, const tca_tensor* tensors, uint32_t n_te
                          uint64_t* grids, uint32_t* blocks, uint32_t n_selected);
 /* Checks the contract, then launches, in order on `stream`, every kernel of
  * the program whose launch guards hold. Scalars are passed as doubles in declaration order and converted
- * to their declared types. Locals that live in HBM use a workspace the
- * program allocates on first need and keeps. */
+ * to their declared types. Locals that live in HBM (and the partials of
+ * split reductions) use a workspace the program allocates on first need per
+ * stream and keeps until unload: launches of one program on different
+ * streams may overlap safely. Thread-safe for distinct streams. */
 int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tensors,
                        const uint32_t* free_dims, uint32_t n_free_dims,
                        const double* scalars, uint32_t n_scalars, tca_stream_t stream);

@@ -17,6 +17,7 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <map>
 #include <mutex>
 #include <sstream>
 #include <string>
@@ -104,12 +105,18 @@ struct tca_event_s {
 };
 
 struct tca_program_s {
+  struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+  };
   tca::plan::Plan plan;
   hipModule_t mod = nullptr;
   std::vector<hipFunction_t> funcs;
-  void* workspace = nullptr;
-  size_t workspace_bytes = 0;
-  std::mutex mu;  // guards the workspace
+  // HBM locals and partial scratch, one workspace per stream the program is
+  // launched on: launches on one stream are ordered and may share it,
+  // launches on different streams may overlap and must not.
+  std::map<tca_stream_t, Workspace> workspaces;
+  std::mutex mu;  // guards `workspaces`
 };
 
 extern "C" {
@@ -331,9 +338,10 @@ int tca_program_load(const char* hsaco_path, const char* plan_text, tca_program*
 int tca_program_unload(tca_program p) {
   if (p == nullptr) return TCA_OK;
   int rc = TCA_OK;
-  if (p->workspace != nullptr) {
-    hipError_t e = hipFree(p->workspace);
-    if (e != hipSuccess) rc = hip_fail(e, "hipFree(workspace)");
+  for (auto& kv : p->workspaces) {
+    if (kv.second.ptr == nullptr) continue;
+    hipError_t e = hipFree(kv.second.ptr);
+    if (e != hipSuccess && rc == TCA_OK) rc = hip_fail(e, "hipFree(workspace)");
   }
   if (p->mod != nullptr) {
     hipError_t e = hipModuleUnload(p->mod);
@@ -427,18 +435,19 @@ int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tens
   void* ws = nullptr;
   if (ws_bytes > 0) {
     std::lock_guard<std::mutex> lk(p->mu);
-    if (p->workspace_bytes < ws_bytes) {
-      if (p->workspace != nullptr) {
-        // The previous workspace may still be read by queued kernels.
-        TCA_HIP_TRY(hipDeviceSynchronize());
-        TCA_HIP_TRY(hipFree(p->workspace));
-        p->workspace = nullptr;
-        p->workspace_bytes = 0;
+    tca_program_s::Workspace& w = p->workspaces[stream];
+    if (w.bytes < ws_bytes) {
+      if (w.ptr != nullptr) {
+        // Kernels queued on this stream may still use the smaller workspace.
+        TCA_HIP_TRY(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+        TCA_HIP_TRY(hipFree(w.ptr));
+        w.ptr = nullptr;
+        w.bytes = 0;
       }
-      TCA_HIP_TRY(hipMalloc(&p->workspace, ws_bytes));
-      p->workspace_bytes = ws_bytes;
+      TCA_HIP_TRY(hipMalloc(&w.ptr, ws_bytes));
+      w.bytes = ws_bytes;
     }
-    ws = p->workspace;
+    ws = w.ptr;
   }
 
   // Device pointer of each tensor slot (params from the caller, locals from

@@ -166,3 +166,39 @@ def test_error_paths(rt):
     rc = rt.tca_program_launch(h, arr, 3, None, 0, sc, 1, None)
     assert rc == _lib.TCA_ERR_SHAPE and "N" in _lib.last_error()
     _lib.check(rt.tca_rt_device_sync())  # the device is still healthy
+
+
+def test_one_program_on_two_streams(rt):
+    """A program whose kernels use its workspace (the column family's
+    partials) launched on two streams that overlap: each stream has a
+    workspace of its own, so both results are exact."""
+    R, C = 8192, 1024  # P = 256 row chunks per column block: partials, then the merge
+    rng = np.random.default_rng(11)
+    xs = [rng.integers(-8, 9, size=(R, C)).astype(np.float32) for _ in range(2)]
+    want = [(x.astype(np.float64).sum(axis=0).astype(np.float32), x.max(axis=0)) for x in xs]
+    prog = compiled("col_sum_max_dyn")
+    h = prog.load()
+    from tcacomp_amd.compiler import _descriptors
+    streams, bufs, descs = [], [], []
+    for x in xs:
+        s = ctypes.c_void_p()
+        _lib.check(rt.tca_rt_stream_create(ctypes.byref(s)))
+        dx, ds, dm = Dev(x.nbytes), Dev(C * 4), Dev(C * 4)
+        dx.put(x)
+        streams.append(s)
+        bufs.append((dx, ds, dm))
+        descs.append(_descriptors([TensorDesc(dx.p.value, (R, C), 0), TensorDesc(ds.p.value, (C,), 0),
+                                   TensorDesc(dm.p.value, (C,), 0)]))
+    for _ in range(20):  # interleaved, never synchronized in between
+        for s, arr in zip(streams, descs):
+            _lib.check(rt.tca_program_launch(h, arr, 3, None, 0, None, 0, s))
+    for s in streams:
+        _lib.check(rt.tca_rt_stream_sync(s))
+    for (dx, ds, dm), (ws, wm) in zip(bufs, want):
+        np.testing.assert_array_equal(ds.get((C,), np.float32), ws)
+        np.testing.assert_array_equal(dm.get((C,), np.float32), wm)
+    for s in streams:
+        _lib.check(rt.tca_rt_stream_destroy(s))
+    for b in bufs:
+        for d in b:
+            d.free()
