@@ -208,41 +208,47 @@ def evaluate_scalar(spec, tiles, col, row, scalars):
 
 
 def evaluate_grid(spec, x0, xt, col, row, scalars):
-    """Expected outputs of a grid spec (randprog.GridSpec): x0 [R, C] in the
-    work type, xt [C, R] (read at (c, r)), g [C], r [R] or None. `map`
-    stores y [R, C], `tmap` its transpose [C, R], `colreduce` folds over R
-    (the reduce drops the last live axis of As(C, R)) into [C]. Returns
-    ({output: array}, every float sum exact)."""
+    """Expected outputs of a grid spec (randprog.GridSpec): x0 [(B,) R, C] in
+    the work type, xt [(B,) C, R] (read at (c, r)), g [C], r [R] or None.
+    `map` stores y [(B,) R, C], `tmap` its transpose [(B,) C, R],
+    `colreduce` folds over R (the reduce drops the last live axis of
+    As((B,) C, R)) into [(B,) C]. Returns ({output: array}, every float sum
+    exact)."""
     elem = spec.elem
     dt = np.float32 if elem == "f32" else np.uint32
-    R, C = x0.shape
+    batch = getattr(spec, "batch", False)
+    if not batch:  # one batch index, dropped from the outputs
+        x0 = x0[None]
+        xt = None if xt is None else xt[None]
+    Bn, R, C = x0.shape
     env = {"x0": x0.astype(dt)}
     if xt is not None:
-        env["xt"] = xt.astype(dt).T
+        env["xt"] = np.swapaxes(xt.astype(dt), 1, 2)
     if col is not None:
-        env["g"] = col.astype(dt)[None, :]
+        env["g"] = col.astype(dt)[None, None, :]
     if row is not None:
-        env["r"] = row.astype(dt)[:, None]
+        env["r"] = row.astype(dt)[None, :, None]
     scal = {n: (_f32(v) if elem == "f32" else np.uint32(v)) for n, v in scalars.items()}
     env.update(scal)
     outs, exact = {}, True
     with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
         for st in spec.stmts:
-            val = np.array(np.broadcast_to(np.asarray(_eval(st["expr"], env, elem), dt), (R, C)), dt)
+            val = np.array(np.broadcast_to(np.asarray(_eval(st["expr"], env, elem), dt), (Bn, R, C)), dt)
             if st["kind"] == "map":
-                outs[st["out"]] = val
+                out = val
             elif st["kind"] == "tmap":
-                outs[st["out"]] = np.ascontiguousarray(val.T)
+                out = np.ascontiguousarray(np.swapaxes(val, 1, 2))
             else:
-                red, ok = _reduce(elem, st["comb"], np.ascontiguousarray(val.T))
+                red, ok = _reduce(elem, st["comb"], np.ascontiguousarray(np.swapaxes(val, 1, 2)))
                 exact = exact and ok
                 if st["piped"] is not None:
                     penv = dict(scal)
                     penv["v"] = red
                     if col is not None:
-                        penv["g"] = col.astype(dt)
-                    red = np.broadcast_to(np.asarray(_eval(st["piped"], penv, elem), dt), (C,))
-                outs[st["out"]] = np.array(red, dt)
+                        penv["g"] = col.astype(dt)[None, :]
+                    red = np.broadcast_to(np.asarray(_eval(st["piped"], penv, elem), dt), (Bn, C))
+                out = np.array(red, dt)
+            outs[st["out"]] = out if batch else out[0]
     return outs, exact
 
 
@@ -252,16 +258,20 @@ def evaluate_grid_scalar(spec, x0, xt, col, row, scalars):
     elem = spec.elem
     cast = _f32 if elem == "f32" else np.uint32
     dt = np.float32 if elem == "f32" else np.uint32
-    R, C = x0.shape
+    batch = getattr(spec, "batch", False)
+    if not batch:
+        x0 = x0[None]
+        xt = None if xt is None else xt[None]
+    Bn, R, C = x0.shape
     scal = {n: cast(v) for n, v in scalars.items()}
     combs = {"sum": lambda a, b: a + b, "xor": lambda a, b: a ^ b,
              "max": (lambda a, b: np.fmax(a, b)) if elem == "f32" else (lambda a, b: max(a, b)),
              "min": (lambda a, b: np.fmin(a, b)) if elem == "f32" else (lambda a, b: min(a, b))}
 
-    def env_at(r, c):
-        env = {"x0": cast(x0[r, c])}
+    def env_at(bb, r, c):
+        env = {"x0": cast(x0[bb, r, c])}
         if xt is not None:
-            env["xt"] = cast(xt[c, r])
+            env["xt"] = cast(xt[bb, c, r])
         if col is not None:
             env["g"] = cast(col[c])
         if row is not None:
@@ -273,27 +283,28 @@ def evaluate_grid_scalar(spec, x0, xt, col, row, scalars):
     with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
         for st in spec.stmts:
             if st["kind"] in ("map", "tmap"):
-                out = np.zeros((R, C) if st["kind"] == "map" else (C, R), dt)
-                for r in range(R):
+                out = np.zeros((Bn, R, C) if st["kind"] == "map" else (Bn, C, R), dt)
+                for bb in range(Bn):
+                    for r in range(R):
+                        for c in range(C):
+                            v = cast(_eval(st["expr"], env_at(bb, r, c), elem))
+                            if st["kind"] == "map":
+                                out[bb, r, c] = v
+                            else:
+                                out[bb, c, r] = v
+            else:
+                out = np.zeros((Bn, C), dt)
+                for bb in range(Bn):
                     for c in range(C):
-                        v = cast(_eval(st["expr"], env_at(r, c), elem))
-                        if st["kind"] == "map":
-                            out[r, c] = v
-                        else:
-                            out[c, r] = v
-                outs[st["out"]] = out
-                continue
-            out = np.zeros((C,), dt)
-            for c in range(C):
-                acc = _init(elem, st["comb"])
-                for r in range(R):
-                    acc = cast(combs[st["comb"]](acc, cast(_eval(st["expr"], env_at(r, c), elem))))
-                if st["piped"] is not None:
-                    penv = dict(scal)
-                    penv["v"] = acc
-                    if col is not None:
-                        penv["g"] = cast(col[c])
-                    acc = cast(_eval(st["piped"], penv, elem))
-                out[c] = acc
-            outs[st["out"]] = out
+                        acc = _init(elem, st["comb"])
+                        for r in range(R):
+                            acc = cast(combs[st["comb"]](acc, cast(_eval(st["expr"], env_at(bb, r, c), elem))))
+                        if st["piped"] is not None:
+                            penv = dict(scal)
+                            penv["v"] = acc
+                            if col is not None:
+                                penv["g"] = cast(col[c])
+                            acc = cast(_eval(st["piped"], penv, elem))
+                        out[bb, c] = acc
+            outs[st["out"]] = out if batch else out[0]
     return outs

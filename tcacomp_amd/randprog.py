@@ -322,16 +322,18 @@ class GridSpec:
 
     kind = "grid"
 
-    def __init__(self, name, elem, c, tiles, trans, col, row, scalars, stmts):
+    def __init__(self, name, elem, c, tiles, trans, col, row, scalars, stmts, batch=False):
         self.name, self.elem, self.c, self.tiles, self.trans = name, elem, c, tiles, trans
         self.col, self.row, self.scalars, self.stmts = col, row, scalars, stmts
+        self.batch = batch  # a leading batch axis B: x0 [B, R, C], xt [B, C, R], outputs per batch
 
     def outputs(self):
         return [s["out"] for s in self.stmts]
 
 
-def generate_grid(seed, elem, dynamic):
-    """The spec of random grid program `seed` (deterministic)."""
+def generate_grid(seed, elem, dynamic, batch=False):
+    """The spec of random grid program `seed` (deterministic); `batch` adds a
+    leading batch axis to every tile and output (g and r stay [C] and [R])."""
     rng = random.Random(0x6A09E667 ^ (seed * 0x9E3779B1))
     c = 0 if dynamic else rng.choice(STATIC_C[:8])
     if elem == "f32":
@@ -362,20 +364,21 @@ def generate_grid(seed, elem, dynamic):
         if not any(l in ("x0", "xt") for l in leaves(e)):
             e = ("add", ("leaf", rng.choice(["x0", "xt"] if trans else ["x0"])), e)
         stmts.append({"kind": kind, "expr": e, "comb": comb, "piped": piped, "out": "%s%d" % (kind[0], i)})
-    name = "grid_%s_%s_%d" % (elem, "dyn" if dynamic else "c%d" % c, seed)
-    return GridSpec(name, elem, c, tiles, trans, col, row, scalars, stmts)
+    name = "grid%s_%s_%s_%d" % ("3" if batch else "", elem, "dyn" if dynamic else "c%d" % c, seed)
+    return GridSpec(name, elem, c, tiles, trans, col, row, scalars, stmts, batch)
 
 
 def _build_grid(spec):
     b = NewBuilder(spec.name)
+    B = [b.Dim("B", 0)] if spec.batch else []
     R = b.Dim("R", 0)
     C = b.Dim("C", 0) if spec.c == 0 else b.Dim("e%d" % spec.c, spec.c)
     work = TF32 if spec.elem == "f32" else TU32
     ops = {}  # operand name -> (tensor, subscript axes, cast to the work type)
     x0_storage = spec.tiles[0][1]
-    ops["x0"] = (b.Tensor("x0", _ELEM[x0_storage], R, C), [R, C], x0_storage != spec.elem)
+    ops["x0"] = (b.Tensor("x0", _ELEM[x0_storage], *(B + [R, C])), B + [R, C], x0_storage != spec.elem)
     if spec.trans:
-        ops["xt"] = (b.Tensor("xt", work, C, R), [C, R], False)
+        ops["xt"] = (b.Tensor("xt", work, *(B + [C, R])), B + [C, R], False)
     if spec.col:
         ops["g"] = (b.Tensor("g", work, C), [C], False)
     if spec.row:
@@ -383,7 +386,7 @@ def _build_grid(spec):
     scal = {n: b.ScalarParam(n, work) for n, _ in spec.scalars}
     outs = {}
     for st in spec.stmts:
-        dims = {"map": (R, C), "tmap": (C, R), "colreduce": (C,)}[st["kind"]]
+        dims = {"map": B + [R, C], "tmap": B + [C, R], "colreduce": B + [C]}[st["kind"]]
         outs[st["out"]] = b.Tensor(st["out"], work, *dims)
 
     def fn_for(e, names, pre=()):
@@ -399,19 +402,19 @@ def _build_grid(spec):
     for st in spec.stmts:
         names = [n for n in leaves(st["expr"]) if n not in scal]
         operand_list = [At(ops[n][0], *ops[n][1]) for n in names]
-        chain = b.Stmt().Iter(R, C).Map(operand_list, fn_for(st["expr"], names))
+        chain = b.Stmt().Iter(*(B + [R, C])).Map(operand_list, fn_for(st["expr"], names))
         if st["kind"] == "map":
-            chain.As(R, C).Store(outs[st["out"]], R, C)
+            chain.As(*(B + [R, C])).Store(outs[st["out"]], *(B + [R, C]))
         elif st["kind"] == "tmap":
-            chain.As(R, C).Store(outs[st["out"]], C, R)
+            chain.As(*(B + [R, C])).Store(outs[st["out"]], *(B + [C, R]))
         else:
             init, comb = _init_comb(b, spec.elem, st["comb"])
-            chain = chain.As(C, R).Reduce(init, comb)
+            chain = chain.As(*(B + [C, R])).Reduce(init, comb)
             if st["piped"] is not None:
                 pnames = [n for n in leaves(st["piped"]) if n not in scal and n != "v"]
                 chain = chain.Map([At(ops[n][0], *ops[n][1]) for n in pnames],
-                                  fn_for(st["piped"], pnames, pre=("v",))).As(C)
-            chain.Store(outs[st["out"]], C)
+                                  fn_for(st["piped"], pnames, pre=("v",))).As(*(B + [C]))
+            chain.Store(outs[st["out"]], *(B + [C]))
     return b.Build()
 
 
@@ -431,6 +434,12 @@ GRID_PROGRAMS = ([("f32", True, s) for s in range(40, 46)] + [("f32", False, s) 
                  [("u32", True, s) for s in range(50, 53)] + [("u32", False, s) for s in range(53, 55)])
 
 
+# Random grid programs with a leading batch axis: (elem, dynamic row length, seed).
+GRID3_PROGRAMS = ([("f32", True, s) for s in range(60, 66)] + [("f32", False, s) for s in range(66, 68)] +
+                  [("u32", True, s) for s in range(68, 70)])
+
+
 def specs():
     return ([generate(seed, elem, dyn) for elem, dyn, seed in PROGRAMS] +
-            [generate_grid(seed, elem, dyn) for elem, dyn, seed in GRID_PROGRAMS])
+            [generate_grid(seed, elem, dyn) for elem, dyn, seed in GRID_PROGRAMS] +
+            [generate_grid(seed, elem, dyn, True) for elem, dyn, seed in GRID3_PROGRAMS])

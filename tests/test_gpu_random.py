@@ -144,8 +144,11 @@ def test_random_grid_program(gpu, spec):
     import torch
     prog = _program(spec, False)
     shapes = [(r, spec.c) for r in (1, 37, 300)] if spec.c else GRID_SHAPES
+    lead = (3,) if spec.batch else ()  # batch programs: three batch indices
     for R, C in shapes:
-        print("random", spec.name, (R, C), flush=True)
+        if spec.batch and R * C > (1 << 22):
+            continue
+        print("random", spec.name, lead + (R, C), flush=True)
         sys.stdout.flush()
         for bound in (8, 3, 1):
             rng = np.random.default_rng(zlib.crc32(("%s %d %d %d" % (spec.name, R, C, bound)).encode()))
@@ -153,10 +156,10 @@ def test_random_grid_program(gpu, spec):
                 gen = lambda *shape: rng.integers(-bound, bound + 1, size=shape).astype(np.float32)  # noqa: E731
             else:
                 gen = lambda *shape: rng.integers(0, 1 << 32, size=shape, dtype=np.uint64).astype(np.uint32)  # noqa: E731
-            x0 = gen(R, C)
+            x0 = gen(*lead, R, C)
             if spec.tiles[0][1] == "u8":
                 x0 = x0 & np.uint32(0xFF)
-            xt = gen(C, R) if spec.trans else None
+            xt = gen(*lead, C, R) if spec.trans else None
             g = gen(C) if spec.col else None
             r = gen(R) if spec.row else None
             want, exact = evaluate_grid(spec, x0, xt, g, r, dict(spec.scalars))
@@ -173,7 +176,7 @@ def test_random_grid_program(gpu, spec):
             args.append(desc or d)
         outs = {}
         for st in spec.stmts:
-            oshape = {"map": (R, C), "tmap": (C, R), "colreduce": (C,)}[st["kind"]]
+            oshape = lead + {"map": (R, C), "tmap": (C, R), "colreduce": (C,)}[st["kind"]]
             if spec.elem == "f32":
                 o = torch.full(oshape, CANARY, device=gpu)
                 args.append(o)
@@ -187,7 +190,7 @@ def test_random_grid_program(gpu, spec):
             got = o.cpu().numpy()
             if spec.elem == "u32":
                 got = got.view(np.uint32)
-            np.testing.assert_array_equal(got, want[name], err_msg="%s %s output %s" % (spec.name, (R, C), name))
+            np.testing.assert_array_equal(got, want[name], err_msg="%s %s output %s" % (spec.name, lead + (R, C), name))
         del keep, args, outs
 
 

@@ -19,7 +19,8 @@ def test_programs_are_deterministic_and_distinct():
     again = randprog.specs()
     assert [s.name for s in SPECS + GRIDS] == [s.name for s in again]
     assert [repr(s.stmts) for s in SPECS + GRIDS] == [repr(s.stmts) for s in again]
-    assert len({repr(s.stmts) for s in SPECS + GRIDS}) == len(again)
+    shape = lambda s: repr(sorted((k, v) for k, v in vars(s).items() if k != "name"))  # noqa: E731
+    assert len({shape(s) for s in SPECS + GRIDS}) == len(again)
 
 
 @pytest.mark.parametrize("spec", SPECS, ids=lambda s: s.name)
@@ -123,13 +124,14 @@ def test_inexact_sums_are_reported():
     assert not exact  # partial sums past 2^24
 
 
-def _grid_inputs(spec, R, C, seed):
+def _grid_inputs(spec, R, C, seed, B=2):
     rng = np.random.default_rng(seed)
     if spec.elem == "f32":
         gen = lambda *shape: rng.integers(-4, 5, size=shape).astype(np.float32)  # noqa: E731
     else:
         gen = lambda *shape: rng.integers(0, 1 << 32, size=shape, dtype=np.uint64).astype(np.uint32)  # noqa: E731
-    return (gen(R, C), gen(C, R) if spec.trans else None, gen(C) if spec.col else None,
+    lead = (B,) if spec.batch else ()
+    return (gen(*lead, R, C), gen(*lead, C, R) if spec.trans else None, gen(C) if spec.col else None,
             gen(R) if spec.row else None)
 
 
