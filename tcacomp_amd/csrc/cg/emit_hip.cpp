@@ -1960,8 +1960,9 @@ class Emitter {
   bool EmitCol(int ni, std::string* err) {
     // Swept on MI355X (column sum+max, [8192, 8192] .. [16, 4 Mi]): spans of
     // 64 vectors beat 256 (4.7-5.7 against 4.3-4.8 TB/s), a 1024-block
-    // split target beats 512 and 2048, and 8 rows in flight per thread gain
-    // 2% on [8192, 8192] but lose 20% on [16, 4 Mi] (clamped groups of 8).
+    // split target beats 512 and 2048, 8 rows in flight per thread gain 2%
+    // on [8192, 8192] but lose 20% on [16, 4 Mi] (clamped groups of 8), and
+    // two 16-byte vectors per thread and row (8 f32 columns) lose 11-25%.
     constexpr uint32_t kWaves = 4, kRowsMin = 64, kBlocks = 1024, kUnroll = 4, kMergeWaves = 16, kSpan = 64,
                        kLogSpan = 6;
     const Nest& n = an_.nests[ni];
