@@ -369,6 +369,11 @@ def gemm_bf16_nt():
     return _matmul("gemm_bf16_nt", TBF16, b_nk=True)
 
 
+def gemm_f32_nt():
+    """C5 fp32 with B given as [N][K]."""
+    return _matmul("gemm_f32_nt", TF32, b_nk=True)
+
+
 # ---- the reference suite (testing/kernels/**.tca) ------------------------
 
 def _rank3_reduce(name, k_extent, body, scalars=(), piped=None, piped_scalars=(), middle=False):
@@ -509,6 +514,7 @@ CONFIG_PROGRAMS = {
     "gemm_f32": gemm_f32,
     "gemm_bf16": gemm_bf16,
     "gemm_bf16_nt": gemm_bf16_nt,
+    "gemm_f32_nt": gemm_f32_nt,
     # small-row variants exercised by the parity tests (tails, few lanes per row)
     "row_sum_max_1000": lambda: row_sum_max(1000),
     "row_sum_max_64": lambda: row_sum_max(64),

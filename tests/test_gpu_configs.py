@@ -19,6 +19,7 @@ import pytest
 import oracle
 from helpers import (assert_reduce_close, canaries, compiled, host, out_dev, reduce_tol, run, to_dev)
 from tcacomp_amd import inputs
+from tcacomp_amd.compiler import TensorDesc
 from tcacomp_amd.pkg import EMIT_NO_FUSION, EMIT_NO_GEMM
 
 pytestmark = pytest.mark.gpu
@@ -259,6 +260,42 @@ def test_c5_gemm_exact_integers(gpu, M, N, K):
     run(compiled("gemm_bf16_nt"), [to_dev(ab.view(np.int16), gpu).view(torch.bfloat16),
                                    to_dev(bt.view(np.int16), gpu).view(torch.bfloat16), c])
     assert np.array_equal(host(c), want)
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 64), (4100, 4104, 40), (4352, 4096, 16), (4097, 4096, 33),
+                                   (4096, 4101, 48)])
+@pytest.mark.parametrize("nt", [False, True])
+def test_c5_gemm_f32_large_exact(gpu, M, N, K, nt):
+    """fp32 contractions at C5's scale with ragged edges (M, N not multiples
+    of the 128x128 tile, K not a multiple of the 16-deep slice, unaligned
+    rows), B as [K][N] and as [N][K]. Small-integer operands make every
+    result exact, so every tile, slice and edge must be exact."""
+    _say("C5 f32 large", M, N, K, "nt" if nt else "")
+    rng = np.random.default_rng(M + N + K)
+    a = rng.integers(-4, 5, (M, K)).astype(np.float32)
+    b = rng.integers(-4, 5, (K, N)).astype(np.float32)
+    want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)  # exact: small integers
+    name = "gemm_f32_nt" if nt else "gemm_f32"
+    p = compiled(name)
+    assert p.selected_symbols([TensorDesc(0x1000, (M, K), 0), TensorDesc(0x1000, (N, K) if nt else (K, N), 0),
+                               TensorDesc(0x1000, (M, N), 0)]) == ["tca_%s_k0" % name]
+    c = out_dev((M, N), gpu)
+    bd = np.ascontiguousarray(b.T) if nt else b
+    run(p, [to_dev(a, gpu), to_dev(bd, gpu), c])
+    assert np.array_equal(host(c), want)
+
+
+def test_c5_full_size_f32(gpu):
+    M = N = K = 4096
+    a = inputs.uniform((M, K), -1, 1, 0)
+    b = inputs.uniform((K, N), -1, 1, 1)
+    c = out_dev((M, N), gpu)
+    run(compiled("gemm_f32"), [to_dev(a, gpu), to_dev(b, gpu), c])
+    got = host(c)
+    rows = np.random.default_rng(2).choice(M, 16, replace=False)
+    want = oracle.gemm(np.ascontiguousarray(a[rows]), b, threads=8)
+    assert_reduce_close(got[rows], want, _gemm_bound(a[rows], b, K), K, "gemm f32 4096^3 sample")
+    assert math.isfinite(float(got.sum()))
 
 
 def test_c5_generic_is_sequential(gpu):
