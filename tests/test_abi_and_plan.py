@@ -419,3 +419,32 @@ def test_runtime_null_arguments_are_refused_before_hip():
     assert L.tca_rt_memcpy_h2d(None, None, 0) == 0  # nothing to copy
     assert L.tca_rt_free(None) == 0
     assert L.tca_rt_launch(None, b"k", 1, 64, 0, None, 0, None) == _lib.TCA_ERR_INVALID
+
+
+@pytest.mark.parametrize("name", ["gemm_bf16", "gemm_bf16_nt"])
+def test_dma_gemm_reloads_nothing_from_scratch(name, tmp_path):
+    """The bf16 contraction's main loop waits on hand-counted vmcnt values
+    for its direct-to-LDS loads; a register spill reloaded from scratch while
+    they are in flight would share that counter (an fp32 port that spilled
+    computed wrong results). From the first direct-to-LDS load to the end of
+    that path (its s_endpgm) nothing may be reloaded from scratch; the
+    register-staged edge path after it may. Host-only: compiles to gfx950
+    assembly."""
+    import subprocess
+    e = programs.CONFIG_PROGRAMS[name]().emit()
+    src = tmp_path / "k.hip"
+    src.write_text(e.source)
+    asm = tmp_path / "k.s"
+    flags = [f for f in e.hipcc if f != "--genco"]  # assembly, not a code object
+    r = subprocess.run([os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "bin", "hipcc")] + flags +
+                       ["--cuda-device-only", "-S", "-o", str(asm), "-I", os.path.join(REPO, "tcacomp_amd", "csrc", "include"),
+                        str(src)], capture_output=True, text=True)
+    if r.returncode != 0 and "No such file" in (r.stderr or ""):
+        pytest.skip("hipcc not available")
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = asm.read_text().split("\n")
+    dma = [i for i, l in enumerate(lines) if "global_load_lds_dwordx4" in l]
+    assert dma
+    end = next(i for i in range(dma[-1], len(lines)) if "s_endpgm" in lines[i])
+    reloads = [lines[i].strip() for i in range(dma[0], end) if "scratch_load" in lines[i]]
+    assert not reloads, reloads[:4]
