@@ -498,24 +498,23 @@ __device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, cons
 
 // ---------------------------------------------------------------- fp32 path
 // Tile: BM = BN = 128, BK slices; 4 waves as 2x2, each 64x64 = 2x2 MFMA
-// blocks. DB = false: one LDS buffer, two barriers per slice (store, then
-// compute). DB = true: two buffers; the next slice's global loads are in
-// flight during the MFMAs and land in the other buffer, one barrier per
-// slice. Measured at 4096^3 (interleaved, one box): one buffer of 16-deep
-// slices 116 TFLOP/s; two buffers of 16: 114; one of 32: 102; one of 8:
-// 113 — the 17 KiB of LDS per block of 16-deep slices lets more blocks share
-// a CU, which hides the barriers better than double buffering.
-template <bool B_NK, bool DB = false, int BK = 16, typename Epi>
+// blocks; one LDS buffer, two barriers per slice (store, then compute), the
+// next slice's global loads in flight during the MFMAs. Measured at 4096^3
+// (interleaved, one box): 16-deep slices 116 TFLOP/s; 32-deep 102; 8-deep
+// 113; two LDS buffers of 16-deep slices (one barrier per slice) 114 — the
+// 17 KiB of LDS per block of 16-deep slices lets more blocks share a CU,
+// which hides the barriers better than double buffering.
+template <bool B_NK, int BK = 16, typename Epi>
 __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const float* __restrict__ B,
                                              float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
-  constexpr int BM = 128, BN = 128, NBUF = DB ? 2 : 1;
+  constexpr int BM = 128, BN = 128;
   static_assert(BK == 8 || BK == 16 || BK == 32, "slices of 8, 16 or 32");
   constexpr int LPT = BK / 8;                  // float4 per thread per operand slice
   constexpr int LDA = BK + 1;                  // As[m][k], odd stride: conflict-free column reads
   constexpr int LDB = B_NK ? BK + 1 : BN + 4;  // Bs[n][k] (NK) or Bs[k][n] (KN)
   constexpr int SA = BM * LDA, SB = B_NK ? BN * LDB : BK * LDB;
-  __shared__ float As_all[NBUF * SA];
-  __shared__ __attribute__((aligned(16))) float Bs_all[NBUF * SB];
+  __shared__ float As[SA];
+  __shared__ __attribute__((aligned(16))) float Bs[SB];
   const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   uint32_t tm, tn;
   gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
@@ -571,7 +570,7 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
     if constexpr (B_NK) load_rows(B, N, n0, k0, vec_b, rb);
     else load_b_kn(k0);
   };
-  auto store_lds = [&](float* As, float* Bs) {
+  auto store_lds = [&]() {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const uint32_t v = i * 256u + tid, rr = v / VPR, kv = (v % VPR) * 4u;
@@ -599,7 +598,7 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
       }
     }
   };
-  auto compute = [&](const float* As, const float* Bs) {
+  auto compute = [&]() {
 #pragma unroll
     for (int ks = 0; ks < BK / 2; ++ks) {
       const uint32_t k = ks * 2u + (lane >> 5);
@@ -619,29 +618,13 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
   };
 
   const uint32_t nk = (K + BK - 1) / BK;
-  if constexpr (!DB) {
-    load(0);
-    for (uint32_t kt = 0; kt < nk; ++kt) {
-      __syncthreads();
-      store_lds(As_all, Bs_all);
-      __syncthreads();
-      if (kt + 1 < nk) load((kt + 1) * BK);
-      compute(As_all, Bs_all);
-    }
-  } else if (nk > 0) {
-    // Buffer kt % 2 holds slice kt. Slice kt + 1 is stored into the other
-    // buffer after the MFMAs of slice kt: every wave finished reading that
-    // buffer (slice kt - 1) before the barrier that ended iteration kt - 1.
-    load(0);
-    store_lds(As_all, Bs_all);
+  load(0);
+  for (uint32_t kt = 0; kt < nk; ++kt) {
     __syncthreads();
-    for (uint32_t kt = 0; kt < nk; ++kt) {
-      const uint32_t cur = kt & 1u;
-      if (kt + 1 < nk) load((kt + 1) * BK);
-      compute(As_all + cur * SA, Bs_all + cur * SB);
-      if (kt + 1 < nk) store_lds(As_all + (cur ^ 1u) * SA, Bs_all + (cur ^ 1u) * SB);
-      __syncthreads();
-    }
+    store_lds();
+    __syncthreads();
+    if (kt + 1 < nk) load((kt + 1) * BK);
+    compute();
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
