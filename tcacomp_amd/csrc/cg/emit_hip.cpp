@@ -1708,7 +1708,10 @@ class Emitter {
       part_fn = pk.symbol + "_part";
       merge_fn = pk.symbol + "_merge";
       const std::string splitDim = "__split";
-      extra_dims_.push_back(splitDim + " " + std::to_string(kMaxParts));
+      // One plan dim serves every split kernel of the program (same extent).
+      const std::string splitDecl = splitDim + " " + std::to_string(kMaxParts);
+      if (std::find(extra_dims_.begin(), extra_dims_.end(), splitDecl) == extra_dims_.end())
+        extra_dims_.push_back(splitDecl);
       std::string partSig;
       for (int ci : passes[0]) {
         const ir::Chain& c = g_.chains[ci];
@@ -2415,13 +2418,67 @@ class Emitter {
 
 }  // namespace
 
+namespace {
+
+// Chained reductions (MidChain.Reduce then AfterReduce.Reduce,
+// pkg/chain.go:262 applied twice): a chain root -> reduce 1 -> reduce 2 ...
+// -> piped -> store becomes root -> reduce 1 -> store L, then L -> identity
+// -> reduce 2 ... -> store, L a local over the axes left after reduce 1.
+// The fold is the same (reduce 1's init once per element of L, reduce 2's
+// once per output); each half is a single-reduction chain the row,
+// streaming, column and split-row families take, where the chained form
+// could only fold one output per thread. Repeated until every chain has at
+// most one reduction.
+void SplitChainedReductions(ir::Graph* g) {
+  for (size_t ci = 0; ci < g->chains.size(); ++ci) {
+    if (g->chains[ci].reduces.size() < 2) continue;
+    ir::Chain inner = g->chains[ci];
+    ir::Chain outer = g->chains[ci];
+    std::vector<int> axes = inner.root.as;  // live axes after reduce 1
+    axes.pop_back();
+    const ir::Elem elem = g->exprs[inner.reduces[0].fn.body].type;
+    ir::Tensor t;
+    t.name = "__chain" + std::to_string(ci);
+    t.elem = elem;
+    t.dims = axes;
+    t.local = true;
+    g->tensors.push_back(t);
+    const int tl = static_cast<int>(g->tensors.size()) - 1;
+    inner.reduces.resize(1);
+    inner.has_piped = false;
+    inner.piped = ir::MapStage();
+    inner.store_tensor = tl;
+    inner.store_axes = axes;
+    ir::Expr param;
+    param.op = ir::Op::Param;
+    param.type = elem;
+    param.index = 0;
+    param.text = "v";
+    g->exprs.push_back(param);
+    const int pid = static_cast<int>(g->exprs.size()) - 1;
+    outer.iters = axes;
+    outer.root = ir::MapStage();
+    outer.root.ops.push_back(ir::Operand{tl, axes});
+    outer.root.fn.params = {pid};
+    outer.root.fn.body = pid;
+    outer.root.as = axes;
+    outer.reduces.erase(outer.reduces.begin());
+    g->chains[ci] = inner;
+    g->chains.insert(g->chains.begin() + static_cast<long>(ci) + 1, outer);
+  }
+}
+
+}  // namespace
+
 bool Emit(const ir::Graph& g, const Options& opts, Result* out, std::string* err) {
   std::string verr;
   if (!ir::Verify(g, &verr)) {
     *err = verr;
     return false;
   }
-  Emitter e(g, opts);
+  ir::Graph split = g;
+  if (opts.allow_fused) SplitChainedReductions(&split);
+  Emitter e(split, opts);
   return e.Run(out, err);
 }
 

@@ -258,6 +258,32 @@ def col_sum_u8():
     return b.Build()
 
 
+def chain_sum_max():
+    """Chained reductions in one chain (pkg/chain.go:262 twice): o[b] =
+    s * max over r of (sum over c of x[b, r, c])."""
+    b = NewBuilder("chain_sum_max")
+    B, R, C = b.Dim("B", 0), b.Dim("R", 0), b.Dim("C", 0)
+    x = b.Tensor("x", TF32, B, R, C)
+    o = b.Tensor("o", TF32, B)
+    s = b.ScalarParam("s", TF32)
+    (b.Stmt().Iter(B, R, C).Map([At(x, B, R, C)], lambda v: v).As(B, R, C)
+     .Reduce(b.Float32(0), _sum(b))
+     .Reduce(_neg_inf(b), lambda acc, v: Call("fmaxf", acc, v))
+     .Map([], lambda v: b.Mul(v, s)).As(B).Store(o, B))
+    return b.Build()
+
+
+def chain_total():
+    """A whole-matrix sum written as two chained sums: t = sum_r sum_c x[r, c]."""
+    b = NewBuilder("chain_total")
+    R, C = b.Dim("R", 0), b.Dim("C", 0)
+    x = b.Tensor("x", TF32, R, C)
+    t = b.Tensor("t", TF32)
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C)
+     .Reduce(b.Float32(0), _sum(b)).Reduce(b.Float32(0), _sum(b)).Store(t))
+    return b.Build()
+
+
 # Expression-layer parity programs: one output per expression over [N]
 # operands, so every operator, builtin and cast of the DSL (pkg/expr.go:
 # 140-341, internal/ir/builtins.go:25-33) runs on the device.
@@ -503,6 +529,8 @@ SUITE = {
 # variants (fusion and MFMA disabled) exist so tests can check every family
 # against the same oracle.
 CONFIG_PROGRAMS = {
+    "chain_sum_max": chain_sum_max,
+    "chain_total": chain_total,
     "col_sum_max_dyn": col_sum_max,
     "col_mean_bf16": col_mean_bf16,
     "col_sum_u8": col_sum_u8,
@@ -554,7 +582,8 @@ def all_builds():
     for name, (f, _, _) in sorted(SUITE.items()):
         out.append(("suite_" + name, f, 0))
     # generic-family lowering of the configs (cross-family parity)
-    for name in ("scale_relu", "row_sum_max_1000", "softmax_200", "layernorm_96", "gemm_f32"):
+    for name in ("scale_relu", "row_sum_max_1000", "softmax_200", "layernorm_96", "gemm_f32", "chain_sum_max",
+                 "chain_total"):
         out.append((name + "_generic", CONFIG_PROGRAMS[name], EMIT_NO_FUSION | EMIT_NO_GEMM))
     # seeded random row programs (tests/test_gpu_random.py), some also lowered generically
     from . import randprog

@@ -341,6 +341,8 @@ EXPECTED_FAMILIES = {
     "row_sum_bf16_dyn": ["stream"] * 16, "row_sum_u8_dyn": ["stream"] * 20, "row_stats_u32_dyn": ["stream"] * 12,
     # column reductions: a (partial, merge) pair per vector width
     "col_sum_max_dyn": ["col"] * 6, "col_mean_bf16": ["col"] * 8, "col_sum_u8": ["col"] * 10,
+    # chained reductions split into an inner reduce into a local and an outer reduce of it
+    "chain_sum_max": ["stream"] * 18, "chain_total": ["stream"] * 21,
 }
 
 
@@ -401,6 +403,21 @@ def test_every_registered_program_is_prebuilt():
         if not os.path.exists(p):
             missing.append(name)
     assert not missing, "not prebuilt (run __graft_entry__.build()): %s" % missing
+
+
+def test_every_registered_plan_parses():
+    """The runtime's plan parser (the one tca_program_load runs) accepts the
+    plan of every program the tests and the bench launch: no duplicate or
+    unknown dims, well-formed guards and split records; checked on the CPU
+    so a malformed plan never reaches a GPU run."""
+    bad = []
+    for name, factory, flags in programs.all_builds():
+        rc, h = parse(factory().emit(flags=flags).plan)
+        if rc != 0:
+            bad.append("%s: %s" % (name, _lib.last_error()))
+        else:
+            _lib.lib().tca_program_unload(h)
+    assert not bad, bad
 
 
 def test_build_sources_listed():

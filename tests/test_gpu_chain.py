@@ -1,0 +1,54 @@
+"""Chained reductions in one chain (MidChain.Reduce then AfterReduce.Reduce,
+pkg/chain.go:262 applied twice). The emitter splits such a chain into an
+inner reduction into a local and an outer reduction of that local, so each
+runs on the row/streaming families (and split rows); the fold keeps its
+structure: the inner init once per element of the local, the outer init
+once per output. Integer-valued inputs make every sum exact, so the device
+matches the closed form exactly in any fold order, and matches the generic
+lowering of the same program (one thread per output, sequential folds)."""
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import CANARY, compiled, host, out_dev, run, to_dev
+from tcacomp_amd.pkg import EMIT_NO_FUSION, EMIT_NO_GEMM
+
+pytestmark = pytest.mark.gpu
+GENERIC = EMIT_NO_FUSION | EMIT_NO_GEMM
+
+
+def _ints(shape, bound, seed):
+    return np.random.default_rng(seed).integers(-bound, bound + 1, size=shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("B,R,C", [(1, 1, 1), (3, 5, 7), (2, 1000, 64), (4, 300, 5000), (1, 20000, 16),
+                                   (2, 0, 4), (2, 3, 0), (3, 7, 70001)])
+def test_chain_sum_max(gpu, B, R, C):
+    print("chain_sum_max", B, R, C, flush=True)
+    sys.stdout.flush()
+    x = _ints((B, R, C), 8, B * 1000 + R + C)
+    s = -0.5
+    inner = x.astype(np.float64).sum(axis=2).astype(np.float32)  # exact: small integers
+    want = (np.max(inner, axis=1, initial=-np.inf).astype(np.float32) * np.float32(s)).astype(np.float32)
+    for flags in (0, GENERIC):
+        if flags and R * C > 1 << 20:
+            continue  # the generic lowering folds a whole output per thread
+        o = out_dev((B,), gpu)
+        run(compiled("chain_sum_max", flags), [to_dev(x, gpu), o], scalars=[s])
+        np.testing.assert_array_equal(host(o), want, err_msg="flags %d" % flags)
+
+
+@pytest.mark.parametrize("R,C", [(1, 1), (0, 5), (5, 0), (1000, 1000), (16, 1 << 19), (100000, 3), (3, 70001)])
+def test_chain_total(gpu, R, C):
+    print("chain_total", R, C, flush=True)
+    sys.stdout.flush()
+    x = _ints((R, C), 1, R + C)
+    assert np.abs(x).sum() < 2 ** 24  # exact in any order
+    want = np.float32(x.astype(np.float64).sum())
+    for flags in (0, GENERIC):
+        if flags and R * C > 1 << 20:
+            continue  # the generic lowering folds the whole matrix in one thread
+        t = out_dev((), gpu)
+        run(compiled("chain_total", flags), [to_dev(x, gpu), t])
+        assert host(t) == want, "flags %d: %r != %r" % (flags, host(t), want)
