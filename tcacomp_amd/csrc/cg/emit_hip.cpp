@@ -1962,11 +1962,16 @@ class Emitter {
   // store nothing.
   bool EmitCol(int ni, std::string* err) {
     // Swept on MI355X (column sum+max, [8192, 8192] .. [16, 4 Mi]): spans of
-    // 64 vectors beat 256 (4.7-5.7 against 4.3-4.8 TB/s), a 1024-block
-    // split target beats 512 and 2048, 8 rows in flight per thread gain 2%
-    // on [8192, 8192] but lose 20% on [16, 4 Mi] (clamped groups of 8), and
-    // two 16-byte vectors per thread and row (8 f32 columns) lose 11-25%.
-    constexpr uint32_t kWaves = 4, kRowsMin = 64, kBlocks = 1024, kUnroll = 4, kMergeWaves = 16, kSpan = 64,
+    // 64 vectors beat 256 (4.7-5.7 against 4.3-4.8 TB/s); a 1024-block
+    // split target beats 512, 2048 and 4096; 8 and 16 waves per block lose
+    // 3-20% except on [8192, 8192]; two 16-byte vectors per thread and row
+    // (8 f32 columns) lose 11-25%. Groups of 16 rows in flight per thread
+    // gain 9-11% on [8192, 8192] over groups of 4; as the first and the
+    // last group they cost 18-40% on [16, 4 Mi] (4 rows per wave: clamped
+    // rows re-read, guarded loads wait one by one), so only the main loop
+    // takes 16 rows and the ends keep clamped groups of 4: +7% on
+    // [8192, 8192], +2% on [16, 4 Mi], within 2% on the other shapes.
+    constexpr uint32_t kWaves = 4, kRowsMin = 64, kBlocks = 1024, kUnroll = 16, kEdge = 4, kMergeWaves = 16, kSpan = 64,
                        kLogSpan = 6;
     const Nest& n = an_.nests[ni];
     const ColGeom geo = ColCheck(g_, n.chains);
@@ -2168,15 +2173,16 @@ class Emitter {
             << "[q]);\n";
     };
     {
-      // Rows in groups of kUnroll (loads in flight together). The first and
-      // the last group clamp rows past the chunk to its last row and fold
-      // only the rows they own, so a short chunk still issues its loads at
-      // once.
+      // Rows in groups (loads in flight together): a first group of kEdge
+      // rows, groups of kUnroll rows while whole ones fit, then groups of
+      // kEdge to the chunk's end. The edge groups clamp rows past the chunk
+      // to its last row (unconditional loads stay in flight together) and
+      // fold only the rows they own; row 0 of each is always owned.
       std::ostringstream b;
-      auto group = [&](const std::string& ind, bool clamped, bool first) {
-        for (uint32_t u = 0; u < kUnroll; ++u) {
+      auto group = [&](const std::string& ind, uint32_t rows, bool clamped, bool first) {
+        for (uint32_t u = 0; u < rows; ++u) {
           const std::string us = std::to_string(u);
-          if (clamped) {
+          if (clamped && u > 0) {
             b << ind << "const bool ok_" << us << " = r + " << us << "u * STEP < r_hi;\n";
             b << ind << "const uint32_t rr_" << us << " = ok_" << us << " ? r + " << us << "u * STEP : r_hi - 1u;\n";
             loads(b, ind, "rr_" + us, "_" + us);
@@ -2184,16 +2190,16 @@ class Emitter {
             loads(b, ind, "r + " + us + "u * STEP", "_" + us);
           }
         }
-        for (uint32_t u = 0; u < kUnroll; ++u)
-          fold(b, ind, "_" + std::to_string(u), first && u == 0, clamped && !(first && u == 0) ? "ok_" + std::to_string(u) : "");
+        for (uint32_t u = 0; u < rows; ++u)
+          fold(b, ind, "_" + std::to_string(u), first && u == 0, clamped && u > 0 ? "ok_" + std::to_string(u) : "");
       };
       b << "  uint32_t r = r_lo + slot;\n  const bool has = r < r_hi;\n  if (has) {\n    {\n";
-      group("      ", true, true);
-      b << "    }\n    r += " << kUnroll << "u * STEP;\n";
+      group("      ", kEdge, true, true);
+      b << "    }\n    r += " << kEdge << "u * STEP;\n";
       b << "    for (; r + " << kUnroll - 1 << "u * STEP < r_hi; r += " << kUnroll << "u * STEP) {\n";
-      group("      ", false, false);
-      b << "    }\n    if (r < r_hi) {\n";
-      group("      ", true, false);
+      group("      ", kUnroll, false, false);
+      b << "    }\n    for (; r < r_hi; r += " << kEdge << "u * STEP) {\n";
+      group("      ", kEdge, true, false);
       b << "    }\n  }\n";
       o << b.str();
     }
