@@ -284,6 +284,19 @@ def chain_total():
     return b.Build()
 
 
+def chain3_max_total():
+    """Three chained reductions (pkg/chain.go:262 three times): t = max over b
+    of (sum over r of (sum over c of x[b, r, c]))."""
+    b = NewBuilder("chain3_max_total")
+    B, R, C = b.Dim("B", 0), b.Dim("R", 0), b.Dim("C", 0)
+    x = b.Tensor("x", TF32, B, R, C)
+    t = b.Tensor("t", TF32)
+    (b.Stmt().Iter(B, R, C).Map([At(x, B, R, C)], lambda v: v).As(B, R, C)
+     .Reduce(b.Float32(0), _sum(b)).Reduce(b.Float32(0), _sum(b))
+     .Reduce(_neg_inf(b), lambda acc, v: Call("fmaxf", acc, v)).Store(t))
+    return b.Build()
+
+
 # Expression-layer parity programs: one output per expression over [N]
 # operands, so every operator, builtin and cast of the DSL (pkg/expr.go:
 # 140-341, internal/ir/builtins.go:25-33) runs on the device.
@@ -531,6 +544,7 @@ SUITE = {
 CONFIG_PROGRAMS = {
     "chain_sum_max": chain_sum_max,
     "chain_total": chain_total,
+    "chain3_max_total": chain3_max_total,
     "col_sum_max_dyn": col_sum_max,
     "col_mean_bf16": col_mean_bf16,
     "col_sum_u8": col_sum_u8,
@@ -583,7 +597,7 @@ def all_builds():
         out.append(("suite_" + name, f, 0))
     # generic-family lowering of the configs (cross-family parity)
     for name in ("scale_relu", "row_sum_max_1000", "softmax_200", "layernorm_96", "gemm_f32", "chain_sum_max",
-                 "chain_total"):
+                 "chain_total", "chain3_max_total"):
         out.append((name + "_generic", CONFIG_PROGRAMS[name], EMIT_NO_FUSION | EMIT_NO_GEMM))
     # seeded random row programs (tests/test_gpu_random.py), some also lowered generically
     from . import randprog

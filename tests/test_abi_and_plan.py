@@ -342,7 +342,7 @@ EXPECTED_FAMILIES = {
     # column reductions: a (partial, merge) pair per vector width
     "col_sum_max_dyn": ["col"] * 6, "col_mean_bf16": ["col"] * 8, "col_sum_u8": ["col"] * 10,
     # chained reductions split into an inner reduce into a local and an outer reduce of it
-    "chain_sum_max": ["stream"] * 18, "chain_total": ["stream"] * 21,
+    "chain_sum_max": ["stream"] * 18, "chain_total": ["stream"] * 21, "chain3_max_total": ["stream"] * 27,
 }
 
 

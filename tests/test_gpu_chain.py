@@ -52,3 +52,19 @@ def test_chain_total(gpu, R, C):
         t = out_dev((), gpu)
         run(compiled("chain_total", flags), [to_dev(x, gpu), t])
         assert host(t) == want, "flags %d: %r != %r" % (flags, host(t), want)
+
+
+@pytest.mark.parametrize("B,R,C", [(1, 1, 1), (5, 3, 7), (3, 1000, 100), (2, 20, 70001), (300, 2, 3), (0, 4, 4),
+                                   (4, 0, 4), (4, 4, 0)])
+def test_chain3_max_total(gpu, B, R, C):
+    """Three reduces in one chain: split twice (inner, middle, outer)."""
+    print("chain3_max_total", B, R, C, flush=True)
+    sys.stdout.flush()
+    x = _ints((B, R, C), 4, B * 77 + R * 5 + C)
+    want = np.float32(np.max(x.astype(np.float64).sum(axis=(1, 2)), initial=-np.inf))  # exact: small integers
+    for flags in (0, GENERIC):
+        if flags and B * R * C > 1 << 20:
+            continue  # the generic lowering folds everything in one thread
+        t = out_dev((), gpu)
+        run(compiled("chain3_max_total", flags), [to_dev(x, gpu), t])
+        assert host(t) == want, "flags %d: %r != %r" % (flags, host(t), want)
