@@ -297,6 +297,19 @@ def chain3_max_total():
     return b.Build()
 
 
+def chain_halving():
+    """A chained reduction whose outer fold is not associative: t = fold over
+    r of (acc / 2 + sum over c of x[r, c]) from 0, in ascending r."""
+    b = NewBuilder("chain_halving")
+    R, C = b.Dim("R", 0), b.Dim("C", 0)
+    x = b.Tensor("x", TF32, R, C)
+    t = b.Tensor("t", TF32)
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C)
+     .Reduce(b.Float32(0), _sum(b))
+     .Reduce(b.Float32(0), lambda acc, v: b.Add(b.Mul(acc, b.Float32(0.5)), v)).Store(t))
+    return b.Build()
+
+
 # Expression-layer parity programs: one output per expression over [N]
 # operands, so every operator, builtin and cast of the DSL (pkg/expr.go:
 # 140-341, internal/ir/builtins.go:25-33) runs on the device.
@@ -545,6 +558,7 @@ CONFIG_PROGRAMS = {
     "chain_sum_max": chain_sum_max,
     "chain_total": chain_total,
     "chain3_max_total": chain3_max_total,
+    "chain_halving": chain_halving,
     "col_sum_max_dyn": col_sum_max,
     "col_mean_bf16": col_mean_bf16,
     "col_sum_u8": col_sum_u8,

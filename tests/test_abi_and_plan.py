@@ -362,6 +362,15 @@ def test_config_classification(name):
     assert e.families() == EXPECTED_FAMILIES[name], e.report
 
 
+def test_split_chain_keeps_the_combiner_rules():
+    """A chained reduction is split into one chain per reduce, and each is
+    classified on its own: the inner sum streams, while an outer fold that
+    is not associative-commutative (acc / 2 + now) keeps the generic
+    family's sequential order."""
+    fams = programs.CONFIG_PROGRAMS["chain_halving"]().emit().families()
+    assert fams[-1] == "generic" and set(fams[:-1]) == {"stream"}, fams
+
+
 def test_fusion_disabled_lowers_every_chain_generically():
     e = programs.CONFIG_PROGRAMS["softmax_4096"]().emit(flags=EMIT_NO_FUSION | EMIT_NO_GEMM)
     assert e.families() == ["generic"] * 3

@@ -68,3 +68,21 @@ def test_chain3_max_total(gpu, B, R, C):
         t = out_dev((), gpu)
         run(compiled("chain3_max_total", flags), [to_dev(x, gpu), t])
         assert host(t) == want, "flags %d: %r != %r" % (flags, host(t), want)
+
+
+@pytest.mark.parametrize("R,C", [(1, 1), (0, 3), (3, 0), (7, 1000), (40, 70001), (1000, 16)])
+def test_chain_halving(gpu, R, C):
+    """A streamed inner sum feeding a generic outer fold that is not
+    associative (acc / 2 + now), through the HBM local between them. The
+    expected value repeats the fold in float32, one rounding per operation
+    as on the device (no contraction)."""
+    print("chain_halving", R, C, flush=True)
+    sys.stdout.flush()
+    x = _ints((R, C), 4, R * 3 + C)
+    rows = x.astype(np.float64).sum(axis=1).astype(np.float32)  # exact: small integers
+    acc = np.float32(0)
+    for v in rows:
+        acc = np.float32(np.float32(acc * np.float32(0.5)) + v)
+    t = out_dev((), gpu)
+    run(compiled("chain_halving"), [to_dev(x, gpu), t])
+    assert host(t) == acc, "%r != %r" % (host(t), acc)
