@@ -287,9 +287,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (each config would shard by "
-              "rows, one block of rows per GPU, with no exchange between GPUs). Run with --gpus 1.",
-              file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the row configurations would "
+              "shard by rows with no exchange, the GEMM by row panels of A after an all-gather of B, and each "
+              "GPU would run these same kernels at its shard shape). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
     from tcacomp_amd import _lib
