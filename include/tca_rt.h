@@ -148,7 +148,12 @@ int tca_program_selected(tca_program p, const tca_tensor* tensors, uint32_t n_te
  * to their declared types. Locals that live in HBM (and the partials of
  * split reductions) use a workspace the program allocates on first need per
  * stream and keeps until unload: launches of one program on different
- * streams may overlap safely. Thread-safe for distinct streams. */
+ * streams may overlap safely. Thread-safe: calls that use a workspace hold
+ * the program's lock from sizing it until their last kernel is queued, so
+ * calls on one stream from several threads serialize (a larger launch
+ * synchronizes the stream before it replaces the buffer). The first launch
+ * that needs a workspace allocates (hipMalloc), so it cannot be captured
+ * into a HIP graph. */
 int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tensors,
                        const uint32_t* free_dims, uint32_t n_free_dims,
                        const double* scalars, uint32_t n_scalars, tca_stream_t stream);

@@ -22,33 +22,33 @@
 extern "C" {
 #endif
 
-typedef struct tca_module_s* tca_module;
+typedef struct tca_syntax_module_s* tca_syntax_module;
 
 /* Loads the module rooted at path. On errors returns TCA_ERR_BUILD, *out is
  * NULL and tca_syntax_last_error() holds the diagnostics, one per line
  * ("file:line:col: error: message"). */
-int tca_syntax_parse_module(const char* path, tca_module* out);
+int tca_syntax_parse_module(const char* path, tca_syntax_module* out);
 /* Parses source text held in memory (name labels diagnostics). check = 0
- * stops after parsing (the tree as written, for tca_module_dump); check = 1
+ * stops after parsing (the tree as written, for tca_syntax_module_dump); check = 1
  * also runs the module and kernel checks. @include is not resolved here. */
-int tca_syntax_parse_source(const char* name, const char* src, int32_t check, tca_module* out);
+int tca_syntax_parse_source(const char* name, const char* src, int32_t check, tca_syntax_module* out);
 /* Diagnostics of the last failed parse or build on this thread. */
 const char* tca_syntax_last_error(void);
 
 /* Warnings (and, for check = 0 parses, nothing else) of a loaded module. */
-const char* tca_module_diagnostics(tca_module m);
-uint32_t tca_module_kernel_count(tca_module m);
-const char* tca_module_kernel_name(tca_module m, uint32_t i);
+const char* tca_syntax_module_diagnostics(tca_syntax_module m);
+uint32_t tca_syntax_module_kernel_count(tca_syntax_module m);
+const char* tca_syntax_module_kernel_name(tca_syntax_module m, uint32_t i);
 /* @name(cxx="...") of kernel i, or NULL. */
-const char* tca_module_kernel_cxx_name(tca_module m, uint32_t i);
+const char* tca_syntax_module_kernel_cxx_name(tca_syntax_module m, uint32_t i);
 /* @runtime(cxx_path="...") of the module, or NULL. */
-const char* tca_module_runtime_path(tca_module m);
+const char* tca_syntax_module_runtime_path(tca_syntax_module m);
 /* Canonical indented rendering of the module's tree (owned by the module). */
-const char* tca_module_dump(tca_module m);
+const char* tca_syntax_module_dump(tca_syntax_module m);
 /* Lowers kernel i through the builder rungs and builds it. On success *out
  * is a new builder (free with tca_builder_free). */
-int tca_module_build_kernel(tca_module m, uint32_t i, tca_builder* out);
-void tca_module_free(tca_module m);
+int tca_syntax_module_build_kernel(tca_syntax_module m, uint32_t i, tca_builder* out);
+void tca_syntax_module_free(tca_syntax_module m);
 
 #ifdef __cplusplus
 }

@@ -1,5 +1,5 @@
 """TEST INFRASTRUCTURE ONLY: CPU evaluation of the random row and grid
-programs of tcacomp_amd/randprog.py (the checker of tests/test_gpu_random.py,
+programs of tests/randprog.py (the checker of tests/test_gpu_random.py,
 never the thing measured or shipped; only tests/ may import it).
 
 The DSL semantics restated here, per statement:

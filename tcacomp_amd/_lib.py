@@ -132,14 +132,14 @@ SIGNATURES = [
     ("tca_syntax_parse_module", _c.c_int, [_STR, _c.POINTER(_P)]),
     ("tca_syntax_parse_source", _c.c_int, [_STR, _STR, _I32, _c.POINTER(_P)]),
     ("tca_syntax_last_error", _STR, []),
-    ("tca_module_diagnostics", _STR, [_P]),
-    ("tca_module_kernel_count", _U32, [_P]),
-    ("tca_module_kernel_name", _STR, [_P, _U32]),
-    ("tca_module_kernel_cxx_name", _STR, [_P, _U32]),
-    ("tca_module_runtime_path", _STR, [_P]),
-    ("tca_module_dump", _STR, [_P]),
-    ("tca_module_build_kernel", _c.c_int, [_P, _U32, _c.POINTER(_P)]),
-    ("tca_module_free", None, [_P]),
+    ("tca_syntax_module_diagnostics", _STR, [_P]),
+    ("tca_syntax_module_kernel_count", _U32, [_P]),
+    ("tca_syntax_module_kernel_name", _STR, [_P, _U32]),
+    ("tca_syntax_module_kernel_cxx_name", _STR, [_P, _U32]),
+    ("tca_syntax_module_runtime_path", _STR, [_P]),
+    ("tca_syntax_module_dump", _STR, [_P]),
+    ("tca_syntax_module_build_kernel", _c.c_int, [_P, _U32, _c.POINTER(_P)]),
+    ("tca_syntax_module_free", None, [_P]),
 ]
 
 _lib = None

@@ -64,13 +64,15 @@ def build_library(jobs=8):
     return LIB
 
 
-def build_kernels(jobs=8, force=False):
-    """Emits and compiles every registered program into _kcache/."""
+def build_kernels(jobs=8, force=False, extra=()):
+    """Emits and compiles every registered program, plus `extra` (name,
+    factory, flags) triples such as the test suite's generated programs,
+    into _kcache/; code objects of neither are pruned."""
     from . import compiler, programs
 
     jobs_list = []
     current = set()
-    for name, factory, flags in programs.all_builds():
+    for name, factory, flags in list(programs.all_builds()) + list(extra):
         prog = factory()
         emitted = prog.emit(flags=flags)
         key = compiler.cache_key(emitted.source, emitted.hipcc)
@@ -98,12 +100,12 @@ def build_kernels(jobs=8, force=False):
     return done
 
 
-def build_all(force_kernels=False):
+def build_all(force_kernels=False, extra=()):
     build_library()
     # The freshly built library must be the one loaded.
     from . import _lib
     _lib._lib = None
-    return build_kernels(force=force_kernels)
+    return build_kernels(force=force_kernels, extra=extra)
 
 
 if __name__ == "__main__":

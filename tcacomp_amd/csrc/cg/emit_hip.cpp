@@ -1764,11 +1764,11 @@ class Emitter {
       o << "  constexpr uint32_t CV = " << kChunkVecs << "u, PMAX = " << kMaxParts << "u;\n";
       o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
       o << "  const uint32_t VECS = C / V;\n";
-      o << "  const uint32_t P = min(PMAX, (VECS + CV - 1u) / CV);\n";
+      o << "  const uint32_t P = min(PMAX, tca::hip::ceil_div(VECS, CV));  // VECS >= 1 (launch guard)\n";
       o << "  const uint32_t r = blockIdx.x / P, p = blockIdx.x - r * P;\n";
       o << "  if (r >= " << rowExpr << ") return;  // the grid is rows x P: never taken\n";
-      o << "  const uint32_t L = (VECS + P - 1u) / P;\n";
-      o << "  const uint32_t lo = p * L, hi = min(lo + L, VECS);  // hi - lo > " << kPartBlock << "\n";
+      o << "  const uint32_t L = tca::hip::ceil_div(VECS, P);\n";
+      o << "  const uint32_t lo = p * L, hi = lo + min(L, VECS - lo);  // lo < VECS; hi - lo > " << kPartBlock << "\n";
       o << "  const uint64_t row_base = static_cast<uint64_t>(r) * C;\n";
       o << "  const bool active = true;\n";
       rowCoords("  ");
@@ -1814,7 +1814,7 @@ class Emitter {
         << ") {\n";
       o << "  constexpr uint32_t CV = " << kChunkVecs << "u, PMAX = " << kMaxParts << "u;\n";
       o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
-      o << "  const uint32_t P = min(PMAX, (C / V + CV - 1u) / CV);\n";
+      o << "  const uint32_t P = min(PMAX, tca::hip::ceil_div(C / V, CV));\n";
       o << "  const uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63u;\n";
       o << "  if (r >= " << rowExpr << ") return;  // whole waves\n";
       rowCoords("  ");
@@ -2107,7 +2107,7 @@ class Emitter {
       << "u, SPAN = " << kSpan << "u, LSPAN = " << kLogSpan << "u;  // SPAN column vectors per block\n";
     o << "  const uint32_t C = " << ExtentExpr(g_, geo.c) << ", R = " << ExtentExpr(g_, geo.r) << ";\n";
     o << "  const uint32_t NOUT = " << ProductExpr(geo.outer) << ";\n";
-    o << "  const uint32_t VEC = C / V, CB = (VEC + SPAN - 1u) / SPAN, NCB = NOUT * CB;\n";
+    o << "  const uint32_t VEC = C / V, CB = tca::hip::ceil_div(VEC, SPAN), NCB = NOUT * CB;\n";
     o << "  const uint32_t P = tca::hip::col_split(R, NCB, RMIN, BLOCKS);\n";
     o << "  const uint32_t p = blockIdx.x / NCB, cbk = blockIdx.x - p * NCB;\n";
     o << "  const uint32_t ob = cbk / CB, cb = cbk - ob * CB;\n";
@@ -2243,7 +2243,7 @@ class Emitter {
       << "u, SPAN = " << kSpan << "u;\n";
     o << "  const uint32_t C = " << ExtentExpr(g_, geo.c) << ", R = " << ExtentExpr(g_, geo.r) << ";\n";
     o << "  const uint32_t NOUT = " << ProductExpr(geo.outer) << ";\n";
-    o << "  const uint32_t VEC = C / V, CB = (VEC + SPAN - 1u) / SPAN, NCB = NOUT * CB;\n";
+    o << "  const uint32_t VEC = C / V, CB = tca::hip::ceil_div(VEC, SPAN), NCB = NOUT * CB;\n";
     o << "  const uint32_t P = tca::hip::col_split(R, NCB, RMIN, BLOCKS);  // > 1: launched only then\n";
     o << "  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;\n";
     o << "  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 64u + lane;\n";

@@ -216,10 +216,13 @@ __device__ __forceinline__ uint32_t pack_lanes_log2(uint32_t vecs, uint32_t per_
 // computes the same number at launch): at least rows_min rows per chunk,
 // and no more chunks than keep col_blocks * P <= blocks; 1 when there are
 // no rows or the column blocks alone reach `blocks`.
-__device__ __forceinline__ uint32_t col_split(uint32_t rows, uint32_t col_blocks, uint32_t rows_min,
-                                              uint32_t blocks) {
+// Rounds up without forming rows + rows_min - 1, so rows up to 2^32 - 1 give
+// the host's 64-bit answer. Host-callable for the tests that hold it to the
+// plan's numbers.
+__host__ __device__ __forceinline__ uint32_t col_split(uint32_t rows, uint32_t col_blocks, uint32_t rows_min,
+                                                       uint32_t blocks) {
   if (rows == 0u || col_blocks == 0u) return 1u;
-  uint32_t p = (rows + rows_min - 1u) / rows_min;
+  uint32_t p = (rows - 1u) / rows_min + 1u;
   const uint32_t cap = blocks / col_blocks;
   if (p > cap) p = cap;
   return p ? p : 1u;
@@ -228,7 +231,8 @@ __device__ __forceinline__ uint32_t col_split(uint32_t rows, uint32_t col_blocks
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
 __device__ __forceinline__ uint32_t wave_id() { return threadIdx.x >> 6; }
 
-__device__ __forceinline__ uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1u) / b; }
+// ceil(a / b) for b > 0, exact for every uint32 a (no a + b - 1 that wraps).
+__host__ __device__ __forceinline__ uint32_t ceil_div(uint32_t a, uint32_t b) { return a == 0u ? 0u : (a - 1u) / b + 1u; }
 
 }  // namespace hip
 }  // namespace tca

@@ -433,8 +433,13 @@ int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tens
     ws_bytes += (tca::plan::TensorBytes(pl, t, dims) + 255u) & ~static_cast<size_t>(255u);
   }
   void* ws = nullptr;
+  // Held until the last kernel is enqueued: a launch of this program on the
+  // same stream from another thread that grows the workspace synchronizes
+  // the stream and frees the old buffer, which must not happen between
+  // reading the pointer here and queueing the kernels that use it.
+  std::unique_lock<std::mutex> lk(p->mu, std::defer_lock);
   if (ws_bytes > 0) {
-    std::lock_guard<std::mutex> lk(p->mu);
+    lk.lock();
     tca_program_s::Workspace& w = p->workspaces[stream];
     if (w.bytes < ws_bytes) {
       if (w.ptr != nullptr) {

@@ -6,7 +6,7 @@
 #include "syntax.h"
 #include "tca_syntax.h"
 
-struct tca_module_s {
+struct tca_syntax_module_s {
   tca::syntax::Module m;
   bool checked = false;
   std::string diagnostics;
@@ -17,12 +17,12 @@ namespace {
 
 thread_local std::string g_last_error;
 
-int Finish(tca::syntax::Module&& m, bool checked, const std::vector<tca::syntax::Diagnostic>& d, tca_module* out) {
+int Finish(tca::syntax::Module&& m, bool checked, const std::vector<tca::syntax::Diagnostic>& d, tca_syntax_module* out) {
   if (tca::syntax::HasErrors(d)) {
     g_last_error = "frontend:\n" + tca::syntax::JoinDiagnostics(d, true);
     return TCA_ERR_BUILD;
   }
-  auto* h = new tca_module_s;
+  auto* h = new tca_syntax_module_s;
   h->m = std::move(m);
   h->checked = checked;
   h->diagnostics = tca::syntax::JoinDiagnostics(d, false);
@@ -34,7 +34,7 @@ int Finish(tca::syntax::Module&& m, bool checked, const std::vector<tca::syntax:
 
 extern "C" {
 
-int tca_syntax_parse_module(const char* path, tca_module* out) {
+int tca_syntax_parse_module(const char* path, tca_syntax_module* out) {
   if (out == nullptr || path == nullptr) return TCA_ERR_INVALID;
   *out = nullptr;
   try {
@@ -47,7 +47,7 @@ int tca_syntax_parse_module(const char* path, tca_module* out) {
   }
 }
 
-int tca_syntax_parse_source(const char* name, const char* src, int32_t check, tca_module* out) {
+int tca_syntax_parse_source(const char* name, const char* src, int32_t check, tca_syntax_module* out) {
   if (out == nullptr || src == nullptr) return TCA_ERR_INVALID;
   *out = nullptr;
   try {
@@ -73,16 +73,16 @@ int tca_syntax_parse_source(const char* name, const char* src, int32_t check, tc
 
 const char* tca_syntax_last_error(void) { return g_last_error.c_str(); }
 
-const char* tca_module_diagnostics(tca_module m) { return m ? m->diagnostics.c_str() : ""; }
+const char* tca_syntax_module_diagnostics(tca_syntax_module m) { return m ? m->diagnostics.c_str() : ""; }
 
-uint32_t tca_module_kernel_count(tca_module m) { return m ? static_cast<uint32_t>(m->m.kernels.size()) : 0u; }
+uint32_t tca_syntax_module_kernel_count(tca_syntax_module m) { return m ? static_cast<uint32_t>(m->m.kernels.size()) : 0u; }
 
-const char* tca_module_kernel_name(tca_module m, uint32_t i) {
+const char* tca_syntax_module_kernel_name(tca_syntax_module m, uint32_t i) {
   if (m == nullptr || i >= m->m.kernels.size()) return nullptr;
   return m->m.kernels[i].name.c_str();
 }
 
-const char* tca_module_kernel_cxx_name(tca_module m, uint32_t i) {
+const char* tca_syntax_module_kernel_cxx_name(tca_syntax_module m, uint32_t i) {
   if (m == nullptr || i >= m->m.kernels.size()) return nullptr;
   for (const auto& a : m->m.kernels[i].anns)
     if (a.name == "name")
@@ -91,14 +91,14 @@ const char* tca_module_kernel_cxx_name(tca_module m, uint32_t i) {
   return nullptr;
 }
 
-const char* tca_module_runtime_path(tca_module m) {
+const char* tca_syntax_module_runtime_path(tca_syntax_module m) {
   if (m == nullptr || !m->m.has_runtime) return nullptr;
   for (const auto& kc : m->m.runtime.args)
     if (kc.key == "cxx_path" && kc.kind == tca::syntax::ConstKind::String) return kc.text.c_str();
   return nullptr;
 }
 
-const char* tca_module_dump(tca_module m) {
+const char* tca_syntax_module_dump(tca_syntax_module m) {
   if (m == nullptr) return nullptr;
   try {
     m->dump = tca::syntax::Dump(m->m);
@@ -108,7 +108,7 @@ const char* tca_module_dump(tca_module m) {
   return m->dump.c_str();
 }
 
-int tca_module_build_kernel(tca_module m, uint32_t i, tca_builder* out) {
+int tca_syntax_module_build_kernel(tca_syntax_module m, uint32_t i, tca_builder* out) {
   if (m == nullptr || out == nullptr || i >= m->m.kernels.size()) return TCA_ERR_INVALID;
   *out = nullptr;
   if (!m->checked) {
@@ -141,6 +141,6 @@ int tca_module_build_kernel(tca_module m, uint32_t i, tca_builder* out) {
   }
 }
 
-void tca_module_free(tca_module m) { delete m; }
+void tca_syntax_module_free(tca_syntax_module m) { delete m; }
 
 }  // extern "C"

@@ -613,10 +613,4 @@ def all_builds():
     for name in ("scale_relu", "row_sum_max_1000", "softmax_200", "layernorm_96", "gemm_f32", "chain_sum_max",
                  "chain_total", "chain3_max_total"):
         out.append((name + "_generic", CONFIG_PROGRAMS[name], EMIT_NO_FUSION | EMIT_NO_GEMM))
-    # seeded random row programs (tests/test_gpu_random.py), some also lowered generically
-    from . import randprog
-    for spec in randprog.specs():
-        out.append((spec.name, (lambda s=spec: randprog.build(s)), 0))
-        if spec.name in randprog.GENERIC_TOO:
-            out.append((spec.name + "_generic", (lambda s=spec: randprog.build(s)), EMIT_NO_FUSION | EMIT_NO_GEMM))
     return out

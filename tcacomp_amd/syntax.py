@@ -24,18 +24,18 @@ class Kernel:
         self._i = index
 
     def Name(self):
-        return _lib.lib().tca_module_kernel_name(self._m._h, self._i).decode()
+        return _lib.lib().tca_syntax_module_kernel_name(self._m._h, self._i).decode()
 
     def CxxName(self):
         """@name(cxx="...") or None."""
-        s = _lib.lib().tca_module_kernel_cxx_name(self._m._h, self._i)
+        s = _lib.lib().tca_syntax_module_kernel_cxx_name(self._m._h, self._i)
         return s.decode() if s else None
 
     def Build(self):
         """Lowers the kernel through the builder rungs and builds it."""
         L = _lib.lib()
         out = ctypes.c_void_p()
-        if L.tca_module_build_kernel(self._m._h, self._i, ctypes.byref(out)) != 0:
+        if L.tca_syntax_module_build_kernel(self._m._h, self._i, ctypes.byref(out)) != 0:
             raise BuildError(L.tca_syntax_last_error().decode())
         return Program(Builder._adopt(self.Name(), out.value))
 
@@ -48,10 +48,10 @@ class Module:
         self._h = handle
         self.Source = source
         L = _lib.lib()
-        self.Kernels = [Kernel(self, i) for i in range(L.tca_module_kernel_count(handle))]
-        rt = L.tca_module_runtime_path(handle)
+        self.Kernels = [Kernel(self, i) for i in range(L.tca_syntax_module_kernel_count(handle))]
+        rt = L.tca_syntax_module_runtime_path(handle)
         self.Runtime = rt.decode() if rt else None
-        self.Diagnostics = L.tca_module_diagnostics(handle).decode()
+        self.Diagnostics = L.tca_syntax_module_diagnostics(handle).decode()
 
     def Kernel(self, name):
         for k in self.Kernels:
@@ -60,13 +60,13 @@ class Module:
         raise KeyError(name)
 
     def Dump(self):
-        return _lib.lib().tca_module_dump(self._h).decode()
+        return _lib.lib().tca_syntax_module_dump(self._h).decode()
 
     def __del__(self):
         h = getattr(self, "_h", None)
         if h:
             try:
-                _lib.lib().tca_module_free(h)
+                _lib.lib().tca_syntax_module_free(h)
             except Exception:
                 pass
             self._h = None

@@ -60,6 +60,45 @@ def assert_reduce_close(got, want, term_l2, K, what=""):
         what, int(bad.sum()), float(err.max()), float(bound.reshape(-1)[np.argmax(err.reshape(-1))]))
 
 
+def layernorm_bound(x, gamma, beta, eps):
+    """Per-element bound on |gpu - oracle| for y = (x - mean) * rsqrt(var + eps)
+    * gamma + beta over the last axis: the reduction tolerance carried
+    through the normalisation to first order, in float64.
+
+      mean error   e_m = tol * ||x_row||_2 / C
+      var error    e_v = tol * ||(x - mean)^2||_2 / C
+      rstd error   relative 0.5 * e_v / (var + eps) + 4 * 2^-24 (rsqrt ulps, var + eps)
+      y error      (e_m + |x - mean| * rstd_rel) * rstd * |gamma|
+                   + 8 * 2^-24 * (|x - mean| * rstd * |gamma| + |beta|)  (the row map's roundings)
+    with tol = 1e-5 * sqrt(C). An element at the row mean is held to about
+    1e-5 * |gamma|, not to a fraction of the largest output."""
+    x = x.astype(np.float64)
+    C = x.shape[-1]
+    tol = reduce_tol(C)
+    mean = x.mean(-1, keepdims=True)
+    d = x - mean
+    var = (d * d).mean(-1, keepdims=True)
+    rstd = 1.0 / np.sqrt(var + eps)
+    e_m = tol * np.sqrt((x * x).sum(-1, keepdims=True)) / C
+    e_v = tol * np.sqrt((d ** 4).sum(-1, keepdims=True)) / C
+    r_rel = 0.5 * e_v / (var + eps) + 4 * 2.0 ** -24
+    g = np.abs(gamma.astype(np.float64))
+    return (e_m + np.abs(d) * r_rel) * rstd * g + 8 * 2.0 ** -24 * (np.abs(d) * rstd * g + np.abs(beta))
+
+
+def assert_layernorm_close(got, want, x, gamma, beta, eps, what="layernorm"):
+    """Every element within layernorm_bound; returns the worst err / bound."""
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    bound = layernorm_bound(x, gamma, beta, eps)
+    ratio = err / bound
+    worst = float(ratio.max()) if ratio.size else 0.0
+    i = int(np.argmax(ratio)) if ratio.size else 0
+    print("%s: max err %.3g, worst err/bound %.3g" % (what, float(err.max()) if err.size else 0.0, worst))
+    assert worst <= 1.0, "%s: element %d err %g exceeds its bound %g" % (
+        what, i, float(err.reshape(-1)[i]), float(bound.reshape(-1)[i]))
+    return worst
+
+
 def ulp_diff(a, b):
     """|a - b| in float32 ulps (sign-magnitude ordering)."""
     ai = a.astype(np.float32).view(np.int32).astype(np.int64)

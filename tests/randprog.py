@@ -1,5 +1,5 @@
-"""Seeded random row programs of the DSL: the emitter's families exercised on
-programs nobody wrote by hand.
+"""TEST INFRASTRUCTURE: seeded random row programs of the DSL, the emitter's
+families exercised on programs nobody wrote by hand.
 
 A program is a *spec* (plain Python data) and is built into a pkg.Program by
 build(spec); tests evaluate the same spec on the CPU. Each program iterates
@@ -25,7 +25,7 @@ feed keep every f32 sum exact (integer-valued terms, partial sums below
 """
 import random
 
-from .pkg import TBF16, TF32, TU8, TU32, At, Call, Cast, NewBuilder, Select
+from tcacomp_amd.pkg import EMIT_NO_FUSION, EMIT_NO_GEMM, TBF16, TF32, TU8, TU32, At, Call, Cast, NewBuilder, Select
 
 F32_OPS = ["add", "sub", "mul", "max", "min", "sel", "neg", "abs", "div1"]
 U32_OPS = ["add", "sub", "mul", "max", "min", "sel", "xor", "and", "or"]
@@ -443,3 +443,15 @@ def specs():
     return ([generate(seed, elem, dyn) for elem, dyn, seed in PROGRAMS] +
             [generate_grid(seed, elem, dyn) for elem, dyn, seed in GRID_PROGRAMS] +
             [generate_grid(seed, elem, dyn, True) for elem, dyn, seed in GRID3_PROGRAMS])
+
+
+def all_builds():
+    """(name, program factory, emit flags) of every code object the random
+    programs need: build() prebuilds them beside the product's programs so a
+    GPU run never compiles."""
+    out = []
+    for spec in specs():
+        out.append((spec.name, (lambda s=spec: build(s)), 0))
+        if spec.name in GENERIC_TOO:
+            out.append((spec.name + "_generic", (lambda s=spec: build(s)), EMIT_NO_FUSION | EMIT_NO_GEMM))
+    return out

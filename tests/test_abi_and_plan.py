@@ -474,3 +474,107 @@ def test_dma_gemm_reloads_nothing_from_scratch(name, tmp_path):
     end = next(i for i in range(dma[-1], len(lines)) if "s_endpgm" in lines[i])
     reloads = [lines[i].strip() for i in range(dma[0], end) if "scratch_load" in lines[i]]
     assert not reloads, reloads[:4]
+
+
+@pytest.fixture(scope="module")
+def device_helpers(tmp_path_factory):
+    """tests/c/device_edge.hip built for the host: the __host__ __device__
+    chunk helpers of tca/hip/device.h, the very code the kernels run."""
+    import subprocess
+    out = tmp_path_factory.mktemp("edge") / "device_edge"
+    hipcc = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "bin", "hipcc")
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    r = subprocess.run([hipcc, "--offload-arch=gfx950", "-O1", "-I", os.path.join(REPO, "tcacomp_amd", "csrc", "include"),
+                        os.path.join(REPO, "tests", "c", "device_edge.hip"), "-o", str(out)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+
+    def run(lines):
+        p = subprocess.run([str(out)], input="\n".join(lines) + "\n", capture_output=True, text=True, timeout=60)
+        assert p.returncode == 0, p.stderr
+        return [int(v) for v in p.stdout.split()]
+    return run
+
+
+U32 = 2 ** 32 - 1
+
+
+def test_device_ceil_div_at_the_u32_edge(device_helpers):
+    cases = [(0, 1), (0, 4096), (1, 4096), (4096, 4096), (4097, 4096), (U32, 1), (U32, 64), (U32, 4096),
+             (U32 - 63, 64), (U32 - 4095, 4096), (U32, 512), (2 ** 31, 3), (U32, U32)]
+    got = device_helpers(["ceil_div %d %d" % c for c in cases])
+    assert got == [-(-a // b) for a, b in cases]
+
+
+def _constants(source, names):
+    vals = {}
+    for n in names:
+        m = re.search(r"\b%s = (\d+)u" % n, source)
+        assert m, n
+        vals[n] = int(m.group(1))
+    return vals
+
+
+@pytest.mark.parametrize("R,C", [(U32, 1), (2 ** 31, 1), (2 ** 30 - 1, 4), (U32 // 3, 3), (U32 // 64, 64),
+                                 (64 * 1024 + 1, 2), (1, U32)])
+def test_column_split_device_matches_plan_at_the_u32_edge(device_helpers, R, C):
+    """Column family: the partial kernel's grid is column blocks x P with P
+    from the plan's 64-bit split record; each block recomputes P with the
+    device's col_split. They must agree for every R x C <= 2^32 - 1 (with a
+    32-bit round-up that wraps, blocks with p >= 1 took the one-chunk store
+    path and the merge read partials nobody wrote)."""
+    p = compiler.CompiledProgram("col_sum_max_dyn", programs.CONFIG_PROGRAMS["col_sum_max_dyn"]().emit(), "")
+    k = _constants(p.source, ["RMIN", "BLOCKS", "SPAN"])
+    ts = [TensorDesc(0x1000, (R, C), 0), TensorDesc(0x1000, (C,), 0), TensorDesc(0x1000, (C,), 0)]
+    syms = p.kernel_symbols()
+    arr = compiler._descriptors(ts)
+    sel = (ctypes.c_uint8 * len(syms))()
+    grids = (ctypes.c_uint64 * len(syms))()
+    blocks = (ctypes.c_uint32 * len(syms))()
+    assert _lib.lib().tca_program_selected(p.parsed(), arr, 3, None, 0, sel, grids, blocks, len(syms)) == 0, \
+        _lib.last_error()
+    part = [i for i, s in enumerate(syms) if sel[i] and re.search(r"_p\d+$", s)]
+    assert len(part) == 1, [s for i, s in enumerate(syms) if sel[i]]
+    v = int(syms[part[0]].rsplit("_p", 1)[1])
+    cb, = device_helpers(["ceil_div %d %d" % (C // v, k["SPAN"])])
+    P, = device_helpers(["col_split %d %d %d %d" % (R, cb, k["RMIN"], k["BLOCKS"])])
+    assert grids[part[0]] == cb * P, (syms[part[0]], grids[part[0]], cb, P)
+    merge = [i for i, s in enumerate(syms) if sel[i] and re.search(r"_m\d+$", s)]
+    assert (grids[merge[0]] > 0) == (P > 1)
+
+
+@pytest.mark.parametrize("R,C", [(1, U32), (1, U32 - 1), (3, U32 // 3 - 2), (255, U32 // 255 - 4), (1, 16388)])
+def test_split_rows_device_matches_plan_at_the_u32_edge(device_helpers, R, C):
+    """Split rows: the grid is rows x P from the plan (64-bit, capped at
+    PMAX); the device recomputes P = min(PMAX, ceil_div(VECS, CV)) and the
+    chunk length L = ceil_div(VECS, P). They must agree, and chunks
+    [p*L, p*L + min(L, VECS - p*L)) must tile [0, VECS) exactly."""
+    prog = programs.CONFIG_PROGRAMS["row_sum_max_dyn"]()
+    p = compiler.CompiledProgram("row_sum_max_dyn", prog.emit(), "")
+    src = p.source
+    assert "min(PMAX, tca::hip::ceil_div(VECS, CV))" in src and "tca::hip::ceil_div(VECS, P)" in src
+    assert "hi = lo + min(L, VECS - lo)" in src
+    k = _constants(src, ["CV", "PMAX"])
+    ts = [TensorDesc(0x1000, (R, C), 0), TensorDesc(0x1000, (R,), 0), TensorDesc(0x1000, (R,), 0)]
+    syms = p.kernel_symbols()
+    arr = compiler._descriptors(ts)
+    sel = (ctypes.c_uint8 * len(syms))()
+    grids = (ctypes.c_uint64 * len(syms))()
+    assert _lib.lib().tca_program_selected(p.parsed(), arr, 3, None, 0, sel, grids, None, len(syms)) == 0, \
+        _lib.last_error()
+    part = [i for i, s in enumerate(syms) if sel[i] and re.search(r"_p\d+$", s)]
+    assert len(part) == 1, [s for i, s in enumerate(syms) if sel[i]]
+    v = int(syms[part[0]].rsplit("_p", 1)[1])
+    vecs = C // v
+    cdiv, = device_helpers(["ceil_div %d %d" % (vecs, k["CV"])])
+    P = min(k["PMAX"], cdiv)
+    assert grids[part[0]] == R * P
+    L, = device_helpers(["ceil_div %d %d" % (vecs, P)])
+    covered = 0
+    for q in range(P):
+        lo = q * L
+        assert lo < vecs
+        hi = lo + min(L, vecs - lo)
+        assert hi <= U32 and lo == covered and hi - lo > 1024
+        covered = hi
+    assert covered == vecs

@@ -17,7 +17,8 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import (assert_reduce_close, canaries, compiled, host, out_dev, reduce_tol, run, to_dev)
+from helpers import (assert_layernorm_close, assert_reduce_close, canaries, compiled, host, out_dev, reduce_tol, run,
+                     to_dev)
 from tcacomp_amd import inputs
 from tcacomp_amd.compiler import TensorDesc
 from tcacomp_amd.pkg import EMIT_NO_FUSION, EMIT_NO_GEMM
@@ -160,8 +161,7 @@ def test_c4_layernorm(gpu, name, C, flags, R):
     run(p, [to_dev(x, gpu), to_dev(g, gpu), to_dev(bta, gpu), y], scalars=[float(inv_n), float(eps)])
     got = host(y)
     assert canaries(got) == 0
-    err = np.abs(got.astype(np.float64) - want)
-    assert err.max() <= reduce_tol(C) * (np.abs(want).max() + 1.0), "layernorm err %g" % err.max()
+    assert_layernorm_close(got, want, x, g, bta, float(eps), "C4 %s R=%d" % (name, R))
 
 
 def test_c4_full_size(gpu):
@@ -173,8 +173,9 @@ def test_c4_full_size(gpu):
     p = compiled("layernorm_1024")
     y = out_dev((R, C), gpu)
     run(p, [to_dev(x, gpu), to_dev(g, gpu), to_dev(bta, gpu), y], scalars=[1.0 / C, 1e-5])
-    err = np.abs(host(y).astype(np.float64) - want)
-    assert err.max() <= reduce_tol(C) * (np.abs(want).max() + 1.0)
+    got = host(y)
+    assert canaries(got) == 0
+    assert_layernorm_close(got, want, x, g, bta, 1e-5, "C4 full size")
 
 
 # ---------------------------------------------------------------- C5
@@ -322,3 +323,33 @@ def test_c5_full_size_bf16(gpu):
     bound = _gemm_bound(oracle.bf16_bits_to_f32(a[rows]), oracle.bf16_bits_to_f32(b), K)
     assert_reduce_close(got[rows], want, bound, K, "gemm bf16 4096^3 sample")
     assert math.isfinite(float(got.sum()))
+
+
+@pytest.mark.parametrize("name", ["gemm_f32", "gemm_bf16", "gemm_bf16_nt"])
+def test_c5_full_size_exact(gpu, name):
+    """C5's full shape, 4096^3, on small-integer operands in [-4, 4]: exact
+    in bf16 and fp32, every product exact and every partial sum an integer
+    of magnitude <= 16 * 4096 < 2^24, so every one of the 16.8 M outputs
+    (every tile, slice and MFMA lane) must equal the float64 product."""
+    import torch
+    M = N = K = 4096
+    _say("C5 full exact", name)
+    rng = np.random.default_rng(11)
+    a = rng.integers(-4, 5, (M, K)).astype(np.float32)
+    b = rng.integers(-4, 5, (K, N)).astype(np.float32)
+    want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+    if name == "gemm_f32":
+        ta, tb = to_dev(a, gpu), to_dev(b, gpu)
+    else:
+        bb = oracle.to_bf16_bits(b)
+        if name == "gemm_bf16_nt":
+            bb = np.ascontiguousarray(bb.T)
+        ta = to_dev(oracle.to_bf16_bits(a).view(np.int16), gpu).view(torch.bfloat16)
+        tb = to_dev(bb.view(np.int16), gpu).view(torch.bfloat16)
+    c = out_dev((M, N), gpu)
+    run(compiled(name), [ta, tb, c])
+    got = host(c)
+    assert canaries(got) == 0
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, "%s: %d of %d outputs differ; first at %s: %g vs %g" % (
+        name, len(bad), M * N, tuple(bad[0]), got[tuple(bad[0])], want[tuple(bad[0])])

@@ -2,14 +2,14 @@
 reductions and the row map of a layernorm, fused into the same row / stream
 kernel (one kernel, the per-row value in registers) and also stored as an
 output. y against the oracle's layernorm (same arithmetic: (x - mean) *
-rsqrtf(var + eps) * gamma + beta), tolerance 1e-5*sqrt(K) relative to the
-row's scale; rstd against a float64 evaluation of 1/sqrt(var + eps) within
+rsqrtf(var + eps) * gamma + beta), each element within the reduction
+tolerance 1e-5*sqrt(K) carried through the normalisation (helpers.layernorm_bound); rstd against a float64 evaluation of 1/sqrt(var + eps) within
 the same bound (rsqrtf on the device is ocml's, the oracle's 1/sqrtf)."""
 import numpy as np
 import pytest
 
 import oracle
-from helpers import canaries, compiled, host, out_dev, reduce_tol, run, to_dev
+from helpers import assert_layernorm_close, canaries, compiled, host, out_dev, reduce_tol, run, to_dev
 from tcacomp_amd import inputs
 
 pytestmark = pytest.mark.gpu
@@ -24,8 +24,7 @@ def _check(name, R, C, gpu):
     run(compiled(name), [to_dev(x, gpu), to_dev(g, gpu), to_dev(b, gpu), y, rstd], scalars=[inv_n, eps])
     got, gr = host(y), host(rstd)
     assert canaries(got) == 0 and canaries(gr) == 0
-    err = np.abs(got.astype(np.float64) - want)
-    assert err.max() <= reduce_tol(C) * (np.abs(want).max() + 1.0), "layernorm err %g" % err.max()
+    assert_layernorm_close(got, want, x, g, b, eps, "prefix %s R=%d C=%d" % (name, R, C))
     xd = x.astype(np.float64)
     var = ((xd - xd.mean(1, keepdims=True)) ** 2).mean(1)
     wr = 1.0 / np.sqrt(var + eps)

@@ -1,4 +1,4 @@
-"""Seeded random row programs (tcacomp_amd/randprog.py) on the device
+"""Seeded random row programs (tests/randprog.py) on the device
 against the CPU evaluation of the same spec (oracle/dsl_eval.py).
 
 Each program runs over row counts and row lengths that reach every variant
@@ -18,7 +18,8 @@ import pytest
 
 from dsl_eval import evaluate, evaluate_grid
 from helpers import CANARY
-from tcacomp_amd import compiler, randprog
+import randprog
+from tcacomp_amd import compiler
 from tcacomp_amd.compiler import TensorDesc
 from tcacomp_amd.pkg import EMIT_NO_FUSION, EMIT_NO_GEMM
 

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import assert_reduce_close, canaries, compiled, host, out_dev, reduce_tol, run, to_dev
+from helpers import (assert_layernorm_close, assert_reduce_close, canaries, compiled, host, out_dev, reduce_tol, run,
+                     to_dev)
 from tcacomp_amd import inputs
 
 pytestmark = pytest.mark.gpu
@@ -81,8 +82,7 @@ def test_stream_layernorm(gpu, R, C):
     run(compiled("layernorm_dyn"), [to_dev(x, gpu), to_dev(g, gpu), to_dev(b, gpu), y], scalars=[inv_n, eps])
     got = host(y)
     assert canaries(got) == 0
-    err = np.abs(got.astype(np.float64) - want)
-    assert err.max() <= reduce_tol(C) * (np.abs(want).max() + 1.0), "layernorm err %g" % err.max()
+    assert_layernorm_close(got, want, x, g, b, eps, "stream C4 R=%d C=%d" % (R, C))
 
 
 @pytest.mark.parametrize("R,C", [(1, 16388), (3, 1_000_000), (7, 4097), (255, 8194), (2, 4_000_002),

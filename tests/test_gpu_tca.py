@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import assert_reduce_close, canaries, host, out_dev, reduce_tol, run, to_dev
+from helpers import assert_layernorm_close, assert_reduce_close, canaries, host, out_dev, reduce_tol, run, to_dev
 from tcacomp_amd import compiler, inputs, syntax
 
 pytestmark = pytest.mark.gpu
@@ -75,7 +75,7 @@ def test_tca_c4_layernorm(gpu):
     run(tca("layernorm_1024"), [to_dev(x, gpu), to_dev(g, gpu), to_dev(b, gpu), y], scalars=[1.0 / C, 1e-5])
     got = host(y)
     assert canaries(got) == 0
-    assert np.abs(got.astype(np.float64) - want).max() <= reduce_tol(C) * (np.abs(want).max() + 1.0)
+    assert_layernorm_close(got, want, x, g, b, 1e-5, "tca C4")
 
 
 @pytest.mark.parametrize("name", ["gemm_f32", "gemm_bf16"])

@@ -126,6 +126,37 @@ def test_layernorm_against_float64_and_special_cases():
     assert np.array_equal(yc[0], b)
 
 
+@pytest.mark.parametrize("C", [96, 1024])
+def test_layernorm_bound_is_tight(C):
+    """The per-element layernorm parity bound of the GPU tests
+    (helpers.layernorm_bound): the oracle's fp32 evaluation is inside it
+    against float64, and plausible mistakes are outside it: the mean off by
+    1e-4, rstd off by 1e-4 relative, gamma applied reversed, beta dropped."""
+    from helpers import layernorm_bound
+    rng = np.random.default_rng(C)
+    R = 64
+    x = rng.standard_normal((R, C)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, C).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, C).astype(np.float32)
+    eps = 1e-5
+    bound = layernorm_bound(x, g, b, eps)
+    xd = x.astype(np.float64)
+    mu = xd.mean(1, keepdims=True)
+    rs = 1.0 / np.sqrt(((xd - mu) ** 2).mean(1, keepdims=True) + eps)
+    exact = (xd - mu) * rs * g + b
+    y = oracle.layernorm(x, g, b, float(np.float32(1.0 / C)), eps)
+    assert (np.abs(y - exact) / bound).max() < 0.5
+    planted = {"mean + 1e-4": (xd - mu - 1e-4) * rs * g + b,
+               "rstd * (1 + 1e-4)": (xd - mu) * rs * (1 + 1e-4) * g + b,
+               "gamma reversed": (xd - mu) * rs * g[::-1] + b,
+               "beta dropped": (xd - mu) * rs * g}
+    for what, wrong in planted.items():
+        assert (np.abs(wrong - exact) > bound).any(), what
+    # An element at the row mean is held to about 1e-5 * |gamma|, not to a
+    # fraction of the row's largest output.
+    assert bound.min() < 2e-5 and bound.min() < 1e-3 * np.abs(exact).max()
+
+
 def test_gemm_exact_small_integers_and_orientation():
     rng = np.random.default_rng(5)
     M, N, K = 13, 11, 29

@@ -8,8 +8,8 @@ import pytest
 
 import oracle
 from dsl_eval import evaluate, evaluate_grid, evaluate_grid_scalar, evaluate_scalar
-from tcacomp_amd import randprog
-from tcacomp_amd.randprog import Spec
+import randprog
+from randprog import Spec
 
 SPECS = [s for s in randprog.specs() if getattr(s, "kind", "row") == "row"]
 GRIDS = [s for s in randprog.specs() if getattr(s, "kind", "row") == "grid"]
@@ -148,7 +148,7 @@ def test_grid_evaluator_matches_brute_force(spec):
 
 
 def test_grid_known_answers():
-    from tcacomp_amd.randprog import GridSpec
+    from randprog import GridSpec
     spec = GridSpec("hand", "f32", 0, [("x0", "f32")], True, True, False, [], [
         {"kind": "map", "expr": ("sub", X0, ("leaf", "xt")), "comb": None, "piped": None, "out": "m0"},
         {"kind": "tmap", "expr": X0, "comb": None, "piped": None, "out": "t1"},
