@@ -10,7 +10,7 @@
  *   Stmt().Iter().Map().As().Reduce()...Store() chain rungs
  *        pkg/chain.go:360-552
  *   Builder.Build                      pkg/builder.go:340-370
- *   ir.Print                           internal/ir/print.go:34
+ *   ir.Print                           internal/ir/print.go:34-57 (tca_builder_ir)
  *   cxx.Emit(g, cg.Options) -> cg.Result   internal/cg/cxx/emit.go:85,
  *                                          internal/cg/cg.go:17-64
  * A Go lambda `func(l, r pkg.Expr) pkg.Expr` becomes a begin/end pair here:
@@ -92,8 +92,18 @@ int tca_chain_store(tca_builder b, int32_t chain, int32_t tensor, uint32_t n, co
 
 /* Verifies and freezes the program. */
 int tca_builder_build(tca_builder b);
-/* Canonical IR print of the built program (owned by the builder). */
+/* The reference's canonical IR print of the built program (owned by the
+ * builder): `statement #ID:` blocks in the doc notation, statement IDs
+ * numbered as the reference builder allocates them (the Stmt() reservation
+ * of pkg/builder.go:310-318). Byte-identical to the reference's golden
+ * pkg/testdata/matmul_scale.ir for that program. */
 const char* tca_builder_ir(tca_builder b);
+/* This build's structural dump of the built program (owned by the builder):
+ * declarations with types and extents, each chain's operand axes, reduced
+ * axes and lambda bodies. Equal dumps mean the same program. No counterpart
+ * in the reference (its print omits types and access axes); for tests and
+ * tools that compare programs. */
+const char* tca_builder_ir_full(tca_builder b);
 
 /* Runs the HIP emitter on the built program. kernel_name NULL = the program
  * name; target NULL = "gfx950". */

@@ -121,6 +121,7 @@ SIGNATURES = [
     ("tca_chain_store", _c.c_int, [_P, _I32, _I32, _U32, _c.POINTER(_I32)]),
     ("tca_builder_build", _c.c_int, [_P]),
     ("tca_builder_ir", _STR, [_P]),
+    ("tca_builder_ir_full", _STR, [_P]),
     ("tca_emit", _c.c_int, [_P, _STR, _STR, _I32, _c.POINTER(_P)]),
     ("tca_emit_source", _STR, [_P]),
     ("tca_emit_plan", _STR, [_P]),

@@ -117,6 +117,7 @@ int Builder::Dim(const std::string& name, int64_t extent) {
   g_.dims.push_back(d);
   const int id = static_cast<int>(g_.dims.size()) - 1;
   dim_by_name_[name] = id;
+  Take(1);
   return id;
 }
 
@@ -140,14 +141,16 @@ int Builder::Tensor(const std::string& name, ir::Elem elem, const std::vector<in
   g_.tensors.push_back(t);
   const int id = static_cast<int>(g_.tensors.size()) - 1;
   tensor_by_name_[name] = id;
+  Take(1);
   return id;
 }
 
 int Builder::Local(const std::string& name, ir::Elem elem, const std::vector<int>& dims) {
   if (final_) NoteDecl("local " + name + ": builder already finalized by Build");
   if (dims.empty()) NoteDecl("local " + name + ": must be a tensor type");
-  const int id = Tensor(name, elem, dims);
+  const int id = Tensor(name, elem, dims);  // one ID, as the MemNew node
   g_.tensors[id].local = true;
+  Take(1);  // the extent const (pkg/builder.go:270)
   return id;
 }
 
@@ -166,6 +169,7 @@ int Builder::ScalarParam(const std::string& name, ir::Elem elem) {
   e.index = idx;
   const int id = Intern(e);
   scalar_expr_.push_back(id);
+  Take(1);
   return id;
 }
 
@@ -217,6 +221,13 @@ ir::Elem Builder::ExprType(int id) const {
   return g_.exprs[id].type;
 }
 
+uint64_t Builder::ScalarRefs(const std::vector<int>& ids) const {
+  uint64_t n = 0;
+  for (int id : ids)
+    if (id >= 0 && id < static_cast<int>(g_.exprs.size()) && g_.exprs[id].op == ir::Op::Scalar) ++n;
+  return n;
+}
+
 int Builder::FirstError(const std::vector<int>& ids) const {
   for (int id : ids) {
     if (id < 0 || id >= static_cast<int>(g_.exprs.size())) return -2;
@@ -232,6 +243,7 @@ int Builder::Const(ir::Elem elem, double value) {
   if (elem == ir::Elem::F32) value = static_cast<double>(static_cast<float>(value));
   if (elem == ir::Elem::Bool) value = value != 0.0 ? 1.0 : 0.0;
   e.value = value;
+  Take(1);
   return Intern(e);
 }
 
@@ -264,6 +276,7 @@ int Builder::Bin(ir::BinOp op, int x, int y) {
   e.code = static_cast<int>(op);
   e.type = ir::BinResult(op, tx);
   e.args = {x, y};
+  Take(1 + ScalarRefs(e.args));
   return Intern(e);
 }
 
@@ -296,6 +309,7 @@ int Builder::Un(ir::UnOp op, int x) {
   e.code = static_cast<int>(op);
   e.type = t;
   e.args = {x};
+  Take(1 + ScalarRefs(e.args));
   return Intern(e);
 }
 
@@ -312,6 +326,7 @@ int Builder::Select(int cond, int a, int b) {
   e.op = ir::Op::Select;
   e.type = g_.exprs[a].type;
   e.args = {cond, a, b};
+  Take(1 + ScalarRefs(e.args));
   return Intern(e);
 }
 
@@ -328,6 +343,7 @@ int Builder::Cast(int x, ir::Elem to) {
   e.op = ir::Op::Cast;
   e.type = to;
   e.args = {x};
+  Take(1 + ScalarRefs(e.args));
   return Intern(e);
 }
 
@@ -350,6 +366,7 @@ int Builder::Call(const std::string& name, const std::vector<int>& args) {
   e.type = sig.result;
   e.text = name;
   e.args = args;
+  Take(1 + ScalarRefs(e.args));
   return Intern(e);
 }
 
@@ -357,6 +374,8 @@ int Builder::Stmt() {
   if (final_) NoteDecl("stmt: builder already finalized by Build");
   chains_.emplace_back();
   open_chain_ = static_cast<int>(chains_.size()) - 1;
+  chains_.back().chain.stmt_id = Take(1);
+  chains_.back().chain.ret_id = Take(1);
   return open_chain_;
 }
 
@@ -455,6 +474,7 @@ bool Builder::MapBegin(int chain, const std::vector<ir::Operand>& ops, std::vect
   c.pending_ops = ops;
   c.pending_params = *params;
   c.stage = piped ? kPipedOpen : kRootMapOpen;
+  Take(ops.size() + 2 * n);  // operand references; each parameter and its reference
   return true;
 }
 
@@ -472,6 +492,7 @@ bool Builder::MapEnd(int chain, int body) {
   st.fn.params = c.pending_params;
   st.fn.body = body;
   c.stage = piped ? kAfterMap : kRootAs;
+  Take(ScalarRefs({body}));
   return true;
 }
 
@@ -485,6 +506,7 @@ void Builder::As(int chain, const std::vector<int>& dims) {
     return;
   }
   const std::string what = piped ? "piped map" : "root map";
+  Take((dims.empty() ? 0 : 1) + 3);  // As (when axes are listed), lambda, map, iteration cluster
   for (int d : dims) {
     std::string msg;
     if (!CheckDim(d, what + " as", &msg)) {
@@ -563,6 +585,7 @@ bool Builder::ReduceBegin(int chain, int init, int* acc, int* now) {
   c.pending_params = {*acc, *now};
   c.pending_init = init;
   c.stage = kReduceOpen;
+  Take(4);
   return true;
 }
 
@@ -586,6 +609,7 @@ bool Builder::ReduceEnd(int chain, int body) {
   c.live.pop_back();
   c.chain.reduces.push_back(r);
   c.stage = kAfterReduce;
+  Take(ScalarRefs({r.init, body}) + 3);  // keyed init attribute, lambda, reduce
   return true;
 }
 
@@ -645,10 +669,16 @@ bool Builder::Store(int chain, int tensor, const std::vector<int>& axes) {
   c.chain.store_axes = axes;
   c.stage = kStored;
   open_chain_ = -1;
+  Take(1);
   if (!t.local) {
     bool seen = false;
     for (int o : g_.outputs) seen |= (o == tensor);
-    if (!seen) g_.outputs.push_back(tensor);
+    if (!seen) {
+      // The end node takes the reserved ID of the first chain that stores
+      // an output (pkg/builder.go:351-356).
+      if (g_.outputs.empty()) g_.end_stmt_id = c.chain.ret_id;
+      g_.outputs.push_back(tensor);
+    }
   }
   return true;
 }

@@ -121,6 +121,22 @@ class Builder {
   bool CheckOperands(ChainState& c, const std::vector<ir::Operand>& ops, std::vector<ir::Elem>* elems);
   int FirstError(const std::vector<int>& ids) const;
 
+  // The reference builder's graph-ID counter (internal/ir/node.go:176-183),
+  // advanced by the number of nodes each reference call allocates, so the
+  // print can number statements as the reference does: params 1 each, a
+  // local 2 (extent const, MemNew), an expression node 1 plus 1 per lazy
+  // scalar-param reference it materializes (pkg/expr.go:43-52), Stmt 2
+  // reserved IDs, a map 1 per operand reference and 2 per lambda parameter
+  // and then As + lambda + map + iteration cluster, a reduce 4 for its
+  // parameters and then attribute + lambda + reduce, a store 1.
+  uint64_t Take(uint64_t n) {
+    const uint64_t id = ref_next_;
+    ref_next_ += n;
+    return id;
+  }
+  uint64_t ScalarRefs(const std::vector<int>& ids) const;
+  uint64_t ref_next_ = 1;
+
   ir::Graph g_;
   std::map<std::string, int> dim_by_name_, tensor_by_name_, scalar_by_name_;
   std::map<std::string, int> intern_;

@@ -189,7 +189,8 @@ int tca_builder_build(tca_builder b) {
     if (b->is_built) return TCA_OK;
     if (!b->b.Build(&b->built)) return Status(b, false);
     b->is_built = true;
-    b->ir_text = tca::ir::Print(b->built);
+    b->ir_text = tca::ir::PrintReference(b->built);
+    b->ir_full = tca::ir::Print(b->built);
     return TCA_OK;
   });
 }
@@ -197,6 +198,11 @@ int tca_builder_build(tca_builder b) {
 const char* tca_builder_ir(tca_builder b) {
   if (b == nullptr || !b->is_built) return nullptr;
   return b->ir_text.c_str();
+}
+
+const char* tca_builder_ir_full(tca_builder b) {
+  if (b == nullptr || !b->is_built) return nullptr;
+  return b->ir_full.c_str();
 }
 
 int tca_emit(tca_builder b, const char* kernel_name, const char* target, int32_t flags, tca_emit_result* out) {

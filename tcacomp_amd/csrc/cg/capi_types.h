@@ -15,7 +15,8 @@ struct tca_builder_s {
   tca::pkg::Builder b;
   tca::ir::Graph built;
   bool is_built = false;
-  std::string ir_text;
+  std::string ir_text;  // the reference's canonical print
+  std::string ir_full;  // this build's structural dump
   std::string expr_err;
   std::string err;
 };

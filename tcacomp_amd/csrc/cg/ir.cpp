@@ -1,6 +1,7 @@
 // ir.cpp — element-type tables, the canonical printer and the verifier.
 #include "ir.h"
 
+#include <charconv>
 #include <cmath>
 #include <cstdio>
 #include <functional>
@@ -199,6 +200,237 @@ class Printer {
 }  // namespace
 
 std::string Print(const Graph& g) { return Printer(g).Run(); }
+
+std::string FormatFloat32Go(double v) {
+  const float f = static_cast<float>(v);
+  if (std::isnan(f)) return "NaN";
+  if (std::isinf(f)) return f > 0 ? "+Inf" : "-Inf";
+  const bool neg = std::signbit(f);
+  if (f == 0.0f) return neg ? "-0" : "0";
+  // Shortest digits that round-trip to f, as d.ddde[+-]XX.
+  char buf[64];
+  const auto r = std::to_chars(buf, buf + sizeof(buf), neg ? -f : f, std::chars_format::scientific);
+  const std::string sci(buf, r.ptr);
+  const size_t epos = sci.find('e');
+  const int exp10 = std::stoi(sci.substr(epos + 1));
+  std::string digits;
+  for (size_t i = 0; i < epos; ++i)
+    if (sci[i] != '.') digits += sci[i];
+  while (digits.size() > 1 && digits.back() == '0') digits.pop_back();
+  const int nd = static_cast<int>(digits.size()), dp = exp10 + 1;
+  std::string out = neg ? "-" : "";
+  if (exp10 < -4 || exp10 >= 6) {  // %e with nd - 1 fraction digits, >= 2 exponent digits
+    out += digits[0];
+    if (nd > 1) out += "." + digits.substr(1);
+    const int ae = exp10 < 0 ? -exp10 : exp10;
+    out += exp10 < 0 ? "e-" : "e+";
+    if (ae < 10) out += "0";
+    out += std::to_string(ae);
+    return out;
+  }
+  // %f with max(nd - dp, 0) fraction digits.
+  if (dp > 0) {
+    for (int i = 0; i < dp; ++i) out += i < nd ? digits[i] : '0';
+  } else {
+    out += "0";
+  }
+  const int frac = nd - dp > 0 ? nd - dp : 0;
+  if (frac > 0) {
+    out += ".";
+    for (int i = 0; i < frac; ++i) {
+      const int k = dp + i;
+      out += (k >= 0 && k < nd) ? digits[k] : '0';
+    }
+  }
+  return out;
+}
+
+namespace {
+
+// The reference printer's rendering (internal/ir/print.go): chains as stage
+// lines, scalar expressions with its precedence table (binPrec/exprPrec),
+// constants spelled by type (constText/FormatConst).
+class RefPrinter {
+ public:
+  explicit RefPrinter(const Graph& g) : g_(g) {}
+
+  std::string Run() {
+    std::ostringstream o;
+    bool first = true;
+    for (const Chain& c : g_.chains) {
+      if (!first) o << "\n";
+      first = false;
+      o << "statement #" << c.stmt_id << ":\n";
+      std::vector<std::string> stages;
+      stages.push_back("iter(" + DimList(c.iters) + ") -> " + MapText(c.root, false));
+      for (const ReduceStage& r : c.reduces)
+        stages.push_back("reduce(init=" + Value(r.init) + ", %0, " + LambdaText(r.fn) + ")");
+      if (c.has_piped) stages.push_back("iter() -> " + MapText(c.piped, true));
+      std::string st = "memstore(%" + TensorName(c.store_tensor);
+      for (int a : c.store_axes) st += "[@" + g_.dims[a].name + "]";
+      stages.push_back(st + ", %0)");
+      for (size_t i = 0; i < stages.size(); ++i) {
+        o << "  " << stages[i];
+        if (i + 1 < stages.size()) o << " |\n";
+      }
+      o << "\n";
+    }
+    if (!g_.outputs.empty()) {
+      if (!first) o << "\n";
+      o << "statement #" << g_.end_stmt_id << ":\n  return ";
+      for (size_t i = 0; i < g_.outputs.size(); ++i) o << (i ? ", %" : "%") << g_.tensors[g_.outputs[i]].name;
+      o << "\n";
+    }
+    return o.str();
+  }
+
+ private:
+  // A local is a MemNew allocation in the reference, not a named parameter:
+  // its printer has no name for it.
+  std::string TensorName(int t) const { return g_.tensors[t].local ? "?" : g_.tensors[t].name; }
+
+  std::string DimList(const std::vector<int>& dims) const {
+    std::string s;
+    for (size_t i = 0; i < dims.size(); ++i) s += (i ? ", @" : "@") + g_.dims[dims[i]].name;
+    return s;
+  }
+
+  // A tensor operand renders as its declared type's axes (paramRef case of
+  // the reference's value()), a local as "?".
+  std::string OperandText(const Operand& op) const {
+    const Tensor& t = g_.tensors[op.tensor];
+    if (t.local) return "?";
+    std::string s = t.name;
+    for (int d : t.dims) s += "[@" + g_.dims[d].name + "]";
+    return s;
+  }
+
+  std::string MapText(const MapStage& m, bool piped) const {
+    std::string s = "map(";
+    std::vector<std::string> vals;
+    if (piped) vals.push_back("%0");
+    for (const Operand& op : m.ops) vals.push_back(OperandText(op));
+    for (size_t i = 0; i < vals.size(); ++i) s += (i ? ", " : "") + vals[i];
+    s += ", " + LambdaText(m.fn) + ")";
+    if (!m.as.empty()) s += " as (" + DimList(m.as) + ")";
+    return s;
+  }
+
+  std::string LambdaText(const Lambda& fn) const {
+    std::string s = "lambda(";
+    for (size_t i = 0; i < fn.params.size(); ++i) s += (i ? ", " : "") + g_.exprs[fn.params[i]].text;
+    return s + "): " + Value(fn.body);
+  }
+
+  static int BinPrec(BinOp op) {
+    switch (op) {
+      case BinOp::LOr: return 1;
+      case BinOp::LAnd: return 2;
+      case BinOp::Or: return 3;
+      case BinOp::Xor: return 4;
+      case BinOp::And: return 5;
+      case BinOp::Eq: case BinOp::Ne: return 6;
+      case BinOp::Lt: case BinOp::Le: case BinOp::Gt: case BinOp::Ge: return 7;
+      case BinOp::Shl: case BinOp::Shr: return 8;
+      case BinOp::Add: case BinOp::Sub: return 9;
+      case BinOp::Mul: case BinOp::Div: case BinOp::Mod: return 10;
+    }
+    return 0;
+  }
+  static const char* BinSym(BinOp op) {
+    switch (op) {
+      case BinOp::LOr: return "||";
+      case BinOp::LAnd: return "&&";
+      case BinOp::Or: return "|";
+      case BinOp::Xor: return "^";
+      case BinOp::And: return "&";
+      case BinOp::Eq: return "==";
+      case BinOp::Ne: return "!=";
+      case BinOp::Lt: return "<";
+      case BinOp::Le: return "<=";
+      case BinOp::Gt: return ">";
+      case BinOp::Ge: return ">=";
+      case BinOp::Shl: return "<<";
+      case BinOp::Shr: return ">>";
+      case BinOp::Add: return "+";
+      case BinOp::Sub: return "-";
+      case BinOp::Mul: return "*";
+      case BinOp::Div: return "/";
+      case BinOp::Mod: return "%";
+    }
+    return "?";
+  }
+  static const char* UnSym(UnOp op) {
+    switch (op) {
+      case UnOp::Pos: return "+";
+      case UnOp::Neg: return "-";
+      case UnOp::LNot: return "!";
+      case UnOp::Not: return "~";
+    }
+    return "?";
+  }
+  int Prec(int id) const {
+    const Expr& e = g_.exprs[id];
+    if (e.op == Op::Bin) return BinPrec(static_cast<BinOp>(e.code));
+    if (e.op == Op::Un) return 11;
+    if (e.op == Op::Select) return 0;
+    return 12;
+  }
+
+  std::string ConstText(const Expr& e) const {
+    switch (e.type) {
+      case Elem::I8: case Elem::I16: case Elem::I32:
+        return std::to_string(static_cast<int64_t>(e.value));
+      case Elem::U8: case Elem::U16: case Elem::U32:
+        return std::to_string(static_cast<uint64_t>(e.value));
+      case Elem::Bool:
+        return e.value != 0.0 ? "true" : "false";
+      default: {
+        std::string s = FormatFloat32Go(e.value);
+        if (s.find_first_of(".eE") == std::string::npos) s += ".0";
+        return s;
+      }
+    }
+  }
+
+  std::string Value(int id) const {
+    const Expr& e = g_.exprs[id];
+    switch (e.op) {
+      case Op::Const: return ConstText(e);
+      case Op::Param: return e.text;
+      case Op::Scalar: return g_.scalars[e.index].name;
+      case Op::Bin: {
+        const int p = BinPrec(static_cast<BinOp>(e.code));
+        std::string l = Value(e.args[0]), r = Value(e.args[1]);
+        if (Prec(e.args[0]) < p) l = "(" + l + ")";
+        if (Prec(e.args[1]) <= p) r = "(" + r + ")";
+        return l + " " + BinSym(static_cast<BinOp>(e.code)) + " " + r;
+      }
+      case Op::Un: {
+        std::string x = Value(e.args[0]);
+        if (Prec(e.args[0]) <= 11) x = "(" + x + ")";
+        return UnSym(static_cast<UnOp>(e.code)) + x;
+      }
+      case Op::Select:
+        return Value(e.args[0]) + " ? " + Value(e.args[1]) + " : " + Value(e.args[2]);
+      case Op::Cast:
+        return std::string("cast<") + ElemName(e.type) + ">(" + Value(e.args[0]) + ")";
+      case Op::Call: {
+        std::string s = e.text + "(";
+        for (size_t i = 0; i < e.args.size(); ++i) s += (i ? ", " : "") + Value(e.args[i]);
+        return s + ")";
+      }
+      default:
+        return "<nil>";
+    }
+  }
+
+  const Graph& g_;
+};
+
+}  // namespace
+
+std::string PrintReference(const Graph& g) { return RefPrinter(g).Run(); }
 
 bool Verify(const Graph& g, std::string* err) {
   auto bad = [&](const std::string& m) {

@@ -99,6 +99,11 @@ struct Chain {
   MapStage piped;  // operands follow the piped value (params[0])
   int store_tensor = -1;
   std::vector<int> store_axes;
+  // The reference builder's construction-time IDs (pkg/builder.go:310-318):
+  // Stmt() reserves the statement's ID and an end-node ID before any of the
+  // chain's nodes exist. Only the canonical print reads them.
+  uint64_t stmt_id = 0;
+  uint64_t ret_id = 0;
 
   // Live axes at the store, in order.
   std::vector<int> LiveAxes() const;
@@ -112,14 +117,28 @@ struct Graph {
   std::vector<Expr> exprs;
   std::vector<Chain> chains;
   std::vector<int> outputs;  // non-local stored tensors, first-store order
+  uint64_t end_stmt_id = 0;  // the end node's statement ID: the first output chain's reserved one
 
   bool IsStored(int tensor) const;
   bool IsRead(int tensor) const;
 };
 
-// Canonical, deterministic text form (the reference's ir.Print role,
-// internal/ir/print.go:34).
+// The reference's canonical print (internal/ir/print.go:34-57): one
+// `statement #ID:` block per stored chain, stages in the doc notation
+//   iter(@m, @k) -> map(x[@m][@k], lambda(v): v) as (@m, @k) |
+//   reduce(init=0.0, %0, lambda(acc, now): acc + now) |
+//   memstore(%out[@m], %0)
+// then the end node `return %out, ...`. Statement IDs follow the reference
+// builder's construction-time numbering (Chain::stmt_id).
+std::string PrintReference(const Graph& g);
+// This build's structural dump: every declaration with its type and extent,
+// each chain's operand axes, reduced axes and lambda bodies in SSA form. Two
+// programs are the same program iff their dumps are equal.
 std::string Print(const Graph& g);
+// Go's strconv.FormatFloat(v, 'g', -1, 32) (shortest round-trip float32
+// digits; %e when the decimal exponent is < -4 or >= 6), the spelling the
+// reference's printer uses for float constants before appending ".0".
+std::string FormatFloat32Go(double v);
 // Structural verifier (the reference's ir.Verify role, internal/ir/verify.go:58).
 bool Verify(const Graph& g, std::string* err);
 // Type of a binary operation's result, given its (equal) operand type.

@@ -182,22 +182,69 @@ __device__ __forceinline__ void gemm_bf16_256_dma(const uint16_t* __restrict__ A
         fb[j] = frag_b_tr(Bs, wn + j * 32u, ks * 16u, lane);
     }
   };
-  // One 16-deep step: the MFMAs of the fragments in hand, while the next
-  // step's fragments are read (and, when `dma`, a slice is issued). The
-  // instruction interleave is left to the compiler's scheduler, which moves
-  // MFMAs across the reads and the barrier better than a fixed pattern.
+  // One 16-deep step, issued in a fixed order (each group fenced with
+  // sched_barrier; left to itself the scheduler sank the next step's reads
+  // behind the MFMAs and every step then waited on LDS latency):
+  //   MFMAs on the fragments in hand, j-major, so the B fragment read last in
+  //   the previous step is used last;
+  //   the next step's 12 (8 for [N][K] B) fragment reads, two per MFMA,
+  //   right after the first MFMA: they have the rest of the step to land;
+  //   when `dma`, the slice's 8 direct-to-LDS loads, two per MFMA.
   auto step = [&](uint32_t next_s, uint32_t next_ks, bool dma, uint32_t dma_s, uint32_t dma_k0) {
     bf16x8 ga[4], gb[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) ga[i] = fa[i];
 #pragma unroll
     for (int j = 0; j < 4; ++j) gb[j] = fb[j];
-    if (dma) issue(dma_s, dma_k0);
-    load_frags(next_s, next_ks);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gb[j], ga[i], acc[i][j], 0, 0, 0);
+    const uint16_t* As = a_slice(next_s);
+    const uint16_t* Bs = b_slice(next_s);
+    auto mf = [&](int i, int j) {
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gb[j], ga[i], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto rd_a = [&](int i) {
+      fa[i] = *reinterpret_cast<const bf16x8*>(&As[swz32(wm + i * 32u + (lane & 31u), next_ks * 2u + (lane >> 5))]);
+    };
+    auto rd_b = [&](int j) {
+      if constexpr (B_NK)
+        fb[j] = *reinterpret_cast<const bf16x8*>(&Bs[swz32(wn + j * 32u + (lane & 31u), next_ks * 2u + (lane >> 5))]);
+      else
+        fb[j] = frag_b_tr(Bs, wn + j * 32u, next_ks * 16u, lane);
+    };
+    const uint16_t* a0 = A16 + static_cast<uint64_t>(m0) * K + dma_k0;
+    const uint16_t* b0 = B_NK ? B16 + static_cast<uint64_t>(n0) * K + dma_k0 : B16 + static_cast<uint64_t>(dma_k0) * N + n0;
+    uint16_t* as = a_slice(dma_s);
+    uint16_t* bs = b_slice(dma_s);
+    auto dm = [&](int q) {  // load q/2 of A (q even) or of B (q odd)
+      const uint32_t ch = wave * 4u + (q >> 1);
+      if (q & 1) __builtin_amdgcn_global_load_lds(b0 + offb[q >> 1], (lds_void*)(bs + ch * 512u), 16, 0, 0);
+      else __builtin_amdgcn_global_load_lds(a0 + offa[q >> 1], (lds_void*)(as + ch * 512u), 16, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto fence = []() { __builtin_amdgcn_sched_barrier(0); };
+    fence();
+    mf(0, 0);
+    rd_a(0); rd_a(1); fence();
+    mf(1, 0);
+    rd_a(2); rd_a(3); fence();
+    mf(2, 0);
+    rd_b(0); fence();
+    mf(3, 0);
+    rd_b(1); fence();
+    mf(0, 1);
+    rd_b(2); fence();
+    mf(1, 1);
+    rd_b(3); fence();
+    if (dma) {
+      mf(2, 1); dm(0); dm(1);
+      mf(3, 1); dm(2); dm(3);
+      mf(0, 2); dm(4); dm(5);
+      mf(1, 2); dm(6); dm(7);
+    } else {
+      mf(2, 1); mf(3, 1); mf(0, 2); mf(1, 2);
+    }
+    mf(2, 2); mf(3, 2);
+    mf(0, 3); mf(1, 3); mf(2, 3); mf(3, 3);
   };
   // The barrier waits only for the slice about to be
   // read (vmcnt counts in issue order, 8 loads per slice and lane); a plain

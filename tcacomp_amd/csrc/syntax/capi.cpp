@@ -131,7 +131,8 @@ int tca_syntax_module_build_kernel(tca_syntax_module m, uint32_t i, tca_builder*
       return TCA_ERR_BUILD;
     }
     b->is_built = true;
-    b->ir_text = tca::ir::Print(b->built);
+    b->ir_text = tca::ir::PrintReference(b->built);
+    b->ir_full = tca::ir::Print(b->built);
     *out = b;
     return TCA_OK;
   } catch (const std::exception& e) {

@@ -137,7 +137,13 @@ class Program:
         self.name = b.name
 
     def IR(self):
+        """The reference's canonical print (internal/ir/print.go:34)."""
         s = _lib.lib().tca_builder_ir(self.b._h)
+        return s.decode() if s else ""
+
+    def IRFull(self):
+        """This build's structural dump: equal dumps, same program."""
+        s = _lib.lib().tca_builder_ir_full(self.b._h)
         return s.decode() if s else ""
 
     def emit(self, kernel_name=None, target=None, flags=0):

@@ -135,8 +135,15 @@ static int emit_c2(const char* kcache_hip, char** plan_out) {
   const char* ir;
   char* want;
   REQUIRE(err == NULL || err[0] == '\0', "build", err);
+  /* The reference's print: 5 params take IDs 1-5, the 0.0 init (built
+   * before the first Stmt) 6; the first Stmt reserves 7 (statement) and 8
+   * (end node, claimed by the first output store). */
   ir = tca_builder_ir(b);
-  REQUIRE(ir != NULL && strstr(ir, "row_sum_max_8192") != NULL, "ir", ir);
+  REQUIRE(ir != NULL && strncmp(ir, "statement #7:\n  iter(@R, @e8192) -> map(x[@R][@e8192], lambda(v): v)", 64) == 0,
+          "ir", ir);
+  REQUIRE(strstr(ir, "statement #8:\n  return %sum, %max\n") != NULL, "ir end node", ir);
+  REQUIRE(tca_builder_ir_full(b) != NULL && strstr(tca_builder_ir_full(b), "program row_sum_max_8192") != NULL,
+          "ir full", tca_builder_ir_full(b));
   REQUIRE(tca_emit(b, NULL, "gfx950", 0, &r) == TCA_OK, "emit", tca_builder_error(b));
   REQUIRE(tca_emit_hipcc_argc(r) > 0 && strstr(tca_emit_report(r), "row") != NULL, "emit report",
           tca_emit_report(r));

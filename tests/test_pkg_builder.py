@@ -1,6 +1,8 @@
 """The DSL builder through the C ABI (tca_cg.h) — the reference's pkg tests
 restated: eager checks (pkg/builder_test.go:21-160), typestate
 (pkg/builder_test.go:162), determinism (pkg/determinism_test.go:19-46)."""
+import os
+
 import pytest
 
 from tcacomp_amd.pkg import (TBF16, TF32, TI32, TU32, At, BuildError, Call, Cast, NewBuilder, Select)
@@ -230,7 +232,7 @@ def test_chained_reductions_and_full_typestate():
      .Reduce(b.Float32(float("-inf")), lambda a, v: Call("fmaxf", a, v))
      .Map([], lambda v: b.Mul(v, s)).As(i).Store(o, i))
     p = b.Build()
-    ir = p.IR()
+    ir = p.IRFull()
     assert "reduce init=0:f32 over @k" in ir and "reduce init=-inf:f32 over @j" in ir
     assert "store o[@i]" in ir
 
@@ -249,13 +251,13 @@ def _oracle_program(name):
 
 def test_determinism_print_and_emit():
     p1, p2 = _oracle_program("matmul_scale"), _oracle_program("matmul_scale")
-    assert p1.IR() == p2.IR()
+    assert p1.IR() == p2.IR() and p1.IRFull() == p2.IRFull()
     e1, e2 = p1.emit(), p2.emit()
     assert e1.source == e2.source and e1.plan == e2.plan
 
 
-def test_ir_print_shape():
-    ir = _oracle_program("matmul_scale").IR()
+def test_ir_full_dump_shape():
+    ir = _oracle_program("matmul_scale").IRFull()
     assert ir.splitlines()[0] == "program matmul_scale"
     assert "map on(lhs[@m][@n], rhs[@n][@k]) (l: f32, r: f32) { %0 = mul l r; -> %0: f32 } as(@m, @k, @n)" in ir
     assert "reduce init=0:f32 over @n (acc: f32, now: f32) { %0 = add acc now; -> %0: f32 }" in ir
@@ -278,7 +280,7 @@ def test_gvn_hash_consing_folds_duplicates():
         return b.Mul(a, c)
     b.Stmt().Iter(m).Map([At(x, m)], body).As(m).Store(o, m)
     assert seen["same"]
-    ir = b.Build().IR()
+    ir = b.Build().IRFull()
     assert ir.count(" mul ") == 2 and ir.count(" add ") == 1
 
 
@@ -291,4 +293,78 @@ def test_build_freezes():
     b.Build()
     b.Dim("late", 0)
     b2 = NewBuilder("fresh")
-    assert b2.Build().IR().startswith("program fresh")
+    assert b2.Build().IRFull().startswith("program fresh")
+
+
+def _matmul_scale_reference_order():
+    """pkg/oracle_test.go:16-56, call for call: the builder calls (and so the
+    graph IDs they take) in the reference's order."""
+    b = NewBuilder("matmul_scale")
+    m, k, n = b.Dim("m", 0), b.Dim("k", 0), b.Dim("n", 0)
+    lhs = b.Tensor("lhs", TF32, m, n)
+    rhs = b.Tensor("rhs", TF32, n, k)
+    out = b.Tensor("output", TF32, m, k)
+    scale = b.ScalarParam("scale", TF32)
+    (b.Stmt().Iter(m, k, n).Map([At(lhs, m, n), At(rhs, n, k)], lambda l, r: b.Mul(l, r)).As(m, k, n)
+     .Reduce(b.Float32(0.0), lambda acc, v: b.Add(acc, v)).Map([], lambda v: b.Mul(v, scale)).As(m, k)
+     .Store(out, m, k))
+    return b.Build()
+
+
+def test_ir_print_matches_reference_golden():
+    """tca_builder_ir is the reference's ir.Print: byte-identical to its
+    doc-pinned golden (pkg/testdata/matmul_scale.ir, copied verbatim into
+    tests/golden/; pkg/oracle_test.go:58-63 asserts the same bytes)."""
+    golden = open(os.path.join(os.path.dirname(__file__), "golden", "matmul_scale.ir")).read()
+    assert _matmul_scale_reference_order().IR() == golden
+
+
+def test_ir_print_notation():
+    """Stages the golden does not reach, in the printer's rules
+    (internal/ir/print.go): chained reductions, a local (a MemNew in the
+    reference: no name, `?`), select / cast / call / unary rendering,
+    precedence parentheses (binPrec: right operand parenthesized at equal
+    precedence), typed constants, and one end node over every output in
+    first-store order, numbered with the first output chain's reserved ID.
+    Statement IDs beyond the first chain follow the reference's allocation
+    counts; the reference holds no golden for them (parity unpinned)."""
+    b = NewBuilder("notation")
+    r, c = b.Dim("r", 0), b.Dim("c", 8)
+    x = b.Tensor("x", TF32, r, c)
+    s = b.Tensor("s", TF32, r)
+    q = b.Tensor("q", TF32, r)
+    t = b.Local("t", TF32, r)
+    a = b.ScalarParam("a", TF32)
+    (b.Stmt().Iter(r, c).Map([At(x, r, c)], lambda v: b.Sub(v, b.Sub(a, b.Float32(1.5)))).As(r, c)
+     .Reduce(b.Neg(b.Float32(float("inf"))), lambda acc, v: Call("fmaxf", acc, v)).Store(t, r))
+    (b.Stmt().Iter(r, c).Map([At(x, r, c), At(t, r)], lambda l, m: Select(b.Gt(l, m), Cast(b.Int32(3), TF32), b.Mul(l, b.Add(m, b.Float32(1e-5))))).As(r, c)
+     .Reduce(b.Float32(0), lambda acc, v: b.Add(acc, v)).Store(s, r))
+    (b.Stmt().Iter(r).Map([At(t, r)], lambda v: b.Div(v, b.Float32(1e6))).As(r).Store(q, r))
+    ir = b.Build().IR()
+    # params r, c, x, s, q (1-5), the local (6-7), a (8): the first chain reserves 9 and 10
+    assert ir.startswith("statement #9:\n  iter(@r, @c) -> map(x[@r][@c], lambda(v): v - (a - 1.5)) as (@r, @c) |\n"
+                         "  reduce(init=-+Inf.0, %0, lambda(acc, now): fmaxf(acc, now)) |\n  memstore(%?[@r], %0)\n"), ir
+    assert ("map(x[@r][@c], ?, lambda(l, r): l > r ? cast<f32>(3) : l * (r + 1e-05)) as (@r, @c) |\n"
+            "  reduce(init=0.0, %0, lambda(acc, now): acc + now) |\n  memstore(%s[@r], %0)\n") in ir
+    assert "iter(@r) -> map(?, lambda(v): v / 1e+06) as (@r) |\n  memstore(%q[@r], %0)\n" in ir
+    ids = [int(l.split("#")[1].rstrip(":")) for l in ir.splitlines() if l.startswith("statement #")]
+    assert ids[:3] == sorted(ids[:3]) and len(set(ids)) == 4
+    # the end node: the reserved end ID of chain 2, the first to store an output
+    assert ir.endswith("statement #%d:\n  return %%s, %%q\n" % (ids[1] + 1))
+
+
+@pytest.mark.parametrize("value,text", [
+    (0.0, "0.0"), (-0.0, "-0.0"), (0.1, "0.1"), (0.3, "0.3"), (2.5, "2.5"), (-0.75, "-0.75"),
+    (100000.0, "100000.0"), (123456.7, "123456.7"), (1e6, "1e+06"), (16777216.0, "1.6777216e+07"),
+    (0.0001, "0.0001"), (0.00001, "1e-05"), (3.4028234663852886e38, "3.4028235e+38"),
+    (1.401298464324817e-45, "1e-45"), (1.1754943508222875e-38, "1.1754944e-38"),
+    (float("inf"), "+Inf.0"), (float("nan"), "NaN.0")])
+def test_ir_print_float_constants(value, text):
+    """Float constants as the reference spells them (internal/ir/print.go
+    FormatConst): Go's strconv.FormatFloat(v, 'g', -1, 32), then ".0" when
+    the result has no '.', 'e' or 'E'."""
+    b = NewBuilder("k")
+    m = b.Dim("m", 0)
+    x, o = b.Tensor("x", TF32, m), b.Tensor("o", TF32, m)
+    b.Stmt().Iter(m).Map([At(x, m)], lambda v: b.Mul(v, b.Float32(value))).As(m).Store(o, m)
+    assert "lambda(v): v * %s)" % text in b.Build().IR()
