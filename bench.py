@@ -250,14 +250,12 @@ def _cpu_baseline(key, args, threads):
         return (x.size * 4 + 2 * x.shape[0] * 4) / dt / 1e9, "GB/s", "full [8192,8192]"
     if key == "c3":
         (x,) = args
-        xs = np.ascontiguousarray(x[:2048])
-        dt = best(lambda: oracle.softmax(xs, threads))
-        return 2 * xs.size * 4 / dt / 1e9, "GB/s", "2048 of 16384 rows"
+        dt = best(lambda: oracle.softmax(x, threads))
+        return 2 * x.size * 4 / dt / 1e9, "GB/s", "full [16384,4096]"
     if key == "c4":
         x, g, b = args
-        xs = np.ascontiguousarray(x[:8192])
-        dt = best(lambda: oracle.layernorm(xs, g, b, 1.0 / 1024, 1e-5, threads))
-        return (2 * xs.size * 4 + 2 * 1024 * 4) / dt / 1e9, "GB/s", "8192 of 32768 rows"
+        dt = best(lambda: oracle.layernorm(x, g, b, 1.0 / 1024, 1e-5, threads))
+        return (2 * x.size * 4 + 2 * 1024 * 4) / dt / 1e9, "GB/s", "full [32768,1024]"
     a, b = args
     rows = 16 * max(1, threads)
     asub = np.ascontiguousarray(a[:rows])
@@ -267,13 +265,79 @@ def _cpu_baseline(key, args, threads):
     return 2 * rows * 4096 * 4096 / dt / 1e12, "TFLOP/s", "%d of 4096 rows" % rows
 
 
-def _traffic(symbol):
+def _traffic(symbol, prog):
+    """HBM bytes per launch of `symbol` from profiles/traffic.json (rocprof
+    FETCH_SIZE + WRITE_SIZE, calibration-scaled), with where they come from.
+    The file records the code-object key (a hash of the emitted source, the
+    hipcc flags and the device headers) each figure was profiled with; when
+    the kernel launched here has another key the figure is stale and is not
+    reported."""
     p = os.path.join(REPO, "profiles", "traffic.json")
     if not os.path.exists(p):
-        return None
+        return None, "no profiles/traffic.json"
     with open(p) as f:
         t = json.load(f)
-    return t.get(symbol)
+    e = t.get(symbol)
+    if e is None:
+        return None, "kernel not profiled"
+    if not isinstance(e, dict):
+        return None, "profiled without a code-object key: provenance unknown"
+    key = os.path.basename(prog.hsaco).rsplit("-", 1)[-1].split(".")[0]
+    if e.get("code_object") != key:
+        return None, "stale: kernel changed since it was profiled (%s, now %s)" % (e.get("code_object"), key)
+    return e["bytes"], "profiles/traffic.json (%s, code object %s)" % (t.get("_profiled", "?"), key)
+
+
+def _suite(dev, steps):
+    """The reference's 14 suite kernels at testing/suite.toml's dims, inputs
+    from elem(i): device time per launch (hipEvents over `steps` launches),
+    the reference runner's BenchReport (host launch + synchronize per
+    iteration, 20 iterations), the achieved rate over suite.toml's
+    bench_bytes (and flops for contractions), and the reference's own A6000
+    figures."""
+    import torch
+    from tcacomp_amd import _lib, compiler, programs, suite
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {}
+    for name in sorted(suite.REGISTRY):
+        prog = compiler.compile_program(programs.SUITE[name][0](), jit=os.environ.get("TCA_JIT", "0") != "0")
+        ins, oshape = suite.host_inputs(name)
+        args = [torch.from_numpy(a).to(dev) for a in ins] + [torch.empty(oshape, device=dev)]
+        sc = suite.scalars(name)
+        for _ in range(20):
+            prog.launch(args, scalars=sc, stream=stream)
+        torch.cuda.synchronize()
+        e0, e1 = _events()
+        _lib.check(L.tca_rt_event_record(e0, ctypes.c_void_p(stream)))
+        for _ in range(steps):
+            prog.launch(args, scalars=sc, stream=stream)
+        _lib.check(L.tca_rt_event_record(e1, ctypes.c_void_p(stream)))
+        torch.cuda.synchronize()
+        ms = ctypes.c_float()
+        _lib.check(L.tca_rt_event_elapsed_ms(e0, e1, ctypes.byref(ms)))
+        L.tca_rt_event_destroy(e0)
+        L.tca_rt_event_destroy(e1)
+        dev_us = ms.value * 1e3 / steps
+        host = []
+        for _ in range(20):
+            t0 = time.perf_counter()
+            prog.launch(args, scalars=sc, stream=stream)
+            torch.cuda.synchronize()
+            host.append((time.perf_counter() - t0) * 1e6)
+        cat, dims, tol, bench_bytes = suite.REGISTRY[name]
+        ref_avg, ref_min = suite.REFERENCE_A6000_US[name]
+        e = {"dims": list(dims), "kernels": prog.selected_symbols(args), "device_us": dev_us,
+             "bench_us": {"avg": sum(host) / len(host), "min": min(host)},
+             "bench_bytes": bench_bytes, "achieved_GBps": bench_bytes / (dev_us * 1e-6) / 1e9,
+             "reference_a6000_bench_us": {"avg": ref_avg, "min": ref_min},
+             "speedup_vs_reference_min": ref_min / min(host)}
+        if suite.flops(name):
+            e["achieved_GFLOPs"] = suite.flops(name) / (dev_us * 1e-6) / 1e9
+        out[name] = e
+        print("[bench] suite %s %.2f us device, %.1f us launch+sync (reference A6000 %.1f us)"
+              % (name, dev_us, min(host), ref_min), file=sys.stderr, flush=True)
+    return out
 
 
 def main():
@@ -285,6 +349,7 @@ def main():
     ap.add_argument("--settle-ms", type=float, default=1000.0,
                     help="untimed launches per config before the warmup steps, in wall-clock ms")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    ap.add_argument("--no-suite", action="store_true", help="skip the reference suite's 14 kernels")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the row configurations would "
@@ -296,7 +361,11 @@ def main():
     dev = torch.device("cuda:0")
     _lib.check(_lib.lib().tca_rt_init(0))
     keys = [k for k in args.configs.split(",") if k]
-    threads = int(os.environ.get("TCA_CPU_THREADS", "1"))
+    # The N-core CPU figure uses the host's cores (the box's CPU share: its
+    # OMP_NUM_THREADS), overridable with TCA_CPU_THREADS.
+    ncpu = os.cpu_count() or 1
+    threads = int(os.environ.get("TCA_CPU_THREADS") or os.environ.get("OMP_NUM_THREADS") or ncpu)
+    threads = max(1, min(threads, ncpu))
     results = {}
     for key in keys:
         prog, sets, scalars, work, cpu = _setup(key, dev)
@@ -306,22 +375,24 @@ def main():
                  "host_wall_ms": wall_ms}
         if work["bound"] == "hbm":
             gbs = work["bytes"] / (ms * 1e-3) / 1e9
+            traffic, source = _traffic(sym, prog)
             entry["roofline"] = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                 "frac": gbs / HBM_PEAK_GBS, "traffic": _traffic(sym)}
+                                 "frac": gbs / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": source}
             entry["algorithmic_bytes"] = work["bytes"]
         else:
             tf = work["flops"] / (ms * 1e-3) / 1e12
             peak = MFMA_PEAK_TFLOPS[work["dtype"]]
+            traffic, source = _traffic(sym, prog)
             entry["roofline"] = {"bound": "mfma", "achieved": tf, "peak": peak, "unit": "TFLOP/s",
-                                 "frac": tf / peak, "traffic": _traffic(sym)}
+                                 "frac": tf / peak, "traffic": traffic, "traffic_source": source}
             entry["algorithmic_flops"] = work["flops"]
         if not args.no_cpu and cpu is not None:
             v1, unit, sample = _cpu_baseline(key, cpu[1], 1)
             entry["cpu_baseline"] = {"value": v1, "unit": unit, "cores": 1, "kind": "port", "sample": sample}
-            if threads > 1:
-                vn, _, _ = _cpu_baseline(key, cpu[1], threads)
-                entry["cpu_baseline_ncores"] = {"value": vn, "unit": unit, "cores": threads, "kind": "port",
-                                                "sample": sample}
+            vn, _, sample_n = _cpu_baseline(key, cpu[1], threads)
+            entry["cpu_baseline_ncores"] = {"value": vn, "unit": unit, "cores": threads, "kind": "port",
+                                            "sample": sample_n + " (rows split over the cores, each row's fold order "
+                                            "unchanged: results bit-identical to 1 core)"}
         results[key] = entry
         print("[bench] %s %s %.4f ms %s" % (key, sym, ms, json.dumps(entry["roofline"])), file=sys.stderr,
               flush=True)
@@ -345,8 +416,11 @@ def main():
         "config": {"workload": head["config"], "kernel": head["kernel"]},
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
+        "cpu_baseline_ncores": head.get("cpu_baseline_ncores"),
         "kernels": results,
     }
+    if not args.no_suite:
+        line["suite"] = _suite(dev, 200)
     print(json.dumps(line))
 
 

@@ -54,3 +54,11 @@ def normal(shape, sigma, tensor_id, seed=SEED, chunk=1 << 23):
         r = np.sqrt(-2.0 * np.log(u1))
         out[s:e] = (sigma * r * np.cos(2.0 * np.pi * u2)).astype(np.float32)
     return out.reshape(shape)
+
+
+def elem(n):
+    """The reference suite's input formula (testing/runners/common.cuh:19-21):
+    elem(i) = float32((i * 2654435761 mod 2^32) mod 1000) / 1000, i < 2^32."""
+    i = np.arange(n, dtype=np.uint64)
+    v = ((i * np.uint64(2654435761)) & np.uint64(0xFFFFFFFF)) % np.uint64(1000)
+    return v.astype(np.float32) / np.float32(1000.0)

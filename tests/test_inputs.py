@@ -22,3 +22,11 @@ def test_distributions():
     n = inputs.normal((1 << 20,), 2.0, 0)
     assert abs(float(n.mean())) < 1e-2 and abs(float(n.std()) - 2.0) < 1e-2
     assert np.isfinite(n).all()
+
+
+def test_elem_matches_the_oracle():
+    """The product's elem(i) (the suite runners' input formula) equals the C
+    oracle's restatement of testing/runners/common.cuh:19-21."""
+    import oracle
+    for n in (0, 1, 999, 1001, 1 << 20):
+        assert np.array_equal(inputs.elem(n), oracle.elem(n)), n
