@@ -160,6 +160,21 @@ int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tens
 /* Name of kernel i of the program (for profiling), or NULL. */
 const char* tca_program_kernel_name(tca_program p, uint32_t i);
 
+/* tca_program_launch without any allocation: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * same contract checks and kernels as tca_program_launch; HBM locals and the
+ * partials of split and column reductions live in one 32 MiB scratch array
+ * per device, part of this library's device code, whose address
+ * tca_rt_init(device) takes (call it first on every device used). A launch
+ * whose workspace at these dims exceeds 32 MiB fails with TCA_ERR_INVALID
+ * before anything is queued. Every call on one GPU shares that array and it
+ * keeps the last call's contents: calls whose kernels overlap on one GPU
+ * (other streams, other threads) race; calls on one stream are ordered. */
+int tca_program_launch_noalloc(tca_program p, const tca_tensor* tensors, uint32_t n_tensors,
+                               const uint32_t* free_dims, uint32_t n_free_dims, const double* scalars,
+                               uint32_t n_scalars, tca_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -3,8 +3,9 @@ object the tests and the bench launch.
 
 The host library holds the runtime (plain HIP host API), the plan
 interpreter, the DSL builder, the .tca text frontend and the HIP emitter; it is ordinary C++ built
-with g++ against the ROCm headers. Device code exists only as emitted
-kernels, compiled by hipcc for gfx950 into ``_kcache/``.
+with g++ against the ROCm headers, plus one hipcc-built source (rt/scratch.hip:
+the device array behind the allocation-free launch). Kernels exist only as
+emitted code objects, compiled by hipcc for gfx950 into ``_kcache/``.
 """
 import concurrent.futures
 import os
@@ -34,6 +35,8 @@ SOURCES = [
     "syntax/capi.cpp",
 ]
 
+HIP_SOURCES = ["rt/scratch.hip"]
+
 CXXFLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
             "-I" + os.path.join(ROCM, "include"), "-I" + os.path.join(REPO, "include"),
             "-I" + os.path.join(CSRC, "rt")]
@@ -55,6 +58,15 @@ def build_library(jobs=8):
         obj = os.path.join(OBJ_DIR, s.replace("/", "_").replace(".cpp", ".o"))
         objs.append(obj)
         cmds.append(["g++"] + CXXFLAGS + ["-c", src, "-o", obj])
+    # The one device-code source of the library: the allocation-free
+    # launch's scratch array (a device global, so hipcc builds it for gfx950).
+    for s in HIP_SOURCES:
+        src = os.path.join(CSRC, s)
+        obj = os.path.join(OBJ_DIR, s.replace("/", "_").replace(".hip", ".o"))
+        objs.append(obj)
+        cmds.append([os.path.join(ROCM, "bin", "hipcc"), "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC",
+                     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                     "-I" + os.path.join(CSRC, "rt"), "-c", src, "-o", obj])
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
     tmp = LIB + ".tmp"

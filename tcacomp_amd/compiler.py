@@ -115,17 +115,19 @@ class CompiledProgram:
             self._h = h
         return self._h
 
-    def launch(self, tensors, free_dims=(), scalars=(), stream=None):
+    def launch(self, tensors, free_dims=(), scalars=(), stream=None, noalloc=False):
         """Launches every kernel of the program on `stream` (a hipStream_t
-        handle as int, or None for the current torch stream)."""
+        handle as int, or None for the current torch stream). noalloc takes
+        the workspace from the device's scratch array
+        (tca_program_launch_noalloc) instead of allocating one."""
         h = self.load()
         arr = _descriptors(tensors)
         fd = (ctypes.c_uint32 * max(1, len(free_dims)))(*free_dims)
         sc = (ctypes.c_double * max(1, len(scalars)))(*[float(s) for s in scalars])
         if stream is None:
             stream = _current_stream()
-        _lib.check(_lib.lib().tca_program_launch(h, arr, len(tensors), fd, len(free_dims), sc, len(scalars),
-                                                 ctypes.c_void_p(stream)))
+        fn = _lib.lib().tca_program_launch_noalloc if noalloc else _lib.lib().tca_program_launch
+        _lib.check(fn(h, arr, len(tensors), fd, len(free_dims), sc, len(scalars), ctypes.c_void_p(stream)))
 
     def __del__(self):
         try:

@@ -24,6 +24,7 @@
 #include <vector>
 
 #include "plan.h"
+#include "scratch.h"
 
 namespace {
 
@@ -129,7 +130,11 @@ int tca_rt_init(int device) {
   if (device < 0 || device >= n) return fail(TCA_ERR_INVALID, "init: device %d not present (%d devices)", device, n);
   TCA_HIP_TRY(hipSetDevice(device));
   DeviceLimits l;
-  return query_limits(&l);
+  int rc = query_limits(&l);
+  if (rc != TCA_OK) return rc;
+  // The allocation-free launch's scratch: its device address on this device.
+  TCA_HIP_TRY(tca::rt::ScratchInit(device));
+  return TCA_OK;
 }
 
 int tca_rt_device_info(int device, tca_device_info* out) {
@@ -403,8 +408,15 @@ int tca_program_selected(tca_program p, const tca_tensor* tensors, uint32_t n_te
   return TCA_OK;
 }
 
-int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
-                       uint32_t n_free_dims, const double* scalars, uint32_t n_scalars, tca_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// The body of both launch entry points. `noalloc` takes the workspace from
+// the device's scratch array instead of the program's per-stream workspace.
+int launch_program(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
+                   uint32_t n_free_dims, const double* scalars, uint32_t n_scalars, tca_stream_t stream,
+                   bool noalloc) {
   if (p == nullptr) return fail(TCA_ERR_INVALID, "program_launch: null program");
   if (p->mod == nullptr) return fail(TCA_ERR_INVALID, "program_launch: program was parsed, not loaded");
   const auto& pl = p->plan;
@@ -438,7 +450,18 @@ int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tens
   // the stream and frees the old buffer, which must not happen between
   // reading the pointer here and queueing the kernels that use it.
   std::unique_lock<std::mutex> lk(p->mu, std::defer_lock);
-  if (ws_bytes > 0) {
+  if (noalloc) {
+    int dev = 0;
+    TCA_HIP_TRY(hipGetDevice(&dev));
+    if (ws_bytes > tca::rt::kScratchBytes)
+      return fail(TCA_ERR_INVALID,
+                  "program_launch_noalloc: program %s needs %zu bytes of scratch at these dims, more than the %zu "
+                  "bytes the allocation-free launch has (use tca_program_launch)",
+                  pl.name.c_str(), ws_bytes, tca::rt::kScratchBytes);
+    ws = tca::rt::ScratchPtr(dev);
+    if (ws == nullptr)
+      return fail(TCA_ERR_INVALID, "program_launch_noalloc: tca_rt_init(%d) has not set up this device", dev);
+  } else if (ws_bytes > 0) {
     lk.lock();
     tca_program_s::Workspace& w = p->workspaces[stream];
     if (w.bytes < ws_bytes) {
@@ -495,6 +518,21 @@ int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tens
     if (e != hipSuccess) return hip_fail(e, "hipModuleLaunchKernel");
   }
   return TCA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
+                       uint32_t n_free_dims, const double* scalars, uint32_t n_scalars, tca_stream_t stream) {
+  return launch_program(p, tensors, n_tensors, free_dims, n_free_dims, scalars, n_scalars, stream, false);
+}
+
+int tca_program_launch_noalloc(tca_program p, const tca_tensor* tensors, uint32_t n_tensors,
+                               const uint32_t* free_dims, uint32_t n_free_dims, const double* scalars,
+                               uint32_t n_scalars, tca_stream_t stream) {
+  return launch_program(p, tensors, n_tensors, free_dims, n_free_dims, scalars, n_scalars, stream, true);
 }
 
 }  // extern "C"
