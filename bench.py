@@ -51,6 +51,12 @@ CONFIGS = {
     # C2's reductions over the non-contiguous axis (the column family): the
     # reference's middle-axis reduction form; not a configuration
     "c2c": ("col_sum_max_dyn", "column sum+max f32 [8192,8192] (column family)"),
+    # dependent reductions over the non-contiguous axis (a variance reading
+    # its mean): one column nest of two passes, lowered as a partial + merge
+    # pair per pass ([8192, 8192]: 32 row chunks) or as one whole-column
+    # kernel (64 rows: one chunk); not configurations
+    "c2mv": ("col_mean_var_dyn", "column mean+variance f32 [1,8192,8192] (column family, 2 passes, pairs)"),
+    "c2mw": ("col_mean_var_dyn", "column mean+variance f32 [1,64,1048576] (column family, 2 passes, whole)"),
     # not a configuration: the plain copy used to calibrate rocprof counters
     "copy": ("copy_f32", "copy f32 [8192,8192] (counter calibration)"),
 }
@@ -88,6 +94,18 @@ def _setup(key, dev):
         make = lambda i: [dev_f32(x), torch.empty(C, device=dev), torch.empty(C, device=dev)]  # noqa: E731
         scalars = []
         work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = None
+    elif key in ("c2mv", "c2mw"):
+        R, C = (8192, 8192) if key == "c2mv" else (64, 1 << 20)
+        x = inputs.normal((1, R, C), 1.0, 0)
+        # each pass reads the tile (the program's two reductions): 2 R C 4
+        # bytes, plus the two [C] results
+        algo = 2 * R * C * 4 + 2 * C * 4
+        per_set = algo
+        make = lambda i: [dev_f32(x), torch.empty((1, C), device=dev), torch.empty((1, C), device=dev)]  # noqa: E731
+        scalars = [1.0 / R]
+        work = {"bytes": algo, "bound": "hbm", "shape": [1, R, C], "single_read_bytes": R * C * 4 + 2 * C * 4}
+        per_set = R * C * 4  # the footprint
         cpu = None
     elif key in ("c2v", "c2r"):
         R, C = (1, 64 << 20) if key == "c2v" else (16, 4 << 20)
@@ -345,7 +363,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c2h,c2u,c2c")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c2h,c2u,c2c,c2mv,c2mw")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
                     help="untimed launches per config before the warmup steps, in wall-clock ms")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
@@ -379,6 +397,8 @@ def main():
             entry["roofline"] = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                  "frac": gbs / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": source}
             entry["algorithmic_bytes"] = work["bytes"]
+            if "single_read_bytes" in work:  # the tile read once: the bound a fused single read would meet
+                entry["single_read_GBps"] = work["single_read_bytes"] / (ms * 1e-3) / 1e9
         else:
             tf = work["flops"] / (ms * 1e-3) / 1e12
             peak = MFMA_PEAK_TFLOPS[work["dtype"]]

@@ -212,8 +212,9 @@ def evaluate_grid(spec, x0, xt, col, row, scalars):
     the work type, xt [(B,) C, R] (read at (c, r)), g [C], r [R] or None.
     `map` stores y [(B,) R, C], `tmap` its transpose [(B,) C, R],
     `colreduce` folds over R (the reduce drops the last live axis of
-    As((B,) C, R)) into [(B,) C]. Returns ({output: array}, every float sum
-    exact)."""
+    As((B,) C, R)) into [(B,) C]; later statements read a colreduce result
+    at (batch, column). Returns ({output: array} without the locals, every
+    float sum exact)."""
     elem = spec.elem
     dt = np.float32 if elem == "f32" else np.uint32
     batch = getattr(spec, "batch", False)
@@ -231,6 +232,7 @@ def evaluate_grid(spec, x0, xt, col, row, scalars):
     scal = {n: (_f32(v) if elem == "f32" else np.uint32(v)) for n, v in scalars.items()}
     env.update(scal)
     outs, exact = {}, True
+    colres = {}  # colreduce results [Bn, C], read by later statements at their own column
     with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
         for st in spec.stmts:
             val = np.array(np.broadcast_to(np.asarray(_eval(st["expr"], env, elem), dt), (Bn, R, C)), dt)
@@ -243,12 +245,16 @@ def evaluate_grid(spec, x0, xt, col, row, scalars):
                 exact = exact and ok
                 if st["piped"] is not None:
                     penv = dict(scal)
+                    penv.update(colres)
                     penv["v"] = red
                     if col is not None:
                         penv["g"] = col.astype(dt)[None, :]
                     red = np.broadcast_to(np.asarray(_eval(st["piped"], penv, elem), dt), (Bn, C))
                 out = np.array(red, dt)
-            outs[st["out"]] = out if batch else out[0]
+                colres[st["out"]] = out
+                env[st["out"]] = out[:, None, :]
+            if not st.get("local"):
+                outs[st["out"]] = out if batch else out[0]
     return outs, exact
 
 
@@ -268,6 +274,8 @@ def evaluate_grid_scalar(spec, x0, xt, col, row, scalars):
              "max": (lambda a, b: np.fmax(a, b)) if elem == "f32" else (lambda a, b: max(a, b)),
              "min": (lambda a, b: np.fmin(a, b)) if elem == "f32" else (lambda a, b: min(a, b))}
 
+    colres = {}  # colreduce results [Bn, C]
+
     def env_at(bb, r, c):
         env = {"x0": cast(x0[bb, r, c])}
         if xt is not None:
@@ -277,6 +285,8 @@ def evaluate_grid_scalar(spec, x0, xt, col, row, scalars):
         if row is not None:
             env["r"] = cast(row[r])
         env.update(scal)
+        for name, res in colres.items():
+            env[name] = cast(res[bb, c])
         return env
 
     outs = {}
@@ -301,10 +311,14 @@ def evaluate_grid_scalar(spec, x0, xt, col, row, scalars):
                             acc = cast(combs[st["comb"]](acc, cast(_eval(st["expr"], env_at(bb, r, c), elem))))
                         if st["piped"] is not None:
                             penv = dict(scal)
+                            for name, res in colres.items():
+                                penv[name] = cast(res[bb, c])
                             penv["v"] = acc
                             if col is not None:
                                 penv["g"] = cast(col[c])
                             acc = cast(_eval(st["piped"], penv, elem))
                         out[bb, c] = acc
-            outs[st["out"]] = out if batch else out[0]
+                colres[st["out"]] = out
+            if not st.get("local"):
+                outs[st["out"]] = out if batch else out[0]
     return outs

@@ -95,15 +95,17 @@ class CompiledProgram:
         return _lib.lib().tca_program_check(self.parsed(), arr, len(tensors), fd, len(free_dims))
 
     def selected_symbols(self, tensors, free_dims=()):
-        """The kernels a launch with these tensors runs (launch guards
-        applied), in launch order."""
+        """The kernels a launch with these tensors runs, in launch order:
+        launch guards applied, and kernels whose grid is empty (no outputs,
+        or a split kernel the row-chunk count leaves out) dropped."""
         syms = self.kernel_symbols()
         arr = _descriptors(tensors)
         fd = (ctypes.c_uint32 * max(1, len(free_dims)))(*free_dims)
         out = (ctypes.c_uint8 * max(1, len(syms)))()
+        grids = (ctypes.c_uint64 * max(1, len(syms)))()
         _lib.check(_lib.lib().tca_program_selected(self.parsed(), arr, len(tensors), fd, len(free_dims), out,
-                                                   None, None, len(syms)))
-        return [s for s, f in zip(syms, out) if f]
+                                                   grids, None, len(syms)))
+        return [s for s, f, g in zip(syms, out, grids) if f and g]
 
     # -- GPU
     def load(self):

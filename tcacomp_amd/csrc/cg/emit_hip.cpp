@@ -491,13 +491,18 @@ RowGeom RowCheck(const Graph& g, const std::vector<int>& chains, uint32_t nv_tar
 // contiguous. One reduce per chain with an associative-commutative
 // combiner, stored at (outer..., c); operands are tiles, column vectors
 // ((outer...,) c: one value per output), row vectors ((outer...,) r) and
-// outer scalars; piped maps read column vectors and outer scalars. The
-// chains of a nest read none of each other's results (one pass).
+// outer scalars; piped maps read column vectors and outer scalars. A chain
+// may read the result of an earlier chain of the nest, as a column vector
+// only (the value at its own output): it then runs in a later pass, one
+// pass after the latest chain it reads. Chains read no result of their own
+// or of a later chain, and no two store one tensor.
 struct ColGeom {
   bool ok = false;
   std::string why;
   std::vector<int> as, outer;
   int c = -1, r = -1;
+  std::vector<int> pass;  // per chain of the nest, in nest order: 0, 1, ...
+  int passes = 1;
 };
 
 enum class ColKind { Tile, ColVec, RowVec, Outer, Bad };
@@ -529,26 +534,45 @@ ColGeom ColCheck(const Graph& g, const std::vector<int>& chains) {
   geo.r = geo.as.back();
   geo.c = geo.as[geo.as.size() - 2];
   geo.outer.assign(geo.as.begin(), geo.as.end() - 2);
-  std::set<int> stored;
-  for (int ci : chains) stored.insert(g.chains[ci].store_tensor);
+  std::map<int, size_t> stored;  // result tensor -> position of its chain in the nest
+  for (size_t i = 0; i < chains.size(); ++i)
+    if (!stored.emplace(g.chains[chains[i]].store_tensor, i).second) return no("two chains store one tensor");
   std::vector<int> out_axes(geo.outer);
   out_axes.push_back(geo.c);
-  for (int ci : chains) {
-    const ir::Chain& c = g.chains[ci];
+  geo.pass.assign(chains.size(), 0);
+  for (size_t i = 0; i < chains.size(); ++i) {
+    const ir::Chain& c = g.chains[chains[i]];
     if (c.root.as != geo.as) return no("iteration orders differ");
     if (c.reduces.size() != 1) return no("not exactly one reduction");
     if (!IsMonoidCombiner(g, c.reduces[0])) return no("combiner is not an associative-commutative op over (acc, now)");
     if (c.store_axes != out_axes) return no("store is not at (outer..., column)");
+    // A read of a result of the nest: the producer's pass + 1, or a refusal.
+    auto result = [&](const ir::Operand& o, ColKind k) -> bool {
+      const auto it = stored.find(o.tensor);
+      if (it == stored.end()) return true;
+      if (it->second >= i) {
+        geo.why = "a chain reads a result of itself or of a later chain of the nest";
+        return false;
+      }
+      if (k != ColKind::ColVec) {
+        geo.why = "a chain reads a result of the nest other than at its own column";
+        return false;
+      }
+      geo.pass[i] = std::max(geo.pass[i], geo.pass[it->second] + 1);
+      return true;
+    };
     for (const auto& o : c.root.ops) {
-      if (ClassifyCol(o, geo) == ColKind::Bad) return no("operand " + g.tensors[o.tensor].name + " is not column-shaped");
-      if (stored.count(o.tensor)) return no("a chain reads a result of the same nest");
+      const ColKind k = ClassifyCol(o, geo);
+      if (k == ColKind::Bad) return no("operand " + g.tensors[o.tensor].name + " is not column-shaped");
+      if (!result(o, k)) return no(geo.why);
     }
     if (c.has_piped)
       for (const auto& o : c.piped.ops) {
         const ColKind k = ClassifyCol(o, geo);
         if (k != ColKind::ColVec && k != ColKind::Outer) return no("piped operand is not per output");
-        if (stored.count(o.tensor)) return no("a chain reads a result of the same nest");
+        if (!result(o, k)) return no(geo.why);
       }
+    geo.passes = std::max(geo.passes, geo.pass[i] + 1);
   }
   geo.ok = true;
   return geo;
@@ -1960,6 +1984,15 @@ class Emitter {
   // per block, its 16 waves folding every 16th chunk) combines them. Loads
   // are unmasked: lanes past the last column read the row's last vector and
   // store nothing.
+  //
+  // A nest of several passes (a chain that reads the result of an earlier
+  // one, e.g. a variance reading its mean) has two lowerings, picked at
+  // launch by the same P: with P = 1 one whole-column kernel runs every pass
+  // in turn over all rows, the results a later pass reads handed from the
+  // finishing threads to the block through LDS (no HBM round trip; results
+  // that are locals read only inside the nest are not stored at all); with
+  // P > 1 each pass is its own partial + merge pair, and a later pass loads
+  // an earlier one's result from HBM like any column vector.
   bool EmitCol(int ni, std::string* err) {
     // Swept on MI355X (column sum+max, [8192, 8192] .. [16, 4 Mi]): spans of
     // 64 vectors beat 256 (4.7-5.7 against 4.3-4.8 TB/s); a 1024-block
@@ -2005,29 +2038,54 @@ class Emitter {
       partSig += ",\n    " + CType(pe) + "* __restrict__ p" + std::to_string(ci) + " /* " + nm + " */";
       partArgs += ", p" + std::to_string(ci);
     }
-    // Operands by kind (root and piped maps), each loaded once per kind.
-    std::vector<int> tiles, colvecs, rowvecs, outers;
-    auto note = [](std::vector<int>& v, int t) {
-      if (std::find(v.begin(), v.end(), t) == v.end()) v.push_back(t);
+    // The chains of each pass, and the results of the nest a later pass reads.
+    std::vector<std::vector<int>> passChains(geo.passes);
+    for (size_t i = 0; i < n.chains.size(); ++i) passChains[geo.pass[i]].push_back(n.chains[i]);
+    std::set<int> results, readLater;
+    for (int ci : n.chains) results.insert(g_.chains[ci].store_tensor);
+    // Operands by kind (root and piped maps) over a set of chains, each
+    // loaded once per kind.
+    struct Ops {
+      std::vector<int> tiles, colvecs, rowvecs, outers;
     };
     std::map<int, const ir::Operand*> opOf;
-    for (int ci : n.chains) {
-      const ir::Chain& c = g_.chains[ci];
-      std::vector<const ir::Operand*> ops;
-      for (const auto& op : c.root.ops) ops.push_back(&op);
-      if (c.has_piped)
-        for (const auto& op : c.piped.ops) ops.push_back(&op);
-      for (const ir::Operand* op : ops) {
-        opOf[op->tensor] = op;
-        switch (ClassifyCol(*op, geo)) {
-          case ColKind::Tile: note(tiles, op->tensor); break;
-          case ColKind::ColVec: note(colvecs, op->tensor); break;
-          case ColKind::RowVec: note(rowvecs, op->tensor); break;
-          default: note(outers, op->tensor); break;
+    auto opsOf = [&](const std::vector<int>& cs) {
+      Ops k;
+      auto note = [](std::vector<int>& v, int t) {
+        if (std::find(v.begin(), v.end(), t) == v.end()) v.push_back(t);
+      };
+      for (int ci : cs) {
+        const ir::Chain& c = g_.chains[ci];
+        std::vector<const ir::Operand*> ops;
+        for (const auto& op : c.root.ops) ops.push_back(&op);
+        if (c.has_piped)
+          for (const auto& op : c.piped.ops) ops.push_back(&op);
+        for (const ir::Operand* op : ops) {
+          opOf[op->tensor] = op;
+          switch (ClassifyCol(*op, geo)) {
+            case ColKind::Tile: note(k.tiles, op->tensor); break;
+            case ColKind::ColVec: note(k.colvecs, op->tensor); break;
+            case ColKind::RowVec: note(k.rowvecs, op->tensor); break;
+            default: note(k.outers, op->tensor); break;
+          }
         }
       }
-    }
+      return k;
+    };
+    const Ops all = opsOf(n.chains);
+    for (int t : all.colvecs)
+      if (results.count(t)) readLater.insert(t);
     auto kindOf = [&](int t) { return ClassifyCol(*opOf[t], geo); };
+    // A result the whole-column kernel need not store: a local no chain
+    // outside this nest reads.
+    auto internalLocal = [&](int t) {
+      if (!g_.tensors[t].local) return false;
+      for (size_t nj = 0; nj < an_.nests.size(); ++nj)
+        if (static_cast<int>(nj) != ni)
+          for (int cj : an_.nests[nj].chains)
+            if (ReadSet(g_.chains[cj]).count(t)) return false;
+      return true;
+    };
     // Coordinates: outer axes c<a>, the column `colv`, the row `rowv`.
     auto coordFn = [&](const std::string& colv, const std::string& rowv) {
       return [&, colv, rowv](int a) -> std::string {
@@ -2048,8 +2106,8 @@ class Emitter {
       }
       o << ind << "(void)orem;\n";
     };
-    auto combs = [&](const std::string& ind) {
-      for (int ci : n.chains) {
+    auto combs = [&](const std::string& ind, const std::vector<int>& cs) {
+      for (int ci : cs) {
         const ir::Chain& c = g_.chains[ci];
         const std::string T = CType(g_.exprs[c.root.fn.body].type);
         o << ind << "const auto comb" << ci << " = [](" << T << " acc, " << T << " now) -> " << T << " {\n";
@@ -2062,10 +2120,12 @@ class Emitter {
     };
     // init, the piped map and the store of chain ci's reduced value `acc`
     // (`present`: the value folded anything) at column `col`, with column
-    // vectors read by `colval`.
+    // vectors read by `colval`; `store` false skips the store, and a
+    // non-empty `bcast` also receives the stored value.
     auto finish = [&](std::ostringstream& b, const std::string& ind, int ci, const std::string& acc,
                       const std::string& present, const std::string& col,
-                      const std::function<std::string(int)>& colval) {
+                      const std::function<std::string(int)>& colval, bool store = true,
+                      const std::string& bcast = std::string()) {
       const ir::Chain& c = g_.chains[ci];
       const ir::ReduceStage& r = c.reduces[0];
       const std::string T = CType(g_.exprs[c.root.fn.body].type);
@@ -2093,60 +2153,25 @@ class Emitter {
         val = pg.Gen(c.piped.fn.body);
       }
       const int st = c.store_tensor;
-      b << ind << "t" << st << "[" << Offset(st, c.store_axes, coordFn(col, "0u")) << "] = " << val << ";\n";
+      if (store) b << ind << "t" << st << "[" << Offset(st, c.store_axes, coordFn(col, "0u")) << "] = " << val << ";\n";
+      if (!bcast.empty()) b << ind << bcast << " = " << val << ";\n";
     };
-
-    o << "// statements";
-    for (int ci : n.chains) o << " #" << ci;
-    o << ": column family; reduce over @" << g_.dims[geo.r].name << " (not contiguous) per column of @"
-      << g_.dims[geo.c].name << "\n";
-    // ---- partial folds
-    o << "template <uint32_t V>\n__device__ __forceinline__ void " << sym << "_part(\n    " << sig << partSig
-      << ") {\n";
-    o << "  constexpr uint32_t W = " << kWaves << "u, RMIN = " << kRowsMin << "u, BLOCKS = " << kBlocks
-      << "u, SPAN = " << kSpan << "u, LSPAN = " << kLogSpan << "u;  // SPAN column vectors per block\n";
-    o << "  const uint32_t C = " << ExtentExpr(g_, geo.c) << ", R = " << ExtentExpr(g_, geo.r) << ";\n";
-    o << "  const uint32_t NOUT = " << ProductExpr(geo.outer) << ";\n";
-    o << "  const uint32_t VEC = C / V, CB = tca::hip::ceil_div(VEC, SPAN), NCB = NOUT * CB;\n";
-    o << "  const uint32_t P = tca::hip::col_split(R, NCB, RMIN, BLOCKS);\n";
-    o << "  const uint32_t p = blockIdx.x / NCB, cbk = blockIdx.x - p * NCB;\n";
-    o << "  const uint32_t ob = cbk / CB, cb = cbk - ob * CB;\n";
-    o << "  uint32_t LSL = 0u;  // SL = 2^LSL lanes per row, the smallest power of two >= VEC, at most SPAN\n";
-    o << "  while (LSL < LSPAN && (1u << LSL) < VEC) ++LSL;\n";
-    o << "  const uint32_t SL = 1u << LSL, STEP = (W * 64u) >> LSL;  // STEP rows per block step\n";
-    o << "  const uint32_t cg = threadIdx.x & (SL - 1u), slot = threadIdx.x >> LSL;\n";
-    o << "  const uint32_t cvec = cb * SPAN + cg;\n";
-    o << "  const uint32_t col0 = (cvec < VEC ? cvec : VEC - 1u) * V;  // clamped: loads stay in the row\n";
-    o << "  const uint32_t r_lo = static_cast<uint32_t>(static_cast<uint64_t>(p) * R / P);\n";
-    o << "  const uint32_t r_hi = static_cast<uint32_t>(static_cast<uint64_t>(p + 1u) * R / P);\n";
-    outerCoords("  ", "ob");
-    combs("  ");
-    const auto at0 = coordFn("col0", "0u");
-    for (int t : colvecs)
-      o << "  const auto cv" << t << " = tca::hip::load_vec<" << CType(g_.tensors[t].elem) << ", V>(t" << t << " + "
-        << Offset(t, opOf[t]->axes, at0) << ");\n";
-    for (int t : outers)
-      o << "  const " << CType(g_.tensors[t].elem) << " os" << t << " = t" << t << "[" << Offset(t, opOf[t]->axes, at0)
-        << "];\n";
-    for (int ci : n.chains) {
-      const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
-      o << "  " << T << " part" << ci << "[V];\n";
-      o << "#pragma unroll\n  for (uint32_t q = 0; q < V; ++q) part" << ci << "[q] = " << T << "(0);\n";
-    }
-    // Loads of row `rv` into x<t><sfx> / rv<t><sfx>, then the fold.
-    auto loads = [&](std::ostringstream& b, const std::string& ind, const std::string& rv, const std::string& sfx) {
+    // Loads of row `rv` into x<t><sfx> / rv<t><sfx>, then the fold of the
+    // chains `cs` into part<ci>.
+    auto loads = [&](std::ostringstream& b, const Ops& k, const std::string& ind, const std::string& rv,
+                     const std::string& sfx) {
       const auto at = coordFn("col0", rv);
-      for (int t : tiles)
+      for (int t : k.tiles)
         b << ind << "const auto x" << t << sfx << " = tca::hip::load_vec_nt<" << CType(g_.tensors[t].elem) << ", V>(t"
           << t << " + " << Offset(t, opOf[t]->axes, at) << ");\n";
-      for (int t : rowvecs)
+      for (int t : k.rowvecs)
         b << ind << "const " << CType(g_.tensors[t].elem) << " rv" << t << sfx << " = t" << t << "["
           << Offset(t, opOf[t]->axes, at) << "];\n";
     };
-    auto fold = [&](std::ostringstream& b, const std::string& ind, const std::string& sfx, bool first,
-                    const std::string& ok) {
+    auto fold = [&](std::ostringstream& b, const std::vector<int>& cs, const std::string& ind, const std::string& sfx,
+                    bool first, const std::string& ok) {
       b << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) {\n";
-      for (int ci : n.chains) {
+      for (int ci : cs) {
         const ir::Chain& c = g_.chains[ci];
         ExprGen eg(g_, b, ind + "  ", &counter_);
         for (size_t k = 0; k < c.root.ops.size(); ++k) {
@@ -2167,17 +2192,18 @@ class Emitter {
         else b << ind << "  " << P << " = " << ok << " ? comb" << ci << "(" << P << ", " << ev << ") : " << P << ";\n";
       }
       b << ind << "}\n";
-      for (int ci : n.chains)
+      for (int ci : cs)
         if (FoldFenced(g_.exprs[g_.chains[ci].root.fn.body].type))
           b << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) tca::hip::fold_fence(part" << ci
             << "[q]);\n";
     };
-    {
-      // Rows in groups (loads in flight together): a first group of kEdge
-      // rows, groups of kUnroll rows while whole ones fit, then groups of
-      // kEdge to the chunk's end. The edge groups clamp rows past the chunk
-      // to its last row (unconditional loads stay in flight together) and
-      // fold only the rows they own; row 0 of each is always owned.
+    // The row loop of a block over [r_lo, r_hi) for the chains `cs`: a
+    // first group of kEdge rows, groups of kUnroll rows while whole ones
+    // fit, then groups of kEdge to the chunk's end. The edge groups clamp
+    // rows past the chunk to its last row (unconditional loads stay in
+    // flight together) and fold only the rows they own; row 0 of each is
+    // always owned. Declares `has` (the thread's slot holds a row).
+    auto rowLoop = [&](const std::vector<int>& cs, const Ops& k, const std::string& hasName) {
       std::ostringstream b;
       auto group = [&](const std::string& ind, uint32_t rows, bool clamped, bool first) {
         for (uint32_t u = 0; u < rows; ++u) {
@@ -2185,15 +2211,16 @@ class Emitter {
           if (clamped && u > 0) {
             b << ind << "const bool ok_" << us << " = r + " << us << "u * STEP < r_hi;\n";
             b << ind << "const uint32_t rr_" << us << " = ok_" << us << " ? r + " << us << "u * STEP : r_hi - 1u;\n";
-            loads(b, ind, "rr_" + us, "_" + us);
+            loads(b, k, ind, "rr_" + us, "_" + us);
           } else {
-            loads(b, ind, "r + " + us + "u * STEP", "_" + us);
+            loads(b, k, ind, "r + " + us + "u * STEP", "_" + us);
           }
         }
         for (uint32_t u = 0; u < rows; ++u)
-          fold(b, ind, "_" + std::to_string(u), first && u == 0, clamped && u > 0 ? "ok_" + std::to_string(u) : "");
+          fold(b, cs, ind, "_" + std::to_string(u), first && u == 0, clamped && u > 0 ? "ok_" + std::to_string(u) : "");
       };
-      b << "  uint32_t r = r_lo + slot;\n  const bool has = r < r_hi;\n  if (has) {\n    {\n";
+      b << "  uint32_t r = r_lo + slot;\n  const bool " << hasName << " = r < r_hi;\n  if (" << hasName
+        << ") {\n    {\n";
       group("      ", kEdge, true, true);
       b << "    }\n    r += " << kEdge << "u * STEP;\n";
       b << "    for (; r + " << kUnroll - 1 << "u * STEP < r_hi; r += " << kUnroll << "u * STEP) {\n";
@@ -2201,88 +2228,141 @@ class Emitter {
       b << "    }\n    for (; r < r_hi; r += " << kEdge << "u * STEP) {\n";
       group("      ", kEdge, true, false);
       b << "    }\n  }\n";
-      o << b.str();
-    }
-    // Row slots meet in LDS: slot s holds rows r_lo + s + k STEP.
-    for (int ci : n.chains) {
-      const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
-      o << "  __shared__ " << T << " red" << ci << "[W * 64u * V];\n";
-      o << "  if (has) {\n#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) red" << ci
-        << "[slot * (SL * V) + cg * V + q] = part" << ci << "[q];\n  }\n";
-    }
-    o << "  __syncthreads();\n";
-    o << "  const uint32_t nrow = r_hi - r_lo, nslot = nrow < STEP ? nrow : STEP;  // slots holding rows\n";
-    o << "  if (slot == 0u && cvec < VEC) {  // the threads of slot 0 (threadIdx.x < SL) finish\n";
-    o << "#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) {\n";
-    o << "      const uint32_t cq = cvec * V + q;  // this thread's output column (col0 + q)\n";
-    o << "      (void)cq;\n";
-    for (int ci : n.chains) {
-      const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
-      o << "      " << T << " acc" << ci << " = red" << ci << "[cg * V + q];\n";
-      o << "      for (uint32_t s2 = 1u; s2 < nslot; ++s2) acc" << ci << " = comb" << ci << "(acc" << ci << ", red" << ci
-        << "[s2 * (SL * V) + cg * V + q]);\n";
-    }
-    o << "      if (P == 1u) {\n";
-    {
+      return b.str();
+    };
+    auto partDecls = [&](const std::vector<int>& cs) {
+      for (int ci : cs) {
+        const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+        o << "  " << T << " part" << ci << "[V];\n";
+        o << "#pragma unroll\n  for (uint32_t q = 0; q < V; ++q) part" << ci << "[q] = " << T << "(0);\n";
+      }
+    };
+    // Block geometry shared by the partial and whole-column kernels.
+    auto blockGeom = [&]() {
+      o << "  uint32_t LSL = 0u;  // SL = 2^LSL lanes per row, the smallest power of two >= VEC, at most SPAN\n";
+      o << "  while (LSL < LSPAN && (1u << LSL) < VEC) ++LSL;\n";
+      o << "  const uint32_t SL = 1u << LSL, STEP = (W * 64u) >> LSL;  // STEP rows per block step\n";
+      o << "  const uint32_t cg = threadIdx.x & (SL - 1u), slot = threadIdx.x >> LSL;\n";
+      o << "  const uint32_t cvec = cb * SPAN + cg;\n";
+      o << "  const uint32_t col0 = (cvec < VEC ? cvec : VEC - 1u) * V;  // clamped: loads stay in the row\n";
+    };
+    const auto at0 = coordFn("col0", "0u");
+    auto colvecLoads = [&](const Ops& k, bool skipResults) {
+      for (int t : k.colvecs) {
+        if (skipResults && results.count(t)) continue;
+        o << "  const auto cv" << t << " = tca::hip::load_vec<" << CType(g_.tensors[t].elem) << ", V>(t" << t << " + "
+          << Offset(t, opOf[t]->axes, at0) << ");\n";
+      }
+      for (int t : k.outers)
+        o << "  const " << CType(g_.tensors[t].elem) << " os" << t << " = t" << t << "["
+          << Offset(t, opOf[t]->axes, at0) << "];\n";
+    };
+
+    // ---- partial folds of the chains `cs` (a whole nest of one pass, or
+    // one pass of several)
+    auto emitPart = [&](const std::string& name, const std::vector<int>& cs) {
+      const Ops k = opsOf(cs);
+      o << "template <uint32_t V>\n__device__ __forceinline__ void " << name << "(\n    " << sig << partSig << ") {\n";
+      o << "  constexpr uint32_t W = " << kWaves << "u, RMIN = " << kRowsMin << "u, BLOCKS = " << kBlocks
+        << "u, SPAN = " << kSpan << "u, LSPAN = " << kLogSpan << "u;  // SPAN column vectors per block\n";
+      o << "  const uint32_t C = " << ExtentExpr(g_, geo.c) << ", R = " << ExtentExpr(g_, geo.r) << ";\n";
+      o << "  const uint32_t NOUT = " << ProductExpr(geo.outer) << ";\n";
+      o << "  const uint32_t VEC = C / V, CB = tca::hip::ceil_div(VEC, SPAN), NCB = NOUT * CB;\n";
+      o << "  const uint32_t P = tca::hip::col_split(R, NCB, RMIN, BLOCKS);\n";
+      o << "  const uint32_t p = blockIdx.x / NCB, cbk = blockIdx.x - p * NCB;\n";
+      o << "  const uint32_t ob = cbk / CB, cb = cbk - ob * CB;\n";
+      blockGeom();
+      o << "  const uint32_t r_lo = static_cast<uint32_t>(static_cast<uint64_t>(p) * R / P);\n";
+      o << "  const uint32_t r_hi = static_cast<uint32_t>(static_cast<uint64_t>(p + 1u) * R / P);\n";
+      outerCoords("  ", "ob");
+      combs("  ", cs);
+      colvecLoads(k, false);
+      partDecls(cs);
+      o << rowLoop(cs, k, "has");
+      // Row slots meet in LDS: slot s holds rows r_lo + s + k STEP.
+      for (int ci : cs) {
+        const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+        o << "  __shared__ " << T << " red" << ci << "[W * 64u * V];\n";
+        o << "  if (has) {\n#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) red" << ci
+          << "[slot * (SL * V) + cg * V + q] = part" << ci << "[q];\n  }\n";
+      }
+      o << "  __syncthreads();\n";
+      o << "  const uint32_t nrow = r_hi - r_lo, nslot = nrow < STEP ? nrow : STEP;  // slots holding rows\n";
+      o << "  if (slot == 0u && cvec < VEC) {  // the threads of slot 0 (threadIdx.x < SL) finish\n";
+      o << "#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) {\n";
+      o << "      const uint32_t cq = cvec * V + q;  // this thread's output column (col0 + q)\n";
+      o << "      (void)cq;\n";
+      for (int ci : cs) {
+        const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+        o << "      " << T << " acc" << ci << " = red" << ci << "[cg * V + q];\n";
+        o << "      for (uint32_t s2 = 1u; s2 < nslot; ++s2) acc" << ci << " = comb" << ci << "(acc" << ci << ", red"
+          << ci << "[s2 * (SL * V) + cg * V + q]);\n";
+      }
+      o << "      if (P == 1u) {\n";
+      {
+        std::ostringstream b;
+        for (int ci : cs)
+          finish(b, "        ", ci, "acc" + std::to_string(ci), "nslot > 0u", "cq",
+                 [&](int t) { return "cv" + std::to_string(t) + "[q]"; });
+        o << b.str();
+      }
+      o << "      } else {\n";
+      for (int ci : cs)
+        o << "        p" << ci << "[(static_cast<uint64_t>(p) * NCB + cbk) * (SPAN * V) + cg * V + q] = acc" << ci
+          << ";\n";
+      o << "      }\n    }\n  }\n}\n";
+    };
+    // ---- merge of the P chunks of the chains `cs`: a block takes 64
+    // consecutive outputs, its 16 waves fold chunks w, w + 16, ... (4 loads
+    // in flight, 64 outputs per load: one 256-byte segment), and the waves
+    // meet in LDS.
+    auto emitMerge = [&](const std::string& name, const std::vector<int>& cs) {
+      const Ops k = opsOf(cs);
+      o << "template <uint32_t V>\n__device__ __forceinline__ void " << name << "(\n    " << sig << partSig << ") {\n";
+      o << "  constexpr uint32_t RMIN = " << kRowsMin << "u, BLOCKS = " << kBlocks << "u, MW = " << kMergeWaves
+        << "u, SPAN = " << kSpan << "u;\n";
+      o << "  const uint32_t C = " << ExtentExpr(g_, geo.c) << ", R = " << ExtentExpr(g_, geo.r) << ";\n";
+      o << "  const uint32_t NOUT = " << ProductExpr(geo.outer) << ";\n";
+      o << "  const uint32_t VEC = C / V, CB = tca::hip::ceil_div(VEC, SPAN), NCB = NOUT * CB;\n";
+      o << "  const uint32_t P = tca::hip::col_split(R, NCB, RMIN, BLOCKS);  // > 1: launched only then\n";
+      o << "  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;\n";
+      o << "  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 64u + lane;\n";
+      o << "  const bool active = i < static_cast<uint64_t>(NOUT) * C;\n";
+      o << "  const uint64_t ic = active ? i : 0u;  // lanes past the end read output 0 and store nothing\n";
+      o << "  const uint32_t ob = static_cast<uint32_t>(ic / C), cq = static_cast<uint32_t>(ic - static_cast<uint64_t>(ob) * C);\n";
+      o << "  const uint32_t cb = cq / (SPAN * V), within = cq - cb * (SPAN * V), cbk = ob * CB + cb;\n";
+      o << "  const uint64_t stride = static_cast<uint64_t>(NCB) * (SPAN * V);\n";
+      o << "  const uint64_t base = static_cast<uint64_t>(cbk) * (SPAN * V) + within;\n";
+      outerCoords("  ", "ob");
+      combs("  ", cs);
+      const auto atq = coordFn("cq", "0u");
+      for (int t : k.outers)
+        o << "  const " << CType(g_.tensors[t].elem) << " os" << t << " = t" << t << "["
+          << Offset(t, opOf[t]->axes, atq) << "];\n";
+      for (int ci : cs) {
+        const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+        const std::string A = "acc" + std::to_string(ci), pp = "p" + std::to_string(ci);
+        o << "  " << T << " " << A << " = " << T << "(0);\n";
+        o << "  if (w < P) {\n";
+        o << "    " << A << " = " << pp << "[static_cast<uint64_t>(w) * stride + base];\n";
+        o << "    uint32_t k = w + MW;\n";
+        o << "    for (; k + 3u * MW < P; k += 4u * MW) {\n";
+        for (int u = 0; u < 4; ++u)
+          o << "      const " << T << " m" << u << " = " << pp << "[static_cast<uint64_t>(k + " << u
+            << "u * MW) * stride + base];\n";
+        for (int u = 0; u < 4; ++u) o << "      " << A << " = comb" << ci << "(" << A << ", m" << u << ");\n";
+        o << "    }\n";
+        o << "    for (; k < P; k += MW) " << A << " = comb" << ci << "(" << A << ", " << pp
+          << "[static_cast<uint64_t>(k) * stride + base]);\n";
+        o << "  }\n";
+        o << "  __shared__ " << T << " mred" << ci << "[MW * 64u];\n";
+        o << "  if (w < P) mred" << ci << "[w * 64u + lane] = " << A << ";\n";
+      }
+      o << "  __syncthreads();\n";
+      o << "  if (w != 0u || !active) return;\n";
+      o << "  const uint32_t nw = P < MW ? P : MW;  // waves holding chunks (every one of them holds >= 1)\n";
       std::ostringstream b;
-      for (int ci : n.chains)
-        finish(b, "        ", ci, "acc" + std::to_string(ci), "nslot > 0u", "cq",
-               [&](int t) { return "cv" + std::to_string(t) + "[q]"; });
-      o << b.str();
-    }
-    o << "      } else {\n";
-    for (int ci : n.chains)
-      o << "        p" << ci << "[(static_cast<uint64_t>(p) * NCB + cbk) * (SPAN * V) + cg * V + q] = acc" << ci << ";\n";
-    o << "      }\n    }\n  }\n}\n";
-    // ---- merge of the P chunks: a block takes 64 consecutive outputs, its
-    // 16 waves fold chunks w, w + 16, ... (4 loads in flight, 64 outputs
-    // per load: one 256-byte segment), and the waves meet in LDS.
-    o << "template <uint32_t V>\n__device__ __forceinline__ void " << sym << "_merge(\n    " << sig << partSig
-      << ") {\n";
-    o << "  constexpr uint32_t RMIN = " << kRowsMin << "u, BLOCKS = " << kBlocks << "u, MW = " << kMergeWaves
-      << "u, SPAN = " << kSpan << "u;\n";
-    o << "  const uint32_t C = " << ExtentExpr(g_, geo.c) << ", R = " << ExtentExpr(g_, geo.r) << ";\n";
-    o << "  const uint32_t NOUT = " << ProductExpr(geo.outer) << ";\n";
-    o << "  const uint32_t VEC = C / V, CB = tca::hip::ceil_div(VEC, SPAN), NCB = NOUT * CB;\n";
-    o << "  const uint32_t P = tca::hip::col_split(R, NCB, RMIN, BLOCKS);  // > 1: launched only then\n";
-    o << "  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;\n";
-    o << "  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 64u + lane;\n";
-    o << "  const bool active = i < static_cast<uint64_t>(NOUT) * C;\n";
-    o << "  const uint64_t ic = active ? i : 0u;  // lanes past the end read output 0 and store nothing\n";
-    o << "  const uint32_t ob = static_cast<uint32_t>(ic / C), cq = static_cast<uint32_t>(ic - static_cast<uint64_t>(ob) * C);\n";
-    o << "  const uint32_t cb = cq / (SPAN * V), within = cq - cb * (SPAN * V), cbk = ob * CB + cb;\n";
-    o << "  const uint64_t stride = static_cast<uint64_t>(NCB) * (SPAN * V);\n";
-    o << "  const uint64_t base = static_cast<uint64_t>(cbk) * (SPAN * V) + within;\n";
-    outerCoords("  ", "ob");
-    combs("  ");
-    const auto atq = coordFn("cq", "0u");
-    for (int t : outers)
-      o << "  const " << CType(g_.tensors[t].elem) << " os" << t << " = t" << t << "[" << Offset(t, opOf[t]->axes, atq)
-        << "];\n";
-    for (int ci : n.chains) {
-      const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
-      const std::string A = "acc" + std::to_string(ci), pp = "p" + std::to_string(ci);
-      o << "  " << T << " " << A << " = " << T << "(0);\n";
-      o << "  if (w < P) {\n";
-      o << "    " << A << " = " << pp << "[static_cast<uint64_t>(w) * stride + base];\n";
-      o << "    uint32_t k = w + MW;\n";
-      o << "    for (; k + 3u * MW < P; k += 4u * MW) {\n";
-      for (int u = 0; u < 4; ++u)
-        o << "      const " << T << " m" << u << " = " << pp << "[static_cast<uint64_t>(k + " << u << "u * MW) * stride + base];\n";
-      for (int u = 0; u < 4; ++u) o << "      " << A << " = comb" << ci << "(" << A << ", m" << u << ");\n";
-      o << "    }\n";
-      o << "    for (; k < P; k += MW) " << A << " = comb" << ci << "(" << A << ", " << pp
-        << "[static_cast<uint64_t>(k) * stride + base]);\n";
-      o << "  }\n";
-      o << "  __shared__ " << T << " mred" << ci << "[MW * 64u];\n";
-      o << "  if (w < P) mred" << ci << "[w * 64u + lane] = " << A << ";\n";
-    }
-    o << "  __syncthreads();\n";
-    o << "  if (w != 0u || !active) return;\n";
-    o << "  const uint32_t nw = P < MW ? P : MW;  // waves holding chunks (every one of them holds >= 1)\n";
-    {
-      std::ostringstream b;
-      for (int ci : n.chains) {
+      for (int ci : cs) {
         const std::string A = "acc" + std::to_string(ci);
         b << "  for (uint32_t s2 = 1u; s2 < nw; ++s2) " << A << " = comb" << ci << "(" << A << ", mred" << ci
           << "[s2 * 64u + lane]);\n";
@@ -2291,9 +2371,106 @@ class Emitter {
         });
       }
       o << b.str();
+      o << "}\n";
+    };
+    // ---- every pass of a nest in one block over all rows (P = 1)
+    auto emitWhole = [&](const std::string& name) {
+      o << "template <uint32_t V>\n__device__ __forceinline__ void " << name << "(\n    " << sig << partSig << ") {\n";
+      o << "  constexpr uint32_t W = " << kWaves << "u, SPAN = " << kSpan << "u, LSPAN = " << kLogSpan
+        << "u;  // SPAN column vectors per block\n";
+      o << "  const uint32_t C = " << ExtentExpr(g_, geo.c) << ", R = " << ExtentExpr(g_, geo.r) << ";\n";
+      o << "  const uint32_t VEC = C / V, CB = tca::hip::ceil_div(VEC, SPAN);\n";
+      o << "  const uint32_t cbk = blockIdx.x;  // 64 column vectors of one outer index, every row\n";
+      o << "  const uint32_t ob = cbk / CB, cb = cbk - ob * CB;\n";
+      blockGeom();
+      o << "  const uint32_t r_lo = 0u, r_hi = R;\n";
+      o << "  const uint32_t nslot = R < STEP ? R : STEP;  // slots holding rows\n";
+      outerCoords("  ", "ob");
+      combs("  ", n.chains);
+      colvecLoads(all, true);
+      // Results a later pass reads: the finishing threads hand each to the
+      // block through LDS, converted to the result's element type as a
+      // store and load would.
+      for (int t : readLater) {
+        const std::string E = CType(g_.tensors[t].elem);
+        o << "  __shared__ " << E << " bc" << t << "[64u * V];\n";
+        o << "  " << E << " cv" << t << "[V];\n";
+      }
+      // The row slots of each pass meet in one LDS area, reused by the next
+      // pass after a barrier.
+      size_t area = 0;
+      std::vector<std::map<int, size_t>> at(geo.passes);
+      for (int ps = 0; ps < geo.passes; ++ps) {
+        size_t off = 0;
+        for (int ci : passChains[ps]) {
+          at[ps][ci] = off;
+          off += (ir::ElemBytes(g_.exprs[g_.chains[ci].root.fn.body].type) * kWaves * 64 * vmax + 15) / 16 * 16;
+        }
+        area = std::max(area, off);
+      }
+      o << "  __shared__ __attribute__((aligned(16))) unsigned char lds[" << area << "];\n";
+      o << "  (void)lds;\n";
+      for (int ps = 0; ps < geo.passes; ++ps) {
+        const std::vector<int>& cs = passChains[ps];
+        const Ops k = opsOf(cs);
+        o << "  {  // pass " << ps + 1 << " of " << geo.passes << ": statements";
+        for (int ci : cs) o << " #" << ci;
+        o << "\n";
+        partDecls(cs);
+        o << rowLoop(cs, k, "has");
+        for (int ci : cs) {
+          const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+          o << "  " << T << "* red" << ci << " = reinterpret_cast<" << T << "*>(lds + " << at[ps][ci] << "u);\n";
+          o << "  if (has) {\n#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) red" << ci
+            << "[slot * (SL * V) + cg * V + q] = part" << ci << "[q];\n  }\n";
+        }
+        o << "  __syncthreads();\n";
+        o << "  if (slot == 0u && cvec < VEC) {  // the threads of slot 0 (threadIdx.x < SL) finish\n";
+        o << "#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) {\n";
+        o << "      const uint32_t cq = cvec * V + q;  // this thread's output column (col0 + q)\n";
+        o << "      (void)cq;\n";
+        std::ostringstream b;
+        for (int ci : cs) {
+          const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+          b << "      " << T << " acc" << ci << " = red" << ci << "[cg * V + q];\n";
+          b << "      for (uint32_t s2 = 1u; s2 < nslot; ++s2) acc" << ci << " = comb" << ci << "(acc" << ci << ", red"
+            << ci << "[s2 * (SL * V) + cg * V + q]);\n";
+          const int st = g_.chains[ci].store_tensor;
+          finish(b, "      ", ci, "acc" + std::to_string(ci), "nslot > 0u", "cq",
+                 [&](int t) { return "cv" + std::to_string(t) + "[q]"; }, !internalLocal(st),
+                 readLater.count(st) ? "bc" + std::to_string(st) + "[cg * V + q]" : std::string());
+        }
+        o << b.str();
+        o << "    }\n  }\n";
+        if (ps + 1 < geo.passes)
+          o << "  __syncthreads();  // the partials are read and the handed results written\n";
+        for (int ci : cs) {
+          const int st = g_.chains[ci].store_tensor;
+          if (readLater.count(st))
+            o << "#pragma unroll\n  for (uint32_t q = 0; q < V; ++q) cv" << st << "[q] = bc" << st << "[cg * V + q];\n";
+        }
+        o << "  }\n";
+      }
+      o << "}\n";
+    };
+
+    o << "// statements";
+    for (int ci : n.chains) o << " #" << ci;
+    o << ": column family; reduce over @" << g_.dims[geo.r].name << " (not contiguous) per column of @"
+      << g_.dims[geo.c].name;
+    if (geo.passes > 1) o << " in " << geo.passes << " passes";
+    o << "\n";
+    if (geo.passes == 1) {
+      emitPart(sym + "_part", n.chains);
+      emitMerge(sym + "_merge", n.chains);
+    } else {
+      emitWhole(sym + "_whole");
+      for (int ps = 0; ps < geo.passes; ++ps) {
+        emitPart(sym + "_part" + std::to_string(ps + 1), passChains[ps]);
+        emitMerge(sym + "_merge" + std::to_string(ps + 1), passChains[ps]);
+      }
     }
-    o << "}\n";
-    // ---- one (partial, merge) pair per vector width
+    // ---- the kernels of each vector width
     const std::string args = CallArgs(n);
     const std::string cdim = g_.dims[geo.c].name, rdim = g_.dims[geo.r].name;
     struct Width {
@@ -2312,36 +2489,64 @@ class Emitter {
       }
     }
     const std::string outerTerm = DimProduct(geo.outer) + "/1";
+    const std::string outTerm = DimProduct([&] {
+      std::vector<int> a(geo.outer);
+      a.push_back(geo.c);
+      return a;
+    }()) + "/64";
     for (const auto& wd : widths) {
       const std::string cbTerm = cdim + "/" + std::to_string(kSpan * wd.v);
       const std::string splitRec = rdim + " " + std::to_string(kRowsMin) + " " + std::to_string(kBlocks);
-      for (int merge = 0; merge <= 1; ++merge) {
+      // (symbol suffix, device function, split mode, merge-shaped, chains, what it does)
+      struct K {
+        std::string suffix, fn;
+        int mode;
+        bool merge;
+        std::vector<int> chains;
+        std::string what;
+      };
+      std::vector<K> ks;
+      const std::string v = std::to_string(wd.v);
+      if (geo.passes == 1) {
+        ks.push_back({"_p" + v, "_part", 0, false, n.chains,
+                      " partial: 64 column vectors x a chunk of rows per block, P = col_split"});
+        ks.push_back({"_m" + v, "_merge", 1, true, n.chains,
+                      " merge: 64 outputs per block, 16 waves over the P chunks (P > 1 only)"});
+      } else {
+        ks.push_back({"_w" + v, "_whole", 2, false, n.chains,
+                      " whole: every pass over all rows of 64 column vectors per block, results handed on in LDS "
+                      "(P == 1 only)"});
+        for (int ps = 0; ps < geo.passes; ++ps) {
+          const std::string pn = std::to_string(ps + 1);
+          ks.push_back({"_p" + v + "_" + pn, "_part" + pn, 3, false, passChains[ps],
+                        " pass " + pn + " partial: 64 column vectors x a chunk of rows per block (P > 1 only)"});
+          ks.push_back({"_m" + v + "_" + pn, "_merge" + pn, 1, true, passChains[ps],
+                        " pass " + pn + " merge: 64 outputs per block, 16 waves over the P chunks (P > 1 only)"});
+        }
+      }
+      for (const auto& kd : ks) {
         PlanKernel k = pk;
-        k.symbol = sym + (merge ? "_m" : "_p") + std::to_string(wd.v);
-        k.block = merge ? 64 * kMergeWaves : 256;
+        k.symbol = sym + kd.suffix;
+        k.block = kd.merge ? 64 * kMergeWaves : 256;
         for (const auto& nm : partNames) k.args.push_back("ptr " + nm);
-        if (merge) k.grid.push_back(DimProduct([&] {
-          std::vector<int> a(geo.outer);
-          a.push_back(geo.c);
-          return a;
-        }()) + "/64");
-        else {
+        if (kd.merge) {
+          k.grid.push_back(outTerm);
+        } else {
           k.grid.push_back(outerTerm);
           k.grid.push_back(cbTerm);
         }
-        k.split = splitRec + " " + std::to_string(merge) + " 2 " + outerTerm + " " + cbTerm;
+        k.split = splitRec + " " + std::to_string(kd.mode) + " 2 " + outerTerm + " " + cbTerm;
         if (g_.dims[geo.c].extent == 0)
           k.when.push_back(cdim + " 0 4294967295 " + std::to_string(wd.mod) + " " + std::to_string(wd.rem));
-        o << "extern \"C\" __global__ void __launch_bounds__(" << k.block << ") " << k.symbol << "(\n    " << sig << partSig
-          << ") {\n  " << sym << (merge ? "_merge" : "_part") << "<" << wd.v << "u>(" << args << partArgs << ");\n}\n";
+        o << "extern \"C\" __global__ void __launch_bounds__(" << k.block << ") " << k.symbol << "(\n    " << sig
+          << partSig << ") {\n  " << sym << kd.fn << "<" << wd.v << "u>(" << args << partArgs << ");\n}\n";
         std::ostringstream det;
         det << "reduce @" << rdim << " per column of @" << cdim << " vec=" << wd.v
             << (g_.dims[geo.c].extent == 0 ? " (" + cdim + " % " + std::to_string(wd.mod) + " == " +
                                                   std::to_string(wd.rem) + ")"
                                             : std::string())
-            << (merge ? " merge: 64 outputs per block, 16 waves over the P chunks (P > 1 only)"
-                      : " partial: 64 column vectors x a chunk of rows per block, P = col_split");
-        AddKernel(k, Family::Col, n.chains, det.str());
+            << kd.what;
+        AddKernel(k, Family::Col, kd.chains, det.str());
       }
     }
     o << "\n";

@@ -230,11 +230,12 @@ bool Parse(const std::string& text, Plan* out, std::string* err) {
       uint64_t merge = 0, nt = 0;
       if (tok.size() < 6 || !ParseU64(tok[2], &k.split_rows_min) || !ParseU64(tok[3], &k.split_blocks) ||
           !ParseU64(tok[4], &merge) || !ParseU64(tok[5], &nt) || tok.size() != 6 + nt)
-        return bad("split <dim> <rows-min> <blocks> <merge> <n-terms> <term>...");
+        return bad("split <dim> <rows-min> <blocks> <mode> <n-terms> <term>...");
       k.split_dim = FindDim(p, tok[1]);
       if (k.split_dim < 0) return bad("split names unknown dim " + tok[1]);
-      if (k.split_rows_min == 0 || k.split_blocks == 0 || merge > 1) return bad("bad split on " + tok[1]);
-      k.split_merge = merge == 1;
+      if (k.split_rows_min == 0 || k.split_blocks == 0 || merge > kSplitPartialMany)
+        return bad("bad split on " + tok[1]);
+      k.split_mode = static_cast<int>(merge);
       for (uint64_t i = 0; i < nt; ++i) {
         Term t;
         std::string e;
@@ -338,7 +339,7 @@ std::string Serialize(const Plan& p) {
       o << "pack " << p.dims[k.pack_dim].name << " " << k.pack_epl << " " << k.pack_min_block << "\n";
     if (k.split_dim >= 0) {
       o << "split " << p.dims[k.split_dim].name << " " << k.split_rows_min << " " << k.split_blocks << " "
-        << (k.split_merge ? 1 : 0) << " " << k.split_terms.size();
+        << k.split_mode << " " << k.split_terms.size();
       for (const auto& t : k.split_terms) o << " " << TermText(p, t);
       o << "\n";
     }
@@ -460,8 +461,12 @@ bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims,
   }
   if (k.split_dim >= 0) {
     const uint64_t chunks = SplitChunks(k, dims);
-    if (k.split_merge) g = chunks > 1 ? g : 0;
-    else g *= chunks;
+    switch (k.split_mode) {
+      case kSplitMerge: g = chunks > 1 ? g : 0; break;
+      case kSplitSingle: g = chunks == 1 ? g : 0; break;
+      case kSplitPartialMany: g = chunks > 1 ? g * chunks : 0; break;
+      default: g *= chunks; break;
+    }
     if (g > (1ull << 62)) {
       *err = "kernel " + k.symbol + ": grid overflows";
       return false;

@@ -17,12 +17,14 @@
 //       `dim` elements: S lanes share a row, S the smallest power of two <= the
 //       kernel's block with S * epl >= dim; it launches with max(min-block, S)
 //       lanes per block, max(min-block, S) / S rows each
-//   split <rdim> <rows-min> <blocks> <merge> <n-terms> <term>...    (for the last
+//   split <rdim> <rows-min> <blocks> <mode> <n-terms> <term>...    (for the last
 //       kernel) a reduction over `rdim` split into P row chunks: with B the
 //       product of the terms (the column blocks), P = 1 when rdim or B is 0,
-//       else min(ceil(rdim / rows-min), max(1, blocks / B)). merge 0: the
-//       grid is multiplied by P; merge 1: the kernel (the merge of the P
-//       partials) launches only when P > 1.
+//       else min(ceil(rdim / rows-min), max(1, blocks / B)). mode 0: the
+//       grid is multiplied by P; mode 1: the kernel (the merge of the P
+//       partials) launches only when P > 1; mode 2: the kernel launches only
+//       when P == 1 (a whole-column kernel); mode 3: as mode 0, but only when
+//       P > 1 (the partials of a nest whose P == 1 case is a mode-2 kernel).
 //   when <dim> <lo> <hi> <mod> <rem>    (for the last kernel) the kernel runs only
 //       when lo <= dim <= hi and dim % mod == rem; every guard of a kernel must
 //       hold. Variants of one nest specialised on a run-time dim carry guards
@@ -96,9 +98,14 @@ struct Kernel {
   uint64_t pack_epl = 0, pack_min_block = 0;
   int split_dim = -1;  // >= 0: a row-split reduction (see the split record)
   uint64_t split_rows_min = 0, split_blocks = 0;
-  bool split_merge = false;
+  // What the chunk count P does to this kernel's grid: kSplitPartial = grid
+  // x P, kSplitMerge = launched only when P > 1, kSplitSingle = launched
+  // only when P == 1, kSplitPartialMany = grid x P, launched only when P > 1.
+  int split_mode = 0;
   std::vector<Term> split_terms;
 };
+
+enum SplitMode { kSplitPartial = 0, kSplitMerge = 1, kSplitSingle = 2, kSplitPartialMany = 3 };
 
 struct Plan {
   std::string name;

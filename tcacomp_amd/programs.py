@@ -232,6 +232,28 @@ def col_sum_max():
     return b.Build()
 
 
+def col_mean_var(local_mean=False):
+    """Per-column mean and centred variance of f32 x [B, R, C] over R (the
+    statistics of a batch norm over the leading axes): mean = sum_r x * inv_n,
+    var = sum_r (x - mean)^2 * inv_n. The variance reads the mean at its own
+    column, so one column nest runs two passes; with `local_mean` the mean is
+    a local only the variance reads."""
+    b = NewBuilder("col_mean_var%s_dyn" % ("_l" if local_mean else ""))
+    B, R, C = b.Dim("B", 0), b.Dim("R", 0), b.Dim("C", 0)
+    x = b.Tensor("x", TF32, B, R, C)
+    mean = b.Local("mean", TF32, B, C) if local_mean else b.Tensor("mean", TF32, B, C)
+    var = b.Tensor("var", TF32, B, C)
+    inv_n = b.ScalarParam("inv_n", TF32)
+    (b.Stmt().Iter(B, R, C).Map([At(x, B, R, C)], lambda v: v).As(B, C, R)
+     .Reduce(b.Float32(0), _sum(b))
+     .Map([], lambda v: b.Mul(v, inv_n)).As(B, C).Store(mean, B, C))
+    (b.Stmt().Iter(B, R, C)
+     .Map([At(x, B, R, C), At(mean, B, C)], lambda l, m: b.Mul(b.Sub(l, m), b.Sub(l, m))).As(B, C, R)
+     .Reduce(b.Float32(0), _sum(b))
+     .Map([], lambda v: b.Mul(v, inv_n)).As(B, C).Store(var, B, C))
+    return b.Build()
+
+
 def col_mean_bf16():
     """Per (batch, column) scaled sum of bf16 x [B, R, C] over R, plus a
     column offset: out[b, c] = sum_r f32(x[b, r, c]) * scale + g[c]."""
@@ -561,6 +583,8 @@ CONFIG_PROGRAMS = {
     "chain_halving": chain_halving,
     "col_sum_max_dyn": col_sum_max,
     "col_mean_bf16": col_mean_bf16,
+    "col_mean_var_dyn": col_mean_var,
+    "col_mean_var_l_dyn": lambda: col_mean_var(True),
     "col_sum_u8": col_sum_u8,
     "scale_relu": scale_relu,
     "scale_relu_map": scale_relu_map,

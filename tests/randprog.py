@@ -318,7 +318,11 @@ class GridSpec:
     y [R, C], `tmap` stores the transposed z [C, R]) and reductions over the
     leading axis (`colreduce`: out [C] = fold over R, the iteration order
     written As(C, R) so the reduce drops R). Operands: row tiles x<k> [R, C],
-    a transposed tile xt [C, R] read at (c, r), g [C], r [R], scalars."""
+    a transposed tile xt [C, R] read at (c, r), g [C], r [R], scalars, and
+    (chain programs) the results of earlier colreduce statements, read at
+    their own column — a later reduction reading an earlier one is a
+    dependent column nest (a variance reading its mean). A statement with
+    "local": True stores a local that only later statements read."""
 
     kind = "grid"
 
@@ -328,7 +332,7 @@ class GridSpec:
         self.batch = batch  # a leading batch axis B: x0 [B, R, C], xt [B, C, R], outputs per batch
 
     def outputs(self):
-        return [s["out"] for s in self.stmts]
+        return [s["out"] for s in self.stmts if not s.get("local")]
 
 
 def generate_grid(seed, elem, dynamic, batch=False):
@@ -368,6 +372,59 @@ def generate_grid(seed, elem, dynamic, batch=False):
     return GridSpec(name, elem, c, tiles, trans, col, row, scalars, stmts, batch)
 
 
+def generate_colchain(seed, elem, dynamic, batch=False):
+    """A random grid program of dependent column reductions: a first
+    colreduce over the tiles, then colreduces (at least one), maps and
+    piped maps that read earlier colreduce results at their own column.
+    Combining with an earlier result is mostly + and -, with no division,
+    so f32 values stay integers and the tests' input ranges keep every sum
+    exact. Each result a later statement reads is a local half the time."""
+    rng = random.Random(0xBB67AE85 ^ (seed * 0x9E3779B1))
+    c = 0 if dynamic else rng.choice(STATIC_C[:8])
+    if elem == "f32":
+        tiles = [("x0", rng.choice(["f32", "f32", "bf16"]))]
+        scalars = [("s%d" % k, rng.choice([-1.0, 2.0, 3.0])) for k in range(rng.choice([0, 1]))]
+    else:
+        tiles = [("x0", rng.choice(["u32", "u8"]))]
+        scalars = [("s%d" % k, rng.choice([3, 0xFFFFFFFF])) for k in range(rng.choice([0, 1]))]
+    trans = rng.random() < 0.4
+    col = rng.random() < 0.5
+    row = rng.random() < 0.4
+    pool = ["x0"] + (["xt"] if trans else []) + (["g"] if col else []) + (["r"] if row else [])
+    sc_pool = [n for n, _ in scalars]
+    stmts, prev = [], []
+    n = rng.choice([2, 3, 4])
+    for i in range(n):
+        kind = "colreduce" if i < 2 else rng.choice(["colreduce", "colreduce", "map"])
+        e = _expr(rng, elem, pool + sc_pool, 2, False, 1)
+        if not any(l in ("x0", "xt") for l in leaves(e)):
+            e = ("add", ("leaf", rng.choice(["x0", "xt"] if trans else ["x0"])), e)
+        if prev and (i == 1 or rng.random() < 0.7):
+            op = rng.choice(["add", "sub", "add", "sub"] + (["mul"] if count_mul(e) == 0 else []))
+            e = (op, e, ("leaf", rng.choice(prev)))
+        comb = piped = None
+        if kind == "colreduce":
+            comb = rng.choice(F32_COMBS if elem == "f32" else U32_COMBS)
+            if rng.random() < 0.4:
+                piped = _expr(rng, elem, ["v"] + (["g"] if col else []) + sc_pool + prev, 2, False, 1)
+                if "v" not in leaves(piped):
+                    piped = ("add", ("leaf", "v"), piped)
+        stmts.append({"kind": kind, "expr": e, "comb": comb, "piped": piped, "out": "%s%d" % (kind[0], i),
+                      "local": False})
+        if kind == "colreduce":
+            prev.append("c%d" % i)
+    read = set()
+    for st in stmts:
+        read.update(leaves(st["expr"]))
+        if st["piped"] is not None:
+            read.update(leaves(st["piped"]))
+    for st in stmts:
+        if st["out"] in read and rng.random() < 0.5:
+            st["local"] = True
+    name = "gridc%s_%s_%s_%d" % ("3" if batch else "", elem, "dyn" if dynamic else "c%d" % c, seed)
+    return GridSpec(name, elem, c, tiles, trans, col, row, scalars, stmts, batch)
+
+
 def _build_grid(spec):
     b = NewBuilder(spec.name)
     B = [b.Dim("B", 0)] if spec.batch else []
@@ -387,7 +444,9 @@ def _build_grid(spec):
     outs = {}
     for st in spec.stmts:
         dims = {"map": B + [R, C], "tmap": B + [C, R], "colreduce": B + [C]}[st["kind"]]
-        outs[st["out"]] = b.Tensor(st["out"], work, *dims)
+        outs[st["out"]] = (b.Local if st.get("local") else b.Tensor)(st["out"], work, *dims)
+        if st["kind"] == "colreduce":  # later statements read it at (batch, column)
+            ops[st["out"]] = (outs[st["out"]], B + [C], False)
 
     def fn_for(e, names, pre=()):
         def f(*params):
@@ -439,10 +498,17 @@ GRID3_PROGRAMS = ([("f32", True, s) for s in range(60, 66)] + [("f32", False, s)
                   [("u32", True, s) for s in range(68, 70)])
 
 
+# Random dependent column programs: (elem, dynamic row length, batch axis, seed).
+COLCHAIN_PROGRAMS = ([("f32", True, False, s) for s in range(80, 86)] + [("f32", False, False, s) for s in (86, 87)] +
+                     [("u32", True, False, s) for s in (88, 89)] + [("u32", False, False, 90)] +
+                     [("f32", True, True, s) for s in (91, 92)] + [("u32", True, True, 93)])
+
+
 def specs():
     return ([generate(seed, elem, dyn) for elem, dyn, seed in PROGRAMS] +
             [generate_grid(seed, elem, dyn) for elem, dyn, seed in GRID_PROGRAMS] +
-            [generate_grid(seed, elem, dyn, True) for elem, dyn, seed in GRID3_PROGRAMS])
+            [generate_grid(seed, elem, dyn, True) for elem, dyn, seed in GRID3_PROGRAMS] +
+            [generate_colchain(seed, elem, dyn, batch) for elem, dyn, batch, seed in COLCHAIN_PROGRAMS])
 
 
 def all_builds():

@@ -163,14 +163,69 @@ def test_col_split_geometry(R, C, variant, part_grid, merge_grid):
     assert sel == {base + "p%d" % variant: part_grid, base + "m%d" % variant: merge_grid}, sel
 
 
+@pytest.mark.parametrize("B,R,C,want", [
+    # 4 column blocks, P = min(16, 256) = 16 > 1: a partial + merge pair per pass
+    (1, 1000, 1000, {"p4_1": 4 * 16, "m4_1": 16, "p4_2": 4 * 16, "m4_2": 16}),
+    # <= 64 rows: P = 1, the whole-column kernel runs both passes
+    (3, 64, 1000, {"w4": 3 * 4}),
+    (1, 0, 1000, {"w4": 4}),
+    # 547 column blocks leave room for one chunk: P = 1 over 100 rows
+    (1, 100, 140000, {"w4": 547}),
+    # odd columns: 1-element vectors, 2 column blocks, P = min(16, 512) = 16
+    (2, 1000, 65, {"p1_1": 2 * 2 * 16, "m1_1": 3, "p1_2": 2 * 2 * 16, "m1_2": 3}),
+    (1, 100, 0, {})])
+def test_col_passes_geometry(B, R, C, want):
+    """A column nest of two passes (a variance reading its mean): with one
+    row chunk the whole-column kernel (split mode 2) runs both passes, with
+    more each pass is a partial (mode 3) and merge (mode 1) pair."""
+    e = programs.CONFIG_PROGRAMS["col_mean_var_dyn"]().emit()
+    assert set(e.families()) == {"col"}
+    rc, h = parse(e.plan)
+    assert rc == 0, _lib.last_error()
+    P = 0x1000
+    n = B * R * C
+    arr = compiler._descriptors([TensorDesc(P if n else 0, (B, R, C), 0), TensorDesc(P if B * C else 0, (B, C), 0),
+                                 TensorDesc(P if B * C else 0, (B, C), 0)])
+    syms = e.kernel_symbols()
+    out = (ctypes.c_uint8 * len(syms))()
+    grids = (ctypes.c_uint64 * len(syms))()
+    assert _lib.lib().tca_program_selected(h, arr, 3, None, 0, out, grids, None, len(syms)) == 0, _lib.last_error()
+    sel = {s[len("tca_col_mean_var_dyn_k0_"):]: g for s, f, g in zip(syms, out, grids) if f and g}
+    assert sel == want, sel
+    order = [s for s, f, g in zip(syms, out, grids) if f and g]
+    assert order == sorted(order, key=syms.index)  # launch order: pass 1 pair before pass 2
+
+
 def test_split_record_parse():
     for rec, ok in [("split M 64 2048 0 1 N/256", True), ("split M 64 2048 1 2 1/1 N/4", True),
                     ("split Q 64 2048 0 1 N/256", False), ("split M 0 2048 0 1 N/256", False),
-                    ("split M 64 0 0 1 N/256", False), ("split M 64 2048 2 1 N/256", False),
+                    ("split M 64 0 0 1 N/256", False), ("split M 64 2048 2 1 N/256", True),
+                    ("split M 64 2048 3 1 N/256", True), ("split M 64 2048 4 1 N/256", False),
                     ("split M 64 2048 0 2 N/256", False), ("split M 64 2048 0 1 N/pack", False),
                     ("split M 64 2048 0 1 Q/4", False)]:
         rc, _ = parse(PLAN.replace("arg scalar a\n", "arg scalar a\n%s\n" % rec))
         assert (rc == 0) == ok, (rec, _lib.last_error())
+
+
+@pytest.mark.parametrize("M,P", [(1, 1), (64, 1), (65, 2), (10**6, 512)])
+def test_split_modes_grid(M, P):
+    """The grid each split mode gives. The test plan's kernel grid is
+    ceil(M * N / 1024) * F = 3M at N = 1024, F = 3; its split has N/256 = 4
+    column blocks, so P = min(ceil(M / 64), 2048 / 4). Mode 0 multiplies the
+    grid by P, mode 1 launches only when P > 1, mode 2 only when P == 1,
+    mode 3 multiplies by P but only when P > 1."""
+    base = 3 * M
+    want = {0: base * P, 1: base if P > 1 else 0, 2: base if P == 1 else 0, 3: base * P if P > 1 else 0}
+    for mode, grid in want.items():
+        rc, h = parse(PLAN.replace("arg scalar a\n", "arg scalar a\nsplit M 64 2048 %d 1 N/256\n" % mode))
+        assert rc == 0, _lib.last_error()
+        ts = [TensorDesc(0x1000, (M, 1024, 4), 0), TensorDesc(0x1000, (1024,), 0), TensorDesc(0x1000, (M, 1024), 0)]
+        arr = compiler._descriptors(ts)
+        fd = (ctypes.c_uint32 * 1)(3)
+        sel = (ctypes.c_uint8 * 1)()
+        grids = (ctypes.c_uint64 * 1)()
+        assert _lib.lib().tca_program_selected(h, arr, 3, fd, 1, sel, grids, None, 1) == 0, _lib.last_error()
+        assert sel[0] == 1 and grids[0] == grid, (M, mode, grids[0], grid)
 
 
 @pytest.mark.parametrize("R,C,part_grid,merge_grid", [(1, 16388, 2, 1), (3, 10**6, 3 * 62, 1),

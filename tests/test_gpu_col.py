@@ -9,7 +9,16 @@ Expected values: integer-valued f32 inputs keep every sum exact (partial
 sums below 2^24), so the device matches the float64 sum rounded once, bit
 for bit, in any fold order; max is exact; u8 -> u32 sums are exact;
 col_mean_bf16's piped map is one rounded multiply and one rounded add on
-both sides."""
+both sides.
+
+col_mean_var (a variance reading its mean: one column nest of two passes)
+runs at shapes that reach the whole-column kernel (<= 64 rows, or more
+than 512 column blocks) and the per-pass partial + merge pairs. Its mean is
+an exact sum times f32(1 / R), one rounded multiply: bit for bit. Its
+variance sums f32 terms (x - mean)^2, each rounded once on both sides, in
+an order of the device's choosing: within the fold's rounding bound,
+gamma_(R-1) sum|terms| (gamma_n = n u / (1 - n u), u = 2^-24), plus the
+final multiply's rounding."""
 import sys
 
 import numpy as np
@@ -73,3 +82,29 @@ def test_col_sum_u8(gpu, R, C):
     run(compiled("col_sum_u8"), [to_dev(x, gpu), TensorDesc(o.data_ptr(), (C,), U32)])
     want = (x.astype(np.uint64).sum(axis=0) % (1 << 32)).astype(np.uint32)
     np.testing.assert_array_equal(o.cpu().numpy().view(np.uint32), want)
+
+
+@pytest.mark.parametrize("name", ["col_mean_var_dyn", "col_mean_var_l_dyn"])
+@pytest.mark.parametrize("B,R,C", [(1, 0, 8), (1, 1, 1), (3, 64, 1000), (2, 37, 6), (1, 100, 140000),
+                                   (1, 1000, 1000), (2, 3000, 65), (4, 300, 4100), (1, 65536, 256)])
+def test_col_mean_var(gpu, name, B, R, C):
+    print(name, B, R, C, flush=True)
+    sys.stdout.flush()
+    x = _ints((B, R, C), 8, B * 131 + R * 7 + C)
+    inv_n = np.float32(1.0 / max(R, 1))
+    mean = to_dev(np.full((B, C), CANARY, np.float32), gpu)
+    var = to_dev(np.full((B, C), CANARY, np.float32), gpu)
+    args = [to_dev(x, gpu)] + ([mean] if name == "col_mean_var_dyn" else []) + [var]
+    run(compiled(name), args, scalars=[float(inv_n)])
+    ssum = x.astype(np.float64).sum(axis=1).astype(np.float32)  # exact: |sums| < 2^24
+    want_mean = ssum * inv_n
+    if name == "col_mean_var_dyn":
+        np.testing.assert_array_equal(mean.cpu().numpy(), want_mean)
+    d = x - want_mean[:, None, :]  # f32: each term rounded once, as on the device
+    terms = (d * d).astype(np.float64)
+    exact = terms.sum(axis=1)
+    nu = max(R - 1, 0) * 2.0 ** -24
+    bound = nu / (1 - nu) * np.abs(terms).sum(axis=1) * float(inv_n) + np.abs(exact * float(inv_n)) * 2.0 ** -23
+    got = var.cpu().numpy().astype(np.float64)
+    err = np.abs(got - exact * float(inv_n))
+    assert np.all(err <= bound), (name, B, R, C, float(err.max()), float(bound[err > bound].min(initial=0)))

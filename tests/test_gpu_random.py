@@ -130,6 +130,10 @@ def _check(spec, generic, gpu):
 ROW_SPECS = [s for s in randprog.specs() if getattr(s, "kind", "row") == "row"]
 GRID_SPECS = [s for s in randprog.specs() if getattr(s, "kind", "row") == "grid"]
 GRID_SHAPES = [(1, 0), (0, 5), (1, 1), (37, 3), (300, 64), (37, 1000), (300, 4100), (5, 70001), (1000, 1000)]
+# Dependent column programs also run 100 rows of 140000 columns: 547 column
+# blocks, so one whole-column kernel runs every pass over all 100 rows (the
+# other shapes reach it with <= 64 rows, and the per-pass pairs with more).
+COLCHAIN_SHAPES = GRID_SHAPES + [(100, 140000)]
 
 
 @pytest.mark.parametrize("spec", ROW_SPECS, ids=lambda s: s.name)
@@ -140,11 +144,15 @@ def test_random_program(gpu, spec):
 @pytest.mark.parametrize("spec", GRID_SPECS, ids=lambda s: s.name)
 def test_random_grid_program(gpu, spec):
     """Elementwise maps with broadcast and transposed operands, transposed
-    stores, reductions over the leading axis (elementwise, streaming and
-    generic families)."""
+    stores, reductions over the leading axis (elementwise, streaming,
+    column and generic families), and dependent column reductions: a
+    reduction reading an earlier one's result at its own column (one
+    column nest of several passes: the whole-column kernel, or per-pass
+    partial and merge pairs)."""
     import torch
     prog = _program(spec, False)
-    shapes = [(r, spec.c) for r in (1, 37, 300)] if spec.c else GRID_SHAPES
+    shapes = ([(r, spec.c) for r in (1, 37, 300)] if spec.c else
+              COLCHAIN_SHAPES if spec.name.startswith("gridc") else GRID_SHAPES)
     lead = (3,) if spec.batch else ()  # batch programs: three batch indices
     for R, C in shapes:
         if spec.batch and R * C > (1 << 22):
@@ -177,6 +185,8 @@ def test_random_grid_program(gpu, spec):
             args.append(desc or d)
         outs = {}
         for st in spec.stmts:
+            if st.get("local"):
+                continue
             oshape = lead + {"map": (R, C), "tmap": (C, R), "colreduce": (C,)}[st["kind"]]
             if spec.elem == "f32":
                 o = torch.full(oshape, CANARY, device=gpu)

@@ -3,6 +3,8 @@
 evaluator agrees with a brute-force element loop in the reference's
 sequential fold order (runtime/tca/reducer.h:36-57) on tiny shapes, with
 hand-computed answers, and with the C oracle's row sum and max."""
+import re
+
 import numpy as np
 import pytest
 
@@ -147,6 +149,41 @@ def test_grid_evaluator_matches_brute_force(spec):
             np.testing.assert_array_equal(fast[k], slow[k], err_msg="%s %dx%d %s" % (spec.name, R, C, k))
 
 
+COLCHAINS = [s for s in GRIDS if s.name.startswith("gridc")]
+
+
+def test_colchain_programs_fuse_dependent_reductions():
+    """A dependent column program whose first two reductions read no
+    transposed tile emits them as one column nest of several passes: a
+    whole-column kernel per vector width, and a partial + merge pair per
+    pass. (A transposed tile xt [C, R] is contiguous along R: those nests
+    lower as row reductions of the stream family.)"""
+    fused = 0
+    for spec in COLCHAINS:
+        if any("xt" in randprog.leaves(st["expr"]) for st in spec.stmts[:2]):
+            continue
+        e = randprog.build(spec).emit()
+        k0 = [line.split() for line in e.report.splitlines() if "_k0_" in line.split()[0]]
+        assert {f for _, f, *_ in k0} == {"col"}, e.report
+        syms = [sym for sym, *_ in k0]
+        assert any(re.search(r"_k0_w\d+$", x) for x in syms), syms
+        passes = {int(m.group(1)) for m in (re.search(r"_k0_p\d+_(\d+)$", x) for x in syms) if m}
+        assert len(passes) >= 2 and passes == {int(m.group(1)) for m in
+                                               (re.search(r"_k0_m\d+_(\d+)$", x) for x in syms) if m}
+        fused += 1
+    assert fused >= 10, fused
+
+
+def test_colchain_generator_reads_earlier_results():
+    """Every dependent column program has a reduction that reads the result
+    of an earlier one, and some of those results are locals."""
+    for spec in COLCHAINS:
+        outs = [st["out"] for st in spec.stmts if st["kind"] == "colreduce"]
+        assert any(set(randprog.leaves(st["expr"])) & set(outs[:k])
+                   for k, st in enumerate(s for s in spec.stmts if s["kind"] == "colreduce")), spec.name
+    assert any(st["local"] for spec in COLCHAINS for st in spec.stmts)
+
+
 def test_grid_known_answers():
     from randprog import GridSpec
     spec = GridSpec("hand", "f32", 0, [("x0", "f32")], True, True, False, [], [
@@ -160,3 +197,23 @@ def test_grid_known_answers():
     np.testing.assert_array_equal(out["m0"], [[1 - 10, 2 - 30], [3 - 20, 4 - 40]])
     np.testing.assert_array_equal(out["t1"], [[1, 3], [2, 4]])
     np.testing.assert_array_equal(out["c2"], [4, -6])
+
+
+def test_grid_dependent_known_answers():
+    """A reduction reading an earlier one at its own column, by hand: c0 =
+    column sums (a local), c1 = max over rows of x - c0, piped + c0."""
+    from randprog import GridSpec
+    spec = GridSpec("hand", "f32", 0, [("x0", "f32")], False, False, False, [], [
+        {"kind": "colreduce", "expr": X0, "comb": "sum", "piped": None, "out": "c0", "local": True},
+        {"kind": "colreduce", "expr": ("sub", X0, ("leaf", "c0")), "comb": "max",
+         "piped": ("add", ("leaf", "v"), ("leaf", "c0")), "out": "c1", "local": False},
+        {"kind": "map", "expr": ("mul", X0, ("leaf", "c0")), "comb": None, "piped": None, "out": "m2",
+         "local": False}])
+    x = np.array([[1, 2], [3, 5]], np.float32)
+    out, exact = evaluate_grid(spec, x, None, None, None, {})
+    assert exact and sorted(out) == ["c1", "m2"]
+    np.testing.assert_array_equal(out["c1"], [max(1 - 4, 3 - 4) + 4, max(2 - 7, 5 - 7) + 7])
+    np.testing.assert_array_equal(out["m2"], [[4, 14], [12, 35]])
+    slow = evaluate_grid_scalar(spec, x, None, None, None, {})
+    for k in out:
+        np.testing.assert_array_equal(out[k], slow[k])
