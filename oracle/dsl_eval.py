@@ -8,6 +8,9 @@ The DSL semantics restated here, per statement:
 - Reduce drops the last live axis (pkg/chain.go:262) and folds
   acc = fn(acc, v) starting from init, once per output; an empty reduce
   yields init (runtime/tca/reducer.h:36-57; design/tca.md:299, :711);
+- a second Reduce in the same chain (pkg/chain.go:262 applied again)
+  drops the next live axis, folding the first one's results from its own
+  init, once per remaining output;
 - the piped map after a reduce sees the reduced value first, then its own
   operands, over the remaining axes (pkg/chain.go:301-316);
 - stores write the chain's result at its store subscripts
@@ -17,8 +20,9 @@ rounded, as the device's basic operations are under -ffp-contract=off) or
 wrapping uint32.
 
 The fold order of a float sum is not reproduced: evaluate() reports
-whether every sum is exact (integer-valued terms, sum of magnitudes below
-2^24 per output), in which case every order gives the same float32 and the
+whether every sum is exact (integer-valued finite terms, sum of their
+magnitudes below 2^24 per output; infinities and NaNs fix the result in
+any order), in which case every order gives the same float32 and the
 device must match it exactly. evaluate_scalar() is a brute-force element
 loop in the reference's sequential fold order, used to pin evaluate() on
 tiny inputs.
@@ -82,9 +86,11 @@ def _reduce(elem, comb, terms):
     init = _init(elem, comb)
     if elem == "f32":
         if comb == "sum":
+            # Non-finite terms fix the sum (an infinity, or NaN) in any
+            # order; the finite ones must be integers summing below 2^24.
             t = terms.astype(np.float64)
-            exact = bool(np.all(np.isfinite(t)) and np.all(np.floor(t) == t) and
-                         np.all(np.abs(t).sum(axis=-1) < EXACT_LIMIT))
+            tf = np.where(np.isfinite(t), t, 0.0)
+            exact = bool(np.all(np.floor(tf) == tf) and np.all(np.abs(tf).sum(axis=-1) < EXACT_LIMIT))
             return (init + t.sum(axis=-1)).astype(np.float32), exact
         f = np.fmax if comb == "max" else np.fmin
         if terms.shape[-1] == 0:
@@ -117,6 +123,31 @@ def evaluate(spec, tiles, col, row, scalars):
     outs, exact = {}, True
     with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
         for st in spec.stmts:
+            if st["kind"] in ("chain", "rowreduce"):
+                # chain: fold over C, then over the last row axis (pkg/chain.go:262 twice);
+                # rowreduce: fold row values over the last row axis. Both store [rows[:-1]].
+                if st["kind"] == "chain":
+                    env = {n: a.astype(dt) for n, a in tiles.items()}
+                    if col is not None:
+                        env["g"] = col.astype(dt)
+                    env.update({n: v[..., None] for n, v in rowvals.items()})
+                    env.update(scal)
+                    val = np.broadcast_to(np.asarray(_eval(st["expr"], env, elem), dt), full)
+                    inner, ok = _reduce(elem, st["comb"], val)
+                    red, ok2 = _reduce(elem, st["comb2"], inner)
+                else:
+                    env = dict(rowvals)
+                    env.update(scal)
+                    val = np.broadcast_to(np.asarray(_eval(st["expr"], env, elem), dt), rows)
+                    red, ok = _reduce(elem, st["comb"], np.array(val, dt))
+                    ok2 = True
+                exact = exact and ok and ok2
+                if st["piped"] is not None:
+                    penv = dict(scal)
+                    penv["v"] = red
+                    red = np.broadcast_to(np.asarray(_eval(st["piped"], penv, elem), dt), rows[:-1])
+                outs[st["out"]] = np.array(red, dt)
+                continue
             if st["kind"] in ("reduce", "map"):
                 env = {n: a.astype(dt) for n, a in tiles.items()}
                 if col is not None:
@@ -165,6 +196,34 @@ def evaluate_scalar(spec, tiles, col, row, scalars):
              "min": (lambda a, b: np.fmin(a, b)) if elem == "f32" else (lambda a, b: min(a, b))}
     with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
         for st in spec.stmts:
+            if st["kind"] in ("chain", "rowreduce"):
+                out = np.zeros(rows[:-1], np.float32 if elem == "f32" else np.uint32)
+                outer = st["comb2"] if st["kind"] == "chain" else st["comb"]
+                for sidx in np.ndindex(*rows[:-1]):
+                    acc2 = _init(elem, outer)
+                    for r in range(rows[-1]):
+                        ridx = sidx + (r,)
+                        renv = {n: v[ridx] for n, v in rowvals.items()}
+                        renv.update(scal)
+                        if st["kind"] == "chain":
+                            acc = _init(elem, st["comb"])
+                            for c in range(C):
+                                env = {n: cast(a[ridx + (c,)]) for n, a in tiles.items()}
+                                if col is not None:
+                                    env["g"] = cast(col[c])
+                                env.update(renv)
+                                acc = cast(combs[st["comb"]](acc, cast(_eval(st["expr"], env, elem))))
+                            v = acc
+                        else:
+                            v = cast(_eval(st["expr"], renv, elem))
+                        acc2 = cast(combs[outer](acc2, v))
+                    if st["piped"] is not None:
+                        env = dict(scal)
+                        env["v"] = acc2
+                        acc2 = cast(_eval(st["piped"], env, elem))
+                    out[sidx] = acc2
+                outs[st["out"]] = out
+                continue
             if st["kind"] == "map":
                 out = np.zeros(full, np.float32 if elem == "f32" else np.uint32)
                 for idx in np.ndindex(*full):

@@ -25,7 +25,8 @@ enum class Family {
   Stream,       // S: the same nests with a run-time (or register-exceeding) row length, streamed
   Col,          // C: reductions over a non-contiguous axis (the reduced axis outside the contiguous one)
   Gemm,         // G: dense K-contraction on MFMA
-  Generic       // X: one thread per output element, sequential folds
+  Generic,      // X: one thread per output element, sequential folds
+  Seg           // chained reductions in one kernel: a row reduction into a local, folded over rows per block
 };
 
 const char* FamilyName(Family f);

@@ -43,6 +43,7 @@ const char* FamilyName(Family f) {
     case Family::Col: return "col";
     case Family::Gemm: return "gemm";
     case Family::Generic: return "generic";
+    case Family::Seg: return "seg";
   }
   return "?";
 }
@@ -312,6 +313,13 @@ namespace {
 struct Nest {
   std::vector<int> chains;
   Family family = Family::Generic;
+  // Chained reductions folded in one kernel (the segment kernel): 1 on the
+  // inner nest (a row reduction into a local), 2 on the next nest (its
+  // fold over rows). seg_guard names the segment dim whose run-time value
+  // picks between the segment kernel and the two nests' own kernels; empty:
+  // the segment kernel alone.
+  int seg = 0;
+  std::string seg_guard;
 };
 
 struct Analysis {
@@ -704,6 +712,91 @@ class Emitter {
       else an_.hbm_local[t] = true;
     }
     for (const auto& n : an_.nests) uses_gemm_ |= (n.family == Family::Gemm);
+    // Chained reductions folded in one kernel.
+    for (size_t ni = 0; ni + 1 < an_.nests.size(); ++ni) {
+      std::string guard;
+      if (an_.nests[ni].seg || !MatchSeg(static_cast<int>(ni), &guard)) continue;
+      an_.nests[ni].seg = 1;
+      an_.nests[ni + 1].seg = 2;
+      an_.nests[ni].seg_guard = an_.nests[ni + 1].seg_guard = guard;
+      if (guard.empty()) {  // the local never exists
+        const int L = g_.chains[an_.nests[ni].chains[0]].store_tensor;
+        an_.hbm_local[L] = false;
+        an_.reg_nest[L] = -1;
+      }
+    }
+  }
+
+  // Segments per block of the segment kernel below which the two nests'
+  // own kernels run instead (they spread a segment over many blocks).
+  static constexpr uint64_t kSegMin = 1024;
+
+  // A row reduction into a local L (S..., r), then the next nest's single
+  // chain reducing L over r into (S...): the pattern a chained reduction
+  // splits into (row sums, then their max over the rows of each batch),
+  // and any program written that way. The segment kernel folds both with
+  // one block per segment (an output of the outer reduction), L never
+  // leaving registers. Requires: the inner nest is one chain of the row or
+  // streaming family with one reduction, no piped map, storing the local
+  // at its rows; the outer chain iterates exactly those rows, reads L there
+  // and otherwise only per-segment operands, has one associative-
+  // commutative reduction over r and stores at (S...); no other chain
+  // reads L. *guard receives the segment dim when its extent is a run-time
+  // value (then S must be that one dim), empty when the extents are known
+  // (then at least kSegMin segments).
+  bool MatchSeg(int ni, std::string* guard) {
+    if (!opts_.allow_fused) return false;
+    const Nest& in = an_.nests[ni];
+    const Nest& out = an_.nests[ni + 1];
+    if (in.chains.size() != 1 || out.chains.size() != 1) return false;
+    if (in.family != Family::Row && in.family != Family::Stream) return false;
+    const int ci = in.chains[0], cj = out.chains[0];
+    const ir::Chain& a = g_.chains[ci];
+    const ir::Chain& b = g_.chains[cj];
+    if (a.reduces.size() != 1 || a.has_piped) return false;
+    const int L = a.store_tensor;
+    if (!g_.tensors[L].local) return false;
+    RowGeom geo;
+    if (!RowShape(g_, {ci}, true, &geo) || geo.outer.empty() || a.root.as != geo.as) return false;
+    if (a.store_axes != geo.outer) return false;
+    const std::vector<int> S(geo.outer.begin(), geo.outer.end() - 1);
+    if (S.empty()) return false;
+    if (b.root.as != geo.outer || b.reduces.size() != 1 || !IsMonoidCombiner(g_, b.reduces[0])) return false;
+    if (b.store_axes != S) return false;
+    auto segShaped = [&](const ir::Operand& o) {
+      for (int x : o.axes)
+        if (std::find(S.begin(), S.end(), x) == S.end()) return false;
+      return true;
+    };
+    bool readsL = false;
+    for (const auto& o : b.root.ops) {
+      if (o.tensor == L) {
+        if (o.axes != geo.outer) return false;
+        readsL = true;
+      } else if (!segShaped(o)) {
+        return false;
+      }
+    }
+    if (!readsL) return false;
+    if (b.has_piped)
+      for (const auto& o : b.piped.ops)
+        if (o.tensor == L || !segShaped(o)) return false;
+    if (ReadSet(a).count(b.store_tensor)) return false;
+    for (size_t k = 0; k < g_.chains.size(); ++k)
+      if (an_.live[k] && static_cast<int>(k) != cj && ReadSet(g_.chains[k]).count(L)) return false;
+    bool dynamic = false;
+    uint64_t nseg = 1;
+    for (int d : S) {
+      if (g_.dims[d].extent == 0) dynamic = true;
+      else nseg *= g_.dims[d].extent;
+    }
+    if (!dynamic) {
+      guard->clear();
+      return nseg >= kSegMin;
+    }
+    if (S.size() != 1) return false;
+    *guard = g_.dims[S[0]].name;
+    return true;
   }
 
   bool IsGemm(const std::vector<int>& chains) {
@@ -814,6 +907,18 @@ class Emitter {
   // ------------------------------------------------------------- families
   bool EmitNest(int ni, std::string* err) {
     const Nest& n = an_.nests[ni];
+    if (n.seg == 1 && !EmitSeg(ni, err)) return false;
+    if (n.seg && n.seg_guard.empty()) return true;  // the segment kernel alone
+    const size_t k0 = plan_kernels_.size();
+    if (!EmitFamily(ni, err)) return false;
+    if (n.seg)  // the two nests' own kernels: fewer segments than kSegMin
+      for (size_t k = k0; k < plan_kernels_.size(); ++k)
+        plan_kernels_[k].when.push_back(n.seg_guard + " 0 " + std::to_string(kSegMin - 1) + " 1 0");
+    return true;
+  }
+
+  bool EmitFamily(int ni, std::string* err) {
+    const Nest& n = an_.nests[ni];
     switch (n.family) {
       case Family::Elementwise: return EmitElementwise(ni, err);
       case Family::Row: return EmitRow(ni, err);
@@ -821,6 +926,7 @@ class Emitter {
       case Family::Col: return EmitCol(ni, err);
       case Family::Gemm: return EmitGemmNest(ni, err);
       case Family::Generic: return EmitGeneric(ni, err);
+      case Family::Seg: break;  // emitted with its inner nest (EmitSeg)
     }
     return false;
   }
@@ -2548,6 +2654,295 @@ class Emitter {
             << kd.what;
         AddKernel(k, Family::Col, kd.chains, det.str());
       }
+    }
+    o << "\n";
+    return true;
+  }
+
+  // Seg: a chained reduction folded in one kernel. One 256-thread block per
+  // segment s (an output of the outer reduction) runs the rows r of the
+  // segment in steps of 2 RS rows (each slot two rows, RS apart), RS = 256 /
+  // SL, SL = the smallest power of two with 4 SL >= the row's vectors (at
+  // most 64: longer rows loop), each lane's vectors in groups of 4: 8 loads
+  // in flight per lane before a fold. A row's lanes fold their vectors with the inner
+  // combiner (every lane holds >= 1 vector of a non-empty row), meet by
+  // shuffles, and apply the inner init once: the value the local L would
+  // hold. Lane 0 of the row maps it (the outer chain's root map) and folds
+  // it into its slot's outer partial; the slots meet in LDS, and thread 0
+  // applies the outer init and piped map and stores. L is never stored. The
+  // row loop is uniform over the block (rows past the segment's end read
+  // its last row and fold nothing), so every shuffle runs with the whole
+  // wave. One kernel per vector width, chosen at launch by guards on the
+  // row length.
+  bool EmitSeg(int ni, std::string* err) {
+    (void)err;
+    const Nest& in = an_.nests[ni];
+    const Nest& outn = an_.nests[ni + 1];
+    const int ci = in.chains[0], cj = outn.chains[0];
+    const ir::Chain& a = g_.chains[ci];
+    const ir::Chain& b = g_.chains[cj];
+    const int L = a.store_tensor;
+    RowGeom geo;
+    RowShape(g_, {ci}, true, &geo);
+    const std::vector<int> S(geo.outer.begin(), geo.outer.end() - 1);
+    const int raxis = geo.outer.back(), caxis = geo.col;
+    Nest both;
+    both.chains = {ci, cj};
+    PlanKernel pk;
+    pk.symbol = Sym(g_, prefix_, ni);
+    const std::string sig = Signature(both, &pk);
+    const std::string args = CallArgs(both);
+    const std::string sym = pk.symbol;
+    const uint32_t vmax = RowVecMax(g_, {ci}, geo);
+    std::ostringstream& o = src_;
+    const std::string Tin = CType(g_.exprs[a.root.fn.body].type);
+    const std::string Tout = CType(g_.exprs[b.root.fn.body].type);
+    auto coord = [&](const std::string& col) {
+      return [&, col](int x) -> std::string {
+        if (x == caxis) return col;
+        return "c" + std::to_string(x);
+      };
+    };
+    // Operands of the inner map: row tiles and column vectors per vector,
+    // row scalars per row (r among their axes) or per segment.
+    std::vector<int> tiles, cols, rowsc, segsc;
+    auto note = [](std::vector<int>& v, int t) {
+      if (std::find(v.begin(), v.end(), t) == v.end()) v.push_back(t);
+    };
+    std::map<int, const ir::Operand*> opOf;
+    for (const auto& op : a.root.ops) {
+      opOf[op.tensor] = &op;
+      switch (Classify(op, geo)) {
+        case OpKind::RowTile: note(tiles, op.tensor); break;
+        case OpKind::ColVec: note(cols, op.tensor); break;
+        default:
+          if (std::find(op.axes.begin(), op.axes.end(), raxis) != op.axes.end()) note(rowsc, op.tensor);
+          else note(segsc, op.tensor);
+          break;
+      }
+    }
+    std::vector<const ir::Operand*> outerOps;
+    for (const auto& op : b.root.ops)
+      if (op.tensor != L) outerOps.push_back(&op);
+    if (b.has_piped)
+      for (const auto& op : b.piped.ops) outerOps.push_back(&op);
+    for (const ir::Operand* op : outerOps)
+      if (!opOf.count(op->tensor)) {
+        opOf[op->tensor] = op;
+        note(segsc, op->tensor);
+      }
+
+    o << "// statements #" << ci << " and #" << cj << ": segment family; reduce @" << g_.dims[caxis].name
+      << " per row, then @" << g_.dims[raxis].name << " per segment, in one kernel\n";
+    o << "template <uint32_t V>\n__device__ __forceinline__ void " << sym << "_seg(\n    " << sig << ") {\n";
+    o << "  const uint32_t C = " << ExtentExpr(g_, caxis) << ", R = " << ExtentExpr(g_, raxis) << ";\n";
+    o << "  const uint32_t VEC = C / V;\n";
+    o << "  uint32_t LSL = 0u;  // SL = 2^LSL lanes per row: the smallest power of two with 4 SL >= VEC, <= 64\n";
+    o << "  while (LSL < 6u && (4u << LSL) < VEC) ++LSL;\n";
+    o << "  const uint32_t SL = 1u << LSL, RS = 256u >> LSL;  // RS rows per block step\n";
+    o << "  const uint32_t cg = threadIdx.x & (SL - 1u), slot = threadIdx.x >> LSL;\n";
+    o << "  const uint32_t NV = tca::hip::ceil_div(VEC, SL);  // vectors of the longest lane share\n";
+    o << "  uint32_t srem = blockIdx.x;  // this block's segment\n";
+    for (int k = static_cast<int>(S.size()) - 1; k >= 0; --k) {
+      const int x = S[k];
+      if (k == 0)
+        o << "  const uint32_t c" << x << " = srem;\n";
+      else
+        o << "  const uint32_t c" << x << " = srem % " << ExtentExpr(g_, x) << "; srem /= " << ExtentExpr(g_, x)
+          << ";\n";
+    }
+    o << "  (void)srem;\n";
+    for (int cc : {ci, cj}) {
+      const ir::Chain& c = g_.chains[cc];
+      const std::string T = CType(g_.exprs[c.root.fn.body].type);
+      o << "  const auto comb" << cc << " = [](" << T << " acc, " << T << " now) -> " << T << " {\n";
+      ExprGen cg(g_, o, "    ", &counter_);
+      cg.Bind(c.reduces[0].fn.params[0], "acc");
+      cg.Bind(c.reduces[0].fn.params[1], "now");
+      const std::string r = cg.Gen(c.reduces[0].fn.body);
+      o << "    return " << r << ";\n  };\n";
+    }
+    const auto segAt = coord("0u");
+    for (int t : segsc)
+      o << "  const " << CType(g_.tensors[t].elem) << " os" << t << " = t" << t << "["
+        << Offset(t, opOf[t]->axes, segAt) << "];\n";
+    o << "  " << Tout << " oacc = " << Tout << "(0);\n  bool ohas = false;\n";
+    // Two rows per slot and step (RS apart), each lane's vectors in groups
+    // of 4 (the first group's vector 0 always owned, the rest clamped into
+    // the row and predicated): 8 loads in flight per lane before any fold.
+    constexpr int kRowsPerStep = 2;
+    o << "  for (uint32_t rb = 0u; rb < R; rb += " << kRowsPerStep << "u * RS) {  // uniform over the block\n";
+    for (int j = 0; j < kRowsPerStep; ++j) {
+      const std::string js = std::to_string(j);
+      o << "    const uint32_t r" << js << " = rb + " << js << "u * RS + slot;\n";
+      o << "    const bool rok" << js << " = r" << js << " < R;\n";
+      o << "    const uint32_t rr" << js << " = rok" << js << " ? r" << js
+        << " : R - 1u;  // rows past the end read the last one\n";
+    }
+    auto rowCoord = [&](int j, const std::string& col) {
+      return [&, j, col](int x) -> std::string {
+        if (x == caxis) return col;
+        if (x == raxis) return "rr" + std::to_string(j);
+        return "c" + std::to_string(x);
+      };
+    };
+    for (int j = 0; j < kRowsPerStep; ++j)
+      for (int t : rowsc)
+        o << "    const " << CType(g_.tensors[t].elem) << " rs" << t << "_" << j << " = t" << t << "["
+          << Offset(t, opOf[t]->axes, rowCoord(j, "0u")) << "];\n";
+    for (int j = 0; j < kRowsPerStep; ++j) o << "    " << Tin << " acc" << j << " = " << Tin << "(0);\n";
+    // Loads of vector vc<u> of row j into x<t>_<j>_<u> / cv<t>_<u>; then the fold.
+    auto loads = [&](std::ostringstream& bo, const std::string& ind, int j, const std::string& vv,
+                     const std::string& sfx) {
+      const auto at = rowCoord(j, vv + " * V");
+      for (int t : tiles)
+        bo << ind << "const auto x" << t << sfx << " = tca::hip::load_vec_nt<" << CType(g_.tensors[t].elem) << ", V>(t"
+           << t << " + " << Offset(t, opOf[t]->axes, at) << ");\n";
+    };
+    auto colLoads = [&](std::ostringstream& bo, const std::string& ind, const std::string& vv, const std::string& sfx) {
+      const auto at = rowCoord(0, vv + " * V");
+      for (int t : cols)
+        bo << ind << "const auto cv" << t << sfx << " = tca::hip::load_vec<" << CType(g_.tensors[t].elem) << ", V>(t"
+           << t << " + " << Offset(t, opOf[t]->axes, at) << ");\n";
+    };
+    auto fold = [&](std::ostringstream& bo, const std::string& ind, int j, const std::string& u, bool first,
+                    const std::string& ok) {
+      const std::string acc = "acc" + std::to_string(j);
+      bo << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) {\n";
+      ExprGen eg(g_, bo, ind + "  ", &counter_);
+      for (size_t k = 0; k < a.root.ops.size(); ++k) {
+        const int t = a.root.ops[k].tensor;
+        std::string v;
+        if (std::find(tiles.begin(), tiles.end(), t) != tiles.end())
+          v = "x" + std::to_string(t) + "_" + std::to_string(j) + "_" + u + "[q]";
+        else if (std::find(cols.begin(), cols.end(), t) != cols.end()) v = "cv" + std::to_string(t) + "_" + u + "[q]";
+        else if (std::find(rowsc.begin(), rowsc.end(), t) != rowsc.end())
+          v = "rs" + std::to_string(t) + "_" + std::to_string(j);
+        else v = "os" + std::to_string(t);
+        eg.Bind(a.root.fn.params[k], v);
+      }
+      const std::string ev = eg.Gen(a.root.fn.body);
+      const std::string fold1 = "comb" + std::to_string(ci) + "(" + acc + ", " + ev + ")";
+      if (first) bo << ind << "  " << acc << " = q == 0u ? " << ev << " : " << fold1 << ";\n";
+      else bo << ind << "  " << acc << " = " << ok << " ? " << fold1 << " : " << acc << ";\n";
+      bo << ind << "}\n";
+      if (FoldFenced(g_.exprs[a.root.fn.body].type)) bo << ind << "tca::hip::fold_fence(" << acc << ");\n";
+    };
+    {
+      std::ostringstream bo;
+      auto group = [&](const std::string& ind, bool first) {
+        for (int u = 0; u < 4; ++u) {
+          const std::string us = std::to_string(u);
+          bo << ind << "const uint32_t vi" << us << " = cg + (k + " << us << "u) * SL;\n";
+          bo << ind << "const bool ok" << us << " = vi" << us << " < VEC;\n";
+          bo << ind << "const uint32_t vc" << us << " = ok" << us << " ? vi" << us << " : VEC - 1u;\n";
+          colLoads(bo, ind, "vc" + us, "_" + us);
+          for (int j = 0; j < kRowsPerStep; ++j) loads(bo, ind, j, "vc" + us, "_" + std::to_string(j) + "_" + us);
+        }
+        for (int j = 0; j < kRowsPerStep; ++j)
+          for (int u = 0; u < 4; ++u) fold(bo, ind, j, std::to_string(u), first && u == 0, "ok" + std::to_string(u));
+      };
+      bo << "    if (VEC > 0u) {  // uniform; a lane's first vector cg < VEC (SL <= VEC)\n";
+      bo << "      {\n        const uint32_t k = 0u;\n";
+      group("        ", true);
+      bo << "      }\n";
+      bo << "      for (uint32_t k = 4u; k < NV; k += 4u) {\n";
+      group("        ", false);
+      bo << "      }\n    }\n";
+      o << bo.str();
+    }
+    for (int j = 0; j < kRowsPerStep; ++j) {
+      const std::string js = std::to_string(j);
+      o << "    acc" << js << " = tca::hip::seg_allreduce_rt(acc" << js << ", SL, comb" << ci << ");\n";
+    }
+    for (int j = 0; j < kRowsPerStep; ++j) {
+      const std::string js = std::to_string(j);
+      std::ostringstream bo;
+      ExprGen ig(g_, bo, "    ", &counter_);
+      const std::string init = ig.Gen(a.reduces[0].init);
+      bo << "    " << Tin << " rowv" << js << " = " << init << ";  // the value L holds for row r" << js << "\n";
+      bo << "    if (VEC > 0u) {\n";
+      ExprGen fg(g_, bo, "      ", &counter_);
+      fg.Bind(a.reduces[0].fn.params[0], init);
+      fg.Bind(a.reduces[0].fn.params[1], "acc" + js);
+      const std::string rv = fg.Gen(a.reduces[0].fn.body);
+      bo << "      rowv" << js << " = " << rv << ";\n    }\n";
+      ExprGen mg(g_, bo, "    ", &counter_);
+      for (size_t k = 0; k < b.root.ops.size(); ++k) {
+        const int t = b.root.ops[k].tensor;
+        mg.Bind(b.root.fn.params[k], t == L ? "rowv" + js : "os" + std::to_string(t));
+      }
+      const std::string m = mg.Gen(b.root.fn.body);
+      bo << "    if (cg == 0u && rok" << js << ") {\n      oacc = ohas ? comb" << cj << "(oacc, " << m << ") : " << m
+         << ";\n      ohas = true;\n    }\n";
+      o << bo.str();
+    }
+    o << "  }\n";
+    o << "  __shared__ " << Tout << " oslot[256];\n  __shared__ int hslot[256];\n";
+    o << "  if (cg == 0u) {\n    oslot[slot] = oacc;\n    hslot[slot] = ohas ? 1 : 0;\n  }\n";
+    o << "  __syncthreads();\n";
+    o << "  if (threadIdx.x != 0u) return;\n";
+    o << "  " << Tout << " a = " << Tout << "(0);\n  bool any = false;\n";
+    o << "  for (uint32_t s2 = 0u; s2 < RS; ++s2)\n    if (hslot[s2]) {\n      a = any ? comb" << cj
+      << "(a, oslot[s2]) : oslot[s2];\n      any = true;\n    }\n";
+    {
+      std::ostringstream bo;
+      ExprGen ig(g_, bo, "  ", &counter_);
+      const std::string init = ig.Gen(b.reduces[0].init);
+      bo << "  " << Tout << " fin = " << init << ";\n  if (any) {\n";
+      ExprGen fg(g_, bo, "    ", &counter_);
+      fg.Bind(b.reduces[0].fn.params[0], init);
+      fg.Bind(b.reduces[0].fn.params[1], "a");
+      const std::string fv = fg.Gen(b.reduces[0].fn.body);
+      bo << "    fin = " << fv << ";\n  }\n";
+      std::string val = "fin";
+      if (b.has_piped) {
+        ExprGen pg(g_, bo, "  ", &counter_);
+        pg.Bind(b.piped.fn.params[0], val);
+        for (size_t k = 0; k < b.piped.ops.size(); ++k)
+          pg.Bind(b.piped.fn.params[k + 1], "os" + std::to_string(b.piped.ops[k].tensor));
+        val = pg.Gen(b.piped.fn.body);
+      }
+      const int st = b.store_tensor;
+      bo << "  t" << st << "[" << Offset(st, b.store_axes, segAt) << "] = " << val << ";\n";
+      o << bo.str();
+    }
+    o << "}\n";
+    // One kernel per vector width.
+    const std::string cdim = g_.dims[caxis].name;
+    struct Width {
+      uint32_t v, mod, rem;
+    };
+    std::vector<Width> widths;
+    widths.push_back({vmax, vmax, 0});
+    for (uint32_t v = vmax / 2; v >= 1; v /= 2) widths.push_back({v, 2 * v, v});
+    const uint64_t ext = g_.dims[caxis].extent;
+    if (ext > 0) {
+      std::vector<Width> one;
+      for (const auto& w : widths)
+        if (ext % w.mod == w.rem) {
+          one.push_back(w);
+          break;
+        }
+      widths = one;
+    }
+    for (const auto& wd : widths) {
+      PlanKernel k = pk;
+      k.symbol = sym + "_g" + std::to_string(wd.v);
+      k.block = 256;
+      k.grid.push_back(DimProduct(S) + "/1");
+      if (ext == 0) k.when.push_back(cdim + " 0 4294967295 " + std::to_string(wd.mod) + " " + std::to_string(wd.rem));
+      if (!in.seg_guard.empty()) k.when.push_back(in.seg_guard + " " + std::to_string(kSegMin) + " 4294967295 1 0");
+      o << "extern \"C\" __global__ void __launch_bounds__(256) " << k.symbol << "(\n    " << sig << ") {\n  " << sym
+        << "_seg<" << wd.v << "u>(" << args << ");\n}\n";
+      std::ostringstream det;
+      det << "reduce @" << cdim << " per row then @" << g_.dims[raxis].name << " per segment, one block per segment vec="
+          << wd.v
+          << (ext == 0 ? " (" + cdim + " % " + std::to_string(wd.mod) + " == " + std::to_string(wd.rem) + ")"
+                       : std::string())
+          << (in.seg_guard.empty() ? std::string()
+                                   : " (" + in.seg_guard + " >= " + std::to_string(kSegMin) + " segments)");
+      AddKernel(k, Family::Seg, {ci, cj}, det.str());
     }
     o << "\n";
     return true;

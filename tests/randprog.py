@@ -192,6 +192,60 @@ def generate(seed, elem, dynamic):
     return Spec(name, elem, c, outer, tiles, col, row, scalars, stmts)
 
 
+def generate_rowchain(seed, elem, dynamic):
+    """A random program of chained reductions over rows [B, R] (one in ten
+    over [R]): a `chain` statement (Reduce over C, then Reduce over R, in
+    one chain: pkg/chain.go:262 twice) or a `reduce` into a local followed
+    by a `rowreduce` of it over R (the same pattern written as two chains),
+    with an optional piped map over the result; then possibly a second
+    such statement or a plain row reduction. Both store one value per
+    segment B (a scalar over [R])."""
+    rng = random.Random(0x3C6EF372 ^ (seed * 0x9E3779B1))
+    outer = 1 if rng.random() < 0.1 else 2
+    c = 0 if dynamic else rng.choice(STATIC_C[:8])
+    if elem == "f32":
+        tiles = [("x0", rng.choice(["f32", "f32", "bf16"]))]
+        scalars = [("s%d" % k, rng.choice([-1.0, 2.0, 3.0])) for k in range(rng.choice([0, 1]))]
+    else:
+        tiles = [("x0", rng.choice(["u32", "u32", "u8"]))]
+        scalars = [("s%d" % k, rng.choice([3, 0xFFFFFFFF])) for k in range(rng.choice([0, 1]))]
+    col = rng.random() < 0.5
+    row = rng.random() < 0.3
+    pool = ["x0"] + (["g"] if col else []) + (["r"] if row else [])
+    sc_pool = [n for n, _ in scalars]
+    combs = F32_COMBS if elem == "f32" else U32_COMBS
+    stmts = []
+    for i in range(rng.choice([1, 1, 2])):
+        e = _expr(rng, elem, pool + sc_pool, 2, False, 1)
+        if "x0" not in leaves(e):
+            e = ("add", ("leaf", "x0"), e)
+        piped = None
+        if rng.random() < 0.4:
+            piped = _expr(rng, elem, ["v"] + sc_pool, 2, False, 1)
+            if "v" not in leaves(piped):
+                piped = ("add", ("leaf", "v"), piped)
+        if rng.random() < 0.6:
+            stmts.append({"kind": "chain", "expr": e, "comb": rng.choice(combs), "comb2": rng.choice(combs),
+                          "piped": piped, "out": "o%d" % i, "local": False})
+        else:
+            loc = "l%d" % i
+            stmts.append({"kind": "reduce", "expr": e, "comb": rng.choice(combs), "piped": None, "out": loc,
+                          "local": True})
+            e2 = _expr(rng, elem, [loc] + sc_pool, 2, False, 1)
+            if loc not in leaves(e2):
+                e2 = ("add", ("leaf", loc), e2)
+            stmts.append({"kind": "rowreduce", "expr": e2, "comb": rng.choice(combs), "piped": piped,
+                          "out": "o%d" % i, "local": False})
+    if rng.random() < 0.3:
+        e = _expr(rng, elem, pool + sc_pool, 2, False, 1)
+        if "x0" not in leaves(e):
+            e = ("add", ("leaf", "x0"), e)
+        stmts.append({"kind": "reduce", "expr": e, "comb": rng.choice(combs), "piped": None, "out": "o9",
+                      "local": False})
+    name = "rowc_%s_%s_%d" % (elem, "dyn" if dynamic else "c%d" % c, seed)
+    return Spec(name, elem, c, outer, tiles, col, row, scalars, stmts)
+
+
 def _rename(e, old, new):
     if e[0] == "leaf":
         return ("leaf", new) if e[1] == old else e
@@ -258,6 +312,8 @@ def build(spec):
     for st in spec.stmts:
         if st["kind"] == "map":
             ops[st["out"]] = (b.Tensor(st["out"], work, *full), full, False)
+        elif st["kind"] in ("chain", "rowreduce"):  # one value per segment rows[:-1]
+            ops[st["out"]] = (b.Tensor(st["out"], work, *rows[:-1]), rows[:-1], False)
         elif st["local"]:
             ops[st["out"]] = (b.Local(st["out"], work, *rows), rows, False)
         else:
@@ -291,6 +347,19 @@ def build(spec):
         elif st["kind"] == "rowmap":
             names, operand_list = operands(st["expr"])
             b.Stmt().Iter(*rows).Map(operand_list, fn_for(st["expr"], names)).As(*rows).Store(out_t, *rows)
+        elif st["kind"] in ("chain", "rowreduce"):
+            names, operand_list = operands(st["expr"])
+            it = full if st["kind"] == "chain" else rows
+            chain = b.Stmt().Iter(*it).Map(operand_list, fn_for(st["expr"], names)).As(*it)
+            init, comb = _init_comb(b, spec.elem, st["comb"])
+            chain = chain.Reduce(init, comb)
+            if st["kind"] == "chain":  # a second reduction in the same chain: over the last row axis
+                init2, comb2 = _init_comb(b, spec.elem, st["comb2"])
+                chain = chain.Reduce(init2, comb2)
+            if st["piped"] is not None:
+                pnames, plist = operands(st["piped"], extra=("v",))
+                chain = chain.Map(plist, fn_for(st["piped"], pnames, pre=("v",))).As(*rows[:-1])
+            chain.Store(out_t, *rows[:-1])
         else:
             names, operand_list = operands(st["expr"])
             b.Stmt().Iter(*full).Map(operand_list, fn_for(st["expr"], names)).As(*full).Store(out_t, *full)
@@ -504,11 +573,17 @@ COLCHAIN_PROGRAMS = ([("f32", True, False, s) for s in range(80, 86)] + [("f32",
                      [("f32", True, True, s) for s in (91, 92)] + [("u32", True, True, 93)])
 
 
+# Random chained-reduction programs over rows: (elem, dynamic row length, seed).
+ROWCHAIN_PROGRAMS = ([("f32", True, s) for s in range(100, 106)] + [("f32", False, s) for s in (106, 107)] +
+                     [("u32", True, s) for s in (108, 109, 110)] + [("u32", False, 111)])
+
+
 def specs():
     return ([generate(seed, elem, dyn) for elem, dyn, seed in PROGRAMS] +
             [generate_grid(seed, elem, dyn) for elem, dyn, seed in GRID_PROGRAMS] +
             [generate_grid(seed, elem, dyn, True) for elem, dyn, seed in GRID3_PROGRAMS] +
-            [generate_colchain(seed, elem, dyn, batch) for elem, dyn, batch, seed in COLCHAIN_PROGRAMS])
+            [generate_colchain(seed, elem, dyn, batch) for elem, dyn, batch, seed in COLCHAIN_PROGRAMS] +
+            [generate_rowchain(seed, elem, dyn) for elem, dyn, seed in ROWCHAIN_PROGRAMS])
 
 
 def all_builds():

@@ -196,6 +196,56 @@ def test_col_passes_geometry(B, R, C, want):
     assert order == sorted(order, key=syms.index)  # launch order: pass 1 pair before pass 2
 
 
+@pytest.mark.parametrize("B,C,want", [
+    (1024, 96, ["g4"]), (5000, 6, ["g2"]), (1024, 7, ["g1"]),
+    # fewer than 1024 segments: the two nests' own kernels (row sums into the local, then their max)
+    (1023, 96, ["c4", "k1_c4"]), (3, 7, ["c1", "k1_c4"])])
+def test_chain_segment_selection(B, C, want):
+    """A chained reduction folds in one segment kernel from 1024 segments
+    on (one block each); below that the inner and outer nests keep their
+    own kernels, which spread a segment over many blocks."""
+    e = programs.CONFIG_PROGRAMS["chain_sum_max"]().emit()
+    assert "seg" in e.families()
+    rc, h = parse(e.plan)
+    assert rc == 0, _lib.last_error()
+    R = 40
+    arr = compiler._descriptors([TensorDesc(0x1000, (B, R, C), 0), TensorDesc(0x1000, (B,), 0)])
+    syms = e.kernel_symbols()
+    out = (ctypes.c_uint8 * len(syms))()
+    grids = (ctypes.c_uint64 * len(syms))()
+    assert _lib.lib().tca_program_selected(h, arr, 2, None, 0, out, grids, None, len(syms)) == 0, _lib.last_error()
+    sel = [s[len("tca_chain_sum_max_k0_"):] if s.startswith("tca_chain_sum_max_k0_") else s[len("tca_chain_sum_max_"):]
+           for s, f, g in zip(syms, out, grids) if f and g]
+    assert sel == want, sel
+    if want[0].startswith("g"):
+        assert [g for s, f, g in zip(syms, out, grids) if f and g] == [B]
+
+
+def test_chain_segment_static_drops_the_local():
+    """With the segment count known at compile time (>= 1024), the segment
+    kernel is the only one and the local between the reductions is not in
+    the plan at all (no workspace)."""
+    from tcacomp_amd.pkg import TF32, At, Call, NewBuilder
+    b = NewBuilder("chain_static_seg")
+    B, R, C = b.Dim("B", 2048), b.Dim("R", 0), b.Dim("C", 64)
+    x = b.Tensor("x", TF32, B, R, C)
+    o = b.Tensor("o", TF32, B)
+    (b.Stmt().Iter(B, R, C).Map([At(x, B, R, C)], lambda v: v).As(B, R, C)
+     .Reduce(b.Float32(0), lambda a, v: b.Add(a, v)).Reduce(b.Float32(0), lambda a, v: Call("fmaxf", a, v)).Store(o, B))
+    e = b.Build().emit()
+    assert e.families() == ["seg"], e.report
+    assert "__chain" not in e.plan
+    b2 = NewBuilder("chain_static_few")
+    B, R, C = b2.Dim("B", 1000), b2.Dim("R", 0), b2.Dim("C", 64)
+    x = b2.Tensor("x", TF32, B, R, C)
+    o = b2.Tensor("o", TF32, B)
+    (b2.Stmt().Iter(B, R, C).Map([At(x, B, R, C)], lambda v: v).As(B, R, C)
+     .Reduce(b2.Float32(0), lambda a, v: b2.Add(a, v)).Reduce(b2.Float32(0), lambda a, v: Call("fmaxf", a, v))
+     .Store(o, B))
+    e2 = b2.Build().emit()
+    assert "seg" not in e2.families() and "__chain" in e2.plan
+
+
 def test_split_record_parse():
     for rec, ok in [("split M 64 2048 0 1 N/256", True), ("split M 64 2048 1 2 1/1 N/4", True),
                     ("split Q 64 2048 0 1 N/256", False), ("split M 0 2048 0 1 N/256", False),
@@ -396,8 +446,10 @@ EXPECTED_FAMILIES = {
     "row_sum_bf16_dyn": ["stream"] * 16, "row_sum_u8_dyn": ["stream"] * 20, "row_stats_u32_dyn": ["stream"] * 12,
     # column reductions: a (partial, merge) pair per vector width
     "col_sum_max_dyn": ["col"] * 6, "col_mean_bf16": ["col"] * 8, "col_sum_u8": ["col"] * 10,
-    # chained reductions split into an inner reduce into a local and an outer reduce of it
-    "chain_sum_max": ["stream"] * 18, "chain_total": ["stream"] * 21, "chain3_max_total": ["stream"] * 27,
+    # chained reductions split into an inner reduce into a local and an outer reduce of it; with a
+    # segment dim (B) the pair also has a segment kernel per vector width, chosen from 1024 segments on
+    "chain_sum_max": ["seg"] * 3 + ["stream"] * 18, "chain_total": ["stream"] * 21,
+    "chain3_max_total": ["seg"] * 3 + ["stream"] * 27,
 }
 
 

@@ -5,7 +5,13 @@ runs on the row/streaming families (and split rows); the fold keeps its
 structure: the inner init once per element of the local, the outer init
 once per output. Integer-valued inputs make every sum exact, so the device
 matches the closed form exactly in any fold order, and matches the generic
-lowering of the same program (one thread per output, sequential folds)."""
+lowering of the same program (one thread per output, sequential folds).
+
+With at least 1024 segments (outputs of the outer reduction) the pair runs
+as one segment kernel instead: a block per segment folds each row's inner
+reduction and then the rows, the local never stored; the shapes with
+B >= 1024 reach it (every vector width, rows longer than 4 vectors per
+lane, no rows, empty rows)."""
 import sys
 
 import numpy as np
@@ -23,7 +29,10 @@ def _ints(shape, bound, seed):
 
 
 @pytest.mark.parametrize("B,R,C", [(1, 1, 1), (3, 5, 7), (2, 1000, 64), (4, 300, 5000), (1, 20000, 16),
-                                   (2, 0, 4), (2, 3, 0), (3, 7, 70001)])
+                                   (2, 0, 4), (2, 3, 0), (3, 7, 70001),
+                                   # segment kernel
+                                   (1024, 1, 1), (1024, 40, 96), (1500, 3, 1000), (2048, 0, 8), (1030, 5, 0),
+                                   (1100, 70, 3), (1024, 9, 4100), (1024, 300, 6), (1023, 40, 96)])
 def test_chain_sum_max(gpu, B, R, C):
     print("chain_sum_max", B, R, C, flush=True)
     sys.stdout.flush()
@@ -55,7 +64,7 @@ def test_chain_total(gpu, R, C):
 
 
 @pytest.mark.parametrize("B,R,C", [(1, 1, 1), (5, 3, 7), (3, 1000, 100), (2, 20, 70001), (300, 2, 3), (0, 4, 4),
-                                   (4, 0, 4), (4, 4, 0)])
+                                   (4, 0, 4), (4, 4, 0), (1200, 3, 7), (2000, 17, 130)])
 def test_chain3_max_total(gpu, B, R, C):
     """Three reduces in one chain: split twice (inner, middle, outer)."""
     print("chain3_max_total", B, R, C, flush=True)

@@ -30,7 +30,21 @@ DYN_C = [0, 1, 3, 6, 64, 1000, 4100, 20000, 70001, 140000]
 ROWS = {1: [(1,), (37,), (300,)], 2: [(1, 1), (3, 37), (20, 15)]}
 
 
+# Chained reductions over rows: segments B from 1 to past the segment
+# kernel's 1024, every vector width and long rows; (B, R, C) products kept
+# small enough that f32 sums stay exact.
+ROWC_ROWS = {1: [(1,), (37,), (300,)], 2: [(1, 1), (3, 37), (20, 15), (1024, 3), (1100, 17), (2048, 1), (1024, 0)]}
+ROWC_DYN = [(1, 1, 0), (3, 37, 1), (20, 15, 3), (1024, 3, 6), (1100, 17, 64), (2048, 1, 1000), (1024, 9, 4100),
+            (3, 37, 20000), (1030, 2, 20000), (1024, 0, 5), (1024, 5, 0), (1100, 17, 7), (1024, 3, 70001)]
+
+
 def _shapes(spec, generic):
+    if spec.name.startswith("rowc"):
+        if spec.outer == 1:
+            return [r + (c,) for r in ROWC_ROWS[1] for c in ((spec.c,) if spec.c else (0, 5, 1000, 70001))]
+        if spec.c:
+            return [r[:2] + (spec.c,) for r in ROWC_ROWS[2] if r[0] * max(r[1], 1) * spec.c <= 1 << 24]
+        return ROWC_DYN
     rows = ROWS[spec.outer]
     if spec.c:
         return [r + (spec.c,) for r in rows]
@@ -109,7 +123,7 @@ def _check(spec, generic, gpu):
         for st in spec.stmts:
             if st["local"]:
                 continue
-            oshape = shape if st["kind"] == "map" else rows
+            oshape = shape if st["kind"] == "map" else rows[:-1] if st["kind"] in ("chain", "rowreduce") else rows
             if spec.elem == "f32":
                 o = torch.full(oshape, CANARY, device=gpu)
                 args.append(o)
