@@ -274,15 +274,14 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   const int ta = c.root.ops[m.a_op].tensor, tb = c.root.ops[m.b_op].tensor, tc = c.store_tensor;
   const bool bf16 = m.in == Elem::BF16;
   const int tile = bf16 ? 256 : 128;
-  o << "// contraction over @" << g.dims[m.k].name << " on MFMA (" << (bf16 ? "bf16 32x32x16" : "f32 32x32x2")
-    << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << ", " << tile << "x" << tile << " tiles\n";
-  o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "(\n    " << signature << ") {\n";
-  o << "  const uint32_t M = " << ExtentExpr(g, m.m) << ", N = " << ExtentExpr(g, m.n) << ", K = "
-    << ExtentExpr(g, m.k) << ";\n";
-  o << "  const auto epi = [&](float acc, uint32_t cm, uint32_t cn) -> float {\n";
+  // The fused epilogue (the piped map at (cm, cn)), the same in every kernel.
+  std::ostringstream epi;
+  epi << "  const uint32_t M = " << ExtentExpr(g, m.m) << ", N = " << ExtentExpr(g, m.n) << ", K = "
+      << ExtentExpr(g, m.k) << ";\n";
+  epi << "  const auto epi = [&](float acc, uint32_t cm, uint32_t cn) -> float {\n";
   std::string val = "acc";
   if (c.has_piped) {
-    ExprGen pg(g, o, "    ", counter);
+    ExprGen pg(g, epi, "    ", counter);
     pg.Bind(c.piped.fn.params[0], "acc");
     for (size_t k = 0; k < c.piped.ops.size(); ++k) {
       const auto& op = c.piped.ops[k];
@@ -296,15 +295,47 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
     }
     val = pg.Gen(c.piped.fn.body);
   }
-  o << "    return " << val << ";\n  };\n";
-  o << "  tca::hip::gemm_" << (bf16 ? "bf16" : "f32") << "_" << tile << "<" << (m.b_nk ? "true" : "false") << ">(t" << ta
-    << ", t" << tb << ", t" << tc << ", M, N, K, epi);\n}\n\n";
-  out->block = 256;
-  out->lds = 0;
-  out->grid = {g.dims[m.m].name + "/" + std::to_string(tile), g.dims[m.n].name + "/" + std::to_string(tile)};
-  out->detail = std::string(bf16 ? "bf16" : "f32") + " mfma 32x32 tile=" + std::to_string(tile) + "x" +
-                std::to_string(tile) + (bf16 ? " bk=32 (direct-to-LDS ring; edge tiles 64)" : " bk=32") +
-                (m.b_nk ? " B=[n][k]" : " B=[k][n]");
+  epi << "    return " << val << ";\n  };\n";
+  const std::string args = "(t" + std::to_string(ta) + ", t" + std::to_string(tb) + ", t" + std::to_string(tc) +
+                           ", M, N, K, epi);\n}\n\n";
+  const std::string nk = m.b_nk ? "true" : "false";
+  const std::vector<std::string> grid = {g.dims[m.m].name + "/" + std::to_string(tile),
+                                         g.dims[m.n].name + "/" + std::to_string(tile)};
+  const std::string orient = m.b_nk ? " B=[n][k]" : " B=[k][n]";
+  o << "// contraction over @" << g.dims[m.k].name << " on MFMA (" << (bf16 ? "bf16 32x32x16" : "f32 32x32x2")
+    << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << ", " << tile << "x" << tile << " tiles\n";
+  if (!bf16) {
+    o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "(\n    " << signature << ") {\n"
+      << epi.str() << "  tca::hip::gemm_f32_128<" << nk << ">" << args;
+    GemmKernel k;
+    k.grid = grid;
+    k.detail = "f32 mfma 32x32 tile=128x128 bk=16" + orient;
+    out->kernels.push_back(k);
+    return true;
+  }
+  // bf16: the direct-to-LDS tiles (whole 256x256 blocks, K a positive
+  // multiple of 32, N % 8 == 0) on the 8-wave kernel, launched when there
+  // can be one; every other tile on the 256-thread register-staged kernel,
+  // skipped when every tile is a direct-to-LDS one (M, N multiples of 256,
+  // K a positive multiple of 32). Each kernel returns at once on the
+  // other's tiles.
+  const std::string M = g.dims[m.m].name, N = g.dims[m.n].name, K = g.dims[m.k].name;
+  o << "extern \"C\" __global__ void __launch_bounds__(512) " << symbol << "_w(\n    " << signature << ") {\n"
+    << epi.str() << "  tca::hip::gemm_bf16_256_w8<" << nk << ">" << args;
+  o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "(\n    " << signature << ") {\n"
+    << epi.str() << "  tca::hip::gemm_bf16_256<" << nk << ", decltype(epi), 1, true, true, false, true>" << args;
+  GemmKernel w;
+  w.suffix = "_w";
+  w.block = 512;
+  w.grid = grid;
+  w.when = {M + " 256 4294967295 1 0", N + " 256 4294967295 8 0", K + " 32 4294967295 32 0"};
+  w.detail = "bf16 mfma 32x32 tile=256x256 bk=32 8 waves (direct-to-LDS ring; whole tiles only)" + orient;
+  GemmKernel e;
+  e.grid = grid;
+  e.unless = {M + " 0 4294967295 256 0", N + " 0 4294967295 256 0", K + " 32 4294967295 32 0"};
+  e.detail = "bf16 mfma 32x32 tile=256x256 bk=64 4 waves (edge tiles, K % 32 != 0, N % 8 != 0)" + orient;
+  out->kernels.push_back(w);
+  out->kernels.push_back(e);
   return true;
 }
 
@@ -649,6 +680,7 @@ class Emitter {
     std::vector<std::string> grid;
     std::vector<std::string> args;
     std::vector<std::string> when;  // launch guards: "<dim> <lo> <hi> <mod> <rem>"
+    std::vector<std::string> unless;  // skip guards: the kernel is skipped when all of them hold
     std::string pack;               // packed row kernel: "<dim> <epl> <min block>"
     std::string split;              // row-split reduction: "<dim> <rows-min> <blocks> <merge> <n> <terms>"
   };
@@ -2962,10 +2994,16 @@ class Emitter {
     const std::string sig = Signature(single, &pk);
     GemmEmitted ge;
     if (!EmitGemm(g_, c, m, pk.symbol, sig, &counter_, &src_, &ge, err)) return false;
-    pk.block = ge.block;
-    pk.lds = ge.lds;
-    pk.grid = ge.grid;
-    AddKernel(pk, Family::Gemm, n.chains, ge.detail);
+    for (const auto& gk : ge.kernels) {
+      PlanKernel k = pk;
+      k.symbol = pk.symbol + gk.suffix;
+      k.block = gk.block;
+      k.lds = gk.lds;
+      k.grid = gk.grid;
+      k.when = gk.when;
+      k.unless = gk.unless;
+      AddKernel(k, Family::Gemm, n.chains, gk.detail);
+    }
     return true;
   }
 
@@ -3004,6 +3042,7 @@ class Emitter {
       if (!k.pack.empty()) p << "pack " << k.pack << "\n";
       if (!k.split.empty()) p << "split " << k.split << "\n";
       for (const auto& w : k.when) p << "when " << w << "\n";
+      for (const auto& w : k.unless) p << "unless " << w << "\n";
     }
     p << "end\n";
     return p.str();

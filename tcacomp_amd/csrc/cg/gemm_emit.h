@@ -30,10 +30,16 @@ struct GemmMatch {
   ir::Elem in = ir::Elem::F32;
 };
 
-struct GemmEmitted {
+// One kernel of a contraction: its symbol is the nest's symbol + suffix.
+struct GemmKernel {
+  std::string suffix;
   uint32_t block = 256, lds = 0;
-  std::vector<std::string> grid;
+  std::vector<std::string> grid, when, unless;
   std::string detail;
+};
+
+struct GemmEmitted {
+  std::vector<GemmKernel> kernels;
 };
 
 bool MatchGemm(const ir::Graph& g, const ir::Chain& c, GemmMatch* m);

@@ -299,7 +299,16 @@ __device__ __forceinline__ void gemm_bf16_256_dma(const uint16_t* __restrict__ A
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));  // nothing in flight past the loop
 }
 
-template <bool B_NK, typename Epi, int SWZ = 1, bool SPREAD = true, bool PREFETCH = true, bool DMA = true>
+// The tiles the direct-to-LDS path takes: the whole 256x256 block in range,
+// K a positive multiple of 32 and [K][N] / [N][K] rows 16-byte aligned.
+__device__ __forceinline__ bool gemm_bf16_dma_tile(uint32_t m0, uint32_t n0, uint32_t M, uint32_t N, uint32_t K) {
+  return m0 + 256u <= M && n0 + 256u <= N && K % 32u == 0u && N % 8u == 0u && K > 0u;
+}
+
+// SKIP_DMA: the direct-to-LDS tiles belong to another kernel
+// (gemm_bf16_256_w8); this one returns at once on them.
+template <bool B_NK, typename Epi, int SWZ = 1, bool SPREAD = true, bool PREFETCH = true, bool DMA = true,
+          bool SKIP_DMA = false>
 __device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
                                               float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
   constexpr uint32_t BM = 256, BN = 256, BK = 64, TILE = BM * BK;
@@ -308,7 +317,8 @@ __device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, cons
   uint32_t tm, tn;
   gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
   const uint32_t m0 = tm * BM, n0 = tn * BN;
-  const bool dma_tile = DMA && m0 + BM <= M && n0 + BN <= N && K % 32u == 0u && N % 8u == 0u && K > 0u;
+  if (SKIP_DMA && gemm_bf16_dma_tile(m0, n0, M, N, K)) return;
+  const bool dma_tile = DMA && gemm_bf16_dma_tile(m0, n0, M, N, K);
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wm = (wave >> 1) * 128u, wn = (wave & 1u) * 128u;
   const bool vec_a = (K % 8u) == 0u;
@@ -540,6 +550,192 @@ __device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, cons
       for (int e = 0; e < 16; ++e) {
         const uint32_t m = mr + 32u * i, n = nc + 32u * j + 8u * (e >> 2) + (e & 3);
         if (m < M && n < N) C[static_cast<uint64_t>(m) * N + n] = epi(acc[i][j][e], m, n);
+      }
+}
+
+// -------------------------------------------- bf16 path, 8 waves per tile
+// The direct-to-LDS tiles with 8 waves (512 threads, 2 per SIMD) on the
+// same 256x256 tile, each wave 128x64 (4x2 MFMA blocks, 128 accumulators,
+// so two waves fit a SIMD's registers): while one wave of a SIMD waits on a
+// fragment read, the slice barrier or its loads, the other issues MFMAs. The
+// ring, the LDS layout and the per-step order are gemm_bf16_256_dma's with
+// half the fragments and loads per wave (4 A and 2 B fragments, 4 slice
+// loads per wave and slice). Measured at 4096^2 x 16384 (interleaved, one
+// box): 1226-1308 TFLOP/s against 1144-1176 for the 4-wave loop; at 4096^3
+// 2-3% faster (the C epilogue and the ring's fill do not shrink); a 5-stage
+// ring (160 KiB) and the loop without sched_barrier fences were slower.
+// Every other tile returns at once: gemm_bf16_256 with SKIP_DMA takes them.
+template <bool B_NK, typename Epi>
+__device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
+                                                 float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
+  constexpr uint32_t BM = 256, BN = 256, BK = 32, STAGES = 4, SLICE = 256u * BK;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[STAGES * 2 * SLICE];
+  const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  uint32_t tm, tn;
+  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
+  if (!gemm_bf16_dma_tile(m0, n0, M, N, K)) return;  // gemm_bf16_256<..., SKIP_DMA> takes it
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t wm = (wave >> 2) * 128u, wn = (wave & 3u) * 64u;
+  const uint16_t* __restrict__ A16 = reinterpret_cast<const uint16_t*>(A);
+  const uint16_t* __restrict__ B16 = reinterpret_cast<const uint16_t*>(B);
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  // Per-lane element offsets of the 2 chunks (of 16) this wave fills per
+  // slice and operand: chunk ch = 2*wave + q covers LDS slots 64ch .. +63.
+  uint32_t offa[2], offb[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const uint32_t slot = (wave * 2u + q) * 64u + lane;
+    const uint32_t r = slot >> 2, c = (slot & 3u) ^ ((r >> 2) & 3u);
+    offa[q] = r * K + c * 8u;
+    if constexpr (B_NK) {
+      offb[q] = r * K + c * 8u;
+    } else {
+      const uint32_t k = slot >> 5, sp = slot & 31u;
+      offb[q] = k * N + ((sp ^ ((k & 3u) << 2)) << 3);
+    }
+  }
+  uint16_t* ldsp = lds;
+  auto a_slice = [&](uint32_t s) { return ldsp + s * 2u * SLICE; };
+  auto b_slice = [&](uint32_t s) { return ldsp + s * 2u * SLICE + SLICE; };
+  auto issue = [&](uint32_t s, uint32_t k0) {
+    const uint16_t* a0 = A16 + static_cast<uint64_t>(m0) * K + k0;
+    const uint16_t* b0 = B_NK ? B16 + static_cast<uint64_t>(n0) * K + k0 : B16 + static_cast<uint64_t>(k0) * N + n0;
+    uint16_t* as = a_slice(s);
+    uint16_t* bs = b_slice(s);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t ch = wave * 2u + q;
+      __builtin_amdgcn_global_load_lds(a0 + offa[q], (lds_void*)(as + ch * 512u), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(b0 + offb[q], (lds_void*)(bs + ch * 512u), 16, 0, 0);
+    }
+  };
+  bf16x8 fa[4], fb[2];
+  auto load_frags = [&](uint32_t s, uint32_t ks) {
+    const uint16_t* As = a_slice(s);
+    const uint16_t* Bs = b_slice(s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[i] = *reinterpret_cast<const bf16x8*>(&As[swz32(wm + i * 32u + (lane & 31u), ks * 2u + (lane >> 5))]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if constexpr (B_NK)
+        fb[j] = *reinterpret_cast<const bf16x8*>(&Bs[swz32(wn + j * 32u + (lane & 31u), ks * 2u + (lane >> 5))]);
+      else
+        fb[j] = frag_b_tr(Bs, wn + j * 32u, ks * 16u, lane);
+    }
+  };
+  auto step = [&](uint32_t next_s, uint32_t next_ks, bool dma, uint32_t dma_s, uint32_t dma_k0) {
+    bf16x8 ga[4], gb[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ga[i] = fa[i];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) gb[j] = fb[j];
+    const uint16_t* As = a_slice(next_s);
+    const uint16_t* Bs = b_slice(next_s);
+    auto mf = [&](int i, int j) {
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gb[j], ga[i], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto rd_a = [&](int i) {
+      fa[i] = *reinterpret_cast<const bf16x8*>(&As[swz32(wm + i * 32u + (lane & 31u), next_ks * 2u + (lane >> 5))]);
+    };
+    auto rd_b = [&](int j) {
+      if constexpr (B_NK)
+        fb[j] = *reinterpret_cast<const bf16x8*>(&Bs[swz32(wn + j * 32u + (lane & 31u), next_ks * 2u + (lane >> 5))]);
+      else
+        fb[j] = frag_b_tr(Bs, wn + j * 32u, next_ks * 16u, lane);
+    };
+    const uint16_t* a0 = A16 + static_cast<uint64_t>(m0) * K + dma_k0;
+    const uint16_t* b0 = B_NK ? B16 + static_cast<uint64_t>(n0) * K + dma_k0 : B16 + static_cast<uint64_t>(dma_k0) * N + n0;
+    uint16_t* as = a_slice(dma_s);
+    uint16_t* bs = b_slice(dma_s);
+    auto dm = [&](int q) {
+      const uint32_t ch = wave * 2u + (q >> 1);
+      if (q & 1) __builtin_amdgcn_global_load_lds(b0 + offb[q >> 1], (lds_void*)(bs + ch * 512u), 16, 0, 0);
+      else __builtin_amdgcn_global_load_lds(a0 + offa[q >> 1], (lds_void*)(as + ch * 512u), 16, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto fence = []() { __builtin_amdgcn_sched_barrier(0); };
+    // MFMAs j-major; the next step's 6 fragment reads after the first four;
+    // when `dma`, the slice's 4 direct-to-LDS loads, two per MFMA.
+    fence();
+    mf(0, 0);
+    rd_a(0); rd_a(1); fence();
+    mf(1, 0);
+    rd_a(2); rd_a(3); fence();
+    mf(2, 0);
+    rd_b(0); fence();
+    mf(3, 0);
+    rd_b(1); fence();
+    if (dma) {
+      mf(0, 1); dm(0); dm(1);
+      mf(1, 1); dm(2); dm(3);
+    } else {
+      mf(0, 1); mf(1, 1);
+    }
+    mf(2, 1); mf(3, 1);
+  };
+  // As gemm_bf16_256_dma: the barrier waits for the slice about to be read
+  // (4 loads per slice and lane here) and leaves the step's own fragment
+  // reads (kReads) in flight.
+  constexpr int kReads = B_NK ? 6 : 8;
+  constexpr int kWaitNext = waitcnt_imm(4, kReads), kWaitLast = waitcnt_imm(0, kReads);
+  auto barrier = [&]() {
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  const uint32_t nk = K / BK;
+  const uint32_t pre = nk < STAGES - 1 ? nk : STAGES - 1;
+  for (uint32_t s = 0; s < pre; ++s) issue(s, s * BK);
+  asm volatile("" ::: "memory");
+  // Slice 0 landed: the pre - 1 newer slices (4 loads each) may stay in flight.
+  if (pre >= 3u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
+  else if (pre == 2u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
+  else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+  barrier();
+  load_frags(0, 0);
+  const uint32_t main_end = nk > STAGES - 1 ? nk - (STAGES - 1) : 0u;
+  for (uint32_t kt = 0; kt < main_end; ++kt) {
+    step(kt % STAGES, 1, false, 0, 0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kWaitNext);
+    barrier();
+    step((kt + 1) % STAGES, 0, true, (kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
+  }
+  for (uint32_t kt = main_end; kt < nk; ++kt) {
+    step(kt % STAGES, 1, false, 0, 0);
+    if (kt + 1 < nk) {
+      asm volatile("" ::: "memory");
+      if (kt + 2 < nk) __builtin_amdgcn_s_waitcnt(kWaitNext);
+      else __builtin_amdgcn_s_waitcnt(kWaitLast);
+      barrier();
+    }
+    // On the last iteration this reads a stale buffer whose values are unused.
+    step((kt + 1) % STAGES, 0, false, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));  // nothing in flight past the loop
+  // acc[i][j][4g + q] = C[m][n + q], m = m0 + wm + 32i + lane%32, n = n0 + wn + 32j + 8g + 4*(lane/32).
+  const uint32_t mr = m0 + wm + (lane & 31u), nc = n0 + wn + 4u * (lane >> 5);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t m = mr + 32u * i, n = nc + 32u * j + 8u * g;
+        float4 v;
+        v.x = epi(acc[i][j][4 * g + 0], m, n + 0);
+        v.y = epi(acc[i][j][4 * g + 1], m, n + 1);
+        v.z = epi(acc[i][j][4 * g + 2], m, n + 2);
+        v.w = epi(acc[i][j][4 * g + 3], m, n + 3);
+        *reinterpret_cast<float4*>(C + static_cast<uint64_t>(m) * N + n) = v;
       }
 }
 

@@ -243,16 +243,16 @@ bool Parse(const std::string& text, Plan* out, std::string* err) {
         if (t.packed) return bad("a split term cannot divide by 'pack'");
         k.split_terms.push_back(t);
       }
-    } else if (kw == "when") {
-      if (p.kernels.empty()) return bad("when before any kernel");
+    } else if (kw == "when" || kw == "unless") {
+      if (p.kernels.empty()) return bad(kw + " before any kernel");
       Guard g;
       if (tok.size() != 6 || !ParseU64(tok[2], &g.lo) || !ParseU64(tok[3], &g.hi) || !ParseU64(tok[4], &g.mod) ||
           !ParseU64(tok[5], &g.rem))
-        return bad("when <dim> <lo> <hi> <mod> <rem>");
+        return bad(kw + " <dim> <lo> <hi> <mod> <rem>");
       g.dim = FindDim(p, tok[1]);
-      if (g.dim < 0) return bad("when names unknown dim " + tok[1]);
+      if (g.dim < 0) return bad(kw + " names unknown dim " + tok[1]);
       if (g.mod == 0 || g.rem >= g.mod || g.lo > g.hi) return bad("bad guard on " + tok[1]);
-      p.kernels.back().when.push_back(g);
+      (kw == "when" ? p.kernels.back().when : p.kernels.back().unless).push_back(g);
     } else if (kw == "end") {
       ended = true;
     } else {
@@ -345,6 +345,8 @@ std::string Serialize(const Plan& p) {
     }
     for (const auto& g : k.when)
       o << "when " << p.dims[g.dim].name << " " << g.lo << " " << g.hi << " " << g.mod << " " << g.rem << "\n";
+    for (const auto& g : k.unless)
+      o << "unless " << p.dims[g.dim].name << " " << g.lo << " " << g.hi << " " << g.mod << " " << g.rem << "\n";
   }
   o << "end\n";
   return o.str();
@@ -506,11 +508,16 @@ uint32_t PackRows(const Kernel& k, const std::vector<uint32_t>& dims, uint32_t* 
 }
 
 bool Selected(const Kernel& k, const std::vector<uint32_t>& dims) {
-  for (const auto& g : k.when) {
+  auto holds = [&](const Guard& g) {
     const uint64_t v = dims[g.dim];
-    if (v < g.lo || v > g.hi || v % g.mod != g.rem) return false;
-  }
-  return true;
+    return v >= g.lo && v <= g.hi && v % g.mod == g.rem;
+  };
+  for (const auto& g : k.when)
+    if (!holds(g)) return false;
+  if (k.unless.empty()) return true;
+  for (const auto& g : k.unless)
+    if (!holds(g)) return true;
+  return false;  // every unless guard holds
 }
 
 bool PackArgs(const Kernel& k, const Plan& p, const std::vector<void*>& ptrs, const std::vector<uint32_t>& dims,

@@ -29,6 +29,9 @@
 //       when lo <= dim <= hi and dim % mod == rem; every guard of a kernel must
 //       hold. Variants of one nest specialised on a run-time dim carry guards
 //       that partition its values, so exactly one of them launches.
+//   unless <dim> <lo> <hi> <mod> <rem>  (for the last kernel) the same test; the
+//       kernel is skipped when every one of its unless guards holds (the
+//       complement of a conjunction of when guards another kernel carries).
 //   end
 //
 // The shape contract Bind() enforces is the reference launcher's
@@ -94,6 +97,7 @@ struct Kernel {
   std::vector<Term> grid;
   std::vector<Arg> args;
   std::vector<Guard> when;
+  std::vector<Guard> unless;  // skipped when all of these hold
   int pack_dim = -1;  // >= 0: a packed row kernel (block chosen at launch)
   uint64_t pack_epl = 0, pack_min_block = 0;
   int split_dim = -1;  // >= 0: a row-split reduction (see the split record)

@@ -246,6 +246,53 @@ def test_chain_segment_static_drops_the_local():
     assert "seg" not in e2.families() and "__chain" in e2.plan
 
 
+@pytest.mark.parametrize("M,N,K,want", [
+    (4096, 4096, 4096, ["_w"]),      # every tile whole, K % 32 == 0: the 8-wave kernel alone
+    (4096, 4096, 4128, ["_w"]),
+    (4100, 4096, 4096, ["_w", ""]),  # a partial bottom row of tiles: both, each skipping the other's tiles
+    (4096, 4104, 4096, ["_w", ""]),
+    (4096, 4096, 4100, [""]),        # K % 32 != 0: no tile takes the direct-to-LDS path
+    (4096, 4100, 4096, [""]),        # N % 8 != 0: [K][N] rows not 16-byte aligned, no direct-to-LDS tile
+    (255, 4096, 4096, [""]), (512, 512, 0, [""]), (512, 512, 16, [""])])
+def test_bf16_gemm_kernel_selection(M, N, K, want):
+    """The bf16 contraction's two kernels: the 8-wave direct-to-LDS kernel
+    runs when a whole tile can take it, the register-staged one unless every
+    tile does (plan `unless` guards)."""
+    e = programs.CONFIG_PROGRAMS["gemm_bf16"]().emit()
+    rc, h = parse(e.plan)
+    assert rc == 0, _lib.last_error()
+    arr = compiler._descriptors([TensorDesc(0x1000, (M, K), 2), TensorDesc(0x1000, (K, N), 2),
+                                 TensorDesc(0x1000, (M, N), 0)])
+    syms = e.kernel_symbols()
+    out = (ctypes.c_uint8 * len(syms))()
+    grids = (ctypes.c_uint64 * len(syms))()
+    assert _lib.lib().tca_program_selected(h, arr, 3, None, 0, out, grids, None, len(syms)) == 0, _lib.last_error()
+    sel = [s[len("tca_gemm_bf16_k0"):] for s, f, g in zip(syms, out, grids) if f and g]
+    assert sel == want, (M, N, K, sel)
+
+
+def test_unless_guard_parse():
+    for rec, ok in [("unless M 0 16 4 0", True), ("unless M 0 16 0 0", False), ("unless Q 0 16 4 0", False),
+                    ("unless M 0 16", False)]:
+        rc, _ = parse(PLAN.replace("arg scalar a\n", "arg scalar a\n%s\n" % rec))
+        assert (rc == 0) == ok, (rec, _lib.last_error())
+    # skipped only when every unless guard holds
+    rc, h = parse(PLAN.replace("arg scalar a\n", "arg scalar a\nunless M 0 16 1 0\nunless N 0 8 4 0\n"))
+    assert rc == 0, _lib.last_error()
+
+    def selected(m, n):
+        ts = [TensorDesc(0x1000, (m, n, 4), 0), TensorDesc(0x1000, (n,), 0), TensorDesc(0x1000, (m, n), 0)]
+        arr = compiler._descriptors(ts)
+        fd = (ctypes.c_uint32 * 1)(3)
+        o = (ctypes.c_uint8 * 1)()
+        assert _lib.lib().tca_program_selected(h, arr, 3, fd, 1, o, None, None, 1) == 0, _lib.last_error()
+        return o[0]
+    assert selected(5, 8) == 0  # both hold: skipped
+    assert selected(5, 6) == 1  # N % 4 != 0
+    assert selected(20, 8) == 1  # M > 16
+    assert selected(20, 6) == 1
+
+
 def test_split_record_parse():
     for rec, ok in [("split M 64 2048 0 1 N/256", True), ("split M 64 2048 1 2 1/1 N/4", True),
                     ("split Q 64 2048 0 1 N/256", False), ("split M 0 2048 0 1 N/256", False),
@@ -438,8 +485,8 @@ def test_program_launch_without_module_is_refused():
 
 
 EXPECTED_FAMILIES = {
-    "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"],
-    "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"], "gemm_bf16": ["gemm"],
+    "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"] * 2,
+    "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"], "gemm_bf16": ["gemm"] * 2,
     "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 12, "softmax_dyn": ["stream"] * 6,
     "layernorm_dyn": ["stream"] * 6, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 6,
     # narrow rows: one more width per halving of the element size (8 bf16, 16 u8 elements per vector)
