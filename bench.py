@@ -286,13 +286,20 @@ def _cpu_baseline(key, args, threads):
     return 2 * rows * 4096 * 4096 / dt / 1e12, "TFLOP/s", "%d of 4096 rows" % rows
 
 
-def _traffic(symbol, prog):
+# Configurations whose kernel is profiled (in profiles/traffic.json) at
+# another configuration's shape: their counter bytes are not theirs.
+TRAFFIC_OTHER_SHAPE = {"c5b8": "c5b"}
+
+
+def _traffic(symbol, prog, key=None):
     """HBM bytes per launch of `symbol` from profiles/traffic.json (rocprof
     FETCH_SIZE + WRITE_SIZE, calibration-scaled), with where they come from.
     The file records the code-object key (a hash of the emitted source, the
     hipcc flags and the device headers) each figure was profiled with; when
     the kernel launched here has another key the figure is stale and is not
     reported."""
+    if key in TRAFFIC_OTHER_SHAPE:
+        return None, "profiled at %s's shape only" % TRAFFIC_OTHER_SHAPE[key]
     p = os.path.join(REPO, "profiles", "traffic.json")
     if not os.path.exists(p):
         return None, "no profiles/traffic.json"
@@ -396,7 +403,7 @@ def main():
                  "host_wall_ms": wall_ms}
         if work["bound"] == "hbm":
             gbs = work["bytes"] / (ms * 1e-3) / 1e9
-            traffic, source = _traffic(sym, prog)
+            traffic, source = _traffic(sym, prog, key)
             entry["roofline"] = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                  "frac": gbs / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": source}
             entry["algorithmic_bytes"] = work["bytes"]
@@ -405,7 +412,7 @@ def main():
         else:
             tf = work["flops"] / (ms * 1e-3) / 1e12
             peak = MFMA_PEAK_TFLOPS[work["dtype"]]
-            traffic, source = _traffic(sym, prog)
+            traffic, source = _traffic(sym, prog, key)
             entry["roofline"] = {"bound": "mfma", "achieved": tf, "peak": peak, "unit": "TFLOP/s",
                                  "frac": tf / peak, "traffic": traffic, "traffic_source": source}
             entry["algorithmic_flops"] = work["flops"]
