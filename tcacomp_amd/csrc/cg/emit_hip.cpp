@@ -302,7 +302,7 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   const std::vector<std::string> grid = {g.dims[m.m].name + "/" + std::to_string(tile),
                                          g.dims[m.n].name + "/" + std::to_string(tile)};
   const std::string orient = m.b_nk ? " B=[n][k]" : " B=[k][n]";
-  o << "// contraction over @" << g.dims[m.k].name << " on MFMA (" << (bf16 ? "bf16 32x32x16" : "f32 32x32x2")
+  o << "// contraction over @" << g.dims[m.k].name << " on MFMA (" << (bf16 ? "bf16 16x16x32 whole tiles, 32x32x16 edges" : "f32 32x32x2")
     << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << ", " << tile << "x" << tile << " tiles\n";
   if (!bf16) {
     o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "(\n    " << signature << ") {\n"
@@ -323,13 +323,13 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   o << "extern \"C\" __global__ void __launch_bounds__(512) " << symbol << "_w(\n    " << signature << ") {\n"
     << epi.str() << "  tca::hip::gemm_bf16_256_w8<" << nk << ">" << args;
   o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "(\n    " << signature << ") {\n"
-    << epi.str() << "  tca::hip::gemm_bf16_256<" << nk << ", decltype(epi), 1, true, true, false, true>" << args;
+    << epi.str() << "  tca::hip::gemm_bf16_256<" << nk << ", decltype(epi), 1, true, true, true>" << args;
   GemmKernel w;
   w.suffix = "_w";
   w.block = 512;
   w.grid = grid;
   w.when = {M + " 256 4294967295 1 0", N + " 256 4294967295 8 0", K + " 32 4294967295 32 0"};
-  w.detail = "bf16 mfma 32x32 tile=256x256 bk=32 8 waves (direct-to-LDS ring; whole tiles only)" + orient;
+  w.detail = "bf16 mfma 16x16x32 tile=256x256 bk=32 8 waves (direct-to-LDS ring; whole tiles only)" + orient;
   GemmKernel e;
   e.grid = grid;
   e.unless = {M + " 0 4294967295 256 0", N + " 0 4294967295 256 0", K + " 32 4294967295 32 0"};

@@ -4,10 +4,13 @@
 // WarpReducer collective per output element (a shuffle tree per Reduce and
 // two barriers per Combine; .planning/quick/261030-uai-.../after-cu/gemm.cu:
 // 59-90). Here the contraction runs on MFMA:
-//   bf16 inputs : v_mfma_f32_32x32x16_bf16 (gfx950), fp32 accumulate
+//   bf16 inputs : v_mfma_f32_16x16x32_bf16 (gfx950) on whole 256x256 tiles
+//                 (gemm_bf16_256_w8), v_mfma_f32_32x32x16_bf16 on the edge
+//                 tiles (gemm_bf16_256); fp32 accumulate
 //   fp32 inputs : v_mfma_f32_32x32x2f32, fp32 accumulate
-// Geometry: a 256-thread workgroup (4 waves, 2x2) owns a BMxBN tile of C,
-// each wave a (BM/2)x(BN/2) sub-tile of 32x32 MFMA blocks. K advances in
+// Geometry of the register-staged kernels: a 256-thread workgroup (4 waves,
+// 2x2) owns a BMxBN tile of C, each wave a (BM/2)x(BN/2) sub-tile of 32x32
+// MFMA blocks. K advances in
 // BK slices staged through LDS; the next slice's global loads are issued
 // before the current slice's MFMAs so HBM latency hides under the math.
 // LDS tiles hold every MFMA operand K-contiguous for its row/column (A as
@@ -24,6 +27,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 namespace tca {
 namespace hip {
@@ -56,18 +61,16 @@ __device__ __forceinline__ void gemm_tile_coords(uint32_t tiles_m, uint32_t tile
 // blocks (256 fp32 accumulators per lane). Per 16-deep K step a wave reads
 // 4 A + 4 B fragments (8 x 1 KiB of LDS) for 16 MFMAs.
 //
-// LDS layout: each [256][64] bf16 tile is unpadded (128-byte rows). A
-// 128-bit LDS access is served 16 lanes at a time across 64 four-byte banks
-// (256 bytes), i.e. two rows' worth; a 16-byte slot is (row parity, column
-// group). Logical row r is stored at physical row p = r ^ ((r / 8) % 2) and
-// its column group c at c ^ ((p / 2) % 8):
+// LDS layout: each [256][64] bf16 tile is unpadded (128-byte rows) over 64
+// four-byte banks (256 bytes, two rows' worth; a 16-byte slot is (row
+// parity, column group)). Logical row r is stored at physical row
+// p = r ^ ((r / 8) % 2) and its column group c at c ^ ((p / 2) % 8):
 //     element (r, k) -> p*64 + ((k/8) ^ ((p/2) % 8))*8 + k%8.
-// Then every 16-lane phase hits 16 distinct slots for all three access
-// patterns: fragment reads (16 consecutive rows, one column group), row
-// writes (8 lanes on one row's 8 groups, 8 lanes on the next row) and the
-// transposed B writes (8 lanes on one row, 8 on the row 8 further down,
-// whose parity the row permutation flips). Two such tile pairs (A, B)
-// double-buffer the K loop with one barrier per step: 128 KiB of LDS.
+// A fragment read (32 consecutive rows, one column group per half-wave)
+// then hits 16 distinct slots in each 16-lane cycle of a 128-bit read (the
+// cycles measured on gfx950 are described at gemm_bf16_256_w8). Two such
+// tile pairs (A, B) double-buffer the K loop with one barrier per step:
+// 128 KiB of LDS.
 // SWZ = 0 keeps the plain row-XOR swizzle (c ^ (r % 8)), optimal for a
 // 32-bank / 8-lane-phase LDS; SWZ = 1 is the layout above.
 template <int SWZ>
@@ -83,221 +86,9 @@ __device__ __forceinline__ uint32_t swz64(uint32_t row, uint32_t cg) {
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-// [K][N] B slice in LDS, 64 rows of 256 bf16 (512 bytes), 16-byte slots
-// XOR-swizzled by the row: element (k, n) -> k*256 + ((n/8) ^ 4*(k%4))*8 + n%8.
-// The XOR constant is even, so the two slots a transposing read covers stay
-// adjacent, and four consecutive rows land in four distinct 64-byte bank
-// groups (with the neighbouring 16 columns filling the other four).
-__device__ __forceinline__ uint32_t swz_kn(uint32_t k, uint32_t n) {
-  return k * 256u + ((((n >> 3) ^ ((k & 3u) << 2))) << 3) + (n & 7u);
-}
-
-// MFMA B operand (32 columns x 16 k) from a [K][N] LDS slice with the gfx950
-// transposing read ds_read_b64_tr_b16. Within each 16-lane group, lane j
-// points at four consecutive values R_j of one k row, and lane i receives
-// [R_{i/4}[i%4], R_{4+i/4}[i%4], R_{8+i/4}[i%4], R_{12+i/4}[i%4]]. With
-// lane j addressing row kb + j/4, columns nb + 4(j%4), lane i gets
-// B[kb + e][nb + i] for e = 0..3; a second read at kb + 4 completes the
-// lane's 8 k values. Group g of the wave covers columns 16(g%2) and k half
-// g/2, matching the MFMA B layout (column l%32, k 8(l/32)..+8).
-__device__ __forceinline__ bf16x8 frag_b_tr(const uint16_t* Bs, uint32_t n_col0, uint32_t k0, uint32_t lane) {
-  const uint32_t g = lane >> 4, j = lane & 15u;
-  const uint32_t nb = n_col0 + 16u * (g & 1u), kb = k0 + 8u * (g >> 1);
-  const uint32_t k = kb + (j >> 2), n = nb + 4u * (j & 3u);
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) i16x4*)(Bs + swz_kn(k, n)));
-  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) i16x4*)(Bs + swz_kn(k + 4u, n)));
-  typedef short i16x8 __attribute__((ext_vector_type(8)));
-  const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(bf16x8, v);
-}
-
-// Interior 256x256 tile with K % 32 == 0 and 16-byte aligned rows: both
-// operand slices go HBM -> LDS with global_load_lds_dwordx4 (lane i of an
-// instruction fills bytes [16i, 16i+16) of a 1 KiB LDS chunk, from any
-// global address), so there is no register staging, no ds_write and no
-// register transpose. K advances in 32-deep slices through a 4-stage ring
-// (4 x 32 KiB): three slices are in flight while one is multiplied, with
-// one vmcnt wait and one barrier per slice.
-//
-// [rows][32] operand slices (A, and B given as [n][k]) use 64-byte rows,
-// 16-byte column groups swizzled by c ^ ((r / 4) % 4): a fragment read (16
-// consecutive rows, one group) then covers the 16 slots of a 256-byte bank
-// window. The [K][N] B slice uses swz_kn.
 // s_waitcnt immediate for gfx9: vmcnt[3:0] | expcnt[6:4] (7 = no wait) |
 // lgkmcnt[11:8] | vmcnt[5:4] at [15:14].
 constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | (7 << 4) | ((lgkm & 15) << 8) | ((vm >> 4) << 14); }
-
-__device__ __forceinline__ uint32_t swz32(uint32_t row, uint32_t cg) { return row * 32u + ((cg ^ ((row >> 2) & 3u)) << 3); }
-
-template <bool B_NK>
-__device__ __forceinline__ void gemm_bf16_256_dma(const uint16_t* __restrict__ A16, const uint16_t* __restrict__ B16,
-                                                  uint32_t N, uint32_t K, uint32_t m0, uint32_t n0, uint16_t* lds,
-                                                  f32x16 (&acc)[4][4]) {
-  constexpr uint32_t BK = 32, STAGES = 4, SLICE = 256u * BK;  // elements per operand slice
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t wm = (wave >> 1) * 128u, wn = (wave & 1u) * 128u;
-  // Per-lane element offsets of the 4 chunks (of 16) this wave fills per
-  // slice and operand: chunk ch = 4*wave + q covers LDS slots 64ch .. +63.
-  uint32_t offa[4], offb[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint32_t slot = (wave * 4u + q) * 64u + lane;
-    const uint32_t r = slot >> 2, c = (slot & 3u) ^ ((r >> 2) & 3u);  // inverse of swz32
-    offa[q] = r * K + c * 8u;
-    if constexpr (B_NK) {
-      offb[q] = r * K + c * 8u;
-    } else {
-      const uint32_t k = slot >> 5, sp = slot & 31u;  // [32][256]: 32 slots per row
-      offb[q] = k * N + ((sp ^ ((k & 3u) << 2)) << 3);
-    }
-  }
-  auto a_slice = [&](uint32_t s) { return lds + s * 2u * SLICE; };
-  auto b_slice = [&](uint32_t s) { return lds + s * 2u * SLICE + SLICE; };
-  auto issue = [&](uint32_t s, uint32_t k0) {
-    const uint16_t* a0 = A16 + static_cast<uint64_t>(m0) * K + k0;
-    const uint16_t* b0 = B_NK ? B16 + static_cast<uint64_t>(n0) * K + k0 : B16 + static_cast<uint64_t>(k0) * N + n0;
-    uint16_t* as = a_slice(s);
-    uint16_t* bs = b_slice(s);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t ch = wave * 4u + q;
-      __builtin_amdgcn_global_load_lds(a0 + offa[q], (lds_void*)(as + ch * 512u), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(b0 + offb[q], (lds_void*)(bs + ch * 512u), 16, 0, 0);
-    }
-  };
-  bf16x8 fa[4], fb[4];
-  auto load_frags = [&](uint32_t s, uint32_t ks) {
-    const uint16_t* As = a_slice(s);
-    const uint16_t* Bs = b_slice(s);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      fa[i] = *reinterpret_cast<const bf16x8*>(&As[swz32(wm + i * 32u + (lane & 31u), ks * 2u + (lane >> 5))]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if constexpr (B_NK)
-        fb[j] = *reinterpret_cast<const bf16x8*>(&Bs[swz32(wn + j * 32u + (lane & 31u), ks * 2u + (lane >> 5))]);
-      else
-        fb[j] = frag_b_tr(Bs, wn + j * 32u, ks * 16u, lane);
-    }
-  };
-  // One 16-deep step, issued in a fixed order (each group fenced with
-  // sched_barrier; left to itself the scheduler sank the next step's reads
-  // behind the MFMAs and every step then waited on LDS latency):
-  //   MFMAs on the fragments in hand, j-major, so the B fragment read last in
-  //   the previous step is used last;
-  //   the next step's 12 (8 for [N][K] B) fragment reads, two per MFMA,
-  //   right after the first MFMA: they have the rest of the step to land;
-  //   when `dma`, the slice's 8 direct-to-LDS loads, two per MFMA.
-  auto step = [&](uint32_t next_s, uint32_t next_ks, bool dma, uint32_t dma_s, uint32_t dma_k0) {
-    bf16x8 ga[4], gb[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ga[i] = fa[i];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) gb[j] = fb[j];
-    const uint16_t* As = a_slice(next_s);
-    const uint16_t* Bs = b_slice(next_s);
-    auto mf = [&](int i, int j) {
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gb[j], ga[i], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    };
-    auto rd_a = [&](int i) {
-      fa[i] = *reinterpret_cast<const bf16x8*>(&As[swz32(wm + i * 32u + (lane & 31u), next_ks * 2u + (lane >> 5))]);
-    };
-    auto rd_b = [&](int j) {
-      if constexpr (B_NK)
-        fb[j] = *reinterpret_cast<const bf16x8*>(&Bs[swz32(wn + j * 32u + (lane & 31u), next_ks * 2u + (lane >> 5))]);
-      else
-        fb[j] = frag_b_tr(Bs, wn + j * 32u, next_ks * 16u, lane);
-    };
-    const uint16_t* a0 = A16 + static_cast<uint64_t>(m0) * K + dma_k0;
-    const uint16_t* b0 = B_NK ? B16 + static_cast<uint64_t>(n0) * K + dma_k0 : B16 + static_cast<uint64_t>(dma_k0) * N + n0;
-    uint16_t* as = a_slice(dma_s);
-    uint16_t* bs = b_slice(dma_s);
-    auto dm = [&](int q) {  // load q/2 of A (q even) or of B (q odd)
-      const uint32_t ch = wave * 4u + (q >> 1);
-      if (q & 1) __builtin_amdgcn_global_load_lds(b0 + offb[q >> 1], (lds_void*)(bs + ch * 512u), 16, 0, 0);
-      else __builtin_amdgcn_global_load_lds(a0 + offa[q >> 1], (lds_void*)(as + ch * 512u), 16, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    };
-    auto fence = []() { __builtin_amdgcn_sched_barrier(0); };
-    fence();
-    mf(0, 0);
-    rd_a(0); rd_a(1); fence();
-    mf(1, 0);
-    rd_a(2); rd_a(3); fence();
-    mf(2, 0);
-    rd_b(0); fence();
-    mf(3, 0);
-    rd_b(1); fence();
-    mf(0, 1);
-    rd_b(2); fence();
-    mf(1, 1);
-    rd_b(3); fence();
-    if (dma) {
-      mf(2, 1); dm(0); dm(1);
-      mf(3, 1); dm(2); dm(3);
-      mf(0, 2); dm(4); dm(5);
-      mf(1, 2); dm(6); dm(7);
-    } else {
-      mf(2, 1); mf(3, 1); mf(0, 2); mf(1, 2);
-    }
-    mf(2, 2); mf(3, 2);
-    mf(0, 3); mf(1, 3); mf(2, 3); mf(3, 3);
-  };
-  // The barrier waits only for the slice about to be
-  // read (vmcnt counts in issue order, 8 loads per slice and lane); a plain
-  // __syncthreads() would drain every slice in flight. Its lgkmcnt leaves the
-  // step's own fragment reads (kReads per step) in flight but guarantees that
-  // the reads of the previous iteration, the last ones of the buffer the next
-  // DMA overwrites, have completed: LDS reads complete in order.
-  constexpr int kReads = B_NK ? 8 : 12;
-  constexpr int kWaitNext = waitcnt_imm(8, kReads), kWaitLast = waitcnt_imm(0, kReads);
-  auto barrier = [&]() {
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-  };
-
-  // Pipeline over 32-deep slices in a 4-buffer ring. Iteration kt:
-  //   step A: MFMAs of (kt, k 0-15) while reading the (kt, k 16-31) fragments;
-  //   barrier: slice kt+1 has landed and every wave is done with slice kt-1;
-  //   step B: MFMAs of (kt, k 16-31) while reading the (kt+1, k 0-15)
-  //           fragments and issuing slice kt+3 into kt-1's buffer.
-  // The main loop is branch-free (a branch around the reads or the DMA would
-  // pin the next slice's fragment reads ahead of step B's MFMAs and make them
-  // wait for those reads); the last three iterations, which issue nothing,
-  // are a separate tail.
-  const uint32_t nk = K / BK;
-  const uint32_t pre = nk < STAGES - 1 ? nk : STAGES - 1;
-  for (uint32_t s = 0; s < pre; ++s) issue(s, s * BK);
-  asm volatile("" ::: "memory");
-  if (pre >= 3u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 0));
-  else if (pre == 2u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
-  else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
-  barrier();
-  load_frags(0, 0);
-  const uint32_t main_end = nk > STAGES - 1 ? nk - (STAGES - 1) : 0u;
-  for (uint32_t kt = 0; kt < main_end; ++kt) {
-    step(kt % STAGES, 1, false, 0, 0);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(kWaitNext);
-    barrier();
-    step((kt + 1) % STAGES, 0, true, (kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
-  }
-  for (uint32_t kt = main_end; kt < nk; ++kt) {
-    step(kt % STAGES, 1, false, 0, 0);
-    if (kt + 1 < nk) {
-      asm volatile("" ::: "memory");
-      if (kt + 2 < nk) __builtin_amdgcn_s_waitcnt(kWaitNext);
-      else __builtin_amdgcn_s_waitcnt(kWaitLast);
-      barrier();
-    }
-    // On the last iteration this reads a stale buffer whose values are unused.
-    step((kt + 1) % STAGES, 0, false, 0, 0);
-  }
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));  // nothing in flight past the loop
-}
 
 // The tiles the direct-to-LDS path takes: the whole 256x256 block in range,
 // K a positive multiple of 32 and [K][N] / [N][K] rows 16-byte aligned.
@@ -307,8 +98,7 @@ __device__ __forceinline__ bool gemm_bf16_dma_tile(uint32_t m0, uint32_t n0, uin
 
 // SKIP_DMA: the direct-to-LDS tiles belong to another kernel
 // (gemm_bf16_256_w8); this one returns at once on them.
-template <bool B_NK, typename Epi, int SWZ = 1, bool SPREAD = true, bool PREFETCH = true, bool DMA = true,
-          bool SKIP_DMA = false>
+template <bool B_NK, typename Epi, int SWZ = 1, bool SPREAD = true, bool PREFETCH = true, bool SKIP_DMA = false>
 __device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
                                               float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
   constexpr uint32_t BM = 256, BN = 256, BK = 64, TILE = BM * BK;
@@ -318,7 +108,6 @@ __device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, cons
   gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
   const uint32_t m0 = tm * BM, n0 = tn * BN;
   if (SKIP_DMA && gemm_bf16_dma_tile(m0, n0, M, N, K)) return;
-  const bool dma_tile = DMA && gemm_bf16_dma_tile(m0, n0, M, N, K);
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wm = (wave >> 1) * 128u, wn = (wave & 1u) * 128u;
   const bool vec_a = (K % 8u) == 0u;
@@ -334,9 +123,6 @@ __device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, cons
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  if (dma_tile) {
-    gemm_bf16_256_dma<B_NK>(A16, B16, N, K, m0, n0, &lds[0][0][0], acc);
-  } else {
   u32x4 ra[8], rb[8];
   // Interior tiles (the whole BMxBN block in range, rows 16-byte aligned)
   // take unguarded vector loads addressed as a workgroup-uniform base plus a
@@ -521,7 +307,6 @@ __device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, cons
     }
     __syncthreads();
   }
-  }  // general path
   // acc[i][j][4g + q] = C[m][n + q] with m = m0 + wm + 32i + lane%32 and
   // n = n0 + wn + 32j + 8g + 4*(lane/32).
   const uint32_t mr = m0 + wm + (lane & 31u), nc = n0 + wn + 4u * (lane >> 5);
@@ -554,20 +339,71 @@ __device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, cons
 }
 
 // -------------------------------------------- bf16 path, 8 waves per tile
-// The direct-to-LDS tiles with 8 waves (512 threads, 2 per SIMD) on the
-// same 256x256 tile, each wave 128x64 (4x2 MFMA blocks, 128 accumulators,
-// so two waves fit a SIMD's registers): while one wave of a SIMD waits on a
-// fragment read, the slice barrier or its loads, the other issues MFMAs. The
-// ring, the LDS layout and the per-step order are gemm_bf16_256_dma's with
-// half the fragments and loads per wave (4 A and 2 B fragments, 4 slice
-// loads per wave and slice). Measured at 4096^2 x 16384 (interleaved, one
-// box): 1226-1308 TFLOP/s against 1144-1176 for the 4-wave loop; at 4096^3
-// 2-3% faster (the C epilogue and the ring's fill do not shrink); a 5-stage
-// ring (160 KiB) and the loop without sched_barrier fences were slower.
-// Every other tile returns at once: gemm_bf16_256 with SKIP_DMA takes them.
+// The direct-to-LDS tiles (gemm_bf16_dma_tile): 512 threads, 2 waves per
+// SIMD, each wave 128x64 of C as 8x4 blocks of v_mfma_f32_16x16x32_bf16
+// (32 accumulators of 4, 225 VGPRs, no scratch).
+//
+// Why 16x16x32: the part is power-limited under dense MFMA load. On random
+// bf16 operands an MFMA-only loop sustains 1.78 PFLOP/s with 32x32x16 (the
+// clock drops to 1.81 GHz) and 2.04 PFLOP/s with 16x16x32 (2.05 GHz): half
+// the accumulator traffic per flop. The operand bytes per flop, and so the
+// LDS traffic, are the same for both shapes.
+//
+// K advances in 32-deep slices through a 4-slice ring of A [256][32] and
+// [K][N] B [32][256] (or [N][K] B [256][32]) tiles, 32 KiB per slice,
+// filled by global_load_lds_dwordx4 (lane i of a load writes bytes
+// [16i, 16i + 16) of a 1 KiB LDS chunk, from any global address, so each
+// lane's global address is the inverse of the LDS swizzle). Each slice is
+// two halves of 16 MFMAs per wave:
+//   half 0: A rows 0-63 of the wave x B; reads A rows 64-127 of the slice;
+//   barrier (slice s+1 has landed, every wave is done with slice s-1);
+//   half 1: A rows 64-127 x B; reads A rows 0-63 and B of slice s+1 into the
+//           other B register set, and issues slice s+3 into slice s-1's
+//           buffer, one load per quarter of the half (issued in a burst,
+//           the 8 waves' loads stall their MFMA issue).
+// Two slices per loop iteration, so the two B register sets alternate
+// without copies; the last three slices, which load nothing, are a tail.
+//
+// LDS banks (measured with SQ_LDS_BANK_CONFLICT on gfx950): a 128-bit read
+// is served per half-wave, in two 16-lane cycles split by the parity of
+// lane bits 2^3^4; a 64-bit transposing read serves a half-wave per cycle.
+// The swizzles below keep every cycle on 16 distinct 16-byte bank slots:
+//   [rows][32] (64-byte rows): column group cg of row r at cg ^ 2*((r/8)%2);
+//     a fragment read takes 16 rows x 4 groups (lane l: row l%16, group l/16);
+//   [K][N] B (512-byte rows): 16-byte slot n/8 of row k at
+//     (n/8) ^ 2*((k%4) + 4*((k/8)%2)); a transposing fragment read takes rows
+//     8g..8g+3 (+4) of one 16-column block for lane group g.
+__device__ __forceinline__ uint32_t swz_rows32(uint32_t row, uint32_t cg) {
+  return row * 32u + ((cg ^ (((row >> 3) & 1u) << 1)) << 3);
+}
+__device__ __forceinline__ uint32_t kn_xor(uint32_t k) { return ((k & 3u) | (((k >> 3) & 1u) << 2)) << 1; }
+__device__ __forceinline__ uint32_t swz_kn16(uint32_t k, uint32_t n) {
+  return k * 256u + (((n >> 3) ^ kn_xor(k)) << 3) + (n & 7u);
+}
+
+// B operand of v_mfma_f32_16x16x32_bf16 (lane l: column n_col0 + l%16,
+// k = 8(l/16) .. +8) from a [K][N] slice with the gfx950 transposing read
+// ds_read_b64_tr_b16: within each 16-lane group, lane j points at four
+// consecutive values R_j of one k row and lane i receives
+// [R_{i/4}[i%4], R_{4+i/4}[i%4], R_{8+i/4}[i%4], R_{12+i/4}[i%4]]. With lane j
+// addressing row kb + j/4, columns n_col0 + 4(j%4), lane i gets
+// B[kb + e][n_col0 + i] for e = 0..3; a second read at kb + 4 completes its 8.
+__device__ __forceinline__ bf16x8 frag_b16_tr(const uint16_t* Bs, uint32_t n_col0, uint32_t lane) {
+  const uint32_t g = lane >> 4, j = lane & 15u;
+  const uint32_t k = 8u * g + (j >> 2), n = n_col0 + 4u * (j & 3u);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(Bs + swz_kn16(k, n)));
+  const i16x4 hi =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(Bs + swz_kn16(k + 4u, n)));
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Every other tile returns at once: gemm_bf16_256<..., SKIP_DMA> takes them.
 template <bool B_NK, typename Epi>
 __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
                                                  float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
   constexpr uint32_t BM = 256, BN = 256, BK = 32, STAGES = 4, SLICE = 256u * BK;
   __shared__ __attribute__((aligned(16))) uint16_t lds[STAGES * 2 * SLICE];
   const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -579,164 +415,199 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
   const uint32_t wm = (wave >> 2) * 128u, wn = (wave & 3u) * 64u;
   const uint16_t* __restrict__ A16 = reinterpret_cast<const uint16_t*>(A);
   const uint16_t* __restrict__ B16 = reinterpret_cast<const uint16_t*>(B);
-  f32x16 acc[4][2];
+  f32x4 acc[8][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+      for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.0f;
   // Per-lane element offsets of the 2 chunks (of 16) this wave fills per
   // slice and operand: chunk ch = 2*wave + q covers LDS slots 64ch .. +63.
   uint32_t offa[2], offb[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const uint32_t slot = (wave * 2u + q) * 64u + lane;
-    const uint32_t r = slot >> 2, c = (slot & 3u) ^ ((r >> 2) & 3u);
+    const uint32_t r = slot >> 2, c = (slot & 3u) ^ (((r >> 3) & 1u) << 1);  // inverse of swz_rows32
     offa[q] = r * K + c * 8u;
     if constexpr (B_NK) {
       offb[q] = r * K + c * 8u;
     } else {
-      const uint32_t k = slot >> 5, sp = slot & 31u;
-      offb[q] = k * N + ((sp ^ ((k & 3u) << 2)) << 3);
+      const uint32_t k = slot >> 5, sp = slot & 31u;  // [32][256]: 32 slots per row
+      offb[q] = k * N + ((sp ^ kn_xor(k)) << 3);
     }
   }
   uint16_t* ldsp = lds;
   auto a_slice = [&](uint32_t s) { return ldsp + s * 2u * SLICE; };
   auto b_slice = [&](uint32_t s) { return ldsp + s * 2u * SLICE + SLICE; };
-  auto issue = [&](uint32_t s, uint32_t k0) {
-    const uint16_t* a0 = A16 + static_cast<uint64_t>(m0) * K + k0;
-    const uint16_t* b0 = B_NK ? B16 + static_cast<uint64_t>(n0) * K + k0 : B16 + static_cast<uint64_t>(k0) * N + n0;
-    uint16_t* as = a_slice(s);
-    uint16_t* bs = b_slice(s);
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const uint32_t ch = wave * 2u + q;
-      __builtin_amdgcn_global_load_lds(a0 + offa[q], (lds_void*)(as + ch * 512u), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(b0 + offb[q], (lds_void*)(bs + ch * 512u), 16, 0, 0);
+  auto load = [&](int q, uint32_t s, uint32_t k0) {  // q even: A chunk q/2, q odd: B chunk q/2
+    const uint32_t ch = wave * 2u + (q >> 1);
+    if (q & 1) {
+      const uint16_t* b0 = B_NK ? B16 + static_cast<uint64_t>(n0) * K + k0 : B16 + static_cast<uint64_t>(k0) * N + n0;
+      __builtin_amdgcn_global_load_lds(b0 + offb[q >> 1], (lds_void*)(b_slice(s) + ch * 512u), 16, 0, 0);
+    } else {
+      const uint16_t* a0 = A16 + static_cast<uint64_t>(m0) * K + k0;
+      __builtin_amdgcn_global_load_lds(a0 + offa[q >> 1], (lds_void*)(a_slice(s) + ch * 512u), 16, 0, 0);
     }
   };
-  bf16x8 fa[4], fb[2];
-  auto load_frags = [&](uint32_t s, uint32_t ks) {
+  auto rd_a = [&](const uint16_t* As, uint32_t i) {  // A rows wm + 16i .. +16, all 32 k
+    return *reinterpret_cast<const bf16x8*>(&As[swz_rows32(wm + i * 16u + (lane & 15u), lane >> 4)]);
+  };
+  auto rd_b = [&](const uint16_t* Bs, uint32_t j) {  // B columns wn + 16j .. +16, all 32 k
+    if constexpr (B_NK)
+      return *reinterpret_cast<const bf16x8*>(&Bs[swz_rows32(wn + j * 16u + (lane & 15u), lane >> 4)]);
+    else
+      return frag_b16_tr(Bs, wn + j * 16u, lane);
+  };
+  bf16x8 fa[4], fh[4], fb0[4], fb1[4];  // A rows 0-63, A rows 64-127, the two B sets
+  auto fence = []() { __builtin_amdgcn_sched_barrier(0); };
+  // The MFMA takes the B fragment as its first operand: it computes the C^T
+  // block, so each lane ends up holding four consecutive columns of one row
+  // of C (a 16-byte store). Each group below is fenced with sched_barrier:
+  // left to itself the scheduler sinks the fragment reads behind the MFMAs.
+  auto half0 = [&](auto set, uint32_t s) {
+    bf16x8* gb = decltype(set)::value == 0 ? fb0 : fb1;
     const uint16_t* As = a_slice(s);
-    const uint16_t* Bs = b_slice(s);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      fa[i] = *reinterpret_cast<const bf16x8*>(&As[swz32(wm + i * 32u + (lane & 31u), ks * 2u + (lane >> 5))]);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      if constexpr (B_NK)
-        fb[j] = *reinterpret_cast<const bf16x8*>(&Bs[swz32(wn + j * 32u + (lane & 31u), ks * 2u + (lane >> 5))]);
-      else
-        fb[j] = frag_b_tr(Bs, wn + j * 32u, ks * 16u, lane);
-    }
-  };
-  auto step = [&](uint32_t next_s, uint32_t next_ks, bool dma, uint32_t dma_s, uint32_t dma_k0) {
-    bf16x8 ga[4], gb[2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ga[i] = fa[i];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) gb[j] = fb[j];
-    const uint16_t* As = a_slice(next_s);
-    const uint16_t* Bs = b_slice(next_s);
     auto mf = [&](int i, int j) {
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gb[j], ga[i], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gb[j], fa[i], acc[i][j], 0, 0, 0);
+      fence();
     };
-    auto rd_a = [&](int i) {
-      fa[i] = *reinterpret_cast<const bf16x8*>(&As[swz32(wm + i * 32u + (lane & 31u), next_ks * 2u + (lane >> 5))]);
-    };
-    auto rd_b = [&](int j) {
-      if constexpr (B_NK)
-        fb[j] = *reinterpret_cast<const bf16x8*>(&Bs[swz32(wn + j * 32u + (lane & 31u), next_ks * 2u + (lane >> 5))]);
-      else
-        fb[j] = frag_b_tr(Bs, wn + j * 32u, next_ks * 16u, lane);
-    };
-    const uint16_t* a0 = A16 + static_cast<uint64_t>(m0) * K + dma_k0;
-    const uint16_t* b0 = B_NK ? B16 + static_cast<uint64_t>(n0) * K + dma_k0 : B16 + static_cast<uint64_t>(dma_k0) * N + n0;
-    uint16_t* as = a_slice(dma_s);
-    uint16_t* bs = b_slice(dma_s);
-    auto dm = [&](int q) {
-      const uint32_t ch = wave * 2u + (q >> 1);
-      if (q & 1) __builtin_amdgcn_global_load_lds(b0 + offb[q >> 1], (lds_void*)(bs + ch * 512u), 16, 0, 0);
-      else __builtin_amdgcn_global_load_lds(a0 + offa[q >> 1], (lds_void*)(as + ch * 512u), 16, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    };
-    auto fence = []() { __builtin_amdgcn_sched_barrier(0); };
-    // MFMAs j-major; the next step's 6 fragment reads after the first four;
-    // when `dma`, the slice's 4 direct-to-LDS loads, two per MFMA.
     fence();
     mf(0, 0);
-    rd_a(0); rd_a(1); fence();
+    fh[0] = rd_a(As, 4); fh[1] = rd_a(As, 5); fence();
     mf(1, 0);
-    rd_a(2); rd_a(3); fence();
-    mf(2, 0);
-    rd_b(0); fence();
-    mf(3, 0);
-    rd_b(1); fence();
-    if (dma) {
-      mf(0, 1); dm(0); dm(1);
-      mf(1, 1); dm(2); dm(3);
-    } else {
-      mf(0, 1); mf(1, 1);
-    }
-    mf(2, 1); mf(3, 1);
+    fh[2] = rd_a(As, 6); fh[3] = rd_a(As, 7); fence();
+    mf(2, 0); mf(3, 0);
+    mf(0, 1); mf(1, 1); mf(2, 1); mf(3, 1);
+    mf(0, 2); mf(1, 2); mf(2, 2); mf(3, 2);
+    mf(0, 3); mf(1, 3); mf(2, 3); mf(3, 3);
   };
-  // As gemm_bf16_256_dma: the barrier waits for the slice about to be read
-  // (4 loads per slice and lane here) and leaves the step's own fragment
-  // reads (kReads) in flight.
-  constexpr int kReads = B_NK ? 6 : 8;
-  constexpr int kWaitNext = waitcnt_imm(4, kReads), kWaitLast = waitcnt_imm(0, kReads);
+  auto half1 = [&](auto set, uint32_t ns, bool dma, uint32_t ds, uint32_t dk) {
+    bf16x8* gb = decltype(set)::value == 0 ? fb0 : fb1;
+    bf16x8* nb = decltype(set)::value == 0 ? fb1 : fb0;
+    const uint16_t* As = a_slice(ns);
+    const uint16_t* Bs = b_slice(ns);
+    auto mf = [&](int i, int j) {
+      acc[4 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gb[j], fh[i], acc[4 + i][j], 0, 0, 0);
+      fence();
+    };
+    auto dm = [&](int q) {
+      if (dma) load(q, ds, dk);
+      fence();
+    };
+    fence();
+    mf(0, 0);
+    fa[0] = rd_a(As, 0); fa[1] = rd_a(As, 1); fence();
+    mf(1, 0);
+    fa[2] = rd_a(As, 2); fa[3] = rd_a(As, 3); fence();
+    mf(2, 0);
+    nb[0] = rd_b(Bs, 0); fence();
+    mf(3, 0);
+    nb[1] = rd_b(Bs, 1); fence();
+    mf(0, 1);
+    nb[2] = rd_b(Bs, 2); fence();
+    mf(1, 1);
+    nb[3] = rd_b(Bs, 3); fence();
+    mf(2, 1); dm(0);
+    mf(3, 1);
+    mf(0, 2); dm(1);
+    mf(1, 2);
+    mf(2, 2); dm(2);
+    mf(3, 2);
+    mf(0, 3); dm(3);
+    mf(1, 3); mf(2, 3); mf(3, 3);
+  };
+  // The barrier waits only for the slice about to be read (vmcnt counts in
+  // issue order, 4 loads per slice and lane); its lgkmcnt leaves half 0's 4
+  // fragment reads in flight but guarantees that every earlier read, the
+  // last ones of the buffer the next loads overwrite, has completed: LDS
+  // reads complete in order.
+  constexpr int kReads = 4;
+  auto wait_slices = [](uint32_t d, bool keep_reads) {  // at most d slices of loads still in flight
+    if (keep_reads) {
+      if (d >= 2u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, kReads));
+      else if (d == 1u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, kReads));
+      else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, kReads));
+    } else {
+      if (d >= 2u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
+      else if (d == 1u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
+      else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+    }
+  };
   auto barrier = [&]() {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
+  using Set0 = std::integral_constant<int, 0>;
+  using Set1 = std::integral_constant<int, 1>;
   const uint32_t nk = K / BK;
   const uint32_t pre = nk < STAGES - 1 ? nk : STAGES - 1;
-  for (uint32_t s = 0; s < pre; ++s) issue(s, s * BK);
+  for (uint32_t s = 0; s < pre; ++s)
+    for (int q = 0; q < 4; ++q) load(q, s, s * BK);
   asm volatile("" ::: "memory");
-  // Slice 0 landed: the pre - 1 newer slices (4 loads each) may stay in flight.
-  if (pre >= 3u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
-  else if (pre == 2u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
-  else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+  wait_slices(pre - 1u, false);  // slice 0 landed
   barrier();
-  load_frags(0, 0);
+  // Main slices kt < nk - 3 load slice kt+3: at the barrier of slice kt,
+  // slices up to kt+2 were issued and kt+1 must have landed.
   const uint32_t main_end = nk > STAGES - 1 ? nk - (STAGES - 1) : 0u;
-  for (uint32_t kt = 0; kt < main_end; ++kt) {
-    step(kt % STAGES, 1, false, 0, 0);
+  auto main_slice = [&](auto set, uint32_t kt) {
+    half0(set, kt % STAGES);
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(kWaitNext);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, kReads));
     barrier();
-    step((kt + 1) % STAGES, 0, true, (kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
-  }
-  for (uint32_t kt = main_end; kt < nk; ++kt) {
-    step(kt % STAGES, 1, false, 0, 0);
+    half1(set, (kt + 1) % STAGES, true, (kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
+  };
+  auto tail_slice = [&](auto set, uint32_t kt) {
+    half0(set, kt % STAGES);
     if (kt + 1 < nk) {
       asm volatile("" ::: "memory");
-      if (kt + 2 < nk) __builtin_amdgcn_s_waitcnt(kWaitNext);
-      else __builtin_amdgcn_s_waitcnt(kWaitLast);
+      wait_slices(nk - 2u - kt, true);
       barrier();
     }
-    // On the last iteration this reads a stale buffer whose values are unused.
-    step((kt + 1) % STAGES, 0, false, 0, 0);
+    half1(set, (kt + 1) % STAGES, false, 0, 0);  // the last one reads a stale buffer whose values are unused
+  };
+  // Slice 0's B fragments go into the set that makes the paired loop start on set 0.
+  const bool odd = (main_end & 1u) != 0u;
+  {
+    const uint16_t* As = a_slice(0);
+    const uint16_t* Bs = b_slice(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[i] = rd_a(As, i);
+    if (odd) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fb1[j] = rd_b(Bs, j);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fb0[j] = rd_b(Bs, j);
+    }
   }
+  uint32_t kt = 0;
+  if (odd) {
+    main_slice(Set1{}, 0);
+    kt = 1;
+  }
+  for (; kt < main_end; kt += 2) {
+    main_slice(Set0{}, kt);
+    main_slice(Set1{}, kt + 1);
+  }
+  if (main_end < nk) tail_slice(Set0{}, main_end);
+  if (main_end + 1 < nk) tail_slice(Set1{}, main_end + 1);
+  if (main_end + 2 < nk) tail_slice(Set0{}, main_end + 2);
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));  // nothing in flight past the loop
-  // acc[i][j][4g + q] = C[m][n + q], m = m0 + wm + 32i + lane%32, n = n0 + wn + 32j + 8g + 4*(lane/32).
-  const uint32_t mr = m0 + wm + (lane & 31u), nc = n0 + wn + 4u * (lane >> 5);
+  // acc[i][j][e] = C[m][n], m = m0 + wm + 16i + lane%16, n = n0 + wn + 16j + 4(lane/16) + e.
+  const uint32_t mr = m0 + wm + (lane & 15u), nc = n0 + wn + 4u * (lane >> 4);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const uint32_t m = mr + 32u * i, n = nc + 32u * j + 8u * g;
-        float4 v;
-        v.x = epi(acc[i][j][4 * g + 0], m, n + 0);
-        v.y = epi(acc[i][j][4 * g + 1], m, n + 1);
-        v.z = epi(acc[i][j][4 * g + 2], m, n + 2);
-        v.w = epi(acc[i][j][4 * g + 3], m, n + 3);
-        *reinterpret_cast<float4*>(C + static_cast<uint64_t>(m) * N + n) = v;
-      }
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t m = mr + 16u * i, n = nc + 16u * j;
+      float4 v;
+      v.x = epi(acc[i][j][0], m, n + 0);
+      v.y = epi(acc[i][j][1], m, n + 1);
+      v.z = epi(acc[i][j][2], m, n + 2);
+      v.w = epi(acc[i][j][3], m, n + 3);
+      *reinterpret_cast<float4*>(C + static_cast<uint64_t>(m) * N + n) = v;
+    }
 }
 
 // ---------------------------------------------------------------- fp32 path
