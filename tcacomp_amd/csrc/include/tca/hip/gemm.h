@@ -465,29 +465,34 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
   // block, so each lane ends up holding four consecutive columns of one row
   // of C (a 16-byte store). Each group below is fenced with sched_barrier:
   // left to itself the scheduler sinks the fragment reads behind the MFMAs.
+  // MFMA number c of a half (0..15) takes block (i, j) in snake order,
+  // j = c/4 and i = c%4 or 3 - c%4 for odd j, so consecutive MFMAs share an
+  // operand register (measured: about 3% faster at 4096^3 than j-major,
+  // the part being power-limited).
+  auto blk_i = [](int c) { return ((c >> 2) & 1) ? 3 - (c & 3) : (c & 3); };
   auto half0 = [&](auto set, uint32_t s) {
     bf16x8* gb = decltype(set)::value == 0 ? fb0 : fb1;
     const uint16_t* As = a_slice(s);
-    auto mf = [&](int i, int j) {
+    auto mf = [&](int c) {
+      const int i = blk_i(c), j = c >> 2;
       acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gb[j], fa[i], acc[i][j], 0, 0, 0);
       fence();
     };
     fence();
-    mf(0, 0);
+    mf(0);
     fh[0] = rd_a(As, 4); fh[1] = rd_a(As, 5); fence();
-    mf(1, 0);
+    mf(1);
     fh[2] = rd_a(As, 6); fh[3] = rd_a(As, 7); fence();
-    mf(2, 0); mf(3, 0);
-    mf(0, 1); mf(1, 1); mf(2, 1); mf(3, 1);
-    mf(0, 2); mf(1, 2); mf(2, 2); mf(3, 2);
-    mf(0, 3); mf(1, 3); mf(2, 3); mf(3, 3);
+#pragma unroll
+    for (int c = 2; c < 16; ++c) mf(c);
   };
   auto half1 = [&](auto set, uint32_t ns, bool dma, uint32_t ds, uint32_t dk) {
     bf16x8* gb = decltype(set)::value == 0 ? fb0 : fb1;
     bf16x8* nb = decltype(set)::value == 0 ? fb1 : fb0;
     const uint16_t* As = a_slice(ns);
     const uint16_t* Bs = b_slice(ns);
-    auto mf = [&](int i, int j) {
+    auto mf = [&](int c) {
+      const int i = blk_i(c), j = c >> 2;
       acc[4 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gb[j], fh[i], acc[4 + i][j], 0, 0, 0);
       fence();
     };
@@ -496,26 +501,26 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
       fence();
     };
     fence();
-    mf(0, 0);
+    mf(0);
     fa[0] = rd_a(As, 0); fa[1] = rd_a(As, 1); fence();
-    mf(1, 0);
+    mf(1);
     fa[2] = rd_a(As, 2); fa[3] = rd_a(As, 3); fence();
-    mf(2, 0);
+    mf(2);
     nb[0] = rd_b(Bs, 0); fence();
-    mf(3, 0);
+    mf(3);
     nb[1] = rd_b(Bs, 1); fence();
-    mf(0, 1);
+    mf(4);
     nb[2] = rd_b(Bs, 2); fence();
-    mf(1, 1);
+    mf(5);
     nb[3] = rd_b(Bs, 3); fence();
-    mf(2, 1); dm(0);
-    mf(3, 1);
-    mf(0, 2); dm(1);
-    mf(1, 2);
-    mf(2, 2); dm(2);
-    mf(3, 2);
-    mf(0, 3); dm(3);
-    mf(1, 3); mf(2, 3); mf(3, 3);
+    mf(6); dm(0);
+    mf(7);
+    mf(8); dm(1);
+    mf(9);
+    mf(10); dm(2);
+    mf(11);
+    mf(12); dm(3);
+    mf(13); mf(14); mf(15);
   };
   // The barrier waits only for the slice about to be read (vmcnt counts in
   // issue order, 4 loads per slice and lane); its lgkmcnt leaves half 0's 4
