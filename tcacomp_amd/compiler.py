@@ -5,12 +5,13 @@ toolchain to a harness (CLAUDE.md:18, internal/e2e/harness.go:87-127, with a
 content-addressed fixture cache keyed by the emitted source). This driver is
 that harness for the HIP path: the code object is cached under
 ``tcacomp_amd/_kcache/`` by the SHA-256 of the emitted source, the hipcc
-argv and the device headers, so ``build()`` can prebuild every kernel the
+argv and the device headers the source includes, so ``build()`` can prebuild every kernel the
 tests and the bench use and a GPU box never compiles. ``TCA_JIT=0`` turns a
 cache miss into an error instead of a hipcc run.
 """
 import ctypes
 import hashlib
+import re
 import os
 import subprocess
 
@@ -23,14 +24,29 @@ KCACHE = os.path.join(PKG_DIR, "_kcache")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 
-def _header_digest():
+_INCLUDE_RE = re.compile(r'^\s*#\s*include\s*"([^"]+)"', re.M)
+
+
+def _header_digest(source):
+    """sha256 over the headers under csrc/include that `source` includes,
+    followed transitively (path and contents, in a fixed order): a code
+    object depends on those files only, so a change to one header leaves the
+    keys of kernels that do not include it unchanged."""
+    seen = set()
+    todo = list(_INCLUDE_RE.findall(source))
+    while todo:
+        rel = todo.pop()
+        p = os.path.join(INCLUDE_DIR, rel)
+        if rel in seen or not os.path.isfile(p):
+            continue
+        seen.add(rel)
+        with open(p, "r") as fh:
+            todo.extend(_INCLUDE_RE.findall(fh.read()))
     h = hashlib.sha256()
-    for root, _, files in sorted(os.walk(INCLUDE_DIR)):
-        for f in sorted(files):
-            p = os.path.join(root, f)
-            h.update(p[len(INCLUDE_DIR):].encode())
-            with open(p, "rb") as fh:
-                h.update(fh.read())
+    for rel in sorted(seen):
+        h.update(rel.encode())
+        with open(os.path.join(INCLUDE_DIR, rel), "rb") as fh:
+            h.update(fh.read())
     return h.hexdigest()
 
 
@@ -40,7 +56,7 @@ def cache_key(source, hipcc_args):
     h.update(b"\0")
     h.update(" ".join(hipcc_args).encode())
     h.update(b"\0")
-    h.update(_header_digest().encode())
+    h.update(_header_digest(source).encode())
     return h.hexdigest()[:20]
 
 

@@ -568,6 +568,28 @@ def test_every_registered_program_is_prebuilt():
     assert not missing, "not prebuilt (run __graft_entry__.build()): %s" % missing
 
 
+def test_cache_key_follows_included_headers(tmp_path, monkeypatch):
+    """A code object's key covers the headers its source includes, followed
+    transitively, and no others: editing the contraction header leaves the
+    keys of row kernels (whose traffic figures are profiled per key) alone,
+    and editing a header a kernel includes changes its key."""
+    row = programs.CONFIG_PROGRAMS["row_sum_max_8192"]().emit()
+    gemm = programs.CONFIG_PROGRAMS["gemm_bf16"]().emit()
+    assert '#include "tca/hip/gemm.h"' in gemm.source and "gemm.h" not in row.source
+    inc = tmp_path / "include"
+    import shutil
+    shutil.copytree(compiler.INCLUDE_DIR, inc)
+    monkeypatch.setattr(compiler, "INCLUDE_DIR", str(inc))
+    k_row, k_gemm = compiler.cache_key(row.source, row.hipcc), compiler.cache_key(gemm.source, gemm.hipcc)
+    with open(inc / "tca" / "hip" / "gemm.h", "a") as f:
+        f.write("// edited\n")
+    assert compiler.cache_key(row.source, row.hipcc) == k_row
+    assert compiler.cache_key(gemm.source, gemm.hipcc) != k_gemm
+    with open(inc / "tca" / "hip" / "device.h", "a") as f:
+        f.write("// edited\n")
+    assert compiler.cache_key(row.source, row.hipcc) != k_row
+
+
 def test_every_registered_plan_parses():
     """The runtime's plan parser (the one tca_program_load runs) accepts the
     plan of every program the tests and the bench launch: no duplicate or
