@@ -305,11 +305,14 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   o << "// contraction over @" << g.dims[m.k].name << " on MFMA (" << (bf16 ? "bf16 16x16x32 whole tiles, 32x32x16 edges" : "f32 32x32x2")
     << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << ", " << tile << "x" << tile << " tiles\n";
   if (!bf16) {
-    o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "(\n    " << signature << ") {\n"
+    // Four 256-thread blocks per CU (4 waves per SIMD) need at most 128
+    // registers per lane; left alone the compiler takes 142 (3 per SIMD).
+    o << "extern \"C\" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) " << symbol
+      << "(\n    " << signature << ") {\n"
       << epi.str() << "  tca::hip::gemm_f32_128<" << nk << ">" << args;
     GemmKernel k;
     k.grid = grid;
-    k.detail = "f32 mfma 32x32 tile=128x128 bk=16" + orient;
+    k.detail = "f32 mfma 32x32 tile=128x128 bk=16, two LDS buffers" + orient;
     out->kernels.push_back(k);
     return true;
   }

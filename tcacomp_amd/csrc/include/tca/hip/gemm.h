@@ -616,24 +616,31 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
 }
 
 // ---------------------------------------------------------------- fp32 path
-// Tile: BM = BN = 128, BK slices; 4 waves as 2x2, each 64x64 = 2x2 MFMA
-// blocks; one LDS buffer, two barriers per slice (store, then compute), the
-// next slice's global loads in flight during the MFMAs. Measured at 4096^3
-// (interleaved, one box): 16-deep slices 116 TFLOP/s; 32-deep 102; 8-deep
-// 113; two LDS buffers of 16-deep slices (one barrier per slice) 114 — the
-// 17 KiB of LDS per block of 16-deep slices lets more blocks share a CU,
-// which hides the barriers better than double buffering.
+// Tile: BM = BN = 128, BK-deep slices; 4 waves as 2x2, each 64x64 = 2x2
+// blocks of v_mfma_f32_32x32x2f32 (4 blocks of 39 KiB per CU, 4 waves per
+// SIMD). fp32 MFMA is not power-limited on this part (an MFMA-only loop on
+// random operands holds 2.4 GHz), so the loop is built for issue:
+//   two LDS buffers, one barrier per slice: slice kt+1 is loaded into
+//   registers when slice kt starts and written into the other buffer half
+//   way through slice kt's MFMAs (every wave passed the barrier after that
+//   buffer's last reads);
+//   each 2-deep k step's fragments are read one step ahead;
+//   strides chosen so a fragment read (32 rows or columns at k, the other
+//   32 lanes at k+1) covers 64 distinct banks: LDA = BK + 2 (LDA/2 odd),
+//   [K][N] B rows of BN + 32 floats (the k+1 row lands 32 banks over).
+// Measured at 4096^3 against the single-buffer loop with stride BK + 1
+// (interleaved, one box, bitwise-equal results): 133 against 117 TFLOP/s;
+// 16x16x4f32 blocks on the same loop: 127.
 template <bool B_NK, int BK = 16, typename Epi>
 __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const float* __restrict__ B,
                                              float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
   constexpr int BM = 128, BN = 128;
   static_assert(BK == 8 || BK == 16 || BK == 32, "slices of 8, 16 or 32");
-  constexpr int LPT = BK / 8;                  // float4 per thread per operand slice
-  constexpr int LDA = BK + 1;                  // As[m][k], odd stride: conflict-free column reads
-  constexpr int LDB = B_NK ? BK + 1 : BN + 4;  // Bs[n][k] (NK) or Bs[k][n] (KN)
+  constexpr int LPT = BK / 8;                   // float4 per thread per operand slice
+  constexpr int LDA = BK + 2;                   // As[m][k]
+  constexpr int LDB = B_NK ? BK + 2 : BN + 32;  // Bs[n][k] (NK) or Bs[k][n] (KN)
   constexpr int SA = BM * LDA, SB = B_NK ? BN * LDB : BK * LDB;
-  __shared__ float As[SA];
-  __shared__ __attribute__((aligned(16))) float Bs[SB];
+  __shared__ __attribute__((aligned(16))) float lds[2 * (SA + SB)];
   const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   uint32_t tm, tn;
   gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
@@ -684,30 +691,50 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
       }
     }
   };
+  // Interior tiles (the whole 128x128 block in range, rows 16-byte aligned,
+  // the whole slice inside K) take unguarded float4 loads. The test is
+  // uniform over the workgroup, so it is a scalar branch: with per-lane
+  // guards alone the compiler merges the vector and scalar paths into
+  // single-float loads under divergent branches (117 against 132 TFLOP/s).
+  const bool interior_mn = vec_a && vec_b && m0 + BM <= M && n0 + BN <= N;
   auto load = [&](uint32_t k0) {
+    if (interior_mn && k0 + BK <= K) {
+#pragma unroll
+      for (int i = 0; i < LPT; ++i) {
+        const uint32_t v = i * 256u + tid, rr = v / VPR, kv = (v % VPR) * 4u;
+        ra[i] = *reinterpret_cast<const float4*>(A + static_cast<uint64_t>(m0 + rr) * K + k0 + kv);
+        if constexpr (B_NK) {
+          rb[i] = *reinterpret_cast<const float4*>(B + static_cast<uint64_t>(n0 + rr) * K + k0 + kv);
+        } else {
+          const uint32_t kr = v >> 5, nv = (v & 31u) * 4u;
+          rb[i] = *reinterpret_cast<const float4*>(B + static_cast<uint64_t>(k0 + kr) * N + n0 + nv);
+        }
+      }
+      return;
+    }
     load_rows(A, M, m0, k0, vec_a, ra);
     if constexpr (B_NK) load_rows(B, N, n0, k0, vec_b, rb);
     else load_b_kn(k0);
   };
-  auto store_lds = [&]() {
+  // Rows of LDA (or LDB) floats are 8-byte aligned: a float4 of a [rows][k]
+  // panel is written as two float2.
+  auto store = [&](int buf) {
+    float* As = lds + buf * (SA + SB);
+    float* Bs = As + SA;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const uint32_t v = i * 256u + tid, rr = v / VPR, kv = (v % VPR) * 4u;
-      float* p = &As[rr * LDA + kv];
-      p[0] = ra[i].x;
-      p[1] = ra[i].y;
-      p[2] = ra[i].z;
-      p[3] = ra[i].w;
+      float2* p = reinterpret_cast<float2*>(&As[rr * LDA + kv]);
+      p[0] = make_float2(ra[i].x, ra[i].y);
+      p[1] = make_float2(ra[i].z, ra[i].w);
     }
     if constexpr (B_NK) {
 #pragma unroll
       for (int i = 0; i < LPT; ++i) {
         const uint32_t v = i * 256u + tid, rr = v / VPR, kv = (v % VPR) * 4u;
-        float* p = &Bs[rr * LDB + kv];
-        p[0] = rb[i].x;
-        p[1] = rb[i].y;
-        p[2] = rb[i].z;
-        p[3] = rb[i].w;
+        float2* p = reinterpret_cast<float2*>(&Bs[rr * LDB + kv]);
+        p[0] = make_float2(rb[i].x, rb[i].y);
+        p[1] = make_float2(rb[i].z, rb[i].w);
       }
     } else {
 #pragma unroll
@@ -717,11 +744,22 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
       }
     }
   };
-  auto compute = [&]() {
-#pragma unroll
-    for (int ks = 0; ks < BK / 2; ++ks) {
+
+  const uint32_t nk = (K + BK - 1) / BK;
+  if (nk > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
+  for (uint32_t kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    const float* As = lds + buf * (SA + SB);
+    const float* Bs = As + SA;
+    const bool more = kt + 1 < nk;
+    if (more) load((kt + 1) * BK);
+    float a0[2], b0[2], a1[2], b1[2];
+    auto rd = [&](int ks, float (&fa)[2], float (&fb)[2]) {  // 2-deep step ks: lane l holds k = 2ks + l/32
       const uint32_t k = ks * 2u + (lane >> 5);
-      float fa[2], fb[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) fa[i] = As[(wm + i * 32u + (lane & 31u)) * LDA + k];
 #pragma unroll
@@ -729,21 +767,23 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
         const uint32_t n = wn + j * 32u + (lane & 31u);
         fb[j] = B_NK ? Bs[n * LDB + k] : Bs[k * LDB + n];
       }
+    };
+    auto mm = [&](const float (&fa)[2], const float (&fb)[2]) {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    };
+    rd(0, a0, b0);
+#pragma unroll
+    for (int ks = 0; ks < BK / 2; ks += 2) {
+      rd(ks + 1, a1, b1);
+      mm(a0, b0);
+      if (ks + 2 < BK / 2) rd(ks + 2, a0, b0);
+      mm(a1, b1);
+      if (ks == BK / 4 && more) store(buf ^ 1);
     }
-  };
-
-  const uint32_t nk = (K + BK - 1) / BK;
-  load(0);
-  for (uint32_t kt = 0; kt < nk; ++kt) {
     __syncthreads();
-    store_lds();
-    __syncthreads();
-    if (kt + 1 < nk) load((kt + 1) * BK);
-    compute();
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
