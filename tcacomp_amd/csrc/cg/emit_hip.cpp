@@ -273,7 +273,6 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   std::ostringstream& o = *src;
   const int ta = c.root.ops[m.a_op].tensor, tb = c.root.ops[m.b_op].tensor, tc = c.store_tensor;
   const bool bf16 = m.in == Elem::BF16;
-  const int tile = bf16 ? 256 : 128;
   // The fused epilogue (the piped map at (cm, cn)), the same in every kernel.
   std::ostringstream epi;
   epi << "  const uint32_t M = " << ExtentExpr(g, m.m) << ", N = " << ExtentExpr(g, m.n) << ", K = "
@@ -299,20 +298,34 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   const std::string args = "(t" + std::to_string(ta) + ", t" + std::to_string(tb) + ", t" + std::to_string(tc) +
                            ", M, N, K, epi);\n}\n\n";
   const std::string nk = m.b_nk ? "true" : "false";
-  const std::vector<std::string> grid = {g.dims[m.m].name + "/" + std::to_string(tile),
-                                         g.dims[m.n].name + "/" + std::to_string(tile)};
+  const std::vector<std::string> grid = {g.dims[m.m].name + "/256", g.dims[m.n].name + "/256"};
   const std::string orient = m.b_nk ? " B=[n][k]" : " B=[k][n]";
   o << "// contraction over @" << g.dims[m.k].name << " on MFMA (" << (bf16 ? "bf16 16x16x32 whole tiles, 32x32x16 edges" : "f32 32x32x2")
-    << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << ", " << tile << "x" << tile << " tiles\n";
+    << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << "\n";
   if (!bf16) {
-    // Four 256-thread blocks per CU (4 waves per SIMD) need at most 128
-    // registers per lane; left alone the compiler takes 142 (3 per SIMD).
+    // Two instances of one loop, exactly one launched: 256x256 tiles with 16
+    // waves from M, N >= 4096 on (at least 256 tiles, and the larger tile
+    // reads the L2 less per flop), 128x128 tiles with 4 waves below (more
+    // tiles over the 256 CUs). Both run 4 waves per SIMD: at most 128
+    // registers per lane.
+    const std::string M = g.dims[m.m].name, N = g.dims[m.n].name;
+    o << "extern \"C\" __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) " << symbol
+      << "_w(\n    " << signature << ") {\n"
+      << epi.str() << "  tca::hip::gemm_f32_tile<" << nk << ", 256, 256>" << args;
     o << "extern \"C\" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) " << symbol
       << "(\n    " << signature << ") {\n"
-      << epi.str() << "  tca::hip::gemm_f32_128<" << nk << ">" << args;
+      << epi.str() << "  tca::hip::gemm_f32_tile<" << nk << ", 128, 128>" << args;
+    GemmKernel w;
+    w.suffix = "_w";
+    w.block = 1024;
+    w.grid = {g.dims[m.m].name + "/256", g.dims[m.n].name + "/256"};
+    w.when = {M + " 4096 4294967295 1 0", N + " 4096 4294967295 1 0"};
+    w.detail = "f32 mfma 32x32 tile=256x256 bk=16 16 waves, two LDS buffers (M, N >= 4096)" + orient;
     GemmKernel k;
-    k.grid = grid;
-    k.detail = "f32 mfma 32x32 tile=128x128 bk=16, two LDS buffers" + orient;
+    k.grid = {g.dims[m.m].name + "/128", g.dims[m.n].name + "/128"};
+    k.unless = w.when;
+    k.detail = "f32 mfma 32x32 tile=128x128 bk=16 4 waves, two LDS buffers" + orient;
+    out->kernels.push_back(w);
     out->kernels.push_back(k);
     return true;
   }

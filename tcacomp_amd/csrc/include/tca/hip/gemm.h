@@ -616,10 +616,12 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
 }
 
 // ---------------------------------------------------------------- fp32 path
-// Tile: BM = BN = 128, BK-deep slices; 4 waves as 2x2, each 64x64 = 2x2
-// blocks of v_mfma_f32_32x32x2f32 (4 blocks of 39 KiB per CU, 4 waves per
-// SIMD). fp32 MFMA is not power-limited on this part (an MFMA-only loop on
-// random operands holds 2.4 GHz), so the loop is built for issue:
+// Tile: BM x BN with BM, BN in {128, 256}, BK-deep slices; (BM/64)x(BN/64)
+// waves, each 64x64 = 2x2 blocks of v_mfma_f32_32x32x2f32, 4 waves per SIMD
+// (256x256: one 72 KiB block of 16 waves per CU; 128x128: four 38 KiB
+// blocks of 4 waves), at most 128 registers per lane. fp32 MFMA is not
+// power-limited on this part (an MFMA-only loop on random operands holds
+// 2.4 GHz), so the loop is built for issue:
 //   two LDS buffers, one barrier per slice: slice kt+1 is loaded into
 //   registers when slice kt starts and written into the other buffer half
 //   way through slice kt's MFMAs (every wave passed the barrier after that
@@ -628,15 +630,21 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
 //   strides chosen so a fragment read (32 rows or columns at k, the other
 //   32 lanes at k+1) covers 64 distinct banks: LDA = BK + 2 (LDA/2 odd),
 //   [K][N] B rows of BN + 32 floats (the k+1 row lands 32 banks over).
-// Measured at 4096^3 against the single-buffer loop with stride BK + 1
-// (interleaved, one box, bitwise-equal results): 133 against 117 TFLOP/s;
-// 16x16x4f32 blocks on the same loop: 127.
-template <bool B_NK, int BK = 16, typename Epi>
-__device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const float* __restrict__ B,
-                                             float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
-  constexpr int BM = 128, BN = 128;
-  static_assert(BK == 8 || BK == 16 || BK == 32, "slices of 8, 16 or 32");
-  constexpr int LPT = BK / 8;                   // float4 per thread per operand slice
+// Measured at 4096^3 (interleaved, one box, bitwise-equal results), TFLOP/s:
+// this loop on 128x128 tiles with 4 waves 133, 256x128 with 8 waves 135,
+// 256x256 with 16 waves 137 (the larger tiles read the L2 less per flop,
+// but leave CUs idle below 256 tiles: the emitter takes 256x256 tiles from
+// M, N >= 4096 on and 128x128 tiles below); the earlier single-buffer
+// 128x128 loop with stride BK + 1, 117; 16x16x4f32 blocks on the 128x128
+// loop, 127.
+template <bool B_NK, int BM, int BN, int BK = 16, typename Epi>
+__device__ __forceinline__ void gemm_f32_tile(const float* __restrict__ A, const float* __restrict__ B,
+                                              float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
+  static_assert((BM == 128 || BM == 256) && BM == BN, "square 128 or 256 tiles");
+  static_assert(BK == 16 || BK == 32, "slices of 16 or 32");
+  constexpr int WN = BN / 64, THREADS = 64 * (BM / 64) * WN;
+  constexpr int LPT = BM * BK / 4 / THREADS;    // float4 per thread per operand slice
+  constexpr uint32_t VPN = BN / 4;              // float4 per [K][N] panel row
   constexpr int LDA = BK + 2;                   // As[m][k]
   constexpr int LDB = B_NK ? BK + 2 : BN + 32;  // Bs[n][k] (NK) or Bs[k][n] (KN)
   constexpr int SA = BM * LDA, SB = B_NK ? BN * LDB : BK * LDB;
@@ -646,7 +654,7 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
   gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
   const uint32_t m0 = tm * BM, n0 = tn * BN;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t wm = (wave >> 1) * 64u, wn = (wave & 1u) * 64u;
+  const uint32_t wm = (wave / WN) * 64u, wn = (wave % WN) * 64u;
   const bool vec_a = (K % 4u) == 0u;
   const bool vec_b = B_NK ? (K % 4u) == 0u : (N % 4u) == 0u;
 
@@ -659,12 +667,12 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
   float4 ra[LPT], rb[LPT];
-  // Row-major [rows][K] panel, BK columns: 32 BK float4 -> LPT per thread.
+  // Row-major [rows][K] panel, BK columns: BM BK / 4 float4 -> LPT per thread.
   constexpr uint32_t VPR = BK / 4;  // float4 per panel row
   auto load_rows = [&](const float* __restrict__ P, uint32_t rows, uint32_t r0, uint32_t k0, bool vec, float4* r) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const uint32_t v = i * 256u + tid, rr = v / VPR, kv = (v % VPR) * 4u;
+      const uint32_t v = i * THREADS + tid, rr = v / VPR, kv = (v % VPR) * 4u;
       const uint32_t gr = r0 + rr, gk = k0 + kv;
       if (vec && gr < rows && gk + 4u <= K) {
         r[i] = *reinterpret_cast<const float4*>(P + static_cast<uint64_t>(gr) * K + gk);
@@ -679,7 +687,7 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
   auto load_b_kn = [&](uint32_t k0) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const uint32_t v = i * 256u + tid, kr = v >> 5, nv = (v & 31u) * 4u;
+      const uint32_t v = i * THREADS + tid, kr = v / VPN, nv = (v % VPN) * 4u;
       const uint32_t gk = k0 + kr, gn = n0 + nv;
       if (vec_b && gk < K && gn + 4u <= N) {
         rb[i] = *reinterpret_cast<const float4*>(B + static_cast<uint64_t>(gk) * N + gn);
@@ -691,27 +699,28 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
       }
     }
   };
-  // Interior tiles (the whole 128x128 block in range, rows 16-byte aligned,
-  // the whole slice inside K) take unguarded float4 loads. The test is
-  // uniform over the workgroup, so it is a scalar branch: with per-lane
-  // guards alone the compiler merges the vector and scalar paths into
-  // single-float loads under divergent branches (117 against 132 TFLOP/s).
-  const bool interior_mn = vec_a && vec_b && m0 + BM <= M && n0 + BN <= N;
-  auto load = [&](uint32_t k0) {
-    if (interior_mn && k0 + BK <= K) {
+  // Interior tiles (the whole BMxBN block in range, rows 16-byte aligned,
+  // K a multiple of BK) take unguarded float4 loads. The test is uniform
+  // over the workgroup and made once, outside the K loop (two instances of
+  // the loop): with per-lane guards alone the compiler merges the vector and
+  // scalar paths into single-float loads under divergent branches, and with
+  // the branch inside the loop the two paths join in register copies that
+  // wait for the loads just issued (125 against 137 TFLOP/s).
+  const bool interior = vec_a && vec_b && m0 + BM <= M && n0 + BN <= N && K % BK == 0u;
+  auto load_interior = [&](uint32_t k0) {
 #pragma unroll
-      for (int i = 0; i < LPT; ++i) {
-        const uint32_t v = i * 256u + tid, rr = v / VPR, kv = (v % VPR) * 4u;
-        ra[i] = *reinterpret_cast<const float4*>(A + static_cast<uint64_t>(m0 + rr) * K + k0 + kv);
-        if constexpr (B_NK) {
-          rb[i] = *reinterpret_cast<const float4*>(B + static_cast<uint64_t>(n0 + rr) * K + k0 + kv);
-        } else {
-          const uint32_t kr = v >> 5, nv = (v & 31u) * 4u;
-          rb[i] = *reinterpret_cast<const float4*>(B + static_cast<uint64_t>(k0 + kr) * N + n0 + nv);
-        }
+    for (int i = 0; i < LPT; ++i) {
+      const uint32_t v = i * THREADS + tid, rr = v / VPR, kv = (v % VPR) * 4u;
+      ra[i] = *reinterpret_cast<const float4*>(A + static_cast<uint64_t>(m0 + rr) * K + k0 + kv);
+      if constexpr (B_NK) {
+        rb[i] = *reinterpret_cast<const float4*>(B + static_cast<uint64_t>(n0 + rr) * K + k0 + kv);
+      } else {
+        const uint32_t kr = v / VPN, nv = (v % VPN) * 4u;
+        rb[i] = *reinterpret_cast<const float4*>(B + static_cast<uint64_t>(k0 + kr) * N + n0 + nv);
       }
-      return;
     }
+  };
+  auto load_guarded = [&](uint32_t k0) {
     load_rows(A, M, m0, k0, vec_a, ra);
     if constexpr (B_NK) load_rows(B, N, n0, k0, vec_b, rb);
     else load_b_kn(k0);
@@ -723,7 +732,7 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
     float* Bs = As + SA;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const uint32_t v = i * 256u + tid, rr = v / VPR, kv = (v % VPR) * 4u;
+      const uint32_t v = i * THREADS + tid, rr = v / VPR, kv = (v % VPR) * 4u;
       float2* p = reinterpret_cast<float2*>(&As[rr * LDA + kv]);
       p[0] = make_float2(ra[i].x, ra[i].y);
       p[1] = make_float2(ra[i].z, ra[i].w);
@@ -731,7 +740,7 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
     if constexpr (B_NK) {
 #pragma unroll
       for (int i = 0; i < LPT; ++i) {
-        const uint32_t v = i * 256u + tid, rr = v / VPR, kv = (v % VPR) * 4u;
+        const uint32_t v = i * THREADS + tid, rr = v / VPR, kv = (v % VPR) * 4u;
         float2* p = reinterpret_cast<float2*>(&Bs[rr * LDB + kv]);
         p[0] = make_float2(rb[i].x, rb[i].y);
         p[1] = make_float2(rb[i].z, rb[i].w);
@@ -739,52 +748,56 @@ __device__ __forceinline__ void gemm_f32_128(const float* __restrict__ A, const 
     } else {
 #pragma unroll
       for (int i = 0; i < LPT; ++i) {
-        const uint32_t v = i * 256u + tid, kr = v >> 5, nv = (v & 31u) * 4u;
+        const uint32_t v = i * THREADS + tid, kr = v / VPN, nv = (v % VPN) * 4u;
         *reinterpret_cast<float4*>(&Bs[kr * LDB + nv]) = rb[i];
       }
     }
   };
 
   const uint32_t nk = (K + BK - 1) / BK;
-  if (nk > 0) {
-    load(0);
-    store(0);
-  }
-  __syncthreads();
-  for (uint32_t kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    const float* As = lds + buf * (SA + SB);
-    const float* Bs = As + SA;
-    const bool more = kt + 1 < nk;
-    if (more) load((kt + 1) * BK);
-    float a0[2], b0[2], a1[2], b1[2];
-    auto rd = [&](int ks, float (&fa)[2], float (&fb)[2]) {  // 2-deep step ks: lane l holds k = 2ks + l/32
-      const uint32_t k = ks * 2u + (lane >> 5);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) fa[i] = As[(wm + i * 32u + (lane & 31u)) * LDA + k];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const uint32_t n = wn + j * 32u + (lane & 31u);
-        fb[j] = B_NK ? Bs[n * LDB + k] : Bs[k * LDB + n];
-      }
-    };
-    auto mm = [&](const float (&fa)[2], const float (&fb)[2]) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
-    };
-    rd(0, a0, b0);
-#pragma unroll
-    for (int ks = 0; ks < BK / 2; ks += 2) {
-      rd(ks + 1, a1, b1);
-      mm(a0, b0);
-      if (ks + 2 < BK / 2) rd(ks + 2, a0, b0);
-      mm(a1, b1);
-      if (ks == BK / 4 && more) store(buf ^ 1);
+  auto run = [&](auto load) {  // the K loop, on one of the two load paths
+    if (nk > 0) {
+      load(0);
+      store(0);
     }
     __syncthreads();
-  }
+    for (uint32_t kt = 0; kt < nk; ++kt) {
+      const int buf = kt & 1;
+      const float* As = lds + buf * (SA + SB);
+      const float* Bs = As + SA;
+      const bool more = kt + 1 < nk;
+      if (more) load((kt + 1) * BK);
+      float a0[2], b0[2], a1[2], b1[2];
+      auto rd = [&](int ks, float (&fa)[2], float (&fb)[2]) {  // 2-deep step ks: lane l holds k = 2ks + l/32
+        const uint32_t k = ks * 2u + (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) fa[i] = As[(wm + i * 32u + (lane & 31u)) * LDA + k];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint32_t n = wn + j * 32u + (lane & 31u);
+          fb[j] = B_NK ? Bs[n * LDB + k] : Bs[k * LDB + n];
+        }
+      };
+      auto mm = [&](const float (&fa)[2], const float (&fb)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      };
+      rd(0, a0, b0);
+#pragma unroll
+      for (int ks = 0; ks < BK / 2; ks += 2) {
+        rd(ks + 1, a1, b1);
+        mm(a0, b0);
+        if (ks + 2 < BK / 2) rd(ks + 2, a0, b0);
+        mm(a1, b1);
+        if (ks == BK / 4 && more) store(buf ^ 1);
+      }
+      __syncthreads();
+    }
+  };
+  if (interior) run(load_interior);
+  else run(load_guarded);
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll

@@ -486,7 +486,7 @@ def test_program_launch_without_module_is_refused():
 
 EXPECTED_FAMILIES = {
     "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"] * 2,
-    "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"], "gemm_bf16": ["gemm"] * 2,
+    "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"] * 2, "gemm_bf16": ["gemm"] * 2,
     "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 12, "softmax_dyn": ["stream"] * 6,
     "layernorm_dyn": ["stream"] * 6, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 6,
     # narrow rows: one more width per halving of the element size (8 bf16, 16 u8 elements per vector)

@@ -264,12 +264,13 @@ def test_c5_gemm_exact_integers(gpu, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 64), (4100, 4104, 40), (4352, 4096, 16), (4097, 4096, 33),
-                                   (4096, 4101, 48)])
+                                   (4096, 4101, 48), (4095, 4096, 48), (2100, 3000, 40), (1000, 4224, 33)])
 @pytest.mark.parametrize("nt", [False, True])
 def test_c5_gemm_f32_large_exact(gpu, M, N, K, nt):
     """fp32 contractions at C5's scale with ragged edges (M, N not multiples
-    of the 128x128 tile, K not a multiple of the 16-deep slice, unaligned
-    rows), B as [K][N] and as [N][K]. Small-integer operands make every
+    of the tile, K not a multiple of the 16-deep slice, unaligned rows), B as
+    [K][N] and as [N][K], on both tile sizes: 256x256 (16 waves) from M, N >=
+    4096 on, 128x128 (4 waves) below. Small-integer operands make every
     result exact, so every tile, slice and edge must be exact."""
     _say("C5 f32 large", M, N, K, "nt" if nt else "")
     rng = np.random.default_rng(M + N + K)
@@ -278,8 +279,9 @@ def test_c5_gemm_f32_large_exact(gpu, M, N, K, nt):
     want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)  # exact: small integers
     name = "gemm_f32_nt" if nt else "gemm_f32"
     p = compiled(name)
+    big = M >= 4096 and N >= 4096
     assert p.selected_symbols([TensorDesc(0x1000, (M, K), 0), TensorDesc(0x1000, (N, K) if nt else (K, N), 0),
-                               TensorDesc(0x1000, (M, N), 0)]) == ["tca_%s_k0" % name]
+                               TensorDesc(0x1000, (M, N), 0)]) == ["tca_%s_k0%s" % (name, "_w" if big else "")]
     c = out_dev((M, N), gpu)
     bd = np.ascontiguousarray(b.T) if nt else b
     run(p, [to_dev(a, gpu), to_dev(bd, gpu), c])
