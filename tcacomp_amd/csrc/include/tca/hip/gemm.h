@@ -400,18 +400,22 @@ __device__ __forceinline__ bf16x8 frag_b16_tr(const uint16_t* Bs, uint32_t n_col
 }
 
 // Every other tile returns at once: gemm_bf16_256<..., SKIP_DMA> takes them.
-template <bool B_NK, typename Epi>
+template <bool B_NK, typename Epi, uint32_t STAGES = 4>
 __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
                                                  float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
+  static_assert(STAGES == 4 || STAGES == 5, "a ring of 4 or 5 slices (160 KiB of LDS at most)");
   typedef float f32x4 __attribute__((ext_vector_type(4)));
-  constexpr uint32_t BM = 256, BN = 256, BK = 32, STAGES = 4, SLICE = 256u * BK;
+  constexpr uint32_t BM = 256, BN = 256, BK = 32, SLICE = 256u * BK;
   __shared__ __attribute__((aligned(16))) uint16_t lds[STAGES * 2 * SLICE];
   const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   uint32_t tm, tn;
   gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
   const uint32_t m0 = tm * BM, n0 = tn * BN;
   if (!gemm_bf16_dma_tile(m0, n0, M, N, K)) return;  // gemm_bf16_256<..., SKIP_DMA> takes it
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  // The wave index is uniform over the wave: computed in a scalar register,
+  // the LDS destination of every direct-to-LDS load (the m0 operand) is a
+  // scalar value, with no readfirstlane per load.
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t wm = (wave >> 2) * 128u, wn = (wave & 3u) * 64u;
   const uint16_t* __restrict__ A16 = reinterpret_cast<const uint16_t*>(A);
   const uint16_t* __restrict__ B16 = reinterpret_cast<const uint16_t*>(B);
@@ -530,11 +534,13 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
   constexpr int kReads = 4;
   auto wait_slices = [](uint32_t d, bool keep_reads) {  // at most d slices of loads still in flight
     if (keep_reads) {
-      if (d >= 2u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, kReads));
+      if (d >= 3u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(12, kReads));
+      else if (d == 2u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, kReads));
       else if (d == 1u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, kReads));
       else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, kReads));
     } else {
-      if (d >= 2u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
+      if (d >= 3u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(12, 0));
+      else if (d == 2u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
       else if (d == 1u) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
       else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
     }
@@ -552,13 +558,14 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
   asm volatile("" ::: "memory");
   wait_slices(pre - 1u, false);  // slice 0 landed
   barrier();
-  // Main slices kt < nk - 3 load slice kt+3: at the barrier of slice kt,
-  // slices up to kt+2 were issued and kt+1 must have landed.
+  // Main slices kt < nk - (STAGES - 1) load slice kt + STAGES - 1: at the
+  // barrier of slice kt, slices up to kt + STAGES - 2 were issued and kt+1
+  // must have landed (STAGES - 3 newer slices may remain in flight).
   const uint32_t main_end = nk > STAGES - 1 ? nk - (STAGES - 1) : 0u;
   auto main_slice = [&](auto set, uint32_t kt) {
     half0(set, kt % STAGES);
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, kReads));
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(4 * static_cast<int>(STAGES - 3), kReads));
     barrier();
     half1(set, (kt + 1) % STAGES, true, (kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
   };
@@ -598,6 +605,7 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
   if (main_end < nk) tail_slice(Set0{}, main_end);
   if (main_end + 1 < nk) tail_slice(Set1{}, main_end + 1);
   if (main_end + 2 < nk) tail_slice(Set0{}, main_end + 2);
+  if (STAGES > 4 && main_end + 3 < nk) tail_slice(Set1{}, main_end + 3);
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));  // nothing in flight past the loop
   // acc[i][j][e] = C[m][n], m = m0 + wm + 16i + lane%16, n = n0 + wn + 16j + 4(lane/16) + e.
   const uint32_t mr = m0 + wm + (lane & 15u), nc = n0 + wn + 4u * (lane >> 4);
