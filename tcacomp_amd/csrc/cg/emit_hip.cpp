@@ -330,13 +330,16 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
     return true;
   }
   // bf16: the direct-to-LDS tiles (whole 256x256 blocks, K a positive
-  // multiple of 32, N % 8 == 0) on the 8-wave kernel, launched when there
-  // can be one; every other tile on the 256-thread register-staged kernel,
-  // skipped when every tile is a direct-to-LDS one (M, N multiples of 256,
-  // K a positive multiple of 32). Each kernel returns at once on the
-  // other's tiles.
+  // multiple of 32, N % 8 == 0) on an 8-wave kernel, launched when there can
+  // be one: A in 64-deep slices when K % 64 == 0 and K >= 256 (_w), else in
+  // 32-deep slices (_v); every other tile on the 256-thread register-staged
+  // kernel, skipped when every tile is a direct-to-LDS one (M, N multiples of
+  // 256, K a positive multiple of 32). Each kernel returns at once on the
+  // other kernels' tiles.
   const std::string M = g.dims[m.m].name, N = g.dims[m.n].name, K = g.dims[m.k].name;
   o << "extern \"C\" __global__ void __launch_bounds__(512) " << symbol << "_w(\n    " << signature << ") {\n"
+    << epi.str() << "  tca::hip::gemm_bf16_a64<" << nk << ">" << args;
+  o << "extern \"C\" __global__ void __launch_bounds__(512) " << symbol << "_v(\n    " << signature << ") {\n"
     << epi.str() << "  tca::hip::gemm_bf16_256_w8<" << nk << ">" << args;
   o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "(\n    " << signature << ") {\n"
     << epi.str() << "  tca::hip::gemm_bf16_256<" << nk << ", decltype(epi), 1, true, true, true>" << args;
@@ -344,13 +347,21 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   w.suffix = "_w";
   w.block = 512;
   w.grid = grid;
-  w.when = {M + " 256 4294967295 1 0", N + " 256 4294967295 8 0", K + " 32 4294967295 32 0"};
-  w.detail = "bf16 mfma 16x16x32 tile=256x256 bk=32 8 waves (direct-to-LDS ring; whole tiles only)" + orient;
+  w.when = {M + " 256 4294967295 1 0", N + " 256 4294967295 8 0", K + " 256 4294967295 64 0"};
+  w.detail = "bf16 mfma 16x16x32 tile=256x256 8 waves, A in 64-deep slices (direct-to-LDS rings; whole tiles, K % 64 == 0, K >= 256)" + orient;
+  GemmKernel v;
+  v.suffix = "_v";
+  v.block = 512;
+  v.grid = grid;
+  v.when = {M + " 256 4294967295 1 0", N + " 256 4294967295 8 0", K + " 32 4294967295 32 0"};
+  v.unless = {K + " 256 4294967295 64 0"};
+  v.detail = "bf16 mfma 16x16x32 tile=256x256 bk=32 8 waves (direct-to-LDS ring; whole tiles, K % 64 != 0 or K < 256)" + orient;
   GemmKernel e;
   e.grid = grid;
   e.unless = {M + " 0 4294967295 256 0", N + " 0 4294967295 256 0", K + " 32 4294967295 32 0"};
   e.detail = "bf16 mfma 32x32 tile=256x256 bk=64 4 waves (edge tiles, K % 32 != 0, N % 8 != 0)" + orient;
   out->kernels.push_back(w);
+  out->kernels.push_back(v);
   out->kernels.push_back(e);
   return true;
 }

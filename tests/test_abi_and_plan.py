@@ -247,17 +247,21 @@ def test_chain_segment_static_drops_the_local():
 
 
 @pytest.mark.parametrize("M,N,K,want", [
-    (4096, 4096, 4096, ["_w"]),      # every tile whole, K % 32 == 0: the 8-wave kernel alone
-    (4096, 4096, 4128, ["_w"]),
+    (4096, 4096, 4096, ["_w"]),      # every tile whole, K % 64 == 0, K >= 256: the 64-deep-A kernel alone
+    (4096, 4096, 4128, ["_v"]),      # K % 64 == 32: the 32-deep kernel alone
+    (4096, 4096, 192, ["_v"]),       # K % 64 == 0 but K < 256
+    (4096, 4096, 256, ["_w"]),
     (4100, 4096, 4096, ["_w", ""]),  # a partial bottom row of tiles: both, each skipping the other's tiles
     (4096, 4104, 4096, ["_w", ""]),
+    (4100, 4096, 4128, ["_v", ""]),
     (4096, 4096, 4100, [""]),        # K % 32 != 0: no tile takes the direct-to-LDS path
     (4096, 4100, 4096, [""]),        # N % 8 != 0: [K][N] rows not 16-byte aligned, no direct-to-LDS tile
     (255, 4096, 4096, [""]), (512, 512, 0, [""]), (512, 512, 16, [""])])
 def test_bf16_gemm_kernel_selection(M, N, K, want):
-    """The bf16 contraction's two kernels: the 8-wave direct-to-LDS kernel
-    runs when a whole tile can take it, the register-staged one unless every
-    tile does (plan `unless` guards)."""
+    """The bf16 contraction's three kernels: an 8-wave direct-to-LDS kernel
+    runs when a whole tile can take it (A in 64-deep slices when K % 64 == 0
+    and K >= 256, else in 32-deep slices), the register-staged one unless
+    every tile does (plan `when` / `unless` guards)."""
     e = programs.CONFIG_PROGRAMS["gemm_bf16"]().emit()
     rc, h = parse(e.plan)
     assert rc == 0, _lib.last_error()
@@ -485,8 +489,8 @@ def test_program_launch_without_module_is_refused():
 
 
 EXPECTED_FAMILIES = {
-    "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"] * 2,
-    "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"] * 2, "gemm_bf16": ["gemm"] * 2,
+    "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"] * 3,
+    "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"] * 2, "gemm_bf16": ["gemm"] * 3,
     "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 12, "softmax_dyn": ["stream"] * 6,
     "layernorm_dyn": ["stream"] * 6, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 6,
     # narrow rows: one more width per halving of the element size (8 bf16, 16 u8 elements per vector)

@@ -236,13 +236,17 @@ def test_c5_gemm_bf16_nt(gpu, M, N, K):
     assert_reduce_close(got, want, bound, K, "gemm bf16 nt")
 
 
-@pytest.mark.parametrize("M,N,K", [(96, 160, 64), (256, 512, 96)])
+@pytest.mark.parametrize("M,N,K", [(96, 160, 64), (256, 512, 96), (512, 512, 256), (512, 768, 320), (512, 256, 192),
+                                   (768, 512, 512), (520, 512, 256)])
 def test_c5_gemm_exact_integers(gpu, M, N, K):
     """Small-integer operands: every product and partial sum is exact in
     fp32, so any order gives the exact result (pins the MFMA lane layout,
     the LDS swizzles and the transposing B reads: a transposed, shifted or
-    mis-swizzled fragment cannot pass). 256-multiples take the bf16
-    direct-to-LDS path, the other shape the general path."""
+    mis-swizzled fragment cannot pass). Whole 256x256 tiles take the bf16
+    direct-to-LDS kernels: A in 64-deep slices for K % 64 == 0 and K >= 256
+    (K = 256 and 320 are its shortest loops: 8 and 10 steps, the peeled
+    tail only), 32-deep slices otherwise (K = 96, 192); the rest the
+    general path, in the same launch when tiles of both kinds exist."""
     import torch
     rng = np.random.default_rng(5)
     a = rng.integers(-4, 5, (M, K)).astype(np.float32)
