@@ -330,25 +330,25 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
     return true;
   }
   // bf16: the direct-to-LDS tiles (whole 256x256 blocks, K a positive
-  // multiple of 32, N % 8 == 0) on an 8-wave kernel, launched when there can
-  // be one: A in 64-deep slices when K % 64 == 0 and K >= 256 (_w), else in
-  // 32-deep slices (_v); every other tile on the 256-thread register-staged
-  // kernel, skipped when every tile is a direct-to-LDS one (M, N multiples of
-  // 256, K a positive multiple of 32). Each kernel returns at once on the
-  // other kernels' tiles.
+  // multiple of 32, N % 8 == 0), launched when there can be one: on 4 waves
+  // of 128x128 with A in 64-deep slices when K % 64 == 0 and K >= 256 (_w),
+  // else on 8 waves of 128x64 with 32-deep slices (_v); every other tile on
+  // the 256-thread register-staged kernel, skipped when every tile is a
+  // direct-to-LDS one (M, N multiples of 256, K a positive multiple of 32).
+  // Each kernel returns at once on the other kernels' tiles.
   const std::string M = g.dims[m.m].name, N = g.dims[m.n].name, K = g.dims[m.k].name;
-  o << "extern \"C\" __global__ void __launch_bounds__(512) " << symbol << "_w(\n    " << signature << ") {\n"
-    << epi.str() << "  tca::hip::gemm_bf16_a64<" << nk << ">" << args;
+  o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "_w(\n    " << signature << ") {\n"
+    << epi.str() << "  tca::hip::gemm_bf16_4w<" << nk << ">" << args;
   o << "extern \"C\" __global__ void __launch_bounds__(512) " << symbol << "_v(\n    " << signature << ") {\n"
     << epi.str() << "  tca::hip::gemm_bf16_256_w8<" << nk << ">" << args;
   o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "(\n    " << signature << ") {\n"
     << epi.str() << "  tca::hip::gemm_bf16_256<" << nk << ", decltype(epi), 1, true, true, true>" << args;
   GemmKernel w;
   w.suffix = "_w";
-  w.block = 512;
+  w.block = 256;
   w.grid = grid;
   w.when = {M + " 256 4294967295 1 0", N + " 256 4294967295 8 0", K + " 256 4294967295 64 0"};
-  w.detail = "bf16 mfma 16x16x32 tile=256x256 8 waves, A in 64-deep slices (direct-to-LDS rings; whole tiles, K % 64 == 0, K >= 256)" + orient;
+  w.detail = "bf16 mfma 16x16x32 tile=256x256 4 waves of 128x128, A in 64-deep slices (direct-to-LDS rings; whole tiles, K % 64 == 0, K >= 256)" + orient;
   GemmKernel v;
   v.suffix = "_v";
   v.block = 512;

@@ -5,7 +5,8 @@
 // two barriers per Combine; .planning/quick/261030-uai-.../after-cu/gemm.cu:
 // 59-90). Here the contraction runs on MFMA:
 //   bf16 inputs : v_mfma_f32_16x16x32_bf16 (gfx950) on whole 256x256 tiles
-//                 (gemm_bf16_256_w8), v_mfma_f32_32x32x16_bf16 on the edge
+//                 (gemm_bf16_4w when K % 64 == 0 and K >= 256, else
+//                 gemm_bf16_256_w8), v_mfma_f32_32x32x16_bf16 on the edge
 //                 tiles (gemm_bf16_256); fp32 accumulate
 //   fp32 inputs : v_mfma_f32_32x32x2f32, fp32 accumulate
 // Geometry of the register-staged kernels: a 256-thread workgroup (4 waves,
@@ -400,8 +401,8 @@ __device__ __forceinline__ bf16x8 frag_b16_tr(const uint16_t* Bs, uint32_t n_col
 }
 
 // Every other tile returns at once: gemm_bf16_256<..., SKIP_DMA> takes them.
-// With K % 64 == 0 and K >= 256 the launch takes gemm_bf16_a64 instead (A in
-// 64-deep slices, below).
+// With K % 64 == 0 and K >= 256 the launch takes gemm_bf16_4w instead (4
+// waves of 128x128, A in 64-deep slices, below).
 template <bool B_NK, typename Epi, uint32_t STAGES = 4>
 __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
                                                  float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
@@ -625,31 +626,49 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
     }
 }
 
-// ------------------------------------ bf16 path, 8 waves, 64-deep A slices
-// gemm_bf16_256_w8 with A loaded in 64-deep slices: 128-byte row segments,
-// whole cache lines per direct-to-LDS load, half the L2 requests of the
-// 64-byte segments of 32-deep A slices. A sits in a 3-buffer ring of
-// [256][64] slices (96 KiB), B in a 4-buffer ring of 32-deep slices (64
-// KiB), 160 KiB in all. Step kt (32 k) multiplies the k half kt%2 of A
-// slice kt/2 with B slice kt, in the same two halves and snake order as
-// gemm_bf16_256_w8 (two B register sets, 256 VGPRs, no scratch); half 1 of
-// step kt loads part kt%2 (rows 128(kt%2) .. +127) of A slice kt/2+2, into
-// the buffer of A slice kt/2-1, read last in half 0 of step kt-1, which
-// every wave finished before the barrier of step kt, and B slice kt+3 into
-// the buffer of B slice kt-1, read last in half 1 of step kt-2.
-// [rows][64] A slices (128-byte rows): 16-byte group g of row r at
-// g ^ (r & 6), which keeps the fragment read (16 rows x 4 groups, one k
-// half) on 16 distinct bank slots per cycle of a 128-bit read.
-// Measured against gemm_bf16_256_w8 (interleaved, one box, bitwise-equal
-// results): 4096^3 with rotated inputs 108.7 against 112.2 us, inputs in
-// the Infinity Cache 100.3 against 103.0 us, K = 16384 2.3% faster.
-// Needs K % 64 == 0 and K >= 256 (launch guards pick the kernel).
+// ------------------------------------- bf16 path, 4 waves, 128x128 per wave
+// Whole 256x256 tiles with K % 64 == 0 and K >= 256 (the launch guards pick
+// this kernel): 256 threads, one wave per SIMD, each wave a 128x128 sub-tile
+// of C as 8x8 blocks of v_mfma_f32_16x16x32_bf16, accumulators in AGPRs
+// (256 per lane), 160 VGPRs. Against 8 waves of 128x64 this reads a third
+// less LDS per flop (each A and B fragment feeds 8 blocks instead of 4 or 8
+// and 4), which leaves more of the power budget to the MFMAs: measured
+// interleaved with the 8-wave kernel on one box, 4096^3 with rotated inputs
+// 105.0-105.6 against 107.9-112.4 us, 8192^3 1356-1371 against 1335-1344
+// TFLOP/s, K = 16384 +2%, results bitwise equal.
+// LDS: A in 64-deep slices ([256][64], 128-byte rows, whole cache lines per
+// direct-to-LDS load) in a 3-buffer ring, B in 32-deep slices in a 4-buffer
+// ring, 160 KiB in all; slot s (32 deep) is k half s%2 of A slice s/2 and B
+// slice s.
+// Step kt: wait until slot kt+1 has landed and every read of slot kt has
+// completed, one barrier, then 64 MFMAs on the fragments of slot kt (read
+// during step kt-1) while this step reads all fragments of slot kt+1 into
+// the other register set and loads part kt%2 of A slice kt/2+2 (into the
+// buffer of A slice kt/2-1, last read during step kt-2) and B slice kt+4
+// (into slot kt's buffer).
+// The MFMAs are inline asm with the accumulator tied to one AGPR quad: the
+// compiler's own MFMA, given 256 accumulators, splits them between AGPRs and
+// VGPRs and moves them inside the loop (or spills). The hazards its
+// recogniser does not see for inline asm are covered here:
+//   the zero-initialised AGPRs are fixed (an empty asm per accumulator, so
+//   no zero is re-materialised later) and 16 wait states separate the last
+//   write from the first MFMA (VALU write -> MFMA SrcC read);
+//   24 wait states separate the last MFMA from the epilogue's AGPR reads
+//   (an 8-pass XDL write -> VALU/VMEM read);
+//   the MFMA A/B operands are ds_read results only (a host test checks the
+//   assembly: no VALU writes an MFMA source register), whose completion
+//   s_waitcnt covers; an MFMA's accumulator is written again only by the
+//   64th MFMA after it.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void mfma16_bf16_acc(f32x4_t& c, const bf16x8& b, const bf16x8& a) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(b), "v"(a));
+}
+
 __device__ __forceinline__ uint32_t swz_rows64(uint32_t row, uint32_t g) { return row * 64u + ((g ^ (row & 6u)) << 3); }
 
 template <bool B_NK, typename Epi>
-__device__ __forceinline__ void gemm_bf16_a64(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
-                                               float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
-  typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void gemm_bf16_4w(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
+                                             float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
   constexpr uint32_t BM = 256, BN = 256, ASL = 256u * 64u, BSL = 256u * 32u;
   __shared__ __attribute__((aligned(16))) uint16_t lds[3 * ASL + 4 * BSL];
   const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -658,27 +677,36 @@ __device__ __forceinline__ void gemm_bf16_a64(const __bf16* __restrict__ A, cons
   const uint32_t m0 = tm * BM, n0 = tn * BN;
   if (!gemm_bf16_dma_tile(m0, n0, M, N, K) || K % 64u != 0u || K < 256u) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t wm = (wave >> 2) * 128u, wn = (wave & 3u) * 64u;
+  const uint32_t wm = (wave >> 1) * 128u, wn = (wave & 1u) * 128u;
   const uint16_t* __restrict__ A16 = reinterpret_cast<const uint16_t*>(A);
   const uint16_t* __restrict__ B16 = reinterpret_cast<const uint16_t*>(B);
-  f32x4 acc[8][4];
+  f32x4_t acc[8][8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.0f;
-  uint32_t offa[2], offb[2];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const uint32_t row = 16u * wave + 8u * q + (lane >> 3);
-    offa[q] = row * K + (((lane & 7u) ^ (row & 6u)) << 3);
-    const uint32_t slot = (wave * 2u + q) * 64u + lane;
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("" : "+a"(acc[i][j]));
+  asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  // Per-lane element offsets of the 4 chunks this wave fills per A part
+  // (16 chunks of 8 rows x 128 bytes; wave w: chunks 4w .. 4w+3) and per B
+  // slice (16 chunks of 64 16-byte slots).
+  uint32_t offa[4], offb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t row = 32u * wave + 8u * q + (lane >> 3);
+    offa[q] = row * K + (((lane & 7u) ^ (row & 6u)) << 3);  // inverse of swz_rows64
+    const uint32_t slot = (wave * 4u + q) * 64u + lane;
     if constexpr (B_NK) {
-      const uint32_t r = slot >> 2, c = (slot & 3u) ^ (((r >> 3) & 1u) << 1);
+      const uint32_t r = slot >> 2, c = (slot & 3u) ^ (((r >> 3) & 1u) << 1);  // inverse of swz_rows32
       offb[q] = r * K + c * 8u;
     } else {
-      const uint32_t k = slot >> 5, sp = slot & 31u;
+      const uint32_t k = slot >> 5, sp = slot & 31u;  // [32][256]: 32 slots per row
       offb[q] = k * N + ((sp ^ kn_xor(k)) << 3);
     }
   }
@@ -688,132 +716,115 @@ __device__ __forceinline__ void gemm_bf16_a64(const __bf16* __restrict__ A, cons
   auto load_b = [&](int q, uint32_t s) {
     const uint32_t k0 = s * 32u;
     const uint16_t* b0 = B_NK ? B16 + static_cast<uint64_t>(n0) * K + k0 : B16 + static_cast<uint64_t>(k0) * N + n0;
-    __builtin_amdgcn_global_load_lds(b0 + offb[q], (lds_void*)(b_buf(s) + (wave * 2u + q) * 512u), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(b0 + offb[q], (lds_void*)(b_buf(s) + (wave * 4u + q) * 512u), 16, 0, 0);
   };
-  auto load_a = [&](int q, uint32_t j, uint32_t p) {
+  auto load_a = [&](int q, uint32_t j, uint32_t p) {  // part p (rows 128p .. +127) of A slice j
     const uint16_t* a0 = A16 + static_cast<uint64_t>(m0 + 128u * p) * K + j * 64u;
-    __builtin_amdgcn_global_load_lds(a0 + offa[q], (lds_void*)(a_buf(j) + (16u * p + wave * 2u + q) * 512u), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(a0 + offa[q], (lds_void*)(a_buf(j) + (16u * p + wave * 4u + q) * 512u), 16, 0, 0);
   };
-  auto rd_a = [&](const uint16_t* As, uint32_t h, uint32_t i) {  // A rows wm + 16i .. +16, k half h
-    return *reinterpret_cast<const bf16x8*>(&As[swz_rows64(wm + i * 16u + (lane & 15u), 4u * h + (lane >> 4))]);
+  auto rd_a = [&](uint32_t s, uint32_t i) {  // slot s: A rows wm + 16i .. +16
+    const uint16_t* As = a_buf(s >> 1);
+    return *reinterpret_cast<const bf16x8*>(&As[swz_rows64(wm + i * 16u + (lane & 15u), 4u * (s & 1u) + (lane >> 4))]);
   };
-  auto rd_b = [&](const uint16_t* Bs, uint32_t j) {
+  auto rd_b = [&](uint32_t s, uint32_t j) {  // slot s: B columns wn + 16j .. +16
+    const uint16_t* Bs = b_buf(s);
     if constexpr (B_NK)
       return *reinterpret_cast<const bf16x8*>(&Bs[swz_rows32(wn + j * 16u + (lane & 15u), lane >> 4)]);
     else
       return frag_b16_tr(Bs, wn + j * 16u, lane);
   };
-  bf16x8 fa[4], fh[4], fb0[4], fb1[4];
+  bf16x8 a0s[8], b0s[8], a1s[8], b1s[8];  // two fragment sets: this step's and the next one's
   auto fence = []() { __builtin_amdgcn_sched_barrier(0); };
-  auto blk_i = [](int c) { return ((c >> 2) & 1) ? 3 - (c & 3) : (c & 3); };
-  auto half0 = [&](auto set, uint32_t kt) {
-    bf16x8* gb = decltype(set)::value == 0 ? fb0 : fb1;
-    const uint16_t* As = a_buf(kt >> 1);
-    const uint32_t h = kt & 1u;
-    auto mf = [&](int c) {
-      const int i = blk_i(c), j = c >> 2;
-      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gb[j], fa[i], acc[i][j], 0, 0, 0);
-      fence();
-    };
-    fence();
-    mf(0);
-    fh[0] = rd_a(As, h, 4); fh[1] = rd_a(As, h, 5); fence();
-    mf(1);
-    fh[2] = rd_a(As, h, 6); fh[3] = rd_a(As, h, 7); fence();
-#pragma unroll
-    for (int c = 2; c < 16; ++c) mf(c);
-  };
-  // lda: load part kt%2 of A slice kt/2+2; ldb: load B slice kt+3.
-  auto half1 = [&](auto set, uint32_t kt, bool lda, bool ldb) {
-    bf16x8* gb = decltype(set)::value == 0 ? fb0 : fb1;
-    bf16x8* nb = decltype(set)::value == 0 ? fb1 : fb0;
-    const uint32_t nt = kt + 1u;
-    const uint16_t* As = a_buf(nt >> 1);
-    const uint16_t* Bs = b_buf(nt);
-    const uint32_t h = nt & 1u;
-    auto mf = [&](int c) {
-      const int i = blk_i(c), j = c >> 2;
-      acc[4 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gb[j], fh[i], acc[4 + i][j], 0, 0, 0);
-      fence();
-    };
-    auto da = [&](int q) { if (lda) load_a(q, (kt >> 1) + 2u, kt & 1u); fence(); };
-    auto db = [&](int q) { if (ldb) load_b(q, kt + 3u); fence(); };
-    fence();
-    mf(0);
-    fa[0] = rd_a(As, h, 0); fa[1] = rd_a(As, h, 1); fence();
-    mf(1);
-    fa[2] = rd_a(As, h, 2); fa[3] = rd_a(As, h, 3); fence();
-    mf(2);
-    nb[0] = rd_b(Bs, 0); fence();
-    mf(3);
-    nb[1] = rd_b(Bs, 1); fence();
-    mf(4);
-    nb[2] = rd_b(Bs, 2); fence();
-    mf(5);
-    nb[3] = rd_b(Bs, 3); fence();
-    mf(6); da(0);
-    mf(7);
-    mf(8); da(1);
-    mf(9);
-    mf(10); db(0);
-    mf(11);
-    mf(12); db(1);
-    mf(13); mf(14); mf(15);
-  };
-  constexpr int kReads = 4;
   auto barrier = [&]() {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
+  // MFMA c (0..63) takes block (i, j) with j = c/8 and i snaking over 0..7,
+  // so consecutive MFMAs share an operand register. The operand-swapped
+  // MFMA computes the C^T block: each lane ends up holding four consecutive
+  // columns of one row of C (a 16-byte store).
+  // wait_vm: the loads that may remain in flight at the start of the step
+  // (-1: no wait and no barrier, the last step).
+  auto step = [&](auto set, uint32_t kt, int wait_vm, bool rd, bool ld) {
+    bf16x8* ca = decltype(set)::value == 0 ? a0s : a1s;
+    bf16x8* cb = decltype(set)::value == 0 ? b0s : b1s;
+    bf16x8* na = decltype(set)::value == 0 ? a1s : a0s;
+    bf16x8* nb = decltype(set)::value == 0 ? b1s : b0s;
+    if (wait_vm >= 0) {
+      asm volatile("" ::: "memory");
+      if (wait_vm == 16) __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 0));
+      else if (wait_vm == 8) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
+      else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+      barrier();
+    }
+    const uint32_t ns = kt + 1u;
+    auto mf = [&](int c) {
+      const int j = c >> 3, i = (j & 1) ? 7 - (c & 7) : (c & 7);
+      mfma16_bf16_acc(acc[i][j], cb[j], ca[i]);
+      fence();
+    };
+    auto da = [&](int q) { if (ld) load_a(q, (kt >> 1) + 2u, kt & 1u); fence(); };
+    auto db = [&](int q) { if (ld) load_b(q, kt + 4u); fence(); };
+    fence();
+    if (rd) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) { mf(c); na[c] = rd_a(ns, c); fence(); }
+#pragma unroll
+      for (int c = 0; c < 8; ++c) { mf(8 + c); nb[c] = rd_b(ns, c); fence(); }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 16; ++c) mf(c);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      mf(16 + 8 * q); mf(17 + 8 * q); mf(18 + 8 * q); mf(19 + 8 * q); da(q);
+      mf(20 + 8 * q); mf(21 + 8 * q); mf(22 + 8 * q); mf(23 + 8 * q); db(q);
+    }
+#pragma unroll
+    for (int c = 48; c < 64; ++c) mf(c);
+  };
   using Set0 = std::integral_constant<int, 0>;
   using Set1 = std::integral_constant<int, 1>;
   const uint32_t nk = K / 32u;
-  // Prologue: A0 (4 loads), B0 (2), B1 (2), A1 (4), B2 (2); A0 and B0 landed: 8 newer loads may remain.
-  for (int q = 0; q < 2; ++q) load_a(q, 0, 0);
-  for (int q = 0; q < 2; ++q) load_a(q, 0, 1);
-  for (int q = 0; q < 2; ++q) load_b(q, 0);
-  for (int q = 0; q < 2; ++q) load_b(q, 1);
-  for (int q = 0; q < 2; ++q) load_a(q, 1, 0);
-  for (int q = 0; q < 2; ++q) load_a(q, 1, 1);
-  for (int q = 0; q < 2; ++q) load_b(q, 2);
+  // Prologue: A0 (8 loads), B0 (4), B1 (4), A1 (8), B2 (4), B3 (4); A0 and B0 landed: 20 newer may remain.
+  for (int q = 0; q < 4; ++q) load_a(q, 0, 0);
+  for (int q = 0; q < 4; ++q) load_a(q, 0, 1);
+  for (int q = 0; q < 4; ++q) load_b(q, 0);
+  for (int q = 0; q < 4; ++q) load_b(q, 1);
+  for (int q = 0; q < 4; ++q) load_a(q, 1, 0);
+  for (int q = 0; q < 4; ++q) load_a(q, 1, 1);
+  for (int q = 0; q < 4; ++q) load_b(q, 2);
+  for (int q = 0; q < 4; ++q) load_b(q, 3);
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(20, 0));
   barrier();
-  {
-    const uint16_t* As = a_buf(0);
-    const uint16_t* Bs = b_buf(0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i] = rd_a(As, 0, i);
+  for (int i = 0; i < 8; ++i) a0s[i] = rd_a(0, i);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) fb0[j] = rd_b(Bs, j);
-  }
-  // Main steps: at the barrier of step kt the loads step kt+1 reads were issued in half 1 of step kt-2
-  // at the latest; half 1 of step kt-1 issued 4 more.
-  auto step = [&](auto set, uint32_t kt, int wait_vm, bool lda, bool ldb) {
-    half0(set, kt);
-    asm volatile("" ::: "memory");
-    if (wait_vm == 4) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, kReads));
-    else if (wait_vm == 2) __builtin_amdgcn_s_waitcnt(waitcnt_imm(2, kReads));
-    else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, kReads));
-    barrier();
-    half1(set, kt, lda, ldb);
-  };
-  const uint32_t main_end = nk - 4u;  // even
+  for (int j = 0; j < 8; ++j) b0s[j] = rd_b(0, j);
+  // Loads run while kt < nk - 4 (8 per step). At the start of step kt slot
+  // kt+1 must have landed: for even kt the loads of step kt-3 (16 newer may
+  // remain), for odd kt the A part of step kt-2 (8 newer); in the prologue's
+  // place the same counts are conservative. vmcnt counts in issue order.
+  const uint32_t main_end = nk - 4u;  // even: K % 64 == 0
   for (uint32_t kt = 0; kt < main_end; kt += 2) {
-    step(Set0{}, kt, 4, true, true);
-    step(Set1{}, kt + 1, 4, true, true);
+    step(Set0{}, kt, 16, true, true);
+    step(Set1{}, kt + 1, 8, true, true);
   }
-  step(Set0{}, nk - 4u, 4, false, true);   // loads B slice nk-1 only
-  step(Set1{}, nk - 3u, 2, false, false);  // the last A part landed; B slice nk-1 may remain
-  step(Set0{}, nk - 2u, 0, false, false);
-  half0(Set1{}, nk - 1u);
-  half1(Set1{}, nk - 1u, false, false);  // reads a stale step's fragments, unused
+  step(Set0{}, nk - 4u, 16, true, false);
+  step(Set1{}, nk - 3u, 0, true, false);  // no loads after those of step nk-5
+  step(Set0{}, nk - 2u, 0, true, false);
+  step(Set1{}, nk - 1u, -1, false, false);
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  // acc[i][j][e] = C[m][n], m = m0 + wm + 16i + lane%16, n = n0 + wn + 16j + 4(lane/16) + e.
   const uint32_t mr = m0 + wm + (lane & 15u), nc = n0 + wn + 4u * (lane >> 4);
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 8; ++j) {
       const uint32_t m = mr + 16u * i, n = nc + 16u * j;
       float4 v;
       v.x = epi(acc[i][j][0], m, n + 0);

@@ -627,15 +627,8 @@ def test_runtime_null_arguments_are_refused_before_hip():
     assert L.tca_rt_launch(None, b"k", 1, 64, 0, None, 0, None) == _lib.TCA_ERR_INVALID
 
 
-@pytest.mark.parametrize("name", ["gemm_bf16", "gemm_bf16_nt"])
-def test_dma_gemm_reloads_nothing_from_scratch(name, tmp_path):
-    """The bf16 contraction's main loop waits on hand-counted vmcnt values
-    for its direct-to-LDS loads; a register spill reloaded from scratch while
-    they are in flight would share that counter (an fp32 port that spilled
-    computed wrong results). From the first direct-to-LDS load to the end of
-    that path (its s_endpgm) nothing may be reloaded from scratch; the
-    register-staged edge path after it may. Host-only: compiles to gfx950
-    assembly."""
+def _gemm_asm(name, tmp_path):
+    """The program's emitted source compiled to gfx950 assembly (host-only)."""
     import subprocess
     e = programs.CONFIG_PROGRAMS[name]().emit()
     src = tmp_path / "k.hip"
@@ -648,12 +641,112 @@ def test_dma_gemm_reloads_nothing_from_scratch(name, tmp_path):
     if r.returncode != 0 and "No such file" in (r.stderr or ""):
         pytest.skip("hipcc not available")
     assert r.returncode == 0, r.stderr[-2000:]
-    lines = asm.read_text().split("\n")
+    return asm.read_text().split("\n")
+
+
+@pytest.mark.parametrize("name", ["gemm_bf16", "gemm_bf16_nt"])
+def test_dma_gemm_reloads_nothing_from_scratch(name, tmp_path):
+    """The bf16 contraction's main loop waits on hand-counted vmcnt values
+    for its direct-to-LDS loads; a register spill reloaded from scratch while
+    they are in flight would share that counter (an fp32 port that spilled
+    computed wrong results). From the first direct-to-LDS load to the end of
+    that path (its s_endpgm) nothing may be reloaded from scratch; the
+    register-staged edge path after it may. Host-only: compiles to gfx950
+    assembly."""
+    lines = _gemm_asm(name, tmp_path)
     dma = [i for i, l in enumerate(lines) if "global_load_lds_dwordx4" in l]
     assert dma
     end = next(i for i in range(dma[-1], len(lines)) if "s_endpgm" in lines[i])
     reloads = [lines[i].strip() for i in range(dma[0], end) if "scratch_load" in lines[i]]
     assert not reloads, reloads[:4]
+
+
+def _regs(op):
+    """VGPR or AGPR numbers named by one assembly operand (v5, v[4:7], a[0:3])."""
+    m = re.fullmatch(r"([va])(?:(\d+)|\[(\d+):(\d+)\])", op.strip())
+    if not m:
+        return m, set()
+    lo = int(m.group(2) if m.group(2) is not None else m.group(3))
+    hi = int(m.group(2) if m.group(2) is not None else m.group(4))
+    return m.group(1), set(range(lo, hi + 1))
+
+
+def _vgpr_writes(line):
+    """VGPRs an instruction writes: its first operand when that is a VGPR,
+    for every instruction that has a destination (not stores, LDS writes,
+    direct-to-LDS loads or scalar instructions)."""
+    parts = line.strip().split(None, 1)
+    if len(parts) < 2 or parts[0].startswith(("s_", ";", ".")):
+        return set()
+    mn = parts[0]
+    if "store" in mn or mn.startswith(("ds_write", "ds_store")) or "load_lds" in mn:
+        return set()
+    kind, regs = _regs(parts[1].split(",")[0])
+    return regs if kind == "v" else set()
+
+
+@pytest.mark.parametrize("name", ["gemm_bf16", "gemm_bf16_nt"])
+def test_asm_mfma_kernel_hazards_covered(name, tmp_path):
+    """The 4-wave bf16 contraction issues its MFMAs as inline asm, which the
+    compiler's hazard recogniser does not model. Checked on its gfx950
+    assembly: every MFMA accumulates in place in AGPRs (dst == SrcC); every
+    MFMA A/B operand register reaches the MFMA from a ds_read only (along
+    the straight line and around the main loop's back edge), never from a
+    VALU write; the AGPR zero-init is followed by two s_nop 7 before the
+    first MFMA; three s_nop 7 separate the last MFMA from the first
+    instruction that reads an AGPR outside an MFMA."""
+    lines = _gemm_asm(name, tmp_path)
+    sym = "tca_%s_k0_w:" % name
+    start = next(i for i, l in enumerate(lines) if l.startswith(sym))
+    end = next(i for i in range(start, len(lines)) if lines[i].startswith(".Lfunc_end"))
+    body = lines[start:end]
+    mf = [i for i, l in enumerate(body) if l.strip().startswith("v_mfma")]
+    assert len(mf) > 64
+    heads = [i for i, l in enumerate(body) if "Loop Header" in l]
+    assert len(heads) == 1, heads
+    head = heads[0]
+    label = body[head].split(":")[0]
+    tail = max(i for i, l in enumerate(body) if l.strip().startswith("s_cbranch") and l.strip().endswith(label))
+
+    def writers(idx, reg):
+        """Instructions whose write of reg can reach body[idx]."""
+        found, i, wrapped = [], idx - 1, False
+        while i >= 0:
+            if i == head and head < idx <= tail and not wrapped:
+                # around the back edge first, then on into the preheader
+                for j in range(tail, idx, -1):
+                    if reg in _vgpr_writes(body[j]):
+                        found.append(j)
+                        break
+                wrapped = True
+            if reg in _vgpr_writes(body[i]):
+                found.append(i)
+                return found
+            i -= 1
+        return found
+
+    bad = []
+    for i in mf:
+        ops = [o.strip() for o in body[i].strip().split(None, 1)[1].split(",")]
+        assert ops[0] == ops[3] and ops[0].startswith("a["), body[i]
+        for op in ops[1:3]:
+            kind, regs = _regs(op)
+            assert kind == "v", body[i]
+            for r in regs:
+                for w in writers(i, r):
+                    if not body[w].strip().startswith("ds_read"):
+                        bad.append((body[i].strip(), body[w].strip()))
+    assert not bad, bad[:4]
+    nop7 = [i for i, l in enumerate(body) if l.strip() == "s_nop 7"]
+    inits = [i for i, l in enumerate(body) if l.strip().startswith("v_accvgpr_write")]
+    assert inits and max(inits) < mf[0]
+    assert len([i for i in nop7 if max(inits) < i < mf[0]]) >= 2
+    readers = [i for i, l in enumerate(body) if i > mf[-1] and re.search(r"\ba\[?\d", l)
+               and not l.strip().startswith(("v_mfma", ";"))]
+    assert readers
+    assert len([i for i in nop7 if mf[-1] < i < readers[0]]) >= 3
+    assert not [l for l in body if re.search(r"\ba\[?\d", l) and l.strip().startswith("v_accvgpr_read")
+                and mf[0] < body.index(l) < mf[-1]]
 
 
 @pytest.fixture(scope="module")
