@@ -303,29 +303,40 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   o << "// contraction over @" << g.dims[m.k].name << " on MFMA (" << (bf16 ? "bf16 16x16x32 whole tiles, 32x32x16 edges" : "f32 32x32x2")
     << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << "\n";
   if (!bf16) {
-    // Two instances of one loop, exactly one launched: 256x256 tiles with 16
-    // waves from M, N >= 4096 on (at least 256 tiles, and the larger tile
-    // reads the L2 less per flop), 128x128 tiles with 4 waves below (more
-    // tiles over the 256 CUs). Both run 4 waves per SIMD: at most 128
-    // registers per lane.
-    const std::string M = g.dims[m.m].name, N = g.dims[m.n].name;
+    // From M, N >= 4096 on (at least 256 tiles of 256x256): whole tiles with
+    // K % 32 == 0 and K >= 128 on 4 waves of 128x128 fed by a direct-to-LDS
+    // ring (_w); otherwise 256x256 tiles with 16 waves of 64x64 (_v). Below,
+    // 128x128 tiles with 4 waves (more tiles over the 256 CUs). _v and the
+    // 128x128 kernel are two instances of one loop with edge guards; both run
+    // 4 waves per SIMD: at most 128 registers per lane.
+    const std::string M = g.dims[m.m].name, N = g.dims[m.n].name, K = g.dims[m.k].name;
+    o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "_w(\n    " << signature << ") {\n"
+      << epi.str() << "  tca::hip::gemm_f32_4w<" << nk << ">" << args;
     o << "extern \"C\" __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) " << symbol
-      << "_w(\n    " << signature << ") {\n"
+      << "_v(\n    " << signature << ") {\n"
       << epi.str() << "  tca::hip::gemm_f32_tile<" << nk << ", 256, 256>" << args;
     o << "extern \"C\" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) " << symbol
       << "(\n    " << signature << ") {\n"
       << epi.str() << "  tca::hip::gemm_f32_tile<" << nk << ", 128, 128>" << args;
     GemmKernel w;
     w.suffix = "_w";
-    w.block = 1024;
-    w.grid = {g.dims[m.m].name + "/256", g.dims[m.n].name + "/256"};
-    w.when = {M + " 4096 4294967295 1 0", N + " 4096 4294967295 1 0"};
-    w.detail = "f32 mfma 32x32 tile=256x256 bk=16 16 waves, two LDS buffers (M, N >= 4096)" + orient;
+    w.block = 256;
+    w.grid = {M + "/256", N + "/256"};
+    w.when = {M + " 4096 4294967295 256 0", N + " 4096 4294967295 256 0", K + " 128 4294967295 32 0"};
+    w.detail = "f32 mfma 32x32 tile=256x256 bk=16 4 waves of 128x128, direct-to-LDS ring (whole tiles, M, N >= 4096, K % 32 == 0, K >= 128)" + orient;
+    GemmKernel v;
+    v.suffix = "_v";
+    v.block = 1024;
+    v.grid = {M + "/256", N + "/256"};
+    v.when = {M + " 4096 4294967295 1 0", N + " 4096 4294967295 1 0"};
+    v.unless = w.when;
+    v.detail = "f32 mfma 32x32 tile=256x256 bk=16 16 waves, two LDS buffers (M, N >= 4096)" + orient;
     GemmKernel k;
-    k.grid = {g.dims[m.m].name + "/128", g.dims[m.n].name + "/128"};
-    k.unless = w.when;
+    k.grid = {M + "/128", N + "/128"};
+    k.unless = v.when;
     k.detail = "f32 mfma 32x32 tile=128x128 bk=16 4 waves, two LDS buffers" + orient;
     out->kernels.push_back(w);
+    out->kernels.push_back(v);
     out->kernels.push_back(k);
     return true;
   }

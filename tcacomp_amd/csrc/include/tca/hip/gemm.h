@@ -8,7 +8,8 @@
 //                 (gemm_bf16_4w when K % 64 == 0 and K >= 256, else
 //                 gemm_bf16_256_w8), v_mfma_f32_32x32x16_bf16 on the edge
 //                 tiles (gemm_bf16_256); fp32 accumulate
-//   fp32 inputs : v_mfma_f32_32x32x2f32, fp32 accumulate
+//   fp32 inputs : v_mfma_f32_32x32x2f32 (gemm_f32_4w on whole tiles from
+//                 M, N >= 4096 on, else gemm_f32_tile), fp32 accumulate
 // Geometry of the register-staged kernels: a 256-thread workgroup (4 waves,
 // 2x2) owns a BMxBN tile of C, each wave a (BM/2)x(BN/2) sub-tile of 32x32
 // MFMA blocks. K advances in
@@ -30,6 +31,7 @@
 #include <stdint.h>
 
 #include <type_traits>
+#include <utility>
 
 namespace tca {
 namespace hip {
@@ -1027,6 +1029,211 @@ __device__ __forceinline__ void gemm_f32_tile(const float* __restrict__ A, const
         const uint32_t r = m0 + wm + i * 32u + 8u * (e >> 2) + 4u * (lane >> 5) + (e & 3);
         const uint32_t c = n0 + wn + j * 32u + (lane & 31u);
         if (r < M && c < N) C[static_cast<uint64_t>(r) * N + c] = epi(acc[i][j][e], r, c);
+      }
+}
+
+// ------------------------------------- fp32 path, 4 waves, 128x128 per wave
+// Whole 256x256 tiles with K % 32 == 0 and K >= 128 (the launch guards pick
+// this kernel from M, N >= 4096 on): 256 threads, one wave per SIMD, each
+// wave a 128x128 sub-tile of C as 4x4 blocks of v_mfma_f32_32x32x2f32,
+// accumulators in AGPRs (256 per lane) through inline-asm MFMAs (the same
+// scheme and hazard coverage as gemm_bf16_4w), about 150 VGPRs.
+// LDS: a ring of 4 slots of 16-deep slices loaded straight from global
+// memory (global_load_lds_dwordx4): A (and an [n][k] B) as [256][16] with
+// the 16-byte chunk c of row r at c ^ ((r / 4) % 4), a [k][n] B as [16][264]
+// (rows padded to 1056 bytes: the fragment read of rows k and k + 4 covers
+// the 64 banks once). 133 KiB in all.
+// Slice s: wait until slot s+1 has landed and every read of slot s has
+// completed, one barrier, then 128 MFMAs on the fragments of slot s (read
+// during slice s-1) while this slice reads all fragments of slot s+1 and
+// loads slice s+4 into slot s's buffer.
+// The 2-deep MFMA step (h, e) of a slice (h 0..1, e 0..3) takes k = 8h + e on
+// lanes 0-31 and k = 8h + 4 + e on lanes 32-63, so a lane reads the four k
+// of its row it needs for four steps with one 16-byte read (an [n][k] B
+// too; a [k][n] B as four 4-byte reads). Every k of the slice is summed once;
+// the order of the sums differs from gemm_f32_tile's.
+// Measured interleaved with gemm_f32_tile<.., 256, 256> at 4096^3 (rotated
+// inputs, one box): 945-947 against 1030-1033 us, 145.3 against 133.3
+// TFLOP/s; the error against a float64 sum of the same products 6.95e-5
+// against 8.37e-5 on 64 sampled elements.
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ void mfma32_f32_acc(f32x16_t& c, float a, float b) {
+  asm volatile("v_mfma_f32_32x32x2_f32 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>): a step's
+// MFMAs with compile-time block indices (a loop over them is not unrolled
+// by the compiler at this size, and run-time indices put the accumulators
+// in scratch).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <bool B_NK, typename Epi>
+__device__ __forceinline__ void gemm_f32_4w(const float* __restrict__ A, const float* __restrict__ B,
+                                            float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
+  constexpr uint32_t BM = 256, BN = 256, ASL = 256u * 16u, LDBK = 264u, BSL = B_NK ? 256u * 16u : 16u * LDBK;
+  constexpr uint32_t SLOT = ASL + BSL;
+  __shared__ __attribute__((aligned(16))) float lds[4 * SLOT];
+  const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  uint32_t tm, tn;
+  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
+  if (m0 + BM > M || n0 + BN > N || K % 32u != 0u || K < 128u) return;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t wm = (wave >> 1) * 128u, wn = (wave & 1u) * 128u;
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc[i][j]));
+  asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  // A wave-load (1 KiB) fills 16 rows of a [256][16] slice, or one k row of
+  // a [16][264] slice; wave w fills rows 16(4w) .. 16(4w+3)+15, or k rows
+  // 4w .. 4w+3. Per-lane element offsets (the inverse of the chunk swizzle).
+  uint32_t offa[4], offb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t row = 16u * (4u * wave + q) + (lane >> 2);
+    offa[q] = row * K + 4u * ((lane & 3u) ^ ((row >> 2) & 3u));
+    if constexpr (B_NK) offb[q] = offa[q];
+    else offb[q] = (4u * wave + q) * N + 4u * lane;
+  }
+  float* ldsp = lds;
+  auto a_slot = [&](uint32_t s) { return ldsp + (s & 3u) * SLOT; };
+  auto b_slot = [&](uint32_t s) { return ldsp + (s & 3u) * SLOT + ASL; };
+  auto load = [&](int q, uint32_t s) {  // q 0..3: A rows, q 4..7: B rows
+    const uint32_t k0 = s * 16u;
+    if (q < 4) {
+      const float* a0 = A + static_cast<uint64_t>(m0) * K + k0;
+      __builtin_amdgcn_global_load_lds(a0 + offa[q], (lds_void*)(a_slot(s) + (4u * wave + q) * 256u), 16, 0, 0);
+    } else if constexpr (B_NK) {
+      const float* b0 = B + static_cast<uint64_t>(n0) * K + k0;
+      __builtin_amdgcn_global_load_lds(b0 + offb[q - 4], (lds_void*)(b_slot(s) + (4u * wave + q - 4) * 256u), 16, 0, 0);
+    } else {
+      const float* b0 = B + static_cast<uint64_t>(k0) * N + n0;
+      __builtin_amdgcn_global_load_lds(b0 + offb[q - 4], (lds_void*)(b_slot(s) + (4u * wave + q - 4) * LDBK), 16, 0, 0);
+    }
+  };
+  auto rd_a = [&](uint32_t s, uint32_t i, uint32_t h) {  // rows wm + 32i + lane%32, k 8h + 4(lane/32) .. +3
+    const float* As = a_slot(s);
+    const uint32_t row = wm + 32u * i + (lane & 31u), c = 2u * h + (lane >> 5);
+    return *reinterpret_cast<const f32x4_t*>(&As[row * 16u + 4u * (c ^ ((row >> 2) & 3u))]);
+  };
+  auto rd_b = [&](uint32_t s, uint32_t j, uint32_t h) {  // columns wn + 32j + lane%32, the same k
+    const float* Bs = b_slot(s);
+    const uint32_t col = wn + 32u * j + (lane & 31u);
+    if constexpr (B_NK) {
+      const uint32_t c = 2u * h + (lane >> 5);
+      return *reinterpret_cast<const f32x4_t*>(&Bs[col * 16u + 4u * (c ^ ((col >> 2) & 3u))]);
+    } else {
+      const uint32_t k = 8u * h + 4u * (lane >> 5);
+      f32x4_t v;
+      v[0] = Bs[(k + 0u) * LDBK + col];
+      v[1] = Bs[(k + 1u) * LDBK + col];
+      v[2] = Bs[(k + 2u) * LDBK + col];
+      v[3] = Bs[(k + 3u) * LDBK + col];
+      return v;
+    }
+  };
+  f32x4_t fa0[4][2], fb0[4][2], fa1[4][2], fb1[4][2];  // two fragment sets: this slice's and the next one's
+  auto fence = []() { __builtin_amdgcn_sched_barrier(0); };
+  auto barrier = [&]() {
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  auto step = [&](auto set, uint32_t s, int wait_vm, bool rd, bool ld) {
+    auto& ca = decltype(set)::value == 0 ? fa0 : fa1;
+    auto& cb = decltype(set)::value == 0 ? fb0 : fb1;
+    auto& na = decltype(set)::value == 0 ? fa1 : fa0;
+    auto& nb = decltype(set)::value == 0 ? fb1 : fb0;
+    if (wait_vm >= 0) {
+      asm volatile("" ::: "memory");
+      if (wait_vm == 16) __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 0));
+      else if (wait_vm == 8) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
+      else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+      barrier();
+    }
+    const uint32_t ns = s + 1u;
+    fence();
+    // MFMA c (0..127): 2-deep step t = c/16 (h = t/4, e = t%4), block (i, j)
+    // snaking over 4x4. The next slot's 8 A and 8 B fragment reads follow
+    // MFMAs 0..15, the 8 loads of slice s+4 MFMAs 55, 63, ..., 111.
+    static_for<128>([&](auto ic) {
+      constexpr int c = decltype(ic)::value;
+      constexpr int t = c >> 4, h = t >> 2, e = t & 3, b = c & 15, i = b >> 2, j = (i & 1) ? 3 - (b & 3) : (b & 3);
+      mfma32_f32_acc(acc[i][j], ca[i][h][e], cb[j][h][e]);
+      fence();
+      if constexpr (c < 16) {
+        if (rd) {
+          if constexpr (c < 8) na[c >> 1][c & 1] = rd_a(ns, c >> 1, c & 1);
+          else nb[(c - 8) >> 1][(c - 8) & 1] = rd_b(ns, (c - 8) >> 1, (c - 8) & 1);
+        }
+        fence();
+      }
+      if constexpr (c >= 55 && (c - 55) % 8 == 0 && (c - 55) / 8 < 8) {
+        if (ld) load((c - 55) / 8, s + 4u);
+        fence();
+      }
+    });
+  };
+  using Set0 = std::integral_constant<int, 0>;
+  using Set1 = std::integral_constant<int, 1>;
+  const uint32_t nk = K / 16u;
+  for (uint32_t s = 0; s < 4; ++s)
+    for (int q = 0; q < 8; ++q) load(q, s);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(24, 0));  // slice 0 landed
+  barrier();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      fa0[i][h] = rd_a(0, i, h);
+      fb0[i][h] = rd_b(0, i, h);
+    }
+  // At the start of slice s slot s+1 must have landed: the loads of slices
+  // s+2 and s+3 may remain (16; vmcnt counts in issue order). The loop runs
+  // at least once (K >= 128): a path around it kept the zeroed accumulators
+  // live across an edge and spilled them.
+  const uint32_t main_end = nk - 4u;  // even (K % 32 == 0), at least 4
+  uint32_t s = 0;
+  do {
+    step(Set0{}, s, 16, true, true);
+    step(Set1{}, s + 1, 16, true, true);
+    s += 2;
+  } while (s < main_end);
+  step(Set0{}, nk - 4u, 16, true, false);
+  step(Set1{}, nk - 3u, 8, true, false);
+  step(Set0{}, nk - 2u, 0, true, false);
+  step(Set1{}, nk - 1u, -1, false, false);
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  // 32 wait states: a 16-pass XDL write before the epilogue reads the AGPRs.
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  // acc[i][j][e] = C[r][c], r = m0 + wm + 32i + 8(e/4) + 4(lane/32) + e%4, c = n0 + wn + 32j + lane%32.
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t r = m0 + wm + i * 32u + 8u * (e >> 2) + 4u * (lane >> 5) + (e & 3);
+        const uint32_t c = n0 + wn + j * 32u + (lane & 31u);
+        C[static_cast<uint64_t>(r) * N + c] = epi(acc[i][j][e], r, c);
       }
 }
 

@@ -275,6 +275,34 @@ def test_bf16_gemm_kernel_selection(M, N, K, want):
     assert sel == want, (M, N, K, sel)
 
 
+@pytest.mark.parametrize("M,N,K,want", [
+    (4096, 4096, 4096, ["_w"]),      # whole tiles, K % 32 == 0, K >= 128: the 4-wave direct-to-LDS kernel
+    (4096, 4096, 128, ["_w"]),
+    (4352, 4608, 160, ["_w"]),
+    (4096, 4096, 96, ["_v"]),        # K < 128: the 16-wave 256x256 kernel
+    (4096, 4096, 4112, ["_v"]),      # K % 32 == 16
+    (4100, 4096, 4096, ["_v"]),      # a partial row of tiles
+    (4096, 4100, 4096, ["_v"]),
+    (4095, 4096, 4096, [""]),        # below 4096: 128x128 tiles
+    (1024, 8192, 4096, [""]), (512, 512, 0, [""])])
+def test_f32_gemm_kernel_selection(M, N, K, want):
+    """The fp32 contraction's three kernels, exactly one launched: the 4-wave
+    direct-to-LDS kernel when M, N >= 4096 and every tile is whole (M, N
+    multiples of 256, K % 32 == 0, K >= 128), the 16-wave 256x256 kernel for
+    the other shapes from M, N >= 4096 on, 128x128 tiles below."""
+    e = programs.CONFIG_PROGRAMS["gemm_f32"]().emit()
+    rc, h = parse(e.plan)
+    assert rc == 0, _lib.last_error()
+    arr = compiler._descriptors([TensorDesc(0x1000, (M, K), 0), TensorDesc(0x1000, (K, N), 0),
+                                 TensorDesc(0x1000, (M, N), 0)])
+    syms = e.kernel_symbols()
+    out = (ctypes.c_uint8 * len(syms))()
+    grids = (ctypes.c_uint64 * len(syms))()
+    assert _lib.lib().tca_program_selected(h, arr, 3, None, 0, out, grids, None, len(syms)) == 0, _lib.last_error()
+    sel = [s[len("tca_gemm_f32_k0"):] for s, f, g in zip(syms, out, grids) if f and g]
+    assert sel == want, (M, N, K, sel)
+
+
 def test_unless_guard_parse():
     for rec, ok in [("unless M 0 16 4 0", True), ("unless M 0 16 0 0", False), ("unless Q 0 16 4 0", False),
                     ("unless M 0 16", False)]:
@@ -490,7 +518,7 @@ def test_program_launch_without_module_is_refused():
 
 EXPECTED_FAMILIES = {
     "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"] * 3,
-    "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"] * 2, "gemm_bf16": ["gemm"] * 3,
+    "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"] * 3, "gemm_bf16": ["gemm"] * 3,
     "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 12, "softmax_dyn": ["stream"] * 6,
     "layernorm_dyn": ["stream"] * 6, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 6,
     # narrow rows: one more width per halving of the element size (8 bf16, 16 u8 elements per vector)
@@ -644,10 +672,10 @@ def _gemm_asm(name, tmp_path):
     return asm.read_text().split("\n")
 
 
-@pytest.mark.parametrize("name", ["gemm_bf16", "gemm_bf16_nt"])
+@pytest.mark.parametrize("name", ["gemm_bf16", "gemm_bf16_nt", "gemm_f32", "gemm_f32_nt"])
 def test_dma_gemm_reloads_nothing_from_scratch(name, tmp_path):
-    """The bf16 contraction's main loop waits on hand-counted vmcnt values
-    for its direct-to-LDS loads; a register spill reloaded from scratch while
+    """The contractions' direct-to-LDS main loops wait on hand-counted vmcnt
+    values for their loads; a register spill reloaded from scratch while
     they are in flight would share that counter (an fp32 port that spilled
     computed wrong results). From the first direct-to-LDS load to the end of
     that path (its s_endpgm) nothing may be reloaded from scratch; the
@@ -685,16 +713,17 @@ def _vgpr_writes(line):
     return regs if kind == "v" else set()
 
 
-@pytest.mark.parametrize("name", ["gemm_bf16", "gemm_bf16_nt"])
+@pytest.mark.parametrize("name", ["gemm_bf16", "gemm_bf16_nt", "gemm_f32", "gemm_f32_nt"])
 def test_asm_mfma_kernel_hazards_covered(name, tmp_path):
-    """The 4-wave bf16 contraction issues its MFMAs as inline asm, which the
+    """The 4-wave contractions issue their MFMAs as inline asm, which the
     compiler's hazard recogniser does not model. Checked on its gfx950
     assembly: every MFMA accumulates in place in AGPRs (dst == SrcC); every
     MFMA A/B operand register reaches the MFMA from a ds_read only (along
     the straight line and around the main loop's back edge), never from a
     VALU write; the AGPR zero-init is followed by two s_nop 7 before the
     first MFMA; three s_nop 7 separate the last MFMA from the first
-    instruction that reads an AGPR outside an MFMA."""
+    instruction that reads an AGPR outside an MFMA (an 8-pass bf16 MFMA
+    needs 11 wait states there, a 16-pass fp32 one 19)."""
     lines = _gemm_asm(name, tmp_path)
     sym = "tca_%s_k0_w:" % name
     start = next(i for i, l in enumerate(lines) if l.startswith(sym))

@@ -268,14 +268,17 @@ def test_c5_gemm_exact_integers(gpu, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 64), (4100, 4104, 40), (4352, 4096, 16), (4097, 4096, 33),
-                                   (4096, 4101, 48), (4095, 4096, 48), (2100, 3000, 40), (1000, 4224, 33)])
+                                   (4096, 4101, 48), (4095, 4096, 48), (2100, 3000, 40), (1000, 4224, 33),
+                                   (4096, 4096, 128), (4352, 4608, 160), (4096, 4352, 224)])
 @pytest.mark.parametrize("nt", [False, True])
 def test_c5_gemm_f32_large_exact(gpu, M, N, K, nt):
     """fp32 contractions at C5's scale with ragged edges (M, N not multiples
     of the tile, K not a multiple of the 16-deep slice, unaligned rows), B as
-    [K][N] and as [N][K], on both tile sizes: 256x256 (16 waves) from M, N >=
-    4096 on, 128x128 (4 waves) below. Small-integer operands make every
-    result exact, so every tile, slice and edge must be exact."""
+    [K][N] and as [N][K], on all three kernels: from M, N >= 4096 on the
+    4-wave direct-to-LDS kernel when every tile is whole (K % 32 == 0,
+    K >= 128; here its shortest main loops) and 256x256 tiles with 16 waves
+    otherwise, 128x128 tiles below. Small-integer operands make every result
+    exact, so every tile, slice and edge must be exact."""
     _say("C5 f32 large", M, N, K, "nt" if nt else "")
     rng = np.random.default_rng(M + N + K)
     a = rng.integers(-4, 5, (M, K)).astype(np.float32)
@@ -284,8 +287,9 @@ def test_c5_gemm_f32_large_exact(gpu, M, N, K, nt):
     name = "gemm_f32_nt" if nt else "gemm_f32"
     p = compiled(name)
     big = M >= 4096 and N >= 4096
+    whole = big and M % 256 == 0 and N % 256 == 0 and K % 32 == 0 and K >= 128
     assert p.selected_symbols([TensorDesc(0x1000, (M, K), 0), TensorDesc(0x1000, (N, K) if nt else (K, N), 0),
-                               TensorDesc(0x1000, (M, N), 0)]) == ["tca_%s_k0%s" % (name, "_w" if big else "")]
+                               TensorDesc(0x1000, (M, N), 0)]) == ["tca_%s_k0%s" % (name, "_w" if whole else "_v" if big else "")]
     c = out_dev((M, N), gpu)
     bd = np.ascontiguousarray(b.T) if nt else b
     run(p, [to_dev(a, gpu), to_dev(bd, gpu), c])
@@ -331,7 +335,7 @@ def test_c5_full_size_bf16(gpu):
     assert math.isfinite(float(got.sum()))
 
 
-@pytest.mark.parametrize("name", ["gemm_f32", "gemm_bf16", "gemm_bf16_nt"])
+@pytest.mark.parametrize("name", ["gemm_f32", "gemm_f32_nt", "gemm_bf16", "gemm_bf16_nt"])
 def test_c5_full_size_exact(gpu, name):
     """C5's full shape, 4096^3, on small-integer operands in [-4, 4]: exact
     in bf16 and fp32, every product exact and every partial sum an integer
@@ -346,6 +350,8 @@ def test_c5_full_size_exact(gpu, name):
     want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
     if name == "gemm_f32":
         ta, tb = to_dev(a, gpu), to_dev(b, gpu)
+    elif name == "gemm_f32_nt":
+        ta, tb = to_dev(a, gpu), to_dev(np.ascontiguousarray(b.T), gpu)
     else:
         bb = oracle.to_bf16_bits(b)
         if name == "gemm_bf16_nt":
