@@ -124,3 +124,19 @@ if __name__ == "__main__":
     sys.path.insert(0, REPO)
     out = build_all(force_kernels="--force" in sys.argv)
     print("built %s and %d code object(s)" % (LIB, len(out)))
+
+
+CLI = os.path.join(PKG_DIR, "bin", "tcacomp")
+CLI_OUT = os.path.join(PKG_DIR, "_cli_out")
+CONFIGS_TCA = os.path.join(PKG_DIR, "tca", "configs.tca")
+
+
+def build_cli(jobs=8):
+    """Builds the compiler driver (cmd/tcacomp.c) and runs it the way a user
+    would: `tcacomp compile -o _cli_out tca/configs.tca`, then `make` in the
+    output directory, leaving <kernel>.{hip,plan,hsaco} for every kernel of
+    the configurations' .tca module."""
+    _run(["make", "-s", "-C", os.path.join(CSRC, "..", "cmd")])
+    _run([CLI, "compile", "-o", CLI_OUT, CONFIGS_TCA])
+    _run(["make", "-s", "-j%d" % jobs, "-C", CLI_OUT])
+    return CLI_OUT
