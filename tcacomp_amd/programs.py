@@ -20,6 +20,8 @@ Configurations (BASELINE.json):
 Reference suite (testing/kernels/**.tca, shapes in testing/suite.toml): see
 SUITE below.
 """
+import os
+
 from .pkg import (TBF16, TF16, TF32, TI32, TU8, TU32, At, Call, Cast, NewBuilder, Select)
 
 
@@ -576,6 +578,88 @@ SUITE = {
 # Programs build() precompiles: (factory, emit flags). The generic-family
 # variants (fusion and MFMA disabled) exist so tests can check every family
 # against the same oracle.
+# ---- the reference's own end-to-end programs (internal/e2e, pkg) ---------
+# Each is the graph of one of the reference's numerical e2e tests, written
+# through the pkg rungs; tests/test_gpu_e2e.py runs them on the reference's
+# shapes and inputs (elem(i), testing/runners/common.cuh:19-21) against its
+# CPU references and tolerance (internal/e2e/e2e_test.go:20, reduceTol 2e-3).
+
+def e2e_redwarp():
+    """out[r] = sum_c lhs[r][c]: the reduce_warp golden's graph
+    (internal/e2e/e2e_test.go:134-179 runner, reduceReference :227-240), which
+    TestReduceT1E2E also lowers (internal/e2e/reduce3_test.go:255-266)."""
+    b = NewBuilder("redwarp")
+    R, C = b.Dim("d0", 0), b.Dim("d1", 0)
+    lhs = b.Tensor("lhs", TF32, R, C)
+    out = b.Tensor("out", TF32, R)
+    b.Stmt().Iter(R, C).Map([At(lhs, R, C)], lambda v: v).As(R, C).Reduce(b.Float32(0), _sum(b)).Store(out, R)
+    return b.Build()
+
+
+def e2e_reduce3():
+    """out[i][j] = sum_k lhs[i][j][k], the rank-3 last-axis reduce
+    (internal/e2e/reduce3_test.go:81-117 graph, reduce3Reference :288-300)."""
+    b = NewBuilder("red3")
+    d0, d1, d2 = b.Dim("d0", 0), b.Dim("d1", 0), b.Dim("d2", 0)
+    lhs = b.Tensor("lhs", TF32, d0, d1, d2)
+    out = b.Tensor("out", TF32, d0, d1)
+    (b.Stmt().Iter(d0, d1, d2).Map([At(lhs, d0, d1, d2)], lambda v: v).As(d0, d1, d2)
+     .Reduce(b.Float32(0), _sum(b)).Store(out, d0, d1))
+    return b.Build()
+
+
+def e2e_matmul_store():
+    """out[m][n][k] = lhs[m][k] * rhs[n][k]: the matmul_store golden's graph
+    (the MmLaunch signature, internal/e2e/e2e_test.go:69-71; matmulReference
+    :202-225), a rank-3 map with broadcast operands and no reduction."""
+    b = NewBuilder("mm")
+    d0, d1, d2 = b.Dim("d0", 0), b.Dim("d1", 0), b.Dim("d2", 0)
+    lhs = b.Tensor("lhs", TF32, d0, d2)
+    rhs = b.Tensor("rhs", TF32, d1, d2)
+    out = b.Tensor("out", TF32, d0, d1, d2)
+    (b.Stmt().Iter(d0, d1, d2).Map([At(lhs, d0, d2), At(rhs, d1, d2)], lambda l, r: b.Mul(l, r))
+     .As(d0, d1, d2).Store(out, d0, d1, d2))
+    return b.Build()
+
+
+def e2e_matmul_scale():
+    """output[m][k] = scale * sum_n lhs[m][n] * rhs[n][k]: the doc-pinned
+    oracle program built through the public builder (pkg/oracle_test.go:17-53),
+    the frontend matmul_scale's semantics (internal/e2e/frontend_test.go:
+    194-208)."""
+    b = NewBuilder("matmul_scale")
+    m, k, n = b.Dim("m", 0), b.Dim("k", 0), b.Dim("n", 0)
+    lhs, rhs = b.Tensor("lhs", TF32, m, n), b.Tensor("rhs", TF32, n, k)
+    out = b.Tensor("output", TF32, m, k)
+    scale = b.ScalarParam("scale", TF32)
+    (b.Stmt().Iter(m, k, n).Map([At(lhs, m, n), At(rhs, n, k)], lambda l, r: b.Mul(l, r)).As(m, k, n)
+     .Reduce(b.Float32(0), lambda a, v: b.Add(a, v)).Map([], lambda v: b.Mul(v, scale)).As(m, k)
+     .Store(out, m, k))
+    return b.Build()
+
+
+def _tca_kernel(path):
+    def build():
+        from . import syntax
+        return syntax.ParseModule(path).Kernels[0].Build()
+    return build
+
+
+E2E_TCA_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tca", "e2e")
+
+E2E = {
+    "redwarp": e2e_redwarp,
+    "red3": e2e_reduce3,
+    "mm": e2e_matmul_store,
+    "matmul_scale_pkg": e2e_matmul_scale,
+    # the frontend fixture in both forms of its root map (as clause written,
+    # and inferred), compiled from .tca text (internal/e2e/frontend_test.go:
+    # 340-396)
+    "matmul_scale_written": _tca_kernel(os.path.join(E2E_TCA_DIR, "matmul_scale_written.tca")),
+    "matmul_scale_omitted": _tca_kernel(os.path.join(E2E_TCA_DIR, "matmul_scale_omitted.tca")),
+}
+
+
 CONFIG_PROGRAMS = {
     "chain_sum_max": chain_sum_max,
     "chain_total": chain_total,
@@ -633,6 +717,8 @@ def all_builds():
         out.append((name, f, 0))
     for name, (f, _, _) in sorted(SUITE.items()):
         out.append(("suite_" + name, f, 0))
+    for name, f in sorted(E2E.items()):
+        out.append(("e2e_" + name, f, 0))
     # generic-family lowering of the configs (cross-family parity)
     for name in ("scale_relu", "row_sum_max_1000", "softmax_200", "layernorm_96", "gemm_f32", "chain_sum_max",
                  "chain_total", "chain3_max_total"):
