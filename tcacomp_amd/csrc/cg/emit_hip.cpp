@@ -1092,6 +1092,26 @@ class Emitter {
       }
       return val;
     };
+    // The element body with every operand's value given by `val(piped, k)`.
+    auto bodyWith = [&](std::ostringstream& os, const std::string& ind,
+                        const std::function<std::string(bool piped, int k)>& val) -> std::string {
+      ExprGen eg(g_, os, ind, &counter_);
+      for (size_t k = 0; k < c.root.ops.size(); ++k) eg.Bind(c.root.fn.params[k], val(false, static_cast<int>(k)));
+      std::string v = eg.Gen(c.root.fn.body);
+      for (const auto& r : c.reduces) {
+        ExprGen rg(g_, os, ind, &counter_);
+        rg.Bind(r.fn.params[0], rg.Gen(r.init));
+        rg.Bind(r.fn.params[1], v);
+        v = rg.Gen(r.fn.body);
+      }
+      if (c.has_piped) {
+        ExprGen pg(g_, os, ind, &counter_);
+        pg.Bind(c.piped.fn.params[0], v);
+        for (size_t k = 0; k < c.piped.ops.size(); ++k) pg.Bind(c.piped.fn.params[k + 1], val(true, static_cast<int>(k)));
+        v = pg.Gen(c.piped.fn.body);
+      }
+      return v;
+    };
     // Fast path: the whole strip is in range.
     o << "  if (base + " << (kUnroll - 1) * kVec * kBlock + kVec - 1 << "u < n) {\n";
     for (size_t k = 0; k < c.root.ops.size(); ++k) {
@@ -1120,22 +1140,103 @@ class Emitter {
         << op.tensor << " + base + u * " << kVec * kBlock << "u);\n";
     }
     o << "    }\n";
-    o << "#pragma unroll\n    for (uint32_t u = 0; u < " << kUnroll << "u; ++u) {\n";
-    o << "      tca::hip::vec<" << CType(st.elem) << ", " << kVec << "> out{};\n";
-    o << "#pragma unroll\n      for (uint32_t q = 0; q < " << kVec << "u; ++q) {\n";
-    o << "        const uint64_t e = base + u * " << kVec * kBlock << "u + q;\n";
-    {
+    // Operands not aligned with the store (broadcast or permuted), when the
+    // innermost store extent is a multiple of the vector width (a uniform
+    // test at run time): a vector never crosses a row, so its coordinates are
+    // decomposed once, an operand whose last index is the innermost axis
+    // (contiguous there) is one vector load, and an operand that does not
+    // depend on that axis is one scalar load per vector.
+    const int lastAxis = outAxes.empty() ? -1 : outAxes.back();
+    const bool rowVecPath = anyUnaligned && lastAxis >= 0 && kVec > 1;
+    enum class OpCls { Aligned, RowVec, Bcast, Other };
+    auto classify = [&](const ir::Operand& op, bool aligned) {
+      if (aligned) return OpCls::Aligned;
+      int at = -1, uses = 0;
+      for (size_t i = 0; i < op.axes.size(); ++i)
+        if (op.axes[i] == lastAxis) {
+          at = static_cast<int>(i);
+          ++uses;
+        }
+      if (uses == 0) return OpCls::Bcast;
+      if (uses > 1) return OpCls::Other;
+      for (size_t i = static_cast<size_t>(at) + 1; i < op.axes.size(); ++i)
+        if (g_.dims[op.axes[i]].extent != 1) return OpCls::Other;
+      // One load of at most 16 bytes (the tensor alignment the launcher checks).
+      if (kVec * ir::ElemBytes(g_.tensors[op.tensor].elem) > 16) return OpCls::Other;
+      return OpCls::RowVec;
+    };
+    auto emitComputeLoop = [&](const std::string& ind, bool rowvec) {
+      o << "#pragma unroll\n" << ind << "for (uint32_t u = 0; u < " << kUnroll << "u; ++u) {\n";
+      std::ostringstream pre;
+      std::function<std::string(bool, int, const std::function<std::string(int)>&)> opVal;
+      if (rowvec) {
+        const std::string in2 = ind + "  ";
+        pre << in2 << "const uint64_t v = base + u * " << kVec * kBlock << "u;\n";
+        coordDecl(pre, in2, "v");
+        auto coordV = [&](int a) -> std::string {
+          if (g_.dims[a].extent == 1) return "0u";
+          return "c" + std::to_string(a) + "_v";
+        };
+        auto preload = [&](bool piped, size_t k, const ir::Operand& op, OpCls cls) {
+          const std::string T = CType(g_.tensors[op.tensor].elem);
+          const std::string nm = std::string(piped ? "rp" : "ra") + std::to_string(k);
+          if (cls == OpCls::RowVec)
+            pre << in2 << "const auto " << nm << " = tca::hip::load_vec<" << T << ", " << kVec << ">(t" << op.tensor
+                << " + " << Offset(op.tensor, op.axes, coordV) << ");\n";
+          else if (cls == OpCls::Bcast)
+            pre << in2 << "const " << T << " " << nm << " = t" << op.tensor << "[" << Offset(op.tensor, op.axes, coordV)
+                << "];\n";
+        };
+        for (size_t k = 0; k < c.root.ops.size(); ++k) preload(false, k, c.root.ops[k], classify(c.root.ops[k], rootAligned[k]));
+        for (size_t k = 0; k < pipedAligned.size(); ++k)
+          preload(true, k, c.piped.ops[k], classify(c.piped.ops[k], pipedAligned[k]));
+        opVal = [&](bool piped, int k, const std::function<std::string(int)>& coordQ) -> std::string {
+          const auto& op = piped ? c.piped.ops[k] : c.root.ops[k];
+          const OpCls cls = classify(op, piped ? pipedAligned[k] : rootAligned[k]);
+          const std::string nm = std::string(piped ? "rp" : "ra") + std::to_string(k);
+          switch (cls) {
+            case OpCls::Aligned: return std::string(piped ? "p" : "a") + std::to_string(k) + "[u][q]";
+            case OpCls::RowVec: return nm + "[q]";
+            case OpCls::Bcast: return nm;
+            case OpCls::Other: break;
+          }
+          return "t" + std::to_string(op.tensor) + "[" + Offset(op.tensor, op.axes, coordQ) + "]";
+        };
+      }
+      o << pre.str();
+      o << ind << "  tca::hip::vec<" << CType(st.elem) << ", " << kVec << "> out{};\n";
+      o << "#pragma unroll\n" << ind << "  for (uint32_t q = 0; q < " << kVec << "u; ++q) {\n";
       std::ostringstream bodyS;
-      std::string val = body(bodyS, Indent(4), "e", [&](bool piped, int k) {
-        return std::string(piped ? "p" : "a") + std::to_string(k) + "[u][q]";
-      });
+      std::string val;
+      if (rowvec) {
+        auto coordQ = [&](int a) -> std::string {
+          if (g_.dims[a].extent == 1) return "0u";
+          if (a == lastAxis) return "(c" + std::to_string(a) + "_v + q)";
+          return "c" + std::to_string(a) + "_v";
+        };
+        val = bodyWith(bodyS, ind + "    ", [&](bool piped, int k) { return opVal(piped, k, coordQ); });
+      } else {
+        o << ind << "    const uint64_t e = base + u * " << kVec * kBlock << "u + q;\n";
+        val = body(bodyS, ind + "    ", "e", [&](bool piped, int k) {
+          return std::string(piped ? "p" : "a") + std::to_string(k) + "[u][q]";
+        });
+      }
       o << bodyS.str();
-      o << "        out.set(q, " << val << ");\n";
+      o << ind << "    out.set(q, " << val << ");\n";
+      o << ind << "  }\n";
+      o << ind << "  tca::hip::store_vec_nt<" << CType(st.elem) << ", " << kVec << ">(t" << c.store_tensor
+        << " + base + u * " << kVec * kBlock << "u, out);\n";
+      o << ind << "}\n";
+    };
+    if (rowVecPath) {
+      o << "    if (" << ExtentExpr(g_, lastAxis) << " % " << kVec << "u == 0u) {\n";
+      emitComputeLoop("      ", true);
+      o << "    } else {\n";
+      emitComputeLoop("      ", false);
+      o << "    }\n";
+    } else {
+      emitComputeLoop("    ", false);
     }
-    o << "      }\n";
-    o << "      tca::hip::store_vec_nt<" << CType(st.elem) << ", " << kVec << ">(t" << c.store_tensor
-      << " + base + u * " << kVec * kBlock << "u, out);\n";
-    o << "    }\n";
     o << "  } else {\n";
     o << "    for (uint32_t u = 0; u < " << kUnroll << "u; ++u) {\n";
     o << "      for (uint32_t q = 0; q < " << kVec << "u; ++q) {\n";

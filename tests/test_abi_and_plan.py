@@ -880,3 +880,33 @@ def test_split_rows_device_matches_plan_at_the_u32_edge(device_helpers, R, C):
         assert hi <= U32 and lo == covered and hi - lo > 1024
         covered = hi
     assert covered == vecs
+
+
+def _bias_program():
+    """y[r][c] = x[r][c] * g[c] + b[r], plus z[c][r] read transposed."""
+    from tcacomp_amd.pkg import TF32, At, NewBuilder
+    bld = NewBuilder("ew_bcast")
+    R, C = bld.Dim("R", 0), bld.Dim("C", 0)
+    x, z = bld.Tensor("x", TF32, R, C), bld.Tensor("z", TF32, C, R)
+    g, b = bld.Tensor("g", TF32, C), bld.Tensor("b", TF32, R)
+    y = bld.Tensor("y", TF32, R, C)
+    (bld.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(g, C), At(b, R), At(z, C, R)], lambda v, w, u, t: bld.Add(bld.Add(bld.Mul(v, w), u), t))
+     .As(R, C).Store(y, R, C))
+    return bld.Build()
+
+
+def test_elementwise_broadcast_operands_take_the_row_vector_path():
+    # With the innermost extent a multiple of the vector width (tested at run
+    # time), coordinates are decomposed once per vector: g[c] is one vector
+    # load, b[r] one scalar load, z[c][r] is read per element at c + q; x is
+    # aligned with the store and keeps its streamed vector load.
+    src = _bias_program().emit().source
+    assert "if (d1 % 4u == 0u) {" in src
+    # tensors in declaration order: x t0, z t1, g t2, b t3
+    assert "const auto ra1 = tca::hip::load_vec<float, 4>(t2 + c1_v);" in src
+    assert "const float ra2 = t3[c0_v];" in src
+    assert "t1[((c1_v + q)) * d0 + c0_v]" in src
+    assert "a0[u] = tca::hip::load_vec_nt<float, 4>(t0 + base + u * 1024u);" in src
+    # An elementwise map whose operands all align with the store is unchanged.
+    assert "% 4u == 0u" not in programs.CONFIG_PROGRAMS["scale_relu_map"]().emit().source
