@@ -1003,10 +1003,235 @@ class Emitter {
 
   // E: flat streaming over the stored tensor; operands whose non-unit axes
   // match the store's are read with 16-byte vector loads, others by index.
+  // ---- elementwise maps with transposed operands: 64x64 tiles through LDS
+  // An operand contiguous along the second-innermost store axis P (its last
+  // index) while the store is contiguous along the innermost axis L is read
+  // across rows by a flat strip: every lane a different cache line. Here a
+  // 256-thread block owns a 64 (P) x 64 (L) output tile. Each such operand's
+  // [64 L][64 P] tile is read with 16-byte loads along P, staged in LDS rows
+  // of 65 floats (the odd stride puts the 64 lanes of both the row-wise
+  // writes and the column-wise reads on 64 distinct banks), and read back
+  // transposed; the output, and operands aligned with it along L, move as
+  // 16-byte vectors along L. 4-byte element types only, at most 4 such
+  // operands (66 KiB of LDS).
+  static constexpr int kTrTile = 64, kTrStride = 65, kTrMax = 4;
+
+  enum class TileCls { Aligned, RowVec, Bcast, Tr, Other };
+
+  // The class of operand `op` in a tile over (P, L).
+  TileCls TileClass(const ir::Operand& op, const std::vector<int>& outAxes, int P, int L) const {
+    if (DropUnit(g_, op.axes) == outAxes) return TileCls::Aligned;
+    int atL = -1, atP = -1, usesL = 0, usesP = 0;
+    for (size_t i = 0; i < op.axes.size(); ++i) {
+      if (op.axes[i] == L) atL = static_cast<int>(i), ++usesL;
+      if (op.axes[i] == P) atP = static_cast<int>(i), ++usesP;
+    }
+    auto lastNonUnit = [&]() {
+      for (int i = static_cast<int>(op.axes.size()) - 1; i >= 0; --i)
+        if (g_.dims[op.axes[i]].extent != 1) return i;
+      return -1;
+    };
+    const int last = lastNonUnit();
+    if (usesL == 0) return TileCls::Bcast;
+    if (usesL == 1 && last == atL) return TileCls::RowVec;
+    if (usesL == 1 && usesP == 1 && last == atP) return TileCls::Tr;
+    return TileCls::Other;
+  }
+
+  // Whether chain c takes the tiled kernel: two or more non-unit store axes,
+  // 4-byte elements throughout, and 1..kTrMax transposed operands.
+  bool TiledElementwise(const ir::Chain& c) const {
+    const std::vector<int> outAxes = DropUnit(g_, c.store_axes);
+    if (outAxes.size() < 2) return false;
+    const int L = outAxes.back(), P = outAxes[outAxes.size() - 2];
+    if (ir::ElemBytes(g_.tensors[c.store_tensor].elem) != 4) return false;
+    int tr = 0;
+    auto scan = [&](const std::vector<ir::Operand>& ops) {
+      for (const auto& op : ops) {
+        if (ir::ElemBytes(g_.tensors[op.tensor].elem) != 4) return false;
+        if (TileClass(op, outAxes, P, L) == TileCls::Tr) ++tr;
+      }
+      return true;
+    };
+    if (!scan(c.root.ops)) return false;
+    if (c.has_piped && !scan(c.piped.ops)) return false;
+    return tr >= 1 && tr <= kTrMax;
+  }
+
+  bool EmitElementwiseTiled(int ni) {
+    const Nest& n = an_.nests[ni];
+    const ir::Chain& c = g_.chains[n.chains[0]];
+    const std::vector<int> outAxes = DropUnit(g_, c.store_axes);
+    const int L = outAxes.back(), P = outAxes[outAxes.size() - 2];
+    const std::vector<int> outer(outAxes.begin(), outAxes.end() - 2);
+    PlanKernel pk;
+    pk.symbol = Sym(g_, prefix_, ni);
+    pk.block = 256;
+    pk.grid.push_back(DimProduct(outer) + "/1");
+    pk.grid.push_back(g_.dims[P].name + "/" + std::to_string(kTrTile));
+    pk.grid.push_back(g_.dims[L].name + "/" + std::to_string(kTrTile));
+    const std::string sig = Signature(n, &pk);
+    std::ostringstream& o = src_;
+    const ir::Tensor& st = g_.tensors[c.store_tensor];
+    const std::string sT = CType(st.elem), EL = ExtentExpr(g_, L), EP = ExtentExpr(g_, P);
+    struct OpRef {
+      bool piped;
+      int k;
+      const ir::Operand* op;
+      TileCls cls;
+      int tile;  // LDS tile index of a Tr operand
+    };
+    std::vector<OpRef> ops;
+    int nTiles = 0;
+    for (size_t k = 0; k < c.root.ops.size(); ++k) {
+      const TileCls cls = TileClass(c.root.ops[k], outAxes, P, L);
+      ops.push_back({false, static_cast<int>(k), &c.root.ops[k], cls, cls == TileCls::Tr ? nTiles++ : -1});
+    }
+    if (c.has_piped)
+      for (size_t k = 0; k < c.piped.ops.size(); ++k) {
+        const TileCls cls = TileClass(c.piped.ops[k], outAxes, P, L);
+        ops.push_back({true, static_cast<int>(k), &c.piped.ops[k], cls, cls == TileCls::Tr ? nTiles++ : -1});
+      }
+    auto find = [&](bool piped, int k) -> const OpRef& {
+      for (const auto& r : ops)
+        if (r.piped == piped && r.k == k) return r;
+      return ops.front();
+    };
+    o << "// statement #" << n.chains[0] << ": elementwise family, " << kTrTile << "x" << kTrTile
+      << " tiles, " << nTiles << " transposed operand(s) staged in LDS\n";
+    o << "extern \"C\" __global__ void __launch_bounds__(256) " << pk.symbol << "(\n    " << sig << ") {\n";
+    o << "  __shared__ uint32_t tr_lds[" << nTiles << "][" << kTrTile * kTrStride << "];\n";
+    o << "  const uint32_t nl = tca::hip::ceil_div(" << EL << ", " << kTrTile << "u), np = tca::hip::ceil_div(" << EP
+      << ", " << kTrTile << "u);\n";
+    o << "  uint32_t bid = blockIdx.x;\n";
+    o << "  const uint32_t l0 = (bid % nl) * " << kTrTile << "u; bid /= nl;\n";
+    o << "  const uint32_t p0 = (bid % np) * " << kTrTile << "u; bid /= np;\n";
+    for (int i = static_cast<int>(outer.size()) - 1; i >= 0; --i)
+      o << "  const uint32_t c" << outer[i] << " = bid % " << ExtentExpr(g_, outer[i]) << "; bid /= "
+        << ExtentExpr(g_, outer[i]) << ";\n";
+    o << "  const uint32_t tr = threadIdx.x / 16u, tc = threadIdx.x % 16u;\n";
+    // Coordinates: L and P spelled by the caller, outer axes c<a>, unit 0.
+    auto coordFn = [&](const std::string& l, const std::string& p) {
+      return [this, l, p, L, P](int a) -> std::string {
+        if (g_.dims[a].extent == 1) return "0u";
+        if (a == L) return l;
+        if (a == P) return p;
+        return "c" + std::to_string(a);
+      };
+    };
+    // 1. Transposed operands: rows l0 + tr + 16i of the [L][P] tile, 4 P values each.
+    o << "  const bool p_vec = " << EP << " % 4u == 0u;\n";
+    for (const auto& r : ops) {
+      if (r.cls != TileCls::Tr) continue;
+      const std::string T = CType(g_.tensors[r.op->tensor].elem), t = "t" + std::to_string(r.op->tensor);
+      o << "#pragma unroll\n  for (uint32_t i = 0; i < 4u; ++i) {\n";
+      o << "    const uint32_t lr = tr + 16u * i, l = l0 + lr, p = p0 + 4u * tc;\n";
+      o << "    uint32_t* row = &tr_lds[" << r.tile << "][lr * " << kTrStride << "u + 4u * tc];\n";
+      o << "    if (l < " << EL << " && p_vec && p + 3u < " << EP << ") {\n";
+      o << "      const auto v = tca::hip::load_vec<" << T << ", 4>(" << t << " + "
+        << Offset(r.op->tensor, r.op->axes, coordFn("l", "p")) << ");\n";
+      o << "#pragma unroll\n      for (uint32_t j = 0; j < 4u; ++j) row[j] = __builtin_bit_cast(uint32_t, v[j]);\n";
+      o << "    } else {\n";
+      o << "      for (uint32_t j = 0; j < 4u; ++j)\n";
+      o << "        if (l < " << EL << " && p + j < " << EP << ") row[j] = __builtin_bit_cast(uint32_t, " << t << "["
+        << Offset(r.op->tensor, r.op->axes, coordFn("l", "(p + j)")) << "]);\n";
+      o << "    }\n  }\n";
+    }
+    o << "  __syncthreads();\n";
+    // 2. Output rows p0 + tr + 16i, 4 L values each.
+    o << "  const bool l_vec = " << EL << " % 4u == 0u;\n";
+    o << "#pragma unroll\n  for (uint32_t i = 0; i < 4u; ++i) {\n";
+    o << "    const uint32_t pr = tr + 16u * i, p = p0 + pr, lb = l0 + 4u * tc;\n";
+    o << "    if (p >= " << EP << ") continue;\n";
+    auto trVal = [&](const OpRef& r, const std::string& lr) {
+      return "__builtin_bit_cast(" + CType(g_.tensors[r.op->tensor].elem) + ", tr_lds[" + std::to_string(r.tile) +
+             "][(" + lr + ") * " + std::to_string(kTrStride) + "u + pr])";
+    };
+    // Whole vector along L.
+    o << "    if (l_vec && lb + 3u < " << EL << ") {\n";
+    {
+      std::ostringstream pre;
+      for (const auto& r : ops) {
+        const std::string T = CType(g_.tensors[r.op->tensor].elem), t = "t" + std::to_string(r.op->tensor);
+        const std::string nm = std::string(r.piped ? "tp" : "ta") + std::to_string(r.k);
+        if (r.cls == TileCls::Aligned || r.cls == TileCls::RowVec)
+          pre << "      const auto " << nm << " = tca::hip::load_vec<" << T << ", 4>(" << t << " + "
+              << Offset(r.op->tensor, r.op->axes, coordFn("lb", "p")) << ");\n";
+        else if (r.cls == TileCls::Bcast)
+          pre << "      const " << T << " " << nm << " = " << t << "["
+              << Offset(r.op->tensor, r.op->axes, coordFn("lb", "p")) << "];\n";
+      }
+      o << pre.str();
+      o << "      tca::hip::vec<" << sT << ", 4> out{};\n";
+      o << "#pragma unroll\n      for (uint32_t q = 0; q < 4u; ++q) {\n";
+      std::ostringstream bodyS;
+      std::string val = TiledBody(c, bodyS, Indent(4), [&](bool piped, int k) -> std::string {
+        const OpRef& r = find(piped, k);
+        const std::string nm = std::string(piped ? "tp" : "ta") + std::to_string(k);
+        switch (r.cls) {
+          case TileCls::Aligned:
+          case TileCls::RowVec: return nm + "[q]";
+          case TileCls::Bcast: return nm;
+          case TileCls::Tr: return trVal(r, "4u * tc + q");
+          case TileCls::Other: break;
+        }
+        return "t" + std::to_string(r.op->tensor) + "[" + Offset(r.op->tensor, r.op->axes, coordFn("(lb + q)", "p")) + "]";
+      });
+      o << bodyS.str();
+      o << "        out.set(q, " << val << ");\n";
+      o << "      }\n";
+      o << "      tca::hip::store_vec_nt<" << sT << ", 4>(t" << c.store_tensor << " + "
+        << Offset(c.store_tensor, c.store_axes, coordFn("lb", "p")) << ", out);\n";
+    }
+    // Ragged edge or L not a multiple of 4: element by element.
+    o << "    } else {\n";
+    o << "      for (uint32_t q = 0; q < 4u; ++q) {\n";
+    o << "        if (lb + q >= " << EL << ") break;\n";
+    {
+      std::ostringstream bodyS;
+      std::string val = TiledBody(c, bodyS, Indent(4), [&](bool piped, int k) -> std::string {
+        const OpRef& r = find(piped, k);
+        if (r.cls == TileCls::Tr) return trVal(r, "4u * tc + q");
+        return "t" + std::to_string(r.op->tensor) + "[" + Offset(r.op->tensor, r.op->axes, coordFn("(lb + q)", "p")) + "]";
+      });
+      o << bodyS.str();
+      o << "        t" << c.store_tensor << "[" << Offset(c.store_tensor, c.store_axes, coordFn("(lb + q)", "p"))
+        << "] = " << val << ";\n";
+    }
+    o << "      }\n    }\n  }\n}\n\n";
+    AddKernel(pk, Family::Elementwise, n.chains,
+              "tile=" + std::to_string(kTrTile) + "x" + std::to_string(kTrTile) + " lds_tiles=" + std::to_string(nTiles) +
+                  " block=256");
+    return true;
+  }
+
+  // The element body of chain c (root map, degenerate reduces, piped map)
+  // with operand values from `val(piped, k)`.
+  std::string TiledBody(const ir::Chain& c, std::ostringstream& os, const std::string& ind,
+                        const std::function<std::string(bool, int)>& val) {
+    ExprGen eg(g_, os, ind, &counter_);
+    for (size_t k = 0; k < c.root.ops.size(); ++k) eg.Bind(c.root.fn.params[k], val(false, static_cast<int>(k)));
+    std::string v = eg.Gen(c.root.fn.body);
+    for (const auto& r : c.reduces) {
+      ExprGen rg(g_, os, ind, &counter_);
+      rg.Bind(r.fn.params[0], rg.Gen(r.init));
+      rg.Bind(r.fn.params[1], v);
+      v = rg.Gen(r.fn.body);
+    }
+    if (c.has_piped) {
+      ExprGen pg(g_, os, ind, &counter_);
+      pg.Bind(c.piped.fn.params[0], v);
+      for (size_t k = 0; k < c.piped.ops.size(); ++k) pg.Bind(c.piped.fn.params[k + 1], val(true, static_cast<int>(k)));
+      v = pg.Gen(c.piped.fn.body);
+    }
+    return v;
+  }
+
   bool EmitElementwise(int ni, std::string* err) {
     (void)err;
     const Nest& n = an_.nests[ni];
     const ir::Chain& c = g_.chains[n.chains[0]];
+    if (TiledElementwise(c)) return EmitElementwiseTiled(ni);
     PlanKernel pk;
     pk.symbol = Sym(g_, prefix_, ni);
     // Elements per vector: 16 bytes of the widest tensor moved in vectors

@@ -882,31 +882,58 @@ def test_split_rows_device_matches_plan_at_the_u32_edge(device_helpers, R, C):
     assert covered == vecs
 
 
-def _bias_program():
-    """y[r][c] = x[r][c] * g[c] + b[r], plus z[c][r] read transposed."""
+def _bias_program(transposed=True):
+    """y[r][c] = x[r][c] * g[c] + b[r] (+ z[c][r], read transposed)."""
     from tcacomp_amd.pkg import TF32, At, NewBuilder
-    bld = NewBuilder("ew_bcast")
+    bld = NewBuilder("ew_bcast" if transposed else "ew_bias")
     R, C = bld.Dim("R", 0), bld.Dim("C", 0)
-    x, z = bld.Tensor("x", TF32, R, C), bld.Tensor("z", TF32, C, R)
+    x = bld.Tensor("x", TF32, R, C)
+    z = bld.Tensor("z", TF32, C, R) if transposed else None
     g, b = bld.Tensor("g", TF32, C), bld.Tensor("b", TF32, R)
     y = bld.Tensor("y", TF32, R, C)
-    (bld.Stmt().Iter(R, C)
-     .Map([At(x, R, C), At(g, C), At(b, R), At(z, C, R)], lambda v, w, u, t: bld.Add(bld.Add(bld.Mul(v, w), u), t))
-     .As(R, C).Store(y, R, C))
+    ops = [At(x, R, C), At(g, C), At(b, R)] + ([At(z, C, R)] if transposed else [])
+    if transposed:
+        body = lambda v, w, u, t: bld.Add(bld.Add(bld.Mul(v, w), u), t)  # noqa: E731
+    else:
+        body = lambda v, w, u: bld.Add(bld.Mul(v, w), u)  # noqa: E731
+    bld.Stmt().Iter(R, C).Map(ops, body).As(R, C).Store(y, R, C)
     return bld.Build()
 
 
 def test_elementwise_broadcast_operands_take_the_row_vector_path():
     # With the innermost extent a multiple of the vector width (tested at run
     # time), coordinates are decomposed once per vector: g[c] is one vector
-    # load, b[r] one scalar load, z[c][r] is read per element at c + q; x is
-    # aligned with the store and keeps its streamed vector load.
-    src = _bias_program().emit().source
+    # load, b[r] one scalar load; x is aligned with the store and keeps its
+    # streamed vector load.
+    src = _bias_program(False).emit().source
+    # tensors in declaration order: x t0, g t1, b t2, y t3
     assert "if (d1 % 4u == 0u) {" in src
-    # tensors in declaration order: x t0, z t1, g t2, b t3
-    assert "const auto ra1 = tca::hip::load_vec<float, 4>(t2 + c1_v);" in src
-    assert "const float ra2 = t3[c0_v];" in src
-    assert "t1[((c1_v + q)) * d0 + c0_v]" in src
+    assert "const auto ra1 = tca::hip::load_vec<float, 4>(t1 + c1_v);" in src
+    assert "const float ra2 = t2[c0_v];" in src
     assert "a0[u] = tca::hip::load_vec_nt<float, 4>(t0 + base + u * 1024u);" in src
     # An elementwise map whose operands all align with the store is unchanged.
     assert "% 4u == 0u" not in programs.CONFIG_PROGRAMS["scale_relu_map"]().emit().source
+
+
+def test_elementwise_transposed_operand_takes_the_lds_tile_kernel():
+    # z[c][r] under y[r][c]: 64x64 tiles, z staged through LDS rows of 65
+    # words, read back transposed; the grid is (outer) x ceil(R/64) x ceil(C/64).
+    e = _bias_program(True).emit()
+    src = e.source
+    # tensors in declaration order: x t0, z t1, g t2, b t3, y t4
+    assert "__shared__ uint32_t tr_lds[1][4160];" in src
+    assert "tca::hip::load_vec<float, 4>(t1 + (l) * d0 + p)" in src
+    assert "tr_lds[0][(4u * tc + q) * 65u + pr]" in src
+    assert "tca::hip::store_vec_nt<float, 4>(t4 + (p) * d1 + lb, out);" in src
+    assert "kernel tca_ew_bcast_k0 256 0 3 1/1 R/64 C/64" in e.plan
+    ptr = 0x1000
+    for R, C, grid in ((1000, 1000, 16 * 16), (64, 4100, 1 * 65), (0, 5, 0), (5, 70001, 1 * 1094)):
+        prog = compiler.CompiledProgram("ew_bcast", e, "")
+        ts = [TensorDesc(ptr if R * C else 0, (R, C), 0), TensorDesc(ptr if R * C else 0, (C, R), 0),
+              TensorDesc(ptr if C else 0, (C,), 0), TensorDesc(ptr if R else 0, (R,), 0),
+              TensorDesc(ptr if R * C else 0, (R, C), 0)]
+        arr = compiler._descriptors(ts)
+        sel = (ctypes.c_uint8 * 1)()
+        grids = (ctypes.c_uint64 * 1)()
+        _lib.check(_lib.lib().tca_program_selected(prog.parsed(), arr, 5, None, 0, sel, grids, None, 1))
+        assert grids[0] == grid, (R, C, grids[0])
