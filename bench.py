@@ -60,6 +60,12 @@ CONFIGS = {
     # C5 bf16 at 8192^3: not a configuration; four tiles per CU instead of one, so the C epilogue
     # and the ring's fill weigh a quarter as much
     "c5b8": ("gemm_bf16", "gemm bf16 -> f32 8192^3 (not a configuration)"),
+    # elementwise maps whose operands are not aligned with the store: not
+    # configurations. y = x*g + b + z^T (z read transposed through LDS tiles),
+    # and the reference's matmul_store e2e program out[m][n][k] = lhs[m][k] *
+    # rhs[n][k] (broadcast operands read per vector; 4 GiB written)
+    "c1t": ("ew_bias_tr", "y = x*g[c] + b[r] + z^T f32 [8192,8192] (elementwise, transposed operand via LDS tiles)"),
+    "c1m": ("e2e:mm", "out[m][n][k] = lhs[m][k]*rhs[n][k] f32 1024^3 (elementwise, broadcast operands)"),
     # not a configuration: the plain copy used to calibrate rocprof counters
     "copy": ("copy_f32", "copy f32 [8192,8192] (counter calibration)"),
 }
@@ -82,7 +88,8 @@ def _setup(key, dev):
     from tcacomp_amd import inputs, programs, compiler
 
     name = CONFIGS[key][0]
-    prog = compiler.compile_program(programs.CONFIG_PROGRAMS[name](), jit=os.environ.get("TCA_JIT", "0") != "0")
+    factory = programs.E2E[name[4:]] if name.startswith("e2e:") else programs.CONFIG_PROGRAMS[name]
+    prog = compiler.compile_program(factory(), jit=os.environ.get("TCA_JIT", "0") != "0")
     streamed = key in STREAM_OF
     key = STREAM_OF.get(key, key)
 
@@ -136,6 +143,25 @@ def _setup(key, dev):
             scalars = [0.37]
         per_set = algo
         work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = None
+    elif key == "c1t":
+        R = C = 8192
+        x, z = inputs.uniform((R, C), -1, 1, 0), inputs.uniform((C, R), -1, 1, 1)
+        g, bt = inputs.uniform((C,), -1, 1, 2), inputs.uniform((R,), -1, 1, 3)
+        algo = 3 * R * C * 4 + (R + C) * 4
+        per_set = algo
+        make = lambda i: [dev_f32(x), dev_f32(z), dev_f32(g), dev_f32(bt), torch.empty((R, C), device=dev)]  # noqa: E731
+        scalars = []
+        work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = None
+    elif key == "c1m":
+        d = 1024
+        lhs, rhs = inputs.uniform((d, d), 0, 1, 0), inputs.uniform((d, d), 0, 1, 1)
+        algo = d * d * d * 4 + 2 * d * d * 4
+        per_set = algo
+        make = lambda i: [dev_f32(lhs), dev_f32(rhs), torch.empty((d, d, d), device=dev)]  # noqa: E731
+        scalars = []
+        work = {"bytes": algo, "bound": "hbm", "shape": [d, d, d]}
         cpu = None
     elif key == "copy":
         R = C = 8192
@@ -373,7 +399,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c2h,c2u,c2c,c2mv,c2mw,c5b8")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c2h,c2u,c2c,c2mv,c2mw,c5b8,c1t,c1m")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
                     help="untimed launches per config before the warmup steps, in wall-clock ms")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")

@@ -1119,18 +1119,56 @@ class Emitter {
         return "c" + std::to_string(a);
       };
     };
-    // 1. Transposed operands: rows l0 + tr + 16i of the [L][P] tile, 4 P values each.
+    // 1. Output rows p0 + tr + 16i, 4 L values each. The operands read
+    // straight from memory are loaded first, so their latency overlaps the
+    // tile's (whose LDS writes wait for its own loads).
+    o << "  const bool l_vec = " << EL << " % 4u == 0u;\n";
+    o << "  const uint32_t lb = l0 + 4u * tc;\n";
+    o << "  bool full[4];\n";
+    for (const auto& r : ops) {
+      const std::string T = CType(g_.tensors[r.op->tensor].elem);
+      const std::string nm = std::string(r.piped ? "tp" : "ta") + std::to_string(r.k);
+      if (r.cls == TileCls::Aligned || r.cls == TileCls::RowVec)
+        o << "  tca::hip::vec<" << T << ", 4> " << nm << "[4];\n";
+      else if (r.cls == TileCls::Bcast)
+        o << "  " << T << " " << nm << "[4];\n";
+    }
+    o << "#pragma unroll\n  for (uint32_t i = 0; i < 4u; ++i) {\n";
+    o << "    const uint32_t p = p0 + tr + 16u * i;\n";
+    o << "    full[i] = p < " << EP << " && l_vec && lb + 3u < " << EL << ";\n";
+    o << "    if (full[i]) {\n";
+    for (const auto& r : ops) {
+      const std::string T = CType(g_.tensors[r.op->tensor].elem), t = "t" + std::to_string(r.op->tensor);
+      const std::string nm = std::string(r.piped ? "tp" : "ta") + std::to_string(r.k);
+      // Aligned operands are read once (streamed); row-contiguous ones are
+      // re-read by every row of the grid.
+      if (r.cls == TileCls::Aligned || r.cls == TileCls::RowVec)
+        o << "      " << nm << "[i] = tca::hip::load_vec" << (r.cls == TileCls::Aligned ? "_nt" : "") << "<" << T
+          << ", 4>(" << t << " + " << Offset(r.op->tensor, r.op->axes, coordFn("lb", "p")) << ");\n";
+      else if (r.cls == TileCls::Bcast)
+        o << "      " << nm << "[i] = " << t << "[" << Offset(r.op->tensor, r.op->axes, coordFn("lb", "p")) << "];\n";
+    }
+    o << "    }\n  }\n";
+    // 2. Transposed operands: rows l0 + tr + 16i of the [L][P] tile, 4 P values each.
     o << "  const bool p_vec = " << EP << " % 4u == 0u;\n";
     for (const auto& r : ops) {
       if (r.cls != TileCls::Tr) continue;
       const std::string T = CType(g_.tensors[r.op->tensor].elem), t = "t" + std::to_string(r.op->tensor);
+      const std::string zv = "zv" + std::to_string(r.tile), zf = "zf" + std::to_string(r.tile);
+      // All four row loads first, then the LDS writes (which wait for them).
+      o << "  tca::hip::vec<" << T << ", 4> " << zv << "[4];\n  bool " << zf << "[4];\n";
+      o << "#pragma unroll\n  for (uint32_t i = 0; i < 4u; ++i) {\n";
+      o << "    const uint32_t l = l0 + tr + 16u * i, p = p0 + 4u * tc;\n";
+      o << "    " << zf << "[i] = l < " << EL << " && p_vec && p + 3u < " << EP << ";\n";
+      o << "    if (" << zf << "[i]) " << zv << "[i] = tca::hip::load_vec_nt<" << T << ", 4>(" << t << " + "
+        << Offset(r.op->tensor, r.op->axes, coordFn("l", "p")) << ");\n";
+      o << "  }\n";
       o << "#pragma unroll\n  for (uint32_t i = 0; i < 4u; ++i) {\n";
       o << "    const uint32_t lr = tr + 16u * i, l = l0 + lr, p = p0 + 4u * tc;\n";
       o << "    uint32_t* row = &tr_lds[" << r.tile << "][lr * " << kTrStride << "u + 4u * tc];\n";
-      o << "    if (l < " << EL << " && p_vec && p + 3u < " << EP << ") {\n";
-      o << "      const auto v = tca::hip::load_vec<" << T << ", 4>(" << t << " + "
-        << Offset(r.op->tensor, r.op->axes, coordFn("l", "p")) << ");\n";
-      o << "#pragma unroll\n      for (uint32_t j = 0; j < 4u; ++j) row[j] = __builtin_bit_cast(uint32_t, v[j]);\n";
+      o << "    if (" << zf << "[i]) {\n";
+      o << "#pragma unroll\n      for (uint32_t j = 0; j < 4u; ++j) row[j] = __builtin_bit_cast(uint32_t, " << zv
+        << "[i][j]);\n";
       o << "    } else {\n";
       o << "      for (uint32_t j = 0; j < 4u; ++j)\n";
       o << "        if (l < " << EL << " && p + j < " << EP << ") row[j] = __builtin_bit_cast(uint32_t, " << t << "["
@@ -1138,30 +1176,17 @@ class Emitter {
       o << "    }\n  }\n";
     }
     o << "  __syncthreads();\n";
-    // 2. Output rows p0 + tr + 16i, 4 L values each.
-    o << "  const bool l_vec = " << EL << " % 4u == 0u;\n";
+    // 3. Compute and store.
     o << "#pragma unroll\n  for (uint32_t i = 0; i < 4u; ++i) {\n";
-    o << "    const uint32_t pr = tr + 16u * i, p = p0 + pr, lb = l0 + 4u * tc;\n";
+    o << "    const uint32_t pr = tr + 16u * i, p = p0 + pr;\n";
     o << "    if (p >= " << EP << ") continue;\n";
     auto trVal = [&](const OpRef& r, const std::string& lr) {
       return "__builtin_bit_cast(" + CType(g_.tensors[r.op->tensor].elem) + ", tr_lds[" + std::to_string(r.tile) +
              "][(" + lr + ") * " + std::to_string(kTrStride) + "u + pr])";
     };
     // Whole vector along L.
-    o << "    if (l_vec && lb + 3u < " << EL << ") {\n";
+    o << "    if (full[i]) {\n";
     {
-      std::ostringstream pre;
-      for (const auto& r : ops) {
-        const std::string T = CType(g_.tensors[r.op->tensor].elem), t = "t" + std::to_string(r.op->tensor);
-        const std::string nm = std::string(r.piped ? "tp" : "ta") + std::to_string(r.k);
-        if (r.cls == TileCls::Aligned || r.cls == TileCls::RowVec)
-          pre << "      const auto " << nm << " = tca::hip::load_vec<" << T << ", 4>(" << t << " + "
-              << Offset(r.op->tensor, r.op->axes, coordFn("lb", "p")) << ");\n";
-        else if (r.cls == TileCls::Bcast)
-          pre << "      const " << T << " " << nm << " = " << t << "["
-              << Offset(r.op->tensor, r.op->axes, coordFn("lb", "p")) << "];\n";
-      }
-      o << pre.str();
       o << "      tca::hip::vec<" << sT << ", 4> out{};\n";
       o << "#pragma unroll\n      for (uint32_t q = 0; q < 4u; ++q) {\n";
       std::ostringstream bodyS;
@@ -1170,8 +1195,8 @@ class Emitter {
         const std::string nm = std::string(piped ? "tp" : "ta") + std::to_string(k);
         switch (r.cls) {
           case TileCls::Aligned:
-          case TileCls::RowVec: return nm + "[q]";
-          case TileCls::Bcast: return nm;
+          case TileCls::RowVec: return nm + "[i][q]";
+          case TileCls::Bcast: return nm + "[i]";
           case TileCls::Tr: return trVal(r, "4u * tc + q");
           case TileCls::Other: break;
         }

@@ -578,6 +578,21 @@ SUITE = {
 # Programs build() precompiles: (factory, emit flags). The generic-family
 # variants (fusion and MFMA disabled) exist so tests can check every family
 # against the same oracle.
+def ew_bias_tr():
+    """y[r][c] = x[r][c] * g[c] + b[r] + z[c][r]: an elementwise map with an
+    aligned, a column-broadcast, a row-broadcast and a transposed operand (the
+    transposed one staged through LDS tiles)."""
+    b = NewBuilder("ew_bias_tr")
+    R, C = b.Dim("R", 0), b.Dim("C", 0)
+    x, z = b.Tensor("x", TF32, R, C), b.Tensor("z", TF32, C, R)
+    g, bb = b.Tensor("g", TF32, C), b.Tensor("b", TF32, R)
+    y = b.Tensor("y", TF32, R, C)
+    (b.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(g, C), At(bb, R), At(z, C, R)], lambda v, w, u, t: b.Add(b.Add(b.Mul(v, w), u), t))
+     .As(R, C).Store(y, R, C))
+    return b.Build()
+
+
 # ---- the reference's own end-to-end programs (internal/e2e, pkg) ---------
 # Each is the graph of one of the reference's numerical e2e tests, written
 # through the pkg rungs; tests/test_gpu_e2e.py runs them on the reference's
@@ -686,6 +701,8 @@ CONFIG_PROGRAMS = {
     "layernorm_96": lambda: layernorm(96),
     "softmax_16384": lambda: softmax(16384),
     "copy_f32": copy_f32,
+    # an elementwise map with broadcast and transposed operands
+    "ew_bias_tr": ew_bias_tr,
     # the same nests with the row length a run-time dim: the streaming family
     "row_sum_max_dyn": lambda: row_sum_max(0),
     "softmax_dyn": lambda: softmax(0),

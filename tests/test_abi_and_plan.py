@@ -922,7 +922,7 @@ def test_elementwise_transposed_operand_takes_the_lds_tile_kernel():
     src = e.source
     # tensors in declaration order: x t0, z t1, g t2, b t3, y t4
     assert "__shared__ uint32_t tr_lds[1][4160];" in src
-    assert "tca::hip::load_vec<float, 4>(t1 + (l) * d0 + p)" in src
+    assert "tca::hip::load_vec_nt<float, 4>(t1 + (l) * d0 + p)" in src
     assert "tr_lds[0][(4u * tc + q) * 65u + pr]" in src
     assert "tca::hip::store_vec_nt<float, 4>(t4 + (p) * d1 + lb, out);" in src
     assert "kernel tca_ew_bcast_k0 256 0 3 1/1 R/64 C/64" in e.plan
