@@ -1960,7 +1960,7 @@ class Emitter {
     const uint32_t lgBlock = 31 - __builtin_clz(kBlock), lgMin = 31 - __builtin_clz(kMinBlock);
     o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
     o << "  const uint32_t VECS = C / V;\n";
-    o << "  const uint32_t LS = tca::hip::pack_lanes_log2(VECS, " << kCache << "u, " << lgBlock
+    o << "  const uint32_t LS = tca::hip::pack_lanes_log2(VECS, NV > 0u ? NV : " << kCache << "u, " << lgBlock
       << "u);  // S = 2^LS lanes per row\n";
     o << "  const uint32_t LB = LS > " << lgMin << "u ? LS : " << lgMin << "u;  // the block: 2^LB = max(" << kMinBlock
       << ", S) lanes\n";
@@ -2422,19 +2422,29 @@ class Emitter {
       widths.push_back({vmax, vmax, 0});
       for (uint32_t v = vmax / 2; v >= 1; v /= 2) widths.push_back({v, 2 * v, v});
     }
-    const uint64_t cachedVecs = uint64_t{kBlock} * kCache;
+    // A nest of several passes re-reads a streamed row once per pass; longer
+    // rows stay in registers for it: 8 vectors per lane of a 1024-lane block
+    // (rows of up to 8192 vectors), a variant of its own (its register count
+    // is set by its cache depth; 16 vectors spilled to scratch for 16- and
+    // 8-byte vectors). A single pass reads the row once either way and keeps
+    // the 4-vector cache only.
+    std::vector<uint32_t> caches = {kCache};
+    if (passes.size() > 1) caches.push_back(2 * kCache);
+    const uint64_t cachedVecs = uint64_t{kBlock} * caches.back();
     const std::string symbol = pk.symbol;
     const std::string rowGuard =
         geo.outer.size() == 1 ? g_.dims[geo.outer[0]].name : std::string();  // the split's row-count dim
     for (const auto& w : widths) {
-      for (int cached = 1; cached >= 0; --cached) {
-        const uint64_t lo = cached ? 0 : (cachedVecs + 1) * w.v;
-        const uint64_t hi = cached ? cachedVecs * w.v : 0xffffffffull;
+      for (size_t ci = 0; ci <= caches.size(); ++ci) {
+        const bool cached = ci < caches.size();
+        const uint32_t kc = cached ? caches[ci] : 0u;
+        const uint64_t lo = !cached ? (cachedVecs + 1) * w.v : ci == 0 ? 0 : (uint64_t{kBlock} * caches[ci - 1] + 1) * w.v;
+        const uint64_t hi = cached ? uint64_t{kBlock} * kc * w.v : 0xffffffffull;
         if (!cached && split && rowGuard.empty()) continue;  // a full reduction always splits
         PlanKernel vk = pk;
-        vk.symbol = symbol + (cached ? "_c" : "_s") + std::to_string(w.v);
+        vk.symbol = symbol + (cached ? "_c" : "_s") + std::to_string(w.v) + (kc > kCache ? "x" + std::to_string(kc) : "");
         vk.block = kBlock;
-        vk.pack = cdim + " " + std::to_string(kCache * w.v) + " " + std::to_string(kMinBlock);
+        vk.pack = cdim + " " + std::to_string((cached ? kc : kCache) * w.v) + " " + std::to_string(kMinBlock);
         vk.grid.push_back(DimProduct(geo.outer) + "/pack");
         vk.when.push_back(cdim + " " + std::to_string(lo) + " " + std::to_string(hi) + " " + std::to_string(w.mod) +
                           " " + std::to_string(w.rem));
@@ -2443,16 +2453,16 @@ class Emitter {
           << ") {\n";
         if (cached) {
           o << "  const uint32_t vecs = (" << ExtentExpr(g_, geo.col) << ") / " << w.v << "u;\n";
-          o << "  const uint32_t ls = tca::hip::pack_lanes_log2(vecs, " << kCache << "u, " << lgBlock << "u);\n";
-          o << "  if (vecs == (" << kCache << "u << ls)) " << body_fn << "<" << w.v << "u, " << kCache << "u, true>(" << args
+          o << "  const uint32_t ls = tca::hip::pack_lanes_log2(vecs, " << kc << "u, " << lgBlock << "u);\n";
+          o << "  if (vecs == (" << kc << "u << ls)) " << body_fn << "<" << w.v << "u, " << kc << "u, true>(" << args
             << ");\n";
-          o << "  else " << body_fn << "<" << w.v << "u, " << kCache << "u, false>(" << args << ");\n}\n";
+          o << "  else " << body_fn << "<" << w.v << "u, " << kc << "u, false>(" << args << ");\n}\n";
         } else {
           o << "  " << body_fn << "<" << w.v << "u, 0u, false>(" << args << ");\n}\n";
         }
         std::ostringstream det;
         det << "row=runtime (" << cdim << " % " << w.mod << " == " << w.rem << ", " << lo << ".." << hi << ": "
-            << (cached ? "cached " + std::to_string(kCache) + " vectors/lane" : std::string("streamed")) << ") vec=" << w.v
+            << (cached ? "cached " + std::to_string(kc) + " vectors/lane" : std::string("streamed")) << ") vec=" << w.v
             << " lanes/row=runtime(<=" << kBlock << ") passes=" << passes.size() << " block=max(" << kMinBlock
             << ",lanes/row)";
         AddKernel(vk, Family::Stream, n.chains, det.str());

@@ -519,8 +519,8 @@ def test_program_launch_without_module_is_refused():
 EXPECTED_FAMILIES = {
     "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"] * 3,
     "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"] * 3, "gemm_bf16": ["gemm"] * 3,
-    "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 12, "softmax_dyn": ["stream"] * 6,
-    "layernorm_dyn": ["stream"] * 6, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 6,
+    "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 12, "softmax_dyn": ["stream"] * 9,
+    "layernorm_dyn": ["stream"] * 9, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 9,
     # narrow rows: one more width per halving of the element size (8 bf16, 16 u8 elements per vector)
     "row_sum_bf16_dyn": ["stream"] * 16, "row_sum_u8_dyn": ["stream"] * 20, "row_stats_u32_dyn": ["stream"] * 12,
     # column reductions: a (partial, merge) pair per vector width
@@ -937,3 +937,26 @@ def test_elementwise_transposed_operand_takes_the_lds_tile_kernel():
         grids = (ctypes.c_uint64 * 1)()
         _lib.check(_lib.lib().tca_program_selected(prog.parsed(), arr, 5, None, 0, sel, grids, None, 1))
         assert grids[0] == grid, (R, C, grids[0])
+
+
+@pytest.mark.parametrize("name", ["softmax_dyn", "layernorm_dyn", "layernorm_rstd_dyn"])
+def test_stream_row_caches_fit_registers(name, tmp_path):
+    """Nests of several passes keep rows of up to 8192 vectors in registers
+    (a variant with 8 vectors per lane of a 1024-lane block, taken above the
+    4-vector cache's 4096): every kernel of the program compiles without
+    scratch. Host-only: compiles to gfx950 assembly."""
+    lines = _gemm_asm(name, tmp_path)
+    text = "\n".join(lines)
+    names = re.findall(r"^\s+\.name:\s+(tca_\S+)", text, re.M)
+    priv = [int(v) for v in re.findall(r"\.private_segment_fixed_size: (\d+)", text)]
+    assert any(n.endswith("_c4x8") for n in names), names
+    assert len(names) == len(priv)
+    assert all(p == 0 for p in priv), [(n, p) for n, p in zip(names, priv) if p]
+    plan = programs.CONFIG_PROGRAMS[name]().emit().plan
+    # f32 rows of 4 * 4096 < C <= 4 * 8192 take the 8-deep cache; longer rows stream.
+    assert "when C 16388 32768 4 0" in plan and "when C 32772 4294967295 4 0" in plan
+
+
+def test_single_pass_stream_nest_keeps_one_cache_depth():
+    plan = programs.CONFIG_PROGRAMS["row_sum_max_dyn"]().emit().plan
+    assert "_c4x8" not in plan and "when C 16388 4294967295 4 0" in plan

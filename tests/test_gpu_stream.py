@@ -55,7 +55,14 @@ def test_stream_matches_register_family(gpu):
                         2 * np.sqrt((x.astype(np.float64) ** 2).sum(1)), C, "stream vs row")
 
 
-@pytest.mark.parametrize("C", [1, 5, 200, 4096, 4098, 12002, 16384, 20000])
+# Row lengths on both sides of every guard of the f32 variants: 4-vector cache
+# (V 4: C <= 16384, V 2: <= 8192, V 1: <= 4096), 8-vector cache (V 4: <= 32768,
+# V 2: <= 16384, V 1: <= 8192), streamed beyond.
+STREAM_MULTIPASS_C = [1, 5, 200, 4096, 4097, 4098, 8193, 9001, 12002, 16384, 16386, 20000, 20002, 32768, 32772,
+                      40000]
+
+
+@pytest.mark.parametrize("C", STREAM_MULTIPASS_C)
 @pytest.mark.parametrize("R", [1, 37])
 def test_stream_softmax(gpu, R, C):
     _say("stream C3", R, C)
@@ -70,7 +77,7 @@ def test_stream_softmax(gpu, R, C):
     assert np.abs(got.astype(np.float64).sum(1) - 1.0).max() <= reduce_tol(C)
 
 
-@pytest.mark.parametrize("C", [3, 96, 1024, 4097, 5000, 8194, 16384, 20000])
+@pytest.mark.parametrize("C", [3, 96, 1024, 5000, 8194] + STREAM_MULTIPASS_C[4:])
 @pytest.mark.parametrize("R", [1, 37])
 def test_stream_layernorm(gpu, R, C):
     _say("stream C4", R, C)
