@@ -246,12 +246,13 @@ bool Parse(const std::string& text, Plan* out, std::string* err) {
     } else if (kw == "when" || kw == "unless") {
       if (p.kernels.empty()) return bad(kw + " before any kernel");
       Guard g;
-      if (tok.size() != 6 || !ParseU64(tok[2], &g.lo) || !ParseU64(tok[3], &g.hi) || !ParseU64(tok[4], &g.mod) ||
-          !ParseU64(tok[5], &g.rem))
-        return bad(kw + " <dim> <lo> <hi> <mod> <rem>");
+      g.pow2 = tok.size() == 7 && tok[6] == "pow2";
+      if ((tok.size() != 6 && !g.pow2) || !ParseU64(tok[2], &g.lo) || !ParseU64(tok[3], &g.hi) ||
+          !ParseU64(tok[4], &g.mod) || !ParseU64(tok[5], &g.rem))
+        return bad(kw + " <dim> <lo> <hi> <mod> <rem> [pow2]");
       g.dim = FindDim(p, tok[1]);
       if (g.dim < 0) return bad(kw + " names unknown dim " + tok[1]);
-      if (g.mod == 0 || g.rem >= g.mod || g.lo > g.hi) return bad("bad guard on " + tok[1]);
+      if (g.mod == 0 || g.rem >= g.mod || g.lo > g.hi || (g.pow2 && g.rem != 0)) return bad("bad guard on " + tok[1]);
       (kw == "when" ? p.kernels.back().when : p.kernels.back().unless).push_back(g);
     } else if (kw == "end") {
       ended = true;
@@ -510,7 +511,10 @@ uint32_t PackRows(const Kernel& k, const std::vector<uint32_t>& dims, uint32_t* 
 bool Selected(const Kernel& k, const std::vector<uint32_t>& dims) {
   auto holds = [&](const Guard& g) {
     const uint64_t v = dims[g.dim];
-    return v >= g.lo && v <= g.hi && v % g.mod == g.rem;
+    if (!(v >= g.lo && v <= g.hi && v % g.mod == g.rem)) return false;
+    if (!g.pow2) return true;
+    const uint64_t q = v / g.mod;
+    return q != 0 && (q & (q - 1)) == 0;
   };
   for (const auto& g : k.when)
     if (!holds(g)) return false;

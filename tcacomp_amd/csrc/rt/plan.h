@@ -32,6 +32,9 @@
 //   unless <dim> <lo> <hi> <mod> <rem>  (for the last kernel) the same test; the
 //       kernel is skipped when every one of its unless guards holds (the
 //       complement of a conjunction of when guards another kernel carries).
+//       Either record may end in `pow2` (with rem 0): the guard then also
+//       requires dim / mod to be a power of two (a row of exactly mod * 2^k
+//       elements: the streaming family's exact-fit kernels).
 //   end
 //
 // The shape contract Bind() enforces is the reference launcher's
@@ -88,6 +91,7 @@ struct Arg {
 struct Guard {
   int dim = 0;  // index into Plan::dims
   uint64_t lo = 0, hi = 0xffffffffull, mod = 1, rem = 0;
+  bool pow2 = false;  // additionally dim / mod is a power of two (rem == 0)
 };
 
 struct Kernel {

@@ -83,7 +83,8 @@ def test_launch_guards():
 
 
 @pytest.mark.parametrize("R,C,variants", [
-    (3, 0, ["c4"]), (3, 64, ["c4"]), (3, 4096, ["c4"]), (3, 4100, ["c4"]), (3, 16384, ["c4"]),
+    # rows of exactly 4 * 2^k vectors take the exact-fit kernel (c4e)
+    (3, 0, ["c4"]), (3, 64, ["c4e"]), (3, 4096, ["c4e"]), (3, 4100, ["c4"]), (3, 16384, ["c4e"]), (3, 16380, ["c4"]),
     (300, 16388, ["s4"]), (3, 6, ["c2"]), (3, 2046, ["c2"]), (3, 8190, ["c2"]), (300, 8194, ["s2"]),
     (3, 1, ["c1"]), (3, 1023, ["c1"]), (3, 4095, ["c1"]), (300, 4097, ["s1"]),
     # few long rows: the split pair (partial folds, then the merge), in launch order
@@ -108,12 +109,12 @@ def test_stream_variant_selection(R, C, variants):
 
 @pytest.mark.parametrize("prog,dtype,R,C,variants", [
     # bf16 rows summed into f32: 8-element (16-byte) vectors, halved by the row length's residue
-    ("row_sum_bf16_dyn", 2, 3, 1000, ["c8"]), ("row_sum_bf16_dyn", 2, 3, 32768, ["c8"]),
+    ("row_sum_bf16_dyn", 2, 3, 1000, ["c8"]), ("row_sum_bf16_dyn", 2, 3, 32768, ["c8e"]),
     ("row_sum_bf16_dyn", 2, 300, 32776, ["s8"]), ("row_sum_bf16_dyn", 2, 3, 32776, ["p8", "m8"]),
     ("row_sum_bf16_dyn", 2, 3, 12, ["c4"]), ("row_sum_bf16_dyn", 2, 300, 16388, ["s4"]),
     ("row_sum_bf16_dyn", 2, 3, 6, ["c2"]), ("row_sum_bf16_dyn", 2, 3, 5, ["c1"]),
     # u8 rows: 16-element vectors
-    ("row_sum_u8_dyn", 7, 3, 4096, ["c16"]), ("row_sum_u8_dyn", 7, 300, 65552, ["s16"]),
+    ("row_sum_u8_dyn", 7, 3, 4096, ["c16e"]), ("row_sum_u8_dyn", 7, 300, 65552, ["s16"]),
     ("row_sum_u8_dyn", 7, 1, 65552, ["p16", "m16"]), ("row_sum_u8_dyn", 7, 3, 1000, ["c8"]),
     ("row_sum_u8_dyn", 7, 3, 20, ["c4"]), ("row_sum_u8_dyn", 7, 3, 6, ["c2"]), ("row_sum_u8_dyn", 7, 3, 0, ["c16"]),
     ("row_sum_u8_dyn", 7, 300, 4097, ["s1"])])
@@ -301,6 +302,27 @@ def test_f32_gemm_kernel_selection(M, N, K, want):
     assert _lib.lib().tca_program_selected(h, arr, 3, None, 0, out, grids, None, len(syms)) == 0, _lib.last_error()
     sel = [s[len("tca_gemm_f32_k0"):] for s, f, g in zip(syms, out, grids) if f and g]
     assert sel == want, (M, N, K, sel)
+
+
+def test_pow2_guard():
+    """`when`/`unless` ... pow2: dim % mod == 0 and dim / mod a power of two
+    (the streaming family's exact-fit kernels)."""
+    plan = ("tca-plan 1\nprogram p\ndim C 0\ntensor x f32 in 1 C\n"
+            "kernel ke 256 0 1 C/256\narg ptr x\nwhen C 0 4294967295 16 0 pow2\n"
+            "kernel kg 256 0 1 C/256\narg ptr x\nunless C 0 4294967295 16 0 pow2\nend\n")
+    rc, h = parse(plan)
+    assert rc == 0, _lib.last_error()
+    for C, want in ((0, "kg"), (16, "ke"), (32, "ke"), (48, "kg"), (64, "ke"), (16 << 20, "ke"), (17, "kg"),
+                    (16 * 1023, "kg")):
+        arr = compiler._descriptors([TensorDesc(0x1000 if C else 0, (C,), 0)])
+        out = (ctypes.c_uint8 * 2)()
+        assert _lib.lib().tca_program_selected(h, arr, 1, None, 0, out, None, None, 2) == 0, _lib.last_error()
+        assert [k for k, f in zip(("ke", "kg"), out) if f] == [want], C
+    _lib.lib().tca_program_unload(h)
+    rc, _ = parse(plan.replace("16 0 pow2", "16 1 pow2", 1))
+    assert rc == _lib.TCA_ERR_INVALID and "bad guard" in _lib.last_error()
+    rc, _ = parse(plan.replace(" pow2\n", " pow3\n", 1))
+    assert rc == _lib.TCA_ERR_INVALID and "[pow2]" in _lib.last_error()
 
 
 def test_unless_guard_parse():
@@ -519,16 +541,16 @@ def test_program_launch_without_module_is_refused():
 EXPECTED_FAMILIES = {
     "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"] * 3,
     "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"] * 3, "gemm_bf16": ["gemm"] * 3,
-    "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 12, "softmax_dyn": ["stream"] * 9,
-    "layernorm_dyn": ["stream"] * 9, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 9,
+    "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 13, "softmax_dyn": ["stream"] * 10,
+    "layernorm_dyn": ["stream"] * 10, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 10,
     # narrow rows: one more width per halving of the element size (8 bf16, 16 u8 elements per vector)
-    "row_sum_bf16_dyn": ["stream"] * 16, "row_sum_u8_dyn": ["stream"] * 20, "row_stats_u32_dyn": ["stream"] * 12,
+    "row_sum_bf16_dyn": ["stream"] * 17, "row_sum_u8_dyn": ["stream"] * 21, "row_stats_u32_dyn": ["stream"] * 13,
     # column reductions: a (partial, merge) pair per vector width
     "col_sum_max_dyn": ["col"] * 6, "col_mean_bf16": ["col"] * 8, "col_sum_u8": ["col"] * 10,
     # chained reductions split into an inner reduce into a local and an outer reduce of it; with a
     # segment dim (B) the pair also has a segment kernel per vector width, chosen from 1024 segments on
-    "chain_sum_max": ["seg"] * 3 + ["stream"] * 18, "chain_total": ["stream"] * 21,
-    "chain3_max_total": ["seg"] * 3 + ["stream"] * 27,
+    "chain_sum_max": ["seg"] * 3 + ["stream"] * 20, "chain_total": ["stream"] * 23,
+    "chain3_max_total": ["seg"] * 3 + ["stream"] * 30,
 }
 
 
