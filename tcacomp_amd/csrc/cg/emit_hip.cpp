@@ -2406,6 +2406,216 @@ class Emitter {
       }
       o << "}\n";
     }
+    // Few long rows of a nest of several passes (softmax, layernorm): each
+    // pass over its own grid of row chunks. A reduction pass is a partial
+    // kernel (a chunk of >= 2048 vectors per 1024-lane block, one partial per
+    // chunk into the [rows][512] scratch) and a merge (one wave per row: init,
+    // piped map, store); a row-map pass is one kernel writing its chunk of the
+    // row tile. Results a later pass reads come from memory: outputs where
+    // they are, register locals in plan-only locals of their own shape.
+    // Applies to nests of reduction and row-map passes only (no per-row
+    // chains, no pass reading a tile the nest produces), rows indexed by at
+    // most one axis, in the streamed range with rows <= kSplitRows.
+    bool splitMulti = passes.size() > 1 && geo.outer.size() <= 1;
+    for (const auto& ps : passes)
+      if (IsRowScalarChain(g_.chains[ps[0]], geo)) splitMulti = false;
+    for (int t : tiles)
+      if (produced.count(t)) splitMulti = false;
+    std::string smSig, smArgs;
+    std::vector<std::string> smPlanArgs;
+    std::vector<std::pair<std::string, size_t>> smFns;  // (device function, pass)
+    if (splitMulti) {
+      const std::string splitDim = "__split";
+      const std::string splitDecl = splitDim + " " + std::to_string(kMaxParts);
+      if (std::find(extra_dims_.begin(), extra_dims_.end(), splitDecl) == extra_dims_.end())
+        extra_dims_.push_back(splitDecl);
+      for (const auto& ps : passes) {
+        if (g_.chains[ps[0]].reduces.empty()) continue;
+        for (int ci : ps) {
+          const ir::Elem pe = g_.exprs[g_.chains[ci].root.fn.body].type;
+          const std::string nm = "__part" + std::to_string(ci);
+          std::string t = nm + " " + ir::ElemName(pe) + " local " + std::to_string(geo.outer.size() + 1);
+          for (int a : geo.outer) t += " " + g_.dims[a].name;
+          t += " " + splitDim;
+          if (std::find(extra_tensors_.begin(), extra_tensors_.end(), t) == extra_tensors_.end())
+            extra_tensors_.push_back(t);
+          smSig += ",\n    " + CType(pe) + "* __restrict__ p" + std::to_string(ci) + " /* " + nm + " */";
+          smArgs += ", p" + std::to_string(ci);
+          smPlanArgs.push_back("ptr " + nm);
+          // A register local gets memory of its own shape for the later passes.
+          const int st = g_.chains[ci].store_tensor;
+          if (isReg(st) && !an_.hbm_local[st]) {
+            const ir::Tensor& tt = g_.tensors[st];
+            std::string lt = tt.name + " " + ir::ElemName(tt.elem) + " local " + std::to_string(tt.dims.size());
+            for (int d : tt.dims) lt += " " + g_.dims[d].name;
+            if (std::find(extra_tensors_.begin(), extra_tensors_.end(), lt) == extra_tensors_.end())
+              extra_tensors_.push_back(lt);
+            smSig += ",\n    " + CType(tt.elem) + "* __restrict__ t" + std::to_string(st) + " /* " + tt.name +
+                     " (row results of the split passes) */";
+            smArgs += ", t" + std::to_string(st);
+            smPlanArgs.push_back("ptr " + tt.name);
+          }
+        }
+      }
+      const std::string rowExpr = ProductExpr(geo.outer);
+      // Row scalars of pass p's chains, loaded from memory; bound for elemValue.
+      auto loadRowScalars = [&](size_t p, const std::string& ind) {
+        std::set<int> done;
+        for (int ci : passes[p]) {
+          const ir::Chain& c = g_.chains[ci];
+          std::vector<const ir::Operand*> ops;
+          for (const auto& op : c.root.ops) ops.push_back(&op);
+          if (c.has_piped)
+            for (const auto& op : c.piped.ops) ops.push_back(&op);
+          for (const ir::Operand* op : ops) {
+            if (Classify(*op, geo) != OpKind::RowScalar || !done.insert(op->tensor).second) continue;
+            const std::string T = CType(g_.tensors[op->tensor].elem);
+            o << ind << "const " << T << " rs" << op->tensor << " = t" << op->tensor << "["
+              << Offset(op->tensor, op->axes, coord) << "];\n";
+            regScalar[op->tensor] = "rs" + std::to_string(op->tensor);
+          }
+        }
+      };
+      auto combsOf = [&](size_t p, const std::string& ind) {
+        for (int ci : passes[p]) {
+          const ir::Chain& c = g_.chains[ci];
+          const std::string T = CType(g_.exprs[c.root.fn.body].type);
+          o << ind << "const auto comb" << ci << " = [](" << T << " acc, " << T << " now) -> " << T << " {\n";
+          ExprGen cg(g_, o, ind + "  ", &counter_);
+          cg.Bind(c.reduces[0].fn.params[0], "acc");
+          cg.Bind(c.reduces[0].fn.params[1], "now");
+          const std::string r = cg.Gen(c.reduces[0].fn.body);
+          o << ind << "  return " << r << ";\n" << ind << "};\n";
+        }
+      };
+      auto chunkHead = [&]() {
+        o << "  constexpr uint32_t CV = " << kChunkVecs << "u, PMAX = " << kMaxParts << "u;\n";
+        o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
+        o << "  const uint32_t VECS = C / V;\n";
+        o << "  const uint32_t P = min(PMAX, tca::hip::ceil_div(VECS, CV));  // VECS >= 1 (launch guard)\n";
+        o << "  const uint32_t r = blockIdx.x / P, p = blockIdx.x - r * P;\n";
+        o << "  if (r >= " << rowExpr << ") return;  // the grid is rows x P: never taken\n";
+        o << "  const uint32_t L = tca::hip::ceil_div(VECS, P);\n";
+        o << "  const uint32_t lo = p * L, hi = lo + min(L, VECS - lo);  // lo < VECS; hi - lo > " << kPartBlock << "\n";
+        o << "  const uint64_t row_base = static_cast<uint64_t>(r) * C;\n";
+        o << "  const bool active = true;\n";
+        for (int a : geo.outer) o << "  const uint32_t c" << a << " = r;\n";
+      };
+      for (size_t p = 0; p < passes.size(); ++p) {
+        const ir::Chain& c0 = g_.chains[passes[p][0]];
+        const bool red = !c0.reduces.empty();
+        const std::string tag = std::to_string(p + 1);
+        if (red) {
+          // Partial folds of pass p.
+          const std::string fn = pk.symbol + "_spart" + tag;
+          smFns.push_back({fn, p});
+          o << "// statements";
+          for (int ci : passes[p]) o << " #" << ci;
+          o << ": split rows, pass " << tag << ", partial folds\n";
+          o << "template <uint32_t V>\n__device__ __forceinline__ void " << fn << "(\n    " << sig << smSig << ") {\n";
+          chunkHead();
+          loadRowScalars(p, "  ");
+          combsOf(p, "  ");
+          for (int ci : passes[p]) {
+            const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+            o << "  " << T << " part" << ci << " = " << T << "(0);\n";
+          }
+          std::ostringstream b;
+          b << "  {\n    const uint32_t vc = lo + threadIdx.x;\n";
+          operands(b, p, "    ", false, "vc", "");
+          work(b, p, "    ", false, "vc", "true", "", true);
+          b << "  }\n  uint32_t v0 = lo + threadIdx.x + " << kPartBlock << "u;\n";
+          b << "  for (; v0 + " << 3 * kPartBlock << "u < hi; v0 += " << 4 * kPartBlock << "u) {\n";
+          for (uint32_t u = 0; u < 4; ++u) b << "    const uint32_t vc_" << u << " = v0 + " << u * kPartBlock << "u;\n";
+          for (uint32_t u = 0; u < 4; ++u) operands(b, p, "    ", false, "vc_" + std::to_string(u), "_" + std::to_string(u));
+          for (uint32_t u = 0; u < 4; ++u)
+            work(b, p, "    ", false, "vc_" + std::to_string(u), "true", "_" + std::to_string(u), false);
+          b << "  }\n  for (; v0 < hi; v0 += " << kPartBlock << "u) {\n    const uint32_t vc = v0;\n";
+          operands(b, p, "    ", false, "vc", "");
+          work(b, p, "    ", false, "vc", "true", "", false);
+          b << "  }\n";
+          o << b.str();
+          for (int ci : passes[p]) {
+            const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+            o << "  part" << ci << " = tca::hip::seg_allreduce<64>(part" << ci << ", comb" << ci << ");\n";
+            o << "  __shared__ " << T << " red" << ci << "[" << kPartBlock / 64 << "];\n";
+            o << "  if ((threadIdx.x & 63u) == 0u) red" << ci << "[threadIdx.x >> 6] = part" << ci << ";\n";
+          }
+          o << "  __syncthreads();\n  if (threadIdx.x == 0u) {\n";
+          for (int ci : passes[p]) {
+            const std::string T = CType(g_.exprs[g_.chains[ci].root.fn.body].type);
+            o << "    " << T << " acc" << ci << " = red" << ci << "[0];\n";
+            o << "    for (uint32_t w = 1; w < " << kPartBlock / 64 << "u; ++w) acc" << ci << " = comb" << ci << "(acc"
+              << ci << ", red" << ci << "[w]);\n";
+            o << "    p" << ci << "[static_cast<uint64_t>(r) * PMAX + p] = acc" << ci << ";\n";
+          }
+          o << "  }\n}\n";
+          // Merge of pass p: one wave per row.
+          const std::string mfn = pk.symbol + "_smerge" + tag;
+          smFns.push_back({mfn, p});
+          o << "template <uint32_t V>\n__device__ __forceinline__ void " << mfn << "(\n    " << sig << smSig << ") {\n";
+          o << "  constexpr uint32_t CV = " << kChunkVecs << "u, PMAX = " << kMaxParts << "u;\n";
+          o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
+          o << "  const uint32_t P = min(PMAX, tca::hip::ceil_div(C / V, CV));\n";
+          o << "  const uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63u;\n";
+          o << "  if (r >= " << rowExpr << ") return;  // whole waves\n";
+          for (int a : geo.outer) o << "  const uint32_t c" << a << " = r;\n";
+          loadRowScalars(p, "  ");
+          combsOf(p, "  ");
+          for (int ci : passes[p]) {
+            const ir::Chain& c = g_.chains[ci];
+            const int st = c.store_tensor;
+            const std::string T = CType(g_.exprs[c.root.fn.body].type);
+            const std::string A = "m" + std::to_string(ci), H = "h" + std::to_string(ci);
+            o << "  " << T << " " << A << " = " << T << "(0);\n  bool " << H << " = false;\n";
+            o << "  {\n    " << T << " pv[PMAX / 64u];\n";
+            o << "#pragma unroll\n    for (uint32_t k = 0; k < PMAX / 64u; ++k)\n";
+            o << "      pv[k] = p" << ci << "[static_cast<uint64_t>(r) * PMAX + min(lane + 64u * k, P - 1u)];\n";
+            o << "#pragma unroll\n    for (uint32_t k = 0; k < PMAX / 64u; ++k) {\n";
+            o << "      if (lane + 64u * k < P) {\n";
+            o << "        " << A << " = " << H << " ? comb" << ci << "(" << A << ", pv[k]) : pv[k];\n        " << H
+              << " = true;\n      }\n    }\n  }\n";
+            o << "  " << A << " = tca::hip::wave_allreduce_present(" << A << ", " << H << ", comb" << ci << ");\n";
+            o << "  if (lane == 0u) {\n";
+            const ir::ReduceStage& rs = c.reduces[0];
+            ExprGen fg(g_, o, "    ", &counter_);
+            fg.Bind(rs.fn.params[0], fg.Gen(rs.init));
+            fg.Bind(rs.fn.params[1], A);
+            std::string val = fg.Gen(rs.fn.body);  // P >= 1: init applied once to the row's total
+            if (c.has_piped) {
+              ExprGen pg(g_, o, "    ", &counter_);
+              pg.Bind(c.piped.fn.params[0], val);
+              for (size_t k = 0; k < c.piped.ops.size(); ++k)
+                pg.Bind(c.piped.fn.params[k + 1], "rs" + std::to_string(c.piped.ops[k].tensor));
+              val = pg.Gen(c.piped.fn.body);
+            }
+            o << "    t" << st << "[" << Offset(st, c.store_axes, coord) << "] = " << val << ";\n";
+            o << "  }\n";
+          }
+          o << "}\n";
+        } else {
+          // Row map of pass p over the chunk.
+          const std::string fn = pk.symbol + "_smap" + tag;
+          smFns.push_back({fn, p});
+          o << "// statement #" << passes[p][0] << ": split rows, pass " << tag << ", row map over a chunk\n";
+          o << "template <uint32_t V>\n__device__ __forceinline__ void " << fn << "(\n    " << sig << smSig << ") {\n";
+          chunkHead();
+          loadRowScalars(p, "  ");
+          std::ostringstream b;
+          b << "  uint32_t v0 = lo + threadIdx.x;\n";
+          b << "  for (; v0 + " << 3 * kPartBlock << "u < hi; v0 += " << 4 * kPartBlock << "u) {\n";
+          for (uint32_t u = 0; u < 4; ++u) b << "    const uint32_t vc_" << u << " = v0 + " << u * kPartBlock << "u;\n";
+          for (uint32_t u = 0; u < 4; ++u) operands(b, p, "    ", false, "vc_" + std::to_string(u), "_" + std::to_string(u));
+          for (uint32_t u = 0; u < 4; ++u)
+            work(b, p, "    ", false, "vc_" + std::to_string(u), "true", "_" + std::to_string(u), false);
+          b << "  }\n  for (; v0 < hi; v0 += " << kPartBlock << "u) {\n    const uint32_t vc = v0;\n";
+          operands(b, p, "    ", false, "vc", "");
+          work(b, p, "    ", false, "vc", "true", "", false);
+          b << "  }\n";
+          o << b.str() << "}\n";
+        }
+      }
+    }
     // One kernel per (vector width, cached | streamed); launch guards on the
     // row length pick exactly one: the widest width W (16 bytes of the
     // widest row-shaped tensor) for C % W == 0, then each smaller power of
@@ -2440,7 +2650,7 @@ class Emitter {
         const uint32_t kc = cached ? caches[ci] : 0u;
         const uint64_t lo = !cached ? (cachedVecs + 1) * w.v : ci == 0 ? 0 : (uint64_t{kBlock} * caches[ci - 1] + 1) * w.v;
         const uint64_t hi = cached ? uint64_t{kBlock} * kc * w.v : 0xffffffffull;
-        if (!cached && split && rowGuard.empty()) continue;  // a full reduction always splits
+        if (!cached && (split || splitMulti) && rowGuard.empty()) continue;  // one row: always split
         // A cached row of exactly kc * 2^k vectors (every lane holds kc: no
         // ownership test or clamp) runs a kernel of its own, so the general
         // path's registers do not set its occupancy (layernorm, 1024-lane
@@ -2463,7 +2673,8 @@ class Emitter {
           const std::string fit = cdim + " 0 4294967295 " + std::to_string(uint64_t{kc} * w.v) + " 0 pow2";
           if (exact) vk.when.push_back(fit);
           else if (canExact) vk.unless.push_back(fit);
-          if (!cached && split) vk.when.push_back(rowGuard + " " + std::to_string(kSplitRows + 1) + " 4294967295 1 0");
+          if (!cached && (split || splitMulti))
+            vk.when.push_back(rowGuard + " " + std::to_string(kSplitRows + 1) + " 4294967295 1 0");
           o << "extern \"C\" __global__ void __launch_bounds__(" << kBlock << ") " << vk.symbol << "(\n    " << sig
             << ") {\n";
           if (cached && canExact) {
@@ -2484,6 +2695,37 @@ class Emitter {
               << ") vec=" << w.v << " lanes/row=runtime(<=" << kBlock << ") passes=" << passes.size() << " block=max("
               << kMinBlock << ",lanes/row)";
           AddKernel(vk, Family::Stream, n.chains, det.str());
+        }
+      }
+      if (splitMulti) {
+        const uint64_t lo = (cachedVecs + 1) * w.v;
+        for (const auto& fp : smFns) {
+          const std::string& fn = fp.first;
+          const bool merge = fn.find("_smerge") != std::string::npos, map = fn.find("_smap") != std::string::npos;
+          const std::string tag = std::to_string(fp.second + 1);
+          PlanKernel sk = pk;
+          sk.symbol = symbol + (merge ? "_m" : map ? "_w" : "_p") + std::to_string(w.v) + "_" + tag;
+          sk.block = merge ? 256 : kPartBlock;
+          for (const auto& a : smPlanArgs) sk.args.push_back(a);
+          if (merge) {
+            sk.grid.push_back(rowGuard.empty() ? std::string("1/1") : DimProduct(geo.outer) + "/4");
+          } else {
+            if (!rowGuard.empty()) sk.grid.push_back(DimProduct(geo.outer) + "/1");
+            sk.grid.push_back(cdim + "/" + std::to_string(uint64_t{kChunkVecs} * w.v) + ":" + std::to_string(kMaxParts));
+          }
+          sk.when.push_back(cdim + " " + std::to_string(lo) + " 4294967295 " + std::to_string(w.mod) + " " +
+                            std::to_string(w.rem));
+          if (!rowGuard.empty()) sk.when.push_back(rowGuard + " 0 " + std::to_string(kSplitRows) + " 1 0");
+          o << "extern \"C\" __global__ void __launch_bounds__(" << sk.block << ") " << sk.symbol << "(\n    " << sig
+            << smSig << ") {\n  " << fn << "<" << w.v << "u>(" << args << smArgs << ");\n}\n";
+          std::ostringstream det;
+          det << "row=runtime (" << cdim << " % " << w.mod << " == " << w.rem << ", >= " << lo
+              << (rowGuard.empty() ? std::string() : ", rows <= " + std::to_string(kSplitRows)) << ": split, pass "
+              << tag << ") vec=" << w.v
+              << (merge ? " merge: one wave per row over <= " + std::to_string(kMaxParts) + " partials"
+                        : (map ? " row map: " : " partial: ") + std::to_string(kPartBlock) + " lanes per chunk of >= " +
+                              std::to_string(kChunkVecs / 2) + " vectors");
+          AddKernel(sk, Family::Stream, n.chains, det.str());
         }
       }
       if (!split) continue;

@@ -541,8 +541,8 @@ def test_program_launch_without_module_is_refused():
 EXPECTED_FAMILIES = {
     "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"] * 3,
     "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"] * 3, "gemm_bf16": ["gemm"] * 3,
-    "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 13, "softmax_dyn": ["stream"] * 10,
-    "layernorm_dyn": ["stream"] * 10, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 10,
+    "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 13, "softmax_dyn": ["stream"] * 25,
+    "layernorm_dyn": ["stream"] * 25, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 10,
     # narrow rows: one more width per halving of the element size (8 bf16, 16 u8 elements per vector)
     "row_sum_bf16_dyn": ["stream"] * 17, "row_sum_u8_dyn": ["stream"] * 21, "row_stats_u32_dyn": ["stream"] * 13,
     # column reductions: a (partial, merge) pair per vector width
@@ -982,3 +982,24 @@ def test_stream_row_caches_fit_registers(name, tmp_path):
 def test_single_pass_stream_nest_keeps_one_cache_depth():
     plan = programs.CONFIG_PROGRAMS["row_sum_max_dyn"]().emit().plan
     assert "_c4x8" not in plan and "when C 16388 4294967295 4 0" in plan
+
+
+@pytest.mark.parametrize("R,C,variants", [
+    # rows of <= 8192 vectors stay in registers whatever the row count
+    (3, 32768, ["c4x8"]), (3, 16384, ["c4e"]),
+    # longer rows: streamed from 256 rows on, split into passes below
+    (256, 32772, ["s4"]), (255, 32772, ["p4_1", "m4_1", "p4_2", "m4_2", "w4_3"]),
+    (1, 1 << 20, ["p4_1", "m4_1", "p4_2", "m4_2", "w4_3"]), (2, 16386, ["p2_1", "m2_1", "p2_2", "m2_2", "w2_3"]),
+    (7, 8193, ["p1_1", "m1_1", "p1_2", "m1_2", "w1_3"]), (300, 8193, ["s1"])])
+def test_multipass_split_selection(R, C, variants):
+    """Few long rows of a nest of several passes (softmax: max, sum, map):
+    each pass over its own grid of row chunks, in pass order."""
+    e = programs.CONFIG_PROGRAMS["softmax_dyn"]().emit()
+    rc, h = parse(e.plan)
+    assert rc == 0, _lib.last_error()
+    arr = compiler._descriptors([TensorDesc(0x1000, (R, C), 0), TensorDesc(0x1000, (R, C), 0)])
+    syms = e.kernel_symbols()
+    out = (ctypes.c_uint8 * len(syms))()
+    assert _lib.lib().tca_program_selected(h, arr, 2, None, 0, out, None, None, len(syms)) == 0, _lib.last_error()
+    assert [s for s, f in zip(syms, out) if f] == ["tca_softmax_dyn_k0_" + v for v in variants]
+    _lib.lib().tca_program_unload(h)

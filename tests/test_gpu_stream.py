@@ -154,3 +154,51 @@ def test_split_integer_rows(gpu):
 def test_stream_empty_grid(gpu):
     s, m = out_dev((0,), gpu), out_dev((0,), gpu)
     run(compiled("row_sum_max_dyn"), [to_dev(np.zeros((0, 5), np.float32), gpu), s, m])  # no workgroups launched
+
+
+# Few long rows of a multi-pass nest: one grid of row chunks per pass (rows <=
+# 255 in the streamed range), against the streamed kernel (256 rows) and the
+# oracle; V 4, 2 and 1 rows, chunk counts from 3 to 512.
+MULTIPASS_SPLIT_SHAPES = [(1, 40000), (7, 32772), (3, 100003), (2, 1_000_002), (255, 33000), (256, 33000),
+                          (1, 4_000_000)]
+
+
+@pytest.mark.parametrize("R,C", MULTIPASS_SPLIT_SHAPES)
+def test_split_softmax(gpu, R, C):
+    _say("split C3", R, C)
+    x = inputs.normal((R, C), 2.0, 0)
+    want = oracle.softmax(x)
+    y = out_dev((R, C), gpu)
+    run(compiled("softmax_dyn"), [to_dev(x, gpu), y])
+    got = host(y)
+    assert canaries(got) == 0
+    rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want.astype(np.float64)), 1e-30)
+    assert rel.max() <= reduce_tol(C), "softmax relative error %g" % rel.max()
+    assert np.abs(got.astype(np.float64).sum(1) - 1.0).max() <= reduce_tol(C)
+
+
+@pytest.mark.parametrize("R,C", MULTIPASS_SPLIT_SHAPES)
+def test_split_layernorm(gpu, R, C):
+    _say("split C4", R, C)
+    x = inputs.normal((R, C), 1.0, 0)
+    g, b = inputs.uniform((C,), 0.5, 1.5, 1), inputs.uniform((C,), -0.1, 0.1, 2)
+    inv_n, eps = float(np.float32(1.0 / C)), 1e-5
+    want = oracle.layernorm(x, g, b, inv_n, eps)
+    y = out_dev((R, C), gpu)
+    run(compiled("layernorm_dyn"), [to_dev(x, gpu), to_dev(g, gpu), to_dev(b, gpu), y], scalars=[inv_n, eps])
+    got = host(y)
+    assert canaries(got) == 0
+    # At a million terms the oracle's sequential fp32 sum of squares is itself
+    # off by ~1e-3 in the output (20x the bound, measured against float64), so
+    # the bound holds the GPU to the float64 evaluation of the same formula,
+    # and the oracle to the reference's own end-to-end tolerance
+    # (internal/e2e/e2e_test.go:20, reduceTol 2e-3).
+    xd = x.astype(np.float64)
+    mean = xd.sum(1, keepdims=True) * inv_n
+    var = ((xd - mean) ** 2).sum(1, keepdims=True) * inv_n
+    want64 = (xd - mean) / np.sqrt(var + eps) * g.astype(np.float64) + b.astype(np.float64)
+    assert_layernorm_close(got, want64, x, g, b, eps, "split C4 R=%d C=%d vs float64" % (R, C))
+    diff = float(np.abs(got.astype(np.float64) - want).max())
+    print("split C4 R=%d C=%d: max |gpu - oracle| %.3g" % (R, C, diff))
+    if C <= 1_100_000:  # at 4 M terms the sequential fold alone is off by ~1.2e-2
+        assert diff <= 2e-3
