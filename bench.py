@@ -44,6 +44,9 @@ CONFIGS = {
     # not configurations; shown because one workgroup per row would idle the GPU
     "c2v": ("vec_sum_max", "sum+max of one f32 vector [67108864] (split rows, full reduction)"),
     "c2r": ("row_sum_max_dyn", "row sum+max f32 [16,4194304] (split rows)"),
+    # C3's softmax on few long rows: each of its three passes over a grid of
+    # row chunks (partial + merge per reduction pass, a chunked row map)
+    "c3r": ("softmax_dyn", "row softmax f32 [64,1048576] (few long rows: passes split over row chunks)"),
     # C2's reductions over narrow element types (16-byte vectors of 8 bf16 /
     # 16 u8 elements): not configurations, the same family on other dtypes
     "c2h": ("row_sum_bf16_dyn", "row sum+max bf16 -> f32 [8192,16384] (streaming family)"),
@@ -190,6 +193,15 @@ def _setup(key, dev):
         scalars = []
         work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
         cpu = ("c2", (x,))
+    elif key == "c3r":
+        R, C = 64, 1 << 20
+        x = inputs.normal((R, C), 2.0, 0)
+        algo = 2 * R * C * 4
+        per_set = algo
+        make = lambda i: [dev_f32(x), torch.empty((R, C), device=dev)]  # noqa: E731
+        scalars = []
+        work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = None
     elif key == "c3":
         R, C = 16384, 4096
         x = inputs.normal((R, C), 2.0, 0)
@@ -399,7 +411,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c2h,c2u,c2c,c2mv,c2mw,c5b8,c1t,c1m")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c3r,c2h,c2u,c2c,c2mv,c2mw,c5b8,c1t,c1m")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
                     help="untimed launches per config before the warmup steps, in wall-clock ms")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
