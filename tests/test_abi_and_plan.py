@@ -137,12 +137,12 @@ def test_narrow_stream_variant_selection(prog, dtype, R, C, variants):
 
 
 @pytest.mark.parametrize("R,C,variant,part_grid,merge_grid", [
-    (8192, 8192, 4, 32 * 32, 128),     # 32 column blocks (64 vectors each) x P = min(128, 1024 / 32) row chunks
-    (65536, 1024, 4, 4 * 256, 16),     # P = min(1024, 256); the merge takes 64 outputs per block
-    (1024, 65536, 4, 256 * 4, 1024),   # P = min(16, 4)
-    (16, 4 << 20, 4, 16384, 0),        # the column blocks alone exceed 1024: P = 1, no merge
+    (8192, 8192, 4, 64 * 16, 128),     # 64 column blocks (32 vectors each) x P = min(128, 1024 / 64) row chunks
+    (65536, 1024, 4, 8 * 128, 16),     # P = min(1024, 128); the merge takes 64 outputs per block
+    (1024, 65536, 4, 512 * 2, 1024),   # P = min(16, 2)
+    (16, 4 << 20, 4, 32768, 0),        # the column blocks alone exceed 1024: P = 1, no merge
     (100, 3, 1, 2, 1),                 # odd columns: 1-element vectors; P = min(2, 1024)
-    (64, 1022, 2, 8, 0),               # C % 4 == 2: 511 vectors, 8 column blocks; P = min(1, 128) = 1
+    (64, 1022, 2, 16, 0),              # C % 4 == 2: 511 vectors, 16 column blocks; P = min(1, 64) = 1
     (0, 100, 4, 1, 0),                 # no rows: one chunk, init stored
     (100, 0, 4, 0, 0)])                # no columns: nothing runs
 def test_col_split_geometry(R, C, variant, part_grid, merge_grid):
@@ -165,15 +165,15 @@ def test_col_split_geometry(R, C, variant, part_grid, merge_grid):
 
 
 @pytest.mark.parametrize("B,R,C,want", [
-    # 4 column blocks, P = min(16, 256) = 16 > 1: a partial + merge pair per pass
-    (1, 1000, 1000, {"p4_1": 4 * 16, "m4_1": 16, "p4_2": 4 * 16, "m4_2": 16}),
+    # 8 column blocks, P = min(16, 128) = 16 > 1: a partial + merge pair per pass
+    (1, 1000, 1000, {"p4_1": 8 * 16, "m4_1": 16, "p4_2": 8 * 16, "m4_2": 16}),
     # <= 64 rows: P = 1, the whole-column kernel runs both passes
-    (3, 64, 1000, {"w4": 3 * 4}),
-    (1, 0, 1000, {"w4": 4}),
-    # 547 column blocks leave room for one chunk: P = 1 over 100 rows
-    (1, 100, 140000, {"w4": 547}),
-    # odd columns: 1-element vectors, 2 column blocks, P = min(16, 512) = 16
-    (2, 1000, 65, {"p1_1": 2 * 2 * 16, "m1_1": 3, "p1_2": 2 * 2 * 16, "m1_2": 3}),
+    (3, 64, 1000, {"w4": 3 * 8}),
+    (1, 0, 1000, {"w4": 8}),
+    # 1094 column blocks leave room for one chunk: P = 1 over 100 rows
+    (1, 100, 140000, {"w4": 1094}),
+    # odd columns: 1-element vectors, 3 column blocks, P = min(16, 170) = 16
+    (2, 1000, 65, {"p1_1": 2 * 3 * 16, "m1_1": 3, "p1_2": 2 * 3 * 16, "m1_2": 3}),
     (1, 100, 0, {})])
 def test_col_passes_geometry(B, R, C, want):
     """A column nest of two passes (a variance reading its mean): with one
