@@ -24,7 +24,7 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, AMD published
-MFMA_PEAK_TFLOPS = {"f32": 157.3, "bf16": 2500.0}  # dense, AMD published
+MFMA_PEAK_TFLOPS = {"f32": 157.3, "bf16": 2500.0, "f16": 2500.0}  # dense, AMD published
 MALL_DEFEAT_BYTES = 768 << 20
 
 CONFIGS = {
@@ -35,6 +35,8 @@ CONFIGS = {
     "c4": ("layernorm_1024", "C4 layernorm f32 [32768,1024]"),
     "c5f": ("gemm_f32", "C5 gemm f32 4096^3"),
     "c5b": ("gemm_bf16", "C5 gemm bf16-in f32-acc 4096^3"),
+    # C5's contraction on f16 inputs: not a configuration (the bf16 kernels with the f16 MFMAs)
+    "c5h": ("gemm_f16", "gemm f16-in f32-acc 4096^3 (not a configuration)"),
     # C2-C4 with the row length a run-time dim (streaming row family); same
     # data and algorithmic bytes, not configurations of their own
     "c2s": ("row_sum_max_dyn", "C2 with run-time row length (streaming family)"),
@@ -231,6 +233,11 @@ def _setup(key, dev):
             tb = torch.from_numpy(b).to(dev).to(torch.bfloat16)
             elt = 2
             dt = "bf16"
+        elif key == "c5h":
+            ta = torch.from_numpy(a).to(dev).to(torch.float16)
+            tb = torch.from_numpy(b).to(dev).to(torch.float16)
+            elt = 2
+            dt = "f16"
         else:
             ta, tb = dev_f32(a), dev_f32(b)
             elt = 4
@@ -240,7 +247,7 @@ def _setup(key, dev):
         scalars = []
         work = {"flops": 2 * M * N * K, "bound": "mfma", "dtype": dt, "shape": [M, N, K],
                 "bytes": per_set}
-        cpu = (key, (a, b)) if key != "c5b8" else None
+        cpu = (key, (a, b)) if key not in ("c5b8", "c5h") else None
     nsets = max(2, math.ceil(MALL_DEFEAT_BYTES / per_set))
     sets = [make(i) for i in range(nsets)]
     if streamed:
@@ -411,7 +418,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c3r,c2h,c2u,c2c,c2mv,c2mw,c5b8,c1t,c1m")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c3r,c2h,c2u,c2c,c2mv,c2mw,c5b8,c5h,c1t,c1m")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
                     help="untimed launches per config before the warmup steps, in wall-clock ms")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")

@@ -272,7 +272,10 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   (void)err;
   std::ostringstream& o = *src;
   const int ta = c.root.ops[m.a_op].tensor, tb = c.root.ops[m.b_op].tensor, tc = c.store_tensor;
-  const bool bf16 = m.in == Elem::BF16;
+  // 16-bit inputs (bf16 or f16) share the bf16 kernels; f16 selects their
+  // _f16 MFMAs and hands them its tensors as 16-bit words.
+  const bool f16 = m.in == Elem::F16;
+  const bool bf16 = m.in == Elem::BF16 || f16;
   // The fused epilogue (the piped map at (cm, cn)), the same in every kernel.
   std::ostringstream epi;
   epi << "  const uint32_t M = " << ExtentExpr(g, m.m) << ", N = " << ExtentExpr(g, m.n) << ", K = "
@@ -295,12 +298,15 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
     val = pg.Gen(c.piped.fn.body);
   }
   epi << "    return " << val << ";\n  };\n";
-  const std::string args = "(t" + std::to_string(ta) + ", t" + std::to_string(tb) + ", t" + std::to_string(tc) +
-                           ", M, N, K, epi);\n}\n\n";
+  const std::string args =
+      f16 ? "(reinterpret_cast<const __bf16*>(t" + std::to_string(ta) + "), reinterpret_cast<const __bf16*>(t" +
+                std::to_string(tb) + "), t" + std::to_string(tc) + ", M, N, K, epi);\n}\n\n"
+          : "(t" + std::to_string(ta) + ", t" + std::to_string(tb) + ", t" + std::to_string(tc) + ", M, N, K, epi);\n}\n\n";
   const std::string nk = m.b_nk ? "true" : "false";
   const std::vector<std::string> grid = {g.dims[m.m].name + "/256", g.dims[m.n].name + "/256"};
   const std::string orient = m.b_nk ? " B=[n][k]" : " B=[k][n]";
-  o << "// contraction over @" << g.dims[m.k].name << " on MFMA (" << (bf16 ? "bf16 16x16x32 whole tiles, 32x32x16 edges" : "f32 32x32x2")
+  o << "// contraction over @" << g.dims[m.k].name << " on MFMA ("
+    << (f16 ? "f16 16x16x32 whole tiles, 32x32x16 edges" : bf16 ? "bf16 16x16x32 whole tiles, 32x32x16 edges" : "f32 32x32x2")
     << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << "\n";
   if (!bf16) {
     // From M, N >= 4096 on (at least 256 tiles of 256x256): whole tiles with
@@ -349,28 +355,30 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   // Each kernel returns at once on the other kernels' tiles.
   const std::string M = g.dims[m.m].name, N = g.dims[m.n].name, K = g.dims[m.k].name;
   o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "_w(\n    " << signature << ") {\n"
-    << epi.str() << "  tca::hip::gemm_bf16_4w<" << nk << ">" << args;
+    << epi.str() << "  tca::hip::gemm_bf16_4w<" << nk << (f16 ? ", decltype(epi), true" : "") << ">" << args;
   o << "extern \"C\" __global__ void __launch_bounds__(512) " << symbol << "_v(\n    " << signature << ") {\n"
-    << epi.str() << "  tca::hip::gemm_bf16_256_w8<" << nk << ">" << args;
+    << epi.str() << "  tca::hip::gemm_bf16_256_w8<" << nk << (f16 ? ", decltype(epi), 4, true" : "") << ">" << args;
   o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "(\n    " << signature << ") {\n"
-    << epi.str() << "  tca::hip::gemm_bf16_256<" << nk << ", decltype(epi), 1, true, true, true>" << args;
+    << epi.str() << "  tca::hip::gemm_bf16_256<" << nk << ", decltype(epi), 1, true, true, true" << (f16 ? ", true" : "")
+    << ">" << args;
   GemmKernel w;
   w.suffix = "_w";
   w.block = 256;
   w.grid = grid;
   w.when = {M + " 256 4294967295 1 0", N + " 256 4294967295 8 0", K + " 256 4294967295 64 0"};
-  w.detail = "bf16 mfma 16x16x32 tile=256x256 4 waves of 128x128, A in 64-deep slices (direct-to-LDS rings; whole tiles, K % 64 == 0, K >= 256)" + orient;
+  const std::string ty = f16 ? "f16" : "bf16";
+  w.detail = ty + " mfma 16x16x32 tile=256x256 4 waves of 128x128, A in 64-deep slices (direct-to-LDS rings; whole tiles, K % 64 == 0, K >= 256)" + orient;
   GemmKernel v;
   v.suffix = "_v";
   v.block = 512;
   v.grid = grid;
   v.when = {M + " 256 4294967295 1 0", N + " 256 4294967295 8 0", K + " 32 4294967295 32 0"};
   v.unless = {K + " 256 4294967295 64 0"};
-  v.detail = "bf16 mfma 16x16x32 tile=256x256 bk=32 8 waves (direct-to-LDS ring; whole tiles, K % 64 != 0 or K < 256)" + orient;
+  v.detail = ty + " mfma 16x16x32 tile=256x256 bk=32 8 waves (direct-to-LDS ring; whole tiles, K % 64 != 0 or K < 256)" + orient;
   GemmKernel e;
   e.grid = grid;
   e.unless = {M + " 0 4294967295 256 0", N + " 0 4294967295 256 0", K + " 32 4294967295 32 0"};
-  e.detail = "bf16 mfma 32x32 tile=256x256 bk=64 4 waves (edge tiles, K % 32 != 0, N % 8 != 0)" + orient;
+  e.detail = ty + " mfma 32x32 tile=256x256 bk=64 4 waves (edge tiles, K % 32 != 0, N % 8 != 0)" + orient;
   out->kernels.push_back(w);
   out->kernels.push_back(v);
   out->kernels.push_back(e);

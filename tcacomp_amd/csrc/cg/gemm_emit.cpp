@@ -13,7 +13,7 @@ using ir::Op;
 
 namespace {
 
-// Body operand i is param p, or cast<f32>(param p) when the param is bf16.
+// Body operand i is param p, or cast<f32>(param p) when the param is bf16 or f16.
 bool IsParamOrCast(const ir::Graph& g, int id, int param, Elem* in) {
   const ir::Expr& e = g.exprs[id];
   if (id == param) {
@@ -22,7 +22,7 @@ bool IsParamOrCast(const ir::Graph& g, int id, int param, Elem* in) {
   }
   if (e.op == Op::Cast && e.type == Elem::F32 && e.args[0] == param) {
     *in = g.exprs[param].type;
-    return *in == Elem::BF16;
+    return *in == Elem::BF16 || *in == Elem::F16;
   }
   return false;
 }

@@ -5,6 +5,7 @@
 // two barriers per Combine; .planning/quick/261030-uai-.../after-cu/gemm.cu:
 // 59-90). Here the contraction runs on MFMA:
 //   bf16 inputs : v_mfma_f32_16x16x32_bf16 (gfx950) on whole 256x256 tiles
+//                 (f16 inputs: the same kernels with the _f16 MFMAs)
 //                 (gemm_bf16_4w when K % 64 == 0 and K >= 256, else
 //                 gemm_bf16_256_w8), v_mfma_f32_32x32x16_bf16 on the edge
 //                 tiles (gemm_bf16_256); fp32 accumulate
@@ -38,6 +39,26 @@ namespace hip {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// The 16-bit contractions below move raw 16-bit values (as bf16x8 registers)
+// through memory, LDS and registers; F16 selects the MFMA that reads them as
+// IEEE half (v_mfma_f32_*_f16) instead of bfloat16. The fp32 accumulation,
+// the operand layout and every data movement are the same for both.
+template <bool F16, typename Acc>
+__device__ __forceinline__ Acc mfma_32x32x16_16b(const bf16x8& a, const bf16x8& b, const Acc& c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+template <bool F16, typename Acc>
+__device__ __forceinline__ Acc mfma_16x16x32_16b(const bf16x8& a, const bf16x8& b, const Acc& c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -101,7 +122,8 @@ __device__ __forceinline__ bool gemm_bf16_dma_tile(uint32_t m0, uint32_t n0, uin
 
 // SKIP_DMA: the direct-to-LDS tiles belong to another kernel
 // (gemm_bf16_256_w8); this one returns at once on them.
-template <bool B_NK, typename Epi, int SWZ = 1, bool SPREAD = true, bool PREFETCH = true, bool SKIP_DMA = false>
+template <bool B_NK, typename Epi, int SWZ = 1, bool SPREAD = true, bool PREFETCH = true, bool SKIP_DMA = false,
+          bool F16 = false>
 __device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
                                               float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
   constexpr uint32_t BM = 256, BN = 256, BK = 64, TILE = BM * BK;
@@ -290,7 +312,7 @@ __device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, cons
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gb[j], ga[i], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_32x32x16_16b<F16>(gb[j], ga[i], acc[i][j]);
       if (SPREAD && has1) {
         if (ks == 0) store_a(nbuf, 0);
         if (ks == 1) store_a(nbuf, 1);
@@ -405,7 +427,7 @@ __device__ __forceinline__ bf16x8 frag_b16_tr(const uint16_t* Bs, uint32_t n_col
 // Every other tile returns at once: gemm_bf16_256<..., SKIP_DMA> takes them.
 // With K % 64 == 0 and K >= 256 the launch takes gemm_bf16_4w instead (4
 // waves of 128x128, A in 64-deep slices, below).
-template <bool B_NK, typename Epi, uint32_t STAGES = 4>
+template <bool B_NK, typename Epi, uint32_t STAGES = 4, bool F16 = false>
 __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
                                                  float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
   static_assert(STAGES == 4 || STAGES == 5, "a ring of 4 or 5 slices (160 KiB of LDS at most)");
@@ -484,7 +506,7 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
     const uint16_t* As = a_slice(s);
     auto mf = [&](int c) {
       const int i = blk_i(c), j = c >> 2;
-      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gb[j], fa[i], acc[i][j], 0, 0, 0);
+      acc[i][j] = mfma_16x16x32_16b<F16>(gb[j], fa[i], acc[i][j]);
       fence();
     };
     fence();
@@ -502,7 +524,7 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
     const uint16_t* Bs = b_slice(ns);
     auto mf = [&](int c) {
       const int i = blk_i(c), j = c >> 2;
-      acc[4 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gb[j], fh[i], acc[4 + i][j], 0, 0, 0);
+      acc[4 + i][j] = mfma_16x16x32_16b<F16>(gb[j], fh[i], acc[4 + i][j]);
       fence();
     };
     auto dm = [&](int q) {
@@ -662,13 +684,17 @@ __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, c
 //   s_waitcnt covers; an MFMA's accumulator is written again only by the
 //   64th MFMA after it.
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+template <bool F16 = false>
 __device__ __forceinline__ void mfma16_bf16_acc(f32x4_t& c, const bf16x8& b, const bf16x8& a) {
-  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(b), "v"(a));
+  if constexpr (F16)
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(b), "v"(a));
+  else
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(b), "v"(a));
 }
 
 __device__ __forceinline__ uint32_t swz_rows64(uint32_t row, uint32_t g) { return row * 64u + ((g ^ (row & 6u)) << 3); }
 
-template <bool B_NK, typename Epi>
+template <bool B_NK, typename Epi, bool F16 = false>
 __device__ __forceinline__ void gemm_bf16_4w(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
                                              float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
   constexpr uint32_t BM = 256, BN = 256, ASL = 256u * 64u, BSL = 256u * 32u;
@@ -762,7 +788,7 @@ __device__ __forceinline__ void gemm_bf16_4w(const __bf16* __restrict__ A, const
     const uint32_t ns = kt + 1u;
     auto mf = [&](int c) {
       const int j = c >> 3, i = (j & 1) ? 7 - (c & 7) : (c & 7);
-      mfma16_bf16_acc(acc[i][j], cb[j], ca[i]);
+      mfma16_bf16_acc<F16>(acc[i][j], cb[j], ca[i]);
       fence();
     };
     auto da = [&](int q) { if (ld) load_a(q, (kt >> 1) + 2u, kt & 1u); fence(); };

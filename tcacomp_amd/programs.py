@@ -440,6 +440,17 @@ def gemm_bf16():
     return _matmul("gemm_bf16", TBF16)
 
 
+def gemm_f16():
+    """C5's contraction with f16 inputs, fp32 accumulate (the bf16 kernels
+    with the f16 MFMAs)."""
+    return _matmul("gemm_f16", TF16)
+
+
+def gemm_f16_nt():
+    """f16 inputs with B given as [N][K]."""
+    return _matmul("gemm_f16_nt", TF16, b_nk=True)
+
+
 def gemm_bf16_nt():
     """C5 with B given as [N][K] (the qk_score orientation), bf16 inputs."""
     return _matmul("gemm_bf16_nt", TBF16, b_nk=True)
@@ -694,6 +705,8 @@ CONFIG_PROGRAMS = {
     "gemm_bf16": gemm_bf16,
     "gemm_bf16_nt": gemm_bf16_nt,
     "gemm_f32_nt": gemm_f32_nt,
+    "gemm_f16": gemm_f16,
+    "gemm_f16_nt": gemm_f16_nt,
     # small-row variants exercised by the parity tests (tails, few lanes per row)
     "row_sum_max_1000": lambda: row_sum_max(1000),
     "row_sum_max_64": lambda: row_sum_max(64),

@@ -694,7 +694,7 @@ def _gemm_asm(name, tmp_path):
     return asm.read_text().split("\n")
 
 
-@pytest.mark.parametrize("name", ["gemm_bf16", "gemm_bf16_nt", "gemm_f32", "gemm_f32_nt"])
+@pytest.mark.parametrize("name", ["gemm_bf16", "gemm_bf16_nt", "gemm_f16", "gemm_f16_nt", "gemm_f32", "gemm_f32_nt"])
 def test_dma_gemm_reloads_nothing_from_scratch(name, tmp_path):
     """The contractions' direct-to-LDS main loops wait on hand-counted vmcnt
     values for their loads; a register spill reloaded from scratch while
@@ -735,7 +735,7 @@ def _vgpr_writes(line):
     return regs if kind == "v" else set()
 
 
-@pytest.mark.parametrize("name", ["gemm_bf16", "gemm_bf16_nt", "gemm_f32", "gemm_f32_nt"])
+@pytest.mark.parametrize("name", ["gemm_bf16", "gemm_bf16_nt", "gemm_f16", "gemm_f16_nt", "gemm_f32", "gemm_f32_nt"])
 def test_asm_mfma_kernel_hazards_covered(name, tmp_path):
     """The 4-wave contractions issue their MFMAs as inline asm, which the
     compiler's hazard recogniser does not model. Checked on its gfx950
