@@ -2777,12 +2777,12 @@ class Emitter {
 
   // C: reductions over a non-contiguous axis. Threads span the contiguous
   // axis in vectors of V elements (16 bytes of the widest tile or column
-  // vector): SL = min(64, smallest power of two >= C / V) threads per row
-  // and 256 / SL rows per block step, 256 threads per block. A block owns 64
+  // vector): SL = min(32, smallest power of two >= C / V) threads per row
+  // and 256 / SL rows per block step, 256 threads per block. A block owns 32
   // column vectors of one outer index and a chunk of the reduced axis: P
   // chunks, P = col_split(R, column blocks, 64, 1024) — enough blocks to
   // fill the GPU, >= 64 rows each, and a partial scratch of at most
-  // 1024 x 64 vectors. Chunk p covers rows [p R / P, (p + 1) R / P), never empty when
+  // 1024 x 32 vectors. Chunk p covers rows [p R / P, (p + 1) R / P), never empty when
   // P > 1 (P <= R). Each thread folds its columns over its rows in registers
   // with 4 rows in flight; the row slots of a block meet in LDS. With P = 1
   // the block applies init and the piped map and stores; otherwise it writes
@@ -3189,7 +3189,7 @@ class Emitter {
         << "u;  // SPAN column vectors per block\n";
       o << "  const uint32_t C = " << ExtentExpr(g_, geo.c) << ", R = " << ExtentExpr(g_, geo.r) << ";\n";
       o << "  const uint32_t VEC = C / V, CB = tca::hip::ceil_div(VEC, SPAN);\n";
-      o << "  const uint32_t cbk = blockIdx.x;  // 64 column vectors of one outer index, every row\n";
+      o << "  const uint32_t cbk = blockIdx.x;  // SPAN column vectors of one outer index, every row\n";
       o << "  const uint32_t ob = cbk / CB, cb = cbk - ob * CB;\n";
       blockGeom();
       o << "  const uint32_t r_lo = 0u, r_hi = R;\n";
@@ -3318,17 +3318,17 @@ class Emitter {
       const std::string v = std::to_string(wd.v);
       if (geo.passes == 1) {
         ks.push_back({"_p" + v, "_part", 0, false, n.chains,
-                      " partial: 64 column vectors x a chunk of rows per block, P = col_split"});
+                      " partial: " + std::to_string(kSpan) + " column vectors x a chunk of rows per block, P = col_split"});
         ks.push_back({"_m" + v, "_merge", 1, true, n.chains,
                       " merge: 64 outputs per block, 16 waves over the P chunks (P > 1 only)"});
       } else {
         ks.push_back({"_w" + v, "_whole", 2, false, n.chains,
-                      " whole: every pass over all rows of 64 column vectors per block, results handed on in LDS "
+                      " whole: every pass over all rows of " + std::to_string(kSpan) + " column vectors per block, results handed on in LDS "
                       "(P == 1 only)"});
         for (int ps = 0; ps < geo.passes; ++ps) {
           const std::string pn = std::to_string(ps + 1);
           ks.push_back({"_p" + v + "_" + pn, "_part" + pn, 3, false, passChains[ps],
-                        " pass " + pn + " partial: 64 column vectors x a chunk of rows per block (P > 1 only)"});
+                        " pass " + pn + " partial: " + std::to_string(kSpan) + " column vectors x a chunk of rows per block (P > 1 only)"});
           ks.push_back({"_m" + v + "_" + pn, "_merge" + pn, 1, true, passChains[ps],
                         " pass " + pn + " merge: 64 outputs per block, 16 waves over the P chunks (P > 1 only)"});
         }
