@@ -298,14 +298,46 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
     val = pg.Gen(c.piped.fn.body);
   }
   epi << "    return " << val << ";\n  };\n";
-  const std::string args =
-      f16 ? "(reinterpret_cast<const __bf16*>(t" + std::to_string(ta) + "), reinterpret_cast<const __bf16*>(t" +
-                std::to_string(tb) + "), t" + std::to_string(tc) + ", M, N, K, epi);\n}\n\n"
-          : "(t" + std::to_string(ta) + ", t" + std::to_string(tb) + ", t" + std::to_string(tc) + ", M, N, K, epi);\n}\n\n";
+  // A batched contraction runs one grid of tiles per batch: the workgroup id
+  // splits into (batch, tile), the operands led by the batch axis and C are
+  // offset to that batch, and the kernel maps the tile index as it maps the
+  // workgroup id of a single contraction. `args(T)` is the call for square
+  // tiles of T.
+  const bool batched = m.batch >= 0;
+  auto args = [&](uint32_t T) {
+    std::string a = "t" + std::to_string(ta), b = "t" + std::to_string(tb), cc = "t" + std::to_string(tc);
+    std::string pre, tile;
+    if (batched) {
+      const std::string Ts = std::to_string(T) + "u";
+      pre = "  const uint32_t tiles = ((M + " + Ts + " - 1u) / " + Ts + ") * ((N + " + Ts + " - 1u) / " + Ts +
+            "), bb = blockIdx.x / tiles;\n";
+      if (m.a_batched) a = "(" + a + " + (size_t)bb * M * K)";
+      if (m.b_batched) b = "(" + b + " + (size_t)bb * K * N)";
+      cc = "(" + cc + " + (size_t)bb * M * N)";
+      tile = ", blockIdx.x - bb * tiles";
+    }
+    if (f16) {
+      a = "reinterpret_cast<const __bf16*>(" + a + ")";
+      b = "reinterpret_cast<const __bf16*>(" + b + ")";
+    }
+    return std::make_pair(pre, "(" + a + ", " + b + ", " + cc + ", M, N, K, epi" + tile + ");\n}\n\n");
+  };
   const std::string nk = m.b_nk ? "true" : "false";
-  const std::vector<std::string> grid = {g.dims[m.m].name + "/256", g.dims[m.n].name + "/256"};
-  const std::string orient = m.b_nk ? " B=[n][k]" : " B=[k][n]";
-  o << "// contraction over @" << g.dims[m.k].name << " on MFMA ("
+  // Grid terms: [batch x] tiles of the (m, n) plane.
+  auto tiles = [&](uint32_t T) {
+    std::vector<std::string> t;
+    if (batched) t.push_back(g.dims[m.batch].name + "/1");
+    t.push_back(g.dims[m.m].name + "/" + std::to_string(T));
+    t.push_back(g.dims[m.n].name + "/" + std::to_string(T));
+    return t;
+  };
+  const std::vector<std::string> grid = tiles(256);
+  std::string orient = m.b_nk ? " B=[n][k]" : " B=[k][n]";
+  if (batched)
+    orient += std::string(" batch=@") + g.dims[m.batch].name + " A " + (m.a_batched ? "per batch" : "shared") + ", B " +
+              (m.b_batched ? "per batch" : "shared");
+  o << "// " << (batched ? "batched (over @" + g.dims[m.batch].name + ") " : "") << "contraction over @"
+    << g.dims[m.k].name << " on MFMA ("
     << (f16 ? "f16 16x16x32 whole tiles, 32x32x16 edges" : bf16 ? "bf16 16x16x32 whole tiles, 32x32x16 edges" : "f32 32x32x2")
     << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << "\n";
   if (!bf16) {
@@ -316,29 +348,30 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
     // 128x128 kernel are two instances of one loop with edge guards; both run
     // 4 waves per SIMD: at most 128 registers per lane.
     const std::string M = g.dims[m.m].name, N = g.dims[m.n].name, K = g.dims[m.k].name;
+    const auto a256 = args(256), a128 = args(128);
     o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "_w(\n    " << signature << ") {\n"
-      << epi.str() << "  tca::hip::gemm_f32_4w<" << nk << ">" << args;
+      << epi.str() << a256.first << "  tca::hip::gemm_f32_4w<" << nk << ">" << a256.second;
     o << "extern \"C\" __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) " << symbol
       << "_v(\n    " << signature << ") {\n"
-      << epi.str() << "  tca::hip::gemm_f32_tile<" << nk << ", 256, 256>" << args;
+      << epi.str() << a256.first << "  tca::hip::gemm_f32_tile<" << nk << ", 256, 256>" << a256.second;
     o << "extern \"C\" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) " << symbol
       << "(\n    " << signature << ") {\n"
-      << epi.str() << "  tca::hip::gemm_f32_tile<" << nk << ", 128, 128>" << args;
+      << epi.str() << a128.first << "  tca::hip::gemm_f32_tile<" << nk << ", 128, 128>" << a128.second;
     GemmKernel w;
     w.suffix = "_w";
     w.block = 256;
-    w.grid = {M + "/256", N + "/256"};
+    w.grid = tiles(256);
     w.when = {M + " 4096 4294967295 256 0", N + " 4096 4294967295 256 0", K + " 128 4294967295 32 0"};
     w.detail = "f32 mfma 32x32 tile=256x256 bk=16 4 waves of 128x128, direct-to-LDS ring (whole tiles, M, N >= 4096, K % 32 == 0, K >= 128)" + orient;
     GemmKernel v;
     v.suffix = "_v";
     v.block = 1024;
-    v.grid = {M + "/256", N + "/256"};
+    v.grid = tiles(256);
     v.when = {M + " 4096 4294967295 1 0", N + " 4096 4294967295 1 0"};
     v.unless = w.when;
     v.detail = "f32 mfma 32x32 tile=256x256 bk=16 16 waves, two LDS buffers (M, N >= 4096)" + orient;
     GemmKernel k;
-    k.grid = {M + "/128", N + "/128"};
+    k.grid = tiles(128);
     k.unless = v.when;
     k.detail = "f32 mfma 32x32 tile=128x128 bk=16 4 waves, two LDS buffers" + orient;
     out->kernels.push_back(w);
@@ -354,13 +387,16 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   // direct-to-LDS one (M, N multiples of 256, K a positive multiple of 32).
   // Each kernel returns at once on the other kernels' tiles.
   const std::string M = g.dims[m.m].name, N = g.dims[m.n].name, K = g.dims[m.k].name;
+  const auto a256 = args(256);
   o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "_w(\n    " << signature << ") {\n"
-    << epi.str() << "  tca::hip::gemm_bf16_4w<" << nk << (f16 ? ", decltype(epi), true" : "") << ">" << args;
+    << epi.str() << a256.first << "  tca::hip::gemm_bf16_4w<" << nk << (f16 ? ", decltype(epi), true" : "") << ">"
+    << a256.second;
   o << "extern \"C\" __global__ void __launch_bounds__(512) " << symbol << "_v(\n    " << signature << ") {\n"
-    << epi.str() << "  tca::hip::gemm_bf16_256_w8<" << nk << (f16 ? ", decltype(epi), 4, true" : "") << ">" << args;
+    << epi.str() << a256.first << "  tca::hip::gemm_bf16_256_w8<" << nk << (f16 ? ", decltype(epi), 4, true" : "")
+    << ">" << a256.second;
   o << "extern \"C\" __global__ void __launch_bounds__(256) " << symbol << "(\n    " << signature << ") {\n"
-    << epi.str() << "  tca::hip::gemm_bf16_256<" << nk << ", decltype(epi), 1, true, true, true" << (f16 ? ", true" : "")
-    << ">" << args;
+    << epi.str() << a256.first << "  tca::hip::gemm_bf16_256<" << nk << ", decltype(epi), 1, true, true, true"
+    << (f16 ? ", true" : "") << ">" << a256.second;
   GemmKernel w;
   w.suffix = "_w";
   w.block = 256;

@@ -31,7 +31,7 @@ bool IsParamOrCast(const ir::Graph& g, int id, int param, Elem* in) {
 
 bool MatchGemm(const ir::Graph& g, const ir::Chain& c, GemmMatch* m) {
   if (c.root.ops.size() != 2 || c.reduces.size() != 1) return false;
-  if (c.root.as.size() != 3) return false;
+  if (c.root.as.size() != 3 && c.root.as.size() != 4) return false;
   const ir::ReduceStage& r = c.reduces[0];
   // init +0.0f
   const ir::Expr& init = g.exprs[r.init];
@@ -50,29 +50,54 @@ bool MatchGemm(const ir::Graph& g, const ir::Chain& c, GemmMatch* m) {
   bool swapped = IsParamOrCast(g, body.args[0], p1, &e1) && IsParamOrCast(g, body.args[1], p0, &e0);
   if (!direct && !swapped) return false;
   if (e0 != e1) return false;
-  // Axes.
+  // Axes: [m][n], or [b][m][n] with a leading batch axis.
   const int k = r.axis;
   std::vector<int> live = c.LiveAxes();
-  if (live.size() != 2 || c.store_axes.size() != 2) return false;
+  const size_t nst = c.root.as.size() - 1;
+  if (live.size() != nst || c.store_axes.size() != nst) return false;
   if (g.tensors[c.store_tensor].elem != Elem::F32) return false;
-  const int mAx = c.store_axes[0], nAx = c.store_axes[1];
+  const int bAx = nst == 3 ? c.store_axes[0] : -1;
+  const int mAx = c.store_axes[nst - 2], nAx = c.store_axes[nst - 1];
+  // An operand's axes are (x, y), or (b, x, y) when batched.
+  auto is2 = [&](const std::vector<int>& ax, int x, int y, bool* batched) {
+    if (ax.size() == 2 && ax[0] == x && ax[1] == y) {
+      *batched = false;
+      return true;
+    }
+    if (bAx >= 0 && ax.size() == 3 && ax[0] == bAx && ax[1] == x && ax[2] == y) {
+      *batched = true;
+      return true;
+    }
+    return false;
+  };
   const auto& o0 = c.root.ops[0].axes;
   const auto& o1 = c.root.ops[1].axes;
-  auto isA = [&](const std::vector<int>& ax) { return ax.size() == 2 && ax[0] == mAx && ax[1] == k; };
-  auto isBkn = [&](const std::vector<int>& ax) { return ax.size() == 2 && ax[0] == k && ax[1] == nAx; };
-  auto isBnk = [&](const std::vector<int>& ax) { return ax.size() == 2 && ax[0] == nAx && ax[1] == k; };
   GemmMatch out;
-  if (isA(o0) && (isBkn(o1) || isBnk(o1))) {
+  bool ab = false, bb = false;
+  auto tryAB = [&](const std::vector<int>& a, const std::vector<int>& b) {
+    if (!is2(a, mAx, k, &ab)) return false;
+    if (is2(b, k, nAx, &bb)) {
+      out.b_nk = false;
+      return true;
+    }
+    if (is2(b, nAx, k, &bb)) {
+      out.b_nk = true;
+      return true;
+    }
+    return false;
+  };
+  if (tryAB(o0, o1)) {
     out.a_op = 0;
     out.b_op = 1;
-    out.b_nk = isBnk(o1);
-  } else if (isA(o1) && (isBkn(o0) || isBnk(o0))) {
+  } else if (tryAB(o1, o0)) {
     out.a_op = 1;
     out.b_op = 0;
-    out.b_nk = isBnk(o0);
   } else {
     return false;
   }
+  out.batch = bAx;
+  out.a_batched = ab;
+  out.b_batched = bb;
   // Piped epilogue operands must be indexed by m and/or n only.
   if (c.has_piped)
     for (const auto& op : c.piped.ops)

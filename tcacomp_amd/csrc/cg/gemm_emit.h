@@ -6,8 +6,11 @@
 //     cast<f32>(l)*cast<f32>(r) for bf16 operands;
 //   - exactly one reduce, over the last `as` axis k, with init +0.0f and
 //     combiner acc+now (either order);
-//   - the store writes out[m][n] (f32) over the two remaining axes;
-//   - one operand is indexed [m][k], the other [k][n] or [n][k];
+//   - the store writes out[m][n] (f32) over the two remaining axes, or
+//     out[b][m][n] with a leading batch axis b (one contraction per b);
+//   - one operand is indexed [m][k], the other [k][n] or [n][k], each
+//     optionally led by the batch axis (an operand without it is shared by
+//     every batch);
 //   - an optional piped map becomes the MFMA epilogue (scalars and tensor
 //     operands indexed by m and/or n).
 // Anything else falls back to another family; the match never guesses.
@@ -26,7 +29,9 @@ namespace cg {
 struct GemmMatch {
   int a_op = -1, b_op = -1;  // root operand indices
   int m = -1, n = -1, k = -1;
-  bool b_nk = false;  // B indexed [n][k]
+  int batch = -1;                          // leading batch axis, or -1
+  bool a_batched = false, b_batched = false;  // operand led by the batch axis
+  bool b_nk = false;                       // B indexed [n][k]
   ir::Elem in = ir::Elem::F32;
 };
 

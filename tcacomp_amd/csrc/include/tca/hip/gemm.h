@@ -66,9 +66,12 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // dealt round-robin over the 8 XCDs; regrouping so that each XCD receives a
 // contiguous run of tiles (and walking those runs in GROUP_M-row bands) keeps
 // the A row panels and B column panels a run touches inside one XCD's L2.
-__device__ __forceinline__ void gemm_tile_coords(uint32_t tiles_m, uint32_t tiles_n, uint32_t* tm, uint32_t* tn) {
+// `tile` is the linear tile index: the workgroup id, or for a batched
+// contraction the workgroup id within its batch (the emitted kernel passes it).
+__device__ __forceinline__ void gemm_tile_coords(uint32_t tiles_m, uint32_t tiles_n, uint32_t* tm, uint32_t* tn,
+                                                 uint32_t tile) {
   const uint32_t total = tiles_m * tiles_n;
-  uint32_t b = blockIdx.x;
+  uint32_t b = tile;
   if (total % 8u == 0u) b = (b % 8u) * (total / 8u) + b / 8u;
   const uint32_t kGroup = 8u;
   const uint32_t band = kGroup * tiles_n;
@@ -125,12 +128,13 @@ __device__ __forceinline__ bool gemm_bf16_dma_tile(uint32_t m0, uint32_t n0, uin
 template <bool B_NK, typename Epi, int SWZ = 1, bool SPREAD = true, bool PREFETCH = true, bool SKIP_DMA = false,
           bool F16 = false>
 __device__ __forceinline__ void gemm_bf16_256(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
-                                              float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
+                                              float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi,
+                                              uint32_t tile = ~0u) {
   constexpr uint32_t BM = 256, BN = 256, BK = 64, TILE = BM * BK;
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][TILE];  // [buffer][A, B]
   const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   uint32_t tm, tn;
-  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
+  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn, tile == ~0u ? blockIdx.x : tile);
   const uint32_t m0 = tm * BM, n0 = tn * BN;
   if (SKIP_DMA && gemm_bf16_dma_tile(m0, n0, M, N, K)) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -429,14 +433,15 @@ __device__ __forceinline__ bf16x8 frag_b16_tr(const uint16_t* Bs, uint32_t n_col
 // waves of 128x128, A in 64-deep slices, below).
 template <bool B_NK, typename Epi, uint32_t STAGES = 4, bool F16 = false>
 __device__ __forceinline__ void gemm_bf16_256_w8(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
-                                                 float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
+                                                 float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi,
+                                                 uint32_t tile = ~0u) {
   static_assert(STAGES == 4 || STAGES == 5, "a ring of 4 or 5 slices (160 KiB of LDS at most)");
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   constexpr uint32_t BM = 256, BN = 256, BK = 32, SLICE = 256u * BK;
   __shared__ __attribute__((aligned(16))) uint16_t lds[STAGES * 2 * SLICE];
   const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   uint32_t tm, tn;
-  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
+  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn, tile == ~0u ? blockIdx.x : tile);
   const uint32_t m0 = tm * BM, n0 = tn * BN;
   if (!gemm_bf16_dma_tile(m0, n0, M, N, K)) return;  // gemm_bf16_256<..., SKIP_DMA> takes it
   // The wave index is uniform over the wave: computed in a scalar register,
@@ -696,12 +701,13 @@ __device__ __forceinline__ uint32_t swz_rows64(uint32_t row, uint32_t g) { retur
 
 template <bool B_NK, typename Epi, bool F16 = false>
 __device__ __forceinline__ void gemm_bf16_4w(const __bf16* __restrict__ A, const __bf16* __restrict__ B,
-                                             float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
+                                             float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi,
+                                             uint32_t tile = ~0u) {
   constexpr uint32_t BM = 256, BN = 256, ASL = 256u * 64u, BSL = 256u * 32u;
   __shared__ __attribute__((aligned(16))) uint16_t lds[3 * ASL + 4 * BSL];
   const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   uint32_t tm, tn;
-  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
+  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn, tile == ~0u ? blockIdx.x : tile);
   const uint32_t m0 = tm * BM, n0 = tn * BN;
   if (!gemm_bf16_dma_tile(m0, n0, M, N, K) || K % 64u != 0u || K < 256u) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -887,7 +893,8 @@ __device__ __forceinline__ void gemm_bf16_4w(const __bf16* __restrict__ A, const
 // loop, 127.
 template <bool B_NK, int BM, int BN, int BK = 16, typename Epi>
 __device__ __forceinline__ void gemm_f32_tile(const float* __restrict__ A, const float* __restrict__ B,
-                                              float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
+                                              float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi,
+                                              uint32_t tile = ~0u) {
   static_assert((BM == 128 || BM == 256) && BM == BN, "square 128 or 256 tiles");
   static_assert(BK == 16 || BK == 32, "slices of 16 or 32");
   constexpr int WN = BN / 64, THREADS = 64 * (BM / 64) * WN;
@@ -899,7 +906,7 @@ __device__ __forceinline__ void gemm_f32_tile(const float* __restrict__ A, const
   __shared__ __attribute__((aligned(16))) float lds[2 * (SA + SB)];
   const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   uint32_t tm, tn;
-  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
+  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn, tile == ~0u ? blockIdx.x : tile);
   const uint32_t m0 = tm * BM, n0 = tn * BN;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wm = (wave / WN) * 64u, wn = (wave % WN) * 64u;
@@ -1102,13 +1109,14 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 template <bool B_NK, typename Epi>
 __device__ __forceinline__ void gemm_f32_4w(const float* __restrict__ A, const float* __restrict__ B,
-                                            float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi) {
+                                            float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, Epi epi,
+                                            uint32_t tile = ~0u) {
   constexpr uint32_t BM = 256, BN = 256, ASL = 256u * 16u, LDBK = 264u, BSL = B_NK ? 256u * 16u : 16u * LDBK;
   constexpr uint32_t SLOT = ASL + BSL;
   __shared__ __attribute__((aligned(16))) float lds[4 * SLOT];
   const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   uint32_t tm, tn;
-  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn);
+  gemm_tile_coords(tiles_m, tiles_n, &tm, &tn, tile == ~0u ? blockIdx.x : tile);
   const uint32_t m0 = tm * BM, n0 = tn * BN;
   if (m0 + BM > M || n0 + BN > N || K % 32u != 0u || K < 128u) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);

@@ -461,6 +461,48 @@ def gemm_f32_nt():
     return _matmul("gemm_f32_nt", TF32, b_nk=True)
 
 
+def _bmatmul(name, elem, b_nk=False, a_batched=True, b_batched=True, epilogue=None, scalars=()):
+    """out[b][m][n] = sum_k lhs[b][m][k] * rhs[b][k][n] (rhs [b][n][k] when
+    b_nk); an operand built without the batch axis is shared by every batch."""
+    b = NewBuilder(name)
+    B, M, K, N = b.Dim("B", 0), b.Dim("M", 0), b.Dim("K", 0), b.Dim("N", 0)
+    lhs = b.Tensor("lhs", elem, *((B, M, K) if a_batched else (M, K)))
+    rdims = (N, K) if b_nk else (K, N)
+    rhs = b.Tensor("rhs", elem, *(((B,) + rdims) if b_batched else rdims))
+    out = b.Tensor("out", TF32, B, M, N)
+    sc = [b.ScalarParam(s, TF32) for s in scalars]
+    if elem == TF32:
+        body = lambda l, r: b.Mul(l, r)  # noqa: E731
+    else:
+        body = lambda l, r: b.Mul(Cast(l, TF32), Cast(r, TF32))  # noqa: E731
+    la = At(lhs, B, M, K) if a_batched else At(lhs, M, K)
+    rb = At(rhs, *(((B,) if b_batched else ()) + ((N, K) if b_nk else (K, N))))
+    ar = (b.Stmt().Iter(B, M, N, K).Map([la, rb], body).As(B, M, N, K)
+          .Reduce(b.Float32(0), _sum(b)))
+    if epilogue is not None:
+        ar.Map([], lambda v: epilogue(b, v, *sc)).As(B, M, N).Store(out, B, M, N)
+    else:
+        ar.Store(out, B, M, N)
+    return b.Build()
+
+
+def bmm_f32():
+    """A batch of fp32 contractions, both operands per batch."""
+    return _bmatmul("bmm_f32", TF32)
+
+
+def bmm_bf16_nt():
+    """A batch of bf16 contractions with B given as [b][N][K]: the per-head
+    scores Q @ K^T of attention."""
+    return _bmatmul("bmm_bf16_nt", TBF16, b_nk=True)
+
+
+def bmm_f16_shared_scale():
+    """A batch of f16 contractions against one shared B, times a scale."""
+    return _bmatmul("bmm_f16_shared_scale", TF16, b_batched=False,
+                    epilogue=lambda b, v, s: b.Mul(v, s), scalars=("scale",))
+
+
 # ---- the reference suite (testing/kernels/**.tca) ------------------------
 
 def _rank3_reduce(name, k_extent, body, scalars=(), piped=None, piped_scalars=(), middle=False):
@@ -707,6 +749,10 @@ CONFIG_PROGRAMS = {
     "gemm_f32_nt": gemm_f32_nt,
     "gemm_f16": gemm_f16,
     "gemm_f16_nt": gemm_f16_nt,
+    # batched contractions: one (m, n) grid of tiles per batch
+    "bmm_f32": bmm_f32,
+    "bmm_bf16_nt": bmm_bf16_nt,
+    "bmm_f16_shared_scale": bmm_f16_shared_scale,
     # small-row variants exercised by the parity tests (tails, few lanes per row)
     "row_sum_max_1000": lambda: row_sum_max(1000),
     "row_sum_max_64": lambda: row_sum_max(64),
