@@ -361,16 +361,44 @@ def _traffic(symbol, prog, key=None):
     return e["bytes"], "profiles/traffic.json (%s, code object %s)" % (t.get("_profiled", "?"), key)
 
 
+def _window_us(prog, args, sc, stream, steps, hold_cycles=0):
+    """Microseconds per launch between two events around `steps` launches.
+    With hold_cycles > 0 a spin kernel of that many clock cycles is queued
+    first, so the launches are all queued before the GPU reaches them and
+    run back to back: the window is then device time per launch (kernel
+    durations and the dispatch gaps between them), not the host's launch
+    rate."""
+    import torch
+    from tcacomp_amd import _lib
+    L = _lib.lib()
+    e0, e1 = _events()
+    torch.cuda.synchronize()
+    if hold_cycles:
+        torch.cuda._sleep(int(hold_cycles))
+    _lib.check(L.tca_rt_event_record(e0, ctypes.c_void_p(stream)))
+    for _ in range(steps):
+        prog.launch(args, scalars=sc, stream=stream)
+    _lib.check(L.tca_rt_event_record(e1, ctypes.c_void_p(stream)))
+    torch.cuda.synchronize()
+    ms = ctypes.c_float()
+    _lib.check(L.tca_rt_event_elapsed_ms(e0, e1, ctypes.byref(ms)))
+    L.tca_rt_event_destroy(e0)
+    L.tca_rt_event_destroy(e1)
+    return ms.value * 1e3 / steps
+
+
 def _suite(dev, steps):
     """The reference's 14 suite kernels at testing/suite.toml's dims, inputs
-    from elem(i): device time per launch (hipEvents over `steps` launches),
+    from elem(i): kernel_us, the device time per launch (`steps` launches
+    queued behind a spin kernel, so they run back to back: the kernels'
+    durations plus the dispatch gaps between them); launch_rate_us, the
+    same event window without the hold (bounded by the host's launch rate);
     the reference runner's BenchReport (host launch + synchronize per
-    iteration, 20 iterations), the achieved rate over suite.toml's
-    bench_bytes (and flops for contractions), and the reference's own A6000
-    figures."""
+    iteration, 20 iterations); the achieved rate over suite.toml's
+    bench_bytes (and flops for contractions) at kernel_us; and the
+    reference's own A6000 figures."""
     import torch
-    from tcacomp_amd import _lib, compiler, programs, suite
-    L = _lib.lib()
+    from tcacomp_amd import compiler, programs, suite
     stream = torch.cuda.current_stream().cuda_stream
     out = {}
     for name in sorted(suite.REGISTRY):
@@ -381,17 +409,16 @@ def _suite(dev, steps):
         for _ in range(20):
             prog.launch(args, scalars=sc, stream=stream)
         torch.cuda.synchronize()
-        e0, e1 = _events()
-        _lib.check(L.tca_rt_event_record(e0, ctypes.c_void_p(stream)))
+        rate_us = _window_us(prog, args, sc, stream, steps)
+        # Hold the queue for three times the host's enqueue time (clock
+        # cycles at up to 2.4 GHz), so every launch is queued before the
+        # first one runs.
+        t0 = time.perf_counter()
         for _ in range(steps):
             prog.launch(args, scalars=sc, stream=stream)
-        _lib.check(L.tca_rt_event_record(e1, ctypes.c_void_p(stream)))
+        enqueue_s = time.perf_counter() - t0
         torch.cuda.synchronize()
-        ms = ctypes.c_float()
-        _lib.check(L.tca_rt_event_elapsed_ms(e0, e1, ctypes.byref(ms)))
-        L.tca_rt_event_destroy(e0)
-        L.tca_rt_event_destroy(e1)
-        dev_us = ms.value * 1e3 / steps
+        dev_us = _window_us(prog, args, sc, stream, steps, hold_cycles=3 * enqueue_s * 2.4e9)
         host = []
         for _ in range(20):
             t0 = time.perf_counter()
@@ -400,16 +427,16 @@ def _suite(dev, steps):
             host.append((time.perf_counter() - t0) * 1e6)
         cat, dims, tol, bench_bytes = suite.REGISTRY[name]
         ref_avg, ref_min = suite.REFERENCE_A6000_US[name]
-        e = {"dims": list(dims), "kernels": prog.selected_symbols(args), "device_us": dev_us,
-             "bench_us": {"avg": sum(host) / len(host), "min": min(host)},
+        e = {"dims": list(dims), "kernels": prog.selected_symbols(args), "kernel_us": dev_us,
+             "launch_rate_us": rate_us, "bench_us": {"avg": sum(host) / len(host), "min": min(host)},
              "bench_bytes": bench_bytes, "achieved_GBps": bench_bytes / (dev_us * 1e-6) / 1e9,
              "reference_a6000_bench_us": {"avg": ref_avg, "min": ref_min},
              "speedup_vs_reference_min": ref_min / min(host)}
         if suite.flops(name):
             e["achieved_GFLOPs"] = suite.flops(name) / (dev_us * 1e-6) / 1e9
         out[name] = e
-        print("[bench] suite %s %.2f us device, %.1f us launch+sync (reference A6000 %.1f us)"
-              % (name, dev_us, min(host), ref_min), file=sys.stderr, flush=True)
+        print("[bench] suite %s %.2f us per launch on the device, %.2f us launch rate, %.1f us launch+sync "
+              "(reference A6000 %.1f us)" % (name, dev_us, rate_us, min(host), ref_min), file=sys.stderr, flush=True)
     return out
 
 

@@ -159,6 +159,12 @@ int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tens
                        const double* scalars, uint32_t n_scalars, tca_stream_t stream);
 /* Name of kernel i of the program (for profiling), or NULL. */
 const char* tca_program_kernel_name(tca_program p, uint32_t i);
+/* The program's plan as this library reads it, printed back in the plan
+ * format (one canonical spelling of every record: parsing it again gives the
+ * same plan), or NULL for a null program. The text lives until the program
+ * is unloaded. No counterpart in the reference (its launcher is emitted
+ * code, not data); for tools and tests that inspect or rewrite plans. */
+const char* tca_program_plan_text(tca_program p);
 
 /* tca_program_launch without any allocation: no counterpart in the
  * reference. For callers that cannot allocate device memory (code under HIP

@@ -96,6 +96,7 @@ SIGNATURES = [
     ("tca_program_launch_noalloc", _c.c_int,
      [_P, _c.POINTER(tca_tensor), _U32, _c.POINTER(_U32), _U32, _c.POINTER(_c.c_double), _U32, _P]),
     ("tca_program_kernel_name", _STR, [_P, _U32]),
+    ("tca_program_plan_text", _STR, [_P]),
     # builder + emitter (tca_cg.h)
     ("tca_builder_new", _P, [_STR]),
     ("tca_builder_free", None, [_P]),

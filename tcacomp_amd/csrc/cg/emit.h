@@ -37,6 +37,8 @@ struct Options {
   bool comments = true;
   bool allow_fused = true;       // false: every chain lowers to the generic family
   bool allow_gemm = true;
+  // The contractions' small-tile kernels for output planes of M*N <= 2^20.
+  bool allow_gemm_split = true;
   // Geometry knobs (power-of-two values; 0 = default). Row family: target
   // 16-byte vectors per lane and row operand (lanes per row follow from it).
   // Elementwise family: 16-byte vectors per thread and operand.

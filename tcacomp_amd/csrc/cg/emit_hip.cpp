@@ -267,8 +267,8 @@ std::string Sym(const Graph& g, const std::string& prefix, int k) {
 using namespace detail;
 
 bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std::string& symbol,
-              const std::string& signature, int* counter, std::ostringstream* src, GemmEmitted* out,
-              std::string* err) {
+              const std::string& signature, int nest, bool small, int* counter, std::ostringstream* src,
+              GemmEmitted* out, std::string* err) {
   (void)err;
   std::ostringstream& o = *src;
   const int ta = c.root.ops[m.a_op].tensor, tb = c.root.ops[m.b_op].tensor, tc = c.store_tensor;
@@ -340,6 +340,73 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
     << g.dims[m.k].name << " on MFMA ("
     << (f16 ? "f16 16x16x32 whole tiles, 32x32x16 edges" : bf16 ? "bf16 16x16x32 whole tiles, 32x32x16 edges" : "f32 32x32x2")
     << "), B indexed " << (m.b_nk ? "[n][k]" : "[k][n]") << "\n";
+  // Output planes of at most kGemmSmallMax elements: 32x32 tiles with K
+  // split over the 16 waves of a workgroup and, when the tiles are fewer
+  // than the split target, over P chunks (the split record; P > 1 adds the
+  // merge kernel). The tile kernels below carry the complementary guard.
+  std::string bigWhen;
+  if (small) {
+    const std::string Ms = g.dims[m.m].name, Ns = g.dims[m.n].name, Ks = g.dims[m.k].name;
+    const uint32_t kKcMin = bf16 ? 1024u : 512u;  // 4 steps per wave and chunk
+    const uint32_t kBlocks = 512u;                // two 16-wave workgroups per CU
+    const std::string part = "__gemmpart" + std::to_string(nest), pdim = "__gemmdim" + std::to_string(nest);
+    out->extra_dims.push_back(pdim + " " + std::to_string(uint64_t{kBlocks} * 1024u));
+    out->extra_tensors.push_back(part + " f32 local 1 " + pdim);
+    const std::string psig = ",\n    float* __restrict__ pw /* " + part + " */";
+    auto body = [&](bool merge) {
+      std::ostringstream b;
+      b << epi.str() << "  const uint32_t tiles = ((M + 31u) / 32u) * ((N + 31u) / 32u);\n"
+        << "  const uint32_t T = " << (batched ? ExtentExpr(g, m.batch) + " * tiles" : std::string("tiles")) << ";\n"
+        << "  const uint32_t P = tca::hip::gemm_split_chunks(K, T, " << kKcMin << "u, " << kBlocks << "u);\n"
+        << (merge ? "  const uint32_t gt = blockIdx.x;\n" : "  const uint32_t gt = blockIdx.x % T, p = blockIdx.x / T;\n");
+      std::string a = "t" + std::to_string(ta), bo = "t" + std::to_string(tb), cc = "t" + std::to_string(tc);
+      if (batched) {
+        b << "  const uint32_t bb = gt / tiles, tile = gt - bb * tiles;\n";
+        if (m.a_batched) a = "(" + a + " + (size_t)bb * M * K)";
+        if (m.b_batched) bo = "(" + bo + " + (size_t)bb * K * N)";
+        cc = "(" + cc + " + (size_t)bb * M * N)";
+      } else {
+        b << "  const uint32_t tile = gt;\n";
+      }
+      if (merge)
+        b << "  tca::hip::gemm_small_merge(" << cc << ", pw, M, N, epi, tile, gt, T, P);\n}\n\n";
+      else
+        b << "  tca::hip::gemm_small<" << (bf16 ? "true" : "false") << ", " << (m.b_nk ? "true" : "false")
+          << ", decltype(epi)" << (f16 ? ", true" : "") << ">(" << a << ", " << bo << ", " << cc
+          << ", pw, M, N, K, epi, tile, gt, T, p, P);\n}\n\n";
+      return b.str();
+    };
+    o << "extern \"C\" __global__ void __launch_bounds__(1024) " << symbol << "_s(\n    " << signature << psig
+      << ") {\n" << body(false);
+    o << "extern \"C\" __global__ void __launch_bounds__(1024) " << symbol << "_sm(\n    " << signature << psig
+      << ") {\n" << body(true);
+    std::vector<std::string> t32;
+    if (batched) t32.push_back(g.dims[m.batch].name + "/1");
+    t32.push_back(Ms + "/32");
+    t32.push_back(Ns + "/32");
+    std::string splitTerms = std::to_string(t32.size());
+    for (const auto& t : t32) splitTerms += " " + t;
+    const std::string splitRec = Ks + " " + std::to_string(kKcMin) + " " + std::to_string(kBlocks);
+    const std::string smallWhen = Ms + "*" + Ns + " 0 " + std::to_string(kGemmSmallMax) + " 1 0";
+    bigWhen = Ms + "*" + Ns + " " + std::to_string(kGemmSmallMax + 1) + " 18446744073709551615 1 0";
+    const std::string ty = f16 ? "f16 mfma 32x32x16" : bf16 ? "bf16 mfma 32x32x16" : "f32 mfma 32x32x2";
+    GemmKernel s;
+    s.suffix = "_s";
+    s.block = 1024;
+    s.grid = t32;
+    s.when = {smallWhen};
+    s.extra_args = {"ptr " + part};
+    s.split = splitRec + " 0 " + splitTerms;
+    s.detail = ty + " tile=32x32, K split over 16 waves (and P chunks of >= " + std::to_string(kKcMin) +
+               " when the tiles are fewer than " + std::to_string(kBlocks) + "; M*N <= " +
+               std::to_string(kGemmSmallMax) + ")" + orient;
+    GemmKernel sm = s;
+    sm.suffix = "_sm";
+    sm.split = splitRec + " 1 " + splitTerms;
+    sm.detail = ty + " small-tile merge: the P chunk partials of each 32x32 tile added in chunk order (P > 1 only)";
+    out->kernels.push_back(s);
+    out->kernels.push_back(sm);
+  }
   if (!bf16) {
     // From M, N >= 4096 on (at least 256 tiles of 256x256): whole tiles with
     // K % 32 == 0 and K >= 128 on 4 waves of 128x128 fed by a direct-to-LDS
@@ -373,6 +440,7 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
     GemmKernel k;
     k.grid = tiles(128);
     k.unless = v.when;
+    if (!bigWhen.empty()) k.when.push_back(bigWhen);
     k.detail = "f32 mfma 32x32 tile=128x128 bk=16 4 waves, two LDS buffers" + orient;
     out->kernels.push_back(w);
     out->kernels.push_back(v);
@@ -415,6 +483,8 @@ bool EmitGemm(const Graph& g, const ir::Chain& c, const GemmMatch& m, const std:
   e.grid = grid;
   e.unless = {M + " 0 4294967295 256 0", N + " 0 4294967295 256 0", K + " 32 4294967295 32 0"};
   e.detail = ty + " mfma 32x32 tile=256x256 bk=64 4 waves (edge tiles, K % 32 != 0, N % 8 != 0)" + orient;
+  if (!bigWhen.empty())
+    for (GemmKernel* k : {&w, &v, &e}) k->when.push_back(bigWhen);
   out->kernels.push_back(w);
   out->kernels.push_back(v);
   out->kernels.push_back(e);
@@ -3700,7 +3770,9 @@ class Emitter {
     Nest single = n;
     const std::string sig = Signature(single, &pk);
     GemmEmitted ge;
-    if (!EmitGemm(g_, c, m, pk.symbol, sig, &counter_, &src_, &ge, err)) return false;
+    if (!EmitGemm(g_, c, m, pk.symbol, sig, ni, opts_.allow_gemm_split, &counter_, &src_, &ge, err)) return false;
+    for (const auto& d : ge.extra_dims) extra_dims_.push_back(d);
+    for (const auto& t : ge.extra_tensors) extra_tensors_.push_back(t);
     for (const auto& gk : ge.kernels) {
       PlanKernel k = pk;
       k.symbol = pk.symbol + gk.suffix;
@@ -3709,6 +3781,8 @@ class Emitter {
       k.grid = gk.grid;
       k.when = gk.when;
       k.unless = gk.unless;
+      for (const auto& a : gk.extra_args) k.args.push_back(a);
+      k.split = gk.split;
       AddKernel(k, Family::Gemm, n.chains, gk.detail);
     }
     return true;

@@ -40,17 +40,28 @@ struct GemmKernel {
   std::string suffix;
   uint32_t block = 256, lds = 0;
   std::vector<std::string> grid, when, unless;
+  std::vector<std::string> extra_args;  // plan args after the signature's ("ptr <local>")
+  std::string split;                    // the plan's split record, if any
   std::string detail;
 };
 
 struct GemmEmitted {
   std::vector<GemmKernel> kernels;
+  std::vector<std::string> extra_dims;     // plan-only dims: "<name> <extent>"
+  std::vector<std::string> extra_tensors;  // plan-only locals: "<name> <dtype> local <rank> <dims...>"
 };
 
+// Output planes of at most kGemmSmallMax elements (M*N) take the small-tile
+// kernel (32x32 tiles, K split over the waves of a workgroup and, when the
+// tiles are few, over workgroups); larger ones the 128/256 tile kernels.
+constexpr uint64_t kGemmSmallMax = 1ull << 20;
+
+// `nest` names the partial scratch of the small kernel's K split
+// (__gemmpart<nest>); `small` false leaves the small kernel out.
 bool MatchGemm(const ir::Graph& g, const ir::Chain& c, GemmMatch* m);
 bool EmitGemm(const ir::Graph& g, const ir::Chain& c, const GemmMatch& m, const std::string& symbol,
-              const std::string& signature, int* counter, std::ostringstream* src, GemmEmitted* out,
-              std::string* err);
+              const std::string& signature, int nest, bool small, int* counter, std::ostringstream* src,
+              GemmEmitted* out, std::string* err);
 
 namespace detail {
 std::string CType(ir::Elem e);

@@ -1271,6 +1271,235 @@ __device__ __forceinline__ void gemm_f32_4w(const float* __restrict__ A, const f
       }
 }
 
+// ------------------------------------------------ small contractions, K split
+// The tile kernels above give one workgroup a 128x128 or 256x256 tile and
+// the whole of K, so a contraction with few tiles (the reference suite's
+// gemm, mlp, mm_* and qk_score have M, N <= 192: one or two workgroups) runs
+// on one or two CUs, walking K alone (testing/kernels/tiling/mm_splitk.tca:1-2
+// names the split-k schedule class for them). Here a workgroup of 16 waves
+// owns a 32x32 tile of C and a chunk of K:
+//   - the chunk's k steps (8 deep for f32, 16 deep for 16-bit inputs) are
+//     dealt round-robin to the 16 waves; each wave accumulates the whole
+//     32x32 tile in one MFMA block (4 x v_mfma_f32_32x32x2f32 per step, or
+//     one v_mfma_f32_32x32x16_{bf16,f16});
+//   - the waves' tiles meet in LDS and are summed in wave order;
+//   - with P > 1 chunks (P = gemm_split_chunks(K, tiles, KCMIN, BLOCKS),
+//     the formula of the launch plan's split record) the workgroup of chunk
+//     p writes its sum to a partial scratch [P][tiles][1024] and a second
+//     kernel (gemm_small_merge) adds the P partials in chunk order.
+// Every order is fixed, so the result does not depend on the schedule.
+// Operands go from memory straight into the MFMA operand registers (no LDS
+// staging: the waves of a workgroup read disjoint k, so nothing is shared
+// inside it; neighbouring tiles share panels through the L2):
+//   f32 step at k0, lane l (r = l % 32, h = l / 32): A[m0+r][k0+4h+e] and
+//   B[k0+4h+e][n0+r] for e = 0..3, one float4 where the operand is
+//   K-contiguous; MFMA e sums k0+e (lanes 0-31) and k0+4+e (lanes 32-63), so
+//   a step sums each of its 8 k once;
+//   16-bit step at k0: lane l holds A[m0+r][k0+8h .. +7] and
+//   B[k0+8h .. +7][n0+r] (the 32x32x16 operand layout), one MFMA.
+// Result element i of lane l is C[m0 + 8(i/4) + 4(l/32) + i%4][n0 + l%32];
+// a wave's tile goes to LDS element-major (word i*64 + l: conflict-free) and
+// thread t = i*64 + l of the workgroup sums word t over the waves.
+constexpr uint32_t kSmallWaves = 16;
+
+// P chunks of K for `tiles` output tiles: enough workgroups to reach
+// `blocks`, each chunk at least kc_min deep (1 when K or tiles is 0). The
+// launch plan's split record computes the same number (SplitChunks).
+__host__ __device__ __forceinline__ uint32_t gemm_split_chunks(uint32_t k, uint32_t tiles, uint32_t kc_min,
+                                                               uint32_t blocks) {
+  if (k == 0u || tiles == 0u) return 1u;
+  uint32_t p = (k - 1u) / kc_min + 1u;
+  const uint32_t cap = blocks / tiles;
+  if (p > cap) p = cap;
+  return p ? p : 1u;
+}
+
+// Coordinates (row, column) inside a 32x32 tile of the value thread t holds
+// after the wave merge.
+__device__ __forceinline__ uint32_t small_row(uint32_t t) {
+  const uint32_t i = t >> 6, l = t & 63u;
+  return 8u * (i >> 2) + 4u * (l >> 5) + (i & 3u);
+}
+__device__ __forceinline__ uint32_t small_col(uint32_t t) { return t & 31u; }
+
+// A wave's steps of its chunk: s = s_begin + wave + j * kSmallWaves below
+// s_end. Steps whose operands are all in range (an interior tile and a whole
+// step of K) are loaded without guards, up to four before their MFMAs (the
+// later ones under wave-uniform tests); the decision is made once, outside
+// the loops: a load that could take either path inside the loop joins the
+// two in register copies that wait for the loads just issued, which
+// serialises the steps. The rest (at most one short step of K on interior
+// tiles; every step of an edge tile) take the guarded loads one at a time.
+// `load(fast, s, &a, &b)` loads step s into registers of type Reg,
+// `mma(a, b)` accumulates it.
+template <uint32_t KS, typename Reg, typename Load, typename Mma>
+__device__ __forceinline__ void small_steps(uint32_t s_begin, uint32_t s_end, uint32_t wave, bool interior,
+                                            uint32_t K, Load&& load, Mma&& mma) {
+  using Fast = std::true_type;
+  using Slow = std::false_type;
+  constexpr uint32_t W = kSmallWaves;
+  uint32_t s = s_begin + wave;
+  if (interior) {
+    const uint32_t whole = K / KS;  // steps lying wholly inside K
+    const uint32_t fe = s_end < whole ? s_end : whole;
+    // After a group, s moves past the steps it took: the next of this wave's
+    // steps, so the guarded loop below starts at the first one at or past fe.
+    for (; s < fe; s += W * (1u + (s + W < fe) + (s + 2u * W < fe) + (s + 3u * W < fe))) {
+      const bool h1 = s + W < fe, h2 = s + 2u * W < fe, h3 = s + 3u * W < fe;
+      Reg a0, b0, a1, b1, a2, b2, a3, b3;
+      load(Fast{}, s, &a0, &b0);
+      if (h1) load(Fast{}, s + W, &a1, &b1);
+      if (h2) load(Fast{}, s + 2u * W, &a2, &b2);
+      if (h3) load(Fast{}, s + 3u * W, &a3, &b3);
+      mma(a0, b0);
+      if (h1) mma(a1, b1);
+      if (h2) mma(a2, b2);
+      if (h3) mma(a3, b3);
+    }
+  }
+  for (; s < s_end; s += W) {
+    Reg a0, b0;
+    load(Slow{}, s, &a0, &b0);
+    mma(a0, b0);
+  }
+}
+
+// `tile` is the tile within its contraction (row-major over ceil(N/32)
+// columns of tiles), `gtile` the tile's index over all T tiles of the
+// launch (batches included): the partial scratch is indexed by it.
+template <bool H16, bool B_NK, typename Epi, bool F16 = false>
+__device__ __forceinline__ void gemm_small(const void* __restrict__ Av, const void* __restrict__ Bv,
+                                           float* __restrict__ C, float* __restrict__ part, uint32_t M, uint32_t N,
+                                           uint32_t K, Epi epi, uint32_t tile, uint32_t gtile, uint32_t T, uint32_t p,
+                                           uint32_t P) {
+  constexpr uint32_t KS = H16 ? 16u : 8u;   // k per step
+  constexpr uint32_t KPL = H16 ? 8u : 4u;   // k per lane and step
+  __shared__ __attribute__((aligned(16))) float red[kSmallWaves * 1024u];
+  const uint32_t tiles_n = (N + 31u) / 32u;
+  const uint32_t m0 = (tile / tiles_n) * 32u, n0 = (tile % tiles_n) * 32u;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t r = lane & 31u, h = lane >> 5;
+  const uint32_t am = m0 + r, bn = n0 + r;
+  // Chunk p: whole steps [s_begin, s_end) (the last step of K may be short).
+  const uint32_t steps = K / KS + (K % KS != 0u ? 1u : 0u);
+  const uint32_t per = steps / P + (steps % P != 0u ? 1u : 0u);
+  const uint32_t s_begin = p * per < steps ? p * per : steps;
+  const uint32_t s_end = s_begin + per < steps ? s_begin + per : steps;
+  // Unguarded vector loads: the whole tile in range and every lane's k run
+  // 16-byte aligned (K a multiple of the run; the tensors are 16-byte
+  // aligned and so is every batch's slice then).
+  const bool interior = m0 + 32u <= M && n0 + 32u <= N && K % KPL == 0u;
+  f32x16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  if constexpr (!H16) {
+    const float* __restrict__ A = static_cast<const float*>(Av);
+    const float* __restrict__ B = static_cast<const float*>(Bv);
+    auto load = [&](auto fast, uint32_t s, float4* a, float4* b) {
+      const uint32_t k0 = s * KS + KPL * h;
+      if constexpr (decltype(fast)::value) {
+        *a = *reinterpret_cast<const float4*>(A + static_cast<uint64_t>(am) * K + k0);
+        if constexpr (B_NK) {
+          *b = *reinterpret_cast<const float4*>(B + static_cast<uint64_t>(bn) * K + k0);
+        } else {
+          const float* q = B + static_cast<uint64_t>(k0) * N + bn;
+          *b = make_float4(q[0], q[N], q[2u * N], q[3u * N]);
+        }
+        return;
+      } else {
+      float va[4], vb[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t k = k0 + e;
+        va[e] = (am < M && k < K) ? A[static_cast<uint64_t>(am) * K + k] : 0.0f;
+        if constexpr (B_NK) vb[e] = (bn < N && k < K) ? B[static_cast<uint64_t>(bn) * K + k] : 0.0f;
+        else vb[e] = (bn < N && k < K) ? B[static_cast<uint64_t>(k) * N + bn] : 0.0f;
+      }
+      *a = make_float4(va[0], va[1], va[2], va[3]);
+      *b = make_float4(vb[0], vb[1], vb[2], vb[3]);
+      }
+    };
+    auto mma = [&](const float4& a, const float4& b) {
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, acc, 0, 0, 0);
+    };
+    small_steps<KS, float4>(s_begin, s_end, wave, interior, K, load, mma);
+  } else {
+    const uint16_t* __restrict__ A = static_cast<const uint16_t*>(Av);
+    const uint16_t* __restrict__ B = static_cast<const uint16_t*>(Bv);
+    auto load = [&](auto fast, uint32_t s, u32x4* a, u32x4* b) {
+      const uint32_t k0 = s * KS + KPL * h;
+      if constexpr (decltype(fast)::value) {
+        *a = *reinterpret_cast<const u32x4*>(A + static_cast<uint64_t>(am) * K + k0);
+        if constexpr (B_NK) {
+          *b = *reinterpret_cast<const u32x4*>(B + static_cast<uint64_t>(bn) * K + k0);
+        } else {
+          const uint16_t* q = B + static_cast<uint64_t>(k0) * N + bn;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            (*b)[e] = static_cast<uint32_t>(q[(2u * e) * N]) | (static_cast<uint32_t>(q[(2u * e + 1u) * N]) << 16);
+        }
+        return;
+      } else {
+      uint32_t va[8], vb[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t k = k0 + e;
+        va[e] = (am < M && k < K) ? A[static_cast<uint64_t>(am) * K + k] : 0u;
+        if constexpr (B_NK) vb[e] = (bn < N && k < K) ? B[static_cast<uint64_t>(bn) * K + k] : 0u;
+        else vb[e] = (bn < N && k < K) ? B[static_cast<uint64_t>(k) * N + bn] : 0u;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        (*a)[e] = va[2 * e] | (va[2 * e + 1] << 16);
+        (*b)[e] = vb[2 * e] | (vb[2 * e + 1] << 16);
+      }
+      }
+    };
+    auto mma = [&](const u32x4& a, const u32x4& b) {
+      acc = mfma_32x32x16_16b<F16>(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc);
+    };
+    small_steps<KS, u32x4>(s_begin, s_end, wave, interior, K, load, mma);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) red[wave * 1024u + static_cast<uint32_t>(i) * 64u + lane] = acc[i];
+  __syncthreads();
+  float sum = red[tid];
+#pragma unroll
+  for (uint32_t w = 1; w < kSmallWaves; ++w) sum += red[w * 1024u + tid];
+  if (P > 1u) {
+    part[(static_cast<uint64_t>(p) * T + gtile) * 1024u + tid] = sum;
+    return;
+  }
+  const uint32_t m = m0 + small_row(tid), n = n0 + small_col(tid);
+  if (m < M && n < N) C[static_cast<uint64_t>(m) * N + n] = epi(sum, m, n);
+}
+
+// The P > 1 merge: one 1024-thread workgroup per tile, thread t adds word t
+// of the tile's P partials in chunk order, applies the epilogue and stores.
+template <typename Epi>
+__device__ __forceinline__ void gemm_small_merge(float* __restrict__ C, const float* __restrict__ part, uint32_t M,
+                                                 uint32_t N, Epi epi, uint32_t tile, uint32_t gtile, uint32_t T,
+                                                 uint32_t P) {
+  const uint32_t tid = threadIdx.x, tiles_n = (N + 31u) / 32u;
+  const uint32_t m = (tile / tiles_n) * 32u + small_row(tid), n = (tile % tiles_n) * 32u + small_col(tid);
+  const float* q = part + static_cast<uint64_t>(gtile) * 1024u + tid;
+  const uint64_t stride = static_cast<uint64_t>(T) * 1024u;
+  float sum = q[0];
+  uint32_t c = 1;
+  for (; c + 4u <= P; c += 4u) {
+    const float v0 = q[c * stride], v1 = q[(c + 1u) * stride], v2 = q[(c + 2u) * stride], v3 = q[(c + 3u) * stride];
+    sum += v0;
+    sum += v1;
+    sum += v2;
+    sum += v3;
+  }
+  for (; c < P; ++c) sum += q[c * stride];
+  if (m < M && n < N) C[static_cast<uint64_t>(m) * N + n] = epi(sum, m, n);
+}
+
 }  // namespace hip
 }  // namespace tca
 

@@ -250,8 +250,15 @@ bool Parse(const std::string& text, Plan* out, std::string* err) {
       if ((tok.size() != 6 && !g.pow2) || !ParseU64(tok[2], &g.lo) || !ParseU64(tok[3], &g.hi) ||
           !ParseU64(tok[4], &g.mod) || !ParseU64(tok[5], &g.rem))
         return bad(kw + " <dim> <lo> <hi> <mod> <rem> [pow2]");
-      g.dim = FindDim(p, tok[1]);
-      if (g.dim < 0) return bad(kw + " names unknown dim " + tok[1]);
+      for (size_t start = 0;;) {  // d1*d2*...: the product of the named dims
+        const size_t star = tok[1].find('*', start);
+        const std::string dn = tok[1].substr(start, star == std::string::npos ? std::string::npos : star - start);
+        const int d = FindDim(p, dn);
+        if (d < 0) return bad(kw + " names unknown dim " + dn);
+        g.dims.push_back(d);
+        if (star == std::string::npos) break;
+        start = star + 1;
+      }
       if (g.mod == 0 || g.rem >= g.mod || g.lo > g.hi || (g.pow2 && g.rem != 0)) return bad("bad guard on " + tok[1]);
       (kw == "when" ? p.kernels.back().when : p.kernels.back().unless).push_back(g);
     } else if (kw == "end") {
@@ -314,6 +321,14 @@ uint64_t TermValue(const Kernel& k, const Term& t, const std::vector<uint32_t>& 
   return q;
 }
 
+std::string GuardText(const Plan& p, const Guard& g) {
+  std::ostringstream o;
+  for (size_t i = 0; i < g.dims.size(); ++i) o << (i ? "*" : "") << p.dims[g.dims[i]].name;
+  o << " " << g.lo << " " << g.hi << " " << g.mod << " " << g.rem;
+  if (g.pow2) o << " pow2";
+  return o.str();
+}
+
 }  // namespace
 
 std::string Serialize(const Plan& p) {
@@ -344,10 +359,8 @@ std::string Serialize(const Plan& p) {
       for (const auto& t : k.split_terms) o << " " << TermText(p, t);
       o << "\n";
     }
-    for (const auto& g : k.when)
-      o << "when " << p.dims[g.dim].name << " " << g.lo << " " << g.hi << " " << g.mod << " " << g.rem << "\n";
-    for (const auto& g : k.unless)
-      o << "unless " << p.dims[g.dim].name << " " << g.lo << " " << g.hi << " " << g.mod << " " << g.rem << "\n";
+    for (const auto& g : k.when) o << "when " << GuardText(p, g) << "\n";
+    for (const auto& g : k.unless) o << "unless " << GuardText(p, g) << "\n";
   }
   o << "end\n";
   return o.str();
@@ -510,7 +523,11 @@ uint32_t PackRows(const Kernel& k, const std::vector<uint32_t>& dims, uint32_t* 
 
 bool Selected(const Kernel& k, const std::vector<uint32_t>& dims) {
   auto holds = [&](const Guard& g) {
-    const uint64_t v = dims[g.dim];
+    uint64_t v = 1;  // a product of at most a few u32 dims; saturates rather than wraps
+    for (int d : g.dims) {
+      const uint64_t x = dims[d];
+      v = (x != 0 && v > ~uint64_t{0} / x) ? ~uint64_t{0} : v * x;
+    }
     if (!(v >= g.lo && v <= g.hi && v % g.mod == g.rem)) return false;
     if (!g.pow2) return true;
     const uint64_t q = v / g.mod;

@@ -27,7 +27,9 @@
 //       P > 1 (the partials of a nest whose P == 1 case is a mode-2 kernel).
 //   when <dim> <lo> <hi> <mod> <rem>    (for the last kernel) the kernel runs only
 //       when lo <= dim <= hi and dim % mod == rem; every guard of a kernel must
-//       hold. Variants of one nest specialised on a run-time dim carry guards
+//       hold. <dim> may be a product of dims, d1*d2*... (its value taken in
+//       64 bits): the contractions pick their small-tile kernel by the size of
+//       the output plane, M*N. Variants of one nest specialised on a run-time dim carry guards
 //       that partition its values, so exactly one of them launches.
 //   unless <dim> <lo> <hi> <mod> <rem>  (for the last kernel) the same test; the
 //       kernel is skipped when every one of its unless guards holds (the
@@ -89,7 +91,7 @@ struct Arg {
 };
 
 struct Guard {
-  int dim = 0;  // index into Plan::dims
+  std::vector<int> dims;  // indices into Plan::dims; the guarded value is their product
   uint64_t lo = 0, hi = 0xffffffffull, mod = 1, rem = 0;
   bool pow2 = false;  // additionally dim / mod is a power of two (rem == 0)
 };

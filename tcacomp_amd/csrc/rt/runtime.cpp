@@ -118,6 +118,7 @@ struct tca_program_s {
   // launches on different streams may overlap and must not.
   std::map<tca_stream_t, Workspace> workspaces;
   std::mutex mu;  // guards `workspaces`
+  std::string plan_text;  // tca_program_plan_text's buffer, filled on first request
 };
 
 extern "C" {
@@ -370,6 +371,13 @@ int tca_program_signature(tca_program p, uint32_t* n_tensors, uint32_t* n_free_d
 const char* tca_program_kernel_name(tca_program p, uint32_t i) {
   if (p == nullptr || i >= p->plan.kernels.size()) return nullptr;
   return p->plan.kernels[i].symbol.c_str();
+}
+
+const char* tca_program_plan_text(tca_program p) {
+  if (p == nullptr) return nullptr;
+  std::lock_guard<std::mutex> lk(p->mu);
+  if (p->plan_text.empty()) p->plan_text = tca::plan::Serialize(p->plan);
+  return p->plan_text.c_str();
 }
 
 int tca_program_check(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,

@@ -36,6 +36,7 @@ _NEG, _POS, _LNOT, _NOT = range(4)
 
 EMIT_NO_FUSION = 1
 EMIT_NO_GEMM = 2
+EMIT_NO_GEMM_SPLIT = 4  # no small-tile K-split contraction kernels (the tile kernels only)
 
 
 class BuildError(Exception):

@@ -497,6 +497,17 @@ def bmm_bf16_nt():
     return _bmatmul("bmm_bf16_nt", TBF16, b_nk=True)
 
 
+def bmm_f32_nt_shared_a():
+    """fp32 contractions with one A [M][K] shared by every batch and B given
+    as [b][N][K]."""
+    return _bmatmul("bmm_f32_nt_shared_a", TF32, b_nk=True, a_batched=False)
+
+
+def bmm_bf16():
+    """A batch of bf16 contractions, B given as [b][K][N]."""
+    return _bmatmul("bmm_bf16", TBF16)
+
+
 def bmm_f16_shared_scale():
     """A batch of f16 contractions against one shared B, times a scale."""
     return _bmatmul("bmm_f16_shared_scale", TF16, b_batched=False,
@@ -753,6 +764,8 @@ CONFIG_PROGRAMS = {
     "bmm_f32": bmm_f32,
     "bmm_bf16_nt": bmm_bf16_nt,
     "bmm_f16_shared_scale": bmm_f16_shared_scale,
+    "bmm_f32_nt_shared_a": bmm_f32_nt_shared_a,
+    "bmm_bf16": bmm_bf16,
     # small-row variants exercised by the parity tests (tails, few lanes per row)
     "row_sum_max_1000": lambda: row_sum_max(1000),
     "row_sum_max_64": lambda: row_sum_max(64),
@@ -787,7 +800,7 @@ CONFIG_PROGRAMS = {
 
 def all_builds():
     """(program factory, flags) pairs for every code object build() makes."""
-    from .pkg import EMIT_NO_FUSION, EMIT_NO_GEMM
+    from .pkg import EMIT_NO_FUSION, EMIT_NO_GEMM, EMIT_NO_GEMM_SPLIT
     out = []
     for name, f in sorted(CONFIG_PROGRAMS.items()):
         out.append((name, f, 0))
@@ -799,4 +812,14 @@ def all_builds():
     for name in ("scale_relu", "row_sum_max_1000", "softmax_200", "layernorm_96", "gemm_f32", "chain_sum_max",
                  "chain_total", "chain3_max_total"):
         out.append((name + "_generic", CONFIG_PROGRAMS[name], EMIT_NO_FUSION | EMIT_NO_GEMM))
+    # the contractions on their tile kernels alone: small output planes take
+    # the small-tile kernel otherwise, and the tests hold both to the oracle
+    for name in TILE_ONLY:
+        out.append((name + "_tiles", CONFIG_PROGRAMS[name], EMIT_NO_GEMM_SPLIT))
     return out
+
+
+# Contractions the tests also run with EMIT_NO_GEMM_SPLIT (the 128/256 tile
+# kernels at every shape).
+TILE_ONLY = ("gemm_f32", "gemm_f32_nt", "gemm_bf16", "gemm_bf16_nt", "gemm_f16", "gemm_f16_nt", "bmm_f32",
+             "bmm_bf16_nt", "bmm_f16_shared_scale", "bmm_f32_nt_shared_a", "bmm_bf16")

@@ -257,12 +257,16 @@ def test_chain_segment_static_drops_the_local():
     (4100, 4096, 4128, ["_v", ""]),
     (4096, 4096, 4100, [""]),        # K % 32 != 0: no tile takes the direct-to-LDS path
     (4096, 4100, 4096, [""]),        # N % 8 != 0: [K][N] rows not 16-byte aligned, no direct-to-LDS tile
-    (255, 4096, 4096, [""]), (512, 512, 0, [""]), (512, 512, 16, [""])])
+    (257, 4096, 4096, ["_w", ""]), (1025, 1025, 16, [""]),
+    # output planes of at most 2^20 elements: the small-tile K-split kernel
+    (255, 4096, 4096, ["_s"]), (512, 512, 0, ["_s"]), (512, 512, 16, ["_s"]), (64, 64, 4096, ["_s", "_sm"])])
 def test_bf16_gemm_kernel_selection(M, N, K, want):
-    """The bf16 contraction's three kernels: an 8-wave direct-to-LDS kernel
+    """The bf16 contraction's three tile kernels: an 8-wave direct-to-LDS kernel
     runs when a whole tile can take it (A in 64-deep slices when K % 64 == 0
     and K >= 256, else in 32-deep slices), the register-staged one unless
-    every tile does (plan `when` / `unless` guards)."""
+    every tile does (plan `when` / `unless` guards); output planes of
+    M*N <= 2^20 take the small-tile kernel instead (and its merge when K is
+    split over workgroups)."""
     e = programs.CONFIG_PROGRAMS["gemm_bf16"]().emit()
     rc, h = parse(e.plan)
     assert rc == 0, _lib.last_error()
@@ -285,7 +289,8 @@ def test_bf16_gemm_kernel_selection(M, N, K, want):
     (4100, 4096, 4096, ["_v"]),      # a partial row of tiles
     (4096, 4100, 4096, ["_v"]),
     (4095, 4096, 4096, [""]),        # below 4096: 128x128 tiles
-    (1024, 8192, 4096, [""]), (512, 512, 0, [""])])
+    (1024, 8192, 4096, [""]), (1025, 1024, 64, [""]),
+    (1024, 1024, 4096, ["_s"]), (512, 512, 0, ["_s"]), (32, 32, 4096, ["_s", "_sm"])])
 def test_f32_gemm_kernel_selection(M, N, K, want):
     """The fp32 contraction's three kernels, exactly one launched: the 4-wave
     direct-to-LDS kernel when M, N >= 4096 and every tile is whole (M, N
@@ -539,8 +544,9 @@ def test_program_launch_without_module_is_refused():
 
 
 EXPECTED_FAMILIES = {
-    "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"] * 3,
-    "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"] * 3, "gemm_bf16": ["gemm"] * 3,
+    # contractions: the small-tile kernel and its merge, then three tile kernels
+    "scale_relu": ["elementwise"], "scale_relu_map": ["elementwise"], "row_sum_max_8192": ["row"], "gemm_bf16_nt": ["gemm"] * 5,
+    "softmax_4096": ["row"], "layernorm_1024": ["row"], "gemm_f32": ["gemm"] * 5, "gemm_bf16": ["gemm"] * 5,
     "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 13, "softmax_dyn": ["stream"] * 25,
     "layernorm_dyn": ["stream"] * 25, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 10,
     # narrow rows: one more width per halving of the element size (8 bf16, 16 u8 elements per vector)

@@ -14,8 +14,12 @@ import pytest
 import oracle
 from helpers import assert_reduce_close, canaries, compiled, host, out_dev, run, to_dev
 from tcacomp_amd import inputs
+from tcacomp_amd.pkg import EMIT_NO_GEMM_SPLIT
 
 pytestmark = pytest.mark.gpu
+# Batches of small planes take the small-tile kernel by default; with
+# EMIT_NO_GEMM_SPLIT the tile kernels the shapes were chosen for.
+SPLIT = pytest.mark.parametrize("flags", [0, EMIT_NO_GEMM_SPLIT], ids=["small", "tiles"])
 
 
 def _say(*a):
@@ -48,12 +52,13 @@ def _check(got, a, b, nt, scale=1.0, what=""):
 
 
 @pytest.mark.parametrize("B,M,N,K", [(3, 33, 65, 17), (2, 256, 256, 128), (2, 300, 130, 64)])
-def test_bmm_f32(gpu, B, M, N, K):
-    _say("bmm f32", B, M, N, K)
+@SPLIT
+def test_bmm_f32(gpu, B, M, N, K, flags):
+    _say("bmm f32", B, M, N, K, flags)
     a = inputs.uniform((B, M, K), -1, 1, 0)
     b = inputs.uniform((B, K, N), -1, 1, 1)
     c = out_dev((B, M, N), gpu)
-    run(compiled("bmm_f32"), [to_dev(a, gpu), to_dev(b, gpu), c])
+    run(compiled("bmm_f32", flags), [to_dev(a, gpu), to_dev(b, gpu), c])
     got = host(c)
     assert canaries(got) == 0
     _check(got, a, b, False, what="bmm f32")
@@ -81,24 +86,26 @@ BF16_SHAPES = [(3, 33, 65, 40), (4, 256, 512, 96), (2, 512, 256, 256), (3, 300, 
 
 
 @pytest.mark.parametrize("B,M,N,K", BF16_SHAPES)
-def test_bmm_bf16_nt(gpu, B, M, N, K):
-    _say("bmm bf16 nt", B, M, N, K)
+@SPLIT
+def test_bmm_bf16_nt(gpu, B, M, N, K, flags):
+    _say("bmm bf16 nt", B, M, N, K, flags)
     a = oracle.to_bf16_bits(inputs.uniform((B, M, K), -1, 1, 2))
     b = oracle.to_bf16_bits(inputs.uniform((B, N, K), -1, 1, 3))
     c = out_dev((B, M, N), gpu)
-    run(compiled("bmm_bf16_nt"), [_dev16(a, gpu), _dev16(b, gpu), c])
+    run(compiled("bmm_bf16_nt", flags), [_dev16(a, gpu), _dev16(b, gpu), c])
     got = host(c)
     assert canaries(got) == 0
     _check(got, a, b, True, what="bmm bf16 nt")
 
 
 @pytest.mark.parametrize("B,M,N,K", [(3, 300, 520, 256), (2, 256, 256, 96), (1, 17, 9, 8)])
-def test_bmm_f16_shared_rhs_scale(gpu, B, M, N, K):
-    _say("bmm f16 shared", B, M, N, K)
+@SPLIT
+def test_bmm_f16_shared_rhs_scale(gpu, B, M, N, K, flags):
+    _say("bmm f16 shared", B, M, N, K, flags)
     a = inputs.uniform((B, M, K), -1, 1, 4).astype(np.float16)
     b = inputs.uniform((K, N), -1, 1, 5).astype(np.float16)
     c = out_dev((B, M, N), gpu)
-    run(compiled("bmm_f16_shared_scale"), [to_dev(a, gpu), to_dev(b, gpu), c], scalars=[0.5])
+    run(compiled("bmm_f16_shared_scale", flags), [to_dev(a, gpu), to_dev(b, gpu), c], scalars=[0.5])
     got = host(c)
     assert canaries(got) == 0
     _check(got, a, b, False, scale=0.5, what="bmm f16 shared")

@@ -21,10 +21,15 @@ from helpers import (assert_layernorm_close, assert_reduce_close, canaries, comp
                      to_dev)
 from tcacomp_amd import inputs
 from tcacomp_amd.compiler import TensorDesc
-from tcacomp_amd.pkg import EMIT_NO_FUSION, EMIT_NO_GEMM
+from tcacomp_amd.pkg import EMIT_NO_FUSION, EMIT_NO_GEMM, EMIT_NO_GEMM_SPLIT
 
 pytestmark = pytest.mark.gpu
 GENERIC = EMIT_NO_FUSION | EMIT_NO_GEMM
+# Contractions at these shapes take the small-tile K-split kernel (output
+# planes of M*N <= 2^20); TILES holds the same programs to the oracle on the
+# 128/256 tile kernels.
+TILES = EMIT_NO_GEMM_SPLIT
+SPLIT = pytest.mark.parametrize("flags", [0, TILES], ids=["small", "tiles"])
 
 
 def _say(*a):
@@ -187,12 +192,13 @@ def _gemm_bound(a, b, K):
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (33, 65, 17), (128, 128, 128), (200, 136, 300), (512, 384, 1024),
                                    (64, 64, 0)])
-def test_c5_gemm_f32(gpu, M, N, K):
-    _say("C5 f32", M, N, K)
+@SPLIT
+def test_c5_gemm_f32(gpu, M, N, K, flags):
+    _say("C5 f32", M, N, K, flags)
     a = inputs.uniform((M, K), -1, 1, 0)
     b = inputs.uniform((K, N), -1, 1, 1)
     want = oracle.gemm(a, b)
-    p = compiled("gemm_f32")
+    p = compiled("gemm_f32", flags)
     c = out_dev((M, N), gpu)
     run(p, [to_dev(a, gpu), to_dev(b, gpu), c])
     got = host(c)
@@ -201,13 +207,14 @@ def test_c5_gemm_f32(gpu, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 8), (33, 65, 17), (128, 128, 128), (200, 136, 300), (512, 384, 1024)])
-def test_c5_gemm_bf16(gpu, M, N, K):
+@SPLIT
+def test_c5_gemm_bf16(gpu, M, N, K, flags):
     import torch
-    _say("C5 bf16", M, N, K)
+    _say("C5 bf16", M, N, K, flags)
     a = oracle.to_bf16_bits(inputs.uniform((M, K), -1, 1, 0))
     b = oracle.to_bf16_bits(inputs.uniform((K, N), -1, 1, 1))
     want = oracle.gemm(a, b)
-    p = compiled("gemm_bf16")
+    p = compiled("gemm_bf16", flags)
     c = out_dev((M, N), gpu)
     ta = to_dev(a.view(np.int16), gpu).view(torch.bfloat16)
     tb = to_dev(b.view(np.int16), gpu).view(torch.bfloat16)
@@ -219,17 +226,18 @@ def test_c5_gemm_bf16(gpu, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 8), (33, 65, 17), (256, 256, 32), (512, 768, 512), (300, 520, 96)])
-def test_c5_gemm_bf16_nt(gpu, M, N, K):
+@SPLIT
+def test_c5_gemm_bf16_nt(gpu, M, N, K, flags):
     """B given as [N][K]: shapes cover the direct-to-LDS interior path
     (256-multiples, K % 32 == 0) and the general edge path in one launch."""
     import torch
-    _say("C5 bf16 NT", M, N, K)
+    _say("C5 bf16 NT", M, N, K, flags)
     a = oracle.to_bf16_bits(inputs.uniform((M, K), -1, 1, 0))
     b = oracle.to_bf16_bits(inputs.uniform((N, K), -1, 1, 1))
     want = oracle.gemm(a, b, b_nk=True)
     c = out_dev((M, N), gpu)
-    run(compiled("gemm_bf16_nt"), [to_dev(a.view(np.int16), gpu).view(torch.bfloat16),
-                                   to_dev(b.view(np.int16), gpu).view(torch.bfloat16), c])
+    run(compiled("gemm_bf16_nt", flags), [to_dev(a.view(np.int16), gpu).view(torch.bfloat16),
+                                          to_dev(b.view(np.int16), gpu).view(torch.bfloat16), c])
     got = host(c)
     assert canaries(got) == 0
     bound = _gemm_bound(oracle.bf16_bits_to_f32(a), np.ascontiguousarray(oracle.bf16_bits_to_f32(b).T), K)
@@ -238,7 +246,8 @@ def test_c5_gemm_bf16_nt(gpu, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(96, 160, 64), (256, 512, 96), (512, 512, 256), (512, 768, 320), (512, 256, 192),
                                    (768, 512, 512), (520, 512, 256)])
-def test_c5_gemm_exact_integers(gpu, M, N, K):
+@SPLIT
+def test_c5_gemm_exact_integers(gpu, M, N, K, flags):
     """Small-integer operands: every product and partial sum is exact in
     fp32, so any order gives the exact result (pins the MFMA lane layout,
     the LDS swizzles and the transposing B reads: a transposed, shifted or
@@ -246,24 +255,26 @@ def test_c5_gemm_exact_integers(gpu, M, N, K):
     direct-to-LDS kernels: A in 64-deep slices for K % 64 == 0 and K >= 256
     (K = 256 and 320 are its shortest loops: 8 and 10 steps, the peeled
     tail only), 32-deep slices otherwise (K = 96, 192); the rest the
-    general path, in the same launch when tiles of both kinds exist."""
+    general path, in the same launch when tiles of both kinds exist (with
+    `tiles`; the default build runs them all on the small-tile kernel)."""
     import torch
+    _say("C5 exact", M, N, K, flags)
     rng = np.random.default_rng(5)
     a = rng.integers(-4, 5, (M, K)).astype(np.float32)
     b = rng.integers(-4, 5, (K, N)).astype(np.float32)
     want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
     c = out_dev((M, N), gpu)
-    run(compiled("gemm_f32"), [to_dev(a, gpu), to_dev(b, gpu), c])
+    run(compiled("gemm_f32", flags), [to_dev(a, gpu), to_dev(b, gpu), c])
     assert np.array_equal(host(c), want)
     ab, bb = oracle.to_bf16_bits(a), oracle.to_bf16_bits(b)
     c = out_dev((M, N), gpu)
-    run(compiled("gemm_bf16"), [to_dev(ab.view(np.int16), gpu).view(torch.bfloat16),
-                                to_dev(bb.view(np.int16), gpu).view(torch.bfloat16), c])
+    run(compiled("gemm_bf16", flags), [to_dev(ab.view(np.int16), gpu).view(torch.bfloat16),
+                                       to_dev(bb.view(np.int16), gpu).view(torch.bfloat16), c])
     assert np.array_equal(host(c), want)
     bt = np.ascontiguousarray(bb.T)
     c = out_dev((M, N), gpu)
-    run(compiled("gemm_bf16_nt"), [to_dev(ab.view(np.int16), gpu).view(torch.bfloat16),
-                                   to_dev(bt.view(np.int16), gpu).view(torch.bfloat16), c])
+    run(compiled("gemm_bf16_nt", flags), [to_dev(ab.view(np.int16), gpu).view(torch.bfloat16),
+                                          to_dev(bt.view(np.int16), gpu).view(torch.bfloat16), c])
     assert np.array_equal(host(c), want)
 
 

@@ -12,6 +12,7 @@ import pytest
 import oracle
 from helpers import assert_reduce_close, canaries, compiled, host, out_dev, run, to_dev
 from tcacomp_amd import inputs
+from tcacomp_amd.pkg import EMIT_NO_GEMM_SPLIT
 
 pytestmark = pytest.mark.gpu
 
@@ -32,13 +33,16 @@ SHAPES = [(1, 1, 8), (33, 65, 17), (256, 256, 32), (256, 512, 96), (512, 384, 10
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
 @pytest.mark.parametrize("nt", [False, True])
-def test_gemm_f16(gpu, M, N, K, nt):
-    _say("C5 f16", M, N, K, "nt" if nt else "nn")
+@pytest.mark.parametrize("flags", [0, EMIT_NO_GEMM_SPLIT], ids=["small", "tiles"])
+def test_gemm_f16(gpu, M, N, K, nt, flags):
+    """These output planes take the small-tile kernel by default and the
+    tile kernels named above with EMIT_NO_GEMM_SPLIT."""
+    _say("C5 f16", M, N, K, "nt" if nt else "nn", flags)
     a = inputs.uniform((M, K), -1, 1, 0).astype(np.float16)
     b = inputs.uniform((N, K) if nt else (K, N), -1, 1, 1).astype(np.float16)
     want = oracle.gemm(a.astype(np.float32), b.astype(np.float32), b_nk=nt)
     c = out_dev((M, N), gpu)
-    run(compiled("gemm_f16_nt" if nt else "gemm_f16"), [to_dev(a, gpu), to_dev(b, gpu), c])
+    run(compiled("gemm_f16_nt" if nt else "gemm_f16", flags), [to_dev(a, gpu), to_dev(b, gpu), c])
     got = host(c)
     assert canaries(got) == 0
     b_kn = np.ascontiguousarray(b.T) if nt else b
