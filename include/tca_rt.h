@@ -159,6 +159,17 @@ int tca_program_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tens
                        const double* scalars, uint32_t n_scalars, tca_stream_t stream);
 /* Name of kernel i of the program (for profiling), or NULL. */
 const char* tca_program_kernel_name(tca_program p, uint32_t i);
+/* The argument block kernel `kernel` would be launched with for these
+ * tensors, free dims and scalars, written to buf (the HIP kernarg layout:
+ * natural alignment, pointers 8 bytes, dims and scalars 4), *size receiving
+ * its length. A local in the program's workspace appears as its byte offset
+ * from a workspace at address 0. Host-only (no GPU, no launch); the same
+ * shape contract as tca_program_launch, TCA_ERR_INVALID when that kernel does
+ * not run at these dims or `cap` is too small. No counterpart in the
+ * reference; for tests and for tools that launch the code object themselves. */
+int tca_program_kernel_args(tca_program p, const tca_tensor* tensors, uint32_t n_tensors,
+                            const uint32_t* free_dims, uint32_t n_free_dims, const double* scalars,
+                            uint32_t n_scalars, uint32_t kernel, void* buf, size_t cap, size_t* size);
 /* The program's plan as this library reads it, printed back in the plan
  * format (one canonical spelling of every record: parsing it again gives the
  * same plan), or NULL for a null program. The text lives until the program

@@ -8,7 +8,9 @@ import ctypes
 import os
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG_DIR, "libtcacomp.so")
+# TCA_LIB names another build of the same library (the sanitizer gate loads
+# tcacomp_amd/_asan/libtcacomp.so, built with AddressSanitizer and UBSan).
+LIB_PATH = os.environ.get("TCA_LIB") or os.path.join(PKG_DIR, "libtcacomp.so")
 
 TCA_MAX_RANK = 8
 
@@ -97,6 +99,7 @@ SIGNATURES = [
      [_P, _c.POINTER(tca_tensor), _U32, _c.POINTER(_U32), _U32, _c.POINTER(_c.c_double), _U32, _P]),
     ("tca_program_kernel_name", _STR, [_P, _U32]),
     ("tca_program_plan_text", _STR, [_P]),
+    ("tca_program_kernel_args", _I32, [_P, _P, _U32, _P, _U32, _P, _U32, _U32, _P, _c.c_size_t, _P]),
     # builder + emitter (tca_cg.h)
     ("tca_builder_new", _P, [_STR]),
     ("tca_builder_free", None, [_P]),

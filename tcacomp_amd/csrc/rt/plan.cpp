@@ -148,6 +148,7 @@ bool Parse(const std::string& text, Plan* out, std::string* err) {
     }
     if (kw == "program") {
       if (tok.size() != 2) return bad("program <name>");
+      if (!p.name.empty()) return bad("duplicate program record");
       p.name = tok[1];
     } else if (kw == "dim") {
       uint64_t e = 0;
@@ -269,6 +270,7 @@ bool Parse(const std::string& text, Plan* out, std::string* err) {
   }
   if (!header) return bad("empty plan");
   if (!ended) return bad("missing 'end'");
+  if (p.name.empty()) return bad("plan has no program record");
   if (p.kernels.empty()) return bad("plan has no kernel");
   for (const auto& k : p.kernels)
     for (const auto& t : k.grid)
@@ -541,54 +543,39 @@ bool Selected(const Kernel& k, const std::vector<uint32_t>& dims) {
   return false;  // every unless guard holds
 }
 
-bool PackArgs(const Kernel& k, const Plan& p, const std::vector<void*>& ptrs, const std::vector<uint32_t>& dims,
-              const double* scalars, std::vector<unsigned char>* blob, std::string* err) {
+bool LayoutArgs(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims, std::vector<unsigned char>* blob,
+                std::vector<ArgSlot>* slots, std::string* err) {
   blob->clear();
-  auto put = [&](const void* src, size_t n) {
-    size_t off = (blob->size() + n - 1) / n * n;  // natural alignment
+  slots->clear();
+  auto place = [&](size_t n) {  // natural alignment
+    const size_t off = (blob->size() + n - 1) / n * n;
     blob->resize(off + n, 0);
-    std::memcpy(blob->data() + off, src, n);
+    return static_cast<uint32_t>(off);
   };
   for (const auto& a : k.args) {
     switch (a.kind) {
       case ArgKind::Ptr: {
-        void* ptr = ptrs[a.index];
-        put(&ptr, sizeof(ptr));
+        ArgSlot s;
+        s.offset = place(sizeof(void*));
+        s.kind = ArgKind::Ptr;
+        s.index = a.index;
+        slots->push_back(s);
         break;
       }
       case ArgKind::Dim: {
-        uint32_t v = dims[a.index];
-        put(&v, sizeof(v));
+        // The offset first: place() may reallocate the blob.
+        const uint32_t v = dims[a.index];
+        const uint32_t off = place(sizeof(v));
+        std::memcpy(blob->data() + off, &v, sizeof(v));
         break;
       }
       case ArgKind::Scalar: {
-        const double v = scalars[a.index];
-        switch (p.scalars[a.index].dtype) {
-          case TCA_F32:
-          case TCA_F16:
-          case TCA_BF16: {
-            float f = static_cast<float>(v);
-            put(&f, 4);
-            break;
-          }
-          case TCA_U32:
-          case TCA_U16:
-          case TCA_U8: {
-            uint32_t u = static_cast<uint32_t>(v);
-            put(&u, 4);
-            break;
-          }
-          case TCA_BOOL: {
-            int32_t b = v != 0.0 ? 1 : 0;
-            put(&b, 4);
-            break;
-          }
-          default: {
-            int32_t i = static_cast<int32_t>(v);
-            put(&i, 4);
-            break;
-          }
-        }
+        ArgSlot s;
+        s.offset = place(4);
+        s.kind = ArgKind::Scalar;
+        s.index = a.index;
+        s.dtype = p.scalars[a.index].dtype;
+        slots->push_back(s);
         break;
       }
     }
@@ -596,6 +583,46 @@ bool PackArgs(const Kernel& k, const Plan& p, const std::vector<void*>& ptrs, co
   if (blob->empty()) {
     *err = "kernel " + k.symbol + " has no arguments";
     return false;
+  }
+  return true;
+}
+
+void SetScalar(unsigned char* blob, const ArgSlot& s, double v) {
+  switch (s.dtype) {
+    case TCA_F32:
+    case TCA_F16:
+    case TCA_BF16: {
+      const float f = static_cast<float>(v);
+      std::memcpy(blob + s.offset, &f, 4);
+      break;
+    }
+    case TCA_U32:
+    case TCA_U16:
+    case TCA_U8: {
+      const uint32_t u = static_cast<uint32_t>(v);
+      std::memcpy(blob + s.offset, &u, 4);
+      break;
+    }
+    case TCA_BOOL: {
+      const int32_t b = v != 0.0 ? 1 : 0;
+      std::memcpy(blob + s.offset, &b, 4);
+      break;
+    }
+    default: {
+      const int32_t i = static_cast<int32_t>(v);
+      std::memcpy(blob + s.offset, &i, 4);
+      break;
+    }
+  }
+}
+
+bool PackArgs(const Kernel& k, const Plan& p, const std::vector<void*>& ptrs, const std::vector<uint32_t>& dims,
+              const double* scalars, std::vector<unsigned char>* blob, std::string* err) {
+  std::vector<ArgSlot> slots;
+  if (!LayoutArgs(k, p, dims, blob, &slots, err)) return false;
+  for (const auto& s : slots) {
+    if (s.kind == ArgKind::Ptr) std::memcpy(blob->data() + s.offset, &ptrs[s.index], sizeof(void*));
+    else SetScalar(blob->data(), s, scalars[s.index]);
   }
   return true;
 }

@@ -156,6 +156,19 @@ bool Selected(const Kernel& k, const std::vector<uint32_t>& dims);
 bool PackArgs(const Kernel& k, const Plan& p, const std::vector<void*>& ptrs, const std::vector<uint32_t>& dims,
               const double* scalars, std::vector<unsigned char>* blob, std::string* err);
 
+// The same layout split in two, for launches that repeat one shape: a blob
+// with every dim argument written (pointers and scalars zero) and the slots
+// left to fill per call. SetPtr / SetScalar fill one slot.
+struct ArgSlot {
+  uint32_t offset = 0;
+  ArgKind kind = ArgKind::Ptr;  // Ptr or Scalar
+  int index = 0;                // tensor or scalar index
+  int dtype = TCA_F32;          // a scalar's declared type
+};
+bool LayoutArgs(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims, std::vector<unsigned char>* blob,
+                std::vector<ArgSlot>* slots, std::string* err);
+void SetScalar(unsigned char* blob, const ArgSlot& s, double v);
+
 }  // namespace plan
 }  // namespace tca
 

@@ -18,6 +18,7 @@
 #include <cstring>
 #include <fstream>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <sstream>
 #include <string>
@@ -110,6 +111,26 @@ struct tca_program_s {
     void* ptr = nullptr;
     size_t bytes = 0;
   };
+  // Everything a launch decides from the shapes alone, kept for the last
+  // shape launched: a repeat launch at that shape compares the shapes,
+  // checks the pointers, fills pointer and scalar slots into copies of the
+  // argument blobs and launches (no Bind, no guard or grid evaluation, no
+  // heap allocation).
+  struct Prepared {
+    uint32_t n_tensors = 0, n_free = 0;
+    std::vector<uint32_t> key;        // per tensor: rank, dtype, dims...; then the free dims
+    std::vector<uint8_t> nonempty;    // per tensor parameter: it has elements (data must be valid)
+    std::vector<int> param_of;        // per plan tensor: its parameter index, -1 for a local
+    std::vector<size_t> local_off;    // per plan tensor: offset of a local in the workspace
+    size_t ws_bytes = 0;
+    struct Launch {
+      hipFunction_t fn = nullptr;
+      uint32_t grid = 0, block = 0, lds = 0;
+      std::vector<unsigned char> blob;         // dims written, pointer and scalar slots zero
+      std::vector<tca::plan::ArgSlot> slots;
+    };
+    std::vector<Launch> launches;
+  };
   tca::plan::Plan plan;
   hipModule_t mod = nullptr;
   std::vector<hipFunction_t> funcs;
@@ -117,7 +138,8 @@ struct tca_program_s {
   // launched on: launches on one stream are ordered and may share it,
   // launches on different streams may overlap and must not.
   std::map<tca_stream_t, Workspace> workspaces;
-  std::mutex mu;  // guards `workspaces`
+  std::mutex mu;  // guards `workspaces` and `prepared`
+  std::shared_ptr<const Prepared> prepared;
   std::string plan_text;  // tca_program_plan_text's buffer, filled on first request
 };
 
@@ -420,21 +442,48 @@ int tca_program_selected(tca_program p, const tca_tensor* tensors, uint32_t n_te
 
 namespace {
 
-// The body of both launch entry points. `noalloc` takes the workspace from
-// the device's scratch array instead of the program's per-stream workspace.
-int launch_program(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
-                   uint32_t n_free_dims, const double* scalars, uint32_t n_scalars, tca_stream_t stream,
-                   bool noalloc) {
-  if (p == nullptr) return fail(TCA_ERR_INVALID, "program_launch: null program");
-  if (p->mod == nullptr) return fail(TCA_ERR_INVALID, "program_launch: program was parsed, not loaded");
+// Writes this call's pointers and scalars into the slots of a prepared
+// argument blob: a parameter's data pointer, or a local's address in the
+// workspace `ws`.
+void fill_args(unsigned char* blob, const std::vector<tca::plan::ArgSlot>& slots, const std::vector<int>& param_of,
+               const std::vector<size_t>& local_off, const tca_tensor* tensors, void* ws, const double* scalars) {
+  for (const auto& sl : slots) {
+    if (sl.kind == tca::plan::ArgKind::Ptr) {
+      const int pi = param_of[sl.index];
+      void* ptr = pi >= 0 ? tensors[pi].data : static_cast<char*>(ws) + local_off[sl.index];
+      std::memcpy(blob + sl.offset, &ptr, sizeof ptr);
+    } else {
+      tca::plan::SetScalar(blob, sl, scalars[sl.index]);
+    }
+  }
+}
+
+// The launch decisions for one shape (the slow path, run when the shapes
+// differ from the cached ones): Bind (the shape contract and its errors),
+// the workspace layout, then per kernel its guards, grid, block, geometry
+// and argument layout.
+int prepare_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
+                   uint32_t n_free_dims, std::shared_ptr<tca_program_s::Prepared>* out) {
   const auto& pl = p->plan;
   std::vector<uint32_t> dims;
   std::string err;
   int code = tca::plan::Bind(pl, tensors, n_tensors, free_dims, n_free_dims, &dims, &err);
   if (code != TCA_OK) return fail(code, "%s", err.c_str());
-  if (n_scalars != pl.scalars.size())
-    return fail(TCA_ERR_INVALID, "program %s takes %zu scalar(s), got %u", pl.name.c_str(), pl.scalars.size(), n_scalars);
-  if (n_scalars > 0 && scalars == nullptr) return fail(TCA_ERR_INVALID, "program_launch: null scalars");
+  auto pr = std::make_shared<tca_program_s::Prepared>();
+  pr->n_tensors = n_tensors;
+  pr->n_free = n_free_dims;
+  for (uint32_t i = 0; i < n_tensors; ++i) {
+    const tca_tensor& t = tensors[i];
+    pr->key.push_back(t.rank);
+    pr->key.push_back(static_cast<uint32_t>(t.dtype));
+    uint64_t elems = 1;
+    for (uint32_t a = 0; a < t.rank; ++a) {
+      pr->key.push_back(t.dims[a]);
+      elems *= t.dims[a];
+    }
+    pr->nonempty.push_back(elems > 0 ? 1 : 0);
+  }
+  for (uint32_t i = 0; i < n_free_dims; ++i) pr->key.push_back(free_dims[i]);
 
   // HBM locals: one workspace, each local at a 256-byte aligned offset; only
   // the locals some kernel selected for these dims takes (a variant's
@@ -445,59 +494,17 @@ int launch_program(tca_program p, const tca_tensor* tensors, uint32_t n_tensors,
     for (const auto& a : k.args)
       if (a.kind == tca::plan::ArgKind::Ptr) used[a.index] = true;
   }
-  std::vector<size_t> local_off(pl.tensors.size(), 0);
-  size_t ws_bytes = 0;
+  pr->local_off.assign(pl.tensors.size(), 0);
+  pr->param_of.assign(pl.tensors.size(), -1);
+  int next_param = 0;
   for (size_t t = 0; t < pl.tensors.size(); ++t) {
-    if (pl.tensors[t].role != tca::plan::Role::Local || !used[t]) continue;
-    local_off[t] = ws_bytes;
-    ws_bytes += (tca::plan::TensorBytes(pl, t, dims) + 255u) & ~static_cast<size_t>(255u);
-  }
-  void* ws = nullptr;
-  // Held until the last kernel is enqueued: a launch of this program on the
-  // same stream from another thread that grows the workspace synchronizes
-  // the stream and frees the old buffer, which must not happen between
-  // reading the pointer here and queueing the kernels that use it.
-  std::unique_lock<std::mutex> lk(p->mu, std::defer_lock);
-  if (noalloc) {
-    int dev = 0;
-    TCA_HIP_TRY(hipGetDevice(&dev));
-    if (ws_bytes > tca::rt::kScratchBytes)
-      return fail(TCA_ERR_INVALID,
-                  "program_launch_noalloc: program %s needs %zu bytes of scratch at these dims, more than the %zu "
-                  "bytes the allocation-free launch has (use tca_program_launch)",
-                  pl.name.c_str(), ws_bytes, tca::rt::kScratchBytes);
-    ws = tca::rt::ScratchPtr(dev);
-    if (ws == nullptr)
-      return fail(TCA_ERR_INVALID, "program_launch_noalloc: tca_rt_init(%d) has not set up this device", dev);
-  } else if (ws_bytes > 0) {
-    lk.lock();
-    tca_program_s::Workspace& w = p->workspaces[stream];
-    if (w.bytes < ws_bytes) {
-      if (w.ptr != nullptr) {
-        // Kernels queued on this stream may still use the smaller workspace.
-        TCA_HIP_TRY(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
-        TCA_HIP_TRY(hipFree(w.ptr));
-        w.ptr = nullptr;
-        w.bytes = 0;
-      }
-      TCA_HIP_TRY(hipMalloc(&w.ptr, ws_bytes));
-      w.bytes = ws_bytes;
+    if (pl.tensors[t].role != tca::plan::Role::Local) {
+      pr->param_of[t] = next_param++;
+      continue;
     }
-    ws = w.ptr;
-  }
-
-  // Device pointer of each tensor slot (params from the caller, locals from
-  // the workspace).
-  std::vector<void*> ptrs(pl.tensors.size(), nullptr);
-  {
-    uint32_t ti = 0;
-    for (size_t t = 0; t < pl.tensors.size(); ++t) {
-      if (pl.tensors[t].role == tca::plan::Role::Local) {
-        ptrs[t] = static_cast<char*>(ws) + local_off[t];
-      } else {
-        ptrs[t] = tensors[ti++].data;
-      }
-    }
+    if (!used[t]) continue;
+    pr->local_off[t] = pr->ws_bytes;
+    pr->ws_bytes += (tca::plan::TensorBytes(pl, t, dims) + 255u) & ~static_cast<size_t>(255u);
   }
 
   DeviceLimits l;
@@ -516,13 +523,115 @@ int launch_program(tca_program p, const tca_tensor* tensors, uint32_t n_tensors,
     (void)tca::plan::PackRows(k, dims, &block);  // packed row kernels size the block at launch
     rc = check_geometry(static_cast<uint32_t>(grid), block, k.lds, l.max_threads, l.max_lds);
     if (rc != TCA_OK) return rc;
-    std::vector<unsigned char> blob;
-    if (!tca::plan::PackArgs(k, pl, ptrs, dims, scalars, &blob, &err)) return fail(TCA_ERR_INVALID, "%s", err.c_str());
-    size_t size = blob.size();
-    void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, blob.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
+    tca_program_s::Prepared::Launch L;
+    L.fn = p->funcs.empty() ? nullptr : p->funcs[ki];
+    L.grid = static_cast<uint32_t>(grid);
+    L.block = block;
+    L.lds = k.lds;
+    if (!tca::plan::LayoutArgs(k, pl, dims, &L.blob, &L.slots, &err)) return fail(TCA_ERR_INVALID, "%s", err.c_str());
+    pr->launches.push_back(std::move(L));
+  }
+  *out = std::move(pr);
+  return TCA_OK;
+}
+
+// Whether a launch with these arguments repeats the prepared shape with
+// usable pointers; anything else takes the slow path, which reports the
+// error a mismatch deserves.
+bool repeats(const tca_program_s::Prepared& pr, const tca_tensor* tensors, uint32_t n_tensors,
+             const uint32_t* free_dims, uint32_t n_free_dims) {
+  if (n_tensors != pr.n_tensors || n_free_dims != pr.n_free) return false;
+  if ((n_tensors > 0 && tensors == nullptr) || (n_free_dims > 0 && free_dims == nullptr)) return false;
+  const uint32_t* k = pr.key.data();
+  for (uint32_t i = 0; i < n_tensors; ++i) {
+    const tca_tensor& t = tensors[i];
+    if (t.rank != *k++ || static_cast<uint32_t>(t.dtype) != *k++) return false;
+    for (uint32_t a = 0; a < t.rank; ++a)
+      if (t.dims[a] != *k++) return false;
+    if (pr.nonempty[i] && (t.data == nullptr || (reinterpret_cast<uintptr_t>(t.data) % 16u) != 0u)) return false;
+  }
+  for (uint32_t i = 0; i < n_free_dims; ++i)
+    if (free_dims[i] != *k++) return false;
+  return true;
+}
+
+// The body of both launch entry points. `noalloc` takes the workspace from
+// the device's scratch array instead of the program's per-stream workspace.
+int launch_program(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
+                   uint32_t n_free_dims, const double* scalars, uint32_t n_scalars, tca_stream_t stream,
+                   bool noalloc) {
+  if (p == nullptr) return fail(TCA_ERR_INVALID, "program_launch: null program");
+  if (p->mod == nullptr) return fail(TCA_ERR_INVALID, "program_launch: program was parsed, not loaded");
+  const auto& pl = p->plan;
+  std::shared_ptr<const tca_program_s::Prepared> pr;
+  {
+    std::lock_guard<std::mutex> lk(p->mu);
+    pr = p->prepared;
+  }
+  if (!pr || !repeats(*pr, tensors, n_tensors, free_dims, n_free_dims)) {
+    std::shared_ptr<tca_program_s::Prepared> fresh;
+    int rc = prepare_launch(p, tensors, n_tensors, free_dims, n_free_dims, &fresh);
+    if (rc != TCA_OK) return rc;
+    pr = fresh;
+    std::lock_guard<std::mutex> lk(p->mu);
+    p->prepared = fresh;
+  }
+  if (n_scalars != pl.scalars.size())
+    return fail(TCA_ERR_INVALID, "program %s takes %zu scalar(s), got %u", pl.name.c_str(), pl.scalars.size(), n_scalars);
+  if (n_scalars > 0 && scalars == nullptr) return fail(TCA_ERR_INVALID, "program_launch: null scalars");
+
+  void* ws = nullptr;
+  // Held until the last kernel is enqueued: a launch of this program on the
+  // same stream from another thread that grows the workspace synchronizes
+  // the stream and frees the old buffer, which must not happen between
+  // reading the pointer here and queueing the kernels that use it.
+  std::unique_lock<std::mutex> lk(p->mu, std::defer_lock);
+  if (pr->ws_bytes > 0 && noalloc) {
+    int dev = 0;
+    TCA_HIP_TRY(hipGetDevice(&dev));
+    if (pr->ws_bytes > tca::rt::kScratchBytes)
+      return fail(TCA_ERR_INVALID,
+                  "program_launch_noalloc: program %s needs %zu bytes of scratch at these dims, more than the %zu "
+                  "bytes the allocation-free launch has (use tca_program_launch)",
+                  pl.name.c_str(), pr->ws_bytes, tca::rt::kScratchBytes);
+    ws = tca::rt::ScratchPtr(dev);
+    if (ws == nullptr)
+      return fail(TCA_ERR_INVALID, "program_launch_noalloc: tca_rt_init(%d) has not set up this device", dev);
+  } else if (pr->ws_bytes > 0) {
+    lk.lock();
+    tca_program_s::Workspace& w = p->workspaces[stream];
+    if (w.bytes < pr->ws_bytes) {
+      if (w.ptr != nullptr) {
+        // Kernels queued on this stream may still use the smaller workspace.
+        TCA_HIP_TRY(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+        TCA_HIP_TRY(hipFree(w.ptr));
+        w.ptr = nullptr;
+        w.bytes = 0;
+      }
+      TCA_HIP_TRY(hipMalloc(&w.ptr, pr->ws_bytes));
+      w.bytes = pr->ws_bytes;
+    }
+    ws = w.ptr;
+  }
+
+  for (const auto& L : pr->launches) {
+    // The kernel arguments: the prepared blob with the pointers and scalars
+    // of this call written into their slots (on the stack for every
+    // kernarg block this emitter writes).
+    unsigned char small[512];
+    std::vector<unsigned char> big;
+    unsigned char* blob = small;
+    if (L.blob.size() > sizeof small) {
+      big.resize(L.blob.size());
+      blob = big.data();
+    }
+    std::memcpy(blob, L.blob.data(), L.blob.size());
+    fill_args(blob, L.slots, pr->param_of, pr->local_off, tensors, ws, scalars);
+    size_t size = L.blob.size();
+    void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, blob, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
                       HIP_LAUNCH_PARAM_END};
-    hipError_t e = hipModuleLaunchKernel(p->funcs[ki], static_cast<uint32_t>(grid), 1, 1, block, 1, 1, k.lds,
-                                         static_cast<hipStream_t>(stream), nullptr, config);
+    hipError_t e = hipModuleLaunchKernel(L.fn, L.grid, 1, 1, L.block, 1, 1, L.lds, static_cast<hipStream_t>(stream),
+                                         nullptr, config);
     if (e != hipSuccess) return hip_fail(e, "hipModuleLaunchKernel");
   }
   return TCA_OK;
@@ -541,6 +650,55 @@ int tca_program_launch_noalloc(tca_program p, const tca_tensor* tensors, uint32_
                                const uint32_t* free_dims, uint32_t n_free_dims, const double* scalars,
                                uint32_t n_scalars, tca_stream_t stream) {
   return launch_program(p, tensors, n_tensors, free_dims, n_free_dims, scalars, n_scalars, stream, true);
+}
+
+int tca_program_kernel_args(tca_program p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
+                            uint32_t n_free_dims, const double* scalars, uint32_t n_scalars, uint32_t kernel,
+                            void* buf, size_t cap, size_t* size) {
+  if (p == nullptr) return fail(TCA_ERR_INVALID, "program_kernel_args: null program");
+  const auto& pl = p->plan;
+  if (kernel >= pl.kernels.size())
+    return fail(TCA_ERR_INVALID, "program_kernel_args: program has %zu kernel(s), asked for %u", pl.kernels.size(), kernel);
+  std::vector<uint32_t> dims;
+  std::string err;
+  int code = tca::plan::Bind(pl, tensors, n_tensors, free_dims, n_free_dims, &dims, &err);
+  if (code != TCA_OK) return fail(code, "%s", err.c_str());
+  if (n_scalars != pl.scalars.size())
+    return fail(TCA_ERR_INVALID, "program %s takes %zu scalar(s), got %u", pl.name.c_str(), pl.scalars.size(), n_scalars);
+  if (n_scalars > 0 && scalars == nullptr) return fail(TCA_ERR_INVALID, "program_kernel_args: null scalars");
+  const auto& k = pl.kernels[kernel];
+  uint64_t grid = 0;
+  if (!tca::plan::Selected(k, dims) || !tca::plan::GridSize(k, pl, dims, &grid, &err) || grid == 0)
+    return fail(TCA_ERR_INVALID, "program_kernel_args: kernel %s does not run at these dims", k.symbol.c_str());
+  // The workspace layout of a launch at these dims (the locals of the
+  // selected kernels at 256-byte aligned offsets).
+  std::vector<bool> used(pl.tensors.size(), false);
+  for (const auto& kk : pl.kernels) {
+    if (!tca::plan::Selected(kk, dims)) continue;
+    for (const auto& a : kk.args)
+      if (a.kind == tca::plan::ArgKind::Ptr) used[a.index] = true;
+  }
+  std::vector<size_t> local_off(pl.tensors.size(), 0);
+  std::vector<int> param_of(pl.tensors.size(), -1);
+  size_t ws_bytes = 0;
+  int next_param = 0;
+  for (size_t t = 0; t < pl.tensors.size(); ++t) {
+    if (pl.tensors[t].role != tca::plan::Role::Local) {
+      param_of[t] = next_param++;
+    } else if (used[t]) {
+      local_off[t] = ws_bytes;
+      ws_bytes += (tca::plan::TensorBytes(pl, t, dims) + 255u) & ~static_cast<size_t>(255u);
+    }
+  }
+  std::vector<unsigned char> blob;
+  std::vector<tca::plan::ArgSlot> slots;
+  if (!tca::plan::LayoutArgs(k, pl, dims, &blob, &slots, &err)) return fail(TCA_ERR_INVALID, "%s", err.c_str());
+  fill_args(blob.data(), slots, param_of, local_off, tensors, nullptr, scalars);
+  if (size != nullptr) *size = blob.size();
+  if (buf == nullptr || cap < blob.size())
+    return fail(TCA_ERR_INVALID, "program_kernel_args: %zu bytes needed, room for %zu", blob.size(), cap);
+  std::memcpy(buf, blob.data(), blob.size());
+  return TCA_OK;
 }
 
 }  // extern "C"

@@ -18,12 +18,18 @@
  *       compared with the C oracle (oracle/oracle.c, linked by the test):
  *       max bit-identical, sum within 1e-5 * sqrt(C) * ||row||_2.
  *
+ *       It then times the host side of a launch: tca_program_launch against
+ *       tca_rt_launch of the same kernel with a prepacked argument blob (the
+ *       hipModuleLaunchKernel call alone), both on a one-workgroup problem.
+ *
  * Prints one "ok ..." line and exits 0, or prints the failure and exits 1.
  */
+#define _POSIX_C_SOURCE 199309L
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include "tca_cg.h"
 #include "tca_rt.h"
@@ -212,6 +218,65 @@ static int host_checks(const char* plan, const char* tca_path) {
   return 0;
 }
 
+static double now_us(void) {
+  struct timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return (double)ts.tv_sec * 1e6 + (double)ts.tv_nsec * 1e-3;
+}
+
+/* Median over 15 batches of the host time per call of 200 calls of `launch`
+ * (the device drained between batches, so the queue never fills). */
+#define LAUNCH_BATCH 200
+#define LAUNCH_BATCHES 15
+static int cmp_double(const void* a, const void* b) {
+  double x = *(const double*)a, y = *(const double*)b;
+  return x < y ? -1 : x > y;
+}
+
+static int time_launch_cost(const char* plan, const char* hsaco, void* dx, void* ds, void* dm, double* prog_us,
+                            double* raw_us) {
+  tca_program p = NULL;
+  tca_module m = NULL;
+  tca_tensor ts[3];
+  unsigned char blob[32];
+  uint32_t one = 1, cols = COLS;
+  double tp[LAUNCH_BATCHES], tr[LAUNCH_BATCHES];
+  int b, i;
+  REQUIRE(tca_program_load(hsaco, plan, &p) == TCA_OK, "program load", tca_rt_last_error());
+  REQUIRE(tca_rt_module_load(hsaco, &m) == TCA_OK, "module load", tca_rt_last_error());
+  set_tensor(&ts[0], dx, 2, 1, COLS);
+  set_tensor(&ts[1], ds, 1, 1, 0);
+  set_tensor(&ts[2], dm, 1, 1, 0);
+  /* The kernel's arguments (its plan: ptr x, ptr sum, ptr max, dim R, dim e8192). */
+  memcpy(blob, &dx, 8);
+  memcpy(blob + 8, &ds, 8);
+  memcpy(blob + 16, &dm, 8);
+  memcpy(blob + 24, &one, 4);
+  memcpy(blob + 28, &cols, 4);
+  for (b = 0; b < LAUNCH_BATCHES; ++b) {
+    double t0;
+    REQUIRE(tca_rt_device_sync() == TCA_OK, "sync", tca_rt_last_error());
+    t0 = now_us();
+    for (i = 0; i < LAUNCH_BATCH; ++i)
+      REQUIRE(tca_program_launch(p, ts, 3, NULL, 0, NULL, 0, NULL) == TCA_OK, "launch", tca_rt_last_error());
+    tp[b] = (now_us() - t0) / LAUNCH_BATCH;
+    REQUIRE(tca_rt_device_sync() == TCA_OK, "sync", tca_rt_last_error());
+    t0 = now_us();
+    for (i = 0; i < LAUNCH_BATCH; ++i)
+      REQUIRE(tca_rt_launch(m, "tca_row_sum_max_8192_k0", 1, 512, 0, blob, sizeof blob, NULL) == TCA_OK, "raw launch",
+              tca_rt_last_error());
+    tr[b] = (now_us() - t0) / LAUNCH_BATCH;
+  }
+  REQUIRE(tca_rt_device_sync() == TCA_OK, "sync", tca_rt_last_error());
+  qsort(tp, LAUNCH_BATCHES, sizeof(double), cmp_double);
+  qsort(tr, LAUNCH_BATCHES, sizeof(double), cmp_double);
+  *prog_us = tp[LAUNCH_BATCHES / 2];
+  *raw_us = tr[LAUNCH_BATCHES / 2];
+  REQUIRE(tca_rt_module_unload(m) == TCA_OK, "module unload", tca_rt_last_error());
+  REQUIRE(tca_program_unload(p) == TCA_OK, "unload", tca_rt_last_error());
+  return 0;
+}
+
 static int gpu_run(const char* plan, const char* hsaco, uint32_t rows) {
   tca_program p = NULL;
   tca_event e0 = NULL, e1 = NULL;
@@ -224,7 +289,7 @@ static int gpu_run(const char* plan, const char* hsaco, uint32_t rows) {
   void *dx = NULL, *ds = NULL, *dm = NULL;
   tca_tensor ts[3];
   float ms = 0.0f;
-  double worst = 0.0;
+  double worst = 0.0, prog_us = 0.0, raw_us = 0.0;
   uint32_t r, c;
 
   REQUIRE(x && got_s && got_m && want_s && want_m, "host alloc", "");
@@ -268,11 +333,13 @@ static int gpu_run(const char* plan, const char* hsaco, uint32_t rows) {
   }
   tca_rt_event_destroy(e0);
   tca_rt_event_destroy(e1);
+  REQUIRE(tca_program_unload(p) == TCA_OK, "unload", tca_rt_last_error());
+  if (time_launch_cost(plan, hsaco, dx, ds, dm, &prog_us, &raw_us) != 0) return 1;
   tca_rt_free(dx);
   tca_rt_free(ds);
   tca_rt_free(dm);
-  REQUIRE(tca_program_unload(p) == TCA_OK, "unload", tca_rt_last_error());
-  printf("ok gpu rows=%u max_abs_sum_err=%.3g launch_ms=%.4f\n", rows, worst, (double)ms);
+  printf("ok gpu rows=%u max_abs_sum_err=%.3g launch_ms=%.4f host_us_per_launch=%.2f host_us_per_raw_launch=%.2f\n",
+         rows, worst, (double)ms, prog_us, raw_us);
   free(x);
   free(got_s);
   free(got_m);
