@@ -440,6 +440,45 @@ def _suite(dev, steps):
     return out
 
 
+def _gemm_sweep(dev, steps):
+    """Contractions at small and medium output planes (the small-tile K-split
+    kernel up to M*N = 2^20, the tile kernels above): M, N in {64, 256, 1024,
+    2048}, K in {64, 4096}, f32 and bf16 inputs, B as [K][N] and [N][K];
+    device time per launch from the held window (kernels back to back)."""
+    import torch
+    from tcacomp_amd import compiler, programs
+    stream = torch.cuda.current_stream().cuda_stream
+    out = []
+    for pname in ("gemm_f32", "gemm_f32_nt", "gemm_bf16", "gemm_bf16_nt"):
+        prog = compiler.compile_program(programs.CONFIG_PROGRAMS[pname](), jit=os.environ.get("TCA_JIT", "0") != "0")
+        nt, bf = pname.endswith("_nt"), "bf16" in pname
+        for M in (64, 256, 1024, 2048):
+            for N in (64, 256, 1024, 2048):
+                for K in (64, 4096):
+                    g = torch.Generator(device=dev).manual_seed(M + N + K)
+                    a = torch.rand((M, K), device=dev, generator=g) * 2 - 1
+                    b = torch.rand((N, K) if nt else (K, N), device=dev, generator=g) * 2 - 1
+                    if bf:
+                        a, b = a.to(torch.bfloat16), b.to(torch.bfloat16)
+                    args = [a, b, torch.empty((M, N), device=dev)]
+                    for _ in range(10):
+                        prog.launch(args, stream=stream)
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    for _ in range(steps):
+                        prog.launch(args, stream=stream)
+                    enq = time.perf_counter() - t0
+                    torch.cuda.synchronize()
+                    us = _window_us(prog, args, [], stream, steps, hold_cycles=3 * enq * 2.4e9)
+                    e = {"program": pname, "M": M, "N": N, "K": K, "kernels": prog.selected_symbols(args),
+                         "us": us, "TFLOPs": 2.0 * M * N * K / (us * 1e-6) / 1e12}
+                    out.append(e)
+                    print("[bench] sweep %s %dx%dx%d %.2f us %.2f TFLOP/s %s" % (
+                        pname, M, N, K, us, e["TFLOPs"], [s.split("_k0")[-1] for s in e["kernels"]]),
+                        file=sys.stderr, flush=True)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -450,6 +489,8 @@ def main():
                     help="untimed launches per config before the warmup steps, in wall-clock ms")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--no-suite", action="store_true", help="skip the reference suite's 14 kernels")
+    ap.add_argument("--gemm-sweep", action="store_true",
+                    help="only the contraction sweep (M, N in 64..2048, K in 64, 4096; one JSON line of its own)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the row configurations would "
@@ -460,6 +501,9 @@ def main():
     from tcacomp_amd import _lib
     dev = torch.device("cuda:0")
     _lib.check(_lib.lib().tca_rt_init(0))
+    if args.gemm_sweep:
+        print(json.dumps({"gemm_sweep": _gemm_sweep(dev, args.steps)}))
+        return
     keys = [k for k in args.configs.split(",") if k]
     # The N-core CPU figure uses the host's cores (the box's CPU share: its
     # OMP_NUM_THREADS), overridable with TCA_CPU_THREADS.

@@ -28,7 +28,12 @@ class Parser {
         pending.clear();
       } else {
         Error(Cur().pos, std::string("expected declaration, found ") + TokName(Cur().kind));
+        const size_t before = pos_;
         Sync();
+        // Sync stops at a '}' it does not consume; stepping over it here is
+        // what keeps a stray '}' from being reported forever (the loop
+        // would otherwise never advance).
+        if (pos_ == before) Advance();
       }
     }
     for (const auto& a : pending) Error(a.pos, "annotation @" + a.name + " does not precede a kernel");
@@ -198,7 +203,12 @@ class Parser {
     Expect(Tok::LBrace);
     while (!At(Tok::RBrace) && !At(Tok::Eof)) {
       Stmt s;
+      const size_t before = pos_;
       if (ParseStmt(&s)) k->body.push_back(std::move(s));
+      // A statement that fails on a token its recovery stops at ('kernel',
+      // '@') consumes nothing; the body then ends there, so the module loop
+      // takes that declaration up again.
+      if (pos_ == before) break;
     }
     Expect(Tok::RBrace);
     return true;

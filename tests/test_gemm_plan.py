@@ -161,3 +161,22 @@ def test_product_guard_names_known_dims(bad):
     h = ctypes.c_void_p()
     assert _lib.lib().tca_program_parse(plan.encode(), ctypes.byref(h)) != 0
     assert "unknown dim" in _lib.last_error()
+
+
+# Findings of the plan fuzzer (tests/c/fuzz.cpp under AddressSanitizer and
+# UBSan, tests/sanitize.py), kept as regression cases: each input must be
+# refused with the stated error.
+FUZZ_FINDINGS = [
+    # no program record: the plan parsed with an empty name, and its printed
+    # form ("program " alone) did not parse again
+    ("tca-plan 1\ndim R 0\ntensor x f32 in 1 R\nkernel k 64 0 1 R/64\narg ptr x\nend\n", "no program record"),
+    ("tca-plan 1\nprogram a\nprogram b\ndim R 0\ntensor x f32 in 1 R\nkernel k 64 0 1 R/64\narg ptr x\nend\n",
+     "duplicate program record"),
+]
+
+
+@pytest.mark.parametrize("text,msg", FUZZ_FINDINGS)
+def test_plan_fuzz_findings(text, msg):
+    h = ctypes.c_void_p()
+    assert _lib.lib().tca_program_parse(text.encode(), ctypes.byref(h)) != 0
+    assert msg in _lib.last_error(), _lib.last_error()

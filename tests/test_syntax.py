@@ -170,6 +170,26 @@ def test_parser_reports_and_recovers():
     assert "does not precede a kernel" in errors_of('kernel k() -> f32 { return x; }\n@name(cxx="K")', check=False)[0]
 
 
+# Findings of the .tca fuzzer (tests/c/fuzz.cpp under AddressSanitizer and
+# UBSan, tests/sanitize.py), kept as regression cases. The recovery skips to a
+# ';', '}', 'kernel' or '@' without consuming the last three, so a stray '}'
+# at module level, or a statement failing on 'kernel' or '@', recovered to the
+# same token forever (the reference's recovery has the same loop,
+# internal/syntax/parser/parser.go:105-140); each now reports once and parsing
+# goes on past it.
+@pytest.mark.parametrize("src,want", [
+    ("}", ["1:1: error: expected declaration, found }"]),
+    ("} } kernel", ["1:1: error: expected declaration, found }", "1:3: error: expected declaration, found }"]),
+    ("kernel k() -> f32 { @ }", ["1:21: error: expected statement, found @"]),
+    ("kernel k() -> f32 { kernel k2() -> f32 { return x; } }", ["1:21: error: expected statement, found kernel"]),
+])
+def test_parser_recovery_always_advances(src, want):
+    errs = errors_of(src, check=False)
+    for w in want:
+        assert any(w in e for e in errs), errs
+    assert len(errs) < 10, errs
+
+
 def test_unchecked_dump_keeps_omitted_cells_empty_and_check_fills_them():
     # root `as` omitted (inferred from the bindings), piped `as` omitted (the
     # live axes), lambda return omitted (the body's type)
