@@ -183,9 +183,11 @@ const char* tca_program_plan_text(tca_program p);
  * same contract checks and kernels as tca_program_launch; HBM locals and the
  * partials of split and column reductions live in one 32 MiB scratch array
  * per device, part of this library's device code, whose address
- * tca_rt_init(device) takes (call it first on every device used). A launch
- * whose workspace at these dims exceeds 32 MiB fails with TCA_ERR_INVALID
- * before anything is queued. Every call on one GPU shares that array and it
+ * tca_rt_init(device) takes (call it first on every device used; a launch
+ * with no workspace at these dims uses no scratch and runs without it, one
+ * that needs scratch on a device tca_rt_init has not set up fails with
+ * TCA_ERR_INVALID). A launch whose workspace at these dims exceeds 32 MiB
+ * fails with TCA_ERR_INVALID before anything is queued. Every call on one GPU shares that array and it
  * keeps the last call's contents: calls whose kernels overlap on one GPU
  * (other streams, other threads) race; calls on one stream are ordered. */
 int tca_program_launch_noalloc(tca_program p, const tca_tensor* tensors, uint32_t n_tensors,

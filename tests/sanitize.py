@@ -64,7 +64,10 @@ def build(jobs=8):
     import concurrent.futures
     os.makedirs(ASAN_DIR, exist_ok=True)
     srcs = [os.path.join(tb.CSRC, s) for s in tb.SOURCES]
-    headers = glob.glob(os.path.join(tb.CSRC, "**", "*.h"), recursive=True) + glob.glob(os.path.join(REPO, "include", "*.h"))
+    # The host library's own headers (the device headers under csrc/include
+    # go into emitted kernels, never into the library).
+    headers = [h for h in glob.glob(os.path.join(tb.CSRC, "**", "*.h"), recursive=True)
+               if os.sep + "include" + os.sep not in h] + glob.glob(os.path.join(REPO, "include", "*.h"))
     tests_src = [os.path.join(CDIR, "fuzz.cpp"), os.path.join(CDIR, "abi_consumer.c")]
     key = _digest(srcs + headers + tests_src + [os.path.join(tb.CSRC, s) for s in tb.HIP_SOURCES], " ".join(SAN))
     stamp = os.path.join(ASAN_DIR, "stamp")

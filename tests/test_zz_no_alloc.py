@@ -78,3 +78,47 @@ def test_noalloc_refuses_oversized_workspace(gpu):
     assert "32" in str(e.value) or "scratch" in str(e.value)
     torch.cuda.synchronize()
     assert torch.equal(out[:8, 0], y)
+
+
+_NO_INIT = r"""
+import sys
+sys.path[:0] = [{repo!r}, {tests!r}]
+import numpy as np
+import torch
+from helpers import compiled
+from tcacomp_amd import _lib, inputs
+# tca_rt_init is never called in this process: torch sets the device up.
+x = torch.from_numpy(inputs.normal((64, 8192), 1.0, 3)).to("cuda:0")
+p = compiled("row_sum_max_8192")  # no workspace
+outs = [torch.empty(64, device="cuda:0") for _ in range(2)]
+p.launch([x] + outs, noalloc=True)
+torch.cuda.synchronize()
+s, m = (o.cpu().numpy() for o in outs)
+xs = x.cpu().numpy()
+assert np.array_equal(m, xs.max(1)), "max"
+assert np.allclose(s, xs.astype(np.float64).sum(1), rtol=0, atol=1e-3), "sum"
+q = compiled("row_sum_max_dyn")  # split rows at 3 x 1 M: a partial scratch
+y = torch.zeros((3, 1 << 20), device="cuda:0")
+try:
+    q.launch([y, torch.empty(3, device="cuda:0"), torch.empty(3, device="cuda:0")], noalloc=True)
+except _lib.TcaError as e:
+    assert "has not set up this device" in str(e), str(e)
+    print("ok no-init")
+else:
+    raise SystemExit("a launch that needs scratch ran without tca_rt_init")
+"""
+
+
+def test_noalloc_without_init_needs_no_scratch(gpu):
+    """A program with no workspace launches allocation-free in a process that
+    never called tca_rt_init (nothing of the scratch array is needed); one
+    that needs scratch there fails with the init error, before any kernel
+    is queued. A fresh process: this one has called tca_rt_init."""
+    import os
+    import subprocess
+    here = os.path.dirname(os.path.abspath(__file__))
+    code = _NO_INIT.format(repo=os.path.dirname(here), tests=here)
+    print("noalloc without init (subprocess)", flush=True)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=110,
+                       env=dict(os.environ, TCA_JIT="0"))
+    assert r.returncode == 0 and "ok no-init" in r.stdout, r.stdout + r.stderr[-3000:]
