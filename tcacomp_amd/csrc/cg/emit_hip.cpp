@@ -550,6 +550,80 @@ OpKind Classify(const ir::Operand& o, const RowGeom& geo) {
 // shallower than the nest): a per-row scalar computation.
 bool IsRowScalarChain(const ir::Chain& c, const RowGeom& geo) { return c.root.as.size() + 1 == geo.as.size(); }
 
+// Structural equality of two root-map bodies (expression a in chain ca, b in
+// chain cb): the same operators, types, constants and builtins, and a
+// parameter of one equal to a parameter of the other when both read the same
+// operand (tensor and subscripts).
+bool SameRowExpr(const ir::Graph& g, int a, const ir::Chain& ca, int b, const ir::Chain& cb) {
+  const ir::Expr& x = g.exprs[a];
+  const ir::Expr& y = g.exprs[b];
+  if (x.op == ir::Op::Param || y.op == ir::Op::Param) {
+    if (x.op != y.op) return false;
+    auto operandOf = [](const ir::Chain& c, int pid) -> const ir::Operand* {
+      for (size_t k = 0; k < c.root.fn.params.size(); ++k)
+        if (c.root.fn.params[k] == pid) return &c.root.ops[k];
+      return nullptr;
+    };
+    const ir::Operand* oa = operandOf(ca, a);
+    const ir::Operand* ob = operandOf(cb, b);
+    return oa != nullptr && ob != nullptr && oa->tensor == ob->tensor && oa->axes == ob->axes;
+  }
+  if (a == b) return true;  // one hash-consed node with no parameter below it
+  if (x.op != y.op || x.type != y.type || x.code != y.code || x.index != y.index || x.text != y.text ||
+      x.args.size() != y.args.size())
+    return false;
+  if (x.op == ir::Op::Const && !(x.value == y.value && std::signbit(x.value) == std::signbit(y.value))) return false;
+  for (size_t i = 0; i < x.args.size(); ++i)
+    if (!SameRowExpr(g, x.args[i], ca, y.args[i], cb)) return false;
+  return true;
+}
+
+// A softmax's two reductions, fusable into one read of the row with the
+// online normaliser (tca::hip::online_expsum_add): chain A folds t over the
+// row with fmaxf from -inf (f32, no piped map) into a row scalar, and chain
+// B folds expf(t - a) with + (f32), where a is A's result read at the row
+// and t is A's root body. Then
+//   sum over the row of expf(t - a) = sum over chunks of s_c * expf(m_c - a),
+// m_c a chunk's maximum and s_c its sum of expf(t - m_c). B's init and piped
+// map are applied at its merge as usual.
+bool OnlineMaxExpSum(const ir::Graph& g, const ir::Chain& A, const ir::Chain& B, const RowGeom& geo) {
+  if (A.reduces.size() != 1 || B.reduces.size() != 1 || A.has_piped) return false;
+  if (g.exprs[A.root.fn.body].type != ir::Elem::F32 || g.exprs[B.root.fn.body].type != ir::Elem::F32) return false;
+  if (g.tensors[A.store_tensor].elem != ir::Elem::F32) return false;
+  const ir::ReduceStage& ra = A.reduces[0];
+  // -inf: a literal, or a negated +inf literal (how the .tca source spells it)
+  auto negInf = [&](int id) {
+    const ir::Expr& e = g.exprs[id];
+    if (e.op == ir::Op::Const) return std::isinf(e.value) && e.value < 0;
+    if (e.op != ir::Op::Un || static_cast<ir::UnOp>(e.code) != ir::UnOp::Neg) return false;
+    const ir::Expr& v = g.exprs[e.args[0]];
+    return v.op == ir::Op::Const && std::isinf(v.value) && v.value > 0;
+  };
+  if (g.exprs[ra.init].type != ir::Elem::F32 || !negInf(ra.init)) return false;
+  auto accNow = [&](const ir::ReduceStage& r, const ir::Expr& e) {
+    const int acc = r.fn.params[0], now = r.fn.params[1];
+    return e.args.size() == 2 && ((e.args[0] == acc && e.args[1] == now) || (e.args[0] == now && e.args[1] == acc));
+  };
+  const ir::Expr& ca = g.exprs[ra.fn.body];
+  if (ca.op != ir::Op::Call || ca.text != "fmaxf" || !accNow(ra, ca)) return false;
+  const ir::ReduceStage& rb = B.reduces[0];
+  const ir::Expr& cb = g.exprs[rb.fn.body];
+  if (cb.op != ir::Op::Bin || static_cast<ir::BinOp>(cb.code) != ir::BinOp::Add || !accNow(rb, cb)) return false;
+  const ir::Expr& bb = g.exprs[B.root.fn.body];
+  if (bb.op != ir::Op::Call || bb.text != "expf" || bb.args.size() != 1) return false;
+  const ir::Expr& sub = g.exprs[bb.args[0]];
+  if (sub.op != ir::Op::Bin || static_cast<ir::BinOp>(sub.code) != ir::BinOp::Sub) return false;
+  const ir::Expr& pa = g.exprs[sub.args[1]];
+  if (pa.op != ir::Op::Param) return false;
+  for (size_t k = 0; k < B.root.fn.params.size(); ++k) {
+    if (B.root.fn.params[k] != sub.args[1]) continue;
+    const ir::Operand& op = B.root.ops[k];
+    if (op.tensor != A.store_tensor || op.axes != A.store_axes || Classify(op, geo) != OpKind::RowScalar) return false;
+    return SameRowExpr(g, A.root.fn.body, A, sub.args[0], B);
+  }
+  return false;
+}
+
 // The structural conditions shared by the register-resident row family and
 // the streaming row family: every chain iterates (outer..., col) in one
 // order, or only (outer...) — the prefix fusion of a shallower nest
@@ -2535,9 +2609,39 @@ class Emitter {
       if (IsRowScalarChain(g_.chains[ps[0]], geo)) splitMulti = false;
     for (int t : tiles)
       if (produced.count(t)) splitMulti = false;
+    // Softmax's max and exp-sum passes, fused into one pass over the row's
+    // chunks with the online normaliser: onlinePair[p] for the first pass of
+    // such a pair (pass p + 1 then has no kernels of its own); the chunk
+    // maxima the sums were taken against go to a partial of their own.
+    std::vector<bool> onlinePair(passes.size(), false);
+    std::set<int> onlineSum;  // chain B of each fused pair
+    if (splitMulti)
+      for (size_t p = 0; p + 1 < passes.size(); ++p)
+        if (passes[p].size() == 1 && passes[p + 1].size() == 1 &&
+            OnlineMaxExpSum(g_, g_.chains[passes[p][0]], g_.chains[passes[p + 1][0]], geo) &&
+            (p == 0 || !onlinePair[p - 1])) {
+          onlinePair[p] = true;
+          onlineSum.insert(passes[p + 1][0]);
+        }
+    // A fused pair followed by the nest's last pass, a row map (softmax's
+    // normalisation): each row-map workgroup computes the pair's two values
+    // for its row from the partials (at most 512 pairs, read from the L2)
+    // instead of a merge kernel storing them first; one workgroup per row
+    // still stores them. The merge launch and its dependency were 4.6 us of
+    // the 131 us of softmax over [64, 1 Mi].
+    std::set<size_t> foldedMerge;
+    for (size_t p = 0; p + 3 == passes.size(); ++p)
+      if (onlinePair[p] && g_.chains[passes[p + 2][0]].reduces.empty()) foldedMerge.insert(p);
     std::string smSig, smArgs;
     std::vector<std::string> smPlanArgs;
     std::vector<std::pair<std::string, size_t>> smFns;  // (device function, pass)
+    // Vectors per chunk of a split kernel whose chunks are not kChunkVecs.
+    std::map<std::string, uint32_t> smChunk;
+    // The fused softmax passes take chunks 4x as long (16 vectors per lane):
+    // with 4 a lane, the many short workgroups spent a quarter of their time
+    // in the block's tail (the pair merges, the partials' stores); 8x (32 a
+    // lane, one round of workgroups at [64, 1 Mi]) measured 3% slower.
+    constexpr uint32_t kOnlineChunkVecs = 4 * kChunkVecs;
     if (splitMulti) {
       const std::string splitDim = "__split";
       const std::string splitDecl = splitDim + " " + std::to_string(kMaxParts);
@@ -2556,6 +2660,17 @@ class Emitter {
           smSig += ",\n    " + CType(pe) + "* __restrict__ p" + std::to_string(ci) + " /* " + nm + " */";
           smArgs += ", p" + std::to_string(ci);
           smPlanArgs.push_back("ptr " + nm);
+          if (onlineSum.count(ci)) {
+            const std::string sn = "__shift" + std::to_string(ci);
+            std::string st = sn + " f32 local " + std::to_string(geo.outer.size() + 1);
+            for (int a : geo.outer) st += " " + g_.dims[a].name;
+            st += " " + splitDim;
+            if (std::find(extra_tensors_.begin(), extra_tensors_.end(), st) == extra_tensors_.end())
+              extra_tensors_.push_back(st);
+            smSig += ",\n    float* __restrict__ q" + std::to_string(ci) + " /* " + sn + " */";
+            smArgs += ", q" + std::to_string(ci);
+            smPlanArgs.push_back("ptr " + sn);
+          }
           // A register local gets memory of its own shape for the later passes.
           const int st = g_.chains[ci].store_tensor;
           if (isReg(st) && !an_.hbm_local[st]) {
@@ -2573,8 +2688,15 @@ class Emitter {
       }
       const std::string rowExpr = ProductExpr(geo.outer);
       // Row scalars of pass p's chains, loaded from memory; bound for elemValue.
+      // Those in `computed` are values the kernel computes itself (a folded
+      // merge's aval and bval): bound, not loaded.
+      std::map<int, std::string> computed;
       auto loadRowScalars = [&](size_t p, const std::string& ind) {
         std::set<int> done;
+        for (const auto& kv : computed) {
+          regScalar[kv.first] = kv.second;
+          done.insert(kv.first);
+        }
         for (int ci : passes[p]) {
           const ir::Chain& c = g_.chains[ci];
           std::vector<const ir::Operand*> ops;
@@ -2602,8 +2724,8 @@ class Emitter {
           o << ind << "  return " << r << ";\n" << ind << "};\n";
         }
       };
-      auto chunkHead = [&]() {
-        o << "  constexpr uint32_t CV = " << kChunkVecs << "u, PMAX = " << kMaxParts << "u;\n";
+      auto chunkHead = [&](uint32_t cv) {
+        o << "  constexpr uint32_t CV = " << cv << "u, PMAX = " << kMaxParts << "u;\n";
         o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
         o << "  const uint32_t VECS = C / V;\n";
         o << "  const uint32_t P = min(PMAX, tca::hip::ceil_div(VECS, CV));  // VECS >= 1 (launch guard)\n";
@@ -2615,10 +2737,174 @@ class Emitter {
         o << "  const bool active = true;\n";
         for (int a : geo.outer) o << "  const uint32_t c" << a << " = r;\n";
       };
+      // The values the fused pair (passes p, p + 1) stores for row r, in every
+      // lane of each wave that runs this: aval, A's result (its partial
+      // maxima folded, init applied), and bval, B's (the chunk pairs summed
+      // as s_c * expf(m_c - aval), NaN when aval is -inf, then init and piped
+      // map). Needs r, lane and C in scope; names are prefixed so the code can
+      // sit in the row map that reads the two values.
+      auto pairValues = [&](size_t p, const std::string& ind) {
+        const int ca = passes[p][0], cb = passes[p + 1][0];
+        const ir::Chain& A = g_.chains[ca];
+        const ir::Chain& B = g_.chains[cb];
+        const int ta = A.store_tensor;
+        const std::string sa = std::to_string(ca), sb = std::to_string(cb);
+        o << ind << "const uint32_t PF = min(" << kMaxParts << "u, tca::hip::ceil_div(C / V, " << kOnlineChunkVecs
+          << "u));  // the fused partial's chunks\n";
+        o << ind << "const auto pcomb = [](float acc, float now) -> float {\n";
+        {
+          ExprGen cg(g_, o, ind + "  ", &counter_);
+          cg.Bind(A.reduces[0].fn.params[0], "acc");
+          cg.Bind(A.reduces[0].fn.params[1], "now");
+          const std::string rr = cg.Gen(A.reduces[0].fn.body);
+          o << ind << "  return " << rr << ";\n" << ind << "};\n";
+        }
+        o << ind << "float pm = 0.0f;\n" << ind << "bool ph = false;\n";
+        o << ind << "{\n" << ind << "  float pv[" << kMaxParts / 64 << "];\n#pragma unroll\n" << ind
+          << "  for (uint32_t k = 0; k < " << kMaxParts / 64 << "u; ++k)\n" << ind << "    pv[k] = p" << sa
+          << "[static_cast<uint64_t>(r) * " << kMaxParts << "u + min((threadIdx.x & 63u) + 64u * k, PF - 1u)];\n"
+          << "#pragma unroll\n" << ind << "  for (uint32_t k = 0; k < " << kMaxParts / 64 << "u; ++k) {\n" << ind
+          << "    if ((threadIdx.x & 63u) + 64u * k < PF) {\n" << ind << "      pm = ph ? pcomb(pm, pv[k]) : pv[k];\n"
+          << ind << "      ph = true;\n" << ind << "    }\n" << ind << "  }\n" << ind << "}\n";
+        o << ind << "pm = tca::hip::wave_allreduce_present(pm, ph, pcomb);\n";
+        {
+          const ir::ReduceStage& rs = A.reduces[0];
+          ExprGen fg(g_, o, ind, &counter_);
+          fg.Bind(rs.fn.params[0], fg.Gen(rs.init));
+          fg.Bind(rs.fn.params[1], "pm");
+          const std::string val = fg.Gen(rs.fn.body);  // PF >= 1: init applied once to the row's total
+          o << ind << "const float aval = " << val << ";  // the value A stores and B reads\n";
+        }
+        // Row scalars B's piped map reads besides A's result.
+        std::map<int, std::string> piped;
+        if (B.has_piped)
+          for (const auto& op : B.piped.ops) {
+            if (op.tensor == ta || piped.count(op.tensor)) continue;
+            piped[op.tensor] = "prs" + std::to_string(op.tensor);
+            o << ind << "const " << CType(g_.tensors[op.tensor].elem) << " prs" << op.tensor << " = t" << op.tensor
+              << "[" << Offset(op.tensor, op.axes, coord) << "];\n";
+          }
+        o << ind << "float psum = 0.0f;\n#pragma unroll\n" << ind << "for (uint32_t k = 0; k < " << kMaxParts / 64
+          << "u; ++k) {\n" << ind << "  const uint32_t c = (threadIdx.x & 63u) + 64u * k;\n" << ind
+          << "  if (c < PF)\n" << ind << "    psum += p" << sb << "[static_cast<uint64_t>(r) * " << kMaxParts
+          << "u + c] * expf(q" << sb << "[static_cast<uint64_t>(r) * " << kMaxParts << "u + c] - aval);\n" << ind
+          << "}\n" << ind << "for (int off = 32; off > 0; off >>= 1) psum += __shfl_xor(psum, off, 64);\n";
+        o << ind << "const float ptotal = aval == -__builtin_inff() ? __builtin_nanf(\"\") : psum;\n";
+        {
+          const ir::ReduceStage& rs = B.reduces[0];
+          ExprGen fg(g_, o, ind, &counter_);
+          fg.Bind(rs.fn.params[0], fg.Gen(rs.init));
+          fg.Bind(rs.fn.params[1], "ptotal");
+          std::string val = fg.Gen(rs.fn.body);
+          if (B.has_piped) {
+            ExprGen pg(g_, o, ind, &counter_);
+            pg.Bind(B.piped.fn.params[0], val);
+            for (size_t k = 0; k < B.piped.ops.size(); ++k) {
+              const int t = B.piped.ops[k].tensor;
+              pg.Bind(B.piped.fn.params[k + 1], t == ta ? std::string("aval") : piped[t]);
+            }
+            val = pg.Gen(B.piped.fn.body);
+          }
+          o << ind << "const " << CType(g_.tensors[B.store_tensor].elem) << " bval = " << val << ";\n";
+        }
+      };
+      // Passes p (A: max of t) and p + 1 (B: sum of expf(t - a)) of a
+      // softmax in one read of each chunk: the partial folds A's maximum as
+      // pass p's partial does and, from the same element values, the online
+      // pair (m_c, s_c) (tca::hip::online_expsum_add), merged over the lanes
+      // and waves in a fixed order; the merge (one wave per row) finishes A
+      // (init, store) and then B from the pairs: sum over chunks of
+      // s_c * expf(m_c - a), a the value A stored (NaN when a is -inf: every
+      // element -inf or NaN, where the direct sum is NaN), then B's init and
+      // piped map.
+      auto emitOnlinePair = [&](size_t p) {
+        const int ca = passes[p][0], cb = passes[p + 1][0];
+        const ir::Chain& A = g_.chains[ca];
+        const ir::Chain& B = g_.chains[cb];
+        const int ta = A.store_tensor, tb = B.store_tensor;
+        const std::string tag = std::to_string(p + 1), sa = std::to_string(ca), sb = std::to_string(cb);
+        const std::string fn = pk.symbol + "_spart" + tag;
+        smFns.push_back({fn, p});
+        smChunk[fn] = kOnlineChunkVecs;
+        o << "// statements #" << ca << " #" << cb << ": split rows, passes " << p + 1 << " and " << p + 2
+          << " in one read (max, then the online exp-sum against the chunk maxima), partial folds\n";
+        o << "template <uint32_t V>\n__device__ __forceinline__ void " << fn << "(\n    " << sig << smSig << ") {\n";
+        chunkHead(kOnlineChunkVecs);
+        loadRowScalars(p, "  ");
+        combsOf(p, "  ");
+        o << "  float part" << sa << " = 0.0f, om = -__builtin_inff(), os = 0.0f;\n";
+        auto step = [&](std::ostringstream& b, const std::string& ind, const std::string& sfx, bool first) {
+          b << ind << "float ev" << sfx << "[V];\n";
+          b << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) {\n";
+          std::ostringstream es;
+          const std::string ev = elemValue(es, ind + "  ", A, sfx);
+          b << es.str() << ind << "  const float e = " << ev << ";\n";
+          const std::string folded = "comb" + sa + "(part" + sa + ", e)";
+          b << ind << "  part" << sa << " = " << (first ? "q == 0u ? e : " + folded : folded) << ";\n";
+          b << ind << "  ev" << sfx << "[q] = e;\n" << ind << "}\n";
+          b << ind << "tca::hip::online_expsum_add(om, os, ev" << sfx << ");\n";
+        };
+        constexpr uint32_t kU = 4;  // 8 vectors in flight per lane measured 5% slower
+        std::ostringstream b;
+        b << "  {\n    const uint32_t vc = lo + threadIdx.x;\n";
+        operands(b, p, "    ", false, "vc", "");
+        step(b, "    ", "", true);
+        b << "  }\n  uint32_t v0 = lo + threadIdx.x + " << kPartBlock << "u;\n";
+        b << "  for (; v0 + " << (kU - 1) * kPartBlock << "u < hi; v0 += " << kU * kPartBlock << "u) {\n";
+        for (uint32_t u = 0; u < kU; ++u) b << "    const uint32_t vc_" << u << " = v0 + " << u * kPartBlock << "u;\n";
+        for (uint32_t u = 0; u < kU; ++u) operands(b, p, "    ", false, "vc_" + std::to_string(u), "_" + std::to_string(u));
+        for (uint32_t u = 0; u < kU; ++u) step(b, "    ", "_" + std::to_string(u), false);
+        b << "  }\n  for (; v0 < hi; v0 += " << kPartBlock << "u) {\n    const uint32_t vc = v0;\n";
+        operands(b, p, "    ", false, "vc", "");
+        step(b, "    ", "", false);
+        b << "  }\n";
+        o << b.str();
+        o << "  part" << sa << " = tca::hip::seg_allreduce<64>(part" << sa << ", comb" << sa << ");\n";
+        o << "  for (int off = 32; off > 0; off >>= 1)\n"
+          << "    tca::hip::online_expsum_merge(om, os, __shfl_xor(om, off, 64), __shfl_xor(os, off, 64));\n";
+        o << "  __shared__ float red" << sa << "[" << kPartBlock / 64 << "], redm[" << kPartBlock / 64 << "], reds["
+          << kPartBlock / 64 << "];\n";
+        o << "  if ((threadIdx.x & 63u) == 0u) {\n    red" << sa << "[threadIdx.x >> 6] = part" << sa
+          << ";\n    redm[threadIdx.x >> 6] = om;\n    reds[threadIdx.x >> 6] = os;\n  }\n";
+        // The waves' results meet in lanes 0..15 of wave 0 (a 4-step
+        // butterfly: a serial fold by one thread was the tail of every one
+        // of the many short workgroups).
+        static_assert(kPartBlock / 64 == 16, "16 waves per chunk");
+        o << "  __syncthreads();\n  if (threadIdx.x < 64u) {\n";
+        o << "    const uint32_t w = threadIdx.x & 15u;\n";
+        o << "    float acc = red" << sa << "[w], m = threadIdx.x < 16u ? redm[w] : -__builtin_inff(), s = threadIdx.x < "
+             "16u ? reds[w] : 0.0f;\n";
+        o << "    acc = tca::hip::seg_allreduce<16>(acc, comb" << sa << ");\n";
+        o << "    for (int off = 8; off > 0; off >>= 1)\n"
+          << "      tca::hip::online_expsum_merge(m, s, __shfl_xor(m, off, 64), __shfl_xor(s, off, 64));\n";
+        o << "    if (threadIdx.x == 0u) {\n";
+        o << "      p" << sa << "[static_cast<uint64_t>(r) * PMAX + p] = acc;\n";
+        o << "      p" << sb << "[static_cast<uint64_t>(r) * PMAX + p] = s;\n";
+        o << "      q" << sb << "[static_cast<uint64_t>(r) * PMAX + p] = m;\n    }\n  }\n}\n";
+        if (foldedMerge.count(p)) return;  // the row map computes (a, S) itself
+        // The merge: one wave per row.
+        const std::string mfn = pk.symbol + "_smerge" + tag;
+        smFns.push_back({mfn, p});
+        smChunk[mfn] = kOnlineChunkVecs;
+        o << "template <uint32_t V>\n__device__ __forceinline__ void " << mfn << "(\n    " << sig << smSig << ") {\n";
+        o << "  constexpr uint32_t PMAX = " << kMaxParts << "u;\n";
+        o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
+        o << "  const uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63u;\n";
+        o << "  if (r >= " << ProductExpr(geo.outer) << ") return;  // whole waves\n";
+        for (int a : geo.outer) o << "  const uint32_t c" << a << " = r;\n";
+        pairValues(p, "  ");
+        o << "  if (lane == 0u) {\n    t" << ta << "[" << Offset(ta, A.store_axes, coord) << "] = aval;\n    t" << tb
+          << "[" << Offset(tb, B.store_axes, coord) << "] = bval;\n  }\n}\n";
+      };
       for (size_t p = 0; p < passes.size(); ++p) {
         const ir::Chain& c0 = g_.chains[passes[p][0]];
         const bool red = !c0.reduces.empty();
         const std::string tag = std::to_string(p + 1);
+        if (onlinePair[p]) {
+          emitOnlinePair(p);
+          ++p;  // pass p + 1 is folded into pass p's kernels
+          continue;
+        }
         if (red) {
           // Partial folds of pass p.
           const std::string fn = pk.symbol + "_spart" + tag;
@@ -2627,7 +2913,7 @@ class Emitter {
           for (int ci : passes[p]) o << " #" << ci;
           o << ": split rows, pass " << tag << ", partial folds\n";
           o << "template <uint32_t V>\n__device__ __forceinline__ void " << fn << "(\n    " << sig << smSig << ") {\n";
-          chunkHead();
+          chunkHead(kChunkVecs);
           loadRowScalars(p, "  ");
           combsOf(p, "  ");
           for (int ci : passes[p]) {
@@ -2713,8 +2999,21 @@ class Emitter {
           smFns.push_back({fn, p});
           o << "// statement #" << passes[p][0] << ": split rows, pass " << tag << ", row map over a chunk\n";
           o << "template <uint32_t V>\n__device__ __forceinline__ void " << fn << "(\n    " << sig << smSig << ") {\n";
-          chunkHead();
+          chunkHead(kChunkVecs);
+          const bool folded = p >= 2 && foldedMerge.count(p - 2);
+          if (folded) {
+            // The fused pair's values for this row, computed here (every wave).
+            const ir::Chain& A = g_.chains[passes[p - 2][0]];
+            const ir::Chain& B = g_.chains[passes[p - 1][0]];
+            pairValues(p - 2, "  ");
+            o << "  if (p == 0u && threadIdx.x == 0u) {\n    t" << A.store_tensor << "["
+              << Offset(A.store_tensor, A.store_axes, coord) << "] = aval;\n    t" << B.store_tensor << "["
+              << Offset(B.store_tensor, B.store_axes, coord) << "] = bval;\n  }\n";
+            computed[A.store_tensor] = "aval";
+            computed[B.store_tensor] = "bval";
+          }
           loadRowScalars(p, "  ");
+          computed.clear();
           std::ostringstream b;
           b << "  uint32_t v0 = lo + threadIdx.x;\n";
           b << "  for (; v0 + " << 3 * kPartBlock << "u < hi; v0 += " << 4 * kPartBlock << "u) {\n";
@@ -2825,7 +3124,9 @@ class Emitter {
             sk.grid.push_back(rowGuard.empty() ? std::string("1/1") : DimProduct(geo.outer) + "/4");
           } else {
             if (!rowGuard.empty()) sk.grid.push_back(DimProduct(geo.outer) + "/1");
-            sk.grid.push_back(cdim + "/" + std::to_string(uint64_t{kChunkVecs} * w.v) + ":" + std::to_string(kMaxParts));
+            const auto cv = smChunk.find(fn);
+            const uint64_t chunk = cv == smChunk.end() ? kChunkVecs : cv->second;
+            sk.grid.push_back(cdim + "/" + std::to_string(chunk * w.v) + ":" + std::to_string(kMaxParts));
           }
           sk.when.push_back(cdim + " " + std::to_string(lo) + " 4294967295 " + std::to_string(w.mod) + " " +
                             std::to_string(w.rem));

@@ -234,6 +234,49 @@ __device__ __forceinline__ uint32_t wave_id() { return threadIdx.x >> 6; }
 // ceil(a / b) for b > 0, exact for every uint32 a (no a + b - 1 that wraps).
 __host__ __device__ __forceinline__ uint32_t ceil_div(uint32_t a, uint32_t b) { return a == 0u ? 0u : (a - 1u) / b + 1u; }
 
+// e^x as 2^(x log2 e) on the hardware exp2 (v_exp_f32, 1 ulp), for the
+// terms of the online normaliser's sums: rounding the product adds at most
+// |x| 2^-24 ln 2 of relative error, 2.7e-6 for |x| <= 44 (x <= 0 here; below
+// -44 a term is under 2^-63 of the largest, 1, and does not register in an
+// f32 sum). -inf gives 0, NaN NaN.
+__device__ __forceinline__ float exp_term(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+// The online normaliser of a softmax (Milakov & Gimelshein 2018, "Online
+// normalizer calculation for softmax"): a running maximum m of the values
+// seen (NaN never enters it; -inf until a larger value arrives) and
+// s = sum of expf(v - m) over them, rescaled whenever m grows. Then
+// sum(expf(v - a)) = s * expf(m - a) for any a. The special values behave as
+// in that sum evaluated directly with a >= m: a NaN value or an exp(inf - inf)
+// makes s NaN, and a -inf value adds nothing. The caller handles a = -inf
+// (every value -inf or NaN, where the direct sum is NaN).
+// N values at a time: their maximum first (fmaxf: NaN left out), one
+// rescale when it exceeds m, then one exponential per value, on the
+// hardware exp2 (exp_term). With a rescale per value and ocml's expf (about
+// 16 instructions: range reduction with a split log2(e), ldexp, overflow
+// clamps) the fused softmax partial was VALU-bound at 2.1x the time of its
+// read; per vector and on exp_term it is bound by the read again.
+template <int N>
+__device__ __forceinline__ void online_expsum_add(float& m, float& s, const float (&v)[N]) {
+  float g = v[0];
+#pragma unroll
+  for (int i = 1; i < N; ++i) g = fmaxf(g, v[i]);
+  if (g > m) {
+    s *= exp_term(m - g);
+    m = g;
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) s += v[i] != -__builtin_inff() ? exp_term(v[i] - m) : 0.0f;
+}
+
+// Merges another lane's (m2, s2) into (m, s): commutative, so a butterfly
+// over the wave leaves every lane with the same pair. The factors are
+// exp_term(m - M), m <= M (the same bound as the terms).
+__device__ __forceinline__ void online_expsum_merge(float& m, float& s, float m2, float s2) {
+  const float M = fmaxf(m, m2);
+  s = (m == M ? s : s * exp_term(m - M)) + (m2 == M ? s2 : s2 * exp_term(m2 - M));
+  m = M;
+}
+
 }  // namespace hip
 }  // namespace tca
 

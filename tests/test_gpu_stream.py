@@ -177,6 +177,34 @@ def test_split_softmax(gpu, R, C):
     assert np.abs(got.astype(np.float64).sum(1) - 1.0).max() <= reduce_tol(C)
 
 
+@pytest.mark.parametrize("C", [40000, 1_000_002])
+def test_split_softmax_special_values(gpu, C):
+    """Split rows fold the max and the exp-sum in one read (the online
+    normaliser); special values must come out as the sequential definition
+    gives them (the oracle): -inf entries of a finite row are 0, a row of
+    only -inf is NaN (expf(-inf - -inf)), a +inf entry makes its row NaN
+    (expf(inf - inf)), a NaN entry makes its row NaN, and a row whose
+    maximum is the first or the last element scales the others right."""
+    _say("split C3 special values", C)
+    x = inputs.normal((6, C), 2.0, 4)
+    x[0, ::7] = -np.inf
+    x[1, :] = -np.inf
+    x[2, C // 3] = np.inf
+    x[3, C // 2] = np.nan
+    x[4, 0] = 40.0
+    x[5, -1] = 40.0
+    want = oracle.softmax(x)
+    y = out_dev((6, C), gpu)
+    run(compiled("softmax_dyn"), [to_dev(x, gpu), y])
+    got = host(y)
+    assert np.array_equal(np.isnan(got), np.isnan(want)), [int(np.isnan(got[i]).sum()) for i in range(6)]
+    fin = ~np.isnan(want)
+    rel = np.abs(got[fin].astype(np.float64) - want[fin]) / np.maximum(np.abs(want[fin].astype(np.float64)), 1e-30)
+    assert rel.max() <= reduce_tol(C), "softmax relative error %g" % rel.max()
+    assert np.all(got[0, ::7] == 0.0)
+    assert np.isnan(got[1]).all() and np.isnan(got[2]).all() and np.isnan(got[3]).all()
+
+
 @pytest.mark.parametrize("R,C", MULTIPASS_SPLIT_SHAPES)
 def test_split_layernorm(gpu, R, C):
     _say("split C4", R, C)
