@@ -60,8 +60,10 @@ CONFIGS = {
     # its mean): one column nest of two passes, lowered as a partial + merge
     # pair per pass ([8192, 8192]: 32 row chunks) or as one whole-column
     # kernel (64 rows: one chunk); not configurations
-    "c2mv": ("col_mean_var_dyn", "column mean+variance f32 [1,8192,8192] (column family, 2 passes, pairs)"),
-    "c2mw": ("col_mean_var_dyn", "column mean+variance f32 [1,64,1048576] (column family, 2 passes, whole)"),
+    "c2mv": ("col_mean_var_dyn", "column mean+variance f32 [1,8192,8192] (column family, one read: pairwise "
+                                 "mean and centred sum of squares, partial + merge)"),
+    "c2mw": ("col_mean_var_dyn", "column mean+variance f32 [1,64,1048576] (column family, one read: pairwise "
+                                 "mean and centred sum of squares, one chunk)"),
     # C5 bf16 at 8192^3: not a configuration; four tiles per CU instead of one, so the C epilogue
     # and the ring's fill weigh a quarter as much
     "c5b8": ("gemm_bf16", "gemm bf16 -> f32 8192^3 (not a configuration)"),
@@ -113,9 +115,9 @@ def _setup(key, dev):
     elif key in ("c2mv", "c2mw"):
         R, C = (8192, 8192) if key == "c2mv" else (64, 1 << 20)
         x = inputs.normal((1, R, C), 1.0, 0)
-        # each pass reads the tile (the program's two reductions): 2 R C 4
-        # bytes, plus the two [C] results
-        algo = 2 * R * C * 4 + 2 * C * 4
+        # the tile read once (the two reductions fused into one read), plus
+        # the two [C] results
+        algo = R * C * 4 + 2 * C * 4
         per_set = algo
         make = lambda i: [dev_f32(x), torch.empty((1, C), device=dev), torch.empty((1, C), device=dev)]  # noqa: E731
         scalars = [1.0 / R]

@@ -16,7 +16,7 @@ import os
 import subprocess
 
 from . import _lib
-from .pkg import EMIT_NO_FUSION, EMIT_NO_GEMM, EMIT_NO_GEMM_SPLIT  # noqa: F401  (re-exported)
+from .pkg import EMIT_NO_FUSION, EMIT_NO_GEMM, EMIT_NO_GEMM_SPLIT, EMIT_NO_PASS_FUSION  # noqa: F401  (re-exported)
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 INCLUDE_DIR = os.path.join(PKG_DIR, "csrc", "include")

@@ -219,6 +219,7 @@ int tca_emit(tca_builder b, const char* kernel_name, const char* target, int32_t
     o.allow_fused = (flags & TCA_EMIT_NO_FUSION) == 0;
     o.allow_gemm = (flags & TCA_EMIT_NO_GEMM) == 0;
     o.allow_gemm_split = (flags & TCA_EMIT_NO_GEMM_SPLIT) == 0;
+    o.allow_pass_fusion = (flags & TCA_EMIT_NO_PASS_FUSION) == 0;
     o.row_vectors_per_lane = (flags >> 8) & 0xf;
     o.elementwise_unroll = (flags >> 12) & 0xf;
     auto* r = new tca_emit_result_s;

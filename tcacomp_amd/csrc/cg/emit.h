@@ -39,6 +39,9 @@ struct Options {
   bool allow_gemm = true;
   // The contractions' small-tile kernels for output planes of M*N <= 2^20.
   bool allow_gemm_split = true;
+  // Two passes of a nest that read one input fused into one read where the
+  // arithmetic allows (online softmax normaliser, pairwise mean/variance).
+  bool allow_pass_fusion = true;
   // Geometry knobs (power-of-two values; 0 = default). Row family: target
   // 16-byte vectors per lane and row operand (lanes per row follow from it).
   // Elementwise family: 16-byte vectors per thread and operand.

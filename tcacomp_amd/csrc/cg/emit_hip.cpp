@@ -843,6 +843,49 @@ ColGeom ColCheck(const Graph& g, const std::vector<int>& chains) {
   return geo;
 }
 
+// A mean and a centred sum of squares over the reduced axis, fusable into
+// one read of the tile (Chan, Golub & LeVeque, "Updating formulae and a
+// pairwise algorithm for computing sample variances", 1979): chain A folds
+// t with + from 0 (f32) into m (its result after init and piped map, an f32
+// column vector), and chain B folds (t - m) * (t - m) with + from 0 (f32),
+// where m is read at B's own column and t is A's root body. For rows split
+// into groups g of n_g rows with sums S_g and M2_g = sum over g of
+// (t - S_g / n_g)^2,
+//   sum over the rows of (t - m)^2 = M2 + n (S / n - m)^2,
+//   M2 of a union a + b = M2_a + M2_b + (S_b / n_b - S_a / n_a)^2 n_a n_b / (n_a + n_b),
+// exactly in real arithmetic and every term non-negative, so no
+// cancellation. B's piped map is applied to that sum as usual.
+bool ChanMeanVar(const ir::Graph& g, const ir::Chain& A, const ir::Chain& B, const ColGeom& geo) {
+  if (A.reduces.size() != 1 || B.reduces.size() != 1) return false;
+  if (g.exprs[A.root.fn.body].type != ir::Elem::F32 || g.exprs[B.root.fn.body].type != ir::Elem::F32) return false;
+  if (g.tensors[A.store_tensor].elem != ir::Elem::F32) return false;
+  auto zeroAdd = [&](const ir::ReduceStage& r) {
+    const ir::Expr& init = g.exprs[r.init];
+    if (init.op != ir::Op::Const || init.type != ir::Elem::F32 || init.value != 0.0) return false;
+    const ir::Expr& e = g.exprs[r.fn.body];
+    const int acc = r.fn.params[0], now = r.fn.params[1];
+    return e.op == ir::Op::Bin && static_cast<ir::BinOp>(e.code) == ir::BinOp::Add && e.args.size() == 2 &&
+           ((e.args[0] == acc && e.args[1] == now) || (e.args[0] == now && e.args[1] == acc));
+  };
+  if (!zeroAdd(A.reduces[0]) || !zeroAdd(B.reduces[0])) return false;
+  const ir::Expr& sq = g.exprs[B.root.fn.body];
+  if (sq.op != ir::Op::Bin || static_cast<ir::BinOp>(sq.code) != ir::BinOp::Mul || sq.args.size() != 2) return false;
+  if (!SameRowExpr(g, sq.args[0], B, sq.args[1], B)) return false;
+  const ir::Expr& d = g.exprs[sq.args[0]];
+  if (d.op != ir::Op::Bin || static_cast<ir::BinOp>(d.code) != ir::BinOp::Sub || d.args.size() != 2) return false;
+  if (g.exprs[d.args[1]].op != ir::Op::Param) return false;
+  for (size_t k = 0; k < B.root.fn.params.size(); ++k) {
+    if (B.root.fn.params[k] != d.args[1]) continue;
+    const ir::Operand& op = B.root.ops[k];
+    if (op.tensor != A.store_tensor || op.axes != A.store_axes || ClassifyCol(op, geo) != ColKind::ColVec) return false;
+    if (B.has_piped)
+      for (const auto& po : B.piped.ops)
+        if (po.tensor == A.store_tensor) return false;
+    return SameRowExpr(g, A.root.fn.body, A, d.args[0], B);
+  }
+  return false;
+}
+
 // ---- elementwise family check --------------------------------------------
 
 bool DegenerateReduces(const Graph& g, const ir::Chain& c) {
@@ -2615,7 +2658,7 @@ class Emitter {
     // maxima the sums were taken against go to a partial of their own.
     std::vector<bool> onlinePair(passes.size(), false);
     std::set<int> onlineSum;  // chain B of each fused pair
-    if (splitMulti)
+    if (splitMulti && opts_.allow_pass_fusion)
       for (size_t p = 0; p + 1 < passes.size(); ++p)
         if (passes[p].size() == 1 && passes[p + 1].size() == 1 &&
             OnlineMaxExpSum(g_, g_.chains[passes[p][0]], g_.chains[passes[p + 1][0]], geo) &&
@@ -3259,6 +3302,10 @@ class Emitter {
     for (size_t i = 0; i < n.chains.size(); ++i) passChains[geo.pass[i]].push_back(n.chains[i]);
     std::set<int> results, readLater;
     for (int ci : n.chains) results.insert(g_.chains[ci].store_tensor);
+    // A mean and its centred sum of squares: one read (ChanMeanVar).
+    const bool chan = opts_.allow_pass_fusion && geo.passes == 2 && passChains[0].size() == 1 &&
+                      passChains[1].size() == 1 &&
+                      ChanMeanVar(g_, g_.chains[passChains[0][0]], g_.chains[passChains[1][0]], geo);
     // Operands by kind (root and piped maps) over a set of chains, each
     // loaded once per kind.
     struct Ops {
@@ -3670,15 +3717,223 @@ class Emitter {
       o << "}\n";
     };
 
+    // ---- a mean and its centred sum of squares in one read (chan): the
+    // partial keeps per thread the sum S of chain A's values (folded row by
+    // row, as the unfused pass folds it) and M2, the sum of squares about the
+    // mean of the rows folded so far, updated per group of rows held in
+    // registers (tca::hip::chan_merge's formula); row slots and chunks merge
+    // the same way, in slot and chunk order, and the finish takes
+    // m = A's result and B's sum as M2 + n (S / n - m)^2.
+    const int chA = chan ? passChains[0][0] : -1, chB = chan ? passChains[1][0] : -1;
+    auto chanLoop = [&](const Ops& k) {
+      std::ostringstream b;
+      const ir::Chain& A = g_.chains[chA];
+      const std::string SA = "part" + std::to_string(chA);
+      auto group = [&](const std::string& ind, uint32_t rows, bool clamped, bool first) {
+        for (uint32_t u = 0; u < rows; ++u) {
+          const std::string us = std::to_string(u);
+          if (clamped && u > 0) {
+            b << ind << "const bool ok_" << us << " = r + " << us << "u * STEP < r_hi;\n";
+            b << ind << "const uint32_t rr_" << us << " = ok_" << us << " ? r + " << us << "u * STEP : r_hi - 1u;\n";
+            loads(b, k, ind, "rr_" + us, "_" + us);
+          } else {
+            loads(b, k, ind, "r + " + us + "u * STEP", "_" + us);
+          }
+        }
+        if (clamped) {
+          b << ind << "const float nu = 1.0f";
+          for (uint32_t u = 1; u < rows; ++u) b << " + (ok_" << u << " ? 1.0f : 0.0f)";
+          b << ";  // rows of this group\n" << ind << "const float rnu = 1.0f / nu;\n";
+        } else {
+          b << ind << "constexpr float nu = " << rows << ".0f, rnu = 1.0f / nu;\n";
+        }
+        if (!first) b << ind << "const float rcn = 1.0f / cn, wgt = cn * nu / (cn + nu);\n";
+        b << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) {\n";
+        for (uint32_t u = 0; u < rows; ++u) {
+          ExprGen eg(g_, b, ind + "  ", &counter_);
+          for (size_t j = 0; j < A.root.ops.size(); ++j) {
+            const int t = A.root.ops[j].tensor;
+            std::string v;
+            switch (kindOf(t)) {
+              case ColKind::Tile: v = "x" + std::to_string(t) + "_" + std::to_string(u) + "[q]"; break;
+              case ColKind::ColVec: v = "cv" + std::to_string(t) + "[q]"; break;
+              case ColKind::RowVec: v = "rv" + std::to_string(t) + "_" + std::to_string(u); break;
+              default: v = "os" + std::to_string(t); break;
+            }
+            eg.Bind(A.root.fn.params[j], v);
+          }
+          const std::string ev = eg.Gen(A.root.fn.body);
+          b << ind << "  const float e" << u << " = " << ev << ";\n";
+        }
+        b << ind << "  float gs = e0;  // the group's sum, mean and centred sum of squares\n";
+        for (uint32_t u = 1; u < rows; ++u)
+          b << ind << "  gs = " << (clamped ? "ok_" + std::to_string(u) + " ? gs + e" + std::to_string(u) + " : gs"
+                                            : "gs + e" + std::to_string(u))
+            << ";\n";
+        b << ind << "  const float gm = gs * rnu;\n";
+        b << ind << "  float g2 = (e0 - gm) * (e0 - gm);\n";
+        for (uint32_t u = 1; u < rows; ++u) {
+          b << ind << "  { const float d = e" << u << " - gm; g2 = ";
+          if (clamped) b << "ok_" << u << " ? fmaf(d, d, g2) : g2; }\n";
+          else b << "fmaf(d, d, g2); }\n";
+        }
+        if (first) {
+          b << ind << "  m2[q] = g2;\n";
+        } else {
+          b << ind << "  const float dl = gm - " << SA << "[q] * rcn;  // the group's mean less the running mean\n";
+          b << ind << "  m2[q] += g2 + dl * dl * wgt;\n";
+        }
+        for (uint32_t u = 0; u < rows; ++u) {
+          const std::string e = "e" + std::to_string(u);
+          if (first && u == 0) b << ind << "  " << SA << "[q] = e0;\n";
+          else if (clamped && u > 0)
+            b << ind << "  " << SA << "[q] = ok_" << u << " ? comb" << chA << "(" << SA << "[q], " << e << ") : " << SA
+              << "[q];\n";
+          else b << ind << "  " << SA << "[q] = comb" << chA << "(" << SA << "[q], " << e << ");\n";
+        }
+        b << ind << "}\n" << ind << "cn += nu;\n";
+      };
+      b << "  uint32_t r = r_lo + slot;\n  const bool has = r < r_hi;\n  float cn = 0.0f;  // rows this thread folded\n";
+      b << "  if (has) {\n    {\n";
+      group("      ", kEdge, true, true);
+      b << "    }\n    r += " << kEdge << "u * STEP;\n";
+      b << "    for (; r + " << kUnroll - 1 << "u * STEP < r_hi; r += " << kUnroll << "u * STEP) {\n";
+      group("      ", kUnroll, false, false);
+      b << "    }\n    for (; r < r_hi; r += " << kEdge << "u * STEP) {\n";
+      group("      ", kEdge, true, false);
+      b << "    }\n  }\n  (void)cn;\n";
+      return b.str();
+    };
+    // The finish of a fused pair from (S, M2, n) in acc<A>, m2a, na.
+    auto chanFinish = [&](std::ostringstream& b, const std::string& ind, const std::string& present,
+                          const std::function<std::string(int)>& colval) {
+      const int sa = g_.chains[chA].store_tensor;
+      b << ind << "float mv = 0.0f;  // chain A's result, as chain B reads it\n";
+      finish(b, ind, chA, "acc" + std::to_string(chA), present, "cq", colval, !internalLocal(sa), "mv");
+      b << ind << "const float dm = acc" << chA << " * (1.0f / na) - mv;\n";
+      b << ind << "const float tot = m2a + na * dm * dm;  // the sum over the rows of (t - m)^2\n";
+      finish(b, ind, chB, "tot", present, "cq", colval);
+    };
+    auto emitChanPart = [&](const std::string& name) {
+      const Ops k = opsOf(n.chains);
+      const std::string SA = "part" + std::to_string(chA);
+      o << "template <uint32_t V>\n__device__ __forceinline__ void " << name << "(\n    " << sig << partSig << ") {\n";
+      o << "  constexpr uint32_t W = " << kWaves << "u, RMIN = " << kRowsMin << "u, BLOCKS = " << kBlocks
+        << "u, SPAN = " << kSpan << "u, LSPAN = " << kLogSpan << "u;  // SPAN column vectors per block\n";
+      o << "  const uint32_t C = " << ExtentExpr(g_, geo.c) << ", R = " << ExtentExpr(g_, geo.r) << ";\n";
+      o << "  const uint32_t NOUT = " << ProductExpr(geo.outer) << ";\n";
+      o << "  const uint32_t VEC = C / V, CB = tca::hip::ceil_div(VEC, SPAN), NCB = NOUT * CB;\n";
+      o << "  const uint32_t P = tca::hip::col_split(R, NCB, RMIN, BLOCKS);\n";
+      o << "  const uint32_t p = blockIdx.x / NCB, cbk = blockIdx.x - p * NCB;\n";
+      o << "  const uint32_t ob = cbk / CB, cb = cbk - ob * CB;\n";
+      blockGeom();
+      o << "  const uint32_t r_lo = static_cast<uint32_t>(static_cast<uint64_t>(p) * R / P);\n";
+      o << "  const uint32_t r_hi = static_cast<uint32_t>(static_cast<uint64_t>(p + 1u) * R / P);\n";
+      outerCoords("  ", "ob");
+      combs("  ", {chA});
+      colvecLoads(k, true);
+      partDecls({chA});
+      o << "  float m2[V];\n#pragma unroll\n  for (uint32_t q = 0; q < V; ++q) m2[q] = 0.0f;\n";
+      o << chanLoop(k);
+      o << "  __shared__ float red" << chA << "[W * 64u * V], red" << chB << "[W * 64u * V];\n";
+      o << "  if (has) {\n#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) {\n";
+      o << "      red" << chA << "[slot * (SL * V) + cg * V + q] = " << SA << "[q];\n";
+      o << "      red" << chB << "[slot * (SL * V) + cg * V + q] = m2[q];\n    }\n  }\n";
+      o << "  __syncthreads();\n";
+      o << "  const uint32_t nrow = r_hi - r_lo, nslot = nrow < STEP ? nrow : STEP;  // slots holding rows\n";
+      o << "  if (slot == 0u && cvec < VEC) {  // the threads of slot 0 (threadIdx.x < SL) finish\n";
+      o << "#pragma unroll\n    for (uint32_t q = 0; q < V; ++q) {\n";
+      o << "      const uint32_t cq = cvec * V + q;  // this thread's output column (col0 + q)\n";
+      o << "      (void)cq;\n";
+      o << "      float acc" << chA << " = red" << chA << "[cg * V + q], m2a = red" << chB << "[cg * V + q];\n";
+      o << "      float na = nslot > 0u ? static_cast<float>((nrow - 1u) / STEP + 1u) : 0.0f;  // slot 0's rows\n";
+      o << "      for (uint32_t s2 = 1u; s2 < nslot; ++s2)\n";
+      o << "        tca::hip::chan_merge(acc" << chA << ", m2a, na, red" << chA << "[s2 * (SL * V) + cg * V + q], red" << chB
+        << "[s2 * (SL * V) + cg * V + q], static_cast<float>((nrow - s2 - 1u) / STEP + 1u));\n";
+      o << "      if (P == 1u) {\n";
+      {
+        std::ostringstream b;
+        chanFinish(b, "        ", "nslot > 0u", [&](int t) { return "cv" + std::to_string(t) + "[q]"; });
+        o << b.str();
+      }
+      o << "      } else {\n";
+      o << "        const uint64_t at = (static_cast<uint64_t>(p) * NCB + cbk) * (SPAN * V) + cg * V + q;\n";
+      o << "        p" << chA << "[at] = acc" << chA << ";\n        p" << chB << "[at] = m2a;\n";
+      o << "      }\n    }\n  }\n}\n";
+    };
+    // Merge: as emitMerge, folding (S, M2, n) of the chunks with chan_merge.
+    auto emitChanMerge = [&](const std::string& name) {
+      const Ops k = opsOf(n.chains);
+      const std::string A = "acc" + std::to_string(chA), pa = "p" + std::to_string(chA), pb = "p" + std::to_string(chB);
+      o << "template <uint32_t V>\n__device__ __forceinline__ void " << name << "(\n    " << sig << partSig << ") {\n";
+      o << "  constexpr uint32_t RMIN = " << kRowsMin << "u, BLOCKS = " << kBlocks << "u, MW = " << kMergeWaves
+        << "u, SPAN = " << kSpan << "u;\n";
+      o << "  const uint32_t C = " << ExtentExpr(g_, geo.c) << ", R = " << ExtentExpr(g_, geo.r) << ";\n";
+      o << "  const uint32_t NOUT = " << ProductExpr(geo.outer) << ";\n";
+      o << "  const uint32_t VEC = C / V, CB = tca::hip::ceil_div(VEC, SPAN), NCB = NOUT * CB;\n";
+      o << "  const uint32_t P = tca::hip::col_split(R, NCB, RMIN, BLOCKS);  // > 1: launched only then\n";
+      o << "  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;\n";
+      o << "  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 64u + lane;\n";
+      o << "  const bool active = i < static_cast<uint64_t>(NOUT) * C;\n";
+      o << "  const uint64_t ic = active ? i : 0u;  // lanes past the end read output 0 and store nothing\n";
+      o << "  const uint32_t ob = static_cast<uint32_t>(ic / C), cq = static_cast<uint32_t>(ic - static_cast<uint64_t>(ob) * C);\n";
+      o << "  const uint32_t cb = cq / (SPAN * V), within = cq - cb * (SPAN * V), cbk = ob * CB + cb;\n";
+      o << "  const uint64_t stride = static_cast<uint64_t>(NCB) * (SPAN * V);\n";
+      o << "  const uint64_t base = static_cast<uint64_t>(cbk) * (SPAN * V) + within;\n";
+      o << "  // rows of chunk c: [c R / P, (c + 1) R / P)\n";
+      o << "  const auto rows = [&](uint32_t c) {\n";
+      o << "    return static_cast<float>(static_cast<uint32_t>(static_cast<uint64_t>(c + 1u) * R / P - "
+           "static_cast<uint64_t>(c) * R / P));\n  };\n";
+      outerCoords("  ", "ob");
+      const auto atq = coordFn("cq", "0u");
+      for (int t : k.outers)
+        o << "  const " << CType(g_.tensors[t].elem) << " os" << t << " = t" << t << "["
+          << Offset(t, opOf[t]->axes, atq) << "];\n";
+      o << "  float " << A << " = 0.0f, m2a = 0.0f, na = 0.0f;\n";
+      o << "  if (w < P) {\n";
+      o << "    " << A << " = " << pa << "[static_cast<uint64_t>(w) * stride + base];\n";
+      o << "    m2a = " << pb << "[static_cast<uint64_t>(w) * stride + base];\n";
+      o << "    na = rows(w);\n";
+      o << "    uint32_t k = w + MW;\n";
+      o << "    for (; k + 3u * MW < P; k += 4u * MW) {\n";
+      for (int u = 0; u < 4; ++u)
+        o << "      const float cs" << u << " = " << pa << "[static_cast<uint64_t>(k + " << u << "u * MW) * stride + base], cm"
+          << u << " = " << pb << "[static_cast<uint64_t>(k + " << u << "u * MW) * stride + base];\n";
+      for (int u = 0; u < 4; ++u)
+        o << "      tca::hip::chan_merge(" << A << ", m2a, na, cs" << u << ", cm" << u << ", rows(k + " << u << "u * MW));\n";
+      o << "    }\n";
+      o << "    for (; k < P; k += MW)\n      tca::hip::chan_merge(" << A << ", m2a, na, " << pa
+        << "[static_cast<uint64_t>(k) * stride + base], " << pb << "[static_cast<uint64_t>(k) * stride + base], rows(k));\n";
+      o << "  }\n";
+      o << "  __shared__ float mredS[MW * 64u], mredM[MW * 64u], mredN[MW];\n";
+      o << "  if (w < P) {\n    mredS[w * 64u + lane] = " << A << ";\n    mredM[w * 64u + lane] = m2a;\n";
+      o << "    if (lane == 0u) mredN[w] = na;\n  }\n";
+      o << "  __syncthreads();\n";
+      o << "  if (w != 0u || !active) return;\n";
+      o << "  const uint32_t nw = P < MW ? P : MW;  // waves holding chunks (every one of them holds >= 1)\n";
+      o << "  for (uint32_t s2 = 1u; s2 < nw; ++s2)\n";
+      o << "    tca::hip::chan_merge(" << A << ", m2a, na, mredS[s2 * 64u + lane], mredM[s2 * 64u + lane], mredN[s2]);\n";
+      std::ostringstream b;
+      chanFinish(b, "  ", "true", [&](int t) {
+        return "t" + std::to_string(t) + "[" + Offset(t, opOf[t]->axes, atq) + "]";
+      });
+      o << b.str();
+      o << "}\n";
+    };
+
     o << "// statements";
     for (int ci : n.chains) o << " #" << ci;
     o << ": column family; reduce over @" << g_.dims[geo.r].name << " (not contiguous) per column of @"
       << g_.dims[geo.c].name;
     if (geo.passes > 1) o << " in " << geo.passes << " passes";
+    if (chan) o << ", fused into one read (a mean and its centred sum of squares)";
     o << "\n";
     if (geo.passes == 1) {
       emitPart(sym + "_part", n.chains);
       emitMerge(sym + "_merge", n.chains);
+    } else if (chan) {
+      emitChanPart(sym + "_chanpart");
+      emitChanMerge(sym + "_chanmerge");
     } else {
       emitWhole(sym + "_whole");
       for (int ps = 0; ps < geo.passes; ++ps) {
@@ -3728,6 +3983,13 @@ class Emitter {
                       " partial: " + std::to_string(kSpan) + " column vectors x a chunk of rows per block, P = col_split"});
         ks.push_back({"_m" + v, "_merge", 1, true, n.chains,
                       " merge: 64 outputs per block, 16 waves over the P chunks (P > 1 only)"});
+      } else if (chan) {
+        ks.push_back({"_p" + v, "_chanpart", 0, false, n.chains,
+                      " mean and centred sum of squares in one read: " + std::to_string(kSpan) +
+                          " column vectors x a chunk of rows per block, P = col_split"});
+        ks.push_back({"_m" + v, "_chanmerge", 1, true, n.chains,
+                      " merge of (sum, centred sum of squares, rows): 64 outputs per block, 16 waves over the P chunks "
+                      "(P > 1 only)"});
       } else {
         ks.push_back({"_w" + v, "_whole", 2, false, n.chains,
                       " whole: every pass over all rows of " + std::to_string(kSpan) + " column vectors per block, results handed on in LDS "

@@ -277,6 +277,17 @@ __device__ __forceinline__ void online_expsum_merge(float& m, float& s, float m2
   m = M;
 }
 
+// Pairwise union of two sets of values, each held as its sum s, its count
+// n (> 0) and m2, the sum of squares about its own mean (Chan, Golub &
+// LeVeque 1979): m2 of the union = m2 + m2b + (sb/nb - s/n)^2 n nb / (n + nb),
+// every term non-negative. The sums add in the order written (s, then sb).
+__device__ __forceinline__ void chan_merge(float& s, float& m2, float& n, float sb, float m2b, float nb) {
+  const float d = sb / nb - s / n;
+  m2 += m2b + d * d * (n * nb / (n + nb));
+  s += sb;
+  n += nb;
+}
+
 }  // namespace hip
 }  // namespace tca
 

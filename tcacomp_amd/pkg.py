@@ -37,6 +37,7 @@ _NEG, _POS, _LNOT, _NOT = range(4)
 EMIT_NO_FUSION = 1
 EMIT_NO_GEMM = 2
 EMIT_NO_GEMM_SPLIT = 4  # no small-tile K-split contraction kernels (the tile kernels only)
+EMIT_NO_PASS_FUSION = 8  # every pass of a multi-pass nest reads its input (no one-read fusions)
 
 
 class BuildError(Exception):

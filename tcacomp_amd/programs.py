@@ -800,7 +800,7 @@ CONFIG_PROGRAMS = {
 
 def all_builds():
     """(program factory, flags) pairs for every code object build() makes."""
-    from .pkg import EMIT_NO_FUSION, EMIT_NO_GEMM, EMIT_NO_GEMM_SPLIT
+    from .pkg import EMIT_NO_FUSION, EMIT_NO_GEMM, EMIT_NO_GEMM_SPLIT, EMIT_NO_PASS_FUSION
     out = []
     for name, f in sorted(CONFIG_PROGRAMS.items()):
         out.append((name, f, 0))
@@ -816,7 +816,16 @@ def all_builds():
     # the small-tile kernel otherwise, and the tests hold both to the oracle
     for name in TILE_ONLY:
         out.append((name + "_tiles", CONFIG_PROGRAMS[name], EMIT_NO_GEMM_SPLIT))
+    # multi-pass nests with each pass reading its input (the one-read
+    # fusions' unfused lowering, held to the same oracle)
+    for name in PASS_FUSED:
+        out.append((name + "_passes", CONFIG_PROGRAMS[name], EMIT_NO_PASS_FUSION))
     return out
+
+
+# Programs whose passes fuse into one read by default (online softmax
+# normaliser, pairwise mean/variance); the tests also run them unfused.
+PASS_FUSED = ("softmax_dyn", "col_mean_var_dyn", "col_mean_var_l_dyn")
 
 
 # Contractions the tests also run with EMIT_NO_GEMM_SPLIT (the 128/256 tile

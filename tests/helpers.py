@@ -106,3 +106,40 @@ def ulp_diff(a, b):
     ai = np.where(ai < 0, -(ai & 0x7FFFFFFF), ai)
     bi = np.where(bi < 0, -(bi & 0x7FFFFFFF), bi)
     return np.abs(ai - bi)
+
+
+def fused_var_merge_depth(R):
+    """Merges along any chain of the column family's one-read mean and
+    variance, for every geometry: a thread's groups of rows (<= R / 16 + 2),
+    row slots (<= 256), the chunks of a merge wave and the waves (<= 1024 /
+    16 + 16)."""
+    return -(-R // 16) + 2 + min(R, 256) + 64 + 16
+
+
+def fused_var_bound(x, m, inv_n):
+    """(exact, bound) for the one-read variance over axis -2 of x [..., R, C]
+    given the device's mean m [..., C]: exact = inv_n * sum over R of
+    (x - m)^2 in float64, and the bound 2 (D + 16) kappa u T (D the merge
+    depth, kappa^2 = 1 + R mean^2 / sum (x - mean)^2; each merge adds
+    non-negative terms with a few roundings each, and a merge's difference
+    of means an absolute error of a few u times the mean) plus the sum's own
+    rounding, gamma_R sum|x|, entering as (gamma_R sum|x|)^2 / R, plus the
+    final multiply's rounding. Pinned against a float32 model of the kernels
+    in tests/test_col_fused_model.py, where a dropped between-group term or
+    a wrong pair weight leaves it."""
+    u = 2.0 ** -24
+    R = x.shape[-2]
+    x64 = x.astype(np.float64)
+    d = x64 - np.asarray(m, np.float64)[..., None, :]
+    T = (d * d).sum(axis=-2)
+    if R == 0:
+        return T * float(inv_n), np.zeros_like(T)
+    mu = x64.mean(axis=-2)
+    c = x64 - mu[..., None, :]
+    Tc = (c * c).sum(axis=-2)
+    kappa = np.sqrt(1.0 + R * mu * mu / np.where(Tc > 0, Tc, 1.0))
+    kappa = np.where(Tc > 0, kappa, 1.0)
+    g = R * u / (1 - R * u)
+    sum_err = (g * np.abs(x64).sum(axis=-2)) ** 2 / R
+    b = (2 * (fused_var_merge_depth(R) + 16) * kappa * u + 2.0 ** -23) * T + sum_err
+    return T * float(inv_n), b * float(inv_n)

@@ -164,22 +164,27 @@ def test_col_split_geometry(R, C, variant, part_grid, merge_grid):
     assert sel == {base + "p%d" % variant: part_grid, base + "m%d" % variant: merge_grid}, sel
 
 
-@pytest.mark.parametrize("B,R,C,want", [
-    # 8 column blocks, P = min(16, 128) = 16 > 1: a partial + merge pair per pass
-    (1, 1000, 1000, {"p4_1": 8 * 16, "m4_1": 16, "p4_2": 8 * 16, "m4_2": 16}),
-    # <= 64 rows: P = 1, the whole-column kernel runs both passes
-    (3, 64, 1000, {"w4": 3 * 8}),
-    (1, 0, 1000, {"w4": 8}),
+@pytest.mark.parametrize("fused", [True, False], ids=["one_read", "passes"])
+@pytest.mark.parametrize("B,R,C,want,want_passes", [
+    # 8 column blocks, P = min(16, 128) = 16 > 1: one fused partial + merge, or a pair per pass
+    (1, 1000, 1000, {"p4": 8 * 16, "m4": 16}, {"p4_1": 8 * 16, "m4_1": 16, "p4_2": 8 * 16, "m4_2": 16}),
+    # <= 64 rows: P = 1, one kernel (the fused partial finishing, or the whole-column kernel over both passes)
+    (3, 64, 1000, {"p4": 3 * 8}, {"w4": 3 * 8}),
+    (1, 0, 1000, {"p4": 8}, {"w4": 8}),
     # 1094 column blocks leave room for one chunk: P = 1 over 100 rows
-    (1, 100, 140000, {"w4": 1094}),
+    (1, 100, 140000, {"p4": 1094}, {"w4": 1094}),
     # odd columns: 1-element vectors, 3 column blocks, P = min(16, 170) = 16
-    (2, 1000, 65, {"p1_1": 2 * 3 * 16, "m1_1": 3, "p1_2": 2 * 3 * 16, "m1_2": 3}),
-    (1, 100, 0, {})])
-def test_col_passes_geometry(B, R, C, want):
-    """A column nest of two passes (a variance reading its mean): with one
-    row chunk the whole-column kernel (split mode 2) runs both passes, with
-    more each pass is a partial (mode 3) and merge (mode 1) pair."""
-    e = programs.CONFIG_PROGRAMS["col_mean_var_dyn"]().emit()
+    (2, 1000, 65, {"p1": 2 * 3 * 16, "m1": 3}, {"p1_1": 2 * 3 * 16, "m1_1": 3, "p1_2": 2 * 3 * 16, "m1_2": 3}),
+    (1, 100, 0, {}, {})])
+def test_col_passes_geometry(B, R, C, want, want_passes, fused):
+    """A column nest of two passes (a variance reading its mean). Fused (the
+    default): a partial keeping the sum and the centred sum of squares, read
+    once, finishing itself with one row chunk (split mode 0) and followed by
+    a merge with more (mode 1). With EMIT_NO_PASS_FUSION: with one row chunk
+    the whole-column kernel (split mode 2) runs both passes, with more each
+    pass is a partial (mode 3) and merge (mode 1) pair."""
+    from tcacomp_amd.pkg import EMIT_NO_PASS_FUSION
+    e = programs.CONFIG_PROGRAMS["col_mean_var_dyn"]().emit(flags=0 if fused else EMIT_NO_PASS_FUSION)
     assert set(e.families()) == {"col"}
     rc, h = parse(e.plan)
     assert rc == 0, _lib.last_error()
@@ -192,9 +197,9 @@ def test_col_passes_geometry(B, R, C, want):
     grids = (ctypes.c_uint64 * len(syms))()
     assert _lib.lib().tca_program_selected(h, arr, 3, None, 0, out, grids, None, len(syms)) == 0, _lib.last_error()
     sel = {s[len("tca_col_mean_var_dyn_k0_"):]: g for s, f, g in zip(syms, out, grids) if f and g}
-    assert sel == want, sel
+    assert sel == (want if fused else want_passes), sel
     order = [s for s, f, g in zip(syms, out, grids) if f and g]
-    assert order == sorted(order, key=syms.index)  # launch order: pass 1 pair before pass 2
+    assert order == sorted(order, key=syms.index)  # launch order: partials before their merges, pass 1 first
 
 
 @pytest.mark.parametrize("B,C,want", [

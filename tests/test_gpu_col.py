@@ -12,20 +12,26 @@ col_mean_bf16's piped map is one rounded multiply and one rounded add on
 both sides.
 
 col_mean_var (a variance reading its mean: one column nest of two passes)
-runs at shapes that reach the whole-column kernel (<= 64 rows, or more
-than 512 column blocks) and the per-pass partial + merge pairs. Its mean is
-an exact sum times f32(1 / R), one rounded multiply: bit for bit. Its
-variance sums f32 terms (x - mean)^2, each rounded once on both sides, in
-an order of the device's choosing: within the fold's rounding bound,
-gamma_(R-1) sum|terms| (gamma_n = n u / (1 - n u), u = 2^-24), plus the
-final multiply's rounding."""
+runs in both lowerings: fused into one read (the default: each partial
+keeps the sum and the centred sum of squares, merged pairwise) and pass by
+pass (EMIT_NO_PASS_FUSION: the whole-column kernel at <= 64 rows or more
+than 512 column blocks, otherwise a partial + merge pair per pass), at
+shapes that reach one chunk and many. Its mean is an exact sum times
+f32(1 / R), one rounded multiply: bit for bit. Pass by pass, its variance
+sums f32 terms (x - mean)^2, each rounded once on both sides, in an order of
+the device's choosing: within the fold's rounding bound, gamma_(R-1)
+sum|terms| (gamma_n = n u / (1 - n u), u = 2^-24), plus the final
+multiply's rounding. Fused, within helpers.fused_var_bound around the exact
+sum of (x - mean)^2 (the pairwise update's bound, pinned on a float32 model
+of the kernels in tests/test_col_fused_model.py)."""
 import sys
 
 import numpy as np
 import pytest
 
-from helpers import CANARY, compiled, run, to_dev
+from helpers import CANARY, compiled, fused_var_bound, run, to_dev
 from tcacomp_amd.compiler import TensorDesc
+from tcacomp_amd.pkg import EMIT_NO_PASS_FUSION
 
 pytestmark = pytest.mark.gpu
 
@@ -84,27 +90,74 @@ def test_col_sum_u8(gpu, R, C):
     np.testing.assert_array_equal(o.cpu().numpy().view(np.uint32), want)
 
 
+FUSED = pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["one_read", "passes"])
+
+
+def _passes_bound(x, want_mean, inv_n):
+    """(exact, bound) of the per-pass lowering: f32 terms (x - mean)^2, each
+    rounded once as on the device, summed in an order of the device's
+    choosing (gamma_(R-1) sum|terms|), plus the final multiply's rounding."""
+    R = x.shape[1]
+    d = x - want_mean[:, None, :]
+    terms = (d * d).astype(np.float64)
+    exact = terms.sum(axis=1)
+    nu = max(R - 1, 0) * 2.0 ** -24
+    bound = nu / (1 - nu) * np.abs(terms).sum(axis=1) * float(inv_n) + np.abs(exact * float(inv_n)) * 2.0 ** -23
+    return exact * float(inv_n), bound
+
+
+@FUSED
 @pytest.mark.parametrize("name", ["col_mean_var_dyn", "col_mean_var_l_dyn"])
 @pytest.mark.parametrize("B,R,C", [(1, 0, 8), (1, 1, 1), (3, 64, 1000), (2, 37, 6), (1, 100, 140000),
                                    (1, 1000, 1000), (2, 3000, 65), (4, 300, 4100), (1, 65536, 256)])
-def test_col_mean_var(gpu, name, B, R, C):
-    print(name, B, R, C, flush=True)
+def test_col_mean_var(gpu, name, B, R, C, flags):
+    print(name, B, R, C, flags, flush=True)
     sys.stdout.flush()
     x = _ints((B, R, C), 8, B * 131 + R * 7 + C)
     inv_n = np.float32(1.0 / max(R, 1))
     mean = to_dev(np.full((B, C), CANARY, np.float32), gpu)
     var = to_dev(np.full((B, C), CANARY, np.float32), gpu)
     args = [to_dev(x, gpu)] + ([mean] if name == "col_mean_var_dyn" else []) + [var]
-    run(compiled(name), args, scalars=[float(inv_n)])
+    run(compiled(name, flags), args, scalars=[float(inv_n)])
     ssum = x.astype(np.float64).sum(axis=1).astype(np.float32)  # exact: |sums| < 2^24
     want_mean = ssum * inv_n
     if name == "col_mean_var_dyn":
         np.testing.assert_array_equal(mean.cpu().numpy(), want_mean)
-    d = x - want_mean[:, None, :]  # f32: each term rounded once, as on the device
-    terms = (d * d).astype(np.float64)
-    exact = terms.sum(axis=1)
-    nu = max(R - 1, 0) * 2.0 ** -24
-    bound = nu / (1 - nu) * np.abs(terms).sum(axis=1) * float(inv_n) + np.abs(exact * float(inv_n)) * 2.0 ** -23
+    if flags:
+        want, bound = _passes_bound(x, want_mean, inv_n)
+    else:
+        want, bound = fused_var_bound(x, want_mean, inv_n)
     got = var.cpu().numpy().astype(np.float64)
-    err = np.abs(got - exact * float(inv_n))
+    err = np.abs(got - want)
     assert np.all(err <= bound), (name, B, R, C, float(err.max()), float(bound[err > bound].min(initial=0)))
+
+
+@FUSED
+@pytest.mark.parametrize("kind", ["offset", "drift"])
+@pytest.mark.parametrize("B,R,C", [(1, 5000, 1000), (2, 300, 4100), (1, 100000, 48), (1, 64, 4096), (3, 7, 33)])
+def test_col_mean_var_float(gpu, kind, B, R, C, flags):
+    """Non-integer columns far from zero mean (normal around 100) and with a
+    mean that moves along the rows: the mean within the sequential sum's
+    bound of the float64 mean, the variance within its lowering's bound
+    around the device's own mean."""
+    print("col_mean_var_float", kind, B, R, C, flags, flush=True)
+    sys.stdout.flush()
+    rng = np.random.default_rng(B * 7 + R + C)
+    x = rng.standard_normal((B, R, C))
+    x += 100.0 if kind == "offset" else np.linspace(0.0, 50.0, R)[None, :, None]
+    x = x.astype(np.float32)
+    inv_n = np.float32(1.0 / R)
+    mean = to_dev(np.full((B, C), CANARY, np.float32), gpu)
+    var = to_dev(np.full((B, C), CANARY, np.float32), gpu)
+    run(compiled("col_mean_var_dyn", flags), [to_dev(x, gpu), mean, var], scalars=[float(inv_n)])
+    m = mean.cpu().numpy()
+    x64 = x.astype(np.float64)
+    g = R * 2.0 ** -24 / (1 - R * 2.0 ** -24)
+    mean_bound = (g * np.abs(x64).sum(axis=1) + np.abs(x64.sum(axis=1)) * 2.0 ** -23) * float(inv_n)
+    assert np.all(np.abs(m - x64.sum(axis=1) * float(inv_n)) <= mean_bound)
+    if flags:
+        want, bound = _passes_bound(x, m, inv_n)
+    else:
+        want, bound = fused_var_bound(x, m, inv_n)
+    err = np.abs(var.cpu().numpy().astype(np.float64) - want)
+    assert np.all(err <= bound), (kind, B, R, C, float(err.max()), float(bound[err > bound].min(initial=0)))
