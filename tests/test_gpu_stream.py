@@ -16,6 +16,7 @@ import oracle
 from helpers import (assert_layernorm_close, assert_reduce_close, canaries, compiled, host, out_dev, reduce_tol, run,
                      to_dev)
 from tcacomp_amd import inputs
+from tcacomp_amd.pkg import EMIT_NO_PASS_FUSION
 
 pytestmark = pytest.mark.gpu
 
@@ -163,13 +164,16 @@ MULTIPASS_SPLIT_SHAPES = [(1, 40000), (7, 32772), (3, 100003), (2, 1_000_002), (
                           (1, 4_000_000)]
 
 
+@pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["online", "passes"])
 @pytest.mark.parametrize("R,C", MULTIPASS_SPLIT_SHAPES)
-def test_split_softmax(gpu, R, C):
-    _say("split C3", R, C)
+def test_split_softmax(gpu, R, C, flags):
+    """Both lowerings of split rows: the online normaliser (max and exp-sum
+    in one read of each chunk) and one partial + merge per pass."""
+    _say("split C3", R, C, flags)
     x = inputs.normal((R, C), 2.0, 0)
     want = oracle.softmax(x)
     y = out_dev((R, C), gpu)
-    run(compiled("softmax_dyn"), [to_dev(x, gpu), y])
+    run(compiled("softmax_dyn", flags), [to_dev(x, gpu), y])
     got = host(y)
     assert canaries(got) == 0
     rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want.astype(np.float64)), 1e-30)
