@@ -1244,8 +1244,14 @@ class Emitter {
   // writes and the column-wise reads on 64 distinct banks), and read back
   // transposed; the output, and operands aligned with it along L, move as
   // 16-byte vectors along L. 4-byte element types only, at most 4 such
-  // operands (66 KiB of LDS).
-  static constexpr int kTrTile = 64, kTrStride = 65, kTrMax = 4;
+  // operands (66 KiB of LDS). With at most 2 such operands the tile is
+  // 128 x 128 for a 1024-thread block (LDS rows of 129 floats, 66 KiB per
+  // operand): measured on y = x * g[c] + b[r] + z^T at 8192^2, 125.8 us
+  // against 164 us for 64 x 64 tiles (128 x 64: 141, 64 x 128: 134,
+  // 128 x 128 with 512 or 256 threads: 130 / 133, 128 x 256: 132); the
+  // longer row segments each block reads and writes (512 bytes) are what
+  // pays.
+  static constexpr int kTrTile = 64, kTrMax = 4, kTrLarge = 128, kTrMaxLarge = 2;
 
   enum class TileCls { Aligned, RowVec, Bcast, Tr, Other };
 
@@ -1295,12 +1301,21 @@ class Emitter {
     const std::vector<int> outAxes = DropUnit(g_, c.store_axes);
     const int L = outAxes.back(), P = outAxes[outAxes.size() - 2];
     const std::vector<int> outer(outAxes.begin(), outAxes.end() - 2);
+    // Tile edge T: 128 while the LDS tiles (T (T + 1) floats each) fit two
+    // workgroups per CU, else 64. Q = T / 4 lanes per row of 4-element
+    // vectors, and Q rows per step of the T * T / 16 threads.
+    int nTr = 0;
+    for (const auto& op : c.root.ops) nTr += TileClass(op, outAxes, P, L) == TileCls::Tr;
+    if (c.has_piped)
+      for (const auto& op : c.piped.ops) nTr += TileClass(op, outAxes, P, L) == TileCls::Tr;
+    const int T = nTr <= kTrMaxLarge ? kTrLarge : kTrTile, Q = T / 4, S = T + 1, NT = T * T / 16;
+    const std::string Ts = std::to_string(T) + "u", Qs = std::to_string(Q) + "u", Ss = std::to_string(S) + "u";
     PlanKernel pk;
     pk.symbol = Sym(g_, prefix_, ni);
-    pk.block = 256;
+    pk.block = NT;
     pk.grid.push_back(DimProduct(outer) + "/1");
-    pk.grid.push_back(g_.dims[P].name + "/" + std::to_string(kTrTile));
-    pk.grid.push_back(g_.dims[L].name + "/" + std::to_string(kTrTile));
+    pk.grid.push_back(g_.dims[P].name + "/" + std::to_string(T));
+    pk.grid.push_back(g_.dims[L].name + "/" + std::to_string(T));
     const std::string sig = Signature(n, &pk);
     std::ostringstream& o = src_;
     const ir::Tensor& st = g_.tensors[c.store_tensor];
@@ -1328,19 +1343,19 @@ class Emitter {
         if (r.piped == piped && r.k == k) return r;
       return ops.front();
     };
-    o << "// statement #" << n.chains[0] << ": elementwise family, " << kTrTile << "x" << kTrTile
-      << " tiles, " << nTiles << " transposed operand(s) staged in LDS\n";
-    o << "extern \"C\" __global__ void __launch_bounds__(256) " << pk.symbol << "(\n    " << sig << ") {\n";
-    o << "  __shared__ uint32_t tr_lds[" << nTiles << "][" << kTrTile * kTrStride << "];\n";
-    o << "  const uint32_t nl = tca::hip::ceil_div(" << EL << ", " << kTrTile << "u), np = tca::hip::ceil_div(" << EP
-      << ", " << kTrTile << "u);\n";
+    o << "// statement #" << n.chains[0] << ": elementwise family, " << T << "x" << T << " tiles, " << nTiles
+      << " transposed operand(s) staged in LDS\n";
+    o << "extern \"C\" __global__ void __launch_bounds__(" << NT << ") " << pk.symbol << "(\n    " << sig << ") {\n";
+    o << "  __shared__ uint32_t tr_lds[" << nTiles << "][" << T * S << "];\n";
+    o << "  const uint32_t nl = tca::hip::ceil_div(" << EL << ", " << Ts << "), np = tca::hip::ceil_div(" << EP << ", "
+      << Ts << ");\n";
     o << "  uint32_t bid = blockIdx.x;\n";
-    o << "  const uint32_t l0 = (bid % nl) * " << kTrTile << "u; bid /= nl;\n";
-    o << "  const uint32_t p0 = (bid % np) * " << kTrTile << "u; bid /= np;\n";
+    o << "  const uint32_t l0 = (bid % nl) * " << Ts << "; bid /= nl;\n";
+    o << "  const uint32_t p0 = (bid % np) * " << Ts << "; bid /= np;\n";
     for (int i = static_cast<int>(outer.size()) - 1; i >= 0; --i)
       o << "  const uint32_t c" << outer[i] << " = bid % " << ExtentExpr(g_, outer[i]) << "; bid /= "
         << ExtentExpr(g_, outer[i]) << ";\n";
-    o << "  const uint32_t tr = threadIdx.x / 16u, tc = threadIdx.x % 16u;\n";
+    o << "  const uint32_t tr = threadIdx.x / " << Qs << ", tc = threadIdx.x % " << Qs << ";\n";
     // Coordinates: L and P spelled by the caller, outer axes c<a>, unit 0.
     auto coordFn = [&](const std::string& l, const std::string& p) {
       return [this, l, p, L, P](int a) -> std::string {
@@ -1350,7 +1365,7 @@ class Emitter {
         return "c" + std::to_string(a);
       };
     };
-    // 1. Output rows p0 + tr + 16i, 4 L values each. The operands read
+    // 1. Output rows p0 + tr + Q i, 4 L values each. The operands read
     // straight from memory are loaded first, so their latency overlaps the
     // tile's (whose LDS writes wait for its own loads).
     o << "  const bool l_vec = " << EL << " % 4u == 0u;\n";
@@ -1365,7 +1380,7 @@ class Emitter {
         o << "  " << T << " " << nm << "[4];\n";
     }
     o << "#pragma unroll\n  for (uint32_t i = 0; i < 4u; ++i) {\n";
-    o << "    const uint32_t p = p0 + tr + 16u * i;\n";
+    o << "    const uint32_t p = p0 + tr + " << Qs << " * i;\n";
     o << "    full[i] = p < " << EP << " && l_vec && lb + 3u < " << EL << ";\n";
     o << "    if (full[i]) {\n";
     for (const auto& r : ops) {
@@ -1380,7 +1395,7 @@ class Emitter {
         o << "      " << nm << "[i] = " << t << "[" << Offset(r.op->tensor, r.op->axes, coordFn("lb", "p")) << "];\n";
     }
     o << "    }\n  }\n";
-    // 2. Transposed operands: rows l0 + tr + 16i of the [L][P] tile, 4 P values each.
+    // 2. Transposed operands: rows l0 + tr + Q i of the [L][P] tile, 4 P values each.
     o << "  const bool p_vec = " << EP << " % 4u == 0u;\n";
     for (const auto& r : ops) {
       if (r.cls != TileCls::Tr) continue;
@@ -1389,14 +1404,14 @@ class Emitter {
       // All four row loads first, then the LDS writes (which wait for them).
       o << "  tca::hip::vec<" << T << ", 4> " << zv << "[4];\n  bool " << zf << "[4];\n";
       o << "#pragma unroll\n  for (uint32_t i = 0; i < 4u; ++i) {\n";
-      o << "    const uint32_t l = l0 + tr + 16u * i, p = p0 + 4u * tc;\n";
+      o << "    const uint32_t l = l0 + tr + " << Qs << " * i, p = p0 + 4u * tc;\n";
       o << "    " << zf << "[i] = l < " << EL << " && p_vec && p + 3u < " << EP << ";\n";
       o << "    if (" << zf << "[i]) " << zv << "[i] = tca::hip::load_vec_nt<" << T << ", 4>(" << t << " + "
         << Offset(r.op->tensor, r.op->axes, coordFn("l", "p")) << ");\n";
       o << "  }\n";
       o << "#pragma unroll\n  for (uint32_t i = 0; i < 4u; ++i) {\n";
-      o << "    const uint32_t lr = tr + 16u * i, l = l0 + lr, p = p0 + 4u * tc;\n";
-      o << "    uint32_t* row = &tr_lds[" << r.tile << "][lr * " << kTrStride << "u + 4u * tc];\n";
+      o << "    const uint32_t lr = tr + " << Qs << " * i, l = l0 + lr, p = p0 + 4u * tc;\n";
+      o << "    uint32_t* row = &tr_lds[" << r.tile << "][lr * " << Ss << " + 4u * tc];\n";
       o << "    if (" << zf << "[i]) {\n";
       o << "#pragma unroll\n      for (uint32_t j = 0; j < 4u; ++j) row[j] = __builtin_bit_cast(uint32_t, " << zv
         << "[i][j]);\n";
@@ -1409,11 +1424,11 @@ class Emitter {
     o << "  __syncthreads();\n";
     // 3. Compute and store.
     o << "#pragma unroll\n  for (uint32_t i = 0; i < 4u; ++i) {\n";
-    o << "    const uint32_t pr = tr + 16u * i, p = p0 + pr;\n";
+    o << "    const uint32_t pr = tr + " << Qs << " * i, p = p0 + pr;\n";
     o << "    if (p >= " << EP << ") continue;\n";
     auto trVal = [&](const OpRef& r, const std::string& lr) {
       return "__builtin_bit_cast(" + CType(g_.tensors[r.op->tensor].elem) + ", tr_lds[" + std::to_string(r.tile) +
-             "][(" + lr + ") * " + std::to_string(kTrStride) + "u + pr])";
+             "][(" + lr + ") * " + Ss + " + pr])";
     };
     // Whole vector along L.
     o << "    if (full[i]) {\n";
@@ -1456,8 +1471,8 @@ class Emitter {
     }
     o << "      }\n    }\n  }\n}\n\n";
     AddKernel(pk, Family::Elementwise, n.chains,
-              "tile=" + std::to_string(kTrTile) + "x" + std::to_string(kTrTile) + " lds_tiles=" + std::to_string(nTiles) +
-                  " block=256");
+              "tile=" + std::to_string(T) + "x" + std::to_string(T) + " lds_tiles=" + std::to_string(nTiles) +
+                  " block=" + std::to_string(NT));
     return true;
   }
 
@@ -3461,8 +3476,9 @@ class Emitter {
             << "[q]);\n";
     };
     // The row loop of a block over [r_lo, r_hi) for the chains `cs`: a
-    // first group of kEdge rows, groups of kUnroll rows while whole ones
-    // fit, then groups of kEdge to the chunk's end. The edge groups clamp
+    // first group of kUnroll rows when every slot owns that many, else of
+    // kEdge rows, groups of kUnroll rows while whole ones fit, then groups
+    // of kEdge to the chunk's end. The edge groups clamp
     // rows past the chunk to its last row (unconditional loads stay in
     // flight together) and fold only the rows they own; row 0 of each is
     // always owned. Declares `has` (the thread's slot holds a row).
@@ -3483,9 +3499,14 @@ class Emitter {
           fold(b, cs, ind, "_" + std::to_string(u), first && u == 0, clamped && u > 0 ? "ok_" + std::to_string(u) : "");
       };
       b << "  uint32_t r = r_lo + slot;\n  const bool " << hasName << " = r < r_hi;\n  if (" << hasName
-        << ") {\n    {\n";
+        << ") {\n";
+      // A first group of 16 when every slot of the block owns >= 16 rows
+      // (block-uniform), else of 4 (clamped).
+      b << "    if (r_hi - r_lo >= " << kUnroll << "u * STEP) {\n";
+      group("      ", kUnroll, false, true);
+      b << "      r += " << kUnroll << "u * STEP;\n    } else {\n";
       group("      ", kEdge, true, true);
-      b << "    }\n    r += " << kEdge << "u * STEP;\n";
+      b << "      r += " << kEdge << "u * STEP;\n    }\n";
       b << "    for (; r + " << kUnroll - 1 << "u * STEP < r_hi; r += " << kUnroll << "u * STEP) {\n";
       group("      ", kUnroll, false, false);
       b << "    }\n    for (; r < r_hi; r += " << kEdge << "u * STEP) {\n";
@@ -3794,9 +3815,12 @@ class Emitter {
         b << ind << "}\n" << ind << "cn += nu;\n";
       };
       b << "  uint32_t r = r_lo + slot;\n  const bool has = r < r_hi;\n  float cn = 0.0f;  // rows this thread folded\n";
-      b << "  if (has) {\n    {\n";
+      b << "  if (has) {\n";
+      b << "    if (r_hi - r_lo >= " << kUnroll << "u * STEP) {  // every slot owns >= 16 rows\n";
+      group("      ", kUnroll, false, true);
+      b << "      r += " << kUnroll << "u * STEP;\n    } else {\n";
       group("      ", kEdge, true, true);
-      b << "    }\n    r += " << kEdge << "u * STEP;\n";
+      b << "      r += " << kEdge << "u * STEP;\n    }\n";
       b << "    for (; r + " << kUnroll - 1 << "u * STEP < r_hi; r += " << kUnroll << "u * STEP) {\n";
       group("      ", kUnroll, false, false);
       b << "    }\n    for (; r < r_hi; r += " << kEdge << "u * STEP) {\n";

@@ -951,18 +951,20 @@ def test_elementwise_broadcast_operands_take_the_row_vector_path():
 
 
 def test_elementwise_transposed_operand_takes_the_lds_tile_kernel():
-    # z[c][r] under y[r][c]: 64x64 tiles, z staged through LDS rows of 65
-    # words, read back transposed; the grid is (outer) x ceil(R/64) x ceil(C/64).
+    # z[c][r] under y[r][c]: with at most two transposed operands, 128x128
+    # tiles for 1024 threads, z staged through LDS rows of 129 words, read
+    # back transposed; the grid is (outer) x ceil(R/128) x ceil(C/128).
     e = _bias_program(True).emit()
     src = e.source
     # tensors in declaration order: x t0, z t1, g t2, b t3, y t4
-    assert "__shared__ uint32_t tr_lds[1][4160];" in src
+    assert "__shared__ uint32_t tr_lds[1][16512];" in src
+    assert "__launch_bounds__(1024)" in src
     assert "tca::hip::load_vec_nt<float, 4>(t1 + (l) * d0 + p)" in src
-    assert "tr_lds[0][(4u * tc + q) * 65u + pr]" in src
+    assert "tr_lds[0][(4u * tc + q) * 129u + pr]" in src
     assert "tca::hip::store_vec_nt<float, 4>(t4 + (p) * d1 + lb, out);" in src
-    assert "kernel tca_ew_bcast_k0 256 0 3 1/1 R/64 C/64" in e.plan
+    assert "kernel tca_ew_bcast_k0 1024 0 3 1/1 R/128 C/128" in e.plan
     ptr = 0x1000
-    for R, C, grid in ((1000, 1000, 16 * 16), (64, 4100, 1 * 65), (0, 5, 0), (5, 70001, 1 * 1094)):
+    for R, C, grid in ((1000, 1000, 8 * 8), (64, 4100, 1 * 33), (0, 5, 0), (5, 70001, 1 * 547), (128, 256, 2)):
         prog = compiler.CompiledProgram("ew_bcast", e, "")
         ts = [TensorDesc(ptr if R * C else 0, (R, C), 0), TensorDesc(ptr if R * C else 0, (C, R), 0),
               TensorDesc(ptr if C else 0, (C,), 0), TensorDesc(ptr if R else 0, (R,), 0),
@@ -972,6 +974,22 @@ def test_elementwise_transposed_operand_takes_the_lds_tile_kernel():
         grids = (ctypes.c_uint64 * 1)()
         _lib.check(_lib.lib().tca_program_selected(prog.parsed(), arr, 5, None, 0, sel, grids, None, 1))
         assert grids[0] == grid, (R, C, grids[0])
+
+
+def test_elementwise_three_transposed_operands_keep_64_tiles():
+    # Three transposed operands would need 198 KiB of LDS at 128x128: 64x64
+    # tiles for 256 threads (LDS rows of 65 words, 3 x 16.6 KiB).
+    from tcacomp_amd.pkg import TF32, At, NewBuilder
+    bld = NewBuilder("ew_tr3")
+    R, C = bld.Dim("R", 0), bld.Dim("C", 0)
+    zs = [bld.Tensor("z%d" % i, TF32, C, R) for i in range(3)]
+    y = bld.Tensor("y", TF32, R, C)
+    bld.Stmt().Iter(R, C).Map([At(z, C, R) for z in zs],
+                              lambda a, b, c: bld.Add(bld.Add(a, b), c)).As(R, C).Store(y, R, C)
+    e = bld.Build().emit()
+    assert "__shared__ uint32_t tr_lds[3][4160];" in e.source and "__launch_bounds__(256)" in e.source
+    assert "tr_lds[2][(4u * tc + q) * 65u + pr]" in e.source
+    assert "kernel tca_ew_tr3_k0 256 0 3 1/1 R/64 C/64" in e.plan
 
 
 @pytest.mark.parametrize("name", ["softmax_dyn", "layernorm_dyn", "layernorm_rstd_dyn"])
