@@ -2890,53 +2890,55 @@ class Emitter {
         chunkHead(kOnlineChunkVecs);
         loadRowScalars(p, "  ");
         combsOf(p, "  ");
-        o << "  float part" << sa << " = 0.0f, om = -__builtin_inff(), os = 0.0f;\n";
-        auto step = [&](std::ostringstream& b, const std::string& ind, const std::string& sfx, bool first) {
-          b << ind << "float ev" << sfx << "[V];\n";
+        // The running maximum om is chain A's partial too: a fold of the
+        // same values with fmaxf from -inf, which A's init is.
+        o << "  float om = -__builtin_inff(), os = 0.0f;\n";
+        // The values of vector `sfx` into ev[at * V + q].
+        auto values = [&](std::ostringstream& b, const std::string& ind, const std::string& sfx, uint32_t at) {
           b << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) {\n";
           std::ostringstream es;
           const std::string ev = elemValue(es, ind + "  ", A, sfx);
-          b << es.str() << ind << "  const float e = " << ev << ";\n";
-          const std::string folded = "comb" + sa + "(part" + sa + ", e)";
-          b << ind << "  part" << sa << " = " << (first ? "q == 0u ? e : " + folded : folded) << ";\n";
-          b << ind << "  ev" << sfx << "[q] = e;\n" << ind << "}\n";
-          b << ind << "tca::hip::online_expsum_add(om, os, ev" << sfx << ");\n";
+          b << es.str() << ind << "  ev[" << at << "u * V + q] = " << ev << ";\n" << ind << "}\n";
         };
-        constexpr uint32_t kU = 4;  // 8 vectors in flight per lane measured 5% slower
+        // One online update per kU vectors (kU V values: one rescale test
+        // and at most one rescale per group). 8 vectors in flight per lane
+        // measured 5% slower.
+        constexpr uint32_t kU = 4;
         std::ostringstream b;
         b << "  {\n    const uint32_t vc = lo + threadIdx.x;\n";
         operands(b, p, "    ", false, "vc", "");
-        step(b, "    ", "", true);
+        b << "    float ev[V];\n";
+        values(b, "    ", "", 0);
+        b << "    tca::hip::online_expsum_add(om, os, ev);\n";
         b << "  }\n  uint32_t v0 = lo + threadIdx.x + " << kPartBlock << "u;\n";
         b << "  for (; v0 + " << (kU - 1) * kPartBlock << "u < hi; v0 += " << kU * kPartBlock << "u) {\n";
         for (uint32_t u = 0; u < kU; ++u) b << "    const uint32_t vc_" << u << " = v0 + " << u * kPartBlock << "u;\n";
         for (uint32_t u = 0; u < kU; ++u) operands(b, p, "    ", false, "vc_" + std::to_string(u), "_" + std::to_string(u));
-        for (uint32_t u = 0; u < kU; ++u) step(b, "    ", "_" + std::to_string(u), false);
+        b << "    float ev[" << kU << " * V];\n";
+        for (uint32_t u = 0; u < kU; ++u) values(b, "    ", "_" + std::to_string(u), u);
+        b << "    tca::hip::online_expsum_add(om, os, ev);\n";
         b << "  }\n  for (; v0 < hi; v0 += " << kPartBlock << "u) {\n    const uint32_t vc = v0;\n";
         operands(b, p, "    ", false, "vc", "");
-        step(b, "    ", "", false);
+        b << "    float ev[V];\n";
+        values(b, "    ", "", 0);
+        b << "    tca::hip::online_expsum_add(om, os, ev);\n";
         b << "  }\n";
         o << b.str();
-        o << "  part" << sa << " = tca::hip::seg_allreduce<64>(part" << sa << ", comb" << sa << ");\n";
         o << "  for (int off = 32; off > 0; off >>= 1)\n"
           << "    tca::hip::online_expsum_merge(om, os, __shfl_xor(om, off, 64), __shfl_xor(os, off, 64));\n";
-        o << "  __shared__ float red" << sa << "[" << kPartBlock / 64 << "], redm[" << kPartBlock / 64 << "], reds["
-          << kPartBlock / 64 << "];\n";
-        o << "  if ((threadIdx.x & 63u) == 0u) {\n    red" << sa << "[threadIdx.x >> 6] = part" << sa
-          << ";\n    redm[threadIdx.x >> 6] = om;\n    reds[threadIdx.x >> 6] = os;\n  }\n";
+        o << "  __shared__ float redm[" << kPartBlock / 64 << "], reds[" << kPartBlock / 64 << "];\n";
+        o << "  if ((threadIdx.x & 63u) == 0u) {\n    redm[threadIdx.x >> 6] = om;\n    reds[threadIdx.x >> 6] = os;\n  }\n";
         // The waves' results meet in lanes 0..15 of wave 0 (a 4-step
         // butterfly: a serial fold by one thread was the tail of every one
         // of the many short workgroups).
         static_assert(kPartBlock / 64 == 16, "16 waves per chunk");
         o << "  __syncthreads();\n  if (threadIdx.x < 64u) {\n";
         o << "    const uint32_t w = threadIdx.x & 15u;\n";
-        o << "    float acc = red" << sa << "[w], m = threadIdx.x < 16u ? redm[w] : -__builtin_inff(), s = threadIdx.x < "
-             "16u ? reds[w] : 0.0f;\n";
-        o << "    acc = tca::hip::seg_allreduce<16>(acc, comb" << sa << ");\n";
+        o << "    float m = threadIdx.x < 16u ? redm[w] : -__builtin_inff(), s = threadIdx.x < 16u ? reds[w] : 0.0f;\n";
         o << "    for (int off = 8; off > 0; off >>= 1)\n"
           << "      tca::hip::online_expsum_merge(m, s, __shfl_xor(m, off, 64), __shfl_xor(s, off, 64));\n";
         o << "    if (threadIdx.x == 0u) {\n";
-        o << "      p" << sa << "[static_cast<uint64_t>(r) * PMAX + p] = acc;\n";
+        o << "      p" << sa << "[static_cast<uint64_t>(r) * PMAX + p] = m;  // chain A's partial: the chunk's maximum\n";
         o << "      p" << sb << "[static_cast<uint64_t>(r) * PMAX + p] = s;\n";
         o << "      q" << sb << "[static_cast<uint64_t>(r) * PMAX + p] = m;\n    }\n  }\n}\n";
         if (foldedMerge.count(p)) return;  // the row map computes (a, S) itself

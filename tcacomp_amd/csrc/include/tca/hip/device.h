@@ -254,18 +254,26 @@ __device__ __forceinline__ float exp_term(float x) { return __builtin_amdgcn_exp
 // hardware exp2 (exp_term). With a rescale per value and ocml's expf (about
 // 16 instructions: range reduction with a split log2(e), ldexp, overflow
 // clamps) the fused softmax partial was VALU-bound at 2.1x the time of its
-// read; per vector and on exp_term it is bound by the read again.
+// read. The rescale sits behind a wave-uniform branch (taken while some
+// lane's maximum grows: rarely, after a chunk's first vectors), and a -inf
+// value needs no test of its own: the shift is m, or 0 while m is -inf
+// (then every value so far is -inf or NaN), and exp2(-inf) = 0, so each
+// value costs a subtract, a multiply, an exp2 and an add, with s exactly
+// as the per-value form gives it.
 template <int N>
 __device__ __forceinline__ void online_expsum_add(float& m, float& s, const float (&v)[N]) {
   float g = v[0];
 #pragma unroll
   for (int i = 1; i < N; ++i) g = fmaxf(g, v[i]);
-  if (g > m) {
-    s *= exp_term(m - g);
-    m = g;
+  if (__builtin_amdgcn_ballot_w64(g > m) != 0u) {
+    if (g > m) {
+      s *= exp_term(m - g);
+      m = g;
+    }
   }
+  const float sh = m == -__builtin_inff() ? 0.0f : m;
 #pragma unroll
-  for (int i = 0; i < N; ++i) s += v[i] != -__builtin_inff() ? exp_term(v[i] - m) : 0.0f;
+  for (int i = 0; i < N; ++i) s += exp_term(v[i] - sh);
 }
 
 // Merges another lane's (m2, s2) into (m, s): commutative, so a butterfly
