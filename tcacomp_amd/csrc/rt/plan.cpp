@@ -1,6 +1,8 @@
 // plan.cpp — parse, bind and pack a launch plan (format in plan.h).
 #include "plan.h"
 
+#include <limits>
+
 #include <algorithm>
 
 #include <cstring>
@@ -454,11 +456,29 @@ int Bind(const Plan& p, const tca_tensor* tensors, uint32_t n_tensors, const uin
   return TCA_OK;
 }
 
-size_t TensorBytes(const Plan& p, size_t tensor, const std::vector<uint32_t>& dims) {
-  const Tensor& t = p.tensors[tensor];
-  size_t n = DtypeBytes(t.dtype);
-  for (int d : t.dims) n *= dims[d];
-  return n;
+bool WorkspaceLayout(const Plan& p, const std::vector<uint32_t>& dims, const std::vector<bool>& used,
+                     std::vector<size_t>* off, size_t* total, std::string* err) {
+  constexpr size_t kMax = std::numeric_limits<size_t>::max();
+  off->assign(p.tensors.size(), 0);
+  *total = 0;
+  for (size_t t = 0; t < p.tensors.size(); ++t) {
+    if (p.tensors[t].role != Role::Local || !used[t]) continue;
+    size_t n = DtypeBytes(p.tensors[t].dtype);
+    for (int d : p.tensors[t].dims) {
+      if (dims[d] != 0 && n > kMax / dims[d]) {
+        *err = "program " + p.name + ": local " + p.tensors[t].name + " exceeds the address space at these dims";
+        return false;
+      }
+      n *= dims[d];
+    }
+    if (n > kMax - 255u || *total > kMax - ((n + 255u) & ~static_cast<size_t>(255u))) {
+      *err = "program " + p.name + ": workspace exceeds the address space at these dims";
+      return false;
+    }
+    (*off)[t] = *total;
+    *total += (n + 255u) & ~static_cast<size_t>(255u);
+  }
+  return true;
 }
 
 bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims, uint64_t* grid, std::string* err) {

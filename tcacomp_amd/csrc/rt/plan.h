@@ -141,7 +141,11 @@ std::string Serialize(const Plan& p);
 int Bind(const Plan& p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,
          uint32_t n_free_dims, std::vector<uint32_t>* dims, std::string* err);
 
-size_t TensorBytes(const Plan& p, size_t tensor, const std::vector<uint32_t>& dims);
+// The workspace at bound dims: every local that `used` marks at a 256-byte
+// aligned offset, in declaration order (`off` per plan tensor, `total` the
+// bytes). False, with `err` set, when a size does not fit in size_t.
+bool WorkspaceLayout(const Plan& p, const std::vector<uint32_t>& dims, const std::vector<bool>& used,
+                     std::vector<size_t>* off, size_t* total, std::string* err);
 bool GridSize(const Kernel& k, const Plan& p, const std::vector<uint32_t>& dims, uint64_t* grid, std::string* err);
 // Rows per block of a packed kernel (1 otherwise); *block receives the
 // launch block size.

@@ -450,7 +450,9 @@ void fill_args(unsigned char* blob, const std::vector<tca::plan::ArgSlot>& slots
   for (const auto& sl : slots) {
     if (sl.kind == tca::plan::ArgKind::Ptr) {
       const int pi = param_of[sl.index];
-      void* ptr = pi >= 0 ? tensors[pi].data : static_cast<char*>(ws) + local_off[sl.index];
+      // integer arithmetic: the host-only query lays locals out from address 0
+      void* ptr = pi >= 0 ? tensors[pi].data
+                          : reinterpret_cast<void*>(reinterpret_cast<uintptr_t>(ws) + local_off[sl.index]);
       std::memcpy(blob + sl.offset, &ptr, sizeof ptr);
     } else {
       tca::plan::SetScalar(blob, sl, scalars[sl.index]);
@@ -494,18 +496,12 @@ int prepare_launch(tca_program p, const tca_tensor* tensors, uint32_t n_tensors,
     for (const auto& a : k.args)
       if (a.kind == tca::plan::ArgKind::Ptr) used[a.index] = true;
   }
-  pr->local_off.assign(pl.tensors.size(), 0);
+  if (!tca::plan::WorkspaceLayout(pl, dims, used, &pr->local_off, &pr->ws_bytes, &err))
+    return fail(TCA_ERR_INVALID, "%s", err.c_str());
   pr->param_of.assign(pl.tensors.size(), -1);
   int next_param = 0;
-  for (size_t t = 0; t < pl.tensors.size(); ++t) {
-    if (pl.tensors[t].role != tca::plan::Role::Local) {
-      pr->param_of[t] = next_param++;
-      continue;
-    }
-    if (!used[t]) continue;
-    pr->local_off[t] = pr->ws_bytes;
-    pr->ws_bytes += (tca::plan::TensorBytes(pl, t, dims) + 255u) & ~static_cast<size_t>(255u);
-  }
+  for (size_t t = 0; t < pl.tensors.size(); ++t)
+    if (pl.tensors[t].role != tca::plan::Role::Local) pr->param_of[t] = next_param++;
 
   DeviceLimits l;
   int rc = query_limits(&l);
@@ -678,18 +674,14 @@ int tca_program_kernel_args(tca_program p, const tca_tensor* tensors, uint32_t n
     for (const auto& a : kk.args)
       if (a.kind == tca::plan::ArgKind::Ptr) used[a.index] = true;
   }
-  std::vector<size_t> local_off(pl.tensors.size(), 0);
+  std::vector<size_t> local_off;
   std::vector<int> param_of(pl.tensors.size(), -1);
   size_t ws_bytes = 0;
+  if (!tca::plan::WorkspaceLayout(pl, dims, used, &local_off, &ws_bytes, &err))
+    return fail(TCA_ERR_INVALID, "%s", err.c_str());
   int next_param = 0;
-  for (size_t t = 0; t < pl.tensors.size(); ++t) {
-    if (pl.tensors[t].role != tca::plan::Role::Local) {
-      param_of[t] = next_param++;
-    } else if (used[t]) {
-      local_off[t] = ws_bytes;
-      ws_bytes += (tca::plan::TensorBytes(pl, t, dims) + 255u) & ~static_cast<size_t>(255u);
-    }
-  }
+  for (size_t t = 0; t < pl.tensors.size(); ++t)
+    if (pl.tensors[t].role != tca::plan::Role::Local) param_of[t] = next_param++;
   std::vector<unsigned char> blob;
   std::vector<tca::plan::ArgSlot> slots;
   if (!tca::plan::LayoutArgs(k, pl, dims, &blob, &slots, &err)) return fail(TCA_ERR_INVALID, "%s", err.c_str());

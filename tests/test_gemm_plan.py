@@ -6,6 +6,7 @@ library (tca_program_plan_text) parses to the same plan: same text again,
 same selection at every shape, product guards and pow2 flags included.
 tests/test_gpu_gemm_small.py runs the kernels."""
 import ctypes
+import struct
 
 import pytest
 
@@ -180,3 +181,26 @@ def test_plan_fuzz_findings(text, msg):
     h = ctypes.c_void_p()
     assert _lib.lib().tca_program_parse(text.encode(), ctypes.byref(h)) != 0
     assert msg in _lib.last_error(), _lib.last_error()
+
+
+def test_workspace_overflow_is_an_error():
+    """A local whose bytes at the bound dims do not fit in size_t (free dims
+    chosen by the caller) fails the launch contract instead of wrapping the
+    workspace size (a fuzz finding: the layout of tca_program_kernel_args and
+    of a launch overflowed, and the query added the wrapped offset to a null
+    workspace base)."""
+    text = ("tca-plan 1\nprogram ovf\ndim A 0\ndim Bd 0\ndim Cd 0\ntensor x f32 in 1 A\n"
+            "tensor w f32 local 3 A Bd Cd\nkernel k 64 0 1 A/64\narg ptr x\narg ptr w\nend\n")
+    h = _parse(text)
+    arr = compiler._descriptors([compiler.TensorDesc(0x1000, (1024,), 0)])
+    buf = (ctypes.c_ubyte * 64)()
+    size = ctypes.c_size_t()
+    for fd, ok in (((1 << 31, 1 << 31), False), ((1 << 20, 1 << 12), True)):
+        free = (ctypes.c_uint32 * 2)(*fd)
+        rc = _lib.lib().tca_program_kernel_args(h, arr, 1, free, 2, None, 0, 0, buf, 64, ctypes.byref(size))
+        if ok:
+            assert rc == 0, _lib.last_error()
+            assert struct.unpack_from("<Q", bytes(buf), 8)[0] == 0  # the only local, at workspace offset 0
+        else:
+            assert rc != 0 and "exceeds the address space" in _lib.last_error(), _lib.last_error()
+    _lib.lib().tca_program_unload(h)
