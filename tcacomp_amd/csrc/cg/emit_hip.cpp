@@ -3293,10 +3293,20 @@ class Emitter {
     const std::string sig = Signature(n, &pk);
     const std::string sym = pk.symbol;
     std::ostringstream& o = src_;
+    // The chains of each pass.
+    std::vector<std::vector<int>> passChains(geo.passes);
+    for (size_t i = 0; i < n.chains.size(); ++i) passChains[geo.pass[i]].push_back(n.chains[i]);
+    // A mean and its centred sum of squares: one read (ChanMeanVar).
+    const bool chan = opts_.allow_pass_fusion && geo.passes == 2 && passChains[0].size() == 1 &&
+                      passChains[1].size() == 1 &&
+                      ChanMeanVar(g_, g_.chains[passChains[0][0]], g_.chains[passChains[1][0]], geo);
+    // Vectors are 16 bytes of the widest tile or column vector a kernel
+    // loads (the one-read kernels never load the nest's own results).
     size_t widest = 1;
     for (int ci : n.chains)
       for (const auto& op : g_.chains[ci].root.ops) {
         const ColKind k = ClassifyCol(op, geo);
+        if (chan && k == ColKind::ColVec && op.tensor == g_.chains[passChains[0][0]].store_tensor) continue;
         if (k == ColKind::Tile || k == ColKind::ColVec)
           widest = std::max(widest, ir::ElemBytes(g_.tensors[op.tensor].elem));
       }
@@ -3314,15 +3324,9 @@ class Emitter {
       partSig += ",\n    " + CType(pe) + "* __restrict__ p" + std::to_string(ci) + " /* " + nm + " */";
       partArgs += ", p" + std::to_string(ci);
     }
-    // The chains of each pass, and the results of the nest a later pass reads.
-    std::vector<std::vector<int>> passChains(geo.passes);
-    for (size_t i = 0; i < n.chains.size(); ++i) passChains[geo.pass[i]].push_back(n.chains[i]);
+    // The results of the nest a later pass reads.
     std::set<int> results, readLater;
     for (int ci : n.chains) results.insert(g_.chains[ci].store_tensor);
-    // A mean and its centred sum of squares: one read (ChanMeanVar).
-    const bool chan = opts_.allow_pass_fusion && geo.passes == 2 && passChains[0].size() == 1 &&
-                      passChains[1].size() == 1 &&
-                      ChanMeanVar(g_, g_.chains[passChains[0][0]], g_.chains[passChains[1][0]], geo);
     // Operands by kind (root and piped maps) over a set of chains, each
     // loaded once per kind.
     struct Ops {

@@ -271,6 +271,28 @@ def col_mean_bf16():
     return b.Build()
 
 
+def col_mean_var_bf16():
+    """Per-column mean and centred variance of bf16 x [B, R, C] over R, in
+    f32: mean = sum_r f32(x) * inv_n, var = sum_r (f32(x) - mean)^2 *
+    inv_n (16-byte vectors of 8 bf16 columns; the one-read column lowering
+    with a cast in the mean's body)."""
+    b = NewBuilder("col_mean_var_bf16")
+    B, R, C = b.Dim("B", 0), b.Dim("R", 0), b.Dim("C", 0)
+    x = b.Tensor("x", TBF16, B, R, C)
+    mean = b.Tensor("mean", TF32, B, C)
+    var = b.Tensor("var", TF32, B, C)
+    inv_n = b.ScalarParam("inv_n", TF32)
+    (b.Stmt().Iter(B, R, C).Map([At(x, B, R, C)], lambda v: Cast(v, TF32)).As(B, C, R)
+     .Reduce(b.Float32(0), _sum(b))
+     .Map([], lambda v: b.Mul(v, inv_n)).As(B, C).Store(mean, B, C))
+    (b.Stmt().Iter(B, R, C)
+     .Map([At(x, B, R, C), At(mean, B, C)],
+          lambda l, m: b.Mul(b.Sub(Cast(l, TF32), m), b.Sub(Cast(l, TF32), m))).As(B, C, R)
+     .Reduce(b.Float32(0), _sum(b))
+     .Map([], lambda v: b.Mul(v, inv_n)).As(B, C).Store(var, B, C))
+    return b.Build()
+
+
 def col_sum_u8():
     """Column sums of bytes u8 x [R, C] into u32 (16-element vectors)."""
     b = NewBuilder("col_sum_u8")
@@ -748,6 +770,7 @@ CONFIG_PROGRAMS = {
     "col_mean_bf16": col_mean_bf16,
     "col_mean_var_dyn": col_mean_var,
     "col_mean_var_l_dyn": lambda: col_mean_var(True),
+    "col_mean_var_bf16": col_mean_var_bf16,
     "col_sum_u8": col_sum_u8,
     "scale_relu": scale_relu,
     "scale_relu_map": scale_relu_map,
@@ -825,7 +848,7 @@ def all_builds():
 
 # Programs whose passes fuse into one read by default (online softmax
 # normaliser, pairwise mean/variance); the tests also run them unfused.
-PASS_FUSED = ("softmax_dyn", "col_mean_var_dyn", "col_mean_var_l_dyn")
+PASS_FUSED = ("softmax_dyn", "col_mean_var_dyn", "col_mean_var_l_dyn", "col_mean_var_bf16")
 
 
 # Contractions the tests also run with EMIT_NO_GEMM_SPLIT (the 128/256 tile

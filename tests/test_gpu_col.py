@@ -133,6 +133,32 @@ def test_col_mean_var(gpu, name, B, R, C, flags):
 
 
 @FUSED
+@pytest.mark.parametrize("B,R,C", [(1, 0, 16), (1, 1, 8), (2, 37, 24), (3, 64, 1000), (1, 1000, 4096), (2, 3000, 72),
+                                   (1, 65536, 256), (1, 100, 140000), (1, 500, 1004), (1, 700, 1002), (2, 300, 1001)])
+def test_col_mean_var_bf16(gpu, B, R, C, flags):
+    """bf16 columns (16-byte vectors of 8, or 4 / 2 / 1 at other widths),
+    small integers exact in bf16: the mean bit for bit, the variance within
+    its lowering's bound."""
+    import torch
+    print("col_mean_var_bf16", B, R, C, flags, flush=True)
+    sys.stdout.flush()
+    x = _ints((B, R, C), 8, B * 17 + R * 5 + C)
+    inv_n = np.float32(1.0 / max(R, 1))
+    mean = to_dev(np.full((B, C), CANARY, np.float32), gpu)
+    var = to_dev(np.full((B, C), CANARY, np.float32), gpu)
+    xd = torch.from_numpy(x).to(gpu).to(torch.bfloat16)
+    run(compiled("col_mean_var_bf16", flags), [xd, mean, var], scalars=[float(inv_n)])
+    want_mean = x.astype(np.float64).sum(axis=1).astype(np.float32) * inv_n
+    np.testing.assert_array_equal(mean.cpu().numpy(), want_mean)
+    if flags:
+        want, bound = _passes_bound(x, want_mean, inv_n)
+    else:
+        want, bound = fused_var_bound(x, want_mean, inv_n)
+    err = np.abs(var.cpu().numpy().astype(np.float64) - want)
+    assert np.all(err <= bound), (B, R, C, float(err.max()), float(bound[err > bound].min(initial=0)))
+
+
+@FUSED
 @pytest.mark.parametrize("kind", ["offset", "drift"])
 @pytest.mark.parametrize("B,R,C", [(1, 5000, 1000), (2, 300, 4100), (1, 100000, 48), (1, 64, 4096), (3, 7, 33)])
 def test_col_mean_var_float(gpu, kind, B, R, C, flags):
