@@ -2,8 +2,9 @@
 tca_program_launch, through the C ABI.
 
 Each case uses a kernel family with a scratch workspace: split-row partials,
-column-reduction partials, HBM-resident locals (the generic lowering) and a
-chained reduction's local. Two calls in a row, the second with a smaller
+column-reduction partials, HBM-resident locals (the generic lowering), a
+chained reduction's local, split softmax rows and the one-read column mean
+and variance. Two calls in a row, the second with a smaller
 input, each compared bit for bit with the allocating launch of the same
 program on the same inputs (the same kernels run on the same data, so the
 outputs are identical). A workspace beyond the 32 MiB scratch is refused
@@ -28,6 +29,10 @@ CASES = [
     ("col_sum_max_dyn", 0, [(8192, 1024), (300, 512)], lambda R, C: [(C,), (C,)], ()),
     ("softmax_200", GENERIC, [(257, 200), (5, 200)], lambda R, C: [(R, C)], ()),
     ("chain_sum_max", 0, [(6, 40, 96), (3, 17, 96)], None, (-0.5,)),
+    # split softmax rows (online max/exp-sum partials, plan-only row locals)
+    ("softmax_dyn", 0, [(4, 1_000_000), (2, 300_000)], lambda R, C: [(R, C)], ()),
+    # one-read column mean + variance (sum and centred-square partials)
+    ("col_mean_var_dyn", 0, [(2, 8192, 1024), (1, 700, 512)], lambda B, R, C: [(B, C), (B, C)], (1.0 / 8192,)),
 ]
 
 
