@@ -2889,7 +2889,6 @@ class Emitter {
         o << "template <uint32_t V>\n__device__ __forceinline__ void " << fn << "(\n    " << sig << smSig << ") {\n";
         chunkHead(kOnlineChunkVecs);
         loadRowScalars(p, "  ");
-        combsOf(p, "  ");
         // The running maximum om is chain A's partial too: a fold of the
         // same values with fmaxf from -inf, which A's init is.
         o << "  float om = -__builtin_inff(), os = 0.0f;\n";
