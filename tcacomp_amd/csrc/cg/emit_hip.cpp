@@ -3487,24 +3487,27 @@ class Emitter {
     // rows past the chunk to its last row (unconditional loads stay in
     // flight together) and fold only the rows they own; row 0 of each is
     // always owned. Declares `has` (the thread's slot holds a row).
-    auto rowLoop = [&](const std::vector<int>& cs, const Ops& k, const std::string& hasName) {
-      std::ostringstream b;
-      auto group = [&](const std::string& ind, uint32_t rows, bool clamped, bool first) {
-        for (uint32_t u = 0; u < rows; ++u) {
-          const std::string us = std::to_string(u);
-          if (clamped && u > 0) {
-            b << ind << "const bool ok_" << us << " = r + " << us << "u * STEP < r_hi;\n";
-            b << ind << "const uint32_t rr_" << us << " = ok_" << us << " ? r + " << us << "u * STEP : r_hi - 1u;\n";
-            loads(b, k, ind, "rr_" + us, "_" + us);
-          } else {
-            loads(b, k, ind, "r + " + us + "u * STEP", "_" + us);
-          }
+    // The loads of one group of `rows` rows from row r into x<t>_u / rv<t>_u;
+    // `clamped` groups also declare ok_u (row u is the chunk's) and read a
+    // row past the chunk as its last row.
+    auto groupLoads = [&](std::ostringstream& b, const Ops& k, const std::string& ind, uint32_t rows, bool clamped) {
+      for (uint32_t u = 0; u < rows; ++u) {
+        const std::string us = std::to_string(u);
+        if (clamped && u > 0) {
+          b << ind << "const bool ok_" << us << " = r + " << us << "u * STEP < r_hi;\n";
+          b << ind << "const uint32_t rr_" << us << " = ok_" << us << " ? r + " << us << "u * STEP : r_hi - 1u;\n";
+          loads(b, k, ind, "rr_" + us, "_" + us);
+        } else {
+          loads(b, k, ind, "r + " + us + "u * STEP", "_" + us);
         }
-        for (uint32_t u = 0; u < rows; ++u)
-          fold(b, cs, ind, "_" + std::to_string(u), first && u == 0, clamped && u > 0 ? "ok_" + std::to_string(u) : "");
-      };
-      b << "  uint32_t r = r_lo + slot;\n  const bool " << hasName << " = r < r_hi;\n  if (" << hasName
-        << ") {\n";
+      }
+    };
+    // The skeleton of a block's row loop, `group(ind, rows, clamped, first)`
+    // emitting each group: declares `has` (the thread's slot holds a row)
+    // and walks r over the slot's rows.
+    auto rowSkeleton = [&](std::ostringstream& b, const std::string& hasName,
+                           const std::function<void(const std::string&, uint32_t, bool, bool)>& group) {
+      b << "  uint32_t r = r_lo + slot;\n  const bool " << hasName << " = r < r_hi;\n  if (" << hasName << ") {\n";
       // A first group of 16 when every slot of the block owns >= 16 rows
       // (block-uniform), else of 4 (clamped).
       b << "    if (r_hi - r_lo >= " << kUnroll << "u * STEP) {\n";
@@ -3517,6 +3520,14 @@ class Emitter {
       b << "    }\n    for (; r < r_hi; r += " << kEdge << "u * STEP) {\n";
       group("      ", kEdge, true, false);
       b << "    }\n  }\n";
+    };
+    auto rowLoop = [&](const std::vector<int>& cs, const Ops& k, const std::string& hasName) {
+      std::ostringstream b;
+      rowSkeleton(b, hasName, [&](const std::string& ind, uint32_t rows, bool clamped, bool first) {
+        groupLoads(b, k, ind, rows, clamped);
+        for (uint32_t u = 0; u < rows; ++u)
+          fold(b, cs, ind, "_" + std::to_string(u), first && u == 0, clamped && u > 0 ? "ok_" + std::to_string(u) : "");
+      });
       return b.str();
     };
     auto partDecls = [&](const std::vector<int>& cs) {
@@ -3756,16 +3767,7 @@ class Emitter {
       const ir::Chain& A = g_.chains[chA];
       const std::string SA = "part" + std::to_string(chA);
       auto group = [&](const std::string& ind, uint32_t rows, bool clamped, bool first) {
-        for (uint32_t u = 0; u < rows; ++u) {
-          const std::string us = std::to_string(u);
-          if (clamped && u > 0) {
-            b << ind << "const bool ok_" << us << " = r + " << us << "u * STEP < r_hi;\n";
-            b << ind << "const uint32_t rr_" << us << " = ok_" << us << " ? r + " << us << "u * STEP : r_hi - 1u;\n";
-            loads(b, k, ind, "rr_" + us, "_" + us);
-          } else {
-            loads(b, k, ind, "r + " + us + "u * STEP", "_" + us);
-          }
-        }
+        groupLoads(b, k, ind, rows, clamped);
         if (clamped) {
           b << ind << "const float nu = 1.0f";
           for (uint32_t u = 1; u < rows; ++u) b << " + (ok_" << u << " ? 1.0f : 0.0f)";
@@ -3819,18 +3821,9 @@ class Emitter {
         }
         b << ind << "}\n" << ind << "cn += nu;\n";
       };
-      b << "  uint32_t r = r_lo + slot;\n  const bool has = r < r_hi;\n  float cn = 0.0f;  // rows this thread folded\n";
-      b << "  if (has) {\n";
-      b << "    if (r_hi - r_lo >= " << kUnroll << "u * STEP) {  // every slot owns >= 16 rows\n";
-      group("      ", kUnroll, false, true);
-      b << "      r += " << kUnroll << "u * STEP;\n    } else {\n";
-      group("      ", kEdge, true, true);
-      b << "      r += " << kEdge << "u * STEP;\n    }\n";
-      b << "    for (; r + " << kUnroll - 1 << "u * STEP < r_hi; r += " << kUnroll << "u * STEP) {\n";
-      group("      ", kUnroll, false, false);
-      b << "    }\n    for (; r < r_hi; r += " << kEdge << "u * STEP) {\n";
-      group("      ", kEdge, true, false);
-      b << "    }\n  }\n  (void)cn;\n";
+      b << "  float cn = 0.0f;  // rows this thread folded\n";
+      rowSkeleton(b, "has", group);
+      b << "  (void)cn;\n";
       return b.str();
     };
     // The finish of a fused pair from (S, M2, n) in acc<A>, m2a, na.
