@@ -24,6 +24,7 @@
 #include <map>
 #include <set>
 #include <sstream>
+#include <tuple>
 
 #include "gemm_emit.h"
 
@@ -844,18 +845,19 @@ ColGeom ColCheck(const Graph& g, const std::vector<int>& chains) {
 }
 
 // A mean and a centred sum of squares over the reduced axis, fusable into
-// one read of the tile (Chan, Golub & LeVeque, "Updating formulae and a
-// pairwise algorithm for computing sample variances", 1979): chain A folds
-// t with + from 0 (f32) into m (its result after init and piped map, an f32
-// column vector), and chain B folds (t - m) * (t - m) with + from 0 (f32),
-// where m is read at B's own column and t is A's root body. For rows split
-// into groups g of n_g rows with sums S_g and M2_g = sum over g of
-// (t - S_g / n_g)^2,
+// one read of the input (Chan, Golub & LeVeque, "Updating formulae and a
+// pairwise algorithm for computing sample variances", 1979): chain A folds t
+// with + from 0 (f32) into m (its result after init and piped map, f32), and
+// chain B folds (t - m) * (t - m) with + from 0 (f32), where m is read at
+// B's own output index (`atOwnIndex` says whether an operand of B is that
+// read) and t is A's root body. For rows split into groups g of n_g rows with
+// sums S_g and M2_g = sum over g of (t - S_g / n_g)^2,
 //   sum over the rows of (t - m)^2 = M2 + n (S / n - m)^2,
 //   M2 of a union a + b = M2_a + M2_b + (S_b / n_b - S_a / n_a)^2 n_a n_b / (n_a + n_b),
 // exactly in real arithmetic and every term non-negative, so no
 // cancellation. B's piped map is applied to that sum as usual.
-bool ChanMeanVar(const ir::Graph& g, const ir::Chain& A, const ir::Chain& B, const ColGeom& geo) {
+bool MeanSquaresPair(const ir::Graph& g, const ir::Chain& A, const ir::Chain& B,
+                     const std::function<bool(const ir::Operand&)>& atOwnIndex) {
   if (A.reduces.size() != 1 || B.reduces.size() != 1) return false;
   if (g.exprs[A.root.fn.body].type != ir::Elem::F32 || g.exprs[B.root.fn.body].type != ir::Elem::F32) return false;
   if (g.tensors[A.store_tensor].elem != ir::Elem::F32) return false;
@@ -877,13 +879,25 @@ bool ChanMeanVar(const ir::Graph& g, const ir::Chain& A, const ir::Chain& B, con
   for (size_t k = 0; k < B.root.fn.params.size(); ++k) {
     if (B.root.fn.params[k] != d.args[1]) continue;
     const ir::Operand& op = B.root.ops[k];
-    if (op.tensor != A.store_tensor || op.axes != A.store_axes || ClassifyCol(op, geo) != ColKind::ColVec) return false;
-    if (B.has_piped)
-      for (const auto& po : B.piped.ops)
-        if (po.tensor == A.store_tensor) return false;
+    if (op.tensor != A.store_tensor || op.axes != A.store_axes || !atOwnIndex(op)) return false;
     return SameRowExpr(g, A.root.fn.body, A, d.args[0], B);
   }
   return false;
+}
+
+// The column family's form: m read as a column vector at B's own column, and
+// B's piped map reading no result of the nest (the one-read kernels never
+// load the mean from memory).
+bool ChanMeanVar(const ir::Graph& g, const ir::Chain& A, const ir::Chain& B, const ColGeom& geo) {
+  if (B.has_piped)
+    for (const auto& po : B.piped.ops)
+      if (po.tensor == A.store_tensor) return false;
+  return MeanSquaresPair(g, A, B, [&](const ir::Operand& op) { return ClassifyCol(op, geo) == ColKind::ColVec; });
+}
+
+// The streaming row family's form: m read as a row scalar at B's own row.
+bool ChanRowMeanVar(const ir::Graph& g, const ir::Chain& A, const ir::Chain& B, const RowGeom& geo) {
+  return MeanSquaresPair(g, A, B, [&](const ir::Operand& op) { return Classify(op, geo) == OpKind::RowScalar; });
 }
 
 // ---- elementwise family check --------------------------------------------
@@ -2668,19 +2682,26 @@ class Emitter {
     for (int t : tiles)
       if (produced.count(t)) splitMulti = false;
     // Softmax's max and exp-sum passes, fused into one pass over the row's
-    // chunks with the online normaliser: onlinePair[p] for the first pass of
-    // such a pair (pass p + 1 then has no kernels of its own); the chunk
-    // maxima the sums were taken against go to a partial of their own.
+    // chunks with the online normaliser, and a mean with its centred sum of
+    // squares (layernorm's), fused with the pairwise update (chanPair):
+    // onlinePair[p] for the first pass of such a pair (pass p + 1 then has
+    // no kernels of its own); the chunk maxima the softmax sums were taken
+    // against go to a partial of their own.
     std::vector<bool> onlinePair(passes.size(), false);
-    std::set<int> onlineSum;  // chain B of each fused pair
+    std::vector<bool> chanPair(passes.size(), false);  // of those, a mean and its centred sum of squares
+    std::set<int> onlineSum;  // chain B of each fused softmax pair
     if (splitMulti && opts_.allow_pass_fusion)
-      for (size_t p = 0; p + 1 < passes.size(); ++p)
-        if (passes[p].size() == 1 && passes[p + 1].size() == 1 &&
-            OnlineMaxExpSum(g_, g_.chains[passes[p][0]], g_.chains[passes[p + 1][0]], geo) &&
-            (p == 0 || !onlinePair[p - 1])) {
+      for (size_t p = 0; p + 1 < passes.size(); ++p) {
+        if (passes[p].size() != 1 || passes[p + 1].size() != 1 || (p > 0 && onlinePair[p - 1])) continue;
+        const ir::Chain& A = g_.chains[passes[p][0]];
+        const ir::Chain& B = g_.chains[passes[p + 1][0]];
+        if (OnlineMaxExpSum(g_, A, B, geo)) {
           onlinePair[p] = true;
           onlineSum.insert(passes[p + 1][0]);
+        } else if (ChanRowMeanVar(g_, A, B, geo)) {
+          onlinePair[p] = chanPair[p] = true;
         }
+      }
     // A fused pair followed by the nest's last pass, a row map (softmax's
     // normalisation): each row-map workgroup computes the pair's two values
     // for its row from the partials (at most 512 pairs, read from the L2)
@@ -2695,6 +2716,15 @@ class Emitter {
     std::vector<std::pair<std::string, size_t>> smFns;  // (device function, pass)
     // Vectors per chunk of a split kernel whose chunks are not kChunkVecs.
     std::map<std::string, uint32_t> smChunk;
+    // Row maps with a pair's merge folded in whose chunk length is a template
+    // argument: kChunkVecs below kLongMapVecs vectors a row, 4x from there
+    // (one wave's merge per kernel block is then spread over 4x the
+    // vectors). Layernorm over [8, 4 Mi]: 93 -> 79 us, [64, 1 Mi]: 137 ->
+    // 131 us; rows of 16 Ki vectors keep 4 chunks (17 us, not 19, at 32
+    // rows). Softmax's map measured no better with longer chunks at
+    // [64, 1 Mi] and keeps kChunkVecs.
+    std::set<std::string> longMaps;
+    constexpr uint32_t kLongMapVecs = 16 * kChunkVecs;
     // The fused softmax passes take chunks 4x as long (16 vectors per lane):
     // with 4 a lane, the many short workgroups spent a quarter of their time
     // in the block's tail (the pair merges, the partials' stores); 8x (32 a
@@ -2782,8 +2812,8 @@ class Emitter {
           o << ind << "  return " << r << ";\n" << ind << "};\n";
         }
       };
-      auto chunkHead = [&](uint32_t cv) {
-        o << "  constexpr uint32_t CV = " << cv << "u, PMAX = " << kMaxParts << "u;\n";
+      auto chunkHead = [&](const std::string& cv) {
+        o << "  constexpr uint32_t CV = " << cv << ", PMAX = " << kMaxParts << "u;\n";
         o << "  const uint32_t C = " << ExtentExpr(g_, geo.col) << ";\n";
         o << "  const uint32_t VECS = C / V;\n";
         o << "  const uint32_t P = min(PMAX, tca::hip::ceil_div(VECS, CV));  // VECS >= 1 (launch guard)\n";
@@ -2795,17 +2825,108 @@ class Emitter {
         o << "  const bool active = true;\n";
         for (int a : geo.outer) o << "  const uint32_t c" << a << " = r;\n";
       };
-      // The values the fused pair (passes p, p + 1) stores for row r, in every
-      // lane of each wave that runs this: aval, A's result (its partial
-      // maxima folded, init applied), and bval, B's (the chunk pairs summed
-      // as s_c * expf(m_c - aval), NaN when aval is -inf, then init and piped
-      // map). Needs r, lane and C in scope; names are prefixed so the code can
-      // sit in the row map that reads the two values.
-      auto pairValues = [&](size_t p, const std::string& ind) {
+      // B's result from its reduced total `total` (its init and piped map,
+      // A's result bound to aval), declared as bval.
+      auto pairFinishB = [&](size_t p, const std::string& ind, const std::string& total) {
+        const ir::Chain& A = g_.chains[passes[p][0]];
+        const ir::Chain& B = g_.chains[passes[p + 1][0]];
+        const int ta = A.store_tensor;
+        // Row scalars B's piped map reads besides A's result.
+        std::map<int, std::string> piped;
+        if (B.has_piped)
+          for (const auto& op : B.piped.ops) {
+            if (op.tensor == ta || piped.count(op.tensor)) continue;
+            piped[op.tensor] = "prs" + std::to_string(op.tensor);
+            o << ind << "const " << CType(g_.tensors[op.tensor].elem) << " prs" << op.tensor << " = t" << op.tensor
+              << "[" << Offset(op.tensor, op.axes, coord) << "];\n";
+          }
+        const ir::ReduceStage& rs = B.reduces[0];
+        ExprGen fg(g_, o, ind, &counter_);
+        fg.Bind(rs.fn.params[0], fg.Gen(rs.init));
+        fg.Bind(rs.fn.params[1], total);
+        std::string val = fg.Gen(rs.fn.body);
+        if (B.has_piped) {
+          ExprGen pg(g_, o, ind, &counter_);
+          pg.Bind(B.piped.fn.params[0], val);
+          for (size_t k = 0; k < B.piped.ops.size(); ++k) {
+            const int t = B.piped.ops[k].tensor;
+            pg.Bind(B.piped.fn.params[k + 1], t == ta ? std::string("aval") : piped[t]);
+          }
+          val = pg.Gen(B.piped.fn.body);
+        }
+        o << ind << "const " << CType(g_.tensors[B.store_tensor].elem) << " bval = " << val << ";\n";
+      };
+      // pairValues for a mean and its centred sum of squares, from the chunks'
+      // sums S_c and sums of squares about their own means M2_c (n_c values
+      // each, from the chunk bounds): aval = A's init, sum of S_c and piped
+      // map; B's total = sum over c of M2_c + n_c (S_c / n_c - aval)^2, the
+      // sum of squares about aval (each chunk's, exactly, by the parallel
+      // axis theorem). Two butterflies of plain sums: every lane holds the
+      // same values.
+      auto chanPairValues = [&](size_t p, const std::string& ind) {
         const int ca = passes[p][0], cb = passes[p + 1][0];
         const ir::Chain& A = g_.chains[ca];
-        const ir::Chain& B = g_.chains[cb];
-        const int ta = A.store_tensor;
+        const std::string sa = std::to_string(ca), sb = std::to_string(cb);
+        const uint32_t K = kMaxParts / 64;
+        o << ind << "const uint32_t PF = min(" << kMaxParts << "u, tca::hip::ceil_div(C / V, " << kOnlineChunkVecs
+          << "u));  // the fused partial's chunks\n";
+        o << ind << "const uint32_t PVECS = C / V, PL = tca::hip::ceil_div(PVECS, PF);\n";
+        o << ind << "float sv[" << K << "], mv[" << K << "];\n#pragma unroll\n" << ind << "for (uint32_t k = 0; k < " << K
+          << "u; ++k) {\n" << ind << "  const uint64_t at = static_cast<uint64_t>(r) * " << kMaxParts
+          << "u + min((threadIdx.x & 63u) + 64u * k, PF - 1u);\n" << ind << "  sv[k] = p" << sa << "[at];\n" << ind
+          << "  mv[k] = p" << sb << "[at];\n" << ind << "}\n";
+        // Every loaded value is consumed on every path (selects, not
+        // branches): a load left pending on a skipped branch made the
+        // compiler wait for all memory operations (vmcnt(0)) at the head of
+        // the row map's loop, stores included, every iteration.
+        o << ind << "float ps = 0.0f;\n#pragma unroll\n" << ind << "for (uint32_t k = 0; k < " << K << "u; ++k)\n"
+          << ind << "  ps += (threadIdx.x & 63u) + 64u * k < PF ? sv[k] : 0.0f;\n";
+        o << ind << "for (int off = 32; off > 0; off >>= 1) ps += __shfl_xor(ps, off, 64);\n";
+        {
+          const ir::ReduceStage& rs = A.reduces[0];
+          ExprGen fg(g_, o, ind, &counter_);
+          fg.Bind(rs.fn.params[0], fg.Gen(rs.init));
+          fg.Bind(rs.fn.params[1], "ps");
+          std::string val = fg.Gen(rs.fn.body);
+          if (A.has_piped) {
+            std::map<int, std::string> piped;
+            for (const auto& op : A.piped.ops) {
+              if (piped.count(op.tensor)) continue;
+              piped[op.tensor] = "ars" + std::to_string(op.tensor);
+              o << ind << "const " << CType(g_.tensors[op.tensor].elem) << " ars" << op.tensor << " = t" << op.tensor
+                << "[" << Offset(op.tensor, op.axes, coord) << "];\n";
+            }
+            ExprGen pg(g_, o, ind, &counter_);
+            pg.Bind(A.piped.fn.params[0], val);
+            for (size_t k = 0; k < A.piped.ops.size(); ++k)
+              pg.Bind(A.piped.fn.params[k + 1], piped[A.piped.ops[k].tensor]);
+            val = pg.Gen(A.piped.fn.body);
+          }
+          // Every lane holds the same value (the butterfly's sums are
+          // symmetric): a scalar register, as a row scalar loaded from
+          // memory would be.
+          o << ind << "const float aval = tca::hip::wave_uniform(" << val << ");  // the value A stores and B reads\n";
+        }
+        o << ind << "float ptotal = 0.0f;\n#pragma unroll\n" << ind << "for (uint32_t k = 0; k < " << K << "u; ++k) {\n"
+          << ind << "  const uint32_t c = (threadIdx.x & 63u) + 64u * k, cc = min(c, PF - 1u);  // sv[k], mv[k]: chunk cc\n"
+          << ind << "  const float nc = static_cast<float>(min(PL, PVECS - cc * PL) * V);  // cc PL < PVECS\n" << ind
+          << "  const float dc = sv[k] / nc - aval;\n" << ind << "  ptotal += c < PF ? mv[k] + nc * dc * dc : 0.0f;\n"
+          << ind << "}\n";
+        o << ind << "for (int off = 32; off > 0; off >>= 1) ptotal += __shfl_xor(ptotal, off, 64);  // about aval\n";
+        o << ind << "ptotal = tca::hip::wave_uniform(ptotal);\n";
+        // The chunk terms' selects become branches (a division is costly);
+        // the loads used in them are settled here, not at the head of the
+        // caller's loop.
+        o << ind << "tca::hip::wait_vector_memory();\n";
+        pairFinishB(p, ind, "ptotal");
+      };
+      // pairValues for softmax's pair (max, then the sum of expf(t - max)):
+      // aval, A's result (its partial maxima folded, init applied), and B's
+      // total, the chunk pairs summed as s_c * expf(m_c - aval) (NaN when
+      // aval is -inf).
+      auto onlinePairValues = [&](size_t p, const std::string& ind) {
+        const int ca = passes[p][0], cb = passes[p + 1][0];
+        const ir::Chain& A = g_.chains[ca];
         const std::string sa = std::to_string(ca), sb = std::to_string(cb);
         o << ind << "const uint32_t PF = min(" << kMaxParts << "u, tca::hip::ceil_div(C / V, " << kOnlineChunkVecs
           << "u));  // the fused partial's chunks\n";
@@ -2833,38 +2954,24 @@ class Emitter {
           const std::string val = fg.Gen(rs.fn.body);  // PF >= 1: init applied once to the row's total
           o << ind << "const float aval = " << val << ";  // the value A stores and B reads\n";
         }
-        // Row scalars B's piped map reads besides A's result.
-        std::map<int, std::string> piped;
-        if (B.has_piped)
-          for (const auto& op : B.piped.ops) {
-            if (op.tensor == ta || piped.count(op.tensor)) continue;
-            piped[op.tensor] = "prs" + std::to_string(op.tensor);
-            o << ind << "const " << CType(g_.tensors[op.tensor].elem) << " prs" << op.tensor << " = t" << op.tensor
-              << "[" << Offset(op.tensor, op.axes, coord) << "];\n";
-          }
         o << ind << "float psum = 0.0f;\n#pragma unroll\n" << ind << "for (uint32_t k = 0; k < " << kMaxParts / 64
           << "u; ++k) {\n" << ind << "  const uint32_t c = (threadIdx.x & 63u) + 64u * k;\n" << ind
           << "  if (c < PF)\n" << ind << "    psum += p" << sb << "[static_cast<uint64_t>(r) * " << kMaxParts
           << "u + c] * expf(q" << sb << "[static_cast<uint64_t>(r) * " << kMaxParts << "u + c] - aval);\n" << ind
           << "}\n" << ind << "for (int off = 32; off > 0; off >>= 1) psum += __shfl_xor(psum, off, 64);\n";
         o << ind << "const float ptotal = aval == -__builtin_inff() ? __builtin_nanf(\"\") : psum;\n";
-        {
-          const ir::ReduceStage& rs = B.reduces[0];
-          ExprGen fg(g_, o, ind, &counter_);
-          fg.Bind(rs.fn.params[0], fg.Gen(rs.init));
-          fg.Bind(rs.fn.params[1], "ptotal");
-          std::string val = fg.Gen(rs.fn.body);
-          if (B.has_piped) {
-            ExprGen pg(g_, o, ind, &counter_);
-            pg.Bind(B.piped.fn.params[0], val);
-            for (size_t k = 0; k < B.piped.ops.size(); ++k) {
-              const int t = B.piped.ops[k].tensor;
-              pg.Bind(B.piped.fn.params[k + 1], t == ta ? std::string("aval") : piped[t]);
-            }
-            val = pg.Gen(B.piped.fn.body);
-          }
-          o << ind << "const " << CType(g_.tensors[B.store_tensor].elem) << " bval = " << val << ";\n";
-        }
+        pairFinishB(p, ind, "ptotal");
+      };
+      // The values the fused pair (passes p, p + 1) stores for row r, in every
+      // lane of each wave that runs this: aval, A's result, and bval, B's
+      // (its init and piped map applied). Needs r and C in scope; names are
+      // prefixed so the code can sit in the row map that reads the two
+      // values.
+      auto pairValues = [&](size_t p, const std::string& ind) {
+        if (chanPair[p])
+          chanPairValues(p, ind);
+        else
+          onlinePairValues(p, ind);
       };
       // Passes p (A: max of t) and p + 1 (B: sum of expf(t - a)) of a
       // softmax in one read of each chunk: the partial folds A's maximum as
@@ -2884,14 +2991,23 @@ class Emitter {
         const std::string fn = pk.symbol + "_spart" + tag;
         smFns.push_back({fn, p});
         smChunk[fn] = kOnlineChunkVecs;
+        const bool chanKind = chanPair[p];
         o << "// statements #" << ca << " #" << cb << ": split rows, passes " << p + 1 << " and " << p + 2
-          << " in one read (max, then the online exp-sum against the chunk maxima), partial folds\n";
+          << (chanKind ? " in one read (a sum and the centred sum of squares about it, pairwise), partial folds\n"
+                       : " in one read (max, then the online exp-sum against the chunk maxima), partial folds\n");
         o << "template <uint32_t V>\n__device__ __forceinline__ void " << fn << "(\n    " << sig << smSig << ") {\n";
-        chunkHead(kOnlineChunkVecs);
+        chunkHead(std::to_string(kOnlineChunkVecs) + "u");
         loadRowScalars(p, "  ");
-        // The running maximum om is chain A's partial too: a fold of the
-        // same values with fmaxf from -inf, which A's init is.
-        o << "  float om = -__builtin_inff(), os = 0.0f;\n";
+        // Per lane: softmax's running maximum om (chain A's partial too: a
+        // fold of the same values with fmaxf from -inf, which A's init is)
+        // and sum os; or the values' sum cs (A's partial), centred sum of
+        // squares cm (B's) and count cn.
+        if (chanKind)
+          o << "  float cs = 0.0f, cm = 0.0f, cn = 0.0f;\n";
+        else
+          o << "  float om = -__builtin_inff(), os = 0.0f;\n";
+        const std::string upd = chanKind ? "tca::hip::chan_add(cs, cm, cn, ev);\n"
+                                         : "tca::hip::online_expsum_add(om, os, ev);\n";
         // The values of vector `sfx` into ev[at * V + q].
         auto values = [&](std::ostringstream& b, const std::string& ind, const std::string& sfx, uint32_t at) {
           b << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) {\n";
@@ -2899,47 +3015,67 @@ class Emitter {
           const std::string ev = elemValue(es, ind + "  ", A, sfx);
           b << es.str() << ind << "  ev[" << at << "u * V + q] = " << ev << ";\n" << ind << "}\n";
         };
-        // One online update per kU vectors (kU V values: one rescale test
-        // and at most one rescale per group). 8 vectors in flight per lane
-        // measured 5% slower.
+        // One update per kU vectors (kU V values: for softmax one rescale
+        // test and at most one rescale per group). 8 vectors in flight per
+        // lane measured 5% slower.
         constexpr uint32_t kU = 4;
         std::ostringstream b;
         b << "  {\n    const uint32_t vc = lo + threadIdx.x;\n";
         operands(b, p, "    ", false, "vc", "");
         b << "    float ev[V];\n";
         values(b, "    ", "", 0);
-        b << "    tca::hip::online_expsum_add(om, os, ev);\n";
+        b << "    " << upd;
         b << "  }\n  uint32_t v0 = lo + threadIdx.x + " << kPartBlock << "u;\n";
         b << "  for (; v0 + " << (kU - 1) * kPartBlock << "u < hi; v0 += " << kU * kPartBlock << "u) {\n";
         for (uint32_t u = 0; u < kU; ++u) b << "    const uint32_t vc_" << u << " = v0 + " << u * kPartBlock << "u;\n";
         for (uint32_t u = 0; u < kU; ++u) operands(b, p, "    ", false, "vc_" + std::to_string(u), "_" + std::to_string(u));
         b << "    float ev[" << kU << " * V];\n";
         for (uint32_t u = 0; u < kU; ++u) values(b, "    ", "_" + std::to_string(u), u);
-        b << "    tca::hip::online_expsum_add(om, os, ev);\n";
+        b << "    " << upd;
         b << "  }\n  for (; v0 < hi; v0 += " << kPartBlock << "u) {\n    const uint32_t vc = v0;\n";
         operands(b, p, "    ", false, "vc", "");
         b << "    float ev[V];\n";
         values(b, "    ", "", 0);
-        b << "    tca::hip::online_expsum_add(om, os, ev);\n";
+        b << "    " << upd;
         b << "  }\n";
         o << b.str();
-        o << "  for (int off = 32; off > 0; off >>= 1)\n"
-          << "    tca::hip::online_expsum_merge(om, os, __shfl_xor(om, off, 64), __shfl_xor(os, off, 64));\n";
-        o << "  __shared__ float redm[" << kPartBlock / 64 << "], reds[" << kPartBlock / 64 << "];\n";
-        o << "  if ((threadIdx.x & 63u) == 0u) {\n    redm[threadIdx.x >> 6] = om;\n    reds[threadIdx.x >> 6] = os;\n  }\n";
         // The waves' results meet in lanes 0..15 of wave 0 (a 4-step
         // butterfly: a serial fold by one thread was the tail of every one
         // of the many short workgroups).
         static_assert(kPartBlock / 64 == 16, "16 waves per chunk");
-        o << "  __syncthreads();\n  if (threadIdx.x < 64u) {\n";
-        o << "    const uint32_t w = threadIdx.x & 15u;\n";
-        o << "    float m = threadIdx.x < 16u ? redm[w] : -__builtin_inff(), s = threadIdx.x < 16u ? reds[w] : 0.0f;\n";
-        o << "    for (int off = 8; off > 0; off >>= 1)\n"
-          << "      tca::hip::online_expsum_merge(m, s, __shfl_xor(m, off, 64), __shfl_xor(s, off, 64));\n";
-        o << "    if (threadIdx.x == 0u) {\n";
-        o << "      p" << sa << "[static_cast<uint64_t>(r) * PMAX + p] = m;  // chain A's partial: the chunk's maximum\n";
-        o << "      p" << sb << "[static_cast<uint64_t>(r) * PMAX + p] = s;\n";
-        o << "      q" << sb << "[static_cast<uint64_t>(r) * PMAX + p] = m;\n    }\n  }\n}\n";
+        if (chanKind) {
+          o << "  for (int off = 32; off > 0; off >>= 1)\n"
+            << "    tca::hip::chan_merge_present(cs, cm, cn, __shfl_xor(cs, off, 64), __shfl_xor(cm, off, 64), "
+               "__shfl_xor(cn, off, 64));\n";
+          o << "  __shared__ float reds[" << kPartBlock / 64 << "], redm[" << kPartBlock / 64 << "], redn["
+            << kPartBlock / 64 << "];\n";
+          o << "  if ((threadIdx.x & 63u) == 0u) {\n    reds[threadIdx.x >> 6] = cs;\n    redm[threadIdx.x >> 6] = cm;\n"
+               "    redn[threadIdx.x >> 6] = cn;\n  }\n";
+          o << "  __syncthreads();\n  if (threadIdx.x < 64u) {\n";
+          o << "    const uint32_t w = threadIdx.x & 15u;\n";
+          o << "    const bool in = threadIdx.x < 16u;\n";
+          o << "    float s = in ? reds[w] : 0.0f, m = in ? redm[w] : 0.0f, n = in ? redn[w] : 0.0f;\n";
+          o << "    for (int off = 8; off > 0; off >>= 1)\n"
+            << "      tca::hip::chan_merge_present(s, m, n, __shfl_xor(s, off, 64), __shfl_xor(m, off, 64), "
+               "__shfl_xor(n, off, 64));\n";
+          o << "    if (threadIdx.x == 0u) {  // the chunk's count is its vectors times V\n";
+          o << "      p" << sa << "[static_cast<uint64_t>(r) * PMAX + p] = s;\n";
+          o << "      p" << sb << "[static_cast<uint64_t>(r) * PMAX + p] = m;\n    }\n  }\n}\n";
+        } else {
+          o << "  for (int off = 32; off > 0; off >>= 1)\n"
+            << "    tca::hip::online_expsum_merge(om, os, __shfl_xor(om, off, 64), __shfl_xor(os, off, 64));\n";
+          o << "  __shared__ float redm[" << kPartBlock / 64 << "], reds[" << kPartBlock / 64 << "];\n";
+          o << "  if ((threadIdx.x & 63u) == 0u) {\n    redm[threadIdx.x >> 6] = om;\n    reds[threadIdx.x >> 6] = os;\n  }\n";
+          o << "  __syncthreads();\n  if (threadIdx.x < 64u) {\n";
+          o << "    const uint32_t w = threadIdx.x & 15u;\n";
+          o << "    float m = threadIdx.x < 16u ? redm[w] : -__builtin_inff(), s = threadIdx.x < 16u ? reds[w] : 0.0f;\n";
+          o << "    for (int off = 8; off > 0; off >>= 1)\n"
+            << "      tca::hip::online_expsum_merge(m, s, __shfl_xor(m, off, 64), __shfl_xor(s, off, 64));\n";
+          o << "    if (threadIdx.x == 0u) {\n";
+          o << "      p" << sa << "[static_cast<uint64_t>(r) * PMAX + p] = m;  // chain A's partial: the chunk's maximum\n";
+          o << "      p" << sb << "[static_cast<uint64_t>(r) * PMAX + p] = s;\n";
+          o << "      q" << sb << "[static_cast<uint64_t>(r) * PMAX + p] = m;\n    }\n  }\n}\n";
+        }
         if (foldedMerge.count(p)) return;  // the row map computes (a, S) itself
         // The merge: one wave per row.
         const std::string mfn = pk.symbol + "_smerge" + tag;
@@ -2972,7 +3108,7 @@ class Emitter {
           for (int ci : passes[p]) o << " #" << ci;
           o << ": split rows, pass " << tag << ", partial folds\n";
           o << "template <uint32_t V>\n__device__ __forceinline__ void " << fn << "(\n    " << sig << smSig << ") {\n";
-          chunkHead(kChunkVecs);
+          chunkHead(std::to_string(kChunkVecs) + "u");
           loadRowScalars(p, "  ");
           combsOf(p, "  ");
           for (int ci : passes[p]) {
@@ -3056,10 +3192,15 @@ class Emitter {
           // Row map of pass p over the chunk.
           const std::string fn = pk.symbol + "_smap" + tag;
           smFns.push_back({fn, p});
-          o << "// statement #" << passes[p][0] << ": split rows, pass " << tag << ", row map over a chunk\n";
-          o << "template <uint32_t V>\n__device__ __forceinline__ void " << fn << "(\n    " << sig << smSig << ") {\n";
-          chunkHead(kChunkVecs);
           const bool folded = p >= 2 && foldedMerge.count(p - 2);
+          // A map that folds a mean/variance pair's merge takes its chunk
+          // length CVM as a template argument (longMaps).
+          const bool longMap = folded && chanPair[p - 2];
+          if (longMap) longMaps.insert(fn);
+          o << "// statement #" << passes[p][0] << ": split rows, pass " << tag << ", row map over a chunk\n";
+          o << "template <uint32_t V" << (longMap ? ", uint32_t CVM" : "") << ">\n__device__ __forceinline__ void " << fn
+            << "(\n    " << sig << smSig << ") {\n";
+          chunkHead(longMap ? std::string("CVM") : std::to_string(kChunkVecs) + "u");
           if (folded) {
             // The fused pair's values for this row, computed here (every wave).
             const ir::Chain& A = g_.chains[passes[p - 2][0]];
@@ -3171,12 +3312,24 @@ class Emitter {
       }
       if (splitMulti) {
         const uint64_t lo = (cachedVecs + 1) * w.v;
+        // (device function, pass, chunk of a long map's kernel or 0)
+        std::vector<std::tuple<std::string, size_t, uint32_t>> kernels;
         for (const auto& fp : smFns) {
-          const std::string& fn = fp.first;
+          if (!longMaps.count(fp.first)) {
+            kernels.emplace_back(fp.first, fp.second, 0u);
+            continue;
+          }
+          kernels.emplace_back(fp.first, fp.second, kChunkVecs);
+          kernels.emplace_back(fp.first, fp.second, 4 * kChunkVecs);
+        }
+        for (const auto& kf : kernels) {
+          const std::string& fn = std::get<0>(kf);
+          const uint32_t mapChunk = std::get<2>(kf);
           const bool merge = fn.find("_smerge") != std::string::npos, map = fn.find("_smap") != std::string::npos;
-          const std::string tag = std::to_string(fp.second + 1);
+          const bool longChunk = mapChunk > kChunkVecs;
+          const std::string tag = std::to_string(std::get<1>(kf) + 1);
           PlanKernel sk = pk;
-          sk.symbol = symbol + (merge ? "_m" : map ? "_w" : "_p") + std::to_string(w.v) + "_" + tag;
+          sk.symbol = symbol + (merge ? "_m" : map ? (longChunk ? "_wl" : "_w") : "_p") + std::to_string(w.v) + "_" + tag;
           sk.block = merge ? 256 : kPartBlock;
           for (const auto& a : smPlanArgs) sk.args.push_back(a);
           if (merge) {
@@ -3184,21 +3337,26 @@ class Emitter {
           } else {
             if (!rowGuard.empty()) sk.grid.push_back(DimProduct(geo.outer) + "/1");
             const auto cv = smChunk.find(fn);
-            const uint64_t chunk = cv == smChunk.end() ? kChunkVecs : cv->second;
+            const uint64_t chunk = mapChunk ? mapChunk : cv == smChunk.end() ? kChunkVecs : cv->second;
             sk.grid.push_back(cdim + "/" + std::to_string(chunk * w.v) + ":" + std::to_string(kMaxParts));
           }
-          sk.when.push_back(cdim + " " + std::to_string(lo) + " 4294967295 " + std::to_string(w.mod) + " " +
+          // A long map's two kernels split the row lengths at kLongMapVecs vectors.
+          const uint64_t longFrom = uint64_t{kLongMapVecs} * w.v;
+          const uint64_t klo = longChunk ? longFrom : lo;
+          const std::string khi = mapChunk == kChunkVecs ? std::to_string(longFrom - 1) : std::string("4294967295");
+          sk.when.push_back(cdim + " " + std::to_string(klo) + " " + khi + " " + std::to_string(w.mod) + " " +
                             std::to_string(w.rem));
           if (!rowGuard.empty()) sk.when.push_back(rowGuard + " 0 " + std::to_string(kSplitRows) + " 1 0");
           o << "extern \"C\" __global__ void __launch_bounds__(" << sk.block << ") " << sk.symbol << "(\n    " << sig
-            << smSig << ") {\n  " << fn << "<" << w.v << "u>(" << args << smArgs << ");\n}\n";
+            << smSig << ") {\n  " << fn << "<" << w.v << "u" << (mapChunk ? ", " + std::to_string(mapChunk) + "u" : "")
+            << ">(" << args << smArgs << ");\n}\n";
           std::ostringstream det;
-          det << "row=runtime (" << cdim << " % " << w.mod << " == " << w.rem << ", >= " << lo
+          det << "row=runtime (" << cdim << " % " << w.mod << " == " << w.rem << ", " << klo << ".." << khi
               << (rowGuard.empty() ? std::string() : ", rows <= " + std::to_string(kSplitRows)) << ": split, pass "
               << tag << ") vec=" << w.v
               << (merge ? " merge: one wave per row over <= " + std::to_string(kMaxParts) + " partials"
                         : (map ? " row map: " : " partial: ") + std::to_string(kPartBlock) + " lanes per chunk of >= " +
-                              std::to_string(kChunkVecs / 2) + " vectors");
+                              std::to_string((longChunk ? mapChunk : kChunkVecs) / 2) + " vectors");
           AddKernel(sk, Family::Stream, n.chains, det.str());
         }
       }

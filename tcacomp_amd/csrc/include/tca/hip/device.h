@@ -296,6 +296,55 @@ __device__ __forceinline__ void chan_merge(float& s, float& m2, float& n, float 
   n += nb;
 }
 
+// Waits for every vector memory operation of the wave (s_waitcnt vmcnt(0),
+// expcnt and lgkmcnt left at their maxima: the gfx9 encoding). Placed once
+// before a loop, it settles loads that the compiler's wait pass otherwise
+// counts as pending on a branch that skipped their use, and then waits for
+// at the head of every iteration.
+__device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// A value that every lane of the wave holds bit for bit, as a wave-uniform
+// (scalar register) value.
+__device__ __forceinline__ float wave_uniform(float v) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
+// The union as chan_merge forms it, where either side may be empty (n or
+// nb = 0: nothing folded), as lanes and partials that hold no values are.
+// Commutative bit for bit: the two m2 add first, and the sums, the squared
+// difference of means and the weight are symmetric; so a butterfly over a
+// wave leaves every lane with the same triple.
+__device__ __forceinline__ void chan_merge_present(float& s, float& m2, float& n, float sb, float m2b, float nb) {
+  if (nb == 0.0f) return;
+  if (n == 0.0f) {
+    s = sb;
+    m2 = m2b;
+    n = nb;
+    return;
+  }
+  const float d = sb / nb - s / n;
+  m2 = (m2 + m2b) + d * d * (n * nb / (n + nb));
+  s += sb;
+  n += nb;
+}
+
+// Folds N values into (s, m2, n): their sum, their mean (N a power of two:
+// an exact scaling), their centred sum of squares, then chan_merge_present.
+template <int N>
+__device__ __forceinline__ void chan_add(float& s, float& m2, float& n, const float (&v)[N]) {
+  float gs = v[0];
+#pragma unroll
+  for (int i = 1; i < N; ++i) gs += v[i];
+  const float gm = gs * (1.0f / N);
+  float g2 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float d = v[i] - gm;
+    g2 = fmaf(d, d, g2);
+  }
+  chan_merge_present(s, m2, n, gs, g2, static_cast<float>(N));
+}
+
 }  // namespace hip
 }  // namespace tca
 

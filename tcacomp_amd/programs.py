@@ -848,7 +848,7 @@ def all_builds():
 
 # Programs whose passes fuse into one read by default (online softmax
 # normaliser, pairwise mean/variance); the tests also run them unfused.
-PASS_FUSED = ("softmax_dyn", "col_mean_var_dyn", "col_mean_var_l_dyn", "col_mean_var_bf16")
+PASS_FUSED = ("softmax_dyn", "layernorm_dyn", "col_mean_var_dyn", "col_mean_var_l_dyn", "col_mean_var_bf16")
 
 
 # Contractions the tests also run with EMIT_NO_GEMM_SPLIT (the 128/256 tile

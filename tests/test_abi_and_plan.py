@@ -10,7 +10,7 @@ import pytest
 
 from tcacomp_amd import _lib, build, compiler, programs
 from tcacomp_amd.compiler import TensorDesc
-from tcacomp_amd.pkg import EMIT_NO_FUSION, EMIT_NO_GEMM
+from tcacomp_amd.pkg import EMIT_NO_FUSION, EMIT_NO_GEMM, EMIT_NO_PASS_FUSION
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -555,7 +555,7 @@ EXPECTED_FAMILIES = {
     # softmax's max and exp-sum passes share one partial when split (online normaliser), and the row
     # map computes their merge itself
     "copy_f32": ["elementwise"], "row_sum_max_dyn": ["stream"] * 13, "softmax_dyn": ["stream"] * 16,
-    "layernorm_dyn": ["stream"] * 25, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 10,
+    "layernorm_dyn": ["stream"] * 19, "layernorm_rstd_1024": ["row"], "layernorm_rstd_dyn": ["stream"] * 10,
     # narrow rows: one more width per halving of the element size (8 bf16, 16 u8 elements per vector)
     "row_sum_bf16_dyn": ["stream"] * 17, "row_sum_u8_dyn": ["stream"] * 21, "row_stats_u32_dyn": ["stream"] * 13,
     # column reductions: a (partial, merge) pair per vector width
@@ -1037,3 +1037,28 @@ def test_multipass_split_selection(R, C, variants):
     assert _lib.lib().tca_program_selected(h, arr, 2, None, 0, out, None, None, len(syms)) == 0, _lib.last_error()
     assert [s for s, f in zip(syms, out) if f] == ["tca_softmax_dyn_k0_" + v for v in variants]
     _lib.lib().tca_program_unload(h)
+
+
+@pytest.mark.parametrize("flags,C,variants", [
+    (0, 1 << 20, ["p4_1", "wl4_3"]), (0, 262140, ["p4_1", "w4_3"]), (0, 262142, ["p2_1", "wl2_3"]),
+    (EMIT_NO_PASS_FUSION, 1 << 20, ["p4_1", "m4_1", "p4_2", "m4_2", "w4_3"])])
+def test_split_layernorm_selection(flags, C, variants):
+    """Layernorm's mean and centred sum of squares share one read of each
+    chunk (pass 1's partial holds each chunk's sum and its sum of squares
+    about its own mean), merged by the row map, whose chunks are 4x longer
+    from 65536 vectors a row on; unfused, each pass has a partial and a
+    merge."""
+    e = programs.CONFIG_PROGRAMS["layernorm_dyn"]().emit(flags=flags)
+    rc, h = parse(e.plan)
+    assert rc == 0, _lib.last_error()
+    R = 3
+    arr = compiler._descriptors([TensorDesc(0x1000, (R, C), 0), TensorDesc(0x1000, (C,), 0),
+                                 TensorDesc(0x1000, (C,), 0), TensorDesc(0x1000, (R, C), 0)])
+    syms = e.kernel_symbols()
+    out = (ctypes.c_uint8 * len(syms))()
+    assert _lib.lib().tca_program_selected(h, arr, 4, None, 0, out, None, None, len(syms)) == 0, _lib.last_error()
+    assert [s for s, f in zip(syms, out) if f] == ["tca_layernorm_dyn_k0_" + v for v in variants]
+    _lib.lib().tca_program_unload(h)
+    if flags == 0:
+        assert "tca::hip::chan_add(cs, cm, cn, ev);" in e.source
+        assert "ptotal += c < PF ? mv[k] + nc * dc * dc : 0.0f;" in e.source

@@ -209,15 +209,19 @@ def test_split_softmax_special_values(gpu, C):
     assert np.isnan(got[1]).all() and np.isnan(got[2]).all() and np.isnan(got[3]).all()
 
 
+@pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["pairwise", "passes"])
 @pytest.mark.parametrize("R,C", MULTIPASS_SPLIT_SHAPES)
-def test_split_layernorm(gpu, R, C):
-    _say("split C4", R, C)
+def test_split_layernorm(gpu, R, C, flags):
+    """Both lowerings of split rows: the mean and the centred sum of squares
+    in one read of each chunk (each chunk's sum and sum of squares about its
+    own mean, merged pairwise), and one partial + merge per pass."""
+    _say("split C4", R, C, flags)
     x = inputs.normal((R, C), 1.0, 0)
     g, b = inputs.uniform((C,), 0.5, 1.5, 1), inputs.uniform((C,), -0.1, 0.1, 2)
     inv_n, eps = float(np.float32(1.0 / C)), 1e-5
     want = oracle.layernorm(x, g, b, inv_n, eps)
     y = out_dev((R, C), gpu)
-    run(compiled("layernorm_dyn"), [to_dev(x, gpu), to_dev(g, gpu), to_dev(b, gpu), y], scalars=[inv_n, eps])
+    run(compiled("layernorm_dyn", flags), [to_dev(x, gpu), to_dev(g, gpu), to_dev(b, gpu), y], scalars=[inv_n, eps])
     got = host(y)
     assert canaries(got) == 0
     # At a million terms the oracle's sequential fp32 sum of squares is itself
