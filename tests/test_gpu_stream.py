@@ -181,6 +181,42 @@ def test_split_softmax(gpu, R, C, flags):
     assert np.abs(got.astype(np.float64).sum(1) - 1.0).max() <= reduce_tol(C)
 
 
+@pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["pairwise", "passes"])
+@pytest.mark.parametrize("C", [100_000, 300_000])
+def test_split_layernorm_special_rows(gpu, C, flags):
+    """Split layernorm rows that stress the one-read variance: a large
+    offset (mean 1000, spread 1: the sum of squares about each chunk's own
+    mean, not raw squares), a constant row (variance 0), a step between the
+    row's halves (the chunks' means differ: the between-chunk terms carry
+    the variance), and rows holding +inf or NaN, which are NaN throughout
+    as the sequential definition gives them (the oracle). Both lowerings,
+    the 1x and the 4x row-map chunks."""
+    _say("split C4 special rows", C, flags)
+    x = inputs.normal((6, C), 1.0, 6)
+    x[0] += 1000.0
+    x[1] = 3.0
+    x[2, : C // 2] -= 5.0
+    x[2, C // 2:] += 5.0
+    x[3, C // 3] = np.inf
+    x[4, C // 2] = np.nan
+    x[5] *= 1e-3
+    g, b = inputs.uniform((C,), 0.5, 1.5, 1), inputs.uniform((C,), -0.1, 0.1, 2)
+    inv_n, eps = float(np.float32(1.0 / C)), 1e-5
+    want = oracle.layernorm(x, g, b, inv_n, eps)
+    y = out_dev((6, C), gpu)
+    run(compiled("layernorm_dyn", flags), [to_dev(x, gpu), to_dev(g, gpu), to_dev(b, gpu), y], scalars=[inv_n, eps])
+    got = host(y)
+    assert canaries(got) == 0
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.isnan(got[3]).all() and np.isnan(got[4]).all()
+    fin = [0, 1, 2, 5]
+    xd = x[fin].astype(np.float64)
+    mean = xd.sum(1, keepdims=True) * inv_n
+    var = ((xd - mean) ** 2).sum(1, keepdims=True) * inv_n
+    want64 = (xd - mean) / np.sqrt(var + eps) * g.astype(np.float64) + b.astype(np.float64)
+    assert_layernorm_close(got[fin], want64, x[fin], g, b, eps, "split C4 special rows C=%d" % C)
+
+
 @pytest.mark.parametrize("C", [40000, 1_000_002])
 def test_split_softmax_special_values(gpu, C):
     """Split rows fold the max and the exp-sum in one read (the online

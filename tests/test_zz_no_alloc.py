@@ -3,8 +3,8 @@ tca_program_launch, through the C ABI.
 
 Each case uses a kernel family with a scratch workspace: split-row partials,
 column-reduction partials, HBM-resident locals (the generic lowering), a
-chained reduction's local, split softmax rows and the one-read column mean
-and variance. Two calls in a row, the second with a smaller
+chained reduction's local, split softmax and layernorm rows and the one-read
+column mean and variance. Two calls in a row, the second with a smaller
 input, each compared bit for bit with the allocating launch of the same
 program on the same inputs (the same kernels run on the same data, so the
 outputs are identical). A workspace beyond the 32 MiB scratch is refused
@@ -67,6 +67,27 @@ def test_noalloc_matches_allocating_launch(gpu, name, flags, shapes, outs, scala
         for g, w in zip(got, want):
             assert not np.any(g == np.float32(CANARY))
             assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), (name, shape)
+
+
+def test_noalloc_split_layernorm(gpu):
+    """Split layernorm rows (the mean and the centred sum of squares in one
+    read: sum and sum-of-squares partials, plan-only row locals), long rows
+    then shorter ones (the 4x-chunk row map, then the 1x one)."""
+    prog = compiled("layernorm_dyn")
+    for R, C in ((3, 1_000_000), (2, 200_000)):
+        print("noalloc layernorm_dyn", (R, C), flush=True)
+        x = torch.from_numpy(inputs.normal((R, C), 1.0, 3)).to(gpu)
+        g = torch.from_numpy(inputs.uniform((C,), 0.5, 1.5, 4)).to(gpu)
+        b = torch.from_numpy(inputs.uniform((C,), -0.1, 0.1, 5)).to(gpu)
+        _workspace_used(prog, [x])
+        res = []
+        for noalloc in (False, True):
+            y = torch.full((R, C), CANARY, device=gpu)
+            prog.launch([x, g, b, y], scalars=(1.0 / C, 1e-5), noalloc=noalloc)
+            torch.cuda.synchronize()
+            res.append(y.cpu().numpy())
+        assert not np.any(res[1] == np.float32(CANARY))
+        assert np.array_equal(res[1].view(np.uint32), res[0].view(np.uint32)), (R, C)
 
 
 def test_noalloc_refuses_oversized_workspace(gpu):
