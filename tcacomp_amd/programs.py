@@ -132,6 +132,35 @@ def layernorm(cols=1024):
     return b.Build()
 
 
+def row_stats_shift(cols=0):
+    """A mean and a centred sum of squares whose piped maps read row values:
+    m = sum(x) * inv_n + shift[r] (the sum's piped map reads a per-row
+    input), rs = rsqrtf(sum((x - m)^2) * inv_n + eps) + 0.5 * m (the sum of
+    squares' piped map reads m), then y = (x - m) * rs; m and rs are
+    outputs. Exercises the one-read pair's finish beyond layernorm's."""
+    b = NewBuilder("row_stats_shift_%s" % (cols or "dyn"))
+    R, C = b.Dim("R", 0), _static(b, "C", cols)
+    x = b.Tensor("x", TF32, R, C)
+    shift = b.Tensor("shift", TF32, R)
+    m = b.Tensor("m", TF32, R)
+    rs = b.Tensor("rs", TF32, R)
+    y = b.Tensor("y", TF32, R, C)
+    inv_n = b.ScalarParam("inv_n", TF32)
+    eps = b.ScalarParam("eps", TF32)
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: v).As(R, C)
+     .Reduce(b.Float32(0), _sum(b))
+     .Map([At(shift, R)], lambda v, s: b.Add(b.Mul(v, inv_n), s)).As(R).Store(m, R))
+    (b.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(m, R)], lambda l, r: b.Mul(b.Sub(l, r), b.Sub(l, r))).As(R, C)
+     .Reduce(b.Float32(0), _sum(b))
+     .Map([At(m, R)], lambda v, a: b.Add(Call("rsqrtf", b.Add(b.Mul(v, inv_n), eps)), b.Mul(a, b.Float32(0.5))))
+     .As(R).Store(rs, R))
+    (b.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(m, R), At(rs, R)], lambda l, a, s: b.Mul(b.Sub(l, a), s))
+     .As(R, C).Store(y, R, C))
+    return b.Build()
+
+
 def layernorm_rstd(cols=1024):
     """C4 with the reciprocal standard deviation as its own per-row chain
     (iterating only the row axis, one level shallower than the others) and
@@ -806,6 +835,7 @@ CONFIG_PROGRAMS = {
     # a per-row chain fused between the reductions and the row map
     "layernorm_rstd_1024": lambda: layernorm_rstd(1024),
     "layernorm_rstd_dyn": lambda: layernorm_rstd(0),
+    "row_stats_shift_dyn": lambda: row_stats_shift(0),
     # the expression layer: every operator, builtin and cast on the device
     "expr_f32": lambda: _expr_program("expr_f32", TF32, EXPR_F32),
     "expr_i32": lambda: _expr_program("expr_i32", TI32, EXPR_I32),
@@ -848,7 +878,8 @@ def all_builds():
 
 # Programs whose passes fuse into one read by default (online softmax
 # normaliser, pairwise mean/variance); the tests also run them unfused.
-PASS_FUSED = ("softmax_dyn", "layernorm_dyn", "col_mean_var_dyn", "col_mean_var_l_dyn", "col_mean_var_bf16")
+PASS_FUSED = ("softmax_dyn", "layernorm_dyn", "row_stats_shift_dyn", "col_mean_var_dyn", "col_mean_var_l_dyn",
+              "col_mean_var_bf16")
 
 
 # Contractions the tests also run with EMIT_NO_GEMM_SPLIT (the 128/256 tile

@@ -1062,3 +1062,13 @@ def test_split_layernorm_selection(flags, C, variants):
     if flags == 0:
         assert "tca::hip::chan_add(cs, cm, cn, ev);" in e.source
         assert "ptotal += c < PF ? mv[k] + nc * dc * dc : 0.0f;" in e.source
+
+
+def test_split_pair_finish_binds_row_values():
+    """The fused pair's finish in the row map: the mean's piped map loads
+    its per-row operand (shift, tensor 1) at the row, and the sum of
+    squares' piped map reads the mean the map computed (aval), not memory."""
+    e = programs.CONFIG_PROGRAMS["row_stats_shift_dyn"]().emit()
+    assert "const float ars1 = t1[c0];" in e.source
+    assert "(aval * 0x1p-1f)" in e.source
+    assert "_wl4_3" in e.plan and "_m4_1" not in e.plan

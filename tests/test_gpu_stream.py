@@ -182,6 +182,44 @@ def test_split_softmax(gpu, R, C, flags):
 
 
 @pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["pairwise", "passes"])
+@pytest.mark.parametrize("R,C", [(7, 40000), (3, 100_003), (5, 300_000), (2, 1_000_002)])
+def test_split_row_stats_shift(gpu, R, C, flags):
+    """A mean whose piped map adds a per-row input (m = sum(x) inv_n +
+    shift[r]) and a sum of squares about it whose piped map reads m (rs =
+    rsqrtf(T inv_n + eps) + m / 2), both outputs, then y = (x - m) rs; split
+    rows in both lowerings, V 4, 1 and 2, the 1x and 4x row-map chunks.
+    m against the float64 sum (the reduction tolerance on ||x||_2, plus the
+    piped map's two roundings); rs against float64 from the device's m
+    (T = sum (x - m)^2 to the reduction tolerance on ||(x - m)^2||_2,
+    carried through rsqrt to first order, plus 4 ulp); y against (x - m) rs
+    from the device's m and rs (two roundings)."""
+    _say("split row stats shift", R, C, flags)
+    x = inputs.normal((R, C), 1.0, 7)
+    shift = inputs.uniform((R,), -2.0, 2.0, 8)
+    inv_n, eps = float(np.float32(1.0 / C)), 1e-5
+    m, rs, y = out_dev((R,), gpu), out_dev((R,), gpu), out_dev((R, C), gpu)
+    run(compiled("row_stats_shift_dyn", flags), [to_dev(x, gpu), to_dev(shift, gpu), m, rs, y], scalars=[inv_n, eps])
+    gm, grs, gy = host(m).astype(np.float64), host(rs).astype(np.float64), host(y)
+    assert canaries(gy) == 0 and canaries(host(m)) == 0 and canaries(host(rs)) == 0
+    u, tol = 2.0 ** -24, reduce_tol(C)
+    xd = x.astype(np.float64)
+    s64 = xd.sum(1) * inv_n
+    m64 = s64 + shift.astype(np.float64)
+    bound_m = tol * np.sqrt((xd * xd).sum(1)) * inv_n + 2 * u * (np.abs(s64) + np.abs(m64))
+    assert np.all(np.abs(gm - m64) <= bound_m), np.abs(gm - m64) / bound_m
+    d = xd - gm[:, None]
+    T = (d * d).sum(1)
+    q = T * inv_n + eps
+    r64 = 1.0 / np.sqrt(q)
+    rs64 = r64 + 0.5 * gm
+    e_q = tol * np.sqrt((d ** 4).sum(1)) * inv_n
+    bound_rs = 0.5 * e_q / q * r64 + 4 * u * (r64 + np.abs(rs64))
+    assert np.all(np.abs(grs - rs64) <= bound_rs), np.abs(grs - rs64) / bound_rs
+    y64 = d * grs[:, None]
+    assert np.all(np.abs(gy - y64) <= 2 * u * np.abs(d) * np.abs(grs)[:, None] + 2 * u * np.abs(y64))
+
+
+@pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["pairwise", "passes"])
 @pytest.mark.parametrize("C", [100_000, 300_000])
 def test_split_layernorm_special_rows(gpu, C, flags):
     """Split layernorm rows that stress the one-read variance: a large
