@@ -2716,13 +2716,14 @@ class Emitter {
     std::vector<std::pair<std::string, size_t>> smFns;  // (device function, pass)
     // Vectors per chunk of a split kernel whose chunks are not kChunkVecs.
     std::map<std::string, uint32_t> smChunk;
-    // Row maps with a pair's merge folded in whose chunk length is a template
-    // argument: kChunkVecs below kLongMapVecs vectors a row, 4x from there
-    // (one wave's merge per kernel block is then spread over 4x the
-    // vectors). Layernorm over [8, 4 Mi]: 93 -> 79 us, [64, 1 Mi]: 137 ->
-    // 131 us; rows of 16 Ki vectors keep 4 chunks (17 us, not 19, at 32
-    // rows). Softmax's map measured no better with longer chunks at
-    // [64, 1 Mi] and keeps kChunkVecs.
+    // Row maps with a mean/variance pair's merge folded in take their chunk
+    // length as a template argument: kChunkVecs below kLongMapVecs vectors a
+    // row, 4x from there (every wave computes the pair's values before it
+    // streams, and longer chunks spread that over more vectors). Layernorm
+    // over [8, 4 Mi]: 93 -> 79 us, [64, 1 Mi]: 137 -> 131 us; rows of 16 Ki
+    // vectors keep 4 chunks (17 us, not 19, at 32 rows). Softmax's map
+    // measured no better with longer chunks at [64, 1 Mi] and keeps
+    // kChunkVecs.
     std::set<std::string> longMaps;
     constexpr uint32_t kLongMapVecs = 16 * kChunkVecs;
     // The fused softmax passes take chunks 4x as long (16 vectors per lane):
@@ -2875,10 +2876,8 @@ class Emitter {
           << "u; ++k) {\n" << ind << "  const uint64_t at = static_cast<uint64_t>(r) * " << kMaxParts
           << "u + min((threadIdx.x & 63u) + 64u * k, PF - 1u);\n" << ind << "  sv[k] = p" << sa << "[at];\n" << ind
           << "  mv[k] = p" << sb << "[at];\n" << ind << "}\n";
-        // Every loaded value is consumed on every path (selects, not
-        // branches): a load left pending on a skipped branch made the
-        // compiler wait for all memory operations (vmcnt(0)) at the head of
-        // the row map's loop, stores included, every iteration.
+        // Lanes past the row's chunks add 0 (their loads were clamped to the
+        // last chunk).
         o << ind << "float ps = 0.0f;\n#pragma unroll\n" << ind << "for (uint32_t k = 0; k < " << K << "u; ++k)\n"
           << ind << "  ps += (threadIdx.x & 63u) + 64u * k < PF ? sv[k] : 0.0f;\n";
         o << ind << "for (int off = 32; off > 0; off >>= 1) ps += __shfl_xor(ps, off, 64);\n";
@@ -2914,9 +2913,11 @@ class Emitter {
           << ind << "}\n";
         o << ind << "for (int off = 32; off > 0; off >>= 1) ptotal += __shfl_xor(ptotal, off, 64);  // about aval\n";
         o << ind << "ptotal = tca::hip::wave_uniform(ptotal);\n";
-        // The chunk terms' selects become branches (a division is costly);
-        // the loads used in them are settled here, not at the head of the
-        // caller's loop.
+        // The compiler turns the chunk terms' selects into branches (a
+        // division is costly); a load used only inside such a branch counts
+        // as pending on the path that skipped it, and the compiler then
+        // waited for all memory operations (vmcnt(0), stores included) at
+        // the head of the row map's loop, every iteration. Settled here, once.
         o << ind << "tca::hip::wait_vector_memory();\n";
         pairFinishB(p, ind, "ptotal");
       };
