@@ -60,7 +60,9 @@ enum {
 #define TCA_MAX_RANK 8
 
 /* Non-owning, row-major tensor descriptor: the C face of the reference's
- * tca::Tensor<T,R> (runtime/tca/tensor.h:17-40). */
+ * tca::Tensor<T,R> (runtime/tca/tensor.h:17-40). At most 2^32 - 2^16 - 1
+ * elements (TCA_ERR_SHAPE beyond): the u32 index domain less the headroom
+ * the kernels' index steps need. */
 typedef struct tca_tensor {
   void* data;
   uint32_t rank;

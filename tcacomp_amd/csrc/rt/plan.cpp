@@ -420,10 +420,16 @@ int Bind(const Plan& p, const tca_tensor* tensors, uint32_t n_tensors, const uin
              DtypeName(t.dtype);
       return TCA_ERR_SHAPE;
     }
+    // Elements, saturated at kMaxElems + 1 (three u32 extents can overflow
+    // 64 bits); an extent of 0 makes the tensor empty whatever the others.
     uint64_t elems = 1;
+    bool empty = false;
     for (size_t ax = 0; ax < t.dims.size(); ++ax) {
       const int d = t.dims[ax];
-      elems *= a.dims[ax];
+      if (a.dims[ax] == 0)
+        empty = true;
+      else
+        elems = elems > kMaxElems / a.dims[ax] ? kMaxElems + 1 : elems * a.dims[ax];
       if (!known[d]) {
         (*dims)[d] = a.dims[ax];
         known[d] = true;
@@ -434,6 +440,7 @@ int Bind(const Plan& p, const tca_tensor* tensors, uint32_t n_tensors, const uin
         return TCA_ERR_SHAPE;
       }
     }
+    if (empty) elems = 0;
     if (elems > 0 && a.data == nullptr) {
       *err = "tensor " + t.name + " has a null data pointer";
       return TCA_ERR_INVALID;
@@ -442,11 +449,17 @@ int Bind(const Plan& p, const tca_tensor* tensors, uint32_t n_tensors, const uin
       *err = "tensor " + t.name + " data is not 16-byte aligned (vector loads need it)";
       return TCA_ERR_INVALID;
     }
-    if (elems > 0xffffffffull) {
-      *err = "tensor " + t.name + " has more than 2^32-1 elements (u32 index domain)";
+    if (elems > kMaxElems) {
+      *err = "tensor " + t.name + " has more than 2^32-2^16-1 elements (u32 index domain, less 2^16 of headroom "
+             "for the kernels' index arithmetic)";
       return TCA_ERR_SHAPE;
     }
   }
+  for (size_t i = 0; i < free.size(); ++i)
+    if (free_dims[i] > kMaxElems) {
+      *err = "free dim " + p.dims[free[i]].name + " = " + std::to_string(free_dims[i]) + " exceeds 2^32-2^16-1";
+      return TCA_ERR_SHAPE;
+    }
   for (size_t i = 0; i < p.dims.size(); ++i) {
     if (!known[i]) {
       *err = "dim " + p.dims[i].name + " is not bound by any tensor or free-dim argument";

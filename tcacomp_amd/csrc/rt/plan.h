@@ -136,6 +136,12 @@ int DtypeFromName(const std::string& s);
 bool Parse(const std::string& text, Plan* out, std::string* err);
 std::string Serialize(const Plan& p);
 
+// The most elements a tensor may hold (and the largest free dim): the u32
+// index domain less 2^16. The kernels step u32 indices (vectors of a row,
+// rows of a column, lanes of a row) past an extent by less than 2^16 before
+// comparing them with it; the headroom keeps that step from wrapping.
+constexpr uint64_t kMaxElems = (uint64_t{1} << 32) - (uint64_t{1} << 16) - 1;
+
 // Resolves every dim value from the caller's tensors and free dims. Returns
 // a TCA_* status; *dims receives one value per Plan::dims entry.
 int Bind(const Plan& p, const tca_tensor* tensors, uint32_t n_tensors, const uint32_t* free_dims,

@@ -852,12 +852,17 @@ def _constants(source, names):
     return vals
 
 
-@pytest.mark.parametrize("R,C", [(U32, 1), (2 ** 31, 1), (2 ** 30 - 1, 4), (U32 // 3, 3), (U32 // 64, 64),
-                                 (64 * 1024 + 1, 2), (1, U32)])
+# The most elements a tensor may hold (the u32 domain less the kernels'
+# index headroom); larger tensors are refused (test_element_limit_keeps_index_headroom).
+TOP = 2 ** 32 - 2 ** 16 - 1
+
+
+@pytest.mark.parametrize("R,C", [(TOP, 1), (2 ** 31, 1), (TOP // 4, 4), (TOP // 3, 3), (TOP // 64, 64),
+                                 (64 * 1024 + 1, 2), (1, TOP)])
 def test_column_split_device_matches_plan_at_the_u32_edge(device_helpers, R, C):
     """Column family: the partial kernel's grid is column blocks x P with P
     from the plan's 64-bit split record; each block recomputes P with the
-    device's col_split. They must agree for every R x C <= 2^32 - 1 (with a
+    device's col_split. They must agree for every R x C the plan accepts (with a
     32-bit round-up that wraps, blocks with p >= 1 took the one-chunk store
     path and the merge read partials nobody wrote)."""
     p = compiler.CompiledProgram("col_sum_max_dyn", programs.CONFIG_PROGRAMS["col_sum_max_dyn"]().emit(), "")
@@ -880,7 +885,7 @@ def test_column_split_device_matches_plan_at_the_u32_edge(device_helpers, R, C):
     assert (grids[merge[0]] > 0) == (P > 1)
 
 
-@pytest.mark.parametrize("R,C", [(1, U32), (1, U32 - 1), (3, U32 // 3 - 2), (255, U32 // 255 - 4), (1, 16388)])
+@pytest.mark.parametrize("R,C", [(1, TOP), (1, TOP - 1), (3, TOP // 3 - 2), (255, TOP // 255 - 4), (1, 16388)])
 def test_split_rows_device_matches_plan_at_the_u32_edge(device_helpers, R, C):
     """Split rows: the grid is rows x P from the plan (64-bit, capped at
     PMAX); the device recomputes P = min(PMAX, ceil_div(VECS, CV)) and the
@@ -1072,3 +1077,37 @@ def test_split_pair_finish_binds_row_values():
     assert "const float ars1 = t1[c0];" in e.source
     assert "(aval * 0x1p-1f)" in e.source
     assert "_wl4_3" in e.plan and "_m4_1" not in e.plan
+
+
+def _select(name, descs):
+    """(status, last error) of selecting `name`'s kernels for tensors shaped `descs`."""
+    e = programs.CONFIG_PROGRAMS[name]().emit()
+    rc, h = parse(e.plan)
+    assert rc == 0, _lib.last_error()
+    syms = e.kernel_symbols()
+    out = (ctypes.c_uint8 * len(syms))()
+    arr = compiler._descriptors([TensorDesc(0x1000, s, 0) for s in descs])
+    st = _lib.lib().tca_program_selected(h, arr, len(descs), None, 0, out, None, None, len(syms))
+    err = _lib.last_error()
+    _lib.lib().tca_program_unload(h)
+    return st, err
+
+
+def test_element_limit_keeps_index_headroom():
+    """A tensor holds at most 2^32 - 2^16 - 1 elements: the split kernels
+    step a u32 vector index up to 5120 past the row's vectors before
+    comparing (a row of 2^32 - 1 odd elements would wrap it). The largest
+    row selects the split pair; one element more is refused before any
+    launch, and so is a shape whose 64-bit element product wraps to 0
+    (2^31 x 2^31 x 4: counted as empty, it skipped every check before); an
+    extent of 0 beside huge ones is an empty tensor."""
+    top = (1 << 32) - (1 << 16) - 1
+    st, err = _select("row_sum_max_dyn", [(1, top), (1,), (1,)])
+    assert st == 0, err
+    st, err = _select("row_sum_max_dyn", [(1, top + 1), (1,), (1,)])
+    assert st == _lib.TCA_ERR_SHAPE and "2^32-2^16-1" in err, err
+    big = (1 << 32) - 1
+    st, err = _select("col_mean_var_dyn", [(1 << 31, 1 << 31, 4), (1 << 31, 4), (1 << 31, 4)])
+    assert st == _lib.TCA_ERR_SHAPE and "2^32-2^16-1" in err, err
+    st, err = _select("col_mean_var_dyn", [(0, big, big), (0, big), (0, big)])
+    assert st == 0, err
