@@ -13,8 +13,8 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import (assert_layernorm_close, assert_reduce_close, canaries, compiled, host, out_dev, reduce_tol, run,
-                     to_dev)
+from helpers import (CANARY, assert_layernorm_close, assert_reduce_close, canaries, compiled, host, out_dev, reduce_tol,
+                     run, to_dev)
 from tcacomp_amd import inputs
 from tcacomp_amd.pkg import EMIT_NO_PASS_FUSION
 
@@ -179,6 +179,51 @@ def test_split_softmax(gpu, R, C, flags):
     rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want.astype(np.float64)), 1e-30)
     assert rel.max() <= reduce_tol(C), "softmax relative error %g" % rel.max()
     assert np.abs(got.astype(np.float64).sum(1) - 1.0).max() <= reduce_tol(C)
+
+
+# The most elements a tensor may hold: the u32 index domain less the
+# kernels' index headroom (2^16).
+TOP = 2 ** 32 - 2 ** 16 - 1
+
+
+@pytest.mark.parametrize("C", [TOP, TOP - 3], ids=["V1", "V4"])
+def test_split_rows_at_the_element_limit(gpu, C):
+    """One row as long as a tensor may be (17 GB of f32), split over 512
+    chunks, the vector indices within 2^16 of 2^32: zeros with marks 1, 2, 4
+    at the first, the middle and the last element. Row sum + max must be
+    exactly 7 and 4 (an index that wrapped or stopped short changes one);
+    softmax must give a zero 1 / S and a mark e^m / S, S = (C - 3) + e + e^2
+    + e^4 (one read: the online normaliser); layernorm (gamma 1, beta 0;
+    one read: sum and centred sum of squares) must give (x - mean) / sqrt(var
+    + eps) from the closed-form mean 7 / C and variance (21 - 49 / C) / C."""
+    import torch
+    _say("split rows at the element limit", C)
+    x = torch.zeros((1, C), device=gpu)
+    x[0, 0], x[0, C // 2], x[0, C - 1] = 1.0, 2.0, 4.0
+    s, m = out_dev((1,), gpu), out_dev((1,), gpu)
+    run(compiled("row_sum_max_dyn"), [x, s, m])
+    assert host(s)[0] == 7.0 and host(m)[0] == 4.0, (host(s), host(m))
+    at = [0, 1, C // 2, C - 2, C - 1]
+    y = torch.full_like(x, CANARY)
+    run(compiled("softmax_dyn"), [x, y])
+    S = (C - 3) + np.e + np.e ** 2 + np.e ** 4
+    got = y[0, at].double().cpu().numpy()
+    want = np.array([np.e, 1.0, np.e ** 2, 1.0, np.e ** 4]) / S
+    assert np.all(np.abs(got - want) <= 1e-4 * want), (got, want)
+    assert abs(float(y.sum(dtype=torch.float64)) - 1.0) <= 1e-4
+    assert int((y == CANARY).sum()) == 0
+    g, b = torch.ones((C,), device=gpu), torch.zeros((C,), device=gpu)
+    inv_n, eps = float(np.float32(1.0 / C)), 1e-5
+    y.fill_(CANARY)
+    run(compiled("layernorm_dyn"), [x, g, b, y], scalars=[inv_n, eps])
+    mean, var = 7.0 / C, (21.0 - 49.0 / C) / C
+    xa = np.array([1.0, 0.0, 2.0, 0.0, 4.0])
+    want = (xa - mean) / np.sqrt(var + eps)
+    got = y[0, at].double().cpu().numpy()
+    assert np.all(np.abs(got - want) <= 1e-4 * np.abs(want) + 1e-6), (got, want)
+    assert int((y == CANARY).sum()) == 0
+    del x, y, g, b
+    torch.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["pairwise", "passes"])
