@@ -60,6 +60,46 @@ def test_col_sum_max(gpu, R, C):
     np.testing.assert_array_equal(m.cpu().numpy(), want_m)
 
 
+# The most elements a tensor may hold: the u32 index domain less the
+# kernels' index headroom (2^16).
+TOP = 2 ** 32 - 2 ** 16 - 1
+
+
+@pytest.mark.parametrize("R,C", [(TOP, 1), (TOP // 4, 4)], ids=["V1", "V4"])
+def test_col_reductions_at_the_element_limit(gpu, R, C):
+    """Columns as long as a tensor may be (17 GB of f32; the row loops step
+    within 2^16 of 2^32): zeros with marks 1, 2, 4 in the last column at the
+    first, the middle and the last row. Column sum + max must be exactly 7
+    and 4 there and 0 elsewhere; with 4 columns, the one-read mean and
+    variance must give 7 inv_n and (21 - 14 m + R m^2) inv_n (m the stored
+    mean) there, 0 elsewhere."""
+    import torch
+    print("col reductions at the element limit", R, C, flush=True)
+    sys.stdout.flush()
+    x = torch.zeros((R, C), device=gpu)
+    x[0, C - 1], x[R // 2, C - 1], x[R - 1, C - 1] = 1.0, 2.0, 4.0
+    s = torch.full((C,), CANARY, device=gpu)
+    m = torch.full((C,), CANARY, device=gpu)
+    run(compiled("col_sum_max_dyn"), [x, s, m])
+    want_s, want_m = np.zeros(C, np.float32), np.zeros(C, np.float32)
+    want_s[-1], want_m[-1] = 7.0, 4.0
+    np.testing.assert_array_equal(s.cpu().numpy(), want_s)
+    np.testing.assert_array_equal(m.cpu().numpy(), want_m)
+    if C == 1:
+        return
+    inv_n = float(np.float32(1.0 / R))
+    mean = torch.full((1, C), CANARY, device=gpu)
+    var = torch.full((1, C), CANARY, device=gpu)
+    run(compiled("col_mean_var_dyn"), [x.view(1, R, C), mean, var], scalars=[inv_n])
+    gm, gv = mean.cpu().numpy()[0].astype(np.float64), var.cpu().numpy()[0].astype(np.float64)
+    assert np.all(gm[:-1] == 0.0) and np.all(gv[:-1] == 0.0), (gm, gv)
+    assert abs(gm[-1] - 7.0 * inv_n) <= 1e-6 * 7.0 * inv_n, gm
+    wv = (21.0 - 14.0 * gm[-1] + R * gm[-1] ** 2) * inv_n
+    assert abs(gv[-1] - wv) <= 1e-4 * wv, (gv, wv)
+    del x
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("B,R,C", [(1, 1, 8), (2, 1000, 520), (3, 5, 8), (4, 300, 4100), (2, 0, 16),
                                    (5, 2000, 6), (1, 20000, 2048)])
 def test_col_mean_bf16(gpu, B, R, C):
