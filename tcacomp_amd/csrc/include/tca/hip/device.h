@@ -313,7 +313,10 @@ __device__ __forceinline__ float wave_uniform(float v) {
 // nb = 0: nothing folded), as lanes and partials that hold no values are.
 // Commutative bit for bit: the two m2 add first, and the sums, the squared
 // difference of means and the weight are symmetric; so a butterfly over a
-// wave leaves every lane with the same triple.
+// wave leaves every lane with the same triple. The means and the weight use
+// the hardware reciprocal (v_rcp_f32, 1 ulp; counts are >= 1) instead of
+// divisions: a fifth of the split partial's instructions, 48.0 -> 47.0 us at
+// [64, 1 Mi] rows.
 __device__ __forceinline__ void chan_merge_present(float& s, float& m2, float& n, float sb, float m2b, float nb) {
   if (nb == 0.0f) return;
   if (n == 0.0f) {
@@ -322,8 +325,8 @@ __device__ __forceinline__ void chan_merge_present(float& s, float& m2, float& n
     n = nb;
     return;
   }
-  const float d = sb / nb - s / n;
-  m2 = (m2 + m2b) + d * d * (n * nb / (n + nb));
+  const float d = sb * __builtin_amdgcn_rcpf(nb) - s * __builtin_amdgcn_rcpf(n);
+  m2 = (m2 + m2b) + d * d * (n * nb * __builtin_amdgcn_rcpf(n + nb));
   s += sb;
   n += nb;
 }
