@@ -23,6 +23,7 @@ fabsf and a / (|b| + 1); on u32, xor, and, or. The value ranges the tests
 feed keep every f32 sum exact (integer-valued terms, partial sums below
 2^24), so any fold order gives the one correctly rounded result.
 """
+import os
 import random
 
 from tcacomp_amd.pkg import EMIT_NO_FUSION, EMIT_NO_GEMM, TBF16, TF32, TU8, TU32, At, Call, Cast, NewBuilder, Select
@@ -578,12 +579,32 @@ ROWCHAIN_PROGRAMS = ([("f32", True, s) for s in range(100, 106)] + [("f32", Fals
                      [("u32", True, s) for s in (108, 109, 110)] + [("u32", False, 111)])
 
 
+# Further seeds of every generator for a longer search, included when
+# TCA_RANDPROG_EXTENDED=1 at build time (build() prebuilds them) and at test
+# time (tests/test_gpu_random.py runs them): 277 programs.
+EXTENDED = {
+    "row": ([("f32", True, s) for s in range(1000, 1060)] + [("f32", False, s) for s in range(1100, 1140)] +
+            [("u32", True, s) for s in range(1200, 1230)] + [("u32", False, s) for s in range(1300, 1320)]),
+    "grid": ([("f32", True, s) for s in range(2000, 2030)] + [("f32", False, s) for s in range(2030, 2040)] +
+             [("u32", True, s) for s in range(2040, 2050)]),
+    "grid3": [("f32", True, s) for s in range(2100, 2110)] + [("u32", True, s) for s in range(2110, 2115)],
+    "colchain": ([("f32", True, False, s) for s in range(3000, 3020)] +
+                 [("u32", True, False, s) for s in range(3020, 3026)] + [("f32", True, True, s) for s in range(3030, 3036)]),
+    "rowchain": [("f32", True, s) for s in range(4000, 4020)] + [("u32", True, s) for s in range(4020, 4030)],
+}
+
+
 def specs():
-    return ([generate(seed, elem, dyn) for elem, dyn, seed in PROGRAMS] +
-            [generate_grid(seed, elem, dyn) for elem, dyn, seed in GRID_PROGRAMS] +
-            [generate_grid(seed, elem, dyn, True) for elem, dyn, seed in GRID3_PROGRAMS] +
-            [generate_colchain(seed, elem, dyn, batch) for elem, dyn, batch, seed in COLCHAIN_PROGRAMS] +
-            [generate_rowchain(seed, elem, dyn) for elem, dyn, seed in ROWCHAIN_PROGRAMS])
+    rows, grids, grid3s, colchains, rowchains = (PROGRAMS, GRID_PROGRAMS, GRID3_PROGRAMS, COLCHAIN_PROGRAMS,
+                                                 ROWCHAIN_PROGRAMS)
+    if os.environ.get("TCA_RANDPROG_EXTENDED") == "1":
+        rows, grids, grid3s = rows + EXTENDED["row"], grids + EXTENDED["grid"], grid3s + EXTENDED["grid3"]
+        colchains, rowchains = colchains + EXTENDED["colchain"], rowchains + EXTENDED["rowchain"]
+    return ([generate(seed, elem, dyn) for elem, dyn, seed in rows] +
+            [generate_grid(seed, elem, dyn) for elem, dyn, seed in grids] +
+            [generate_grid(seed, elem, dyn, True) for elem, dyn, seed in grid3s] +
+            [generate_colchain(seed, elem, dyn, batch) for elem, dyn, batch, seed in colchains] +
+            [generate_rowchain(seed, elem, dyn) for elem, dyn, seed in rowchains])
 
 
 def all_builds():
