@@ -2512,6 +2512,16 @@ class Emitter {
     // with no row axis (a full reduction) the split replaces the streamed
     // kernel outright.
     constexpr uint32_t kSplitRows = 255, kChunkVecs = 4096, kMaxParts = 512, kPartBlock = 1024;
+    // Nests of several passes also split rows of >= kSplitLongVecs vectors
+    // when there are up to kSplitRowsLong of them: the streamed kernel reads
+    // such a row once per pass (softmax three times), the split passes twice
+    // (the first two passes fused). Softmax [512, 131072]: 161.7 -> 125.2 us,
+    // [1024, 65536]: 152.8 -> 125.0 us, [256, 1 Mi]: 718 -> 529-540 us;
+    // layernorm [512, 131072] 154.8 -> 125.4 us. Shorter rows stay streamed
+    // (layernorm [4096, 40000]: 316 us streamed, 398 split: many short map
+    // chunks, each computing the pair's values), and so do more rows (the
+    // partials are [rows][512]: 8 MiB each at 4095 rows).
+    constexpr uint32_t kSplitRowsLong = 4095, kSplitLongVecs = 16384;
     const bool split = passes.size() == 1 && !g_.chains[passes[0][0]].reduces.empty() && geo.outer.size() <= 1;
     std::string part_fn, merge_fn;
     std::vector<std::string> part_names;
@@ -3287,8 +3297,13 @@ class Emitter {
           const std::string fit = cdim + " 0 4294967295 " + std::to_string(uint64_t{kc} * w.v) + " 0 pow2";
           if (exact) vk.when.push_back(fit);
           else if (canExact) vk.unless.push_back(fit);
-          if (!cached && (split || splitMulti))
+          if (!cached && (split || splitMulti)) {
             vk.when.push_back(rowGuard + " " + std::to_string(kSplitRows + 1) + " 4294967295 1 0");
+            if (splitMulti) {  // not long rows of at most kSplitRowsLong rows: those split
+              vk.unless.push_back(rowGuard + " 0 " + std::to_string(kSplitRowsLong) + " 1 0");
+              vk.unless.push_back(cdim + " " + std::to_string(uint64_t{kSplitLongVecs} * w.v) + " 4294967295 1 0");
+            }
+          }
           o << "extern \"C\" __global__ void __launch_bounds__(" << kBlock << ") " << vk.symbol << "(\n    " << sig
             << ") {\n";
           if (cached && canExact) {
@@ -3347,13 +3362,21 @@ class Emitter {
           const std::string khi = mapChunk == kChunkVecs ? std::to_string(longFrom - 1) : std::string("4294967295");
           sk.when.push_back(cdim + " " + std::to_string(klo) + " " + khi + " " + std::to_string(w.mod) + " " +
                             std::to_string(w.rem));
-          if (!rowGuard.empty()) sk.when.push_back(rowGuard + " 0 " + std::to_string(kSplitRows) + " 1 0");
+          if (!rowGuard.empty()) {  // rows <= kSplitRows, or long rows of at most kSplitRowsLong rows
+            sk.when.push_back(rowGuard + " 0 " + std::to_string(kSplitRowsLong) + " 1 0");
+            sk.unless.push_back(rowGuard + " " + std::to_string(kSplitRows + 1) + " 4294967295 1 0");
+            sk.unless.push_back(cdim + " 0 " + std::to_string(uint64_t{kSplitLongVecs} * w.v - 1) + " 1 0");
+          }
           o << "extern \"C\" __global__ void __launch_bounds__(" << sk.block << ") " << sk.symbol << "(\n    " << sig
             << smSig << ") {\n  " << fn << "<" << w.v << "u" << (mapChunk ? ", " + std::to_string(mapChunk) + "u" : "")
             << ">(" << args << smArgs << ");\n}\n";
           std::ostringstream det;
           det << "row=runtime (" << cdim << " % " << w.mod << " == " << w.rem << ", " << klo << ".." << khi
-              << (rowGuard.empty() ? std::string() : ", rows <= " + std::to_string(kSplitRows)) << ": split, pass "
+              << (rowGuard.empty() ? std::string()
+                                   : ", rows <= " + std::to_string(kSplitRows) + ", or <= " +
+                                         std::to_string(kSplitRowsLong) + " of >= " +
+                                         std::to_string(uint64_t{kSplitLongVecs} * w.v))
+              << ": split, pass "
               << tag << ") vec=" << w.v
               << (merge ? " merge: one wave per row over <= " + std::to_string(kMaxParts) + " partials"
                         : (map ? " row map: " : " partial: ") + std::to_string(kPartBlock) + " lanes per chunk of >= " +

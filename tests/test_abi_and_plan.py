@@ -1026,13 +1026,17 @@ def test_single_pass_stream_nest_keeps_one_cache_depth():
     # longer rows: streamed from 256 rows on, split into passes below
     (256, 32772, ["s4"]), (255, 32772, ["p4_1", "w4_3"]),
     (1, 1 << 20, ["p4_1", "w4_3"]), (2, 16386, ["p2_1", "w2_3"]),
-    (7, 8193, ["p1_1", "w1_3"]), (300, 8193, ["s1"])])
+    (7, 8193, ["p1_1", "w1_3"]), (300, 8193, ["s1"]),
+    # more rows split too when each holds >= 16384 vectors, up to 4095 rows
+    (256, 65536, ["p4_1", "w4_3"]), (256, 65532, ["s4"]), (4095, 65536, ["p4_1", "w4_3"]),
+    (4096, 65536, ["s4"]), (1000, 16385, ["p1_1", "w1_3"]), (1000, 16383, ["s1"]), (300, 32770, ["p2_1", "w2_3"])])
 def test_multipass_split_selection(R, C, variants):
     """Few long rows of a nest of several passes (softmax: max, sum, map):
     each pass over its own grid of row chunks, in pass order; the max and
     the exp-sum share one read (pass 1's partial, the online normaliser), so
     pass 2 has no kernels, and the row map (pass 3) merges their partials
-    itself, so no merge kernel runs either."""
+    itself, so no merge kernel runs either. Up to 4095 rows of at least
+    16384 vectors split as well; shorter rows and more rows stream."""
     e = programs.CONFIG_PROGRAMS["softmax_dyn"]().emit()
     rc, h = parse(e.plan)
     assert rc == 0, _lib.last_error()

@@ -158,10 +158,11 @@ def test_stream_empty_grid(gpu):
 
 
 # Few long rows of a multi-pass nest: one grid of row chunks per pass (rows <=
-# 255 in the streamed range), against the streamed kernel (256 rows) and the
-# oracle; V 4, 2 and 1 rows, chunk counts from 3 to 512.
+# 255 in the streamed range, or up to 4095 rows of >= 16384 vectors), against
+# the streamed kernel (256 rows of 8250 vectors) and the oracle; V 4, 2 and 1
+# rows, chunk counts from 3 to 512.
 MULTIPASS_SPLIT_SHAPES = [(1, 40000), (7, 32772), (3, 100003), (2, 1_000_002), (255, 33000), (256, 33000),
-                          (1, 4_000_000)]
+                          (1, 4_000_000), (300, 65540), (1000, 16385)]
 
 
 @pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["online", "passes"])
