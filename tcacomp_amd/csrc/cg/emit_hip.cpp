@@ -2295,6 +2295,22 @@ class Emitter {
           << " + row_base + static_cast<uint64_t>(v) * V);\n";
       o << "      }\n    }\n";
     }
+    // The exp-sum of a softmax pair (a max, then a sum of expf(E - max)) in
+    // the general register-cached body: its terms take the hardware
+    // exponential (tca::hip::exp_term, relative error <= 2.7e-6 for
+    // arguments down to -44, as the split rows' online normaliser sums), not
+    // ocml's expf. They only form the denominator; the row map's own expf is
+    // kept. Rows of 12000-32000 floats held in registers were bound by the
+    // two expf per element: 16384 x 32000 1012 -> 922 us, x 12000 324 -> 290
+    // us. The exact-fit bodies (EX) and the streamed one (NV = 0) keep expf:
+    // there the same change measured 1-7% slower. With pass fusion off every
+    // expf stays ocml's.
+    std::set<const ir::Chain*> expTermSum;
+    if (opts_.allow_pass_fusion)
+      for (size_t p = 0; p + 1 < passes.size(); ++p)
+        if (passes[p].size() == 1 && passes[p + 1].size() == 1 &&
+            OnlineMaxExpSum(g_, g_.chains[passes[p][0]], g_.chains[passes[p + 1][0]], geo))
+          expTermSum.insert(&g_.chains[passes[p + 1][0]]);
     // Element value of chain c at element q of the vector whose operands are
     // bound to x<t> (tiles and column vectors) at suffix `sfx`.
     auto elemValue = [&](std::ostringstream& os, const std::string& ind, const ir::Chain& c,
@@ -2306,6 +2322,13 @@ class Emitter {
         eg.Bind(c.root.fn.params[k], (kind == OpKind::RowTile || kind == OpKind::ColVec)
                                          ? "x" + std::to_string(op.tensor) + sfx + "[q]"
                                          : rowScalar(op));
+      }
+      if (expTermSum.count(&c)) {  // the body is expf(E - a) (OnlineMaxExpSum)
+        const std::string arg = eg.Gen(g_.exprs[c.root.fn.body].args[0]);
+        const std::string v = "v" + std::to_string(counter_++);
+        os << ind << "const float " << v << " = (EX || NV == 0u) ? expf(" << arg << ") : tca::hip::exp_term(" << arg
+           << ");\n";
+        return v;
       }
       return eg.Gen(c.root.fn.body);
     };
