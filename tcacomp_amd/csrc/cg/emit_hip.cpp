@@ -2401,7 +2401,9 @@ class Emitter {
       b << ind << "const bool ok" << sfx << " = EX || v" << sfx << " < VECS;\n";
       b << ind << "const uint32_t vc" << sfx << " = ok" << sfx << " ? v" << sfx << " : VECS - 1u;\n";
     };
-    for (size_t p = 0; p < passes.size(); ++p) {
+    // One pass of the row body. assign: the pass's results (r<chain>) were
+    // declared by the caller and are assigned here.
+    auto emitPass = [&](size_t p, bool assign) {
       const ir::Chain& c0 = g_.chains[passes[p][0]];
       const bool red = !c0.reduces.empty();
       if (IsRowScalarChain(c0, geo)) {
@@ -2418,7 +2420,7 @@ class Emitter {
         if (!isReg(st) || an_.hbm_local[st])
           o << "    if (active && lane == 0u) t" << st << "[" << Offset(st, c0.store_axes, coord) << "] = " << var
             << ";\n";
-        continue;
+        return;
       }
       o << "    // statement";
       for (int ci : passes[p]) o << " #" << ci;
@@ -2465,7 +2467,7 @@ class Emitter {
       work(b, p, "        ", false, "vc", "ok", "", false);
       b << "      }\n    }\n";
       o << b.str();
-      if (!red) continue;
+      if (!red) return;
       for (int ci : passes[p])
         o << "    part" << ci << " = tca::hip::seg_allreduce_rt(part" << ci << ", SEG, comb" << ci << ");\n";
       o << "    if (WPR > 1u) {\n      if ((threadIdx.x & 63u) == 0u) {\n";
@@ -2507,12 +2509,191 @@ class Emitter {
         }
         const std::string ST = CType(g_.tensors[st].elem);
         const std::string var = "r" + std::to_string(ci);
-        o << "    const " << ST << " " << var << " = " << val << ";\n";
+        o << "    " << (assign ? std::string() : "const " + ST + " ") << var << " = " << val << ";\n";
         regScalar[st] = var;
         if (!isReg(st) || an_.hbm_local[st])
           o << "    if (active && lane == 0u) t" << st << "[" << Offset(st, c.store_axes, coord) << "] = " << var
             << ";\n";
       }
+    };
+    // A softmax pair (a max, then the sum of expf(E - max)) or a mean with its
+    // centred sum of squares, in the streamed body (NV = 0): one read of the
+    // row instead of two. Each lane folds its vectors into the online pair
+    // (tca::hip::online_expsum_add) or the pairwise triple (sum, centred sum
+    // of squares, count: tca::hip::chan_add); the row's lanes meet by
+    // shuffles (both merges are symmetric, so every lane ends with the same
+    // value) and its waves through LDS in wave order. The register-cached
+    // bodies keep the two passes (the row is read from registers either way).
+    std::vector<int> streamPair(passes.size(), 0);  // 1 softmax (online), 2 mean and centred squares
+    if (opts_.allow_pass_fusion)
+      for (size_t p = 0; p + 1 < passes.size(); ++p) {
+        if (passes[p].size() != 1 || passes[p + 1].size() != 1 || (p > 0 && streamPair[p - 1])) continue;
+        const ir::Chain& A = g_.chains[passes[p][0]];
+        const ir::Chain& B = g_.chains[passes[p + 1][0]];
+        if (IsRowScalarChain(A, geo) || IsRowScalarChain(B, geo)) continue;
+        if (OnlineMaxExpSum(g_, A, B, geo))
+          streamPair[p] = 1;
+        else if (ChanRowMeanVar(g_, A, B, geo))
+          streamPair[p] = 2;
+      }
+    auto emitStreamPair = [&](size_t p) {
+      const bool online = streamPair[p] == 1;
+      const int ca = passes[p][0], cb = passes[p + 1][0];
+      const ir::Chain& A = g_.chains[ca];
+      const ir::Chain& B = g_.chains[cb];
+      const int ta = A.store_tensor, tb = B.store_tensor;
+      const std::string sa = std::to_string(ca), sb = std::to_string(cb);
+      const std::string ra = "r" + sa, rb = "r" + sb;
+      const std::string STA = CType(g_.tensors[ta].elem), STB = CType(g_.tensors[tb].elem);
+      o << "    // statements #" << ca << " #" << cb << ": "
+        << (online ? "max and exp-sum" : "sum and centred sum of squares")
+        << " in one read of a streamed row; the register-cached bodies run the two passes\n";
+      o << "    " << STA << " " << ra << ";\n    " << STB << " " << rb << ";\n";
+      o << "    if constexpr (NV > 0u) {\n";
+      emitPass(p, true);
+      emitPass(p + 1, true);
+      o << "    } else {\n";
+      const std::string I = "      ";
+      if (online)
+        o << I << "float om = -__builtin_inff(), os = 0.0f;\n";
+      else
+        o << I << "float cs = 0.0f, cm = 0.0f, cn = 0.0f;\n";
+      // The values of A's element expression for vector `sfx` into
+      // ev[at * V + q]; `ok`: the vector is the lane's (else -inf for the
+      // online pair, whose max and sum it then leaves unchanged).
+      auto values = [&](std::ostringstream& b, const std::string& ind, const std::string& sfx, uint32_t at,
+                        const std::string& ok) {
+        b << "#pragma unroll\n" << ind << "for (uint32_t q = 0; q < V; ++q) {\n";
+        std::ostringstream es;
+        const std::string ev = elemValue(es, ind + "  ", A, sfx);
+        b << es.str() << ind << "  ev[" << at << "u * V + q] = "
+          << (online && !ok.empty() ? ok + " ? " + ev + " : -__builtin_inff()" : ev) << ";\n" << ind << "}\n";
+      };
+      const std::string upd = online ? "tca::hip::online_expsum_add(om, os, ev);\n" : "tca::hip::chan_add(cs, cm, cn, ev);\n";
+      std::ostringstream b;
+      const std::string J = I + "  ", K = J + "  ";
+      b << I << "if (NLANE > 0u) {  // every lane of a streamed row holds >= 1 vector\n" << J << "{\n";
+      b << K << "const uint32_t vc = lane;\n";
+      operands(b, p, K, false, "vc", "");
+      b << K << "float ev[V];\n";
+      values(b, K, "", 0, "");
+      b << K << upd << J << "}\n" << J << "uint32_t k = 1u;\n";
+      b << J << "for (; k + " << kUnroll - 1 << "u < NLANE; k += " << kUnroll << "u) {\n";
+      for (uint32_t u = 0; u < kUnroll; ++u) index(b, K, "k + " + std::to_string(u) + "u", "_" + std::to_string(u));
+      for (uint32_t u = 0; u < kUnroll; ++u) operands(b, p, K, false, "vc_" + std::to_string(u), "_" + std::to_string(u));
+      b << K << "float ev[" << kUnroll << " * V];\n";
+      for (uint32_t u = 0; u < kUnroll; ++u)
+        values(b, K, "_" + std::to_string(u), u, "ok_" + std::to_string(u));
+      if (online) {
+        b << K << upd;
+      } else {  // a lane's last vector may be past the row: fold vector by vector then
+        b << K << "if (ok_" << kUnroll - 1 << ") {\n" << K << "  " << upd << K << "} else {\n";
+        for (uint32_t u = 0; u < kUnroll; ++u)
+          b << K << "  if (ok_" << u << ") tca::hip::chan_add_n<V>(cs, cm, cn, ev + " << u << "u * V);\n";
+        b << K << "}\n";
+      }
+      b << J << "}\n" << J << "for (; k < NLANE; ++k) {\n";
+      index(b, K, "k", "");
+      operands(b, p, K, false, "vc", "");
+      b << K << "float ev[V];\n";
+      values(b, K, "", 0, "ok");
+      if (online)
+        b << K << upd;
+      else
+        b << K << "if (ok) " << upd;
+      b << J << "}\n" << I << "}\n";
+      o << b.str();
+      // The row's lanes (SEG per segment), then its waves in order.
+      if (online) {
+        o << I << "for (uint32_t off = SEG >> 1; off > 0u; off >>= 1)\n"
+          << I << "  tca::hip::online_expsum_merge(om, os, __shfl_xor(om, off, 64), __shfl_xor(os, off, 64));\n";
+        o << I << "if (WPR > 1u) {\n" << J << "if ((threadIdx.x & 63u) == 0u) {\n" << K << "red" << sa
+          << "[threadIdx.x >> 6] = om;\n" << K << "red" << sb << "[threadIdx.x >> 6] = os;\n" << J << "}\n";
+        o << J << "__syncthreads();\n" << J << "const uint32_t w0 = (threadIdx.x >> 6) & ~(WPR - 1u);\n";
+        o << J << "om = red" << sa << "[w0];\n" << J << "os = red" << sb << "[w0];\n";
+        o << J << "for (uint32_t w = 1; w < WPR; ++w) tca::hip::online_expsum_merge(om, os, red" << sa << "[w0 + w], red"
+          << sb << "[w0 + w]);\n" << I << "}\n";
+      } else {
+        o << I << "__shared__ float rn" << sa << "[" << kBlock / 64 << "];\n";
+        o << I << "for (uint32_t off = SEG >> 1; off > 0u; off >>= 1)\n"
+          << I << "  tca::hip::chan_merge_present(cs, cm, cn, __shfl_xor(cs, off, 64), __shfl_xor(cm, off, 64), "
+             "__shfl_xor(cn, off, 64));\n";
+        o << I << "if (WPR > 1u) {\n" << J << "if ((threadIdx.x & 63u) == 0u) {\n" << K << "red" << sa
+          << "[threadIdx.x >> 6] = cs;\n" << K << "red" << sb << "[threadIdx.x >> 6] = cm;\n" << K << "rn" << sa
+          << "[threadIdx.x >> 6] = cn;\n" << J << "}\n";
+        o << J << "__syncthreads();\n" << J << "const uint32_t w0 = (threadIdx.x >> 6) & ~(WPR - 1u);\n";
+        o << J << "cs = red" << sa << "[w0];\n" << J << "cm = red" << sb << "[w0];\n" << J << "cn = rn" << sa << "[w0];\n";
+        o << J << "for (uint32_t w = 1; w < WPR; ++w)\n" << J << "  tca::hip::chan_merge_present(cs, cm, cn, red" << sa
+          << "[w0 + w], red" << sb << "[w0 + w], rn" << sa << "[w0 + w]);\n" << I << "}\n";
+      }
+      // A's result: init once (an empty row yields init), the fold, then
+      // its piped map.
+      {
+        const ir::ReduceStage& r = A.reduces[0];
+        ExprGen ig(g_, o, I, &counter_);
+        const std::string init = ig.Gen(r.init);
+        std::ostringstream fs;
+        ExprGen fg(g_, fs, J, &counter_);
+        fg.Bind(r.fn.params[0], init);
+        fg.Bind(r.fn.params[1], online ? "om" : "cs");
+        const std::string v = fg.Gen(r.fn.body);
+        const std::string T = CType(g_.exprs[A.root.fn.body].type);
+        o << I << T << " fin" << sa << " = " << init << ";\n";
+        o << I << "if (VECS > 0u) {\n" << fs.str() << J << "fin" << sa << " = " << v << ";\n" << I << "}\n";
+        std::string val = "fin" + sa;
+        if (A.has_piped) {
+          ExprGen pg(g_, o, I, &counter_);
+          pg.Bind(A.piped.fn.params[0], val);
+          for (size_t k = 0; k < A.piped.ops.size(); ++k) pg.Bind(A.piped.fn.params[k + 1], rowScalar(A.piped.ops[k]));
+          val = pg.Gen(A.piped.fn.body);
+        }
+        o << I << ra << " = " << val << ";\n";
+      }
+      regScalar[ta] = ra;
+      // B's reduced total against A's result: the sum of expf(t - a) as
+      // s * expf(m - a) (NaN when a is -inf: every term expf(-inf - -inf)),
+      // or the sum of squares about a as M2 + n (S / n - a)^2.
+      {
+        const ir::ReduceStage& r = B.reduces[0];
+        ExprGen ig(g_, o, I, &counter_);
+        const std::string init = ig.Gen(r.init);
+        std::ostringstream fs;
+        if (online)
+          fs << J << "const float ptotal = " << ra << " == -__builtin_inff() ? __builtin_nanf(\"\") : os * expf(om - " << ra
+             << ");\n";
+        else
+          fs << J << "const float pd = cs / cn - " << ra << ";\n" << J << "const float ptotal = cm + cn * pd * pd;\n";
+        ExprGen fg(g_, fs, J, &counter_);
+        fg.Bind(r.fn.params[0], init);
+        fg.Bind(r.fn.params[1], "ptotal");
+        const std::string v = fg.Gen(r.fn.body);
+        const std::string T = CType(g_.exprs[B.root.fn.body].type);
+        o << I << T << " fin" << sb << " = " << init << ";\n";
+        o << I << "if (VECS > 0u) {\n" << fs.str() << J << "fin" << sb << " = " << v << ";\n" << I << "}\n";
+        std::string val = "fin" + sb;
+        if (B.has_piped) {
+          ExprGen pg(g_, o, I, &counter_);
+          pg.Bind(B.piped.fn.params[0], val);
+          for (size_t k = 0; k < B.piped.ops.size(); ++k) pg.Bind(B.piped.fn.params[k + 1], rowScalar(B.piped.ops[k]));
+          val = pg.Gen(B.piped.fn.body);
+        }
+        o << I << rb << " = " << val << ";\n";
+      }
+      for (const auto& [t, ch] : {std::pair<int, const ir::Chain*>{ta, &A}, std::pair<int, const ir::Chain*>{tb, &B}})
+        if (!isReg(t) || an_.hbm_local[t])
+          o << I << "if (active && lane == 0u) t" << t << "[" << Offset(t, ch->store_axes, coord) << "] = r"
+            << (t == ta ? sa : sb) << ";\n";
+      o << "    }\n";
+      regScalar[ta] = ra;
+      regScalar[tb] = rb;
+    };
+    for (size_t p = 0; p < passes.size(); ++p) {
+      if (!streamPair[p]) {
+        emitPass(p, false);
+        continue;
+      }
+      emitStreamPair(p);
+      ++p;  // pass p + 1 is part of the pair
     }
     // Each reduction has its own LDS slots, written once per group: only a
     // next group (a grid-stride step, block-uniform) must wait until every

@@ -331,10 +331,11 @@ __device__ __forceinline__ void chan_merge_present(float& s, float& m2, float& n
   n += nb;
 }
 
-// Folds N values into (s, m2, n): their sum, their mean (N a power of two:
-// an exact scaling), their centred sum of squares, then chan_merge_present.
+// Folds the N values at v into (s, m2, n): their sum, their mean (N a
+// power of two: an exact scaling), their centred sum of squares, then
+// chan_merge_present.
 template <int N>
-__device__ __forceinline__ void chan_add(float& s, float& m2, float& n, const float (&v)[N]) {
+__device__ __forceinline__ void chan_add_n(float& s, float& m2, float& n, const float* v) {
   float gs = v[0];
 #pragma unroll
   for (int i = 1; i < N; ++i) gs += v[i];
@@ -346,6 +347,12 @@ __device__ __forceinline__ void chan_add(float& s, float& m2, float& n, const fl
     g2 = fmaf(d, d, g2);
   }
   chan_merge_present(s, m2, n, gs, g2, static_cast<float>(N));
+}
+
+// chan_add_n over an array of N values.
+template <int N>
+__device__ __forceinline__ void chan_add(float& s, float& m2, float& n, const float (&v)[N]) {
+  chan_add_n<N>(s, m2, n, v);
 }
 
 }  // namespace hip

@@ -1048,6 +1048,25 @@ def test_multipass_split_selection(R, C, variants):
     _lib.lib().tca_program_unload(h)
 
 
+@pytest.mark.parametrize("name,pair", [("softmax_dyn", "tca::hip::online_expsum_add(om, os, ev);"),
+                                       ("layernorm_dyn", "tca::hip::chan_add(cs, cm, cn, ev);")])
+def test_streamed_pair_shares_one_read(name, pair):
+    """The streamed body (more rows than split, or rows too long for the
+    register cache) folds the softmax's max and exp-sum, or layernorm's sum
+    and centred sum of squares, in one read of the row; the register-cached
+    bodies keep the two passes (both under one template, the branch on NV);
+    without pass fusion the streamed body reads the row once per pass."""
+    def rows_body(src):  # the row body: up to the next function template
+        at = src.index("_rows(")
+        return src[at:src.index("\ntemplate <", at)]
+
+    body = rows_body(programs.CONFIG_PROGRAMS[name]().emit().source)
+    assert "in one read of a streamed row" in body and "    if constexpr (NV > 0u) {" in body
+    assert body.count(pair) == 3  # the lane's first vector, the unrolled loop, the tail
+    body = rows_body(programs.CONFIG_PROGRAMS[name]().emit(flags=EMIT_NO_PASS_FUSION).source)
+    assert "in one read of a streamed row" not in body and pair not in body
+
+
 @pytest.mark.parametrize("flags,C,variants", [
     (0, 1 << 20, ["p4_1", "wl4_3"]), (0, 262140, ["p4_1", "w4_3"]), (0, 262142, ["p2_1", "wl2_3"]),
     (EMIT_NO_PASS_FUSION, 1 << 20, ["p4_1", "m4_1", "p4_2", "m4_2", "w4_3"])])

@@ -358,3 +358,104 @@ def test_split_layernorm(gpu, R, C, flags):
     print("split C4 R=%d C=%d: max |gpu - oracle| %.3g" % (R, C, diff))
     if C <= 1_100_000:  # at 4 M terms the sequential fold alone is off by ~1.2e-2
         assert diff <= 2e-3
+
+
+# Streamed rows of a multi-pass nest (too long for the register cache, too
+# many or too short to split): V 4, 2 and 1, 256 to 4100 rows, rows of 8193
+# to 20001 vectors (every lane 8 to 20 vectors, a ragged last round).
+STREAMED_PAIR_SHAPES = [(256, 40000), (300, 20002), (257, 12001), (4100, 20001), (4096, 32772)]
+
+
+@pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["online", "passes"])
+@pytest.mark.parametrize("R,C", STREAMED_PAIR_SHAPES)
+def test_streamed_softmax(gpu, R, C, flags):
+    """The streamed body folds the max and the exp-sum in one read of the
+    row (each lane's online pair, merged over the row's lanes and waves);
+    unfused, one read per pass. Against the oracle."""
+    _say("streamed C3", R, C, flags)
+    x = inputs.normal((R, C), 2.0, 5)
+    want = oracle.softmax(x)
+    y = out_dev((R, C), gpu)
+    run(compiled("softmax_dyn", flags), [to_dev(x, gpu), y])
+    got = host(y)
+    assert canaries(got) == 0
+    rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want.astype(np.float64)), 1e-30)
+    assert rel.max() <= reduce_tol(C), "softmax relative error %g" % rel.max()
+    assert np.abs(got.astype(np.float64).sum(1) - 1.0).max() <= reduce_tol(C)
+
+
+@pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["pairwise", "passes"])
+@pytest.mark.parametrize("R,C", STREAMED_PAIR_SHAPES)
+def test_streamed_layernorm(gpu, R, C, flags):
+    """The streamed body folds the sum and the centred sum of squares in one
+    read of the row (each lane's pairwise triple, merged over the row's
+    lanes and waves); unfused, one read per pass. Against the float64
+    evaluation of the formula, and the oracle within the reference's own
+    end-to-end tolerance."""
+    _say("streamed C4", R, C, flags)
+    x = inputs.normal((R, C), 1.0, 5)
+    g, b = inputs.uniform((C,), 0.5, 1.5, 1), inputs.uniform((C,), -0.1, 0.1, 2)
+    inv_n, eps = float(np.float32(1.0 / C)), 1e-5
+    want = oracle.layernorm(x, g, b, inv_n, eps)
+    y = out_dev((R, C), gpu)
+    run(compiled("layernorm_dyn", flags), [to_dev(x, gpu), to_dev(g, gpu), to_dev(b, gpu), y], scalars=[inv_n, eps])
+    got = host(y)
+    assert canaries(got) == 0
+    xd = x.astype(np.float64)
+    mean = xd.sum(1, keepdims=True) * inv_n
+    var = ((xd - mean) ** 2).sum(1, keepdims=True) * inv_n
+    want64 = (xd - mean) / np.sqrt(var + eps) * g.astype(np.float64) + b.astype(np.float64)
+    assert_layernorm_close(got, want64, x, g, b, eps, "streamed C4 R=%d C=%d vs float64" % (R, C))
+    assert float(np.abs(got.astype(np.float64) - want).max()) <= 2e-3
+
+
+@pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["fused", "passes"])
+@pytest.mark.parametrize("R,C", [(256, 40000), (4100, 20001)])
+def test_streamed_special_rows(gpu, R, C, flags):
+    """Streamed softmax and layernorm rows holding special values, as the
+    split tests hold them: softmax rows with -inf entries (0 out), only
+    -inf (NaN), a +inf or a NaN entry (NaN), the maximum first or last;
+    layernorm rows offset by 1000, constant (variance 0), a step between
+    the halves, +inf, NaN, and a small spread. The other rows are normal."""
+    _say("streamed special rows", R, C, flags)
+    x = inputs.normal((R, C), 2.0, 4)
+    x[0, ::7] = -np.inf
+    x[1, :] = -np.inf
+    x[2, C // 3] = np.inf
+    x[3, C // 2] = np.nan
+    x[4, 0] = 40.0
+    x[5, -1] = 40.0
+    want = oracle.softmax(x)
+    y = out_dev((R, C), gpu)
+    run(compiled("softmax_dyn", flags), [to_dev(x, gpu), y])
+    got = host(y)
+    assert np.array_equal(np.isnan(got), np.isnan(want)), [int(np.isnan(got[i]).sum()) for i in range(6)]
+    fin = ~np.isnan(want)
+    rel = np.abs(got[fin].astype(np.float64) - want[fin]) / np.maximum(np.abs(want[fin].astype(np.float64)), 1e-30)
+    assert rel.max() <= reduce_tol(C), "softmax relative error %g" % rel.max()
+    assert np.all(got[0, ::7] == 0.0)
+    assert np.isnan(got[1]).all() and np.isnan(got[2]).all() and np.isnan(got[3]).all()
+
+    x = inputs.normal((R, C), 1.0, 6)
+    x[0] += 1000.0
+    x[1] = 3.0
+    x[2, : C // 2] -= 5.0
+    x[2, C // 2:] += 5.0
+    x[3, C // 3] = np.inf
+    x[4, C // 2] = np.nan
+    x[5] *= 1e-3
+    g, b = inputs.uniform((C,), 0.5, 1.5, 1), inputs.uniform((C,), -0.1, 0.1, 2)
+    inv_n, eps = float(np.float32(1.0 / C)), 1e-5
+    want = oracle.layernorm(x, g, b, inv_n, eps)
+    y = out_dev((R, C), gpu)
+    run(compiled("layernorm_dyn", flags), [to_dev(x, gpu), to_dev(g, gpu), to_dev(b, gpu), y], scalars=[inv_n, eps])
+    got = host(y)
+    assert canaries(got) == 0
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.isnan(got[3]).all() and np.isnan(got[4]).all()
+    fin = [i for i in range(R) if i not in (3, 4)]
+    xd = x[fin].astype(np.float64)
+    mean = xd.sum(1, keepdims=True) * inv_n
+    var = ((xd - mean) ** 2).sum(1, keepdims=True) * inv_n
+    want64 = (xd - mean) / np.sqrt(var + eps) * g.astype(np.float64) + b.astype(np.float64)
+    assert_layernorm_close(got[fin], want64, x[fin], g, b, eps, "streamed C4 special rows R=%d C=%d" % (R, C))
