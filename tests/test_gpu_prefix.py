@@ -41,3 +41,11 @@ def test_prefix_row_family(gpu, R):
 @pytest.mark.parametrize("R", [1, 37])
 def test_prefix_stream_family(gpu, R, C):
     _check("layernorm_rstd_dyn", R, C, gpu)
+
+
+@pytest.mark.parametrize("R,C", [(300, 40000), (4100, 20001)])
+def test_prefix_streamed_rows(gpu, R, C):
+    """Streamed rows (beyond the register cache, too many to split): the
+    mean and the centred sum of squares in one read, then the per-row rstd
+    chain and the row map."""
+    _check("layernorm_rstd_dyn", R, C, gpu)

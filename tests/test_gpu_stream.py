@@ -228,12 +228,13 @@ def test_split_rows_at_the_element_limit(gpu, C):
 
 
 @pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["pairwise", "passes"])
-@pytest.mark.parametrize("R,C", [(7, 40000), (3, 100_003), (5, 300_000), (2, 1_000_002)])
+@pytest.mark.parametrize("R,C", [(7, 40000), (3, 100_003), (5, 300_000), (2, 1_000_002), (300, 40000), (4100, 20001)])
 def test_split_row_stats_shift(gpu, R, C, flags):
     """A mean whose piped map adds a per-row input (m = sum(x) inv_n +
     shift[r]) and a sum of squares about it whose piped map reads m (rs =
     rsqrtf(T inv_n + eps) + m / 2), both outputs, then y = (x - m) rs; split
-    rows in both lowerings, V 4, 1 and 2, the 1x and 4x row-map chunks.
+    rows in both lowerings, V 4, 1 and 2, the 1x and 4x row-map chunks, and
+    streamed rows (300 of 40000, 4100 of 20001: the pair in one read).
     m against the float64 sum (the reduction tolerance on ||x||_2, plus the
     piped map's two roundings); rs against float64 from the device's m
     (T = sum (x - m)^2 to the reduction tolerance on ||(x - m)^2||_2,
