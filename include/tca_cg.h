@@ -58,8 +58,9 @@ enum { TCA_NEG = 0, TCA_POS, TCA_LNOT, TCA_NOT };
  * TCA_EMIT_NO_GEMM_SPLIT leaves out the contractions' small-tile K-split
  * kernels (every output plane then takes the 128/256 tile kernels).
  * TCA_EMIT_NO_PASS_FUSION keeps every pass of a multi-pass nest its own read
- * of the input (no online softmax normaliser in split rows, no pairwise
- * mean/variance in the column family). */
+ * of the input (no online softmax normaliser and no pairwise mean/variance
+ * in split or streamed rows, no pairwise mean/variance in the column
+ * family). */
 enum { TCA_EMIT_NO_FUSION = 1, TCA_EMIT_NO_GEMM = 2, TCA_EMIT_NO_GEMM_SPLIT = 4, TCA_EMIT_NO_PASS_FUSION = 8 };
 #define TCA_EMIT_ROW_VECTORS(n) ((n) << 8)
 #define TCA_EMIT_EW_UNROLL(n) ((n) << 12)
