@@ -161,6 +161,64 @@ def row_stats_shift(cols=0):
     return b.Build()
 
 
+def softmax_affine(cols=0):
+    """Softmax of E = x * t + bias[c] (t a scalar parameter, bias a column
+    vector), its max and exp-sum also stored: mx = max E, den = sum expf(E -
+    mx), y = expf(E - mx) / den. The one-read pair's element expression then
+    reads a scalar and a column vector besides the row."""
+    b = NewBuilder("softmax_affine_%s" % (cols or "dyn"))
+    R, C = b.Dim("R", 0), _static(b, "C", cols)
+    x = b.Tensor("x", TF32, R, C)
+    bias = b.Tensor("bias", TF32, C)
+    mx = b.Tensor("mx", TF32, R)
+    den = b.Tensor("den", TF32, R)
+    y = b.Tensor("y", TF32, R, C)
+    t = b.ScalarParam("t", TF32)
+
+    def e(v, c):
+        return b.Add(b.Mul(v, t), c)
+
+    (b.Stmt().Iter(R, C).Map([At(x, R, C), At(bias, C)], e).As(R, C)
+     .Reduce(_neg_inf(b), lambda acc, v: Call("fmaxf", acc, v)).Store(mx, R))
+    (b.Stmt().Iter(R, C).Map([At(x, R, C), At(bias, C), At(mx, R)], lambda v, c, m: Call("expf", b.Sub(e(v, c), m)))
+     .As(R, C).Reduce(b.Float32(0), _sum(b)).Store(den, R))
+    (b.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(bias, C), At(mx, R), At(den, R)], lambda v, c, m, s: b.Div(Call("expf", b.Sub(e(v, c), m)), s))
+     .As(R, C).Store(y, R, C))
+    return b.Build()
+
+
+def row_moments_affine(cols=0):
+    """The mean and variance of E = x * g[c] + r[row] (a column and a row
+    vector), both stored: m = sum(E) * inv_n, v = sum((E - m)^2) * inv_n,
+    then y = (E - m) * rsqrtf(v + eps). The one-read pair's element
+    expression then reads a column and a row vector besides the row."""
+    b = NewBuilder("row_moments_affine_%s" % (cols or "dyn"))
+    R, C = b.Dim("R", 0), _static(b, "C", cols)
+    x = b.Tensor("x", TF32, R, C)
+    g = b.Tensor("g", TF32, C)
+    r = b.Tensor("r", TF32, R)
+    m = b.Tensor("m", TF32, R)
+    var = b.Tensor("v", TF32, R)
+    y = b.Tensor("y", TF32, R, C)
+    inv_n = b.ScalarParam("inv_n", TF32)
+    eps = b.ScalarParam("eps", TF32)
+
+    def e(v, c, w):
+        return b.Add(b.Mul(v, c), w)
+
+    (b.Stmt().Iter(R, C).Map([At(x, R, C), At(g, C), At(r, R)], e).As(R, C)
+     .Reduce(b.Float32(0), _sum(b)).Map([], lambda s: b.Mul(s, inv_n)).As(R).Store(m, R))
+    (b.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(g, C), At(r, R), At(m, R)], lambda v, c, w, a: b.Mul(b.Sub(e(v, c, w), a), b.Sub(e(v, c, w), a)))
+     .As(R, C).Reduce(b.Float32(0), _sum(b)).Map([], lambda s: b.Mul(s, inv_n)).As(R).Store(var, R))
+    (b.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(g, C), At(r, R), At(m, R), At(var, R)],
+          lambda v, c, w, a, q: b.Mul(b.Sub(e(v, c, w), a), Call("rsqrtf", b.Add(q, eps))))
+     .As(R, C).Store(y, R, C))
+    return b.Build()
+
+
 def layernorm_rstd(cols=1024):
     """C4 with the reciprocal standard deviation as its own per-row chain
     (iterating only the row axis, one level shallower than the others) and
@@ -836,6 +894,8 @@ CONFIG_PROGRAMS = {
     "layernorm_rstd_1024": lambda: layernorm_rstd(1024),
     "layernorm_rstd_dyn": lambda: layernorm_rstd(0),
     "row_stats_shift_dyn": lambda: row_stats_shift(0),
+    "softmax_affine_dyn": lambda: softmax_affine(0),
+    "row_moments_affine_dyn": lambda: row_moments_affine(0),
     # the expression layer: every operator, builtin and cast on the device
     "expr_f32": lambda: _expr_program("expr_f32", TF32, EXPR_F32),
     "expr_i32": lambda: _expr_program("expr_i32", TI32, EXPR_I32),
@@ -879,7 +939,7 @@ def all_builds():
 # Programs whose passes fuse into one read by default (online softmax
 # normaliser, pairwise mean/variance); the tests also run them unfused.
 PASS_FUSED = ("softmax_dyn", "layernorm_dyn", "row_stats_shift_dyn", "col_mean_var_dyn", "col_mean_var_l_dyn",
-              "col_mean_var_bf16")
+              "col_mean_var_bf16", "softmax_affine_dyn", "row_moments_affine_dyn")
 
 
 # Contractions the tests also run with EMIT_NO_GEMM_SPLIT (the 128/256 tile

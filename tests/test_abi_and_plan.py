@@ -1049,7 +1049,9 @@ def test_multipass_split_selection(R, C, variants):
 
 
 @pytest.mark.parametrize("name,pair", [("softmax_dyn", "tca::hip::online_expsum_add(om, os, ev);"),
-                                       ("layernorm_dyn", "tca::hip::chan_add(cs, cm, cn, ev);")])
+                                       ("layernorm_dyn", "tca::hip::chan_add(cs, cm, cn, ev);"),
+                                       ("softmax_affine_dyn", "tca::hip::online_expsum_add(om, os, ev);"),
+                                       ("row_moments_affine_dyn", "tca::hip::chan_add(cs, cm, cn, ev);")])
 def test_streamed_pair_shares_one_read(name, pair):
     """The streamed body (more rows than split, or rows too long for the
     register cache) folds the softmax's max and exp-sum, or layernorm's sum

@@ -460,3 +460,77 @@ def test_streamed_special_rows(gpu, R, C, flags):
     var = ((xd - mean) ** 2).sum(1, keepdims=True) * inv_n
     want64 = (xd - mean) / np.sqrt(var + eps) * g.astype(np.float64) + b.astype(np.float64)
     assert_layernorm_close(got[fin], want64, x[fin], g, b, eps, "streamed C4 special rows R=%d C=%d" % (R, C))
+
+
+# Register-cached (4- and 8-deep), streamed (4- and 1-wide) and split rows
+# (1x and 4x row-map chunks).
+AFFINE_SHAPES = [(37, 5000), (37, 20002), (300, 40000), (4100, 20001), (3, 100_003), (2, 1_000_002)]
+
+
+@pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["online", "passes"])
+@pytest.mark.parametrize("R,C", AFFINE_SHAPES)
+def test_pair_affine_softmax(gpu, R, C, flags):
+    """Softmax of E = x t + bias[c] with its max and exp-sum stored: the
+    one-read pair's element expression reads a scalar and a column vector.
+    Against float64 from the same float32 inputs: E's own rounding (the
+    device may contract x t + bias into one fma) moves each exponent by
+    <= u (|x t| + |E|), so the outputs get that on top of the reduction
+    tolerance, and the max is within it."""
+    _say("affine softmax", R, C, flags)
+    x = inputs.normal((R, C), 2.0, 11)
+    bias = inputs.uniform((C,), -1.0, 1.0, 12)
+    t = 0.7
+    mx, den, y = out_dev((R,), gpu), out_dev((R,), gpu), out_dev((R, C), gpu)
+    run(compiled("softmax_affine_dyn", flags), [to_dev(x, gpu), to_dev(bias, gpu), mx, den, y], scalars=[t])
+    gm, gd, gy = host(mx).astype(np.float64), host(den).astype(np.float64), host(y)
+    assert canaries(gy) == 0 and canaries(host(mx)) == 0 and canaries(host(den)) == 0
+    u = 2.0 ** -24
+    P = x.astype(np.float64) * np.float64(np.float32(t))
+    E = P + bias.astype(np.float64)
+    e_round = u * (np.abs(P) + np.abs(E))  # E's rounding: an fma, or a product and a sum
+    m64 = E.max(1)
+    assert np.all(np.abs(gm - m64) <= e_round.max(1)), np.abs(gm - m64).max()
+    # against the device's max: the terms and the sum carry E's rounding
+    p = np.exp(E - gm[:, None])
+    d64 = p.sum(1)
+    e_tol = reduce_tol(C) + 2 * e_round.max() + 2 * u * np.abs(gm).max()
+    assert np.all(np.abs(gd - d64) <= e_tol * d64), (np.abs(gd - d64) / d64).max()
+    y64 = p / d64[:, None]
+    rel = np.abs(gy.astype(np.float64) - y64) / np.maximum(y64, 1e-30)
+    assert rel.max() <= 2 * e_tol, "affine softmax relative error %g" % rel.max()
+
+
+@pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["pairwise", "passes"])
+@pytest.mark.parametrize("R,C", AFFINE_SHAPES)
+def test_pair_affine_moments(gpu, R, C, flags):
+    """Mean and variance of E = x g[c] + r[row], both stored, then y = (E -
+    m) rsqrtf(v + eps): the one-read pair's element expression reads a
+    column and a row vector. Against float64 from the same float32 inputs,
+    with E's own rounding (<= u (|x g| + |E|), an fma or a product and a
+    sum) on top of the reduction tolerance; y from the device's m and v."""
+    _say("affine moments", R, C, flags)
+    x = inputs.normal((R, C), 1.0, 13)
+    g = inputs.uniform((C,), 0.5, 1.5, 14)
+    r = inputs.uniform((R,), -2.0, 2.0, 15)
+    inv_n, eps = float(np.float32(1.0 / C)), 1e-5
+    m, v, y = out_dev((R,), gpu), out_dev((R,), gpu), out_dev((R, C), gpu)
+    run(compiled("row_moments_affine_dyn", flags), [to_dev(x, gpu), to_dev(g, gpu), to_dev(r, gpu), m, v, y],
+        scalars=[inv_n, eps])
+    gm, gv, gy = host(m).astype(np.float64), host(v).astype(np.float64), host(y).astype(np.float64)
+    assert canaries(gy) == 0 and canaries(host(m)) == 0 and canaries(host(v)) == 0
+    u, tol = 2.0 ** -24, reduce_tol(C)
+    P = x.astype(np.float64) * g.astype(np.float64)
+    E = P + r.astype(np.float64)[:, None]
+    e_round = u * (np.abs(P) + np.abs(E))  # E's rounding: an fma, or a product and a sum
+    s64 = E.sum(1) * inv_n
+    bound_m = (tol * np.sqrt((E * E).sum(1)) + e_round.sum(1)) * inv_n + 2 * u * np.abs(s64)
+    assert np.all(np.abs(gm - s64) <= bound_m), (np.abs(gm - s64) / bound_m).max()
+    d = E - gm[:, None]
+    v64 = (d * d).sum(1) * inv_n
+    bound_v = (tol * np.sqrt((d ** 4).sum(1)) + 2 * (np.abs(d) * e_round).sum(1)) * inv_n + 2 * u * v64
+    assert np.all(np.abs(gv - v64) <= bound_v), (np.abs(gv - v64) / bound_v).max()
+    rs = 1.0 / np.sqrt(gv + eps)
+    y64 = d * rs[:, None]
+    # E - m rounded, rsqrtf (a few ulp) of v + eps rounded, the product rounded
+    bound_y = (e_round + 2 * u * np.abs(d)) * rs[:, None] + 8 * u * np.abs(y64)
+    assert np.all(np.abs(gy - y64) <= bound_y), (np.abs(gy - y64) / np.maximum(bound_y, 1e-300)).max()
