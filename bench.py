@@ -50,6 +50,8 @@ CONFIGS = {
     # row chunks (partial + merge per reduction pass, a chunked row map)
     "c3r": ("softmax_dyn", "row softmax f32 [64,1048576] (few long rows: passes split over row chunks)"),
     "c4r": ("layernorm_dyn", "row layernorm f32 [64,1048576] (few long rows: passes split over row chunks)"),
+    "c3v": ("softmax_dyn", "row softmax f32 [4096,40000] (streamed rows: max and exp-sum in one read, then the row map)"),
+    "c4v": ("layernorm_dyn", "row layernorm f32 [4096,40000] (streamed rows: mean and centred squares in one read, then the row map)"),
     # C2's reductions over narrow element types (16-byte vectors of 8 bf16 /
     # 16 u8 elements): not configurations, the same family on other dtypes
     "c2h": ("row_sum_bf16_dyn", "row sum+max bf16 -> f32 [8192,16384] (streaming family)"),
@@ -209,6 +211,26 @@ def _setup(key, dev):
         cpu = None
     elif key == "c4r":
         R, C = 64, 1 << 20
+        x = inputs.normal((R, C), 1.0, 0)
+        g = inputs.uniform((C,), 0.5, 1.5, 1)
+        bt = inputs.uniform((C,), -0.1, 0.1, 2)
+        algo = 2 * R * C * 4 + 2 * C * 4
+        per_set = algo
+        make = lambda i: [dev_f32(x), dev_f32(g), dev_f32(bt), torch.empty((R, C), device=dev)]  # noqa: E731
+        scalars = [1.0 / C, 1e-5]
+        work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = None
+    elif key == "c3v":
+        R, C = 4096, 40000
+        x = inputs.normal((R, C), 2.0, 0)
+        algo = 2 * R * C * 4
+        per_set = algo
+        make = lambda i: [dev_f32(x), torch.empty((R, C), device=dev)]  # noqa: E731
+        scalars = []
+        work = {"bytes": algo, "bound": "hbm", "shape": [R, C]}
+        cpu = None
+    elif key == "c4v":
+        R, C = 4096, 40000
         x = inputs.normal((R, C), 1.0, 0)
         g = inputs.uniform((C,), 0.5, 1.5, 1)
         bt = inputs.uniform((C,), -0.1, 0.1, 2)
@@ -505,7 +527,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c3r,c4r,c2h,c2u,c2c,c2mv,c2mw,c5b8,c5h,c1t,c1m")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5f,c5b,c2s,c3s,c4s,c2v,c2r,c3r,c4r,c3v,c4v,c2h,c2u,c2c,c2mv,c2mw,c5b8,c5h,c1t,c1m")
     ap.add_argument("--settle-ms", type=float, default=1000.0,
                     help="untimed launches per config before the warmup steps, in wall-clock ms")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
