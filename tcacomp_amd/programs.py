@@ -219,6 +219,25 @@ def row_moments_affine(cols=0):
     return b.Build()
 
 
+def softmax_bf16(cols=0):
+    """Softmax of bf16 rows computed in f32 (Cast per element) into an f32
+    output: the one-read pair over 8-byte bf16 vectors."""
+    b = NewBuilder("softmax_bf16_%s" % (cols or "dyn"))
+    R, C = b.Dim("R", 0), _static(b, "C", cols)
+    x = b.Tensor("x", TBF16, R, C)
+    y = b.Tensor("y", TF32, R, C)
+    mx = b.Local("mx", TF32, R)
+    den = b.Local("den", TF32, R)
+    (b.Stmt().Iter(R, C).Map([At(x, R, C)], lambda v: Cast(v, TF32)).As(R, C)
+     .Reduce(_neg_inf(b), lambda acc, v: Call("fmaxf", acc, v)).Store(mx, R))
+    (b.Stmt().Iter(R, C).Map([At(x, R, C), At(mx, R)], lambda l, r: Call("expf", b.Sub(Cast(l, TF32), r)))
+     .As(R, C).Reduce(b.Float32(0), _sum(b)).Store(den, R))
+    (b.Stmt().Iter(R, C)
+     .Map([At(x, R, C), At(mx, R), At(den, R)], lambda l, r, s: b.Div(Call("expf", b.Sub(Cast(l, TF32), r)), s))
+     .As(R, C).Store(y, R, C))
+    return b.Build()
+
+
 def layernorm_rstd(cols=1024):
     """C4 with the reciprocal standard deviation as its own per-row chain
     (iterating only the row axis, one level shallower than the others) and
@@ -896,6 +915,7 @@ CONFIG_PROGRAMS = {
     "row_stats_shift_dyn": lambda: row_stats_shift(0),
     "softmax_affine_dyn": lambda: softmax_affine(0),
     "row_moments_affine_dyn": lambda: row_moments_affine(0),
+    "softmax_bf16_dyn": lambda: softmax_bf16(0),
     # the expression layer: every operator, builtin and cast on the device
     "expr_f32": lambda: _expr_program("expr_f32", TF32, EXPR_F32),
     "expr_i32": lambda: _expr_program("expr_i32", TI32, EXPR_I32),
@@ -939,7 +959,7 @@ def all_builds():
 # Programs whose passes fuse into one read by default (online softmax
 # normaliser, pairwise mean/variance); the tests also run them unfused.
 PASS_FUSED = ("softmax_dyn", "layernorm_dyn", "row_stats_shift_dyn", "col_mean_var_dyn", "col_mean_var_l_dyn",
-              "col_mean_var_bf16", "softmax_affine_dyn", "row_moments_affine_dyn")
+              "col_mean_var_bf16", "softmax_affine_dyn", "row_moments_affine_dyn", "softmax_bf16_dyn")
 
 
 # Contractions the tests also run with EMIT_NO_GEMM_SPLIT (the 128/256 tile

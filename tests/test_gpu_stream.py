@@ -534,3 +534,22 @@ def test_pair_affine_moments(gpu, R, C, flags):
     # E - m rounded, rsqrtf (a few ulp) of v + eps rounded, the product rounded
     bound_y = (e_round + 2 * u * np.abs(d)) * rs[:, None] + 8 * u * np.abs(y64)
     assert np.all(np.abs(gy - y64) <= bound_y), (np.abs(gy - y64) / np.maximum(bound_y, 1e-300)).max()
+
+
+@pytest.mark.parametrize("flags", [0, EMIT_NO_PASS_FUSION], ids=["online", "passes"])
+@pytest.mark.parametrize("R,C", AFFINE_SHAPES)
+def test_pair_softmax_bf16_rows(gpu, R, C, flags):
+    """Softmax of bf16 rows computed in f32 (a Cast per element) into an f32
+    output: the pair's loads are 8-byte bf16 vectors. Against the oracle fed
+    the bf16 values widened to f32 (exact), so the arithmetic is the same."""
+    _say("bf16 softmax", R, C, flags)
+    xb = oracle.to_bf16_bits(inputs.normal((R, C), 2.0, 16))
+    want = oracle.softmax(oracle.bf16_bits_to_f32(xb))
+    import torch
+    y = out_dev((R, C), gpu)
+    run(compiled("softmax_bf16_dyn", flags), [to_dev(xb.view(np.int16), gpu).view(torch.bfloat16), y])
+    got = host(y)
+    assert canaries(got) == 0
+    rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want.astype(np.float64)), 1e-30)
+    assert rel.max() <= reduce_tol(C), "bf16 softmax relative error %g" % rel.max()
+    assert np.abs(got.astype(np.float64).sum(1) - 1.0).max() <= reduce_tol(C)
