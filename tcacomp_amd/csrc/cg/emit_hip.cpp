@@ -3466,8 +3466,19 @@ class Emitter {
     // is set by its cache depth; 16 vectors spilled to scratch for 16- and
     // 8-byte vectors). A single pass reads the row once either way and keeps
     // the 4-vector cache only.
+    // A column vector read by several passes stays live across them (the
+    // compiler keeps its loads for the later passes): 8 more vectors beside
+    // the 8-deep cached row spill to scratch, so such nests keep the 4-deep
+    // cache and stream longer rows.
+    size_t colVecPasses = 0;
+    for (const auto& ps : passes) {
+      bool reads = false;
+      for (int ci : ps)
+        for (const auto& op : g_.chains[ci].root.ops) reads = reads || Classify(op, geo) == OpKind::ColVec;
+      colVecPasses += reads ? 1 : 0;
+    }
     std::vector<uint32_t> caches = {kCache};
-    if (passes.size() > 1) caches.push_back(2 * kCache);
+    if (passes.size() > 1 && colVecPasses < 2) caches.push_back(2 * kCache);
     const uint64_t cachedVecs = uint64_t{kBlock} * caches.back();
     const std::string symbol = pk.symbol;
     const std::string rowGuard =

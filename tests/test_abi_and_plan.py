@@ -997,22 +997,29 @@ def test_elementwise_three_transposed_operands_keep_64_tiles():
     assert "kernel tca_ew_tr3_k0 256 0 3 1/1 R/64 C/64" in e.plan
 
 
-@pytest.mark.parametrize("name", ["softmax_dyn", "layernorm_dyn", "layernorm_rstd_dyn"])
-def test_stream_row_caches_fit_registers(name, tmp_path):
+@pytest.mark.parametrize("name,deep", [("softmax_dyn", True), ("layernorm_dyn", True), ("layernorm_rstd_dyn", True),
+                                       ("row_stats_shift_dyn", True), ("softmax_bf16_dyn", True),
+                                       ("softmax_affine_dyn", False), ("row_moments_affine_dyn", False)])
+def test_stream_row_caches_fit_registers(name, deep, tmp_path):
     """Nests of several passes keep rows of up to 8192 vectors in registers
     (a variant with 8 vectors per lane of a 1024-lane block, taken above the
     4-vector cache's 4096): every kernel of the program compiles without
-    scratch. Host-only: compiles to gfx950 assembly."""
+    scratch. A nest whose passes read a column vector in more than one pass
+    (the affine programs: the vector's loads stay live across the passes)
+    keeps the 4-deep cache only and streams longer rows. Host-only: compiles
+    to gfx950 assembly."""
     lines = _gemm_asm(name, tmp_path)
     text = "\n".join(lines)
     names = re.findall(r"^\s+\.name:\s+(tca_\S+)", text, re.M)
     priv = [int(v) for v in re.findall(r"\.private_segment_fixed_size: (\d+)", text)]
-    assert any(n.endswith("_c4x8") for n in names), names
+    assert any(n.endswith("_c4x8") for n in names) == deep, names
     assert len(names) == len(priv)
     assert all(p == 0 for p in priv), [(n, p) for n, p in zip(names, priv) if p]
     plan = programs.CONFIG_PROGRAMS[name]().emit().plan
-    # f32 rows of 4 * 4096 < C <= 4 * 8192 take the 8-deep cache; longer rows stream.
-    assert "when C 16388 32768 4 0" in plan and "when C 32772 4294967295 4 0" in plan
+    if deep:  # f32 rows of 4 * 4096 < C <= 4 * 8192 take the 8-deep cache; longer rows stream
+        assert "when C 16388 32768 4 0" in plan and "when C 32772 4294967295 4 0" in plan
+    else:
+        assert "when C 16388 4294967295 4 0" in plan
 
 
 def test_single_pass_stream_nest_keeps_one_cache_depth():
