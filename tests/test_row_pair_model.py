@@ -1,5 +1,5 @@
-"""Host-only model of the streamed row body's one-read mean and variance
-(layernorm's pair): the device's order of operations restated in float32
+"""Host-only models of the streamed row body's one-read pairs (layernorm's
+mean and variance; softmax's max and exp-sum, below): the device's order of operations restated in float32
 numpy, so the bound the GPU tests hold the device to (helpers.
 assert_layernorm_close) is shown to pass for the right arithmetic and to
 fail for plausible mistakes in it.
@@ -150,3 +150,107 @@ def test_streamed_pair_model_mistakes_fail_the_bound(mistake):
     got = _layernorm(x, g, b, inv_n, eps, mistake)
     with pytest.raises(AssertionError):
         assert_layernorm_close(got, _reference(x, g, b, inv_n, eps), x, g, b, eps, "model with " + mistake)
+
+
+# The softmax pair: each lane's online (m, s) over groups of 16 values
+# (tca::hip::online_expsum_add: the group's max, a rescale when it grows,
+# then the group's terms about the running max; -inf for values past the
+# row), the butterfly and the waves merging (m, s) pairs
+# (tca::hip::online_expsum_merge), then the exp-sum about the row's max a
+# as s e^(m - a). The terms take float64 exp rounded to float32 (the device's
+# v_exp_f32 is within 2.7e-6 relative, far inside the tolerance).
+
+def _exp(v):
+    with np.errstate(invalid="ignore"):
+        return np.exp(v.astype(np.float64)).astype(np.float32)
+
+
+def _online_add(m, s, vals, mistake=None):
+    g = vals.max(axis=1)
+    grow = g > m
+    scale = np.where(grow, _exp(m - np.where(grow, g, m)), F(1))
+    s = np.where(grow & (mistake != "no_rescale"), (s * scale).astype(np.float32), s)
+    m_old = m
+    m = np.where(grow, g, m)
+    sh = np.where((m_old if mistake == "stale_shift" else m) == -np.inf, F(0), m_old if mistake == "stale_shift" else m)
+    for i in range(vals.shape[1]):
+        s = (s + _exp(vals[:, i] - sh)).astype(np.float32)
+    return m, s
+
+
+def _online_merge(m, s, m2, s2):
+    M = np.maximum(m, m2)
+    a = np.where(m == M, s, (s * _exp(m - M)).astype(np.float32))
+    b = np.where(m2 == M, s2, (s2 * _exp(m2 - M)).astype(np.float32))
+    return M, (a + b).astype(np.float32)
+
+
+def model_softmax_row(x, mistake=None):
+    """(max, exp-sum about it) of one f32 row as the streamed body computes them."""
+    S, V = 1024, 4
+    vecs = x.shape[0] // V
+    xv = x.reshape(vecs, V)
+    nlane = -(-vecs // S)
+    lane = np.arange(S)
+    m = np.full(S, -np.inf, F)
+    s = np.zeros(S, F)
+
+    def vec(k):
+        v = lane + k * S
+        return np.where((v < vecs)[:, None], xv[np.minimum(v, vecs - 1)], F(-np.inf))
+
+    m, s = _online_add(m, s, vec(0), mistake)
+    k = 1
+    while k + 3 < nlane:
+        m, s = _online_add(m, s, np.concatenate([vec(k + u) for u in range(4)], axis=1), mistake)
+        k += 4
+    while k < nlane:
+        m, s = _online_add(m, s, vec(k), mistake)
+        k += 1
+    off = 32
+    while off:
+        partner = lane ^ off
+        m, s = _online_merge(m, s, m[partner], s[partner])
+        off >>= 1
+    wm, wsum = m[::64], s[::64]
+    cm, cs = wm[:1], wsum[:1]
+    for w in range(1, S // 64):
+        cm, cs = _online_merge(cm, cs, wm[w:w + 1], wsum[w:w + 1])
+    a = F(max(F(-np.inf), cm[0]))
+    return a, F(cs[0] * _exp(np.array([cm[0] - a], F))[0])
+
+
+def _softmax_rows(C):
+    x = inputs.normal((3, C), 2.0, 22)
+    x[1, -1] = 40.0  # the maximum last: every earlier partial rescales
+    x[2, : C // 2] += 30.0  # the large values first: later groups add small terms
+    return x
+
+
+@pytest.mark.parametrize("C", [40000, 40004, 65540])
+def test_streamed_softmax_model_within_the_gpu_bound(C):
+    """The right arithmetic stays within the relative bound the GPU softmax
+    tests use (reduce_tol), for the exp-sum and so for every output."""
+    from helpers import reduce_tol
+    x = _softmax_rows(C)
+    for r in range(x.shape[0]):
+        a, den = model_softmax_row(x[r])
+        xd = x[r].astype(np.float64)
+        assert a == np.float32(x[r].max())
+        d64 = np.exp(xd - a).sum()
+        assert abs(den - d64) <= reduce_tol(C) * d64, (r, den, d64)
+
+
+@pytest.mark.parametrize("mistake", ["no_rescale", "stale_shift"])
+def test_streamed_softmax_model_mistakes_fail_the_bound(mistake):
+    """A running sum not rescaled when the max grows, or a group's terms
+    taken about the max before the group, break the bound."""
+    from helpers import reduce_tol
+    C = 40000
+    x = _softmax_rows(C)
+    worst = 0.0
+    for r in range(x.shape[0]):
+        a, den = model_softmax_row(x[r], mistake)
+        d64 = np.exp(x[r].astype(np.float64) - a).sum()
+        worst = max(worst, abs(den - d64) / d64 / reduce_tol(C) if np.isfinite(den) else np.inf)
+    assert worst > 1.0, worst
